@@ -1,0 +1,81 @@
+"""Build recipe for libchonk.so (hipcc, gfx950) and the oracle's CPU library.
+
+Run ``python -m chonklm_amd.build`` or call :func:`build_all`. Outputs stay
+in-tree (``chonklm_amd/_lib/libchonk.so``, ``oracle/_build/liborc.so``) so
+that they travel with the repository snapshot to the GPU host.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+LIB_DIR = PKG / "_lib"
+LIB_PATH = LIB_DIR / "libchonk.so"
+OBJ_DIR = LIB_DIR / "obj"
+
+HIP_SOURCES = [PKG / "csrc/hip/engine.hip", PKG / "csrc/hip/kernels.hip"]
+HOST_SOURCES = [PKG / "csrc/host/gguf.cpp", PKG / "csrc/host/quantize.cpp", PKG / "csrc/host/synth.cpp"]
+HEADERS = sorted((PKG / "csrc").rglob("*.h")) + [ROOT / "include/chonk.h"]
+
+ARCH = os.environ.get("CHONK_OFFLOAD_ARCH", "gfx950")
+
+
+def _hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libchonk.so")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass warns about the gfx-only target feature; keep other output
+    lines = [ln for ln in proc.stdout.splitlines() if "packed-fp32-ops' is not a recognized" not in ln]
+    if proc.returncode != 0:
+        raise RuntimeError("build step failed: " + " ".join(cmd) + "\n" + "\n".join(lines))
+
+
+def build_library(jobs: int = 8) -> Path:
+    """Compiles every source (always) and links libchonk.so."""
+    hipcc = _hipcc()
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    common = ["-O3", "-std=c++20", "-fPIC", f"-I{ROOT / 'include'}", "-Wall", "-Wno-unused-function"]
+    gpu = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    jobs_list = []
+    for src in HIP_SOURCES:
+        obj = OBJ_DIR / (src.stem + ".o")
+        jobs_list.append((obj, [hipcc, *gpu, *common, "-c", str(src), "-o", str(obj)]))
+    for src in HOST_SOURCES:
+        obj = OBJ_DIR / (src.stem + ".host.o")
+        jobs_list.append((obj, ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", str(src), "-o", str(obj)]))
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(lambda j: _run(j[1]), jobs_list))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, *gpu, "-shared", "-fPIC", "-o", str(tmp), *[str(o) for o, _ in jobs_list], "-lpthread"])
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_oracle() -> Path | None:
+    """Builds the oracle's CPU restatement (test infrastructure)."""
+    oracle = ROOT / "oracle"
+    if not (oracle / "Makefile").exists():
+        return None
+    _run(["make", "-s", "-B", "-C", str(oracle)])
+    return oracle / "_build" / "liborc.so"
+
+
+def build_all(jobs: int = 8) -> None:
+    build_library(jobs)
+    build_oracle()
+
+
+if __name__ == "__main__":
+    build_all(int(sys.argv[1]) if len(sys.argv) > 1 else 8)
+    print(LIB_PATH)

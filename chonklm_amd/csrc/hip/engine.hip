@@ -1,0 +1,1571 @@
+// Decode engine: GGUF -> device upload, K/V cache, step graphs, C ABI.
+//
+// Host semantics follow the reference's llama-webgpu runtime
+// (src/lib/llama-wgsl-runtime.ts):
+//   loadLlamaWgslModel / buildGgufLlamaManifest   :184-240, :326-425
+//   LlamaWgslEngine.create (buffers, K/V cache)   :669-919
+//   runToken (op order per architecture)          :1025-1150
+//   generateLlamaWgsl (prefix reuse, loop, tok/s) :242-314
+//   reset / position / dispose                    :1011-1023, :1152-1215
+//   argmax penalty list                           :1647-1665
+// and src/lib/sampling.ts:9-16 (needsSamplingReadback).
+//
+// MI355X design: every weight matrix is repacked once into striped streams
+// (device_common.h); one decode step is a fixed list of 5L+2 kernel launches
+// that read the position and token from device memory, captured once into a
+// hipGraph per step kind (with / without logits) and replayed. Device-driven
+// generation appends sampled ids on the device and checks EOS there, so a
+// whole generate call needs no per-token host round trip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../host/ggml_types.h"
+#include "../host/gguf.h"
+#include "../host/synth.h"
+#include "chonk.h"
+#include "kernels.h"
+
+namespace chonk {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HIP_OK(expr)                                                                               \
+  do {                                                                                             \
+    hipError_t e_ = (expr);                                                                        \
+    if (e_ != hipSuccess)                                                                          \
+      throw Error(CHONK_EHIP, std::string("HIP error ") + hipGetErrorString(e_) + " at " #expr);  \
+  } while (0)
+
+// ---- repacking GGUF blocks into stripes -------------------------------------------
+
+struct Stripes {
+  std::vector<uint8_t> s[4];
+};
+
+Stripes repack(uint32_t type, const uint8_t* raw, int64_t N, int64_t K) {
+  TypeTraits t;
+  if (!type_traits(type, &t) || !t.quantized) throw Error(CHONK_EINVAL, "not a GGUF quant type: " + type_name(type));
+  const int64_t nb = N * (K / t.block_elems);
+  Stripes st;
+  auto put = [](std::vector<uint8_t>& v, const uint8_t* p, size_t n) { v.insert(v.end(), p, p + n); };
+  for (int i = 0; i < 4; ++i) st.s[i].reserve((size_t)(nb * t.block_bytes));
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t* p = raw + b * t.block_bytes;
+    switch (type) {
+      case GGML_Q4_K: put(st.s[0], p + 16, 128); put(st.s[1], p, 16); break;
+      case GGML_Q5_K: put(st.s[0], p + 48, 128); put(st.s[1], p, 16); put(st.s[2], p + 16, 32); break;
+      case GGML_Q6_K: put(st.s[0], p, 128); put(st.s[1], p + 128, 64); put(st.s[2], p + 192, 16); put(st.s[3], p + 208, 2); break;
+      case GGML_Q8_0: put(st.s[0], p + 2, 32); put(st.s[1], p, 2); break;
+      case GGML_Q5_0: put(st.s[0], p + 6, 16); put(st.s[1], p + 2, 4); put(st.s[2], p, 2); break;
+      case GGML_Q5_1: put(st.s[0], p + 8, 16); put(st.s[1], p + 4, 4); put(st.s[2], p, 2); put(st.s[3], p + 2, 2); break;
+      default: throw Error(CHONK_EINVAL, "unsupported GGUF tensor type " + type_name(type));
+    }
+  }
+  return st;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Device memory arena: one allocation, bump-allocated 256-byte aligned.
+class Arena {
+ public:
+  void reserve(size_t bytes) {
+    HIP_OK(hipMalloc(&base_, bytes ? bytes : 256));
+    cap_ = bytes;
+  }
+  void* take(size_t bytes) {
+    const size_t n = align256(bytes);
+    if (off_ + n > cap_) throw Error(CHONK_ENOMEM, "device arena exhausted");
+    void* p = (uint8_t*)base_ + off_;
+    off_ += n;
+    return p;
+  }
+  void release() {
+    if (base_) (void)hipFree(base_);
+    base_ = nullptr;
+  }
+  size_t capacity() const { return cap_; }
+
+ private:
+  void* base_ = nullptr;
+  size_t cap_ = 0, off_ = 0;
+};
+
+struct DevMat {
+  QMat q{};
+  uint64_t gguf_bytes = 0;  // bytes of the N rows as stored in GGUF
+};
+
+// ---- model description (buildGgufLlamaManifest) ---------------------------------
+
+struct TensorRef {
+  const GgufTensorInfo* info = nullptr;
+};
+
+struct LayerCfg {
+  uint32_t theta = 10000;
+  int window = 0;
+};
+
+struct ModelCfg {
+  std::string arch;
+  bool gemma = false, interleaved = false, qk_norm = false;
+  int hidden = 0, ffn = 0, vocab = 0, layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
+  float eps = 1e-5f, qk_eps = 1e-5f, scale = 0, embed_scale = 1;
+  std::vector<LayerCfg> layer;
+};
+
+double meta_number(const GgufFile& g, const std::string& key, const double* fallback) {
+  const GgufValue* v = g.value(key);
+  if (v && v->is_number()) return v->number;
+  if (fallback) return *fallback;
+  throw Error(CHONK_EINVAL, "GGUF metadata " + key + " is missing or not numeric");
+}
+
+ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
+  ModelCfg c;
+  const GgufValue* a = g.value("general.architecture");
+  if (!a || a->type != GV_STRING) throw Error(CHONK_EINVAL, "GGUF metadata general.architecture is missing or not a string");
+  c.arch = a->str;
+  if (c.arch == "openelm")
+    throw Error(CHONK_EINVAL, "architecture openelm (fused qkv, per-layer heads) is not supported by this engine yet");
+  if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3")
+    throw Error(CHONK_EINVAL, "Llama GGUF WGSL does not support architecture " + c.arch);
+  c.gemma = c.arch == "gemma3";
+  c.interleaved = c.arch == "llama";
+  const std::string p = c.arch + ".";
+  c.layers = (int)meta_number(g, p + "block_count", nullptr);
+  c.hidden = (int)meta_number(g, p + "embedding_length", nullptr);
+  c.heads = (int)meta_number(g, p + "attention.head_count", nullptr);
+  c.kv_heads = (int)meta_number(g, p + "attention.head_count_kv", nullptr);
+  c.ffn = (int)meta_number(g, p + "feed_forward_length", nullptr);
+  const double hd_default = std::floor((double)c.hidden / std::max(1, c.heads));
+  c.hd = (int)meta_number(g, p + "attention.key_length", &hd_default);
+  c.vocab = def.vocab;
+  const double ctx_default = def.max_context;
+  const int gguf_ctx = (int)meta_number(g, p + "context_length", &ctx_default);
+  c.ctx = std::min(def.max_context, std::min(def.max_context, gguf_ctx));
+  const double eps_default = 1e-5;
+  c.eps = (float)meta_number(g, p + "attention.layer_norm_rms_epsilon", &eps_default);
+  c.qk_eps = c.eps;
+  c.qk_norm = g.find("blk.0.attn_q_norm.weight") && g.find("blk.0.attn_k_norm.weight");
+  c.scale = (float)(1.0 / std::sqrt((double)c.hd));
+  c.embed_scale = c.gemma ? (float)std::sqrt((double)c.hidden) : 1.0f;
+  const double theta_default = 10000, gtheta_default = 1000000, win_default = 0;
+  const double theta = c.gemma ? 10000.0 : meta_number(g, p + "rope.freq_base", &theta_default);
+  const double gtheta = c.gemma ? meta_number(g, "gemma3.rope.freq_base", &gtheta_default) : 0;
+  const int window = c.gemma ? (int)meta_number(g, "gemma3.attention.sliding_window", &win_default) : 0;
+  for (int i = 0; i < c.layers; ++i) {
+    LayerCfg L;
+    const double th = c.gemma ? (i % 6 == 5 ? gtheta : 10000.0) : theta;
+    L.theta = (uint32_t)std::llround(th);
+    L.window = c.gemma ? (i % 6 == 5 ? 0 : window) : 0;
+    c.layer.push_back(L);
+  }
+  // limits of this engine's kernels
+  if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
+    throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+  if (c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8)
+    throw Error(CHONK_EINVAL, "GQA group size must divide heads and be at most 8");
+  if (c.hd != 32 && c.hd != 64 && c.hd != 128 && c.hd != 256)
+    throw Error(CHONK_EINVAL, "head_dim " + std::to_string(c.hd) + " is not supported (32, 64, 128 or 256)");
+  if ((c.vocab + 255) / 256 > 4096) throw Error(CHONK_EINVAL, "vocab above 1048576 is not supported");
+  if (c.gemma && !c.qk_norm) throw Error(CHONK_EINVAL, "Gemma WGSL layer is missing required weights");
+  return c;
+}
+
+// ---- the engine ------------------------------------------------------------------
+
+struct LayerDev {
+  DevMat q, k, v, o, gate, up, down;
+  float *in_norm = nullptr, *post_norm = nullptr, *pre_ffn_norm = nullptr, *post_ffn_norm = nullptr;
+  float *q_norm = nullptr, *k_norm = nullptr;
+  void *kc = nullptr, *vc = nullptr;
+};
+
+struct Launch {
+  enum Kind { MV, ATTN, SEL } kind = MV;
+  MvArgs mv{};
+  AttnArgs at{};
+  SelArgs sel{};
+  int grid = 0;
+  size_t shmem = 0;
+  std::string name;
+  uint64_t weight_bytes = 0;  // GGUF weight bytes read (matvec)
+  int layer = -1;
+};
+
+}  // namespace
+}  // namespace chonk
+
+using namespace chonk;
+
+struct chonk_engine {
+  chonk_model_def def{};
+  std::string model_id;
+  std::vector<int32_t> eos;
+  ModelCfg cfg;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  Arena weights, state;
+  std::vector<LayerDev> layers;
+  DevMat embed, lm_head;
+  float* final_norm = nullptr;
+  size_t kv_elem = 2;
+  // activations
+  float *resA = nullptr, *resB = nullptr, *delta = nullptr, *qkv = nullptr, *attn = nullptr, *ff = nullptr,
+        *logits = nullptr, *part = nullptr;
+  Candidate* cand = nullptr;
+  uint32_t* cnt = nullptr;
+  DevState* st = nullptr;
+  DevSampling* samp = nullptr;
+  int32_t *hist = nullptr, *gen = nullptr;
+  uint32_t *pen_bits = nullptr, *seen_bits = nullptr;
+  int groups = 0, chunk = 0, nchunk = 0;
+  std::vector<Launch> step_logits, step_plain;
+  hipGraph_t graph_logits = nullptr, graph_plain = nullptr;
+  hipGraphExec_t exec_logits = nullptr, exec_plain = nullptr;
+  // pinned host staging
+  DevState* h_state = nullptr;
+  int32_t* h_tok = nullptr;
+  DevSampling* h_samp = nullptr;
+  DevSampling last_samp{};
+  bool samp_valid = false;
+  // host mirror of the conversation
+  int pos = 0;
+  int known_token_pos = -1;  // position whose history slot the device already holds
+  int32_t known_token = 0;
+  bool logits_valid = false;
+  std::vector<int32_t> cached_ids;
+  bool has_cached_next = false;
+  int32_t cached_next = 0;
+  uint64_t weight_bytes_per_token = 0;
+  // status
+  std::atomic<bool> busy{false};
+  bool lost = false;
+  std::string err;
+};
+
+namespace chonk {
+namespace {
+
+struct Guard {
+  chonk_engine* e;
+  explicit Guard(chonk_engine* eng) : e(eng) {
+    bool expected = false;
+    if (!e->busy.compare_exchange_strong(expected, true))
+      throw Error(CHONK_EBUSY, "engine call already in progress");
+    if (e->lost) {
+      e->busy = false;
+      throw Error(CHONK_ELOST, "engine lost after an earlier device error: " + e->err);
+    }
+    (void)hipSetDevice(e->device);
+  }
+  ~Guard() { e->busy = false; }
+};
+
+template <typename F>
+int api(chonk_engine* e, F&& f) {
+  try {
+    if (!e) throw Error(CHONK_EINVAL, "null engine");
+    Guard g(e);
+    try {
+      f();
+    } catch (const Error& x) {
+      if (x.code == CHONK_EHIP) e->lost = true;
+      throw;
+    }
+    return CHONK_OK;
+  } catch (const Error& x) {
+    g_last_error = x.what();
+    if (e && x.code != CHONK_EBUSY) e->err = x.what();
+    return x.code;
+  } catch (const std::exception& x) {
+    g_last_error = x.what();
+    if (e) e->err = x.what();
+    return CHONK_EINVAL;
+  }
+}
+
+template <typename F>
+int api_free(F&& f) {
+  try {
+    f();
+    return CHONK_OK;
+  } catch (const Error& x) {
+    g_last_error = x.what();
+    return x.code;
+  } catch (const std::exception& x) {
+    g_last_error = x.what();
+    return CHONK_EIO;
+  }
+}
+
+const GgufTensorInfo& tensor(const GgufFile& g, const std::string& name) {
+  const GgufTensorInfo* t = g.find(name);
+  if (!t) throw Error(CHONK_EINVAL, "Llama WGSL manifest missing tensor " + name);
+  return *t;
+}
+
+std::vector<uint8_t> read_tensor(const ByteSource& src, const GgufFile& g, const GgufTensorInfo& t) {
+  std::vector<uint8_t> raw((size_t)t.n_bytes);
+  try {
+    src.read(g.data_offset + t.offset, t.n_bytes, raw.data());
+  } catch (const std::exception& e) {
+    throw Error(CHONK_EIO, e.what());
+  }
+  return raw;
+}
+
+// Size of the stripes of an N x K matrix of `type`.
+size_t stripes_bytes(uint32_t type, int64_t N, int64_t K) {
+  TypeTraits t;
+  type_traits(type, &t);
+  const size_t nb = (size_t)(N * (K / t.block_elems));
+  switch (type) {
+    case GGML_Q4_K: return align256(nb * 128) + align256(nb * 16);
+    case GGML_Q5_K: return align256(nb * 128) + align256(nb * 16) + align256(nb * 32);
+    case GGML_Q6_K: return align256(nb * 128) + align256(nb * 64) + align256(nb * 16) + align256(nb * 2);
+    case GGML_Q8_0: return align256(nb * 32) + align256(nb * 2);
+    case GGML_Q5_0: return align256(nb * 16) + align256(nb * 4) + align256(nb * 2);
+    case GGML_Q5_1: return align256(nb * 16) + align256(nb * 4) + align256(nb * 2) + align256(nb * 2);
+  }
+  return 0;
+}
+
+void check_matrix(const GgufTensorInfo& t, int64_t K, int64_t N) {
+  TypeTraits tt;
+  if (!type_traits(t.type, &tt) || !tt.quantized)
+    throw Error(CHONK_EINVAL, "Llama WGSL tensor " + t.name + " is not a supported GGUF quantized tensor");
+  if (K % tt.block_elems != 0 || K % 32 != 0)
+    throw Error(CHONK_EINVAL, "tensor " + t.name + " row length " + std::to_string(K) + " is not a multiple of its " +
+                                  std::to_string(tt.block_elems) + "-element block");
+  if (t.shape.empty() || (int64_t)t.shape[0] != K)
+    throw Error(CHONK_EINVAL, "tensor " + t.name + " row length does not match the model (" + std::to_string(K) + ")");
+  if ((int64_t)(t.n_elements / t.shape[0]) < N)
+    throw Error(CHONK_EINVAL, "tensor " + t.name + " has fewer than " + std::to_string(N) + " rows");
+  if (K > 32768) throw Error(CHONK_EINVAL, "tensor " + t.name + " row length above 32768 is not supported");
+}
+
+DevMat upload_matrix(Arena& arena, const ByteSource& src, const GgufFile& g, const GgufTensorInfo& t, int64_t K,
+                     int64_t N) {
+  check_matrix(t, K, N);
+  std::vector<uint8_t> raw = read_tensor(src, g, t);
+  TypeTraits tt;
+  type_traits(t.type, &tt);
+  const Stripes st = repack(t.type, raw.data(), N, K);
+  DevMat m;
+  m.q.type = (int32_t)t.type;
+  m.q.n = (int32_t)N;
+  m.q.k = (int32_t)K;
+  const uint8_t** dst[4] = {&m.q.s0, &m.q.s1, &m.q.s2, &m.q.s3};
+  for (int i = 0; i < 4; ++i) {
+    if (st.s[i].empty()) continue;
+    void* p = arena.take(st.s[i].size());
+    HIP_OK(hipMemcpy(p, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+    *dst[i] = (const uint8_t*)p;
+  }
+  m.gguf_bytes = (uint64_t)(N * (K / tt.block_elems)) * tt.block_bytes;
+  return m;
+}
+
+float* upload_floats(Arena& arena, const ByteSource& src, const GgufFile& g, const std::string& name, int64_t n) {
+  const GgufTensorInfo& t = tensor(g, name);
+  if (t.type != GGML_F32 && t.type != GGML_F16)
+    throw Error(CHONK_EINVAL, "Llama WGSL tensor " + name + " is " + type_name(t.type) + ", expected float32/float16");
+  if ((int64_t)t.n_elements < n) throw Error(CHONK_EINVAL, "tensor " + name + " is shorter than " + std::to_string(n));
+  std::vector<uint8_t> raw = read_tensor(src, g, t);
+  std::vector<float> f((size_t)n);
+  for (int64_t i = 0; i < n; ++i) {
+    if (t.type == GGML_F32) {
+      std::memcpy(&f[i], raw.data() + 4 * i, 4);
+    } else {
+      uint16_t h;
+      std::memcpy(&h, raw.data() + 2 * i, 2);
+      f[i] = f16_to_f32(h);
+    }
+  }
+  float* p = (float*)arena.take((size_t)n * 4);
+  HIP_OK(hipMemcpy(p, f.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+  return p;
+}
+
+int target_wgs() { return 512; }
+
+// Fills seg geometry for n_out output rows of matrix w (glu: gate/up pairs).
+void plan_seg(MvSeg& sg, const QMat& w, int n_out, bool glu, int wg_begin) {
+  sg.w = w;
+  sg.n_out = n_out;
+  sg.lpr = pick_lpr(w.k / 32);
+  const int ng = kWg / sg.lpr;
+  const int per_pass = glu ? ng / 2 : ng;
+  const int passes = std::max(1, (n_out + per_pass * target_wgs() - 1) / (per_pass * target_wgs()));
+  sg.tile = per_pass * passes;
+  sg.wg_begin = wg_begin;
+}
+
+int seg_wgs(const MvSeg& sg) { return (sg.n_out + sg.tile - 1) / sg.tile; }
+
+void build_steps(chonk_engine* e) {
+  const ModelCfg& c = e->cfg;
+  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, G = c.heads / c.kv_heads;
+  auto mv_base = [&]() {
+    MvArgs a{};
+    a.st = e->st;
+    a.eps = c.eps;
+    a.vocab = c.vocab;
+    a.hist = e->hist;
+    a.embed = e->embed.q;
+    a.embed_scale = c.embed_scale;
+    a.samp = e->samp;
+    a.pen_bits = e->pen_bits;
+    a.cand = e->cand;
+    return a;
+  };
+  auto finish = [&](Launch& L, const MvArgs& a, int max_rows) {
+    L.kind = Launch::MV;
+    L.mv = a;
+    L.grid = 0;
+    for (int i = 0; i < a.nseg; ++i) L.grid += seg_wgs(a.seg[i]);
+    L.shmem = mv_shared_bytes(a.k, max_rows);
+  };
+  std::vector<Launch> steps;
+  for (int i = 0; i < c.layers; ++i) {
+    LayerDev& Ld = e->layers[i];
+    const std::string li = "L" + std::to_string(i) + ".";
+    // qkv
+    {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = H;
+      a.nseg = 3;
+      plan_seg(a.seg[0], Ld.q.q, qdim, false, 0);
+      a.seg[0].out = e->qkv;
+      plan_seg(a.seg[1], Ld.k.q, kvdim, false, seg_wgs(a.seg[0]));
+      a.seg[1].out = e->qkv + qdim;
+      plan_seg(a.seg[2], Ld.v.q, kvdim, false, a.seg[1].wg_begin + seg_wgs(a.seg[1]));
+      a.seg[2].out = e->qkv + qdim + kvdim;
+      a.epi = EPI_STORE;
+      a.w_norm = Ld.in_norm;
+      if (i == 0) {
+        a.pro = PRO_EMBED_NORM;
+        a.res_out = e->resA;
+      } else if (c.gemma) {
+        a.pro = PRO_RES_NORM;
+        a.in = e->resB;
+        a.delta = e->delta;
+        a.w_delta = e->layers[i - 1].post_ffn_norm;
+        a.res_out = e->resA;
+      } else {
+        a.pro = PRO_NORM;
+        a.in = e->resA;
+      }
+      finish(L, a, std::max(a.seg[0].tile, std::max(a.seg[1].tile, a.seg[2].tile)));
+      L.name = li + "qkv";
+      L.weight_bytes = Ld.q.gguf_bytes + Ld.k.gguf_bytes + Ld.v.gguf_bytes + (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
+      L.layer = i;
+      steps.push_back(L);
+    }
+    // attention
+    {
+      Launch L;
+      L.kind = Launch::ATTN;
+      AttnArgs& t = L.at;
+      t.qkv = e->qkv;
+      t.qn_w = c.qk_norm ? Ld.q_norm : nullptr;
+      t.kn_w = c.qk_norm ? Ld.k_norm : nullptr;
+      t.kc = Ld.kc;
+      t.vc = Ld.vc;
+      t.part = e->part;
+      t.cnt = e->cnt;
+      t.out = e->attn;
+      t.st = e->st;
+      t.heads = c.heads;
+      t.kv_heads = c.kv_heads;
+      t.hd = c.hd;
+      t.ctx = c.ctx;
+      t.window = c.layer[i].window;
+      t.chunk = e->chunk;
+      t.nchunk = e->nchunk;
+      t.theta = c.layer[i].theta;
+      t.interleaved = c.interleaved ? 1 : 0;
+      t.kv_f16 = e->kv_elem == 2 ? 1 : 0;
+      t.eps = c.qk_eps;
+      t.scale = c.scale;
+      L.shmem = attn_shared_bytes(G, c.hd, e->chunk);
+      L.grid = c.kv_heads * e->nchunk;
+      L.name = li + "attn";
+      L.layer = i;
+      steps.push_back(L);
+    }
+    // o projection
+    {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = qdim;
+      a.nseg = 1;
+      plan_seg(a.seg[0], Ld.o.q, H, false, 0);
+      a.pro = PRO_PLAIN;
+      a.in = e->attn;
+      if (c.gemma) {
+        a.epi = EPI_STORE;
+        a.seg[0].out = e->delta;
+      } else {
+        a.epi = EPI_ADD;
+        a.seg[0].out = e->resB;
+        a.seg[0].add = e->resA;
+      }
+      finish(L, a, a.seg[0].tile);
+      L.name = li + "oproj";
+      L.weight_bytes = Ld.o.gguf_bytes;
+      L.layer = i;
+      steps.push_back(L);
+    }
+    // gate|up
+    {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = H;
+      a.nseg = 1;
+      plan_seg(a.seg[0], Ld.gate.q, c.ffn, true, 0);
+      a.seg[0].w2 = Ld.up.q;
+      a.seg[0].out = e->ff;
+      a.epi = c.gemma ? EPI_GLU_GELU : EPI_GLU_SILU;
+      if (c.gemma) {
+        a.pro = PRO_RES_NORM;
+        a.in = e->resA;
+        a.delta = e->delta;
+        a.w_delta = Ld.post_norm;
+        a.res_out = e->resB;
+        a.w_norm = Ld.pre_ffn_norm;
+      } else {
+        a.pro = PRO_NORM;
+        a.in = e->resB;
+        a.w_norm = Ld.post_norm;
+      }
+      finish(L, a, 2 * a.seg[0].tile);
+      L.name = li + "gateup";
+      L.weight_bytes = Ld.gate.gguf_bytes + Ld.up.gguf_bytes;
+      L.layer = i;
+      steps.push_back(L);
+    }
+    // down
+    {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = c.ffn;
+      a.nseg = 1;
+      plan_seg(a.seg[0], Ld.down.q, H, false, 0);
+      a.pro = PRO_PLAIN;
+      a.in = e->ff;
+      if (c.gemma) {
+        a.epi = EPI_STORE;
+        a.seg[0].out = e->delta;
+      } else {
+        a.epi = EPI_ADD;
+        a.seg[0].out = e->resA;
+        a.seg[0].add = e->resB;
+      }
+      finish(L, a, a.seg[0].tile);
+      L.name = li + "down";
+      L.weight_bytes = Ld.down.gguf_bytes;
+      L.layer = i;
+      steps.push_back(L);
+    }
+  }
+  e->step_plain = steps;
+  e->step_plain.back().mv.advance_pos = 1;
+  // lm_head + group argmax
+  {
+    Launch L;
+    MvArgs a = mv_base();
+    a.k = H;
+    a.nseg = 1;
+    MvSeg& sg = a.seg[0];
+    sg.w = e->lm_head.q;
+    sg.n_out = c.vocab;
+    sg.lpr = pick_lpr(H / 32);
+    sg.tile = 256;
+    sg.wg_begin = 0;
+    sg.out = e->logits;
+    a.epi = EPI_LOGITS;
+    a.w_norm = e->final_norm;
+    if (c.gemma) {
+      a.pro = PRO_RES_NORM;
+      a.in = e->resB;
+      a.delta = e->delta;
+      a.w_delta = e->layers[c.layers - 1].post_ffn_norm;
+      a.res_out = e->resA;
+    } else {
+      a.pro = PRO_NORM;
+      a.in = e->resA;
+    }
+    finish(L, a, 256);
+    L.name = "lmhead";
+    L.weight_bytes = e->lm_head.gguf_bytes;
+    steps.push_back(L);
+  }
+  {
+    Launch L;
+    L.kind = Launch::SEL;
+    SelArgs& s = L.sel;
+    s.cand = e->cand;
+    s.groups = e->groups;
+    s.vocab = c.vocab;
+    s.ctx = c.ctx;
+    s.samp = e->samp;
+    s.pen_bits = e->pen_bits;
+    s.seen_bits = e->seen_bits;
+    s.hist = e->hist;
+    s.gen = e->gen;
+    s.st = e->st;
+    L.grid = 1;
+    L.name = "select";
+    steps.push_back(L);
+  }
+  e->step_logits = steps;
+}
+
+void enqueue(const Launch& L, hipStream_t s) {
+  switch (L.kind) {
+    case Launch::MV: HIP_OK(launch_matvec(L.mv, L.grid, L.shmem, s)); break;
+    case Launch::ATTN: HIP_OK(launch_attention(L.at, L.shmem, s)); break;
+    case Launch::SEL: HIP_OK(launch_select(L.sel, s)); break;
+  }
+}
+
+void capture(chonk_engine* e, const std::vector<Launch>& steps, hipGraph_t* g, hipGraphExec_t* x) {
+  HIP_OK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  try {
+    for (const Launch& L : steps) enqueue(L, e->stream);
+  } catch (...) {
+    hipGraph_t tmp;
+    (void)hipStreamEndCapture(e->stream, &tmp);
+    throw;
+  }
+  HIP_OK(hipStreamEndCapture(e->stream, g));
+  HIP_OK(hipGraphInstantiate(x, *g, nullptr, nullptr, 0));
+}
+
+void engine_free(chonk_engine* e) {
+  if (!e) return;
+  (void)hipSetDevice(e->device);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  if (e->exec_logits) (void)hipGraphExecDestroy(e->exec_logits);
+  if (e->exec_plain) (void)hipGraphExecDestroy(e->exec_plain);
+  if (e->graph_logits) (void)hipGraphDestroy(e->graph_logits);
+  if (e->graph_plain) (void)hipGraphDestroy(e->graph_plain);
+  e->weights.release();
+  e->state.release();
+  if (e->h_state) (void)hipHostFree(e->h_state);
+  if (e->h_tok) (void)hipHostFree(e->h_tok);
+  if (e->h_samp) (void)hipHostFree(e->h_samp);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, const std::string& label,
+                   chonk_engine** out) {
+  if (!def || !out) throw Error(CHONK_EINVAL, "null argument");
+  if (def->vocab <= 0 || def->max_context <= 0) throw Error(CHONK_EINVAL, "ModelDef vocab and maxContext must be positive");
+  if (def->n_eos < 0 || def->n_eos > 16) throw Error(CHONK_EINVAL, "at most 16 EOS ids are supported");
+  GgufFile g;
+  try {
+    g = read_gguf_header(*src, label);
+  } catch (const Error&) {
+    throw;
+  } catch (const std::exception& x) {
+    throw Error(CHONK_EINVAL, x.what());
+  }
+  std::unique_ptr<chonk_engine, void (*)(chonk_engine*)> e(new chonk_engine(), engine_free);
+  e->def = *def;
+  e->model_id = def->id ? def->id : "";
+  e->eos.assign(def->eos_ids, def->eos_ids + def->n_eos);
+  e->device = def->device;
+  e->cfg = build_config(g, *def);
+  const ModelCfg& c = e->cfg;
+  HIP_OK(hipSetDevice(e->device));
+  HIP_OK(hipStreamCreate(&e->stream));
+  e->kv_elem = def->kv_dtype == CHONK_KV_F32 ? 4 : 2;
+
+  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd;
+  const std::string lm_name = g.find("output.weight") ? "output.weight" : "token_embd.weight";
+  const bool tied = lm_name == "token_embd.weight";
+  // size the weight arena
+  size_t wbytes = 0;
+  auto mat_bytes = [&](const std::string& name, int64_t K, int64_t N) {
+    const GgufTensorInfo& t = tensor(g, name);
+    check_matrix(t, K, N);
+    wbytes += stripes_bytes(t.type, N, K);
+  };
+  auto vec_bytes = [&](int64_t n) { wbytes += align256((size_t)n * 4); };
+  mat_bytes("token_embd.weight", H, c.vocab);
+  if (!tied) mat_bytes(lm_name, H, c.vocab);
+  vec_bytes(H);
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    mat_bytes(p + "attn_q.weight", H, qdim);
+    mat_bytes(p + "attn_k.weight", H, kvdim);
+    mat_bytes(p + "attn_v.weight", H, kvdim);
+    mat_bytes(p + "attn_output.weight", qdim, H);
+    mat_bytes(p + "ffn_gate.weight", H, c.ffn);
+    mat_bytes(p + "ffn_up.weight", H, c.ffn);
+    mat_bytes(p + "ffn_down.weight", c.ffn, H);
+    vec_bytes(H);
+    vec_bytes(H);
+    if (c.gemma) {
+      vec_bytes(H);
+      vec_bytes(H);
+    }
+    if (c.qk_norm) {
+      vec_bytes(c.hd);
+      vec_bytes(c.hd);
+    }
+  }
+  e->weights.reserve(wbytes);
+
+  // state arena: K/V cache + activations + bookkeeping
+  e->groups = (c.vocab + 255) / 256;
+  e->chunk = 16;
+  while (e->chunk < 256 && (int64_t)c.kv_heads * ((c.ctx + e->chunk - 1) / e->chunk) > 512) e->chunk <<= 1;
+  e->nchunk = (c.ctx + e->chunk - 1) / e->chunk;
+  const int G = c.heads / c.kv_heads;
+  const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
+  const size_t bits_words = (size_t)(c.vocab + 31) / 32;
+  size_t sbytes = 2 * align256(kv_bytes) * c.layers;
+  sbytes += 3 * align256((size_t)H * 4) + align256((size_t)(qdim + 2 * kvdim) * 4) + align256((size_t)qdim * 4) +
+            align256((size_t)c.ffn * 4) + align256((size_t)c.vocab * 4) +
+            align256((size_t)c.kv_heads * e->nchunk * G * (c.hd + 2) * 4) + align256((size_t)e->groups * 8) +
+            align256((size_t)c.kv_heads * 4) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
+            2 * align256((size_t)(c.ctx + 1) * 4) + 2 * align256(bits_words * 4);
+  e->state.reserve(sbytes);
+
+  // weights
+  e->embed = upload_matrix(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
+  e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
+  e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    LayerDev L;
+    L.in_norm = upload_floats(e->weights, *src, g, p + "attn_norm.weight", H);
+    L.post_norm = upload_floats(e->weights, *src, g, p + (c.gemma ? "post_attention_norm.weight" : "ffn_norm.weight"), H);
+    if (c.gemma) {
+      L.pre_ffn_norm = upload_floats(e->weights, *src, g, p + "ffn_norm.weight", H);
+      L.post_ffn_norm = upload_floats(e->weights, *src, g, p + "post_ffw_norm.weight", H);
+    }
+    if (c.qk_norm) {
+      L.q_norm = upload_floats(e->weights, *src, g, p + "attn_q_norm.weight", c.hd);
+      L.k_norm = upload_floats(e->weights, *src, g, p + "attn_k_norm.weight", c.hd);
+    }
+    L.q = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_q.weight"), H, qdim);
+    L.k = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_k.weight"), H, kvdim);
+    L.v = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_v.weight"), H, kvdim);
+    L.o = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_output.weight"), qdim, H);
+    L.gate = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_gate.weight"), H, c.ffn);
+    L.up = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_up.weight"), H, c.ffn);
+    L.down = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_down.weight"), c.ffn, H);
+    if (L.gate.q.type != L.up.q.type)
+      throw Error(CHONK_EINVAL, "ffn_gate and ffn_up of layer " + std::to_string(i) + " have different types");
+    L.kc = e->state.take(kv_bytes);
+    L.vc = e->state.take(kv_bytes);
+    e->layers.push_back(L);
+  }
+  uint64_t wpt = e->lm_head.gguf_bytes + e->embed.gguf_bytes / c.vocab + (uint64_t)H * 4;
+  for (const LayerDev& L : e->layers)
+    wpt += L.q.gguf_bytes + L.k.gguf_bytes + L.v.gguf_bytes + L.o.gguf_bytes + L.gate.gguf_bytes + L.up.gguf_bytes +
+           L.down.gguf_bytes + (uint64_t)H * 4 * (c.gemma ? 4 : 2) + (c.qk_norm ? 2ull * c.hd * 4 : 0);
+  e->weight_bytes_per_token = wpt;
+
+  e->resA = (float*)e->state.take((size_t)H * 4);
+  e->resB = (float*)e->state.take((size_t)H * 4);
+  e->delta = (float*)e->state.take((size_t)H * 4);
+  e->qkv = (float*)e->state.take((size_t)(qdim + 2 * kvdim) * 4);
+  e->attn = (float*)e->state.take((size_t)qdim * 4);
+  e->ff = (float*)e->state.take((size_t)c.ffn * 4);
+  e->logits = (float*)e->state.take((size_t)c.vocab * 4);
+  e->part = (float*)e->state.take((size_t)c.kv_heads * e->nchunk * G * (c.hd + 2) * 4);
+  e->cand = (Candidate*)e->state.take((size_t)e->groups * 8);
+  e->cnt = (uint32_t*)e->state.take((size_t)c.kv_heads * 4);
+  e->st = (DevState*)e->state.take(sizeof(DevState));
+  e->samp = (DevSampling*)e->state.take(sizeof(DevSampling));
+  e->hist = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
+  e->gen = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
+  e->pen_bits = (uint32_t*)e->state.take(bits_words * 4);
+  e->seen_bits = (uint32_t*)e->state.take(bits_words * 4);
+  HIP_OK(hipMemset((void*)e->resA, 0, e->state.capacity() - 2 * align256(kv_bytes) * c.layers));
+  for (const LayerDev& L : e->layers) {
+    HIP_OK(hipMemset(L.kc, 0, kv_bytes));
+    HIP_OK(hipMemset(L.vc, 0, kv_bytes));
+  }
+  HIP_OK(hipHostMalloc((void**)&e->h_state, sizeof(DevState), hipHostMallocDefault));
+  HIP_OK(hipHostMalloc((void**)&e->h_tok, 64, hipHostMallocDefault));
+  HIP_OK(hipHostMalloc((void**)&e->h_samp, sizeof(DevSampling), hipHostMallocDefault));
+  std::memset(e->h_samp, 0, sizeof(DevSampling));
+  HIP_OK(hipDeviceSynchronize());
+
+  HIP_OK(init_kernel_attributes());
+  build_steps(e.get());
+  for (const Launch& L : e->step_logits)
+    if (L.shmem > lds_limit())
+      throw Error(CHONK_EINVAL, "kernel " + L.name + " needs " + std::to_string(L.shmem) + " bytes of LDS, above the " +
+                                    std::to_string(lds_limit()) + "-byte limit of this device");
+  capture(e.get(), e->step_plain, &e->graph_plain, &e->exec_plain);
+  capture(e.get(), e->step_logits, &e->graph_logits, &e->exec_logits);
+  *out = e.release();
+}
+
+void upload_state_fields(chonk_engine* e, const DevState& s) {
+  *e->h_state = s;
+  HIP_OK(hipMemcpyAsync(e->st, e->h_state, sizeof(DevState), hipMemcpyHostToDevice, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+}
+
+DevState read_state(chonk_engine* e) {
+  HIP_OK(hipMemcpyAsync(e->h_state, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  return *e->h_state;
+}
+
+// JS Math.round for the penalty milli value (round half up).
+double js_round(double x) { return std::floor(x + 0.5); }
+
+DevSampling make_sampling(chonk_engine* e, const chonk_sampling* s, bool stage1, bool seen) {
+  DevSampling d{};
+  const double temperature = s ? s->temperature : 0.0;
+  const double top_p = s ? s->top_p : 1.0;
+  int top_k = s ? s->top_k : 0;
+  const double rp = s ? s->repetition_penalty : 1.0;
+  if (top_k < 0) top_k = 0;
+  d.temperature = temperature;
+  d.top_p = std::min(std::max(top_p, 0.0), 1.0);
+  d.top_k = top_k;
+  d.seed = s ? s->seed : 0;
+  d.sample_mode = (temperature > 0 || top_p < 1 || top_k > 0) ? 1 : 0;  // needsSamplingReadback
+  d.stage1_penalty = stage1 && rp > 1 ? 1 : 0;
+  d.stage1_pen = (float)js_round(rp * 1000) / 1000.0f;
+  d.repetition_penalty = std::max(rp, 1e-6);
+  d.seen_penalty = seen && d.repetition_penalty != 1 ? 1 : 0;
+  d.n_eos = (int32_t)e->eos.size();
+  for (int i = 0; i < d.n_eos && i < 16; ++i) d.eos[i] = e->eos[i];
+  return d;
+}
+
+void upload_sampling(chonk_engine* e, const DevSampling& d) {
+  if (e->samp_valid && std::memcmp(&e->last_samp, &d, sizeof d) == 0) return;
+  *e->h_samp = d;
+  HIP_OK(hipMemcpyAsync(e->samp, e->h_samp, sizeof d, hipMemcpyHostToDevice, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  e->last_samp = d;
+  e->samp_valid = true;
+}
+
+void upload_bits(chonk_engine* e, uint32_t* dst, const int32_t* ids, size_t n) {
+  std::vector<uint32_t> bits((size_t)(e->cfg.vocab + 31) / 32, 0u);
+  for (size_t i = 0; i < n; ++i) {
+    const int32_t id = ids[i];
+    if (id >= 0 && id < e->cfg.vocab) bits[(size_t)id >> 5] |= 1u << (id & 31);
+  }
+  HIP_OK(hipMemcpy(dst, bits.data(), bits.size() * 4, hipMemcpyHostToDevice));
+}
+
+void put_token(chonk_engine* e, int position, int32_t token) {
+  if (e->known_token_pos == position && e->known_token == token) return;
+  *e->h_tok = token;
+  HIP_OK(hipMemcpyAsync(e->hist + position, e->h_tok, 4, hipMemcpyHostToDevice, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  e->known_token_pos = position;
+  e->known_token = token;
+}
+
+void check_token(const chonk_engine* e, int32_t token) {
+  if (token < 0 || token >= e->cfg.vocab)
+    throw Error(CHONK_EINVAL, "token id " + std::to_string(token) + " outside embedding table");
+}
+
+void engine_reset(chonk_engine* e) {
+  HIP_OK(hipStreamSynchronize(e->stream));
+  const size_t kv_bytes = (size_t)e->cfg.kv_heads * e->cfg.hd * e->cfg.ctx * e->kv_elem;
+  for (const LayerDev& L : e->layers) {
+    HIP_OK(hipMemsetAsync(L.kc, 0, kv_bytes, e->stream));
+    HIP_OK(hipMemsetAsync(L.vc, 0, kv_bytes, e->stream));
+  }
+  DevState s{};
+  upload_state_fields(e, s);
+  e->pos = 0;
+  e->known_token_pos = -1;
+  e->logits_valid = false;
+}
+
+int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
+                  size_t n_pen, const int32_t* seen, size_t n_seen) {
+  if (e->pos >= e->cfg.ctx)
+    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+  check_token(e, token);
+  put_token(e, e->pos, token);
+  if (need_logits) {
+    // argmax(): the penalty list is the last `context` ids (:1649-1653)
+    const double rp = s ? s->repetition_penalty : 1.0;
+    const bool stage1 = rp > 1 && n_pen > 0;
+    const size_t keep = std::min(n_pen, (size_t)e->cfg.ctx);
+    if (stage1) upload_bits(e, e->pen_bits, pen + (n_pen - keep), keep);
+    const DevSampling d = make_sampling(e, s, stage1, n_seen > 0);
+    if (d.sample_mode && d.seen_penalty) upload_bits(e, e->seen_bits, seen, n_seen);
+    upload_sampling(e, d);
+    HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    HIP_OK(hipMemcpyAsync(e->h_state, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
+    HIP_OK(hipStreamSynchronize(e->stream));
+    const DevState st = *e->h_state;
+    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    e->pos += 1;
+    e->known_token_pos = e->pos;
+    e->known_token = st.last_token;
+    e->logits_valid = true;
+    return st.last_token;
+  }
+  HIP_OK(hipGraphLaunch(e->exec_plain, e->stream));
+  e->pos += 1;
+  return 0;
+}
+
+int64_t common_prefix(const std::vector<int32_t>& a, const int32_t* b, size_t nb) {
+  const size_t n = std::min(a.size(), nb);
+  size_t i = 0;
+  while (i < n && a[i] == b[i]) ++i;
+  return (int64_t)i;
+}
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// generateLlamaWgsl's option defaults (:255-262): temperature 0, topP 1,
+// topK 0, repetitionPenalty = opts ?? def.defaultRepetitionPenalty ?? 1
+// (a non-positive or non-finite value means "not given").
+chonk_sampling effective_sampling(const chonk_engine* e, const chonk_sampling* s_in) {
+  chonk_sampling s{};
+  s.temperature = 0;
+  s.top_p = 1;
+  s.top_k = 0;
+  s.repetition_penalty = e->def.default_repetition_penalty > 0 ? e->def.default_repetition_penalty : 1.0;
+  if (s_in) {
+    s.temperature = s_in->temperature;
+    s.top_p = s_in->top_p;
+    s.top_k = s_in->top_k;
+    s.seed = s_in->seed;
+    if (s_in->repetition_penalty > 0 && std::isfinite(s_in->repetition_penalty)) s.repetition_penalty = s_in->repetition_penalty;
+  }
+  return s;
+}
+
+void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new, const chonk_sampling* s_in,
+              std::vector<int32_t>* out, chonk_gen_stats* stats) {
+  const ModelCfg& c = e->cfg;
+  const int64_t max = std::min<int64_t>(max_new > 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
+  const chonk_sampling s = effective_sampling(e, s_in);
+  for (size_t i = 0; i < n_prompt; ++i) check_token(e, prompt[i]);
+  const double t0 = now_ms();
+  int64_t prefix = common_prefix(e->cached_ids, prompt, n_prompt);
+  if (prefix != (int64_t)e->cached_ids.size()) {
+    engine_reset(e);
+    e->cached_ids.clear();
+    e->has_cached_next = false;
+    prefix = 0;
+  }
+  const size_t n_suffix = n_prompt - (size_t)prefix;
+  if ((int64_t)e->pos + (int64_t)n_suffix > c.ctx)
+    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+  auto is_eos = [&](int32_t id) { return std::find(e->eos.begin(), e->eos.end(), id) != e->eos.end(); };
+
+  // penalty list = prompt (+ generated ids, appended on the device)
+  const bool stage1 = s.repetition_penalty > 1;
+  DevSampling d = make_sampling(e, &s, stage1, true);
+  if (stage1 || d.seen_penalty) {
+    upload_bits(e, e->pen_bits, prompt, n_prompt);
+    upload_bits(e, e->seen_bits, prompt, n_prompt);
+  }
+  upload_sampling(e, d);
+
+  DevState st{};
+  st.pos = e->pos;
+  st.generating = max > 0 ? 1 : 0;
+  st.max_generated = (int32_t)std::max<int64_t>(max, 0);
+  int32_t next = 0;
+  bool need_decode_seed = false;
+  double t_prefill_end = t0;
+  if (n_suffix == 0) {
+    next = e->has_cached_next ? e->cached_next : 0;
+    need_decode_seed = true;
+  } else {
+    std::vector<int32_t> suf(prompt + prefix, prompt + n_prompt);
+    HIP_OK(hipMemcpy(e->hist + e->pos, suf.data(), suf.size() * 4, hipMemcpyHostToDevice));
+    upload_state_fields(e, st);
+    for (size_t i = 0; i + 1 < n_suffix; ++i) HIP_OK(hipGraphLaunch(e->exec_plain, e->stream));
+    HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    st = read_state(e);
+    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    e->pos = st.pos;
+    next = st.last_token;
+    e->logits_valid = true;
+    t_prefill_end = now_ms();
+  }
+  std::vector<int32_t> generated;
+  if (max > 0) {
+    if (need_decode_seed) {
+      // first generated id comes from the cache (or is 0); seed the device loop with it
+      *e->h_tok = next;
+      HIP_OK(hipMemcpy(e->hist + e->pos, e->h_tok, 4, hipMemcpyHostToDevice));
+      HIP_OK(hipMemcpy(e->gen, e->h_tok, 4, hipMemcpyHostToDevice));
+      if (stage1 || d.seen_penalty) {
+        std::vector<int32_t> ids(prompt, prompt + n_prompt);
+        ids.push_back(next);
+        upload_bits(e, e->pen_bits, ids.data(), ids.size());
+        upload_bits(e, e->seen_bits, ids.data(), ids.size());
+      }
+      st.pos = e->pos;
+      st.generating = 1;
+      st.n_generated = 1;
+      st.stopped = (is_eos(next) || max <= 1) ? 1 : 0;
+      upload_state_fields(e, st);
+    }
+    // decode: up to max-1 further steps, in batches between host checks
+    int64_t remaining = max - 1;
+    while (remaining > 0 && !st.stopped) {
+      const int64_t batch = std::min<int64_t>(remaining, 32);
+      for (int64_t i = 0; i < batch; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+      remaining -= batch;
+      st = read_state(e);
+      if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    }
+    st = read_state(e);
+    generated.resize((size_t)st.n_generated);
+    if (!generated.empty())
+      HIP_OK(hipMemcpy(generated.data(), e->gen, generated.size() * 4, hipMemcpyDeviceToHost));
+    e->pos = st.pos;
+    next = generated.empty() ? next : generated.back();
+  }
+  // leave the device in API mode
+  st.generating = 0;
+  st.stopped = 0;
+  upload_state_fields(e, st);
+  e->known_token_pos = -1;
+  const double t_end = now_ms();
+  e->cached_ids.assign(prompt, prompt + n_prompt);
+  e->cached_ids.insert(e->cached_ids.end(), generated.begin(), generated.end());
+  const bool last_eos = !generated.empty() && is_eos(generated.back());
+  e->has_cached_next = !last_eos;
+  e->cached_next = next;
+  *out = generated;
+  if (stats) {
+    stats->prefill_ms = t_prefill_end - t0;
+    stats->decode_ms = t_end - t_prefill_end;
+    stats->prompt_tokens = (int32_t)n_prompt;
+    stats->generated_tokens = (int32_t)generated.size();
+    stats->tokens_per_sec = (double)generated.size() / std::max((t_end - t0) / 1000.0, 1e-3);
+  }
+}
+
+// The reference loop (:266-313) stepped from the host through run_token.
+void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new,
+                      const chonk_sampling* s_in, chonk_token_callback cb, void* user, std::vector<int32_t>* out,
+                      chonk_gen_stats* stats) {
+  const int64_t max = std::min<int64_t>(max_new > 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
+  const chonk_sampling s = effective_sampling(e, s_in);
+  for (size_t i = 0; i < n_prompt; ++i) check_token(e, prompt[i]);
+  auto is_eos = [&](int32_t id) { return std::find(e->eos.begin(), e->eos.end(), id) != e->eos.end(); };
+  const double t0 = now_ms();
+  int64_t prefix = common_prefix(e->cached_ids, prompt, n_prompt);
+  if (prefix != (int64_t)e->cached_ids.size()) {
+    engine_reset(e);
+    e->cached_ids.clear();
+    e->has_cached_next = false;
+    prefix = 0;
+  }
+  int32_t next = 0;
+  const size_t n_suffix = n_prompt - (size_t)prefix;
+  if (n_suffix == 0 && e->has_cached_next) {
+    next = e->cached_next;
+  } else {
+    for (size_t i = 0; i < n_suffix; ++i) {
+      const bool need = i + 1 == n_suffix;
+      const size_t n_pen = (size_t)prefix + i + 1;
+      next = run_token(e, prompt[prefix + i], need, &s, prompt, need ? n_pen : 0, prompt, need ? n_pen : 0);
+    }
+  }
+  HIP_OK(hipStreamSynchronize(e->stream));
+  const double t_prefill_end = now_ms();
+  std::vector<int32_t> generated;
+  std::vector<int32_t> ids(prompt, prompt + n_prompt);
+  for (int64_t step = 0; step < max; ++step) {
+    if (cb && cb(user, 0, 0)) break;
+    generated.push_back(next);
+    ids.push_back(next);
+    if (cb) cb(user, 1, next);
+    if (is_eos(next)) break;
+    if (step + 1 >= max) break;
+    next = run_token(e, next, true, &s, ids.data(), ids.size(), ids.data(), ids.size());
+  }
+  const double t_end = now_ms();
+  e->cached_ids = ids;
+  e->has_cached_next = !(!generated.empty() && is_eos(generated.back()));
+  e->cached_next = next;
+  *out = generated;
+  if (stats) {
+    stats->prefill_ms = t_prefill_end - t0;
+    stats->decode_ms = t_end - t_prefill_end;
+    stats->prompt_tokens = (int32_t)n_prompt;
+    stats->generated_tokens = (int32_t)generated.size();
+    stats->tokens_per_sec = (double)generated.size() / std::max((t_end - t0) / 1000.0, 1e-3);
+  }
+}
+
+}  // namespace
+}  // namespace chonk
+
+// ---- C ABI ------------------------------------------------------------------------
+
+extern "C" {
+
+const char* chonk_last_error(void) { return g_last_error.c_str(); }
+
+const char* chonk_engine_last_error(const chonk_engine* e) { return e ? e->err.c_str() : g_last_error.c_str(); }
+
+int chonk_engine_create(const chonk_model_def* def, const char* path, chonk_engine** out) {
+  return api_free([&] {
+    if (!path) throw Error(CHONK_EINVAL, "null path");
+    std::unique_ptr<ByteSource> src;
+    try {
+      src = open_byte_source(path);
+    } catch (const std::exception& x) {
+      throw Error(CHONK_EIO, x.what());
+    }
+    create_engine(def, std::move(src), path, out);
+  });
+}
+
+int chonk_engine_create_from_memory(const chonk_model_def* def, const void* bytes, size_t n, chonk_engine** out) {
+  return api_free([&] {
+    if (!bytes) throw Error(CHONK_EINVAL, "null buffer");
+    create_engine(def, memory_byte_source(bytes, n), "<memory>", out);
+  });
+}
+
+int chonk_engine_destroy(chonk_engine* e) {
+  if (!e) return CHONK_OK;
+  bool expected = false;
+  if (!e->busy.compare_exchange_strong(expected, true)) {
+    g_last_error = "engine call already in progress";
+    return CHONK_EBUSY;
+  }
+  engine_free(e);
+  return CHONK_OK;
+}
+
+int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
+  if (!e || !out) {
+    g_last_error = "null argument";
+    return CHONK_EINVAL;
+  }
+  const ModelCfg& c = e->cfg;
+  out->hidden = c.hidden;
+  out->ffn = c.ffn;
+  out->vocab = c.vocab;
+  out->layers = c.layers;
+  out->heads = c.heads;
+  out->kv_heads = c.kv_heads;
+  out->head_dim = c.hd;
+  out->context = c.ctx;
+  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : 2;
+  out->qk_norm = c.qk_norm;
+  out->interleaved_rope = c.interleaved;
+  out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;
+  out->weight_bytes_per_token = e->weight_bytes_per_token;
+  out->device_bytes = e->weights.capacity() + e->state.capacity();
+  out->kernels_per_step = (int32_t)e->step_logits.size();
+  return CHONK_OK;
+}
+
+int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, const chonk_sampling* s,
+                           const int32_t* penalized, size_t n_penalized, const int32_t* seen, size_t n_seen,
+                           int32_t* out_token) {
+  return api(e, [&] {
+    const int32_t t = run_token(e, token, need_logits != 0, s, penalized, penalized ? n_penalized : 0, seen,
+                                seen ? n_seen : 0);
+    if (out_token) *out_token = t;
+  });
+}
+
+int chonk_engine_generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new_tokens,
+                          const chonk_sampling* s, int32_t* out_ids, size_t out_cap, size_t* n_out,
+                          chonk_gen_stats* stats) {
+  return api(e, [&] {
+    if (!prompt && n_prompt) throw Error(CHONK_EINVAL, "null prompt");
+    std::vector<int32_t> ids;
+    generate(e, prompt, n_prompt, max_new_tokens, s, &ids, stats);
+    const size_t n = std::min(ids.size(), out_cap);
+    if (out_ids && n) std::memcpy(out_ids, ids.data(), n * 4);
+    if (n_out) *n_out = ids.size();
+  });
+}
+
+int chonk_engine_generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new_tokens,
+                                  const chonk_sampling* s, chonk_token_callback callback, void* user,
+                                  int32_t* out_ids, size_t out_cap, size_t* n_out, chonk_gen_stats* stats) {
+  return api(e, [&] {
+    if (!prompt && n_prompt) throw Error(CHONK_EINVAL, "null prompt");
+    std::vector<int32_t> ids;
+    generate_stepped(e, prompt, n_prompt, max_new_tokens, s, callback, user, &ids, stats);
+    const size_t n = std::min(ids.size(), out_cap);
+    if (out_ids && n) std::memcpy(out_ids, ids.data(), n * 4);
+    if (n_out) *n_out = ids.size();
+  });
+}
+
+int chonk_engine_conversation(chonk_engine* e, int32_t* ids, size_t cap, size_t* n_cached, int32_t* next_id) {
+  return api(e, [&] {
+    const size_t n = std::min(cap, e->cached_ids.size());
+    if (ids && n) std::memcpy(ids, e->cached_ids.data(), n * 4);
+    if (n_cached) *n_cached = e->cached_ids.size();
+    if (next_id) *next_id = e->has_cached_next ? e->cached_next : -1;
+  });
+}
+
+int chonk_engine_reset(chonk_engine* e) { return api(e, [&] { engine_reset(e); }); }
+
+int chonk_engine_reset_conversation(chonk_engine* e) {
+  return api(e, [&] {
+    engine_reset(e);
+    e->cached_ids.clear();
+    e->has_cached_next = false;
+  });
+}
+
+int chonk_engine_position(const chonk_engine* e, int32_t* out_pos) {
+  if (!e || !out_pos) {
+    g_last_error = "null argument";
+    return CHONK_EINVAL;
+  }
+  *out_pos = e->pos;
+  return CHONK_OK;
+}
+
+int chonk_engine_read_logits(chonk_engine* e, float* out, size_t n) {
+  return api(e, [&] {
+    if (!e->logits_valid) throw Error(CHONK_EINVAL, "no step has computed logits yet");
+    if (!out || n < (size_t)e->cfg.vocab) throw Error(CHONK_EINVAL, "output buffer smaller than vocab");
+    HIP_OK(hipStreamSynchronize(e->stream));
+    HIP_OK(hipMemcpy(out, e->logits, (size_t)e->cfg.vocab * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int chonk_engine_read_buffer(chonk_engine* e, int32_t which, void* out, size_t n_bytes) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    const void* src = nullptr;
+    size_t bytes = 0;
+    switch (which) {
+      case 0: src = e->resA; bytes = (size_t)c.hidden * 4; break;
+      case 1: src = e->attn; bytes = (size_t)c.heads * c.hd * 4; break;
+      case 2: src = e->cand; bytes = (size_t)e->groups * 8; break;
+      case 3: src = e->qkv; bytes = (size_t)(c.heads + 2 * c.kv_heads) * c.hd * 4; break;
+      default: throw Error(CHONK_EINVAL, "unknown buffer id");
+    }
+    if (!out || n_bytes < bytes) throw Error(CHONK_EINVAL, "output buffer too small");
+    HIP_OK(hipStreamSynchronize(e->stream));
+    HIP_OK(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
+  });
+}
+
+int chonk_engine_read_kv(chonk_engine* e, int32_t layer, int32_t is_value, int32_t pos, float* out) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (layer < 0 || layer >= c.layers || pos < 0 || pos >= c.ctx || !out) throw Error(CHONK_EINVAL, "bad layer/position");
+    HIP_OK(hipStreamSynchronize(e->stream));
+    const LayerDev& L = e->layers[layer];
+    const uint8_t* base = (const uint8_t*)(is_value ? L.vc : L.kc);
+    std::vector<uint8_t> row((size_t)c.hd * e->kv_elem);
+    for (int h = 0; h < c.kv_heads; ++h) {
+      HIP_OK(hipMemcpy(row.data(), base + (((size_t)h * c.ctx + pos) * c.hd) * e->kv_elem, row.size(),
+                       hipMemcpyDeviceToHost));
+      for (int d = 0; d < c.hd; ++d) {
+        if (e->kv_elem == 2) {
+          uint16_t hv;
+          std::memcpy(&hv, row.data() + 2 * d, 2);
+          out[h * c.hd + d] = f16_to_f32(hv);
+        } else {
+          std::memcpy(&out[h * c.hd + d], row.data() + 4 * d, 4);
+        }
+      }
+    }
+  });
+}
+
+int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (pos < 0 || pos >= c.ctx) throw Error(CHONK_EINVAL, "position outside the context");
+    for (int i = 0; i < c.layers; ++i)
+      HIP_OK(launch_fill_kv(e->layers[i].kc, e->layers[i].vc, c.kv_heads, c.ctx, c.hd, pos, e->kv_elem == 2,
+                            seed + 1000003ull * i, e->stream));
+    DevState st{};
+    st.pos = pos;
+    upload_state_fields(e, st);
+    e->pos = pos;
+    e->known_token_pos = -1;
+    e->cached_ids.clear();
+    e->has_cached_next = false;
+  });
+}
+
+int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps, double* ms_total) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (n_warmup < 0 || n_steps <= 0) throw Error(CHONK_EINVAL, "bad step counts");
+    if ((int64_t)e->pos + n_warmup + n_steps > c.ctx)
+      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    DevSampling d = make_sampling(e, nullptr, false, false);
+    upload_sampling(e, d);
+    // the history slot at the current position must hold a token
+    DevState st = read_state(e);
+    int32_t tok = 0;
+    HIP_OK(hipMemcpy(&tok, e->hist + e->pos, 4, hipMemcpyDeviceToHost));
+    check_token(e, tok);
+    for (int i = 0; i < n_warmup; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    hipEvent_t a, b;
+    HIP_OK(hipEventCreate(&a));
+    HIP_OK(hipEventCreate(&b));
+    HIP_OK(hipEventRecord(a, e->stream));
+    for (int i = 0; i < n_steps; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    HIP_OK(hipEventRecord(b, e->stream));
+    HIP_OK(hipEventSynchronize(b));
+    float ms = 0;
+    HIP_OK(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    st = read_state(e);
+    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    e->pos = st.pos;
+    e->known_token_pos = -1;
+    e->logits_valid = true;
+    e->cached_ids.clear();
+    e->has_cached_next = false;
+    if (ms_total) *ms_total = ms;
+  });
+}
+
+int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
+                              size_t name_len, uint64_t* bytes) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (kernel_id < 0 || kernel_id >= (int32_t)e->step_logits.size() || reps <= 0)
+      throw Error(CHONK_EINVAL, "bad kernel id or repetitions");
+    const Launch& L = e->step_logits[(size_t)kernel_id];
+    if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
+    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    const DevState saved = read_state(e);
+    DevState st = saved;
+    st.stopped = 0;
+    st.generating = 0;
+    upload_state_fields(e, st);
+    Launch run = L;
+    if (run.kind == Launch::MV) run.mv.advance_pos = 0;
+    enqueue(run, e->stream);  // warm
+    hipEvent_t a, b;
+    HIP_OK(hipEventCreate(&a));
+    HIP_OK(hipEventCreate(&b));
+    HIP_OK(hipEventRecord(a, e->stream));
+    for (int i = 0; i < reps; ++i) enqueue(run, e->stream);
+    HIP_OK(hipEventRecord(b, e->stream));
+    HIP_OK(hipEventSynchronize(b));
+    float ms = 0;
+    HIP_OK(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    upload_state_fields(e, saved);
+    if (avg_us) *avg_us = (double)ms * 1000.0 / reps;
+    if (name && name_len) std::snprintf(name, name_len, "%s", L.name.c_str());
+    if (bytes) {
+      uint64_t by = L.weight_bytes;
+      if (L.kind == Launch::MV) {
+        by += (uint64_t)L.mv.k * 4;
+        for (int i = 0; i < L.mv.nseg; ++i) by += (uint64_t)L.mv.seg[i].n_out * 4;
+      } else if (L.kind == Launch::ATTN) {
+        const int pos = e->pos;
+        const int w = L.at.window;
+        const int start = (w != 0 && pos + 1 > w) ? pos + 1 - w : 0;
+        by += 2ull * c.kv_heads * c.hd * (uint64_t)(pos + 1 - start) * e->kv_elem;
+        by += (uint64_t)(c.heads + 2 * c.kv_heads) * c.hd * 4 + (uint64_t)c.heads * c.hd * 4;
+      }
+      *bytes = by;
+    }
+  });
+}
+
+int chonk_dequant(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len, float* out) {
+  return api_free([&] {
+    TypeTraits t;
+    if (!type_traits(ggml_type, &t) || !t.quantized) throw Error(CHONK_EINVAL, "unsupported GGUF tensor type " + type_name(ggml_type));
+    if (n_rows <= 0 || row_len <= 0 || row_len % t.block_elems || row_len % 32 || !blocks || !out)
+      throw Error(CHONK_EINVAL, "bad dequant shape");
+    HIP_OK(hipSetDevice(device));
+    const Stripes st = repack(ggml_type, (const uint8_t*)blocks, n_rows, row_len);
+    QMat q{};
+    q.type = (int32_t)ggml_type;
+    q.n = (int32_t)n_rows;
+    q.k = (int32_t)row_len;
+    std::vector<void*> bufs;
+    const uint8_t** dst[4] = {&q.s0, &q.s1, &q.s2, &q.s3};
+    float* d_out = nullptr;
+    try {
+      for (int i = 0; i < 4; ++i) {
+        if (st.s[i].empty()) continue;
+        void* p;
+        HIP_OK(hipMalloc(&p, st.s[i].size()));
+        bufs.push_back(p);
+        HIP_OK(hipMemcpy(p, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+        *dst[i] = (const uint8_t*)p;
+      }
+      HIP_OK(hipMalloc((void**)&d_out, (size_t)(n_rows * row_len) * 4));
+      HIP_OK(launch_dequant(q, d_out, nullptr));
+      HIP_OK(hipDeviceSynchronize());
+      HIP_OK(hipMemcpy(out, d_out, (size_t)(n_rows * row_len) * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      for (void* p : bufs) (void)hipFree(p);
+      if (d_out) (void)hipFree(d_out);
+      throw;
+    }
+    for (void* p : bufs) (void)hipFree(p);
+    (void)hipFree(d_out);
+  });
+}
+
+int chonk_matvec(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
+                 const float* x, float* y, int32_t reps, double* avg_us) {
+  return api_free([&] {
+    TypeTraits t;
+    if (!type_traits(ggml_type, &t) || !t.quantized) throw Error(CHONK_EINVAL, "unsupported GGUF tensor type " + type_name(ggml_type));
+    if (n_rows <= 0 || row_len <= 0 || row_len % t.block_elems || row_len % 32 || row_len > 32768 || !blocks || !x || !y)
+      throw Error(CHONK_EINVAL, "bad matvec shape");
+    HIP_OK(hipSetDevice(device));
+    const Stripes st = repack(ggml_type, (const uint8_t*)blocks, n_rows, row_len);
+    QMat q{};
+    q.type = (int32_t)ggml_type;
+    q.n = (int32_t)n_rows;
+    q.k = (int32_t)row_len;
+    std::vector<void*> bufs;
+    auto dev = [&](size_t n) {
+      void* p;
+      HIP_OK(hipMalloc(&p, n));
+      bufs.push_back(p);
+      return p;
+    };
+    hipStream_t s = nullptr;
+    try {
+      const uint8_t** dst[4] = {&q.s0, &q.s1, &q.s2, &q.s3};
+      for (int i = 0; i < 4; ++i) {
+        if (st.s[i].empty()) continue;
+        void* p = dev(st.s[i].size());
+        HIP_OK(hipMemcpy(p, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+        *dst[i] = (const uint8_t*)p;
+      }
+      float* d_x = (float*)dev((size_t)row_len * 4);
+      float* d_y = (float*)dev((size_t)n_rows * 4);
+      DevState* d_st = (DevState*)dev(sizeof(DevState));
+      HIP_OK(hipMemset(d_st, 0, sizeof(DevState)));
+      HIP_OK(hipMemcpy(d_x, x, (size_t)row_len * 4, hipMemcpyHostToDevice));
+      MvArgs a{};
+      a.nseg = 1;
+      a.k = (int32_t)row_len;
+      a.pro = PRO_PLAIN;
+      a.epi = EPI_STORE;
+      a.in = d_x;
+      a.st = d_st;
+      plan_seg(a.seg[0], q, (int)n_rows, false, 0);
+      a.seg[0].out = d_y;
+      const int grid = seg_wgs(a.seg[0]);
+      const size_t shmem = mv_shared_bytes((int)row_len, a.seg[0].tile);
+      HIP_OK(init_kernel_attributes());
+      if (shmem > lds_limit()) throw Error(CHONK_EINVAL, "row length too large for the LDS limit");
+      HIP_OK(hipStreamCreate(&s));
+      HIP_OK(launch_matvec(a, grid, shmem, s));
+      HIP_OK(hipStreamSynchronize(s));
+      if (reps > 0) {
+        hipEvent_t e0, e1;
+        HIP_OK(hipEventCreate(&e0));
+        HIP_OK(hipEventCreate(&e1));
+        HIP_OK(hipEventRecord(e0, s));
+        for (int i = 0; i < reps; ++i) HIP_OK(launch_matvec(a, grid, shmem, s));
+        HIP_OK(hipEventRecord(e1, s));
+        HIP_OK(hipEventSynchronize(e1));
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        if (avg_us) *avg_us = (double)ms * 1000.0 / reps;
+      }
+      HIP_OK(hipMemcpy(y, d_y, (size_t)n_rows * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      if (s) (void)hipStreamDestroy(s);
+      for (void* p : bufs) (void)hipFree(p);
+      throw;
+    }
+    (void)hipStreamDestroy(s);
+    for (void* p : bufs) (void)hipFree(p);
+  });
+}
+
+int chonk_write_synthetic_gguf(const chonk_synth_config* c, const char* path, int32_t n_threads) {
+  return api_free([&] {
+    if (!c || !path || !c->arch || !c->recipe) throw Error(CHONK_EINVAL, "null argument");
+    SynthConfig s;
+    s.arch = c->arch;
+    s.recipe = c->recipe;
+    s.hidden = c->hidden;
+    s.layers = c->layers;
+    s.heads = c->heads;
+    s.kv_heads = c->kv_heads;
+    s.head_dim = c->head_dim;
+    s.ffn = c->ffn;
+    s.vocab = c->vocab;
+    s.context_length = c->context_length;
+    s.rope_theta = c->rope_theta;
+    s.norm_eps = c->norm_eps;
+    s.sliding_window = c->sliding_window;
+    s.seed = c->seed;
+    s.weight_std = c->weight_std > 0 ? c->weight_std : 0.02f;
+    s.norm_std = c->norm_std > 0 ? c->norm_std : 0.02f;
+    try {
+      write_synthetic_gguf(s, path, n_threads);
+    } catch (const std::exception& x) {
+      throw Error(CHONK_EIO, x.what());
+    }
+  });
+}
+
+int chonk_write_shards(const char* gguf_path, const char* out_dir, uint64_t shard_size, const char* quant) {
+  return api_free([&] {
+    if (!gguf_path || !out_dir) throw Error(CHONK_EINVAL, "null argument");
+    try {
+      write_shards(gguf_path, out_dir, shard_size, quant ? quant : "");
+    } catch (const std::exception& x) {
+      throw Error(CHONK_EIO, x.what());
+    }
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// Kernel argument blocks and launchers of the decode step.
+//
+// One decode step of an L-layer model is 5L + 2 launches:
+//   per layer  qkv      RMSNorm (or embedding gather / residual re-norm) fused
+//                       into the q|k|v dequant-matvec
+//              attn     qk-norm + RoPE + K/V store + split-K GQA attention with
+//                       an in-kernel last-arriver combine
+//              oproj    o-projection (+ residual add)
+//              gateup   RMSNorm + gate|up matvec + SiLU/GELU-tanh product
+//              down     down projection (+ residual add)
+//   final      lmhead   final RMSNorm + lm_head matvec + per-256-id group
+//                       argmax with the repetition penalty (ARGMAX_STAGE1)
+//              select   global argmax (ARGMAX_STAGE2) or the candidate
+//                       sampler, token bookkeeping, position advance
+#pragma once
+
+#include "device_common.h"
+
+namespace chonk {
+
+enum ProMode : int32_t {
+  PRO_PLAIN = 0,         // xs = in
+  PRO_NORM = 1,          // xs = rmsnorm(in) * w_norm
+  PRO_EMBED_NORM = 2,    // r = embed(hist[pos]) * scale; WG0 writes r; xs = rmsnorm(r) * w_norm
+  PRO_RES_NORM = 3,      // r = clamp(in + rmsnorm(delta) * w_delta, +-65000); WG0 writes r; xs = rmsnorm(r) * w_norm
+};
+
+enum EpiMode : int32_t {
+  EPI_STORE = 0,    // out[n] = acc
+  EPI_ADD = 1,      // out[n] = add[n] + acc
+  EPI_GLU_SILU = 2, // out[n] = silu(gate_n) * up_n
+  EPI_GLU_GELU = 3, // out[n] = gelu_tanh(gate_n) * up_n
+  EPI_LOGITS = 4,   // logits[n] = acc; group candidate per 256 rows
+};
+
+struct MvSeg {
+  QMat w;            // matrix (GLU: gate)
+  QMat w2;           // GLU: up
+  float* out;
+  const float* add;  // EPI_ADD residual input
+  int32_t n_out;     // output rows
+  int32_t tile;      // output rows per workgroup
+  int32_t lpr;       // lanes per row (power of two, <= 64)
+  int32_t wg_begin;  // first workgroup of this segment
+};
+
+struct MvArgs {
+  MvSeg seg[3];
+  int32_t nseg;
+  int32_t pro;
+  int32_t epi;
+  int32_t k;              // activation length
+  const float* in;
+  const float* delta;
+  const float* w_delta;
+  const float* w_norm;
+  float* res_out;
+  QMat embed;
+  float embed_scale;
+  float eps;
+  const int32_t* hist;
+  int32_t vocab;
+  int32_t advance_pos;    // WG0 advances st->pos when done (steps without logits)
+  const uint32_t* pen_bits;
+  const DevSampling* samp;
+  Candidate* cand;
+  DevState* st;
+};
+
+struct AttnArgs {
+  const float* qkv;       // q[heads*hd] | k[kv*hd] | v[kv*hd]
+  const float* qn_w;      // per-head q RMSNorm weight (null: none)
+  const float* kn_w;
+  void* kc;               // [kv_heads][C][hd], half or float
+  void* vc;
+  float* part;            // [kv_heads][nchunk][G][hd + 2]
+  uint32_t* cnt;          // [kv_heads], zero between launches
+  float* out;             // [heads*hd]
+  DevState* st;
+  int32_t heads, kv_heads, hd, ctx, window, chunk, nchunk;
+  uint32_t theta;         // Math.round(ropeTheta)
+  int32_t interleaved, kv_f16;
+  float eps, scale;
+};
+
+struct SelArgs {
+  const Candidate* cand;
+  int32_t groups;
+  int32_t vocab;
+  int32_t ctx;
+  const DevSampling* samp;
+  uint32_t* pen_bits;
+  uint32_t* seen_bits;
+  int32_t* hist;          // [ctx + 1]
+  int32_t* gen;           // [ctx + 1]
+  DevState* st;
+};
+
+// Launch parameter helpers -------------------------------------------------------
+size_t mv_shared_bytes(int k, int max_tile_rows);
+size_t attn_shared_bytes(int group, int hd, int chunk);
+int pick_lpr(int units);
+
+// Raises the dynamic LDS limit of the kernels; call once per device before launching.
+hipError_t init_kernel_attributes();
+// Dynamic LDS bytes a launch may request after init_kernel_attributes().
+size_t lds_limit();
+hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s);
+hipError_t launch_select(const SelArgs& a, hipStream_t s);
+
+// Test / utility kernels
+hipError_t launch_dequant(const QMat& w, float* out, hipStream_t s);
+hipError_t launch_fill_kv(void* kc, void* vc, int kv_heads, int ctx, int hd, int pos, int kv_f16, uint64_t seed,
+                          hipStream_t s);
+
+}  // namespace chonk

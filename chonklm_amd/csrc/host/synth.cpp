@@ -1,0 +1,188 @@
+// Synthetic GGUF model writer: seeded random-init decoder weights quantized
+// with the reference block quantizers under a llama.cpp-style type recipe.
+//
+// The tensor names, metadata keys and shapes are the ones the reference's
+// manifest builder reads (src/lib/llama-wgsl-runtime.ts:326-425):
+//   token_embd.weight, output_norm.weight, blk.N.{attn_norm, attn_q, attn_k,
+//   attn_v, attn_output, attn_q_norm, attn_k_norm, ffn_norm, ffn_gate, ffn_up,
+//   ffn_down, post_attention_norm, post_ffw_norm}.weight, and
+//   <arch>.{block_count, embedding_length, feed_forward_length,
+//   attention.head_count, attention.head_count_kv, attention.key_length,
+//   context_length, rope.freq_base, attention.layer_norm_rms_epsilon},
+//   gemma3.attention.sliding_window.
+// Type recipe (Q4_K_M): llama.cpp's llama_tensor_get_type as restated in the
+// header of synth.h.
+#include "synth.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <thread>
+#include <vector>
+
+#include "ggml_types.h"
+#include "gguf.h"
+#include "quantize.h"
+
+namespace chonk {
+namespace {
+
+inline uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+inline uint64_t name_hash(const std::string& s) {
+  uint64_t h = 1469598103934665603ull;  // FNV-1a
+  for (unsigned char c : s) h = (h ^ c) * 1099511628211ull;
+  return h;
+}
+
+// Standard normal value for (stream, index) via Box-Muller on two
+// counter-based uniforms; independent of thread scheduling.
+inline float normal_at(uint64_t stream, uint64_t i) {
+  const uint64_t a = splitmix64(stream ^ splitmix64(2 * i));
+  const uint64_t b = splitmix64(stream ^ splitmix64(2 * i + 1));
+  const double u1 = ((a >> 11) + 1) * (1.0 / 9007199254740993.0);  // (0, 1]
+  const double u2 = (b >> 11) * (1.0 / 9007199254740992.0);        // [0, 1)
+  return (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+}
+
+bool use_more_bits(int i, int n) { return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2; }
+
+uint32_t fallback_type(uint32_t type, uint64_t row_len) {
+  if (row_len % 256 == 0) return type;
+  if (type == GGML_Q4_K) return GGML_Q5_0;
+  if (type == GGML_Q6_K) return GGML_Q8_0;
+  if (type == GGML_Q5_K) return GGML_Q5_1;
+  return type;
+}
+
+struct TensorPlan {
+  std::string name;
+  uint64_t rows;     // N
+  uint64_t row_len;  // K
+  uint32_t type;
+  float mean;        // weights = mean + std * normal
+  float std;
+};
+
+}  // namespace
+
+uint32_t recipe_tensor_type(const std::string& recipe, const std::string& role, int layer, int n_layers,
+                            uint64_t row_len) {
+  if (role == "norm") return GGML_F32;
+  if (recipe == "f32") return GGML_F32;
+  if (recipe == "f16") return GGML_F16;
+  if (recipe == "q8_0") return row_len % 32 == 0 ? GGML_Q8_0 : GGML_F16;
+  if (recipe == "q4_k" || recipe == "q6_k" || recipe == "q5_0") {
+    const uint32_t t = recipe == "q4_k" ? GGML_Q4_K : recipe == "q6_k" ? GGML_Q6_K : GGML_Q5_0;
+    return fallback_type(t, row_len);
+  }
+  if (recipe != "q4_k_m") throw std::runtime_error("unknown quantization recipe " + recipe);
+  uint32_t t = GGML_Q4_K;
+  if (role == "output") {
+    t = row_len % 256 != 0 ? GGML_Q8_0 : GGML_Q6_K;
+  } else if (role == "attn_v" || role == "ffn_down") {
+    if (use_more_bits(layer, n_layers)) t = GGML_Q6_K;
+  }
+  return fallback_type(t, row_len);
+}
+
+void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_threads) {
+  const std::string& a = c.arch;
+  if (a != "llama" && a != "qwen3" && a != "gemma3") throw std::runtime_error("synthetic writer: unsupported arch " + a);
+  if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0)
+    throw std::runtime_error("synthetic writer: non-positive dimension");
+  if (c.heads % c.kv_heads != 0) throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
+  const int head_dim = c.head_dim > 0 ? c.head_dim : c.hidden / c.heads;
+  const uint64_t H = (uint64_t)c.hidden, F = (uint64_t)c.ffn;
+  const uint64_t qdim = (uint64_t)c.heads * head_dim, kvdim = (uint64_t)c.kv_heads * head_dim;
+  const bool gemma = a == "gemma3";
+  const bool qk_norm = a == "qwen3" || gemma;
+  const float w_std = c.weight_std;
+  const float n_std = c.norm_std;
+
+  std::vector<TensorPlan> plan;
+  // tied embeddings: token_embd doubles as the output projection ("output" role)
+  plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H,
+                  recipe_tensor_type(c.recipe, "output", -1, c.layers, H), 0.f, w_std});
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    auto lin = [&](const std::string& role, uint64_t n, uint64_t k) {
+      plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f, w_std});
+    };
+    auto norm = [&](const std::string& role, uint64_t n) { plan.push_back({p + role + ".weight", 1, n, GGML_F32, 1.f, n_std}); };
+    norm("attn_norm", H);
+    lin("attn_q", qdim, H);
+    lin("attn_k", kvdim, H);
+    lin("attn_v", kvdim, H);
+    lin("attn_output", H, qdim);
+    if (qk_norm) {
+      norm("attn_q_norm", (uint64_t)head_dim);
+      norm("attn_k_norm", (uint64_t)head_dim);
+    }
+    if (gemma) norm("post_attention_norm", H);
+    norm("ffn_norm", H);
+    lin("ffn_gate", F, H);
+    lin("ffn_up", F, H);
+    lin("ffn_down", H, F);
+    if (gemma) norm("post_ffw_norm", H);
+  }
+  plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
+
+  GgufWriter w;
+  w.set_string("general.architecture", a);
+  w.set_string("general.name", c.name.empty() ? "synthetic-" + a : c.name);
+  w.set_u32("general.file_type", c.recipe == "q8_0" ? 7u : c.recipe == "q4_k_m" ? 15u : 0u);
+  w.set_u32(a + ".context_length", (uint32_t)c.context_length);
+  w.set_u32(a + ".embedding_length", (uint32_t)c.hidden);
+  w.set_u32(a + ".block_count", (uint32_t)c.layers);
+  w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
+  w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
+  w.set_u32(a + ".attention.head_count_kv", (uint32_t)c.kv_heads);
+  if (c.head_dim > 0) {
+    w.set_u32(a + ".attention.key_length", (uint32_t)head_dim);
+    w.set_u32(a + ".attention.value_length", (uint32_t)head_dim);
+  }
+  w.set_u32(a + ".rope.dimension_count", (uint32_t)head_dim);
+  w.set_f32(a + ".rope.freq_base", c.rope_theta);
+  w.set_f32(a + ".attention.layer_norm_rms_epsilon", c.norm_eps);
+  w.set_u32(a + ".vocab_size", (uint32_t)c.vocab);
+  if (gemma) w.set_u32("gemma3.attention.sliding_window", (uint32_t)c.sliding_window);
+
+  const int nt = std::max(1, n_threads);
+  for (size_t ti = 0; ti < plan.size(); ++ti) {
+    const TensorPlan& t = plan[ti];
+    TypeTraits tt;
+    type_traits(t.type, &tt);
+    const uint64_t row_bytes = t.row_len / tt.block_elems * tt.block_bytes;
+    std::vector<uint8_t> data(row_bytes * t.rows);
+    const uint64_t stream = splitmix64(c.seed ^ name_hash(t.name));
+    std::vector<std::thread> pool;
+    std::vector<std::string> errors(nt);
+    for (int th = 0; th < nt; ++th) {
+      pool.emplace_back([&, th]() {
+        std::vector<float> row(t.row_len);
+        for (uint64_t r = th; r < t.rows; r += nt) {
+          for (uint64_t k = 0; k < t.row_len; ++k) row[k] = t.mean + t.std * normal_at(stream, r * t.row_len + k);
+          if (!quantize_rows(t.type, row.data(), data.data() + r * row_bytes, (int64_t)t.row_len)) {
+            errors[th] = "quantization failed for " + t.name;
+            return;
+          }
+        }
+      });
+    }
+    for (auto& th : pool) th.join();
+    for (const auto& e : errors)
+      if (!e.empty()) throw std::runtime_error(e);
+    std::vector<uint64_t> shape = t.rows == 1 ? std::vector<uint64_t>{t.row_len} : std::vector<uint64_t>{t.row_len, t.rows};
+    w.add_tensor(t.name, shape, t.type, std::move(data));
+  }
+  w.write(path);
+}
+
+}  // namespace chonk

@@ -1,0 +1,111 @@
+"""Model definitions of the decode workloads.
+
+``ModelDef`` carries the fields of the reference's registry entry that the
+llama-webgpu runtime reads (src/lib/registry.ts:14-46): id, vocab, layers,
+maxContext, eosIds, defaultRepetitionPenalty, and the artefact location (a
+GGUF file or a shard directory instead of base + gguf URL).
+
+``WORKLOADS`` are the synthetic decoders the benchmark and tests use: random
+weights (N(0, 0.02) linear weights, 1 + N(0, 0.02) norm weights) quantized
+with the Q4_K_M or Q8_0 recipe. Their maxContext covers prompt + decode
+(the reference's registry caps Qwen3 at 2048 and Gemma-3 at 512 positions,
+registry.ts:191 and :129, which the long-prompt workloads exceed).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+
+@dataclass
+class ModelDef:
+    id: str
+    vocab: int
+    layers: int
+    max_context: int
+    eos_ids: list[int] = field(default_factory=list)
+    path: str = ""  # GGUF file or shard directory (manifest.json + NNNN.bin)
+    default_repetition_penalty: Optional[float] = None
+    runtime: str = "llama-webgpu"
+    kv_dtype: str = "f16"  # "f16" or "f32" (the reference's fp32 cache)
+    device: int = 0
+
+
+@dataclass
+class SynthSpec:
+    arch: str
+    recipe: str
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    ffn: int
+    vocab: int
+    head_dim: int = 0  # 0: hidden // heads, no key_length metadata
+    context_length: int = 32768
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+    sliding_window: int = 0
+    seed: int = 1234
+
+
+@dataclass
+class Workload:
+    name: str
+    spec: SynthSpec
+    max_context: int
+    eos_ids: list[int]
+    prompt_tokens: int
+    decode_tokens: int
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    description: str = ""
+
+    def model_def(self, path: str, kv_dtype: str = "f16", device: int = 0) -> ModelDef:
+        return ModelDef(id=self.name, vocab=self.spec.vocab, layers=self.spec.layers, max_context=self.max_context,
+                        eos_ids=list(self.eos_ids), path=path, kv_dtype=kv_dtype, device=device)
+
+
+SMOLLM2 = dict(arch="llama", hidden=576, layers=30, heads=9, kv_heads=3, ffn=1536, vocab=49152,
+               context_length=8192, rope_theta=100000.0, norm_eps=1e-5)
+QWEN3 = dict(arch="qwen3", hidden=1024, layers=28, heads=16, kv_heads=8, head_dim=128, ffn=3072, vocab=151936,
+             context_length=40960, rope_theta=1000000.0, norm_eps=1e-6)
+GEMMA3 = dict(arch="gemma3", hidden=640, layers=18, heads=4, kv_heads=1, head_dim=256, ffn=2048, vocab=262144,
+              context_length=32768, rope_theta=1000000.0, norm_eps=1e-6, sliding_window=512)
+
+WORKLOADS: dict[str, Workload] = {
+    w.name: w
+    for w in [
+        Workload("smollm2-135m-q4_k_m", SynthSpec(recipe="q4_k_m", **SMOLLM2), max_context=512, eos_ids=[2],
+                 prompt_tokens=32, decode_tokens=128,
+                 description="SmolLM2-135M-shaped llama decoder, Q4_K_M, 32-token prompt, greedy 128"),
+        Workload("smollm2-135m-q8_0", SynthSpec(recipe="q8_0", **SMOLLM2), max_context=512, eos_ids=[2],
+                 prompt_tokens=32, decode_tokens=128,
+                 description="SmolLM2-135M-shaped llama decoder, Q8_0, 32-token prompt, greedy 128"),
+        Workload("qwen3-0.6b-q4_k_m", SynthSpec(recipe="q4_k_m", **QWEN3), max_context=2048 + 256,
+                 eos_ids=[151645, 151643], prompt_tokens=2048, decode_tokens=256,
+                 description="Qwen3-0.6B-shaped decoder, Q4_K_M, 2048-token prompt, greedy 256, fp16 KV"),
+        Workload("gemma3-270m-q4_k_m", SynthSpec(recipe="q4_k_m", **GEMMA3), max_context=1024 + 128,
+                 eos_ids=[1, 106], prompt_tokens=1024, decode_tokens=128, temperature=0.8, top_k=40,
+                 description="Gemma-3-270M-shaped decoder, Q4_K_M (Q8_0 lm_head), 1024-token prompt, "
+                             "top-k 40 / T 0.8 sampling, 128 tokens"),
+        # small decoders for oracle parity (each exercises a different type mix)
+        Workload("tiny-qwen3", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=2,
+                                         head_dim=64, ffn=512, vocab=1200, context_length=4096,
+                                         rope_theta=1000000.0, norm_eps=1e-6, seed=7),
+                 max_context=160, eos_ids=[1199], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-llama", SynthSpec(arch="llama", recipe="q4_k_m", hidden=192, layers=3, heads=6, kv_heads=2,
+                                         ffn=512, vocab=1000, context_length=4096, rope_theta=100000.0,
+                                         norm_eps=1e-5, seed=11),
+                 max_context=160, eos_ids=[2], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-llama-q8", SynthSpec(arch="llama", recipe="q8_0", hidden=192, layers=2, heads=6, kv_heads=2,
+                                            ffn=384, vocab=700, context_length=4096, rope_theta=100000.0,
+                                            norm_eps=1e-5, seed=13),
+                 max_context=160, eos_ids=[2], prompt_tokens=16, decode_tokens=24),
+        Workload("tiny-gemma3", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=320, layers=7, heads=4,
+                                          kv_heads=1, head_dim=128, ffn=512, vocab=1500, context_length=4096,
+                                          rope_theta=1000000.0, norm_eps=1e-6, sliding_window=16, seed=17),
+                 max_context=96, eos_ids=[1, 106], prompt_tokens=40, decode_tokens=24, temperature=0.8, top_k=40),
+    ]
+}

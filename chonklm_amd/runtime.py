@@ -1,0 +1,264 @@
+"""Host-side mirror of the reference's llama-webgpu runtime module API.
+
+Reference: src/lib/llama-wgsl-runtime.ts
+  loadLlamaWgslModel(model, onProgress?, onStep?)        :184-240  -> load_llama_wgsl_model
+  generateLlamaWgsl(loaded, promptIds, opts)             :242-314  -> generate_llama_wgsl
+  disposeLlamaWgsl(loaded)                               :316-318  -> dispose_llama_wgsl
+  resetLlamaWgslConversation(loaded)                     :320-324  -> reset_llama_wgsl_conversation
+  LlamaWgslEngine.runToken / reset / position / dispose  :1011-1215 -> LlamaWgslEngine
+PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6) are exported under the
+same names with the pleias prefix.
+
+Everything below calls libchonk.so through its C ABI (include/chonk.h); there
+is no other execution path. Token ids in, token ids out: text decoding is the
+caller's tokenizer's job (the reference's tokenizer is not on this path), so
+``text`` is produced only when a ``decode`` callable is supplied.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Callable, Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import ChonkError, check, lib
+from .registry import ModelDef, Workload, WORKLOADS
+
+
+def _i32_array(values: Sequence[int]):
+    arr = (C.c_int32 * max(1, len(values)))(*values)
+    return arr, len(values)
+
+
+def _sampling(temperature=None, top_p=None, top_k=None, repetition_penalty=None, seed: int = 0) -> _lib.SamplingC:
+    s = _lib.SamplingC()
+    s.temperature = 0.0 if temperature is None else float(temperature)
+    s.top_p = 1.0 if top_p is None else float(top_p)
+    s.top_k = 0 if top_k is None or not np.isfinite(top_k) else int(max(0, int(top_k)))
+    s.repetition_penalty = -1.0 if repetition_penalty is None else float(repetition_penalty)
+    s.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    return s
+
+
+class LlamaWgslEngine:
+    """One decode engine on one GPU (LlamaWgslEngine, :619-1693)."""
+
+    def __init__(self, model: ModelDef):
+        L = lib()
+        eos, n_eos = _i32_array(model.eos_ids)
+        d = _lib.ModelDefC()
+        d.id = model.id.encode()
+        d.vocab = model.vocab
+        d.layers = model.layers
+        d.max_context = model.max_context
+        d.eos_ids = C.cast(eos, C.POINTER(C.c_int32))
+        d.n_eos = n_eos
+        d.default_repetition_penalty = float(model.default_repetition_penalty or 0.0)
+        d.kv_dtype = _lib.KV_F32 if model.kv_dtype == "f32" else _lib.KV_F16
+        d.device = model.device
+        handle = C.c_void_p()
+        check(L.chonk_engine_create(C.byref(d), model.path.encode(), C.byref(handle)))
+        self._h = handle
+        self.model = model
+        info = _lib.EngineInfoC()
+        check(L.chonk_engine_info_get(self._h, C.byref(info)), self._h)
+        self.info = {name: getattr(info, name) for name, _ in info._fields_}
+
+    # -- reference API --------------------------------------------------------------
+    def run_token(self, token_id: int, need_logits: bool, temperature=None, top_p=None, top_k=None,
+                  repetition_penalty=None, penalized_token_ids: Optional[Sequence[int]] = None,
+                  seen_ids: Optional[Sequence[int]] = None, seed: int = 0) -> int:
+        s = _sampling(temperature, top_p, top_k, 1.0 if repetition_penalty is None else repetition_penalty, seed)
+        pen, n_pen = _i32_array(penalized_token_ids or [])
+        seen, n_seen = _i32_array(seen_ids or [])
+        out = C.c_int32()
+        check(lib().chonk_engine_run_token(self._h, int(token_id), 1 if need_logits else 0, C.byref(s),
+                                           C.cast(pen, C.POINTER(C.c_int32)), n_pen,
+                                           C.cast(seen, C.POINTER(C.c_int32)), n_seen, C.byref(out)), self._h)
+        return int(out.value)
+
+    def reset(self) -> None:
+        check(lib().chonk_engine_reset(self._h), self._h)
+
+    @property
+    def position(self) -> int:
+        v = C.c_int32()
+        check(lib().chonk_engine_position(self._h, C.byref(v)), self._h)
+        return int(v.value)
+
+    def dispose(self) -> None:
+        if self._h:
+            check(lib().chonk_engine_destroy(self._h))
+            self._h = None
+
+    # -- additions for parity tests and measurement ---------------------------------
+    def read_logits(self) -> np.ndarray:
+        out = np.empty(self.info["vocab"], dtype=np.float32)
+        check(lib().chonk_engine_read_logits(self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size), self._h)
+        return out
+
+    def read_buffer(self, which: int) -> np.ndarray:
+        i = self.info
+        sizes = {0: i["hidden"] * 4, 1: i["heads"] * i["head_dim"] * 4, 2: ((i["vocab"] + 255) // 256) * 8,
+                 3: (i["heads"] + 2 * i["kv_heads"]) * i["head_dim"] * 4}
+        buf = np.empty(sizes[which], dtype=np.uint8)
+        check(lib().chonk_engine_read_buffer(self._h, which, buf.ctypes.data, buf.size), self._h)
+        return buf.view(np.float32) if which != 2 else buf
+
+    def read_kv(self, layer: int, is_value: bool, pos: int) -> np.ndarray:
+        out = np.empty(self.info["kv_heads"] * self.info["head_dim"], dtype=np.float32)
+        check(lib().chonk_engine_read_kv(self._h, layer, 1 if is_value else 0, pos,
+                                         out.ctypes.data_as(C.POINTER(C.c_float))), self._h)
+        return out
+
+    def fake_context(self, pos: int, seed: int = 1) -> None:
+        check(lib().chonk_engine_fake_context(self._h, pos, seed), self._h)
+
+    def bench_decode(self, warmup: int, steps: int) -> float:
+        ms = C.c_double()
+        check(lib().chonk_engine_bench_decode(self._h, warmup, steps, C.byref(ms)), self._h)
+        return float(ms.value)
+
+    def bench_kernel(self, kernel_id: int, reps: int) -> tuple[str, float, int]:
+        us = C.c_double()
+        name = C.create_string_buffer(64)
+        nbytes = C.c_uint64()
+        check(lib().chonk_engine_bench_kernel(self._h, kernel_id, reps, C.byref(us), name, 64, C.byref(nbytes)),
+              self._h)
+        return name.value.decode(), float(us.value), int(nbytes.value)
+
+    def conversation(self) -> tuple[list[int], Optional[int]]:
+        n = C.c_size_t()
+        nxt = C.c_int32()
+        check(lib().chonk_engine_conversation(self._h, None, 0, C.byref(n), C.byref(nxt)), self._h)
+        buf = (C.c_int32 * max(1, n.value))()
+        check(lib().chonk_engine_conversation(self._h, buf, n.value, C.byref(n), C.byref(nxt)), self._h)
+        return list(buf[: n.value]), (None if nxt.value < 0 else int(nxt.value))
+
+    def __del__(self):
+        try:
+            self.dispose()
+        except Exception:
+            pass
+
+
+@dataclass
+class LoadedLlamaWgslModel:
+    """LoadedLlamaWgslModel (:174-182); ``ep`` names the execution provider."""
+
+    def_: ModelDef
+    engine: LlamaWgslEngine
+    tokenizer: object = None
+    runtime: str = "llama-webgpu"
+    ep: str = "hip"
+    cached_token_ids: list[int] = field(default_factory=list)
+    cached_next_id: Optional[int] = None
+
+
+def load_llama_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = None,
+                          on_step: Optional[Callable] = None, tokenizer: object = None) -> LoadedLlamaWgslModel:
+    if model.runtime != "llama-webgpu":
+        raise ValueError(f"loadLlamaWgslModel: {model.id} is not configured for the Llama WGSL runtime")
+    if on_step:
+        on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
+    engine = LlamaWgslEngine(model)
+    if on_step:
+        on_step({"step": "ready", "detail": "Llama HIP runtime ready"})
+    return LoadedLlamaWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
+
+
+def generate_llama_wgsl(loaded: LoadedLlamaWgslModel, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None,
+                        temperature=None, top_p=None, top_k=None, repetition_penalty=None,
+                        on_token: Optional[Callable[[dict], None]] = None,
+                        should_stop: Optional[Callable[[], bool]] = None, seed: int = 0,
+                        decode: Optional[Callable[[list[int]], str]] = None) -> dict:
+    """generateLlamaWgsl (:242-314).
+
+    Without callbacks the whole call runs on the device (no per-token host
+    round trip). With ``on_token`` / ``should_stop`` the loop is stepped
+    from the host as in the reference, one readback per token.
+    """
+    L = lib()
+    eng = loaded.engine
+    s = _sampling(temperature, top_p, top_k, repetition_penalty, seed)
+    prompt, n_prompt = _i32_array(list(prompt_ids))
+    cap = max(1, (max_new_tokens if max_new_tokens and max_new_tokens > 0 else 128))
+    out = (C.c_int32 * cap)()
+    n_out = C.c_size_t()
+    stats = _lib.GenStatsC()
+    generated: list[int] = []
+    cumulative = [""]
+
+    if on_token is None and should_stop is None:
+        check(L.chonk_engine_generate(eng._h, C.cast(prompt, C.POINTER(C.c_int32)), n_prompt,
+                                      int(max_new_tokens or 0), C.byref(s), out, cap, C.byref(n_out),
+                                      C.byref(stats)), eng._h)
+        generated = list(out[: n_out.value])
+    else:
+        def _cb(_user, event, token):
+            if event == 0:
+                return 1 if (should_stop and should_stop()) else 0
+            generated.append(int(token))
+            if on_token:
+                text = decode(generated) if decode else ""
+                piece = text[len(cumulative[0]):]
+                cumulative[0] = text
+                on_token({"id": int(token), "text": piece, "cumulative": text})
+            return 0
+
+        cb = _lib.TOKEN_CALLBACK(_cb)
+        check(L.chonk_engine_generate_stepped(eng._h, C.cast(prompt, C.POINTER(C.c_int32)), n_prompt,
+                                              int(max_new_tokens or 0), C.byref(s), C.cast(cb, C.c_void_p), None,
+                                              out, cap, C.byref(n_out), C.byref(stats)), eng._h)
+        generated = list(out[: n_out.value])
+    loaded.cached_token_ids, loaded.cached_next_id = eng.conversation()
+    text = decode(generated) if decode else ""
+    return {"text": text, "ids": generated, "tokensPerSec": stats.tokens_per_sec,
+            "prefillMs": stats.prefill_ms, "decodeMs": stats.decode_ms}
+
+
+def dispose_llama_wgsl(loaded: LoadedLlamaWgslModel) -> None:
+    loaded.engine.dispose()
+
+
+def reset_llama_wgsl_conversation(loaded: LoadedLlamaWgslModel) -> None:
+    check(lib().chonk_engine_reset_conversation(loaded.engine._h), loaded.engine._h)
+    loaded.cached_token_ids = []
+    loaded.cached_next_id = None
+
+
+# PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
+load_pleias_wgsl_model = load_llama_wgsl_model
+generate_pleias_wgsl = generate_llama_wgsl
+dispose_pleias_wgsl = dispose_llama_wgsl
+reset_pleias_wgsl_conversation = reset_llama_wgsl_conversation
+
+
+# ---- model files ------------------------------------------------------------------
+
+def write_synthetic_gguf(workload: Workload | str, path: str, threads: int = 8) -> str:
+    w = WORKLOADS[workload] if isinstance(workload, str) else workload
+    sp = w.spec
+    c = _lib.SynthConfigC()
+    c.arch = sp.arch.encode()
+    c.recipe = sp.recipe.encode()
+    c.hidden, c.layers, c.heads, c.kv_heads = sp.hidden, sp.layers, sp.heads, sp.kv_heads
+    c.head_dim, c.ffn, c.vocab, c.context_length = sp.head_dim, sp.ffn, sp.vocab, sp.context_length
+    c.rope_theta, c.norm_eps, c.sliding_window, c.seed = sp.rope_theta, sp.norm_eps, sp.sliding_window, sp.seed
+    check(lib().chonk_write_synthetic_gguf(C.byref(c), str(path).encode(), int(threads)))
+    return str(path)
+
+
+def shard_gguf(gguf_path: str, out_dir: str, shard_size: int = 24 * 1024 * 1024, quant: str = "") -> str:
+    """scripts/shard-gguf.mjs: <out_dir>/NNNN.bin + manifest.json (24 MiB default shards)."""
+    check(lib().chonk_write_shards(str(gguf_path).encode(), str(out_dir).encode(), int(shard_size), quant.encode()))
+    return str(out_dir)
+
+
+__all__ = [
+    "ChonkError", "LlamaWgslEngine", "LoadedLlamaWgslModel", "ModelDef", "load_llama_wgsl_model",
+    "generate_llama_wgsl", "dispose_llama_wgsl", "reset_llama_wgsl_conversation", "write_synthetic_gguf",
+    "shard_gguf",
+]

@@ -1,0 +1,209 @@
+/*
+ * chonk.h — C ABI of the MI355X decode engine (libchonk.so).
+ *
+ * This is the drop-in boundary for the reference's llama-webgpu runtime. Each
+ * entry point names the reference interface it replaces
+ * (paths relative to the reference repository):
+ *
+ *   chonk_engine_create            loadLlamaWgslModel + LlamaWgslEngine.create
+ *                                  (src/lib/llama-wgsl-runtime.ts:184-240, :669-919)
+ *   chonk_engine_run_token         LlamaWgslEngine.runToken (:1025-1150)
+ *   chonk_engine_generate          generateLlamaWgsl (:242-314)
+ *   chonk_engine_reset             LlamaWgslEngine.reset (:1011-1019)
+ *   chonk_engine_reset_conversation resetLlamaWgslConversation (:320-324)
+ *   chonk_engine_position          LlamaWgslEngine.position (:1021-1023)
+ *   chonk_engine_destroy           disposeLlamaWgsl / LlamaWgslEngine.dispose (:316-318, :1152-1215)
+ *   chonk_engine_read_logits       (new) logits readback for parity tests; the
+ *                                  reference keeps logits GPU-only (:893)
+ *
+ * Conventions: plain pointers and sizes, no ownership transfer. Every function
+ * returns CHONK_OK (0) or a negative status; the message of the last failure
+ * is available from chonk_engine_last_error(engine) or, for calls without an
+ * engine, chonk_last_error(). Messages reuse the reference's wording
+ * ("Llama WGSL context exhausted at N tokens", "unsupported GGUF tensor type
+ * X", "Llama GGUF WGSL does not support architecture X", ...).
+ * An engine is not re-entrant: a call made while another call on the same
+ * engine is in progress returns CHONK_EBUSY (the reference's `active` guard,
+ * :1221-1224). Engines on different threads are independent.
+ * A HIP error marks the engine lost; later calls fail fast with CHONK_ELOST
+ * (the LFM runtime's deviceLost behaviour, lfm-wgsl-runtime.ts:704-707,
+ * :729-731).
+ */
+#ifndef CHONK_H
+#define CHONK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHONK_OK 0
+#define CHONK_EINVAL -1      /* bad argument / unsupported model */
+#define CHONK_EIO -2         /* file or shard read failure */
+#define CHONK_EHIP -3        /* HIP runtime error (engine is now lost) */
+#define CHONK_ECONTEXT -4    /* "Llama WGSL context exhausted at N tokens" */
+#define CHONK_EBUSY -5       /* concurrent call on the same engine */
+#define CHONK_ELOST -6       /* engine lost after an earlier HIP error */
+#define CHONK_ENOMEM -7      /* device allocation failed */
+
+#define CHONK_KV_F16 0       /* fp16 K/V cache (default) */
+#define CHONK_KV_F32 1       /* fp32 K/V cache, the reference layout (:830-831) */
+
+typedef struct chonk_engine chonk_engine;
+
+/* The ModelDef fields the engine reads (src/lib/registry.ts:14-46). */
+typedef struct {
+  const char* id;                    /* ModelDef.id (diagnostics only) */
+  int32_t vocab;                     /* ModelDef.vocab */
+  int32_t layers;                    /* ModelDef.layers */
+  int32_t max_context;               /* ModelDef.maxContext */
+  const int32_t* eos_ids;            /* ModelDef.eosIds */
+  int32_t n_eos;
+  float default_repetition_penalty;  /* ModelDef.defaultRepetitionPenalty (0 = unset -> 1) */
+  int32_t kv_dtype;                  /* CHONK_KV_F16 or CHONK_KV_F32 */
+  int32_t device;                    /* HIP device ordinal */
+} chonk_model_def;
+
+/* SamplingOptions (src/lib/sampling.ts:1-7); seed replaces Math.random():
+ * the uniform draw for the token sampled at position p is
+ * (mix64(seed + 0x9E3779B97F4A7C15*(p+1)) >> 11) * 2^-53 with mix64 the
+ * splitmix64 finaliser. */
+typedef struct {
+  double temperature;         /* default 0 */
+  double top_p;               /* default 1 */
+  int32_t top_k;              /* default 0 */
+  double repetition_penalty;  /* default 1 */
+  uint64_t seed;
+} chonk_sampling;
+
+typedef struct {
+  int32_t hidden, ffn, vocab, layers, heads, kv_heads, head_dim, context;
+  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3 */
+  int32_t qk_norm, interleaved_rope, kv_dtype;
+  uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
+  uint64_t device_bytes;            /* device memory held by the engine */
+  int32_t kernels_per_step;         /* kernel launches in one decode step */
+} chonk_engine_info;
+
+typedef struct {
+  double prefill_ms;     /* wall time of the prompt steps */
+  double decode_ms;      /* wall time of the generated steps */
+  int32_t prompt_tokens;
+  int32_t generated_tokens;
+  double tokens_per_sec; /* generated / (prefill + decode), the reference's formula (:266, :312) */
+} chonk_gen_stats;
+
+const char* chonk_last_error(void);
+const char* chonk_engine_last_error(const chonk_engine* e);
+
+/* Loads a GGUF file, or a directory with manifest.json + NNNN.bin shards
+ * (scripts/shard-gguf.mjs format), uploads the weights and allocates the K/V
+ * cache of min(def->max_context, GGUF context_length) positions. */
+int chonk_engine_create(const chonk_model_def* def, const char* path, chonk_engine** out);
+/* Same from a caller buffer holding a whole GGUF file (copied). */
+int chonk_engine_create_from_memory(const chonk_model_def* def, const void* gguf_bytes, size_t n_bytes,
+                                    chonk_engine** out);
+int chonk_engine_destroy(chonk_engine* e);
+int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out);
+
+/* runToken: processes `token` at the current position; when need_logits is
+ * non-zero, computes logits and selects the next token (greedy argmax, or
+ * the candidate sampler when temperature > 0, top_p < 1 or top_k > 0). The
+ * repetition penalty applies to `penalized` (the reference's
+ * penalizedTokenIds; at most the last `context` ids are used) and, in the
+ * candidate sampler, again to `seen` (seenIds). out_token receives 0 when
+ * need_logits is zero. */
+int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, const chonk_sampling* s,
+                           const int32_t* penalized, size_t n_penalized, const int32_t* seen, size_t n_seen,
+                           int32_t* out_token);
+
+/* generateLlamaWgsl: prefix reuse against the previous conversation, prompt
+ * prefill, then up to max_new_tokens generated ids (stopping after an EOS
+ * id), all on the device without a per-token host round trip. max_new_tokens
+ * <= 0 means 128. The penalty list is prompt + generated, as in the
+ * reference. out_ids receives min(n, out_cap) ids; *n_out the count. */
+int chonk_engine_generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new_tokens,
+                          const chonk_sampling* s, int32_t* out_ids, size_t out_cap, size_t* n_out,
+                          chonk_gen_stats* stats);
+
+/* The same loop stepped from the host one token at a time (one readback per
+ * token, as the reference does), for callers that stream tokens or cancel:
+ * before each generated id is appended, callback(user, 0, 0) is the
+ * reference's shouldStop() (non-zero stops); after it is appended,
+ * callback(user, 1, id) is onToken. Results equal chonk_engine_generate's. */
+typedef int32_t (*chonk_token_callback)(void* user, int32_t event, int32_t token);
+int chonk_engine_generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new_tokens,
+                                  const chonk_sampling* s, chonk_token_callback callback, void* user,
+                                  int32_t* out_ids, size_t out_cap, size_t* n_out, chonk_gen_stats* stats);
+
+/* Conversation cache of the last generate call (LoadedLlamaWgslModel's
+ * cachedTokenIds / cachedNextId, :174-182): *n_cached ids are copied to ids
+ * (up to cap); *next_id is cachedNextId or -1 when it is null. */
+int chonk_engine_conversation(chonk_engine* e, int32_t* ids, size_t cap, size_t* n_cached, int32_t* next_id);
+
+int chonk_engine_reset(chonk_engine* e);
+int chonk_engine_reset_conversation(chonk_engine* e);
+int chonk_engine_position(const chonk_engine* e, int32_t* out_pos);
+
+/* Logits of the last step that computed them (vocab floats). */
+int chonk_engine_read_logits(chonk_engine* e, float* out, size_t n);
+
+/* Intermediate buffers of the last step, for parity tests:
+ * 0 residual after the last layer [hidden], 1 attention output of the last
+ * layer [heads*head_dim], 2 group candidates [ceil(vocab/256) x {f32, u32}],
+ * 3 raw q|k|v projections of the last layer [qdim + 2 kvdim]. */
+int chonk_engine_read_buffer(chonk_engine* e, int32_t which, void* out, size_t n_bytes);
+/* K or V cache row of `layer` at position `pos` as floats [kv_heads*head_dim]. */
+int chonk_engine_read_kv(chonk_engine* e, int32_t layer, int32_t is_value, int32_t pos, float* out);
+
+/* Benchmark hooks -------------------------------------------------------
+ * Runs `n_warmup` then `n_steps` greedy decode steps by graph replay from the
+ * current state (the history token at the current position is consumed), timed
+ * with HIP events on the engine stream. */
+int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps, double* ms_total);
+/* Average duration (microseconds) of one kernel of the decode step, launched
+ * `reps` times back-to-back with the arguments it has in the step, timed with
+ * HIP events on the engine stream. kernel_id indexes the step's launch list;
+ * name receives its label (e.g. "L3.gateup q4_k"); bytes its algorithmic
+ * bytes per launch. */
+int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
+                              size_t name_len, uint64_t* bytes);
+/* Writes `pos` synthetic positions into the K/V cache and sets the position,
+ * so that long-context decode can be measured without a full prefill. */
+int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed);
+
+/* Kernel-level entry points (tests) ---------------------------------------
+ * GGUF rows are given as raw block bytes in host memory; the call uploads
+ * them with the engine's repacking, runs the kernel on `device`, and returns
+ * the result to host memory. */
+int chonk_dequant(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
+                  float* out);
+/* y[N] = W[N,K] x[K]; when reps > 0 also times `reps` back-to-back launches
+ * and stores the mean microseconds in *avg_us. */
+int chonk_matvec(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
+                 const float* x, float* y, int32_t reps, double* avg_us);
+
+/* Model files --------------------------------------------------------------- */
+typedef struct {
+  const char* arch;      /* "llama" | "qwen3" | "gemma3" */
+  const char* recipe;    /* "q4_k_m" | "q8_0" | "q4_k" | "q6_k" | "q5_0" */
+  int32_t hidden, layers, heads, kv_heads, head_dim, ffn, vocab, context_length;
+  float rope_theta, norm_eps;
+  int32_t sliding_window;
+  uint64_t seed;
+  float weight_std;      /* 0 -> 0.02 */
+  float norm_std;        /* 0 -> 0.02 */
+} chonk_synth_config;
+
+/* Writes a seeded random-init decoder as GGUF (see the recipe in synth.h). */
+int chonk_write_synthetic_gguf(const chonk_synth_config* c, const char* path, int32_t n_threads);
+/* Splits a GGUF file into <out_dir>/NNNN.bin + manifest.json. */
+int chonk_write_shards(const char* gguf_path, const char* out_dir, uint64_t shard_size, const char* quant);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,142 @@
+"""Float64 numpy decoder: an independent forward pass for pinning the oracle.
+
+Vectorised restatement of the decoder the reference runs
+(src/lib/llama-wgsl-runtime.ts:1025-1150): llama/qwen3 layers
+(pre-norm, GQA attention with optional per-head q/k RMSNorm, RoPE interleaved
+for GGUF arch "llama" and split-half otherwise, SwiGLU) and gemma3 layers
+(sandwich norms, +-65000 residual clamp, GELU-tanh, sqrt(hidden) embedding
+scale, sliding window on layers i % 6 != 5). Everything is float64 except the
+dequantized weights (exact float32 values) and, optionally, a binary16 K/V
+cache. Closed forms only: no reduction-order mimicry.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .ggufpy import Gguf, matrix, read_gguf
+
+
+class NumpyDecoder:
+    def __init__(self, path: str, vocab: int, max_context: int, kv_f16: bool = False):
+        g: Gguf = read_gguf(path)
+        self.g = g
+        arch = g.kv["general.architecture"]
+        self.arch = arch
+        self.gemma = arch == "gemma3"
+        self.interleaved = arch == "llama"
+        p = arch + "."
+        self.L = int(g.kv[p + "block_count"])
+        self.H = int(g.kv[p + "embedding_length"])
+        self.nh = int(g.kv[p + "attention.head_count"])
+        self.nkv = int(g.kv[p + "attention.head_count_kv"])
+        self.hd = int(g.kv.get(p + "attention.key_length", self.H // self.nh))
+        self.eps = float(np.float32(g.kv.get(p + "attention.layer_norm_rms_epsilon", 1e-5)))
+        self.vocab = vocab
+        self.ctx = min(max_context, int(g.kv.get(p + "context_length", max_context)))
+        self.kv_f16 = kv_f16
+        if self.gemma:
+            gtheta = g.kv.get("gemma3.rope.freq_base", 1e6)
+            win = int(g.kv.get("gemma3.attention.sliding_window", 0))
+            self.theta = [round(gtheta) if i % 6 == 5 else 10000 for i in range(self.L)]
+            self.window = [0 if i % 6 == 5 else win for i in range(self.L)]
+        else:
+            self.theta = [round(g.kv.get(p + "rope.freq_base", 10000.0))] * self.L
+            self.window = [0] * self.L
+        self.qk_norm = "blk.0.attn_q_norm.weight" in g.tensors
+        self.emb = matrix(g, "token_embd.weight").astype(np.float64)
+        self.lm = (matrix(g, "output.weight") if "output.weight" in g.tensors else self.emb).astype(np.float64)
+        self.final_norm = matrix(g, "output_norm.weight").astype(np.float64)
+        self.layers = []
+        for i in range(self.L):
+            b = f"blk.{i}."
+            get = lambda n: matrix(g, b + n).astype(np.float64)
+            lay = dict(q=get("attn_q.weight"), k=get("attn_k.weight"), v=get("attn_v.weight"),
+                       o=get("attn_output.weight"), gate=get("ffn_gate.weight"), up=get("ffn_up.weight"),
+                       down=get("ffn_down.weight"), in_norm=get("attn_norm.weight"))
+            if self.gemma:
+                lay.update(post=get("post_attention_norm.weight"), pre_ffn=get("ffn_norm.weight"),
+                           post_ffn=get("post_ffw_norm.weight"))
+            else:
+                lay.update(post=get("ffn_norm.weight"))
+            if self.qk_norm:
+                lay.update(qn=get("attn_q_norm.weight"), kn=get("attn_k_norm.weight"))
+            self.layers.append(lay)
+        self.reset()
+
+    def reset(self):
+        self.pos = 0
+        self.K = np.zeros((self.L, self.nkv, self.ctx, self.hd))
+        self.V = np.zeros((self.L, self.nkv, self.ctx, self.hd))
+
+    def _rms(self, x, w, eps=None):
+        eps = self.eps if eps is None else eps
+        return x / np.sqrt(np.mean(x * x) + eps) * w
+
+    def _rope(self, x, theta):
+        # x: [heads, hd]; rotate pairs
+        half = self.hd // 2
+        d = np.arange(half)
+        ang = self.pos * np.power(float(theta), -2.0 * d / self.hd)
+        co, si = np.cos(ang), np.sin(ang)
+        y = x.copy()
+        if self.interleaved:
+            a, b = x[:, 0::2], x[:, 1::2]
+            y[:, 0::2] = a * co - b * si
+            y[:, 1::2] = a * si + b * co
+        else:
+            a, b = x[:, :half], x[:, half:]
+            y[:, :half] = a * co - b * si
+            y[:, half:] = a * si + b * co
+        return y
+
+    def step(self, token: int) -> np.ndarray:
+        H, hd, nh, nkv = self.H, self.hd, self.nh, self.nkv
+        x = self.emb[token] * (np.sqrt(H) if self.gemma else 1.0)
+        if self.gemma:
+            x = x * 1.0
+        for i, lay in enumerate(self.layers):
+            n = self._rms(x, lay["in_norm"])
+            q = (lay["q"] @ n).reshape(nh, hd)
+            k = (lay["k"] @ n).reshape(nkv, hd)
+            v = (lay["v"] @ n).reshape(nkv, hd)
+            if self.qk_norm:
+                q = np.stack([self._rms(h, lay["qn"]) for h in q])
+                k = np.stack([self._rms(h, lay["kn"]) for h in k])
+            q = self._rope(q, self.theta[i])
+            k = self._rope(k, self.theta[i])
+            if self.kv_f16:
+                k = k.astype(np.float16).astype(np.float64)
+                v = v.astype(np.float16).astype(np.float64)
+            self.K[i, :, self.pos] = k
+            self.V[i, :, self.pos] = v
+            w = self.window[i]
+            start = self.pos + 1 - w if (w and self.pos + 1 > w) else 0
+            grp = nh // nkv
+            out = np.empty((nh, hd))
+            for h in range(nh):
+                kk = self.K[i, h // grp, start:self.pos + 1]
+                vv = self.V[i, h // grp, start:self.pos + 1]
+                s = kk @ q[h] / np.sqrt(hd)
+                p = np.exp(s - s.max())
+                p /= p.sum()
+                out[h] = p @ vv
+            o = lay["o"] @ out.reshape(-1)
+            if self.gemma:
+                x = np.clip(x + self._rms(o, lay["post"]), -65000, 65000)
+                n = self._rms(x, lay["pre_ffn"])
+                gte = lay["gate"] @ n
+                up = lay["up"] @ n
+                c = 0.7978845608028654
+                gelu = np.where(gte > 10, gte, np.where(gte < -10, 0.0,
+                                0.5 * gte * (1 + np.tanh(c * (gte + 0.044715 * gte ** 3)))))
+                d = lay["down"] @ (gelu * up)
+                x = np.clip(x + self._rms(d, lay["post_ffn"]), -65000, 65000)
+            else:
+                x = x + o
+                n = self._rms(x, lay["post"])
+                gte = lay["gate"] @ n
+                up = lay["up"] @ n
+                x = x + lay["down"] @ (gte / (1 + np.exp(-gte)) * up)
+        self.pos += 1
+        self.last_hidden = x
+        return self.lm[: self.vocab] @ self._rms(x, self.final_norm)

@@ -1,0 +1,197 @@
+"""GPU engine parity against the oracle on small synthetic decoders.
+
+Each tiny workload exercises a different type mix and architecture branch:
+tiny-qwen3 (Q4_K/Q6_K, qk-norm, split RoPE), tiny-llama (Q5_0/Q8_0/Q4_K
+fallbacks, interleaved RoPE, head_dim 32, GQA 3), tiny-llama-q8 (Q8_0
+everywhere), tiny-gemma3 (gemma3 sandwich norms, GELU-tanh, sliding window,
+Q8_0 tied lm_head, top-k/temperature sampling). Bars: identical token ids;
+logits max|d| / max|ref| <= 1e-3 at every step.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from chonklm_amd import WORKLOADS, ChonkError, generate_llama_wgsl, load_llama_wgsl_model
+from chonklm_amd.runtime import LlamaWgslEngine, reset_llama_wgsl_conversation
+from oracle.oracle import OracleModel
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TINY = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
+
+
+def _pair(synth, name, kv="f16", **over):
+    w = WORKLOADS[name]
+    path = synth(name)
+    md = w.model_def(path, kv_dtype=kv)
+    for k, v in over.items():
+        setattr(md, k, v)
+    loaded = load_llama_wgsl_model(md)
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, md.max_context, kv_f16=(kv == "f16"), eos_ids=w.eos_ids)
+    return w, loaded, ref
+
+
+def _prompt(w, seed=0, n=None):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, w.spec.vocab, n or w.prompt_tokens).tolist()
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_step_logits_and_tokens(name, synth):
+    w, loaded, ref = _pair(synth, name)
+    eng = loaded.engine
+    prompt = _prompt(w)
+    toks_g, toks_r = [], []
+    tok = prompt[0]
+    for i in range(len(prompt) + 12):
+        need = i >= len(prompt) - 1
+        if i < len(prompt):
+            tok = prompt[i]
+        a = eng.run_token(tok, need)
+        b = ref.run_token(tok, need)
+        if need:
+            lg, lr = eng.read_logits(), ref.logits()
+            e = rel_err(lg, lr)
+            assert e <= 1e-3, f"{name} step {i}: logits rel err {e:.3e}"
+            assert a == b, f"{name} step {i}: token {a} != {b}"
+            toks_g.append(a)
+            toks_r.append(b)
+            tok = a
+    assert eng.position == ref.position == len(prompt) + 12
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_generate_matches_oracle(name, synth):
+    w, loaded, ref = _pair(synth, name)
+    prompt = _prompt(w, seed=1)
+    out = generate_llama_wgsl(loaded, prompt, w.decode_tokens, temperature=w.temperature, top_k=w.top_k, seed=9)
+    want = ref.generate(prompt, w.decode_tokens, temperature=w.temperature, top_k=w.top_k, seed=9)
+    assert out["ids"] == want
+    assert loaded.engine.position == ref.position
+    assert loaded.cached_token_ids == ref.cached_token_ids
+    assert loaded.cached_next_id == ref.cached_next_id
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-gemma3"])
+def test_stepped_equals_device_loop(name, synth):
+    w, loaded, _ = _pair(synth, name)
+    prompt = _prompt(w, seed=2)
+    a = generate_llama_wgsl(loaded, prompt, 20, temperature=w.temperature, top_k=w.top_k, seed=3)["ids"]
+    reset_llama_wgsl_conversation(loaded)
+    seen = []
+    b = generate_llama_wgsl(loaded, prompt, 20, temperature=w.temperature, top_k=w.top_k, seed=3,
+                            on_token=lambda info: seen.append(info["id"]))["ids"]
+    assert a == b == seen
+
+
+def test_prefix_reuse_matches_oracle(synth):
+    w, loaded, ref = _pair(synth, "tiny-qwen3")
+    p1 = _prompt(w, seed=4, n=10)
+    for turn in range(3):
+        g = generate_llama_wgsl(loaded, p1, 6)["ids"]
+        r = ref.generate(p1, 6)
+        assert g == r, f"turn {turn}"
+        assert loaded.engine.position == ref.position
+        p1 = p1 + g + _prompt(w, seed=10 + turn, n=3)
+    # identical prompt again: cachedNextId path
+    same = list(ref.cached_token_ids)
+    assert generate_llama_wgsl(loaded, same, 4)["ids"] == ref.generate(same, 4)
+
+
+def test_repetition_penalty_and_sampling_paths(synth):
+    w, loaded, ref = _pair(synth, "tiny-llama")
+    eng = loaded.engine
+    prompt = _prompt(w, seed=5, n=12)
+    for i, t in enumerate(prompt[:-1]):
+        eng.run_token(t, False)
+        ref.run_token(t, False)
+    ids = prompt
+    for opts in [dict(repetition_penalty=1.3), dict(temperature=0.7, top_k=5, repetition_penalty=1.2),
+                 dict(temperature=1.1, top_p=0.6), dict(top_k=3)]:
+        a = eng.run_token(ids[-1], True, penalized_token_ids=ids, seen_ids=ids, seed=21, **opts)
+        b = ref.run_token(ids[-1], True, penalized=ids, seen=ids, seed=21, **opts)
+        assert a == b, f"{opts}: {a} != {b}"
+        assert rel_err(eng.read_logits(), ref.logits()) <= 1e-3
+        ids = ids + [a]
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-llama"])
+def test_fp32_kv_cache(name, synth):
+    w, loaded, ref = _pair(synth, name, kv="f32")
+    prompt = _prompt(w, seed=6)
+    out = generate_llama_wgsl(loaded, prompt, 16)
+    assert out["ids"] == ref.generate(prompt, 16)
+    assert rel_err(loaded.engine.read_logits(), ref.logits()) <= 1e-3
+
+
+def test_kv_cache_rows_match(synth):
+    w, loaded, ref = _pair(synth, "tiny-qwen3")
+    eng = loaded.engine
+    for t in _prompt(w, seed=7, n=9):
+        eng.run_token(t, False)
+        ref.run_token(t, False)
+    n = w.spec.kv_heads * w.spec.head_dim
+    for layer in range(w.spec.layers):
+        for pos in (0, 4, 8):
+            for is_v in (False, True):
+                g = eng.read_kv(layer, is_v, pos)
+                r = ref.read_kv(layer, is_v, pos, n)
+                # fp16 cache: at most one binary16 ulp apart
+                assert np.max(np.abs(g - r)) <= np.max(np.abs(r)) * 2e-3 + 1e-6
+
+
+def test_long_context_window(synth):
+    """Sliding-window layers and long positions via the synthetic K/V fill."""
+    w, loaded, ref = _pair(synth, "tiny-gemma3")
+    eng = loaded.engine
+    pos = 80
+    eng.fake_context(pos, seed=3)
+    ref.fake_context(pos, seed=3)
+    tok = 123
+    for _ in range(3):
+        a = eng.run_token(tok, True)
+        b = ref.run_token(tok, True)
+        assert rel_err(eng.read_logits(), ref.logits()) <= 1e-3
+        assert a == b
+        tok = a
+
+
+def test_context_exhaustion_and_reset(synth):
+    w, loaded, _ = _pair(synth, "tiny-llama-q8", max_context=20)
+    eng = loaded.engine
+    for i in range(20):
+        eng.run_token(i + 3, i == 19)
+    with pytest.raises(ChonkError) as ei:
+        eng.run_token(5, True)
+    assert ei.value.status_name == "ECONTEXT"
+    assert "context exhausted at 20 tokens" in str(ei.value)
+    eng.reset()
+    assert eng.position == 0
+    eng.run_token(5, True)
+    assert eng.position == 1
+
+
+def test_bad_token_rejected(synth):
+    w, loaded, _ = _pair(synth, "tiny-llama-q8")
+    with pytest.raises(ChonkError) as ei:
+        loaded.engine.run_token(w.spec.vocab + 5, True)
+    assert "outside embedding table" in str(ei.value)
+    # the engine stays usable
+    loaded.engine.run_token(1, True)
+
+
+def test_shard_directory_load(synth, tmp_path):
+    from chonklm_amd import shard_gguf
+
+    w = WORKLOADS["tiny-qwen3"]
+    path = synth("tiny-qwen3")
+    shard_dir = shard_gguf(path, str(tmp_path / "shards"), shard_size=65536)
+    a = LlamaWgslEngine(w.model_def(shard_dir))
+    b = LlamaWgslEngine(w.model_def(path))
+    prompt = _prompt(w, seed=8, n=6)
+    for i, t in enumerate(prompt):
+        need = i == len(prompt) - 1
+        assert a.run_token(t, need) == b.run_token(t, need)
+    np.testing.assert_array_equal(a.read_logits(), b.read_logits())
