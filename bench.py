@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""Batch-1 decode benchmark on one MI355X.
+
+Workload (default): the Qwen3-0.6B-shaped Q4_K_M decoder (hidden 1024, 28
+layers, 16 q / 8 kv heads, head_dim 128, FFN 3072, vocab 151936, tied Q6_K
+lm_head), random N(0, 0.02) weights, a 2048-token seeded random prompt
+prefilled on the device, then greedy decode with an fp16 K/V cache. A step is
+one decode token; `value` is decode tokens/s over the K timed steps (weights
+and K/V cache resident in HBM; timed with HIP events on the engine stream).
+
+Also reported:
+  roofline      the kernel class with the most time per step, its algorithmic
+                bytes per launch / mean launch time vs 8 TB/s;
+  step_roofline weight + K/V bytes per token / ms per token vs 8 TB/s;
+  q4k_matvec    the Q4_K gate|up matvec's GB/s;
+  cpu_baseline  the oracle (CPU restatement of the reference WGSL
+                arithmetic) timed on a bounded sample of the same decode.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "batch-1 decode tokens/s + Q4_K matvec achieved GB/s vs HBM peak, 1×MI355X"
+HBM_PEAK_GBS = 8000.0
+
+
+def kernel_class(name: str) -> str:
+    return name.split(".", 1)[1] if "." in name else name
+
+
+def build_model(workload: str, cache_dir: Path) -> str:
+    from chonklm_amd import write_synthetic_gguf
+
+    cache_dir.mkdir(parents=True, exist_ok=True)
+    path = cache_dir / f"{workload}.gguf"
+    if not path.exists():
+        tmp = cache_dir / f"{workload}.gguf.tmp"
+        write_synthetic_gguf(workload, str(tmp), threads=min(16, os.cpu_count() or 4))
+        os.replace(tmp, path)
+    return str(path)
+
+
+def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:
+    """Oracle decode steps at the benchmark's context, fake K/V, greedy."""
+    from oracle.oracle import OracleModel
+
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, pos + 64, kv_f16=True, threads=threads)
+    ref.fake_context(pos, seed=1)
+    tok = 1
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        tok = ref.run_token(tok, True)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 64:
+            break
+    ref.close()
+    return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps of the same model at context {pos}..{pos + n} "
+                      f"(synthetic K/V), oracle CPU restatement of the reference WGSL arithmetic, {el:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", default="qwen3-0.6b-q4_k_m")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--no-kernel-times", action="store_true",
+                    help="skip the per-kernel timing pass (profiling runs)")
+    ap.add_argument("--fake-prefill", action="store_true",
+                    help="fill the K/V cache with synthetic values instead of prefilling the prompt "
+                         "(profiling runs: the trace then holds decode steps only)")
+    ap.add_argument("--model-cache", default=os.environ.get("CHONK_MODEL_CACHE", "/tmp/chonk_models"))
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py measures one GPU: batch-1 decode does not shard across GPUs "
+              "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    from chonklm_amd import WORKLOADS, generate_llama_wgsl, load_llama_wgsl_model
+
+    w = WORKLOADS[args.workload]
+    t_build = time.perf_counter()
+    path = build_model(args.workload, Path(args.model_cache))
+    build_s = time.perf_counter() - t_build
+
+    ctx = w.prompt_tokens + 1 + args.warmup + args.steps + 8
+    md = w.model_def(path)
+    md.max_context = ctx
+    loaded = load_llama_wgsl_model(md)
+    eng = loaded.engine
+    info = eng.info
+    prompt = np.random.default_rng(1234).integers(0, w.spec.vocab, w.prompt_tokens).tolist()
+
+    if args.fake_prefill:
+        eng.fake_context(w.prompt_tokens, seed=1)
+        eng.run_token(prompt[-1], True)
+        prefill_ms = float("nan")
+    else:
+        # device prefill of the prompt (+ the first generated token)
+        out = generate_llama_wgsl(loaded, prompt, 1)
+        prefill_ms = out["prefillMs"]
+    pos0 = eng.position
+
+    # timed greedy decode
+    t0 = time.perf_counter()
+    ms = eng.bench_decode(args.warmup, args.steps)
+    wall_ms = (time.perf_counter() - t0) * 1000.0
+    ms_per_step = ms / args.steps
+    tok_s = 1000.0 / ms_per_step
+    pos_end = eng.position
+
+    # per-kernel launch times (HIP events, same arguments as in the step)
+    n_kernels = info["kernels_per_step"]
+    classes: dict[str, dict] = {}
+    for kid in range(0 if args.no_kernel_times else n_kernels - 1):  # select advances the position
+        name, us, nbytes = eng.bench_kernel(kid, args.kernel_reps)
+        c = classes.setdefault(kernel_class(name), {"launches": 0, "us": 0.0, "bytes": 0})
+        c["launches"] += 1
+        c["us"] += us
+        c["bytes"] += nbytes
+    if not classes:
+        classes["none"] = {"launches": 1, "us": float("nan"), "bytes": 0}
+    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["us"])
+    dom_us = dom["us"] / dom["launches"]
+    dom_bytes = dom["bytes"] / dom["launches"]
+    dom_gbs = dom_bytes / dom_us / 1e3
+    gu = classes.get("gateup")
+
+    # whole-step bytes: weights + K/V read at the mean timed position + K/V write
+    kvdim = info["kv_heads"] * info["head_dim"]
+    mean_pos = (pos0 + args.warmup + pos_end) / 2.0
+    kv_bytes = 2 * info["layers"] * kvdim * (mean_pos + 1) * 2
+    step_bytes = info["weight_bytes_per_token"] + kv_bytes
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": w.description or w.name,
+            "name": w.name,
+            "batch": 1,
+            "prompt_tokens": w.prompt_tokens,
+            "context_at_timed_start": pos0 + args.warmup,
+            "context_at_end": pos_end,
+            "kv_cache": "f16",
+            "weights": "Q4_K_M GGUF (Q4_K / Q6_K), random N(0,0.02)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom_name,
+            "achieved": round(dom_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(dom_bytes),
+            "us_per_launch": round(dom_us, 3),
+        },
+        "step_roofline": {
+            "bytes_per_token": int(step_bytes),
+            "weight_bytes_per_token": int(info["weight_bytes_per_token"]),
+            "achieved": round(step_gbs, 1),
+            "unit": "GB/s",
+            "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        },
+        "q4k_matvec": None if not gu else {
+            "kernel": "gateup (Q4_K, fused RMSNorm + SwiGLU)",
+            "achieved": round(gu["bytes"] / gu["us"] / 1e3, 1), "unit": "GB/s",
+            "us_per_launch": round(gu["us"] / gu["launches"], 3)},
+        "kernels": {k: {"launches": v["launches"], "us_per_step": round(v["us"], 2),
+                        "gb_s": round(v["bytes"] / v["us"] / 1e3, 1)} for k, v in classes.items()},
+        "kernel_sum_us": round(sum(v["us"] for v in classes.values()), 2),
+        "wall_ms_timed": round(wall_ms, 3),
+        "prefill_ms": None if prefill_ms != prefill_ms else round(prefill_ms, 2),
+        "prefill_tokens_per_sec": None if prefill_ms != prefill_ms else round(w.prompt_tokens / (prefill_ms / 1000.0), 1),
+        "model_build_s": round(build_s, 1),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        result["cpu_baseline"] = cpu_baseline(path, w, pos0, args.cpu_seconds, threads)
+    loaded.engine.dispose()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

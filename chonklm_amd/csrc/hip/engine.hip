@@ -23,8 +23,11 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -81,6 +84,44 @@ Stripes repack(uint32_t type, const uint8_t* raw, int64_t N, int64_t K) {
 }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Uncached device memory for cross-workgroup exchange (attention partials and
+// arrival counters). Once a kernel has read such memory it is never freed:
+// blocks return to a per-device free list and are reused by later engines.
+class UncachedPool {
+ public:
+  void* take(int device, size_t bytes) {
+    std::lock_guard<std::mutex> l(mu_);
+    auto& fl = free_[device];
+    for (size_t i = 0; i < fl.size(); ++i) {
+      if (fl[i].second >= bytes) {
+        void* p = fl[i].first;
+        sizes_[p] = fl[i].second;
+        fl.erase(fl.begin() + (long)i);
+        return p;
+      }
+    }
+    void* p = nullptr;
+    HIP_OK(hipExtMallocWithFlags(&p, align256(bytes), hipDeviceMallocUncached));
+    sizes_[p] = align256(bytes);
+    return p;
+  }
+  void give_back(int device, void* p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> l(mu_);
+    free_[device].emplace_back(p, sizes_[p]);
+  }
+
+ private:
+  std::mutex mu_;
+  std::map<int, std::vector<std::pair<void*, size_t>>> free_;
+  std::map<void*, size_t> sizes_;
+};
+
+UncachedPool& uncached_pool() {
+  static UncachedPool* pool = new UncachedPool();  // process lifetime, never destroyed
+  return *pool;
+}
 
 // Device memory arena: one allocation, bump-allocated 256-byte aligned.
 class Arena {
@@ -233,11 +274,14 @@ struct chonk_engine {
         *logits = nullptr, *part = nullptr;
   Candidate* cand = nullptr;
   uint32_t* cnt = nullptr;
+  void* uncached = nullptr;       // part + cnt, from the uncached pool
+  bool use_graph = true;
   DevState* st = nullptr;
   DevSampling* samp = nullptr;
   int32_t *hist = nullptr, *gen = nullptr;
   uint32_t *pen_bits = nullptr, *seen_bits = nullptr;
   int groups = 0, chunk = 0, nchunk = 0;
+  std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
   std::vector<Launch> step_logits, step_plain;
   hipGraph_t graph_logits = nullptr, graph_plain = nullptr;
   hipGraphExec_t exec_logits = nullptr, exec_plain = nullptr;
@@ -422,6 +466,19 @@ void plan_seg(MvSeg& sg, const QMat& w, int n_out, bool glu, int wg_begin) {
 
 int seg_wgs(const MvSeg& sg) { return (sg.n_out + sg.tile - 1) / sg.tile; }
 
+// Rotary inverse frequencies theta^(-2d/hd) in f32, evaluated once on the host
+// with the reference's operation order (rope_angle, llama-wgsl-runtime.ts:2884-2887).
+const float* rope_table(chonk_engine* e, uint32_t theta, int hd) {
+  for (const auto& t : e->rope_tables)
+    if (t.first == theta) return t.second;
+  std::vector<float> inv((size_t)hd / 2);
+  for (int d = 0; d < hd / 2; ++d) inv[d] = std::pow((float)theta, (-2.0f * (float)d) / (float)hd);
+  float* p = (float*)e->weights.take(inv.size() * 4);
+  HIP_OK(hipMemcpy(p, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
+  e->rope_tables.emplace_back(theta, p);
+  return p;
+}
+
 void build_steps(chonk_engine* e) {
   const ModelCfg& c = e->cfg;
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, G = c.heads / c.kv_heads;
@@ -508,7 +565,13 @@ void build_steps(chonk_engine* e) {
       t.kv_f16 = e->kv_elem == 2 ? 1 : 0;
       t.eps = c.qk_eps;
       t.scale = c.scale;
-      L.shmem = attn_shared_bytes(G, c.hd, e->chunk);
+      t.merge_floats = attn_merge_floats(G, c.hd, e->nchunk);
+      t.rope_inv = rope_table(e, c.layer[i].theta, c.hd);
+      // full-context layers fetch K/V before the position is known; that reads
+      // the whole cache span of every chunk, so only for short contexts
+      t.spec_kv = (t.window == 0 && c.ctx <= 4096) ? 1 : 0;
+      t.tpp = attn_threads_per_position(c.hd, e->chunk, (int)e->kv_elem);
+      L.shmem = attn_shared_bytes(G, c.hd, e->chunk, e->nchunk, e->kv_elem);
       L.grid = c.kv_heads * e->nchunk;
       L.name = li + "attn";
       L.layer = i;
@@ -673,6 +736,7 @@ void engine_free(chonk_engine* e) {
   if (e->graph_plain) (void)hipGraphDestroy(e->graph_plain);
   e->weights.release();
   e->state.release();
+  uncached_pool().give_back(e->device, e->uncached);
   if (e->h_state) (void)hipHostFree(e->h_state);
   if (e->h_tok) (void)hipHostFree(e->h_tok);
   if (e->h_samp) (void)hipHostFree(e->h_samp);
@@ -737,13 +801,23 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       vec_bytes(c.hd);
       vec_bytes(c.hd);
     }
+    vec_bytes(c.hd / 2);  // rotary table (one per distinct theta at most)
   }
   e->weights.reserve(wbytes);
 
   // state arena: K/V cache + activations + bookkeeping
   e->groups = (c.vocab + 255) / 256;
+  // attention chunk: the smallest power of two >= 16 giving at most ~512
+  // workgroups and at most 32 chunks over the whole context (the last chunk to
+  // finish merges all chunks), capped by the kernel's limit for hd
   e->chunk = 16;
-  while (e->chunk < 256 && (int64_t)c.kv_heads * ((c.ctx + e->chunk - 1) / e->chunk) > 512) e->chunk <<= 1;
+  while (e->chunk < attn_max_chunk(c.hd) &&
+         ((int64_t)c.kv_heads * ((c.ctx + e->chunk - 1) / e->chunk) > 512 || (c.ctx + e->chunk - 1) / e->chunk > 32))
+    e->chunk <<= 1;
+  if (const char* ov = std::getenv("CHONK_ATTN_CHUNK")) {  // tuning override: a power of two in [16, limit]
+    const int v = std::atoi(ov);
+    if (v >= 16 && v <= attn_max_chunk(c.hd) && (v & (v - 1)) == 0) e->chunk = v;
+  }
   e->nchunk = (c.ctx + e->chunk - 1) / e->chunk;
   const int G = c.heads / c.kv_heads;
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
@@ -751,8 +825,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   size_t sbytes = 2 * align256(kv_bytes) * c.layers;
   sbytes += 3 * align256((size_t)H * 4) + align256((size_t)(qdim + 2 * kvdim) * 4) + align256((size_t)qdim * 4) +
             align256((size_t)c.ffn * 4) + align256((size_t)c.vocab * 4) +
-            align256((size_t)c.kv_heads * e->nchunk * G * (c.hd + 2) * 4) + align256((size_t)e->groups * 8) +
-            align256((size_t)c.kv_heads * 4) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
+            align256((size_t)e->groups * 8) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
             2 * align256((size_t)(c.ctx + 1) * 4) + 2 * align256(bits_words * 4);
   e->state.reserve(sbytes);
 
@@ -799,9 +872,15 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->attn = (float*)e->state.take((size_t)qdim * 4);
   e->ff = (float*)e->state.take((size_t)c.ffn * 4);
   e->logits = (float*)e->state.take((size_t)c.vocab * 4);
-  e->part = (float*)e->state.take((size_t)c.kv_heads * e->nchunk * G * (c.hd + 2) * 4);
   e->cand = (Candidate*)e->state.take((size_t)e->groups * 8);
-  e->cnt = (uint32_t*)e->state.take((size_t)c.kv_heads * 4);
+  {
+    const size_t rowf = ((size_t)G * (c.hd + 2) + 3) & ~(size_t)3;
+    const size_t part_bytes = align256((size_t)c.kv_heads * e->nchunk * rowf * 4);
+    e->uncached = uncached_pool().take(e->device, part_bytes + align256((size_t)c.kv_heads * 4));
+    e->part = (float*)e->uncached;
+    e->cnt = (uint32_t*)((uint8_t*)e->uncached + part_bytes);
+    HIP_OK(hipMemset(e->cnt, 0, (size_t)c.kv_heads * 4));
+  }
   e->st = (DevState*)e->state.take(sizeof(DevState));
   e->samp = (DevSampling*)e->state.take(sizeof(DevSampling));
   e->hist = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
@@ -821,6 +900,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
   HIP_OK(init_kernel_attributes());
   build_steps(e.get());
+  const char* ng = std::getenv("CHONK_NO_GRAPH");
+  e->use_graph = !(ng && ng[0] == '1');
   for (const Launch& L : e->step_logits)
     if (L.shmem > lds_limit())
       throw Error(CHONK_EINVAL, "kernel " + L.name + " needs " + std::to_string(L.shmem) + " bytes of LDS, above the " +
@@ -828,6 +909,16 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   capture(e.get(), e->step_plain, &e->graph_plain, &e->exec_plain);
   capture(e.get(), e->step_logits, &e->graph_logits, &e->exec_logits);
   *out = e.release();
+}
+
+// One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
+// cannot trace graph launches) the same launches issued one by one.
+void replay(chonk_engine* e, bool logits) {
+  if (e->use_graph) {
+    HIP_OK(hipGraphLaunch(logits ? e->exec_logits : e->exec_plain, e->stream));
+  } else {
+    for (const Launch& L : logits ? e->step_logits : e->step_plain) enqueue(L, e->stream);
+  }
 }
 
 void upload_state_fields(chonk_engine* e, const DevState& s) {
@@ -927,7 +1018,7 @@ int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_
     const DevSampling d = make_sampling(e, s, stage1, n_seen > 0);
     if (d.sample_mode && d.seen_penalty) upload_bits(e, e->seen_bits, seen, n_seen);
     upload_sampling(e, d);
-    HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    replay(e, true);
     HIP_OK(hipMemcpyAsync(e->h_state, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
     HIP_OK(hipStreamSynchronize(e->stream));
     const DevState st = *e->h_state;
@@ -938,7 +1029,7 @@ int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_
     e->logits_valid = true;
     return st.last_token;
   }
-  HIP_OK(hipGraphLaunch(e->exec_plain, e->stream));
+  replay(e, false);
   e->pos += 1;
   return 0;
 }
@@ -1015,8 +1106,8 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
     std::vector<int32_t> suf(prompt + prefix, prompt + n_prompt);
     HIP_OK(hipMemcpy(e->hist + e->pos, suf.data(), suf.size() * 4, hipMemcpyHostToDevice));
     upload_state_fields(e, st);
-    for (size_t i = 0; i + 1 < n_suffix; ++i) HIP_OK(hipGraphLaunch(e->exec_plain, e->stream));
-    HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    for (size_t i = 0; i + 1 < n_suffix; ++i) replay(e, false);
+    replay(e, true);
     st = read_state(e);
     if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
     e->pos = st.pos;
@@ -1047,7 +1138,7 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
     int64_t remaining = max - 1;
     while (remaining > 0 && !st.stopped) {
       const int64_t batch = std::min<int64_t>(remaining, 32);
-      for (int64_t i = 0; i < batch; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+      for (int64_t i = 0; i < batch; ++i) replay(e, true);
       remaining -= batch;
       st = read_state(e);
       if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
@@ -1345,12 +1436,12 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
     int32_t tok = 0;
     HIP_OK(hipMemcpy(&tok, e->hist + e->pos, 4, hipMemcpyDeviceToHost));
     check_token(e, tok);
-    for (int i = 0; i < n_warmup; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    for (int i = 0; i < n_warmup; ++i) replay(e, true);
     hipEvent_t a, b;
     HIP_OK(hipEventCreate(&a));
     HIP_OK(hipEventCreate(&b));
     HIP_OK(hipEventRecord(a, e->stream));
-    for (int i = 0; i < n_steps; ++i) HIP_OK(hipGraphLaunch(e->exec_logits, e->stream));
+    for (int i = 0; i < n_steps; ++i) replay(e, true);
     HIP_OK(hipEventRecord(b, e->stream));
     HIP_OK(hipEventSynchronize(b));
     float ms = 0;

@@ -71,15 +71,19 @@ struct AttnArgs {
   const float* qkv;       // q[heads*hd] | k[kv*hd] | v[kv*hd]
   const float* qn_w;      // per-head q RMSNorm weight (null: none)
   const float* kn_w;
+  const float* rope_inv;  // [hd/2] theta^(-2d/hd), f32
   void* kc;               // [kv_heads][C][hd], half or float
   void* vc;
-  float* part;            // [kv_heads][nchunk][G][hd + 2]
-  uint32_t* cnt;          // [kv_heads], zero between launches
+  float* part;            // [kv_heads][nchunk] rows of G*(hd+2) floats padded to 4, uncached memory
+  uint32_t* cnt;          // [kv_heads], uncached memory, zero between launches
   float* out;             // [heads*hd]
   DevState* st;
   int32_t heads, kv_heads, hd, ctx, window, chunk, nchunk;
   uint32_t theta;         // Math.round(ropeTheta)
   int32_t interleaved, kv_f16;
+  int32_t merge_floats;   // LDS floats available for staging chunk partials
+  int32_t spec_kv;        // request the chunk's K/V before the position is known
+  int32_t tpp;            // threads per position in the score phase (power of two)
   float eps, scale;
 };
 
@@ -98,7 +102,11 @@ struct SelArgs {
 
 // Launch parameter helpers -------------------------------------------------------
 size_t mv_shared_bytes(int k, int max_tile_rows);
-size_t attn_shared_bytes(int group, int hd, int chunk);
+size_t attn_shared_bytes(int group, int hd, int chunk, int nchunk, int kv_elem);
+int attn_merge_floats(int group, int hd, int nchunk);
+// Largest chunk (positions per attention workgroup) the kernel supports for hd.
+int attn_max_chunk(int hd);
+int attn_threads_per_position(int hd, int chunk, int kv_elem);
 int pick_lpr(int units);
 
 // Raises the dynamic LDS limit of the kernels; call once per device before launching.

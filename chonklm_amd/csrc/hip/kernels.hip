@@ -16,6 +16,7 @@
 // final group argmax is fused into the lm_head matvec epilogue.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "kernels.h"
@@ -27,16 +28,55 @@ namespace {
 
 constexpr float kNegBig = -3.402823e38f;  // the WGSL literal -3.402823e38
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane steps without the LDS crossbar: DPP quad/row permutations inside
+// 16-lane rows, a swizzle across the two rows of a 32-lane half, and scalar
+// lane reads across halves. Every lane of an aligned group of N lanes ends with
+// the same value. Lanes of a group must be active together.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+__device__ __forceinline__ float lane_of(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp<0xb1>(v);   // quad_perm 1,0,3,2
+  if constexpr (N >= 4) v += dpp<0x4e>(v);   // quad_perm 2,3,0,1
+  if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror
+  if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror
+  if constexpr (N >= 32) v += swz_xor16(v);
+  if constexpr (N >= 64) v = lane_of(v, 0) + lane_of(v, 32);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp<0xb1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<0x4e>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<0x141>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<0x140>(v));
+  if constexpr (N >= 32) v = fmaxf(v, swz_xor16(v));
+  if constexpr (N >= 64) v = fmaxf(lane_of(v, 0), lane_of(v, 32));
   return v;
 }
+// runtime group width (power of two in [1, 64])
+__device__ __forceinline__ float group_sum_n(float v, int n) {
+  switch (n) {
+    case 2: return group_sum<2>(v);
+    case 4: return group_sum<4>(v);
+    case 8: return group_sum<8>(v);
+    case 16: return group_sum<16>(v);
+    case 32: return group_sum<32>(v);
+    case 64: return group_sum<64>(v);
+    default: return v;
+  }
+}
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 // Sum over the 256 threads; red must hold 4 floats. Callable repeatedly.
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -79,12 +119,105 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// matvec prologue: activation vector into LDS (xs) plus 16-element run sums.
-__device__ void mv_prologue(const MvArgs& a, float* xs, float* xs16, float* red) {
+// matvec: activation staging, weight streaming, epilogues.
+
+typedef __attribute__((address_space(1))) void gmem_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Copies n floats from global memory into LDS with the CDNA3/4 direct-to-LDS
+// loads (16 bytes per lane, no registers); completion is awaited with
+// s_waitcnt vmcnt(0) + a barrier by the caller.
+__device__ __forceinline__ void lds_dma(const float* src, float* dst, int n) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int base = wave * 256; base < n; base += 4 * 256) {
+    const int idx = base + lane * 4;
+    if (idx < n) __builtin_amdgcn_global_load_lds((gmem_void*)(src + idx), (lds_void*)(dst + base), 16, 0, 0);
+  }
+}
+
+// This workgroup's segment, picked field by field (forming a reference into
+// the argument block would make the compiler copy the whole block to scratch).
+struct SegView {
+  QMat w;
+  const uint8_t *u0, *u1, *u2, *u3;  // GLU up-matrix streams
+  float* out;
+  const float* add;
+  int n_out, tile, lpr, wg_begin;
+};
+
+__device__ __forceinline__ SegView seg_view(const MvArgs& a) {
+  const int b = (int)blockIdx.x;
+  const bool s1 = a.nseg > 1 && b >= a.seg[1].wg_begin;
+  const bool s2 = a.nseg > 2 && b >= a.seg[2].wg_begin;
+#define CHONK_PICK(f) (s2 ? a.seg[2].f : (s1 ? a.seg[1].f : a.seg[0].f))
+  SegView v;
+  v.w.s0 = CHONK_PICK(w.s0);
+  v.w.s1 = CHONK_PICK(w.s1);
+  v.w.s2 = CHONK_PICK(w.s2);
+  v.w.s3 = CHONK_PICK(w.s3);
+  v.w.type = CHONK_PICK(w.type);
+  v.w.n = CHONK_PICK(w.n);
+  v.w.k = CHONK_PICK(w.k);
+  v.w.pad = 0;
+  v.u0 = CHONK_PICK(w2.s0);
+  v.u1 = CHONK_PICK(w2.s1);
+  v.u2 = CHONK_PICK(w2.s2);
+  v.u3 = CHONK_PICK(w2.s3);
+  v.out = CHONK_PICK(out);
+  v.add = CHONK_PICK(add);
+  v.n_out = CHONK_PICK(n_out);
+  v.tile = CHONK_PICK(tile);
+  v.lpr = CHONK_PICK(lpr);
+  v.wg_begin = CHONK_PICK(wg_begin);
+#undef CHONK_PICK
+  return v;
+}
+
+// LDS layout of the matvec kernels (floats):
+//   xs[K] | wn[K] | dl[K] | wd[K] | xs16[K/16] | red[8] | res[...]
+struct MvLds {
+  float *xs, *wn, *dl, *wd, *xs16, *red, *res;
+};
+
+__device__ __forceinline__ MvLds mv_lds(float* smem, int K) {
+  MvLds l;
+  l.xs = smem;
+  l.wn = smem + K;
+  l.dl = smem + 2 * K;
+  l.wd = smem + 3 * K;
+  l.xs16 = smem + 4 * K;
+  l.red = l.xs16 + K / 16;
+  l.res = l.red + 8;
+  return l;
+}
+
+// Issues the activation loads of the prologue (no waiting).
+__device__ __forceinline__ void mv_stage(const MvArgs& a, const MvLds& l) {
+  const int K = a.k;
+  switch (a.pro) {
+    case PRO_PLAIN: lds_dma(a.in, l.xs, K); break;
+    case PRO_NORM:
+      lds_dma(a.in, l.xs, K);
+      lds_dma(a.w_norm, l.wn, K);
+      break;
+    case PRO_RES_NORM:
+      lds_dma(a.in, l.xs, K);
+      lds_dma(a.delta, l.dl, K);
+      lds_dma(a.w_delta, l.wd, K);
+      lds_dma(a.w_norm, l.wn, K);
+      break;
+    default:  // PRO_EMBED_NORM: the row depends on the token; only the norm weight is staged
+      lds_dma(a.w_norm, l.wn, K);
+      break;
+  }
+}
+
+// Completes the prologue once the staged data has landed: xs becomes the
+// matvec input (normalised as the mode requires), xs16 its 16-element sums.
+__device__ void mv_finish(const MvArgs& a, const MvLds& l) {
   const int K = a.k, tid = threadIdx.x;
-  if (a.pro == PRO_PLAIN || a.pro == PRO_NORM) {
-    for (int i = tid; i < K; i += kWg) xs[i] = a.in[i];
-  } else if (a.pro == PRO_EMBED_NORM) {
+  float* xs = l.xs;
+  if (a.pro == PRO_EMBED_NORM) {
     int tok = a.hist[a.st->pos];
     if (tok < 0 || tok >= a.vocab) {
       if (tid == 0 && blockIdx.x == 0) a.st->error = 2;
@@ -100,102 +233,128 @@ __device__ void mv_prologue(const MvArgs& a, float* xs, float* xs16, float* red)
         for (int e = 0; e < 32; ++e) xs[unit_col<T>(u, e)] = __fmul_rn(v[e], a.embed_scale);
       }
     });
-  } else {  // PRO_RES_NORM
+    __syncthreads();
+  } else if (a.pro == PRO_RES_NORM) {
     float ss = 0.f;
-    for (int i = tid; i < K; i += kWg) {
-      const float d = a.delta[i];
-      ss += d * d;
-    }
-    ss = block_sum(ss, red);
+    for (int i = tid; i < K; i += kWg) ss += l.dl[i] * l.dl[i];
+    ss = block_sum(ss, l.red);
     const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
     for (int i = tid; i < K; i += kWg) {
-      const float nd = __fmul_rn(__fmul_rn(a.delta[i], inv), a.w_delta[i]);
-      const float r = __fadd_rn(a.in[i], nd);
-      xs[i] = fminf(fmaxf(r, -65000.0f), 65000.0f);
+      const float nd = __fmul_rn(__fmul_rn(l.dl[i], inv), l.wd[i]);
+      xs[i] = fminf(fmaxf(__fadd_rn(xs[i], nd), -65000.0f), 65000.0f);
     }
+    __syncthreads();
   }
-  __syncthreads();
   if (a.pro != PRO_PLAIN) {
     if ((a.pro == PRO_EMBED_NORM || a.pro == PRO_RES_NORM) && blockIdx.x == 0) {
       for (int i = tid; i < K; i += kWg) a.res_out[i] = xs[i];
     }
     float ss = 0.f;
     for (int i = tid; i < K; i += kWg) ss += xs[i] * xs[i];
-    ss = block_sum(ss, red);
+    ss = block_sum(ss, l.red);
     const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-    for (int i = tid; i < K; i += kWg) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), a.w_norm[i]);
+    for (int i = tid; i < K; i += kWg) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), l.wn[i]);
     __syncthreads();
   }
   for (int j = tid; j < K / 16; j += kWg) {
     const float4* p = (const float4*)(xs + 16 * j);
     const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-    xs16[j] = ((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w)) +
-              ((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w));
+    l.xs16[j] = ((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w)) +
+                ((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w));
   }
   __syncthreads();
 }
 
-// Rows [t0, t0 + nt) of segment g (2*nt interleaved gate/up rows when glu);
-// row results into res[] (virtual row order).
-template <int T>
-__device__ void mv_core(const MvSeg& g, bool glu, int t0, int nt, const float* xs, const float* xs16, float* res) {
+// Rows [t0, t0 + nt) of the segment (2*nt interleaved gate/up rows when GLU).
+// Lane group lg of `lpr` lanes owns virtual rows lg, lg+ng, ...; lane li owns
+// units li, li+lpr, ... of each row. The lane's (row, unit) items are walked
+// row-major in batches of kPf fragments: the first batch is issued together
+// with the activation staging (weights do not depend on it) and each later
+// batch is loaded while the previous one is being reduced.
+template <int T, bool GLU>
+__device__ __forceinline__ bool mv_work(const MvArgs& a, const SegView& g, int t0, int nt, const MvLds& l) {
+  // prefetch depth: 4 fragments of <= 9 dwords, 2 of the larger Q5_K ones
+  constexpr int kPf = sizeof(Frag<T>) > 40 ? 2 : 4;
   const int U = g.w.k >> 5;
   const int lpr = g.lpr;
   const int shift = __builtin_ctz((unsigned)lpr);
   const int ng = kWg >> shift;
   const int lg = threadIdx.x >> shift, li = threadIdx.x & (lpr - 1);
-  const int nv = glu ? 2 * nt : nt;
-  for (int v0 = lg; v0 < nv; v0 += 2 * ng) {
-    const int v1 = v0 + ng;
-    const bool has1 = v1 < nv;
-    const QMat& m0 = (glu && (v0 & 1)) ? g.w2 : g.w;
-    const QMat& m1 = (glu && (v1 & 1)) ? g.w2 : g.w;
-    const int r0 = t0 + (glu ? (v0 >> 1) : v0);
-    const int r1 = t0 + (glu ? (v1 >> 1) : v1);
-    float a0 = 0.f, a1 = 0.f;
-    for (int u = li; u < U; u += lpr) {
-      const Frag<T> f0 = load_unit<T>(m0, r0, u);
-      Frag<T> f1;
-      if (has1) f1 = load_unit<T>(m1, r1, u);
-      a0 += dot_unit<T>(f0, u, xs, xs16);
-      if (has1) a1 += dot_unit<T>(f1, u, xs, xs16);
+  const int nv = nt > 0 ? (GLU ? 2 * nt : nt) : 0;
+  const int rows_lane = lg < nv ? (nv - lg + ng - 1) / ng : 0;
+  const int ucount = (U + lpr - 1) / lpr;  // units per lane (uniform in a lane group)
+  const int items = rows_lane * ucount;
+
+  auto load_item = [&](int ii, Frag<T>& f) {
+    const int r = ii / ucount, j = ii - r * ucount;
+    const int v = lg + r * ng, u = li + j * lpr;
+    if (ii < items && u < U) {
+      QMat m = g.w;
+      if (GLU && (v & 1)) {
+        m.s0 = g.u0;
+        m.s1 = g.u1;
+        m.s2 = g.u2;
+        m.s3 = g.u3;
+      }
+      f = load_unit<T>(m, t0 + (GLU ? (v >> 1) : v), u);
     }
-    for (int off = lpr >> 1; off > 0; off >>= 1) {
-      a0 += __shfl_xor(a0, off, 64);
-      a1 += __shfl_xor(a1, off, 64);
+  };
+
+  mv_stage(a, l);
+  Frag<T> cur[kPf];
+#pragma unroll
+  for (int q = 0; q < kPf; ++q) load_item(q, cur[q]);
+  const int stopped = __hip_atomic_load(&a.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (stopped) return false;
+  mv_finish(a, l);
+
+  const float* xs = l.xs;
+  const float* xs16 = l.xs16;
+  float acc = 0.f;
+  for (int base = 0; base < items; base += kPf) {
+    Frag<T> nxt[kPf];
+#pragma unroll
+    for (int q = 0; q < kPf; ++q) load_item(base + kPf + q, nxt[q]);
+#pragma unroll
+    for (int q = 0; q < kPf; ++q) {
+      const int ii = base + q;
+      if (ii < items) {
+        const int r = ii / ucount, j = ii - r * ucount;
+        const int u = li + j * lpr;
+        if (u < U) acc += dot_unit<T>(cur[q], u, xs, xs16);
+        if (j == ucount - 1) {
+          acc = group_sum_n(acc, lpr);
+          if (li == 0) l.res[lg + r * ng] = acc;
+          acc = 0.f;
+        }
+      }
     }
-    if (li == 0) {
-      res[v0] = a0;
-      if (has1) res[v1] = a1;
-    }
+#pragma unroll
+    for (int q = 0; q < kPf; ++q) cur[q] = nxt[q];
   }
+  return true;
 }
 
-__global__ __launch_bounds__(kWg) void k_matvec(const MvArgs a) {
+template <int EPI>
+__device__ __forceinline__ void matvec_body(const MvArgs& a) {
   extern __shared__ __align__(16) float smem[];
-  if (a.st->stopped) return;
-  const int K = a.k;
-  float* xs = smem;
-  float* xs16 = xs + K;
-  float* red = xs16 + K / 16;      // 4 floats (padded to 8)
-  float* res = red + 8;            // up to max(2*tile, 256) floats
-  int s = 0;
-  if (a.nseg > 1 && (int)blockIdx.x >= a.seg[1].wg_begin) s = 1;
-  if (a.nseg > 2 && (int)blockIdx.x >= a.seg[2].wg_begin) s = 2;
-  const MvSeg& g = s == 0 ? a.seg[0] : (s == 1 ? a.seg[1] : a.seg[2]);
-
-  mv_prologue(a, xs, xs16, red);
-
+  const MvLds l = mv_lds(smem, a.k);
+  const SegView g = seg_view(a);
   const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
-  const bool glu = a.epi == EPI_GLU_SILU || a.epi == EPI_GLU_GELU;
-  if (nt > 0) {
-    with_type(g.w.type, [&]<int T>() { mv_core<T>(g, glu, t0, nt, xs, xs16, res); });
-  }
+  constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
+  // the type is uniform per workgroup, so every thread takes the same branch
+  // (the staging and prologue inside hold barriers)
+  bool live = false;
+  with_type(g.w.type, [&]<int T>() { live = mv_work<T, glu>(a, g, t0, nt, l); });
+  if (!live) return;
   __syncthreads();
 
+  float* res = l.res;
   const int tid = threadIdx.x;
-  switch (a.epi) {
+  switch (EPI) {
     case EPI_STORE:
       for (int t = tid; t < nt; t += kWg) g.out[t0 + t] = res[t];
       break;
@@ -250,211 +409,354 @@ __global__ __launch_bounds__(kWg) void k_matvec(const MvArgs a) {
   if (a.advance_pos && blockIdx.x == 0 && tid == 0) a.st->pos = a.st->pos + 1;
 }
 
+__global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
+__global__ __launch_bounds__(kWg) void k_mv_add(const MvArgs a) { matvec_body<EPI_ADD>(a); }
+__global__ __launch_bounds__(kWg) void k_mv_swiglu(const MvArgs a) { matvec_body<EPI_GLU_SILU>(a); }
+__global__ __launch_bounds__(kWg) void k_mv_geglu(const MvArgs a) { matvec_body<EPI_GLU_GELU>(a); }
+__global__ __launch_bounds__(kWg) void k_mv_logits(const MvArgs a) { matvec_body<EPI_LOGITS>(a); }
+
 // ---------------------------------------------------------------------------
-// GQA decode attention over a chunk of positions, one workgroup per
-// (kv head, chunk). Requires hd in {32, 64, 128, 256}, G <= 8.
+// GQA decode attention, one workgroup per (kv head, chunk of positions).
+//
+//   A  every load that does not depend on the position (the group's q heads,
+//      the new k/v, norm weights, rotary table and, for short full-context
+//      caches, the chunk's K rows into registers and V rows into LDS) is
+//      issued before the position is read.
+//   B  one wave per head: q/k RMSNorm + rotary in one pass; the wave holding
+//      the new k also stores k/v to the cache.
+//   C  each wave owns P = 64/tpp positions (tpp threads per position, each
+//      dotting hd/tpp dims), keeps its own softmax max/sum, then walks its
+//      positions over V with the weights broadcast by readlane.
+//   D  the four wave partials combine into the chunk partial (m, l, acc[hd])
+//      in uncached memory; the last chunk of a kv head to arrive merges.
 constexpr int kMaxG = 8;
 
-__device__ __forceinline__ void load8(const void* cache, int kv_f16, size_t off, float out[8]) {
-  if (kv_f16) {
-    const uint4 raw = *(const uint4*)((const __half*)cache + off);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = h2f(w[i]);
-      out[2 * i + 1] = h2f(w[i] >> 16);
+__host__ __device__ constexpr int attn_tpp(int hd) { return hd / 64 > 2 ? hd / 64 : 2; }
+
+template <bool KV16>
+__device__ __forceinline__ void load_v(const void* tile, int idx, int dpl, float* v) {
+  if constexpr (KV16) {
+    const __half* h = (const __half*)tile + idx;
+    if (dpl == 1) {
+      v[0] = __half2float(h[0]);
+    } else if (dpl == 2) {
+      const uint32_t w = *(const uint32_t*)h;
+      v[0] = h2f(w);
+      v[1] = h2f(w >> 16);
+    } else {
+      const uint2 w = *(const uint2*)h;
+      v[0] = h2f(w.x);
+      v[1] = h2f(w.x >> 16);
+      v[2] = h2f(w.y);
+      v[3] = h2f(w.y >> 16);
     }
   } else {
-    const float4* p = (const float4*)((const float*)cache + off);
-    const float4 a = p[0], b = p[1];
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    const float* f = (const float*)tile + idx;
+    if (dpl == 1) {
+      v[0] = f[0];
+    } else if (dpl == 2) {
+      const float2 w = *(const float2*)f;
+      v[0] = w.x;
+      v[1] = w.y;
+    } else {
+      const float4 w = *(const float4*)f;
+      v[0] = w.x;
+      v[1] = w.y;
+      v[2] = w.z;
+      v[3] = w.w;
+    }
   }
 }
 
-template <int G>
+// o[g][0..DPL) += sum over positions p in [pa, pb) of w_g(p) * V[p][d0..d0+DPL),
+// where w_g(p) sits in lane (p - w0) * tpp of e[g]; four positions per pass
+// so that the LDS reads of a pass overlap.
+template <int G, bool KV16, int DPL>
+__device__ __forceinline__ void v_walk(const void* tile, int hd, int d0, int pa, int pb, int w0, int tpp,
+                                       const float (&e)[G], float (&o)[G][4]) {
+  int p = pa;
+  for (; p + 4 <= pb; p += 4) {
+    float vv[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_v<KV16>(tile, (p + u) * hd + d0, DPL, vv[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sel = (p + u - w0) * tpp;
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[gg]), sel));
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) o[gg][k] += wgt * vv[u][k];
+      }
+    }
+  }
+  for (; p < pb; ++p) {
+    float vv[4];
+    load_v<KV16>(tile, p * hd + d0, DPL, vv);
+    const int sel = (p - w0) * tpp;
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[gg]), sel));
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) o[gg][k] += wgt * vv[k];
+    }
+  }
+}
+
+template <int G, bool KV16>
 __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   extern __shared__ __align__(16) float sm[];
   DevState* st = a.st;
-  if (st->stopped) return;
-  const int pos = st->pos;
-  if (pos >= a.ctx) {
-    if (threadIdx.x == 0) st->error = 1;
-    return;
-  }
   const int kv = blockIdx.x, c = blockIdx.y;
-  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-  const int c_lo = start / a.chunk, c_hi = pos / a.chunk;
-  if (c < c_lo || c > c_hi) return;
-
   const int hd = a.hd, half = hd / 2, CH = a.chunk;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float* q_s = sm;                 // [G][hd]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tpp = a.tpp, P = 64 / tpp;
+  const int my_p = tid / tpp, my_j = tid & (tpp - 1);
+  const int dpt = hd / tpp;
+  const int t_lo = c * CH;  // positions of this chunk: t_lo + p, p < CH
+  constexpr int kElem = KV16 ? 2 : 4;
+  constexpr int kVec = KV16 ? 8 : 16;  // 16-byte K vectors per thread, dpt <= 64
+  const int nvec = dpt * kElem / 16;
+  const int ncp = (a.nchunk + 3) & ~3;
+
+  float* q_s = sm;                 // [G][hd]  raw q, then normalised + rotated
   float* k_new = q_s + G * hd;     // [hd]
   float* v_new = k_new + hd;       // [hd]
-  float* sc_s = v_new + hd;        // [G][CH]
-  float* ml_s = sc_s + G * CH;     // [G][2]
-  float* red = ml_s + 2 * kMaxG;   // [(256 / (hd/8))][G][hd]
+  float* qn = v_new + hd;          // [hd] q-norm weight
+  float* kn = qn + hd;             // [hd] k-norm weight
+  float* inv = kn + hd;            // [hd/2] rotary inverse frequencies (area of hd)
+  float* wpart = inv + hd;         // [4][G][hd] wave partials
+  float* wml = wpart + 4 * G * hd; // [4][kMaxG][2] wave (max, sum)
+  float* wts = wml + 8 * kMaxG;    // [G][ncp] merge weights
+  float* tile = wts + G * ncp;     // V rows [CH][hd] (kElem bytes each), later merge staging
   __shared__ uint32_t s_last;
 
-  const bool own_new = (c == c_hi);
-  const float* qraw = a.qkv;
   const float* kraw = a.qkv + a.heads * hd;
   const float* vraw = kraw + a.kv_heads * hd;
-
-  // A: per-head RMSNorm (or copy) of the group's q heads and, in the chunk
-  // holding `pos`, of the new k.
-  const int nh = G + (own_new ? 1 : 0);
-  for (int hh = wave; hh < nh; hh += 4) {
-    const bool is_k = hh == G;
-    const float* src = is_k ? kraw + kv * hd : qraw + (kv * G + hh) * hd;
-    float* dst = is_k ? k_new : q_s + hh * hd;
-    const float* w = is_k ? a.kn_w : a.qn_w;
-    if (w) {
-      float ss = 0.f;
-      for (int d = lane; d < hd; d += 64) ss += src[d] * src[d];
-      ss = wave_sum(ss);
-      const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
-      for (int d = lane; d < hd; d += 64) dst[d] = __fmul_rn(__fmul_rn(src[d], inv), w[d]);
-    } else {
-      for (int d = lane; d < hd; d += 64) dst[d] = src[d];
+  lds_dma(a.qkv + (size_t)kv * G * hd, q_s, G * hd);
+  lds_dma(kraw + (size_t)kv * hd, k_new, hd);
+  lds_dma(vraw + (size_t)kv * hd, v_new, hd);
+  lds_dma(a.rope_inv, inv, half);
+  if (a.qn_w) {
+    lds_dma(a.qn_w, qn, hd);
+    lds_dma(a.kn_w, kn, hd);
+  }
+  uint4 kreg[kVec];
+  const size_t head_base = (size_t)kv * a.ctx * hd;
+  auto load_chunk = [&](int p_begin, int p_end) {
+    // K: this thread's dims of its position, into registers
+    const int t = t_lo + my_p;
+    if (my_p < CH && my_p >= p_begin && my_p < p_end && t < a.ctx) {
+      const uint4* src = (const uint4*)((const uint8_t*)a.kc + (head_base + (size_t)t * hd + my_j * dpt) * kElem);
+#pragma unroll
+      for (int v = 0; v < kVec; ++v)
+        if (v < nvec) kreg[v] = src[v];
     }
-  }
-  if (own_new)
-    for (int d = tid; d < hd; d += kWg) v_new[d] = vraw[kv * hd + d];
+    // V: rows [p_begin, p_end) of the chunk, direct to LDS
+    const int rows = min(p_end, a.ctx - t_lo) - p_begin;
+    if (rows > 0)
+      lds_dma((const float*)((const uint8_t*)a.vc + (head_base + (size_t)(t_lo + p_begin) * hd) * kElem),
+              (float*)((uint8_t*)tile + (size_t)p_begin * hd * kElem), rows * hd * kElem / 4);
+  };
+  if (a.spec_kv) load_chunk(0, CH);
+  const int stopped = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const int pos = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (stopped) return;
+  if (pos >= a.ctx) {
+    if (tid == 0) st->error = 1;
+    return;
+  }
+  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+  const int c_lo = start / CH, c_hi = pos / CH;
+  if (c < c_lo || c > c_hi) return;
+  const int p_begin = max(start - t_lo, 0);  // valid positions: [p_begin, p_end)
+  const int p_end = min(pos + 1 - t_lo, CH);
+  const int p_new = pos - t_lo;              // in range only in the last chunk
+  const bool own_new = (c == c_hi);
+  if (!a.spec_kv) {
+    load_chunk(p_begin, p_end);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
 
-  // B: rotary embedding in place.
-  const int npairs = nh * half;
-  for (int i = tid; i < npairs; i += kWg) {
-    const int hh = i / half, d = i - hh * half;
-    float* base = hh < G ? q_s + hh * hd : k_new;
-    const int ia = a.interleaved ? 2 * d : d;
-    const int ib = a.interleaved ? 2 * d + 1 : d + half;
-    const float e = __fdiv_rn(-2.0f * (float)d, (float)hd);
-    const float ang = __fmul_rn((float)pos, powf((float)a.theta, e));
-    const float co = cosf(ang), si = sinf(ang);
-    const float x0 = base[ia], x1 = base[ib];
-    base[ia] = __fsub_rn(__fmul_rn(x0, co), __fmul_rn(x1, si));
-    base[ib] = __fadd_rn(__fmul_rn(x0, si), __fmul_rn(x1, co));
+  // B: per-head RMSNorm + rotary, one wave per head; the new k/v to the cache
+  {
+    const int nh = G + (own_new ? 1 : 0);
+    const size_t row = head_base + (size_t)pos * hd;
+    for (int hh = wave; hh < nh; hh += 4) {
+      const bool is_k = hh == G;
+      float* x = is_k ? k_new : q_s + hh * hd;
+      float r = 1.0f;
+      if (a.qn_w) {
+        float ss = 0.f;
+        for (int d = lane; d < hd; d += 64) ss += x[d] * x[d];
+        ss = wave_sum(ss);
+        r = 1.0f / sqrtf(ss / (float)hd + a.eps);
+      }
+      const float* w = is_k ? kn : qn;
+      for (int d = lane; d < half; d += 64) {
+        const int ia = a.interleaved ? 2 * d : d;
+        const int ib = a.interleaved ? 2 * d + 1 : d + half;
+        float x0 = x[ia], x1 = x[ib];
+        if (a.qn_w) {
+          x0 = __fmul_rn(__fmul_rn(x0, r), w[ia]);
+          x1 = __fmul_rn(__fmul_rn(x1, r), w[ib]);
+        }
+        const float ang = __fmul_rn((float)pos, inv[d]);
+        const float co = cosf(ang), si = sinf(ang);
+        float y0 = __fsub_rn(__fmul_rn(x0, co), __fmul_rn(x1, si));
+        float y1 = __fadd_rn(__fmul_rn(x0, si), __fmul_rn(x1, co));
+        if (is_k) {
+          if constexpr (KV16) {
+            const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
+            ((__half*)a.kc)[row + ia] = h0;
+            ((__half*)a.kc)[row + ib] = h1;
+            y0 = __half2float(h0);
+            y1 = __half2float(h1);
+          } else {
+            ((float*)a.kc)[row + ia] = y0;
+            ((float*)a.kc)[row + ib] = y1;
+          }
+        }
+        x[ia] = y0;
+        x[ib] = y1;
+      }
+      if (is_k) {
+        for (int d = lane; d < hd; d += 64) {
+          if constexpr (KV16) {
+            const __half vh = __float2half_rn(v_new[d]);
+            ((__half*)a.vc)[row + d] = vh;
+            ((__half*)tile)[p_new * hd + d] = vh;
+          } else {
+            ((float*)a.vc)[row + d] = v_new[d];
+            tile[p_new * hd + d] = v_new[d];
+          }
+        }
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (own_new) {
-    const size_t row = ((size_t)kv * a.ctx + pos) * hd;
-    for (int d = tid; d < hd; d += kWg) {
-      if (a.kv_f16) {
-        const __half kh = __float2half_rn(k_new[d]), vh = __float2half_rn(v_new[d]);
-        ((__half*)a.kc)[row + d] = kh;
-        ((__half*)a.vc)[row + d] = vh;
-        k_new[d] = __half2float(kh);
-        v_new[d] = __half2float(vh);
+
+  // C: scores, wave-local softmax statistics, weighted V
+  {
+    const bool valid = my_p < CH && my_p >= p_begin && my_p < p_end;
+    float s[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) s[gg] = 0.f;
+    if (valid) {
+      const float* qbase = q_s + my_j * dpt;
+      if (my_p == p_new) {
+        const float* kk = k_new + my_j * dpt;
+        for (int d = 0; d < dpt; ++d)
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg) s[gg] += qbase[gg * hd + d] * kk[d];
       } else {
-        ((float*)a.kc)[row + d] = k_new[d];
-        ((float*)a.vc)[row + d] = v_new[d];
+        constexpr int per = 16 / kElem;  // elements per vector
+#pragma unroll
+        for (int v = 0; v < kVec; ++v) {
+          if (v < nvec) {
+            float kf[8];
+            if constexpr (KV16) {
+              const uint32_t w4[4] = {kreg[v].x, kreg[v].y, kreg[v].z, kreg[v].w};
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                kf[2 * i] = h2f(w4[i]);
+                kf[2 * i + 1] = h2f(w4[i] >> 16);
+              }
+            } else {
+              kf[0] = __uint_as_float(kreg[v].x);
+              kf[1] = __uint_as_float(kreg[v].y);
+              kf[2] = __uint_as_float(kreg[v].z);
+              kf[3] = __uint_as_float(kreg[v].w);
+            }
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+              const float4* qq = (const float4*)(qbase + gg * hd + v * per);
+              const float4 q0 = qq[0];
+              float s4 = (q0.x * kf[0] + q0.y * kf[1]) + (q0.z * kf[2] + q0.w * kf[3]);
+              if constexpr (per == 8) {
+                const float4 q1 = qq[1];
+                s4 += (q1.x * kf[4] + q1.y * kf[5]) + (q1.z * kf[6] + q1.w * kf[7]);
+              }
+              s[gg] += s4;
+            }
+          }
+        }
       }
     }
-  }
-  __syncthreads();
-
-  // C: scores of the chunk's positions.
-  const int t_begin = max(c * CH, start);
-  const int t_end = min(c * CH + CH, pos + 1);
-  const int n = t_end - t_begin;
-  const int slices = hd >> 3;
-  const int ppp = kWg / slices;
-  const int sl = tid % slices, pi = tid / slices;
-  for (int p0 = 0; p0 < n; p0 += ppp) {
-    const int p = p0 + pi;
-    float dots[G];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) dots[gg] = 0.f;
-    if (p < n) {
-      const int t = t_begin + p;
-      float kf[8];
-      if (t == pos) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf[j] = k_new[sl * 8 + j];
-      } else {
-        load8(a.kc, a.kv_f16, ((size_t)kv * a.ctx + t) * hd + sl * 8, kf);
-      }
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        const float* qq = q_s + gg * hd + sl * 8;
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s += qq[j] * kf[j];
-        dots[gg] = s;
-      }
-    }
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg)
-      for (int off = slices >> 1; off > 0; off >>= 1) dots[gg] += __shfl_xor(dots[gg], off, 64);
-    if (sl == 0 && p < n) {
-      for (int gg = 0; gg < G; ++gg) sc_s[gg * CH + p] = dots[gg] * a.scale;
-    }
-  }
-  __syncthreads();
-
-  // D: chunk-local softmax statistics; sc_s becomes exp(s - m).
-  for (int gg = wave; gg < G; gg += 4) {
-    float m = -INFINITY;
-    for (int p = lane; p < n; p += 64) m = fmaxf(m, sc_s[gg * CH + p]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int p = lane; p < n; p += 64) {
-      const float e = expf(sc_s[gg * CH + p] - m);
-      sc_s[gg * CH + p] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      ml_s[2 * gg] = m;
-      ml_s[2 * gg + 1] = l;
-    }
-  }
-  __syncthreads();
-
-  // E: probability-weighted V sum.
-  const int pgroups = ppp;
-  float acc[G][8];
-#pragma unroll
-  for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[gg][j] = 0.f;
-  for (int p = pi; p < n; p += pgroups) {
-    const int t = t_begin + p;
-    float vf[8];
-    if (t == pos) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vf[j] = v_new[sl * 8 + j];
-    } else {
-      load8(a.vc, a.kv_f16, ((size_t)kv * a.ctx + t) * hd + sl * 8, vf);
-    }
+    float e[G], m[G], l[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) {
-      const float w = sc_s[gg * CH + p];
+      s[gg] = group_sum_n(s[gg], tpp);
+      const float sv = valid ? s[gg] * a.scale : -INFINITY;
+      m[gg] = wave_max(sv);
+      e[gg] = valid ? expf(sv - m[gg]) : 0.0f;
+      l[gg] = wave_sum(my_j == 0 ? e[gg] : 0.0f);
+    }
+    // V: lane -> dims [d0, d0 + dpl); positions of this wave in order
+    const int dpl = hd >= 64 ? hd / 64 : 1;
+    const int d0 = (lane * dpl) % hd;
+    const int w0 = wave * P;
+    const int pa = max(p_begin, w0), pb = min(p_end, w0 + P);
+    float o[G][4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[gg][j] += w * vf[j];
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[gg][k] = 0.f;
+    if (dpl == 1)
+      v_walk<G, KV16, 1>(tile, hd, d0, pa, pb, w0, tpp, e, o);
+    else if (dpl == 2)
+      v_walk<G, KV16, 2>(tile, hd, d0, pa, pb, w0, tpp, e, o);
+    else
+      v_walk<G, KV16, 4>(tile, hd, d0, pa, pb, w0, tpp, e, o);
+    if (lane * dpl < hd) {
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (k < dpl) wpart[(wave * G + gg) * hd + d0 + k] = o[gg][k];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        wml[(wave * kMaxG + gg) * 2] = m[gg];
+        wml[(wave * kMaxG + gg) * 2 + 1] = l[gg];
+      }
     }
   }
-#pragma unroll
-  for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) red[((size_t)pi * G + gg) * hd + sl * 8 + j] = acc[gg][j];
   __syncthreads();
 
-  // F: publish the chunk partial (m, l, acc[hd]) per head with write-through
-  // stores, then count arrivals; the last chunk to arrive merges all chunks.
-  float* part = a.part + ((size_t)(kv * a.nchunk + c) * G) * (hd + 2);
+  // D: chunk partial = the four wave partials rescaled to the chunk maximum
+  const int rowf = (G * (hd + 2) + 3) & ~3;  // floats per chunk partial, 16-byte multiple
+  float* part = a.part + (size_t)(kv * a.nchunk + c) * rowf;
   for (int i = tid; i < G * hd; i += kWg) {
-    float s = 0.f;
-    for (int q = 0; q < pgroups; ++q) s += red[(size_t)q * G * hd + i];
     const int gg = i / hd, d = i - gg * hd;
-    st_relaxed(part + gg * (hd + 2) + 2 + d, s);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * kMaxG + gg) * 2]);
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = wml[(w * kMaxG + gg) * 2];
+      if (mw != -INFINITY) acc += wpart[(w * G + gg) * hd + d] * expf(mw - M);
+    }
+    part[gg * (hd + 2) + 2 + d] = acc;
   }
   if (tid < G) {
-    st_relaxed(part + tid * (hd + 2), ml_s[2 * tid]);
-    st_relaxed(part + tid * (hd + 2) + 1, ml_s[2 * tid + 1]);
+    float M = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * kMaxG + tid) * 2]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = wml[(w * kMaxG + tid) * 2];
+      if (mw != -INFINITY) L += wml[(w * kMaxG + tid) * 2 + 1] * expf(mw - M);
+    }
+    *(float2*)(part + tid * (hd + 2)) = make_float2(M, L);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -464,21 +766,72 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
-  for (int i = tid; i < G * hd; i += kWg) {
-    const int gg = i / hd, d = i - gg * hd;
+
+  // merge (last chunk): chunk weights w[g][c] = exp(m_c - M_g) once, then the
+  // acc rows, staged into LDS in batches, weighted and summed
+  const int nact = c_hi - c_lo + 1;
+  const float* rows0 = a.part + (size_t)(kv * a.nchunk + c_lo) * rowf;
+  float* stage = tile;
+  const int per_batch = max(1, a.merge_floats / rowf);
+  lds_dma(rows0, stage, min(per_batch, nact) * rowf);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int gg = wave; gg < G; gg += 4) {
     float M = -INFINITY;
-    for (int cc = c_lo; cc <= c_hi; ++cc) {
-      const float* pp = a.part + ((size_t)(kv * a.nchunk + cc) * G + gg) * (hd + 2);
-      M = fmaxf(M, ld_relaxed(pp));
+    for (int cc = lane; cc < nact; cc += 64) {
+      const float mv = cc < per_batch ? stage[cc * rowf + gg * (hd + 2)] : rows0[(size_t)cc * rowf + gg * (hd + 2)];
+      M = fmaxf(M, mv);
     }
-    float L = 0.f, o = 0.f;
-    for (int cc = c_lo; cc <= c_hi; ++cc) {
-      const float* pp = a.part + ((size_t)(kv * a.nchunk + cc) * G + gg) * (hd + 2);
-      const float f = expf(ld_relaxed(pp) - M);
-      L += ld_relaxed(pp + 1) * f;
-      o += ld_relaxed(pp + 2 + d) * f;
+    M = wave_max(M);
+    float L = 0.f;
+    for (int cc = lane; cc < nact; cc += 64) {
+      const float* pp = cc < per_batch ? stage + cc * rowf + gg * (hd + 2) : rows0 + (size_t)cc * rowf + gg * (hd + 2);
+      const float f = expf(pp[0] - M);
+      wts[gg * ncp + cc] = f;
+      L += pp[1] * f;
     }
-    a.out[(kv * G + gg) * hd + d] = o / L;
+    L = wave_sum(L);
+    if (lane == 0) wml[2 * gg] = 1.0f / L;
+  }
+  __syncthreads();
+  float o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = 0.f;
+  for (int b0 = 0; b0 < nact; b0 += per_batch) {
+    const int nb = min(per_batch, nact - b0);
+    if (b0 > 0) {
+      __syncthreads();  // previous batch consumed
+      lds_dma(rows0 + (size_t)b0 * rowf, stage, nb * rowf);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = tid + q * kWg;
+      if (i < G * hd) {
+        const int gg = i / hd, d = i - gg * hd;
+        const float* src = stage + gg * (hd + 2) + 2 + d;
+        const float* wv = wts + gg * ncp + b0;
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        int cc = 0;
+        for (; cc + 4 <= nb; cc += 4) {
+          acc0 += src[cc * rowf] * wv[cc];
+          acc1 += src[(cc + 1) * rowf] * wv[cc + 1];
+          acc2 += src[(cc + 2) * rowf] * wv[cc + 2];
+          acc3 += src[(cc + 3) * rowf] * wv[cc + 3];
+        }
+        for (; cc < nb; ++cc) acc0 += src[cc * rowf] * wv[cc];
+        o[q] += (acc0 + acc1) + (acc2 + acc3);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = tid + q * kWg;
+    if (i < G * hd) {
+      const int gg = i / hd, d = i - gg * hd;
+      a.out[(kv * G + gg) * hd + d] = o[q] * wml[2 * gg];
+    }
   }
   if (tid == 0) __hip_atomic_store(&a.cnt[kv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -696,18 +1049,32 @@ int pick_lpr(int units) {
 
 size_t mv_shared_bytes(int k, int max_tile_rows) {
   const int res = max_tile_rows * 2 > 768 ? max_tile_rows * 2 : 768;  // GLU rows or logits scratch
-  return sizeof(float) * ((size_t)k + (size_t)k / 16 + 8 + (size_t)res);
+  return sizeof(float) * (4 * (size_t)k + (size_t)k / 16 + 8 + (size_t)res);
 }
 
-size_t attn_shared_bytes(int group, int hd, int chunk) {
-  const int pgroups = kWg / (hd / 8);
-  return sizeof(float) * ((size_t)group * hd + 2 * (size_t)hd + (size_t)group * chunk + 2 * kMaxG +
-                          (size_t)pgroups * group * hd);
+int attn_merge_floats(int group, int hd, int nchunk) {
+  // stage up to 32 KiB of chunk partials per batch; the V tile area is reused
+  const int rowf = (group * (hd + 2) + 3) & ~3;
+  return std::min(nchunk * rowf, std::max(8192, rowf));
 }
 
-namespace {
+size_t attn_shared_bytes(int group, int hd, int chunk, int nchunk, int kv_elem) {
+  const size_t tile = std::max((size_t)chunk * hd * kv_elem / 4, (size_t)attn_merge_floats(group, hd, nchunk));
+  const size_t ncp = ((size_t)nchunk + 3) & ~(size_t)3;
+  return sizeof(float) * ((size_t)(5 * group + 5) * hd + 8 * kMaxG + (size_t)group * ncp + tile);
+}
+
+int attn_max_chunk(int hd) { return kWg / attn_tpp(hd); }
+
+int attn_threads_per_position(int hd, int chunk, int kv_elem) {
+  // enough threads per position to occupy the workgroup, each loading at
+  // least one 16-byte K vector
+  int t = attn_tpp(hd);
+  while (t * chunk < kWg && t * 2 <= hd * kv_elem / 16) t *= 2;
+  return t;
+}
+
 size_t g_lds_limit = 64 * 1024;
-}
 
 size_t lds_limit() { return g_lds_limit; }
 
@@ -720,9 +1087,14 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[9] = {(const void*)k_matvec,       (const void*)k_attention<1>, (const void*)k_attention<2>,
-                        (const void*)k_attention<3>, (const void*)k_attention<4>, (const void*)k_attention<5>,
-                        (const void*)k_attention<6>, (const void*)k_attention<7>, (const void*)k_attention<8>};
+  const void* fns[21] = {
+      (const void*)k_mv_store,               (const void*)k_mv_add,                 (const void*)k_mv_swiglu,
+      (const void*)k_mv_geglu,               (const void*)k_mv_logits,              (const void*)k_attention<1, true>,
+      (const void*)k_attention<2, true>,     (const void*)k_attention<3, true>,     (const void*)k_attention<4, true>,
+      (const void*)k_attention<5, true>,     (const void*)k_attention<6, true>,     (const void*)k_attention<7, true>,
+      (const void*)k_attention<8, true>,     (const void*)k_attention<1, false>,    (const void*)k_attention<2, false>,
+      (const void*)k_attention<3, false>,    (const void*)k_attention<4, false>,    (const void*)k_attention<5, false>,
+      (const void*)k_attention<6, false>,    (const void*)k_attention<7, false>,    (const void*)k_attention<8, false>};
   bool raised = want > 64 * 1024;
   for (const void* f : fns) {
     if (!raised) break;
@@ -735,24 +1107,39 @@ hipError_t init_kernel_attributes() {
 }
 
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s) {
-  hipLaunchKernelGGL(k_matvec, dim3(grid), dim3(kWg), shmem, s, a);
+  switch (a.epi) {
+    case EPI_STORE: hipLaunchKernelGGL(k_mv_store, dim3(grid), dim3(kWg), shmem, s, a); break;
+    case EPI_ADD: hipLaunchKernelGGL(k_mv_add, dim3(grid), dim3(kWg), shmem, s, a); break;
+    case EPI_GLU_SILU: hipLaunchKernelGGL(k_mv_swiglu, dim3(grid), dim3(kWg), shmem, s, a); break;
+    case EPI_GLU_GELU: hipLaunchKernelGGL(k_mv_geglu, dim3(grid), dim3(kWg), shmem, s, a); break;
+    case EPI_LOGITS: hipLaunchKernelGGL(k_mv_logits, dim3(grid), dim3(kWg), shmem, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s) {
   const int group = a.heads / a.kv_heads;
   const dim3 grid(a.kv_heads, a.nchunk);
+#define CHONK_ATTN_CASE(GG)                                                                  \
+  case GG:                                                                                   \
+    if (a.kv_f16)                                                                            \
+      hipLaunchKernelGGL((k_attention<GG, true>), grid, dim3(kWg), shmem, s, a);             \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_attention<GG, false>), grid, dim3(kWg), shmem, s, a);            \
+    break;
   switch (group) {
-    case 1: hipLaunchKernelGGL(k_attention<1>, grid, dim3(kWg), shmem, s, a); break;
-    case 2: hipLaunchKernelGGL(k_attention<2>, grid, dim3(kWg), shmem, s, a); break;
-    case 3: hipLaunchKernelGGL(k_attention<3>, grid, dim3(kWg), shmem, s, a); break;
-    case 4: hipLaunchKernelGGL(k_attention<4>, grid, dim3(kWg), shmem, s, a); break;
-    case 5: hipLaunchKernelGGL(k_attention<5>, grid, dim3(kWg), shmem, s, a); break;
-    case 6: hipLaunchKernelGGL(k_attention<6>, grid, dim3(kWg), shmem, s, a); break;
-    case 7: hipLaunchKernelGGL(k_attention<7>, grid, dim3(kWg), shmem, s, a); break;
-    case 8: hipLaunchKernelGGL(k_attention<8>, grid, dim3(kWg), shmem, s, a); break;
+    CHONK_ATTN_CASE(1)
+    CHONK_ATTN_CASE(2)
+    CHONK_ATTN_CASE(3)
+    CHONK_ATTN_CASE(4)
+    CHONK_ATTN_CASE(5)
+    CHONK_ATTN_CASE(6)
+    CHONK_ATTN_CASE(7)
+    CHONK_ATTN_CASE(8)
     default: return hipErrorInvalidValue;
   }
+#undef CHONK_ATTN_CASE
   return hipGetLastError();
 }
 
