@@ -50,6 +50,26 @@ def build_model(workload: str, cache_dir: Path) -> str:
     return str(path)
 
 
+def profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload` from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summaries kept under profiles/ (lines 'traffic: <kernel> <workload> <bytes>')."""
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic: "):
+                rest = line[len("traffic: "):].rsplit(" ", 2)
+                if len(rest) == 3 and rest[0] == kernel and rest[1] == workload:
+                    return int(rest[2])
+    return None
+
+
+def kernel_symbol(cls: str, info: dict) -> str:
+    """Kernel function behind a step's kernel class (as rocprofv3 names it)."""
+    g = info["heads"] // info["kv_heads"]
+    kv16 = "true" if info.get("kv_dtype", 0) == 0 else "false"  # CHONK_KV_F16 == 0
+    return {"attn": f"k_attention<{g}, {kv16}>", "gateup": "k_mv_swiglu", "qkv": "k_mv_store",
+            "oproj": "k_mv_add", "down": "k_mv_add", "lmhead": "k_mv_logits"}.get(cls, cls)
+
+
 def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:
     """Oracle decode steps at the benchmark's context, fake K/V, greedy."""
     from oracle.oracle import OracleModel
@@ -86,6 +106,9 @@ def main() -> int:
                     help="fill the K/V cache with synthetic values instead of prefilling the prompt "
                          "(profiling runs: the trace then holds decode steps only)")
     ap.add_argument("--model-cache", default=os.environ.get("CHONK_MODEL_CACHE", "/tmp/chonk_models"))
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first run 4 device-to-device copies of MIB MiB (a known-size kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -94,6 +117,18 @@ def main() -> int:
         return 2
 
     from chonklm_amd import WORKLOADS, generate_llama_wgsl, load_llama_wgsl_model
+
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calibration: 4 copies of {n} bytes", file=sys.stderr)
+        del src, dst
 
     w = WORKLOADS[args.workload]
     t_build = time.perf_counter()
@@ -180,7 +215,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(kernel_symbol(dom_name, info), w.name),
+            "kernel_symbol": kernel_symbol(dom_name, info),
             "bytes_per_launch": int(dom_bytes),
             "us_per_launch": round(dom_us, 3),
         },

@@ -468,19 +468,53 @@ __device__ __forceinline__ void load_v(const void* tile, int idx, int dpl, float
   }
 }
 
+// s[g] += q_g[my dims] . k[my dims] for this thread's NV 16-byte K vectors.
+template <int G, bool KV16, int NV>
+__device__ __forceinline__ void score_dot(const uint4* kreg, const float* qbase, int hd, float (&s)[G]) {
+  constexpr int per = KV16 ? 8 : 4;  // elements per vector
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float kf[8];
+    if constexpr (KV16) {
+      const uint32_t w4[4] = {kreg[v].x, kreg[v].y, kreg[v].z, kreg[v].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kf[2 * i] = h2f(w4[i]);
+        kf[2 * i + 1] = h2f(w4[i] >> 16);
+      }
+    } else {
+      kf[0] = __uint_as_float(kreg[v].x);
+      kf[1] = __uint_as_float(kreg[v].y);
+      kf[2] = __uint_as_float(kreg[v].z);
+      kf[3] = __uint_as_float(kreg[v].w);
+    }
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+      const float4* qq = (const float4*)(qbase + gg * hd + v * per);
+      const float4 q0 = qq[0];
+      float s4 = (q0.x * kf[0] + q0.y * kf[1]) + (q0.z * kf[2] + q0.w * kf[3]);
+      if constexpr (per == 8) {
+        const float4 q1 = qq[1];
+        s4 += (q1.x * kf[4] + q1.y * kf[5]) + (q1.z * kf[6] + q1.w * kf[7]);
+      }
+      s[gg] += s4;
+    }
+  }
+}
+
 // o[g][0..DPL) += sum over positions p in [pa, pb) of w_g(p) * V[p][d0..d0+DPL),
-// where w_g(p) sits in lane (p - w0) * tpp of e[g]; four positions per pass
+// where w_g(p) sits in lane (p - w0) * tpp of e[g]; eight positions per pass
 // so that the LDS reads of a pass overlap.
 template <int G, bool KV16, int DPL>
 __device__ __forceinline__ void v_walk(const void* tile, int hd, int d0, int pa, int pb, int w0, int tpp,
                                        const float (&e)[G], float (&o)[G][4]) {
   int p = pa;
-  for (; p + 4 <= pb; p += 4) {
-    float vv[4][4];
+  for (; p + 8 <= pb; p += 8) {
+    float vv[8][4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load_v<KV16>(tile, (p + u) * hd + d0, DPL, vv[u]);
+    for (int u = 0; u < 8; ++u) load_v<KV16>(tile, (p + u) * hd + d0, DPL, vv[u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       const int sel = (p + u - w0) * tpp;
 #pragma unroll
       for (int gg = 0; gg < G; ++gg) {
@@ -543,6 +577,8 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
     lds_dma(a.kn_w, kn, hd);
   }
   uint4 kreg[kVec];
+#pragma unroll
+  for (int v = 0; v < kVec; ++v) kreg[v] = make_uint4(0u, 0u, 0u, 0u);
   const size_t head_base = (size_t)kv * a.ctx * hd;
   auto load_chunk = [&](int p_begin, int p_end) {
     // K: this thread's dims of its position, into registers
@@ -645,48 +681,39 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   // C: scores, wave-local softmax statistics, weighted V
   {
     const bool valid = my_p < CH && my_p >= p_begin && my_p < p_end;
+    if (own_new && my_p == p_new) {
+      // the new position's k (already rounded to the cache type) into the K registers
+      const float* kk = k_new + my_j * dpt;
+#pragma unroll
+      for (int v = 0; v < kVec; ++v) {
+        if (v < nvec) {
+          if constexpr (KV16) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              w4[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[v * 8 + 2 * i])) |
+                      ((uint32_t)__half_as_ushort(__float2half_rn(kk[v * 8 + 2 * i + 1])) << 16);
+            kreg[v] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          } else {
+            kreg[v] = make_uint4(__float_as_uint(kk[v * 4]), __float_as_uint(kk[v * 4 + 1]),
+                                 __float_as_uint(kk[v * 4 + 2]), __float_as_uint(kk[v * 4 + 3]));
+          }
+        }
+      }
+    }
     float s[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) s[gg] = 0.f;
-    if (valid) {
+    {
       const float* qbase = q_s + my_j * dpt;
-      if (my_p == p_new) {
-        const float* kk = k_new + my_j * dpt;
-        for (int d = 0; d < dpt; ++d)
-#pragma unroll
-          for (int gg = 0; gg < G; ++gg) s[gg] += qbase[gg * hd + d] * kk[d];
-      } else {
-        constexpr int per = 16 / kElem;  // elements per vector
-#pragma unroll
-        for (int v = 0; v < kVec; ++v) {
-          if (v < nvec) {
-            float kf[8];
-            if constexpr (KV16) {
-              const uint32_t w4[4] = {kreg[v].x, kreg[v].y, kreg[v].z, kreg[v].w};
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                kf[2 * i] = h2f(w4[i]);
-                kf[2 * i + 1] = h2f(w4[i] >> 16);
-              }
-            } else {
-              kf[0] = __uint_as_float(kreg[v].x);
-              kf[1] = __uint_as_float(kreg[v].y);
-              kf[2] = __uint_as_float(kreg[v].z);
-              kf[3] = __uint_as_float(kreg[v].w);
-            }
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) {
-              const float4* qq = (const float4*)(qbase + gg * hd + v * per);
-              const float4 q0 = qq[0];
-              float s4 = (q0.x * kf[0] + q0.y * kf[1]) + (q0.z * kf[2] + q0.w * kf[3]);
-              if constexpr (per == 8) {
-                const float4 q1 = qq[1];
-                s4 += (q1.x * kf[4] + q1.y * kf[5]) + (q1.z * kf[6] + q1.w * kf[7]);
-              }
-              s[gg] += s4;
-            }
-          }
-        }
+      switch (nvec) {
+        case 1: score_dot<G, KV16, 1>(kreg, qbase, hd, s); break;
+        case 2: score_dot<G, KV16, 2>(kreg, qbase, hd, s); break;
+        case 4: score_dot<G, KV16, 4>(kreg, qbase, hd, s); break;
+        case 8: score_dot<G, KV16, 8>(kreg, qbase, hd, s); break;
+        default:
+          if constexpr (!KV16) score_dot<G, KV16, 16>(kreg, qbase, hd, s);
+          break;
       }
     }
     float e[G], m[G], l[G];
