@@ -1,8 +1,9 @@
 """Build recipe for libchonk.so (hipcc, gfx950) and the oracle's CPU library.
 
 Run ``python -m chonklm_amd.build`` or call :func:`build_all`. Outputs stay
-in-tree (``chonklm_amd/_lib/libchonk.so``, ``oracle/_build/liborc.so``) so
-that they travel with the repository snapshot to the GPU host.
+in-tree (``chonklm_amd/_lib/libchonk.so``, the Node addon
+``chonklm_amd/_lib/chonk_napi.node``, ``oracle/_build/liborc.so``) so that
+they travel with the repository snapshot to the GPU host.
 """
 from __future__ import annotations
 
@@ -62,6 +63,30 @@ def build_library(jobs: int = 8) -> Path:
     return LIB_PATH
 
 
+NAPI_SOURCE = PKG / "csrc/napi/chonk_napi.cpp"
+NAPI_PATH = LIB_DIR / "chonk_napi.node"
+
+
+def _node_include() -> Path | None:
+    for cand in (Path("/usr/include/node"), Path("/usr/local/include/node")):
+        if (cand / "node_api.h").exists():
+            return cand
+    return None
+
+
+def build_napi() -> Path | None:
+    """Builds the Node N-API addon over libchonk.so (skipped when Node's headers are absent)."""
+    inc = _node_include()
+    if inc is None:
+        return None
+    tmp = NAPI_PATH.with_suffix(".node.tmp")
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-DNODE_GYP_MODULE_NAME=chonk_napi",
+          f"-I{inc}", f"-I{ROOT / 'include'}", str(NAPI_SOURCE), "-o", str(tmp), f"-L{LIB_DIR}", "-lchonk",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, NAPI_PATH)
+    return NAPI_PATH
+
+
 def build_oracle() -> Path | None:
     """Builds the oracle's CPU restatement (test infrastructure)."""
     oracle = ROOT / "oracle"
@@ -73,6 +98,7 @@ def build_oracle() -> Path | None:
 
 def build_all(jobs: int = 8) -> None:
     build_library(jobs)
+    build_napi()
     build_oracle()
 
 

@@ -1067,7 +1067,8 @@ chonk_sampling effective_sampling(const chonk_engine* e, const chonk_sampling* s
 void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new, const chonk_sampling* s_in,
               std::vector<int32_t>* out, chonk_gen_stats* stats) {
   const ModelCfg& c = e->cfg;
-  const int64_t max = std::min<int64_t>(max_new > 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
+  // maxNewTokens ?? 128 (:255): a negative value stands for "not given"
+  const int64_t max = std::min<int64_t>(max_new >= 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
   const chonk_sampling s = effective_sampling(e, s_in);
   for (size_t i = 0; i < n_prompt; ++i) check_token(e, prompt[i]);
   const double t0 = now_ms();
@@ -1175,7 +1176,8 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
 void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new,
                       const chonk_sampling* s_in, chonk_token_callback cb, void* user, std::vector<int32_t>* out,
                       chonk_gen_stats* stats) {
-  const int64_t max = std::min<int64_t>(max_new > 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
+  // maxNewTokens ?? 128 (:255): a negative value stands for "not given"
+  const int64_t max = std::min<int64_t>(max_new >= 0 ? max_new : 128, (int64_t)e->def.max_context - (int64_t)n_prompt);
   const chonk_sampling s = effective_sampling(e, s_in);
   for (size_t i = 0; i < n_prompt; ++i) check_token(e, prompt[i]);
   auto is_eos = [&](int32_t id) { return std::find(e->eos.begin(), e->eos.end(), id) != e->eos.end(); };

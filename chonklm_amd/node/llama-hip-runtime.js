@@ -1,0 +1,169 @@
+'use strict';
+// Node host of the MI355X decode engine, with the module API of the
+// reference's src/lib/llama-wgsl-runtime.ts (loadLlamaWgslModel :184-240,
+// generateLlamaWgsl :242-314, disposeLlamaWgsl :316-318,
+// resetLlamaWgslConversation :320-324, LlamaWgslEngine.runToken / reset /
+// position / dispose :1011-1215). ES2019 + CommonJS so that it runs on
+// Node 12; device work goes through the N-API addon over libchonk.so
+// (chonklm_amd/_lib/chonk_napi.node).
+
+const path = require('path');
+
+let addon = null;
+function native() {
+  if (!addon) {
+    // no fallback: without the HIP addon there is no decode path
+    addon = require(path.join(__dirname, '..', '_lib', 'chonk_napi.node'));
+  }
+  return addon;
+}
+
+// Tokenizer stand-in used when the caller gives none: token ids cross the
+// boundary, text is the caller's concern (the reference's Tokenizer.load).
+const idsOnlyTokenizer = {
+  encode() {
+    throw new Error('no tokenizer was given to loadLlamaWgslModel');
+  },
+  decode() {
+    return '';
+  },
+};
+
+function pick(v, dflt) {
+  return v === undefined || v === null ? dflt : v;
+}
+
+function modelFilePath(model, p) {
+  // modelFileUrl (:427-429) for local files: absolute paths are used as they are
+  if (path.isAbsolute(p)) return p;
+  return model.base ? path.join(model.base, p) : p;
+}
+
+function samplingOf(opts, def) {
+  const o = opts || {};
+  return {
+    temperature: pick(o.temperature, 0),
+    topP: pick(o.topP, 1),
+    topK: pick(o.topK, 0),
+    repetitionPenalty: pick(o.repetitionPenalty, pick(def && def.defaultRepetitionPenalty, 1)),
+    seed: pick(o.seed, 0),
+  };
+}
+
+class LlamaWgslEngine {
+  constructor(handle, def) {
+    this.handle = handle;
+    this.def = def;
+    this.info = native().info(handle);
+  }
+
+  // runToken (:1025-1150): processes tokenId at the current position; with
+  // needLogits selects the next token (greedy or the candidate sampler).
+  runToken(tokenId, needLogits, opts) {
+    const o = opts || {};
+    const s = samplingOf(o, null);
+    return native().runToken(this.handle, tokenId, !!needLogits, s, o.penalizedTokenIds || [], o.seenIds || []);
+  }
+
+  reset() {
+    native().reset(this.handle);
+  }
+
+  get position() {
+    return native().position(this.handle);
+  }
+
+  // Logits of the last step that computed them (the reference keeps them on the GPU, :893).
+  readLogits() {
+    return native().readLogits(this.handle);
+  }
+
+  dispose() {
+    native().dispose(this.handle);
+  }
+}
+
+async function loadLlamaWgslModel(model, onProgress, onStep, options) {
+  if (model.runtime !== 'llama-webgpu') {
+    throw new Error(`loadLlamaWgslModel: ${model.id} is not configured for the Llama WGSL runtime`);
+  }
+  if (!model.gguf) throw new Error(`Llama WGSL ${model.id} is missing gguf path`);
+  const file = modelFilePath(model, model.gguf);
+  if (onStep) onStep({ step: 'runtime', detail: 'opening the HIP device' });
+  if (onProgress) onProgress({ loaded: 0, total: 0, file });
+  const handle = await native().createEngine(
+    {
+      id: model.id,
+      vocab: model.vocab,
+      layers: model.layers,
+      maxContext: model.maxContext,
+      eosIds: model.eosIds || [],
+      defaultRepetitionPenalty: pick(model.defaultRepetitionPenalty, 0),
+      kvDtype: pick(model.kvDtype, 'float16'),
+      device: pick(options && options.device, 0),
+    },
+    file,
+  );
+  const engine = new LlamaWgslEngine(handle, model);
+  if (onStep) onStep({ step: 'ready', detail: 'Llama HIP runtime ready' });
+  return {
+    runtime: 'llama-webgpu',
+    def: model,
+    tokenizer: (options && options.tokenizer) || idsOnlyTokenizer,
+    engine,
+    ep: 'hip',
+    cachedTokenIds: [],
+    cachedNextId: null,
+  };
+}
+
+// generateLlamaWgsl (:242-314). Without onToken / shouldStop the whole loop
+// runs on the device; with them it is stepped one token at a time and the
+// callbacks run on this thread between steps, as in the reference.
+async function generateLlamaWgsl(loaded, promptIds, opts) {
+  const o = opts || {};
+  const s = samplingOf(o, loaded.def);
+  const maxArg = o.maxNewTokens === undefined || o.maxNewTokens === null ? -1 : Math.max(0, Math.floor(o.maxNewTokens));
+  const generated = [];
+  let cumulative = '';
+  let callback;
+  if (o.onToken || o.shouldStop) {
+    callback = (event, token) => {
+      if (event === 0) return o.shouldStop ? !!o.shouldStop() : false;
+      generated.push(token);
+      const fullText = loaded.tokenizer.decode(generated);
+      const piece = fullText.slice(cumulative.length);
+      cumulative = fullText;
+      if (o.onToken) o.onToken({ id: token, text: piece, cumulative });
+      return false;
+    };
+  }
+  const res = await native().generate(loaded.engine.handle, promptIds, maxArg, s, callback);
+  const conv = native().conversation(loaded.engine.handle);
+  loaded.cachedTokenIds = conv.cachedTokenIds;
+  loaded.cachedNextId = conv.cachedNextId;
+  const text = callback ? cumulative : loaded.tokenizer.decode(res.ids);
+  return { text, ids: res.ids, tokensPerSec: res.tokensPerSec };
+}
+
+function disposeLlamaWgsl(loaded) {
+  loaded.engine.dispose();
+}
+
+function resetLlamaWgslConversation(loaded) {
+  native().resetConversation(loaded.engine.handle);
+  loaded.cachedTokenIds = [];
+  loaded.cachedNextId = null;
+}
+
+module.exports = {
+  LlamaWgslEngine,
+  loadLlamaWgslModel,
+  generateLlamaWgsl,
+  disposeLlamaWgsl,
+  resetLlamaWgslConversation,
+  // PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
+  loadPleiasWgslModel: loadLlamaWgslModel,
+  generatePleiasWgsl: generateLlamaWgsl,
+  disposePleiasWgsl: disposeLlamaWgsl,
+};

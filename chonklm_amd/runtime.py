@@ -184,7 +184,9 @@ def generate_llama_wgsl(loaded: LoadedLlamaWgslModel, prompt_ids: Sequence[int],
     eng = loaded.engine
     s = _sampling(temperature, top_p, top_k, repetition_penalty, seed)
     prompt, n_prompt = _i32_array(list(prompt_ids))
-    cap = max(1, (max_new_tokens if max_new_tokens and max_new_tokens > 0 else 128))
+    # maxNewTokens ?? 128 (:255); the ABI takes a negative value for "not given"
+    max_arg = -1 if max_new_tokens is None else max(0, int(max_new_tokens))
+    cap = 128 if max_arg < 0 else max(1, max_arg)
     out = (C.c_int32 * cap)()
     n_out = C.c_size_t()
     stats = _lib.GenStatsC()
@@ -193,7 +195,7 @@ def generate_llama_wgsl(loaded: LoadedLlamaWgslModel, prompt_ids: Sequence[int],
 
     if on_token is None and should_stop is None:
         check(L.chonk_engine_generate(eng._h, C.cast(prompt, C.POINTER(C.c_int32)), n_prompt,
-                                      int(max_new_tokens or 0), C.byref(s), out, cap, C.byref(n_out),
+                                      max_arg, C.byref(s), out, cap, C.byref(n_out),
                                       C.byref(stats)), eng._h)
         generated = list(out[: n_out.value])
     else:
@@ -210,7 +212,7 @@ def generate_llama_wgsl(loaded: LoadedLlamaWgslModel, prompt_ids: Sequence[int],
 
         cb = _lib.TOKEN_CALLBACK(_cb)
         check(L.chonk_engine_generate_stepped(eng._h, C.cast(prompt, C.POINTER(C.c_int32)), n_prompt,
-                                              int(max_new_tokens or 0), C.byref(s), C.cast(cb, C.c_void_p), None,
+                                              max_arg, C.byref(s), C.cast(cb, C.c_void_p), None,
                                               out, cap, C.byref(n_out), C.byref(stats)), eng._h)
         generated = list(out[: n_out.value])
     loaded.cached_token_ids, loaded.cached_next_id = eng.conversation()
@@ -233,7 +235,6 @@ def reset_llama_wgsl_conversation(loaded: LoadedLlamaWgslModel) -> None:
 load_pleias_wgsl_model = load_llama_wgsl_model
 generate_pleias_wgsl = generate_llama_wgsl
 dispose_pleias_wgsl = dispose_llama_wgsl
-reset_pleias_wgsl_conversation = reset_llama_wgsl_conversation
 
 
 # ---- model files ------------------------------------------------------------------

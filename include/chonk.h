@@ -121,9 +121,10 @@ int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, 
 
 /* generateLlamaWgsl: prefix reuse against the previous conversation, prompt
  * prefill, then up to max_new_tokens generated ids (stopping after an EOS
- * id), all on the device without a per-token host round trip. max_new_tokens
- * <= 0 means 128. The penalty list is prompt + generated, as in the
- * reference. out_ids receives min(n, out_cap) ids; *n_out the count. */
+ * id), all on the device without a per-token host round trip. A negative
+ * max_new_tokens means "not given" (128); 0 prefills only. The penalty list
+ * is prompt + generated, as in the reference. out_ids receives
+ * min(n, out_cap) ids; *n_out the count. */
 int chonk_engine_generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t max_new_tokens,
                           const chonk_sampling* s, int32_t* out_ids, size_t out_cap, size_t* n_out,
                           chonk_gen_stats* stats);

@@ -181,7 +181,7 @@ class OracleModel:
                  margins: Optional[list] = None) -> list[int]:
         """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314)."""
         prompt = list(prompt_ids)
-        mx = min(max_new_tokens if max_new_tokens and max_new_tokens > 0 else 128, self.max_context - len(prompt))
+        mx = min(128 if max_new_tokens is None else max_new_tokens, self.max_context - len(prompt))
         t = 0.0 if temperature is None else temperature
         tp = 1.0 if top_p is None else top_p
         tk = 0 if top_k is None else top_k
