@@ -66,7 +66,8 @@ def kernel_symbol(cls: str, info: dict) -> str:
     """Kernel function behind a step's kernel class (as rocprofv3 names it)."""
     g = info["heads"] // info["kv_heads"]
     kv16 = "true" if info.get("kv_dtype", 0) == 0 else "false"  # CHONK_KV_F16 == 0
-    return {"attn": f"k_attention<{g}, {kv16}>", "gateup": "k_mv_swiglu", "qkv": "k_mv_store",
+    return {"step": f"k_step<{g}, {kv16}>", "attn": f"k_attention<{g}, {kv16}>", "gateup": "k_mv_swiglu",
+            "qkv": "k_mv_store",
             "oproj": "k_mv_add", "down": "k_mv_add", "lmhead": "k_mv_logits"}.get(cls, cls)
 
 
@@ -172,18 +173,26 @@ def main() -> int:
         c["bytes"] += nbytes
     if not classes:
         classes["none"] = {"launches": 1, "us": float("nan"), "bytes": 0}
-    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["us"])
-    dom_us = dom["us"] / dom["launches"]
-    dom_bytes = dom["bytes"] / dom["launches"]
-    dom_gbs = dom_bytes / dom_us / 1e3
     gu = classes.get("gateup")
 
     # whole-step bytes: weights + K/V read at the mean timed position + K/V write
     kvdim = info["kv_heads"] * info["head_dim"]
     mean_pos = (pos0 + args.warmup + pos_end) / 2.0
-    kv_bytes = 2 * info["layers"] * kvdim * (mean_pos + 1) * 2
+    kv_elem = 2 if info.get("kv_dtype", 0) == 0 else 4
+    kv_bytes = 2 * info["layers"] * kvdim * (mean_pos + 1) * kv_elem
     step_bytes = info["weight_bytes_per_token"] + kv_bytes
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    if info.get("persistent_step"):
+        # one kernel per token: the dominant kernel is the persistent step itself
+        dom_name = "step"
+        dom_us = ms_per_step * 1000.0
+        dom_bytes = step_bytes
+    else:
+        dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["us"])
+        dom_us = dom["us"] / dom["launches"]
+        dom_bytes = dom["bytes"] / dom["launches"]
+    dom_gbs = dom_bytes / dom_us / 1e3
 
     result = {
         "metric": METRIC,
@@ -206,6 +215,7 @@ def main() -> int:
             "context_at_timed_start": pos0 + args.warmup,
             "context_at_end": pos_end,
             "kv_cache": "f16",
+            "persistent_step": bool(info.get("persistent_step")),
             "weights": "Q4_K_M GGUF (Q4_K / Q6_K), random N(0,0.02)",
         },
         "roofline": {
@@ -231,6 +241,7 @@ def main() -> int:
             "kernel": "gateup (Q4_K, fused RMSNorm + SwiGLU)",
             "achieved": round(gu["bytes"] / gu["us"] / 1e3, 1), "unit": "GB/s",
             "us_per_launch": round(gu["us"] / gu["launches"], 3)},
+        # the step's phases timed as standalone kernels (HIP events, 20 launches each)
         "kernels": {k: {"launches": v["launches"], "us_per_step": round(v["us"], 2),
                         "gb_s": round(v["bytes"] / v["us"] / 1e3, 1)} for k, v in classes.items()},
         "kernel_sum_us": round(sum(v["us"] for v in classes.values()), 2),

@@ -73,6 +73,7 @@ class EngineInfoC(C.Structure):
         ("weight_bytes_per_token", C.c_uint64),
         ("device_bytes", C.c_uint64),
         ("kernels_per_step", C.c_int32),
+        ("persistent_step", C.c_int32),
     ]
 
 
@@ -136,6 +137,7 @@ SIGNATURES = [
     ("chonk_engine_read_buffer", C.c_int, [P, C.c_int32, P, C.c_size_t]),
     ("chonk_engine_read_kv", C.c_int, [P, C.c_int32, C.c_int32, C.c_int32, F32P]),
     ("chonk_engine_bench_decode", C.c_int, [P, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
+    ("chonk_engine_profile_step", C.c_int, [P, C.POINTER(C.c_double), C.c_int32, I32P]),
     ("chonk_engine_bench_kernel", C.c_int,
      [P, C.c_int32, C.c_int32, C.POINTER(C.c_double), C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64)]),
     ("chonk_engine_fake_context", C.c_int, [P, C.c_int32, C.c_uint64]),

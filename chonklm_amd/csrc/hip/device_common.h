@@ -71,6 +71,32 @@ struct DevSampling {
 
 constexpr int kWg = 256;  // threads per workgroup for every kernel here
 
+// Global-memory view of a pointer. A load through a generic pointer is a FLAT
+// instruction, which also counts as an LDS access: every later wait for LDS
+// data then waits for the outstanding memory loads too. Pointers read from
+// device-memory tables are generic unless cast.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gbl(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gblw(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+// 16 / 8 / 4-byte global loads (HIP's uint4 / uint2 cannot be assigned from
+// an address-space-qualified object, so the load goes through clang vectors)
+__device__ __forceinline__ uint4 ldg4(const void* p) {
+  const u32x4_t v = *gbl((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg2(const void* p) {
+  const u32x2_t v = *gbl((const u32x2_t*)p);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldg1(const void* p) { return *gbl((const uint32_t*)p); }
+
 // Group candidate written by the lm_head epilogue (ARGMAX_STAGE1 output).
 struct Candidate {
   float value;

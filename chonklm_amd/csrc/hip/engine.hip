@@ -241,10 +241,14 @@ struct LayerDev {
 };
 
 struct Launch {
-  enum Kind { MV, ATTN, SEL } kind = MV;
+  enum Kind { MV, ATTN, SEL, STEP } kind = MV;
   MvArgs mv{};
   AttnArgs at{};
   SelArgs sel{};
+  StepArgs step{};
+  const StepArgs* d_step = nullptr;  // STEP: device copy of `step`
+  int step_group = 0;         // STEP: GQA group and K/V type of the instantiation
+  bool step_kv16 = true;
   int grid = 0;
   size_t shmem = 0;
   std::string name;
@@ -282,7 +286,19 @@ struct chonk_engine {
   uint32_t *pen_bits = nullptr, *seen_bits = nullptr;
   int groups = 0, chunk = 0, nchunk = 0;
   std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
+  // per-phase kernels of one step (qkv, attn, oproj, gateup, down per layer; lm_head, select)
+  std::vector<Launch> kernels_logits, kernels_plain;
+  // what a step replays: the per-phase kernels, or the single persistent step kernel
   std::vector<Launch> step_logits, step_plain;
+  // persistent step (one launch per token)
+  bool use_step = false;
+  int step_group = 0;
+  void* tagged = nullptr;          // tagged activations, epoch and done counter (device memory)
+  StepPhase* d_phases = nullptr;   // phase table (device memory)
+  void* step_uncached = nullptr;   // per-layer attention arrival counters (uncached pool)
+  tagged_t *t_resid = nullptr, *t_attn = nullptr, *t_qkv = nullptr;  // last layer's buffers (readback)
+  std::vector<std::string> phase_names;  // persistent step phases (profiling)
+  StepDebug* step_dbg = nullptr;   // abort record of the persistent step
   hipGraph_t graph_logits = nullptr, graph_plain = nullptr;
   hipGraphExec_t exec_logits = nullptr, exec_plain = nullptr;
   // pinned host staging
@@ -652,8 +668,8 @@ void build_steps(chonk_engine* e) {
       steps.push_back(L);
     }
   }
-  e->step_plain = steps;
-  e->step_plain.back().mv.advance_pos = 1;
+  e->kernels_plain = steps;
+  e->kernels_plain.back().mv.advance_pos = 1;
   // lm_head + group argmax
   {
     Launch L;
@@ -702,7 +718,253 @@ void build_steps(chonk_engine* e) {
     L.name = "select";
     steps.push_back(L);
   }
-  e->step_logits = steps;
+  e->kernels_logits = steps;
+}
+
+// The persistent step: one launch per token, phases in the order of the
+// per-phase kernels above, activations exchanged through tagged buffers.
+// Returns false (and leaves the per-phase kernels in use) when this model's
+// GQA group / K/V type is not compiled into it or it cannot be resident.
+bool build_step(chonk_engine* e) {
+  const ModelCfg& c = e->cfg;
+  const int G = c.heads / c.kv_heads;
+  const bool kv16 = e->kv_elem == 2;
+  if (!step_supported(G, kv16)) return false;
+  int cus = 0;
+  HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
+  if (cus <= 0) return false;
+  const int grid = cus;
+  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn, NL = c.layers;
+  const size_t shmem =
+      step_shared_bytes(std::max(H, std::max(qdim, F)), 0, G, c.hd, e->chunk, e->nchunk, (int)e->kv_elem);
+  if (shmem > lds_limit() || step_occupancy(G, kv16, shmem) < 1) return false;
+
+  // tagged buffers: R0 | RFIN | per layer QKV, ATT, RMID, FF, REND, DO, DD | epoch, done
+  const size_t per_layer = (size_t)(qdim + 2 * kvdim) + qdim + H + F + H + (c.gemma ? 2 * H : 0);
+  const size_t dbg_words = (sizeof(StepDebug) + 7) / 8;
+  const size_t words = 2 * (size_t)H + per_layer * NL + 2 + dbg_words;
+  HIP_OK(hipMalloc(&e->tagged, words * sizeof(tagged_t)));
+  HIP_OK(hipMemset(e->tagged, 0, words * sizeof(tagged_t)));
+  tagged_t* cur = (tagged_t*)e->tagged;
+  auto take = [&](size_t n) {
+    tagged_t* p = cur;
+    cur += n;
+    return p;
+  };
+  tagged_t* r0 = take(H);
+  tagged_t* rfin = take(H);
+  struct TL {
+    tagged_t *qkv, *att, *rmid, *ff, *rend, *d_o, *d_down;
+  };
+  std::vector<TL> tl((size_t)NL);
+  for (int i = 0; i < NL; ++i) {
+    tl[i].qkv = take((size_t)qdim + 2 * kvdim);
+    tl[i].att = take(qdim);
+    tl[i].rmid = take(H);
+    tl[i].ff = take(F);
+    tl[i].rend = take(H);
+    tl[i].d_o = c.gemma ? take(H) : nullptr;
+    tl[i].d_down = c.gemma ? take(H) : nullptr;
+  }
+  uint32_t* epoch = (uint32_t*)take(1);
+  uint32_t* done = (uint32_t*)take(1);
+  e->step_dbg = (StepDebug*)take(dbg_words);
+  const uint32_t one = 1;
+  HIP_OK(hipMemcpy(epoch, &one, 4, hipMemcpyHostToDevice));
+  // per-layer attention arrival counters and chunk partials: within one step a
+  // partial row is written and read exactly once, so a workgroup that merges
+  // several layers never meets a row it has read before (its vector L1 is only
+  // invalidated at kernel start)
+  const size_t rowf = ((size_t)G * (c.hd + 2) + 3) & ~(size_t)3;
+  const size_t part_layer = (size_t)c.kv_heads * e->nchunk * rowf;  // floats
+  const size_t cnt_bytes = align256((size_t)NL * c.kv_heads * 4);
+  e->step_uncached = uncached_pool().take(e->device, cnt_bytes + (size_t)NL * part_layer * 4);
+  uint32_t* cnt = (uint32_t*)e->step_uncached;
+  float* parts = (float*)((uint8_t*)e->step_uncached + cnt_bytes);
+  HIP_OK(hipMemset(cnt, 0, (size_t)NL * c.kv_heads * 4));
+
+  std::vector<StepPhase> ph;
+  auto seg = [&](MvSeg& sg, const QMat& w, int n_out, int tile, int first) {
+    sg.w = w;
+    sg.n_out = n_out;
+    sg.lpr = pick_lpr(w.k / 32);
+    sg.tile = tile;
+    sg.wg_begin = first;
+    return (n_out + tile - 1) / tile;
+  };
+  auto mv = [&](int k) {
+    StepPhase p{};
+    p.kind = PH_MV;
+    p.k = k;
+    p.nseg = 1;
+    return p;
+  };
+  for (int i = 0; i < NL; ++i) {
+    const LayerDev& Ld = e->layers[i];
+    tagged_t* rprev = i == 0 ? r0 : tl[i - 1].rend;
+    {  // q | k | v
+      StepPhase p = mv(H);
+      p.nseg = 3;
+      const int tile = (qdim + 2 * kvdim + grid - 1) / grid;
+      int n = seg(p.seg[0], Ld.q.q, qdim, tile, 0);
+      n += seg(p.seg[1], Ld.k.q, kvdim, tile, n);
+      n += seg(p.seg[2], Ld.v.q, kvdim, tile, n);
+      p.n_tasks = n;
+      p.tout[0] = tl[i].qkv;
+      p.tout[1] = tl[i].qkv + qdim;
+      p.tout[2] = tl[i].qkv + qdim + kvdim;
+      p.epi = EPI_STORE;
+      p.w_norm = Ld.in_norm;
+      if (i == 0) {
+        p.pro = PRO_EMBED_NORM;
+        p.res_out = r0;
+      } else if (c.gemma) {
+        p.pro = PRO_RES_NORM;
+        p.in = tl[i - 1].rmid;
+        p.delta = tl[i - 1].d_down;
+        p.w_delta = e->layers[i - 1].post_ffn_norm;
+        p.res_out = tl[i - 1].rend;
+      } else {
+        p.pro = PRO_NORM;
+        p.in = rprev;
+      }
+      ph.push_back(p);
+    }
+    {  // attention: the per-phase kernel's arguments with per-layer counters
+      StepPhase p{};
+      p.kind = PH_ATTN;
+      for (const Launch& L : e->kernels_logits)
+        if (L.kind == Launch::ATTN && L.layer == i) p.at = L.at;
+      p.at.cnt = cnt + (size_t)i * c.kv_heads;
+      p.at.part = parts + (size_t)i * part_layer;
+      p.n_tasks = c.kv_heads * e->nchunk;
+      p.qkv_in = tl[i].qkv;
+      p.attn_out = tl[i].att;
+      ph.push_back(p);
+    }
+    {  // o projection
+      StepPhase p = mv(qdim);
+      p.n_tasks = seg(p.seg[0], Ld.o.q, H, (H + grid - 1) / grid, 0);
+      p.pro = PRO_PLAIN;
+      p.in = tl[i].att;
+      if (c.gemma) {
+        p.epi = EPI_STORE;
+        p.tout[0] = tl[i].d_o;
+      } else {
+        p.epi = EPI_ADD;
+        p.add = rprev;
+        p.tout[0] = tl[i].rmid;
+      }
+      ph.push_back(p);
+    }
+    {  // gate | up
+      StepPhase p = mv(H);
+      p.n_tasks = seg(p.seg[0], Ld.gate.q, F, (F + grid - 1) / grid, 0);
+      p.seg[0].w2 = Ld.up.q;
+      p.tout[0] = tl[i].ff;
+      p.epi = c.gemma ? EPI_GLU_GELU : EPI_GLU_SILU;
+      if (c.gemma) {
+        p.pro = PRO_RES_NORM;
+        p.in = rprev;
+        p.delta = tl[i].d_o;
+        p.w_delta = Ld.post_norm;
+        p.res_out = tl[i].rmid;
+        p.w_norm = Ld.pre_ffn_norm;
+      } else {
+        p.pro = PRO_NORM;
+        p.in = tl[i].rmid;
+        p.w_norm = Ld.post_norm;
+      }
+      ph.push_back(p);
+    }
+    {  // down
+      StepPhase p = mv(F);
+      p.n_tasks = seg(p.seg[0], Ld.down.q, H, (H + grid - 1) / grid, 0);
+      p.pro = PRO_PLAIN;
+      p.in = tl[i].ff;
+      if (c.gemma) {
+        p.epi = EPI_STORE;
+        p.tout[0] = tl[i].d_down;
+      } else {
+        p.epi = EPI_ADD;
+        p.add = tl[i].rmid;
+        p.tout[0] = tl[i].rend;
+      }
+      ph.push_back(p);
+    }
+  }
+  {  // lm_head + group argmax: one 256-row group per task
+    StepPhase p = mv(H);
+    p.n_tasks = seg(p.seg[0], e->lm_head.q, c.vocab, 256, 0);
+    p.epi = EPI_LOGITS;
+    p.logits = e->logits;
+    p.w_norm = e->final_norm;
+    if (c.gemma) {
+      p.pro = PRO_RES_NORM;
+      p.in = tl[NL - 1].rmid;
+      p.delta = tl[NL - 1].d_down;
+      p.w_delta = e->layers[NL - 1].post_ffn_norm;
+      p.res_out = rfin;
+    } else {
+      p.pro = PRO_NORM;
+      p.in = tl[NL - 1].rend;
+    }
+    ph.push_back(p);
+  }
+  for (const StepPhase& p : ph)
+    for (int si = 0; si < p.nseg && p.kind == PH_MV; ++si)
+      if (2 * p.seg[si].tile > 1024) throw Error(CHONK_EINVAL, "persistent step: matvec tile too large");
+  // device copies: the phase table, then the two argument blocks (with / without logits)
+  const size_t ph_bytes = align256(ph.size() * sizeof(StepPhase));
+  HIP_OK(hipMalloc((void**)&e->d_phases, ph_bytes + 3 * align256(sizeof(StepArgs))));
+  HIP_OK(hipMemcpy(e->d_phases, ph.data(), ph.size() * sizeof(StepPhase), hipMemcpyHostToDevice));
+  StepArgs* d_args = (StepArgs*)((uint8_t*)e->d_phases + ph_bytes);
+
+  StepArgs a{};
+  a.phases = e->d_phases;
+  a.st = e->st;
+  a.epoch = epoch;
+  a.done = done;
+  a.embed = e->embed.q;
+  a.embed_scale = c.embed_scale;
+  a.eps = c.eps;
+  a.vocab = c.vocab;
+  a.hist = e->hist;
+  a.samp = e->samp;
+  a.pen_bits = e->pen_bits;
+  a.cand = e->cand;
+  a.sel = e->kernels_logits.back().sel;
+  a.dbg = e->step_dbg;
+  Launch L;
+  L.kind = Launch::STEP;
+  L.grid = grid;
+  L.shmem = shmem;
+  L.step_group = G;
+  L.step_kv16 = kv16;
+  L.name = "step";
+  L.weight_bytes = e->weight_bytes_per_token;
+  Launch Lp = L;
+  L.step = a;
+  L.step.n_phases = (int32_t)ph.size();
+  L.step.logits = 1;
+  Lp.step = a;
+  Lp.step.n_phases = (int32_t)ph.size() - 1;
+  Lp.step.logits = 0;
+  Lp.weight_bytes = e->weight_bytes_per_token - e->lm_head.gguf_bytes;
+  HIP_OK(hipMemcpy(d_args, &L.step, sizeof(StepArgs), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy((uint8_t*)d_args + align256(sizeof(StepArgs)), &Lp.step, sizeof(StepArgs), hipMemcpyHostToDevice));
+  L.d_step = d_args;
+  Lp.d_step = (const StepArgs*)((uint8_t*)d_args + align256(sizeof(StepArgs)));
+  e->step_logits = {L};
+  e->step_plain = {Lp};
+  for (int i = 0; i < NL; ++i)
+    for (const char* n : {"qkv", "attn", "oproj", "gateup", "down"}) e->phase_names.push_back("L" + std::to_string(i) + "." + n);
+  e->phase_names.push_back("lmhead");
+  e->t_resid = c.gemma ? rfin : tl[NL - 1].rend;
+  e->t_attn = tl[NL - 1].att;
+  e->t_qkv = tl[NL - 1].qkv;
+  e->use_step = true;
+  return true;
 }
 
 void enqueue(const Launch& L, hipStream_t s) {
@@ -710,6 +972,9 @@ void enqueue(const Launch& L, hipStream_t s) {
     case Launch::MV: HIP_OK(launch_matvec(L.mv, L.grid, L.shmem, s)); break;
     case Launch::ATTN: HIP_OK(launch_attention(L.at, L.shmem, s)); break;
     case Launch::SEL: HIP_OK(launch_select(L.sel, s)); break;
+    case Launch::STEP:
+      HIP_OK(launch_step(L.d_step, L.step.phases, L.step_group, L.step_kv16, L.grid, L.shmem, s));
+      break;
   }
 }
 
@@ -737,6 +1002,9 @@ void engine_free(chonk_engine* e) {
   e->weights.release();
   e->state.release();
   uncached_pool().give_back(e->device, e->uncached);
+  if (e->step_uncached) uncached_pool().give_back(e->device, e->step_uncached);
+  if (e->tagged) (void)hipFree(e->tagged);
+  if (e->d_phases) (void)hipFree(e->d_phases);
   if (e->h_state) (void)hipHostFree(e->h_state);
   if (e->h_tok) (void)hipHostFree(e->h_tok);
   if (e->h_samp) (void)hipHostFree(e->h_samp);
@@ -900,9 +1168,14 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
   HIP_OK(init_kernel_attributes());
   build_steps(e.get());
+  e->step_logits = e->kernels_logits;
+  e->step_plain = e->kernels_plain;
+  // the persistent step is the default; CHONK_STEP=0 keeps the per-phase kernels
+  const char* sv = std::getenv("CHONK_STEP");
+  if (!(sv && sv[0] == '0')) build_step(e.get());
   const char* ng = std::getenv("CHONK_NO_GRAPH");
   e->use_graph = !(ng && ng[0] == '1');
-  for (const Launch& L : e->step_logits)
+  for (const Launch& L : e->kernels_logits)
     if (L.shmem > lds_limit())
       throw Error(CHONK_EINVAL, "kernel " + L.name + " needs " + std::to_string(L.shmem) + " bytes of LDS, above the " +
                                     std::to_string(lds_limit()) + "-byte limit of this device");
@@ -1003,6 +1276,31 @@ void engine_reset(chonk_engine* e) {
   e->logits_valid = false;
 }
 
+// The error a step reported, with the persistent step's abort record.
+Error device_error(chonk_engine* e, const DevState& st) {
+  std::string msg = "device reported error code " + std::to_string(st.error);
+  if (st.error == 3 && e->step_dbg) {
+    StepDebug d;
+    if (hipMemcpy(&d, e->step_dbg, sizeof(d), hipMemcpyDeviceToHost) == hipSuccess && d.claimed) {
+      const int n = std::min(1024, e->step_logits.empty() ? 0 : e->step_logits[0].grid);
+      uint64_t lo = ~0ull, hi = 0;
+      for (int i = 0; i < n; ++i) {
+        lo = std::min(lo, d.start[i]);
+        hi = std::max(hi, d.start[i]);
+      }
+      char buf[512];
+      std::snprintf(buf, sizeof buf,
+                    " (persistent step aborted: workgroup %d waited over 20 ms in phase %d task %d for input word %d,"
+                    " tag %u, expected %u, at position %d; workgroup starts spread over %.1f us, abort %.1f us after"
+                    " the first start)",
+                    d.wg, d.phase, d.task, d.index, d.seen, d.want, d.pos, (double)(hi - lo) / 100.0,
+                    (double)(d.abort_time - lo) / 100.0);
+      msg += buf;
+    }
+  }
+  return Error(CHONK_EHIP, msg);
+}
+
 int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
                   size_t n_pen, const int32_t* seen, size_t n_seen) {
   if (e->pos >= e->cfg.ctx)
@@ -1022,7 +1320,7 @@ int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_
     HIP_OK(hipMemcpyAsync(e->h_state, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
     HIP_OK(hipStreamSynchronize(e->stream));
     const DevState st = *e->h_state;
-    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    if (st.error) throw device_error(e, st);
     e->pos += 1;
     e->known_token_pos = e->pos;
     e->known_token = st.last_token;
@@ -1110,7 +1408,7 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
     for (size_t i = 0; i + 1 < n_suffix; ++i) replay(e, false);
     replay(e, true);
     st = read_state(e);
-    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    if (st.error) throw device_error(e, st);
     e->pos = st.pos;
     next = st.last_token;
     e->logits_valid = true;
@@ -1142,7 +1440,7 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
       for (int64_t i = 0; i < batch; ++i) replay(e, true);
       remaining -= batch;
       st = read_state(e);
-      if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+      if (st.error) throw device_error(e, st);
     }
     st = read_state(e);
     generated.resize((size_t)st.n_generated);
@@ -1289,7 +1587,8 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;
   out->weight_bytes_per_token = e->weight_bytes_per_token;
   out->device_bytes = e->weights.capacity() + e->state.capacity();
-  out->kernels_per_step = (int32_t)e->step_logits.size();
+  out->kernels_per_step = (int32_t)e->kernels_logits.size();
+  out->persistent_step = e->use_step ? 1 : 0;
   return CHONK_OK;
 }
 
@@ -1371,16 +1670,27 @@ int chonk_engine_read_buffer(chonk_engine* e, int32_t which, void* out, size_t n
     const ModelCfg& c = e->cfg;
     const void* src = nullptr;
     size_t bytes = 0;
+    const tagged_t* tsrc = nullptr;
     switch (which) {
-      case 0: src = e->resA; bytes = (size_t)c.hidden * 4; break;
-      case 1: src = e->attn; bytes = (size_t)c.heads * c.hd * 4; break;
+      case 0: src = e->resA; tsrc = e->t_resid; bytes = (size_t)c.hidden * 4; break;
+      case 1: src = e->attn; tsrc = e->t_attn; bytes = (size_t)c.heads * c.hd * 4; break;
       case 2: src = e->cand; bytes = (size_t)e->groups * 8; break;
-      case 3: src = e->qkv; bytes = (size_t)(c.heads + 2 * c.kv_heads) * c.hd * 4; break;
+      case 3: src = e->qkv; tsrc = e->t_qkv; bytes = (size_t)(c.heads + 2 * c.kv_heads) * c.hd * 4; break;
       default: throw Error(CHONK_EINVAL, "unknown buffer id");
     }
     if (!out || n_bytes < bytes) throw Error(CHONK_EINVAL, "output buffer too small");
     HIP_OK(hipStreamSynchronize(e->stream));
-    HIP_OK(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
+    if (e->use_step && tsrc) {
+      // tagged words {value, epoch}: keep the values
+      std::vector<uint64_t> w(bytes / 4);
+      HIP_OK(hipMemcpy(w.data(), tsrc, w.size() * 8, hipMemcpyDeviceToHost));
+      for (size_t i = 0; i < w.size(); ++i) {
+        const uint32_t v = (uint32_t)w[i];
+        std::memcpy((uint8_t*)out + 4 * i, &v, 4);
+      }
+    } else {
+      HIP_OK(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
+    }
   });
 }
 
@@ -1451,7 +1761,7 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
     st = read_state(e);
-    if (st.error) throw Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
+    if (st.error) throw device_error(e, st);
     e->pos = st.pos;
     e->known_token_pos = -1;
     e->logits_valid = true;
@@ -1461,13 +1771,53 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
   });
 }
 
+int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases) {
+  return api(e, [&] {
+    if (!e->use_step) throw Error(CHONK_EINVAL, "the engine does not run the persistent step");
+    const ModelCfg& c = e->cfg;
+    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    const Launch& L = e->step_logits[0];
+    const int np = L.step.n_phases, grid = L.grid;
+    const size_t words = (size_t)(np + 1) * grid;
+    uint64_t* tr = nullptr;
+    HIP_OK(hipMalloc(&tr, words * 8));
+    Launch run = L;
+    run.step.trace = tr;
+    StepArgs* slot = (StepArgs*)((uint8_t*)L.d_step + 2 * align256(sizeof(StepArgs)));
+    HIP_OK(hipMemcpy(slot, &run.step, sizeof(StepArgs), hipMemcpyHostToDevice));
+    run.d_step = slot;
+    const DevState saved = read_state(e);
+    DevState st = saved;
+    st.stopped = 0;
+    st.generating = 0;
+    upload_state_fields(e, st);
+    enqueue(run, e->stream);  // warm
+    HIP_OK(hipMemsetAsync(tr, 0, words * 8, e->stream));
+    upload_state_fields(e, st);
+    enqueue(run, e->stream);
+    HIP_OK(hipStreamSynchronize(e->stream));
+    std::vector<uint64_t> h(words);
+    HIP_OK(hipMemcpy(h.data(), tr, words * 8, hipMemcpyDeviceToHost));
+    (void)hipFree(tr);
+    upload_state_fields(e, saved);
+    uint64_t t0 = ~0ull;
+    for (int w = 0; w < grid; ++w) t0 = std::min(t0, h[(size_t)np * grid + w]);
+    for (int p = 0; p < np && p < cap; ++p) {
+      uint64_t end = 0;
+      for (int w = 0; w < grid; ++w) end = std::max(end, h[(size_t)p * grid + w]);
+      phase_end_us[p] = (double)(end - t0) / 100.0;  // 100 MHz wall clock
+    }
+    if (n_phases) *n_phases = np;
+  });
+}
+
 int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
                               size_t name_len, uint64_t* bytes) {
   return api(e, [&] {
     const ModelCfg& c = e->cfg;
-    if (kernel_id < 0 || kernel_id >= (int32_t)e->step_logits.size() || reps <= 0)
+    if (kernel_id < 0 || kernel_id >= (int32_t)e->kernels_logits.size() || reps <= 0)
       throw Error(CHONK_EINVAL, "bad kernel id or repetitions");
-    const Launch& L = e->step_logits[(size_t)kernel_id];
+    const Launch& L = e->kernels_logits[(size_t)kernel_id];
     if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
     if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
     const DevState saved = read_state(e);

@@ -100,6 +100,85 @@ struct SelArgs {
   DevState* st;
 };
 
+// Persistent decode step --------------------------------------------------------
+//
+// The whole token (every layer, lm_head, selection) as one launch of one
+// workgroup per CU. Phases follow each other in the order of the step; a
+// workgroup walks its tasks of every phase (task t of a phase runs on
+// workgroup (t + rot) mod grid). Activations crossing workgroups are "tagged":
+// 8-byte words {f32 value, u32 step epoch} written and read with agent-scope
+// atomics, so a consumer waits for its inputs by polling the words themselves
+// (no counters, no cache maintenance), with a bounded wait that aborts the step
+// (DevState.error = 3) instead of hanging.
+typedef uint64_t tagged_t;
+
+enum PhaseKind : int32_t { PH_MV = 0, PH_ATTN = 1 };
+
+struct StepPhase {
+  int32_t kind;
+  int32_t n_tasks;
+  int32_t rot;
+  int32_t nseg;
+  // PH_MV: up to three matrices sharing the input (q | k | v); seg[i].wg_begin
+  // is the segment's first task, seg[i].tile its rows per task.
+  MvSeg seg[3];
+  int32_t pro, epi, k, pad0;
+  const tagged_t* in;      // input [k] (PRO_PLAIN, PRO_NORM, PRO_RES_NORM)
+  const tagged_t* delta;   // PRO_RES_NORM: branch output to normalise and add
+  const float* w_norm;
+  const float* w_delta;
+  tagged_t* res_out;       // PRO_EMBED_NORM / PRO_RES_NORM: residual [k], written in task slices
+  const tagged_t* add;     // EPI_ADD: residual input [n_out]
+  tagged_t* tout[3];       // per-segment tagged outputs (EPI_STORE / EPI_ADD / EPI_GLU_*)
+  float* logits;           // EPI_LOGITS: plain logits [vocab]
+  // PH_ATTN: one task per (kv head, chunk); q|k|v come from qkv_in, the merged
+  // output goes to attn_out
+  AttnArgs at;
+  const tagged_t* qkv_in;
+  tagged_t* attn_out;
+};
+
+// Record of the first wait that exceeded its time bound (diagnostics).
+struct StepDebug {
+  uint32_t claimed;        // set by the first workgroup that aborts
+  int32_t wg, phase, task, index;
+  uint32_t seen, want;     // tag found at `index` / tag expected
+  int32_t pos;
+  uint64_t abort_time;     // wall clock (100 MHz ticks)
+  uint64_t start[1024];    // per-workgroup start time of the last step
+};
+
+struct StepArgs {
+  const StepPhase* phases;
+  int32_t n_phases;
+  int32_t logits;          // 1: the step ends with token selection
+  DevState* st;
+  uint32_t* epoch;         // step epoch (tags); advanced by the last workgroup
+  uint32_t* done;          // workgroups finished; reset by the last one
+  QMat embed;
+  float embed_scale;
+  float eps;
+  int32_t vocab;
+  int32_t pad0;
+  const int32_t* hist;
+  const DevSampling* samp;
+  const uint32_t* pen_bits;
+  Candidate* cand;
+  SelArgs sel;
+  StepDebug* dbg;
+  uint64_t* trace;         // optional [n_phases + 1][grid] wall-clock stamps: phase ends, then start
+};
+
+// Dynamic LDS bytes of the persistent step for this model.
+size_t step_shared_bytes(int max_k, int max_tile_rows, int group, int hd, int chunk, int nchunk, int kv_elem);
+// Whether the persistent step is compiled for this GQA group / K/V type.
+bool step_supported(int group, bool kv_f16);
+// Workgroups of the persistent step resident per CU with `shmem` bytes of LDS (0: cannot run).
+int step_occupancy(int group, bool kv_f16, size_t shmem);
+// `a` and `phases` point to device memory holding the step's arguments and phase table.
+hipError_t launch_step(const StepArgs* a, const StepPhase* phases, int group, bool kv_f16, int grid, size_t shmem,
+                       hipStream_t s);
+
 // Launch parameter helpers -------------------------------------------------------
 size_t mv_shared_bytes(int k, int max_tile_rows);
 size_t attn_shared_bytes(int group, int hd, int chunk, int nchunk, int kv_elem);

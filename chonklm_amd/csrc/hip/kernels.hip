@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "kernel_common.h"
 #include "kernels.h"
 #include "qdot.h"
 
@@ -26,124 +27,8 @@ namespace chonk {
 
 namespace {
 
-constexpr float kNegBig = -3.402823e38f;  // the WGSL literal -3.402823e38
-
-// Cross-lane steps without the LDS crossbar: DPP quad/row permutations inside
-// 16-lane rows, a swizzle across the two rows of a 32-lane half, and scalar
-// lane reads across halves. Every lane of an aligned group of N lanes ends with
-// the same value. Lanes of a group must be active together.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float swz_xor16(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
-}
-__device__ __forceinline__ float lane_of(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-  if constexpr (N >= 2) v += dpp<0xb1>(v);   // quad_perm 1,0,3,2
-  if constexpr (N >= 4) v += dpp<0x4e>(v);   // quad_perm 2,3,0,1
-  if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror
-  if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror
-  if constexpr (N >= 32) v += swz_xor16(v);
-  if constexpr (N >= 64) v = lane_of(v, 0) + lane_of(v, 32);
-  return v;
-}
-template <int N>
-__device__ __forceinline__ float group_max(float v) {
-  if constexpr (N >= 2) v = fmaxf(v, dpp<0xb1>(v));
-  if constexpr (N >= 4) v = fmaxf(v, dpp<0x4e>(v));
-  if constexpr (N >= 8) v = fmaxf(v, dpp<0x141>(v));
-  if constexpr (N >= 16) v = fmaxf(v, dpp<0x140>(v));
-  if constexpr (N >= 32) v = fmaxf(v, swz_xor16(v));
-  if constexpr (N >= 64) v = fmaxf(lane_of(v, 0), lane_of(v, 32));
-  return v;
-}
-// runtime group width (power of two in [1, 64])
-__device__ __forceinline__ float group_sum_n(float v, int n) {
-  switch (n) {
-    case 2: return group_sum<2>(v);
-    case 4: return group_sum<4>(v);
-    case 8: return group_sum<8>(v);
-    case 16: return group_sum<16>(v);
-    case 32: return group_sum<32>(v);
-    case 64: return group_sum<64>(v);
-    default: return v;
-  }
-}
-__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
-__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
-
-// Sum over the 256 threads; red must hold 4 floats. Callable repeatedly.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
-  if (v != v) return false;
-  if (bv != bv) return true;
-  return (v > bv) || ((v == bv) && (i < bi));
-}
-
-__device__ __forceinline__ bool bit_test(const uint32_t* bits, uint32_t id) {
-  return (bits[id >> 5] >> (id & 31u)) & 1u;
-}
-
-__device__ __forceinline__ void st_relaxed(float* p, float v) {
-  __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_relaxed(const float* p) {
-  return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-}
-
-__device__ __forceinline__ float gelu_tanh(float x) {
-  if (x != x) return 0.0f;
-  if (x > 10.0f) return x;
-  if (x < -10.0f) return 0.0f;
-  const float c = 0.7978845608028654f;
-  const float cube = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
-  const float t = __fadd_rn(1.0f, tanhf(__fmul_rn(c, __fadd_rn(x, cube))));
-  return __fmul_rn(__fmul_rn(0.5f, x), t);
-}
-
-// ---------------------------------------------------------------------------
-// matvec: activation staging, weight streaming, epilogues.
-
-typedef __attribute__((address_space(1))) void gmem_void;
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Copies n floats from global memory into LDS with the CDNA3/4 direct-to-LDS
-// loads (16 bytes per lane, no registers); completion is awaited with
-// s_waitcnt vmcnt(0) + a barrier by the caller.
-__device__ __forceinline__ void lds_dma(const float* src, float* dst, int n) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int base = wave * 256; base < n; base += 4 * 256) {
-    const int idx = base + lane * 4;
-    if (idx < n) __builtin_amdgcn_global_load_lds((gmem_void*)(src + idx), (lds_void*)(dst + base), 16, 0, 0);
-  }
-}
-
 // This workgroup's segment, picked field by field (forming a reference into
 // the argument block would make the compiler copy the whole block to scratch).
-struct SegView {
-  QMat w;
-  const uint8_t *u0, *u1, *u2, *u3;  // GLU up-matrix streams
-  float* out;
-  const float* add;
-  int n_out, tile, lpr, wg_begin;
-};
 
 __device__ __forceinline__ SegView seg_view(const MvArgs& a) {
   const int b = (int)blockIdx.x;
@@ -429,114 +314,6 @@ __global__ __launch_bounds__(kWg) void k_mv_logits(const MvArgs a) { matvec_body
 //      positions over V with the weights broadcast by readlane.
 //   D  the four wave partials combine into the chunk partial (m, l, acc[hd])
 //      in uncached memory; the last chunk of a kv head to arrive merges.
-constexpr int kMaxG = 8;
-
-__host__ __device__ constexpr int attn_tpp(int hd) { return hd / 64 > 2 ? hd / 64 : 2; }
-
-template <bool KV16>
-__device__ __forceinline__ void load_v(const void* tile, int idx, int dpl, float* v) {
-  if constexpr (KV16) {
-    const __half* h = (const __half*)tile + idx;
-    if (dpl == 1) {
-      v[0] = __half2float(h[0]);
-    } else if (dpl == 2) {
-      const uint32_t w = *(const uint32_t*)h;
-      v[0] = h2f(w);
-      v[1] = h2f(w >> 16);
-    } else {
-      const uint2 w = *(const uint2*)h;
-      v[0] = h2f(w.x);
-      v[1] = h2f(w.x >> 16);
-      v[2] = h2f(w.y);
-      v[3] = h2f(w.y >> 16);
-    }
-  } else {
-    const float* f = (const float*)tile + idx;
-    if (dpl == 1) {
-      v[0] = f[0];
-    } else if (dpl == 2) {
-      const float2 w = *(const float2*)f;
-      v[0] = w.x;
-      v[1] = w.y;
-    } else {
-      const float4 w = *(const float4*)f;
-      v[0] = w.x;
-      v[1] = w.y;
-      v[2] = w.z;
-      v[3] = w.w;
-    }
-  }
-}
-
-// s[g] += q_g[my dims] . k[my dims] for this thread's NV 16-byte K vectors.
-template <int G, bool KV16, int NV>
-__device__ __forceinline__ void score_dot(const uint4* kreg, const float* qbase, int hd, float (&s)[G]) {
-  constexpr int per = KV16 ? 8 : 4;  // elements per vector
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float kf[8];
-    if constexpr (KV16) {
-      const uint32_t w4[4] = {kreg[v].x, kreg[v].y, kreg[v].z, kreg[v].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kf[2 * i] = h2f(w4[i]);
-        kf[2 * i + 1] = h2f(w4[i] >> 16);
-      }
-    } else {
-      kf[0] = __uint_as_float(kreg[v].x);
-      kf[1] = __uint_as_float(kreg[v].y);
-      kf[2] = __uint_as_float(kreg[v].z);
-      kf[3] = __uint_as_float(kreg[v].w);
-    }
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      const float4* qq = (const float4*)(qbase + gg * hd + v * per);
-      const float4 q0 = qq[0];
-      float s4 = (q0.x * kf[0] + q0.y * kf[1]) + (q0.z * kf[2] + q0.w * kf[3]);
-      if constexpr (per == 8) {
-        const float4 q1 = qq[1];
-        s4 += (q1.x * kf[4] + q1.y * kf[5]) + (q1.z * kf[6] + q1.w * kf[7]);
-      }
-      s[gg] += s4;
-    }
-  }
-}
-
-// o[g][0..DPL) += sum over positions p in [pa, pb) of w_g(p) * V[p][d0..d0+DPL),
-// where w_g(p) sits in lane (p - w0) * tpp of e[g]; eight positions per pass
-// so that the LDS reads of a pass overlap.
-template <int G, bool KV16, int DPL>
-__device__ __forceinline__ void v_walk(const void* tile, int hd, int d0, int pa, int pb, int w0, int tpp,
-                                       const float (&e)[G], float (&o)[G][4]) {
-  int p = pa;
-  for (; p + 8 <= pb; p += 8) {
-    float vv[8][4];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) load_v<KV16>(tile, (p + u) * hd + d0, DPL, vv[u]);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int sel = (p + u - w0) * tpp;
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[gg]), sel));
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) o[gg][k] += wgt * vv[u][k];
-      }
-    }
-  }
-  for (; p < pb; ++p) {
-    float vv[4];
-    load_v<KV16>(tile, p * hd + d0, DPL, vv);
-    const int sel = (p - w0) * tpp;
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[gg]), sel));
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) o[gg][k] += wgt * vv[k];
-    }
-  }
-}
-
 template <int G, bool KV16>
 __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   extern __shared__ __align__(16) float sm[];
@@ -620,412 +397,15 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
     __syncthreads();
   }
 
-  // B: per-head RMSNorm + rotary, one wave per head; the new k/v to the cache
-  {
-    const int nh = G + (own_new ? 1 : 0);
-    const size_t row = head_base + (size_t)pos * hd;
-    for (int hh = wave; hh < nh; hh += 4) {
-      const bool is_k = hh == G;
-      float* x = is_k ? k_new : q_s + hh * hd;
-      float r = 1.0f;
-      if (a.qn_w) {
-        float ss = 0.f;
-        for (int d = lane; d < hd; d += 64) ss += x[d] * x[d];
-        ss = wave_sum(ss);
-        r = 1.0f / sqrtf(ss / (float)hd + a.eps);
-      }
-      const float* w = is_k ? kn : qn;
-      for (int d = lane; d < half; d += 64) {
-        const int ia = a.interleaved ? 2 * d : d;
-        const int ib = a.interleaved ? 2 * d + 1 : d + half;
-        float x0 = x[ia], x1 = x[ib];
-        if (a.qn_w) {
-          x0 = __fmul_rn(__fmul_rn(x0, r), w[ia]);
-          x1 = __fmul_rn(__fmul_rn(x1, r), w[ib]);
-        }
-        const float ang = __fmul_rn((float)pos, inv[d]);
-        const float co = cosf(ang), si = sinf(ang);
-        float y0 = __fsub_rn(__fmul_rn(x0, co), __fmul_rn(x1, si));
-        float y1 = __fadd_rn(__fmul_rn(x0, si), __fmul_rn(x1, co));
-        if (is_k) {
-          if constexpr (KV16) {
-            const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
-            ((__half*)a.kc)[row + ia] = h0;
-            ((__half*)a.kc)[row + ib] = h1;
-            y0 = __half2float(h0);
-            y1 = __half2float(h1);
-          } else {
-            ((float*)a.kc)[row + ia] = y0;
-            ((float*)a.kc)[row + ib] = y1;
-          }
-        }
-        x[ia] = y0;
-        x[ib] = y1;
-      }
-      if (is_k) {
-        for (int d = lane; d < hd; d += 64) {
-          if constexpr (KV16) {
-            const __half vh = __float2half_rn(v_new[d]);
-            ((__half*)a.vc)[row + d] = vh;
-            ((__half*)tile)[p_new * hd + d] = vh;
-          } else {
-            ((float*)a.vc)[row + d] = v_new[d];
-            tile[p_new * hd + d] = v_new[d];
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  // C: scores, wave-local softmax statistics, weighted V
-  {
-    const bool valid = my_p < CH && my_p >= p_begin && my_p < p_end;
-    if (own_new && my_p == p_new) {
-      // the new position's k (already rounded to the cache type) into the K registers
-      const float* kk = k_new + my_j * dpt;
-#pragma unroll
-      for (int v = 0; v < kVec; ++v) {
-        if (v < nvec) {
-          if constexpr (KV16) {
-            uint32_t w4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              w4[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[v * 8 + 2 * i])) |
-                      ((uint32_t)__half_as_ushort(__float2half_rn(kk[v * 8 + 2 * i + 1])) << 16);
-            kreg[v] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-          } else {
-            kreg[v] = make_uint4(__float_as_uint(kk[v * 4]), __float_as_uint(kk[v * 4 + 1]),
-                                 __float_as_uint(kk[v * 4 + 2]), __float_as_uint(kk[v * 4 + 3]));
-          }
-        }
-      }
-    }
-    float s[G];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) s[gg] = 0.f;
-    {
-      const float* qbase = q_s + my_j * dpt;
-      switch (nvec) {
-        case 1: score_dot<G, KV16, 1>(kreg, qbase, hd, s); break;
-        case 2: score_dot<G, KV16, 2>(kreg, qbase, hd, s); break;
-        case 4: score_dot<G, KV16, 4>(kreg, qbase, hd, s); break;
-        case 8: score_dot<G, KV16, 8>(kreg, qbase, hd, s); break;
-        default:
-          if constexpr (!KV16) score_dot<G, KV16, 16>(kreg, qbase, hd, s);
-          break;
-      }
-    }
-    float e[G], m[G], l[G];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      s[gg] = group_sum_n(s[gg], tpp);
-      const float sv = valid ? s[gg] * a.scale : -INFINITY;
-      m[gg] = wave_max(sv);
-      e[gg] = valid ? expf(sv - m[gg]) : 0.0f;
-      l[gg] = wave_sum(my_j == 0 ? e[gg] : 0.0f);
-    }
-    // V: lane -> dims [d0, d0 + dpl); positions of this wave in order
-    const int dpl = hd >= 64 ? hd / 64 : 1;
-    const int d0 = (lane * dpl) % hd;
-    const int w0 = wave * P;
-    const int pa = max(p_begin, w0), pb = min(p_end, w0 + P);
-    float o[G][4];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[gg][k] = 0.f;
-    if (dpl == 1)
-      v_walk<G, KV16, 1>(tile, hd, d0, pa, pb, w0, tpp, e, o);
-    else if (dpl == 2)
-      v_walk<G, KV16, 2>(tile, hd, d0, pa, pb, w0, tpp, e, o);
-    else
-      v_walk<G, KV16, 4>(tile, hd, d0, pa, pb, w0, tpp, e, o);
-    if (lane * dpl < hd) {
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (k < dpl) wpart[(wave * G + gg) * hd + d0 + k] = o[gg][k];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        wml[(wave * kMaxG + gg) * 2] = m[gg];
-        wml[(wave * kMaxG + gg) * 2 + 1] = l[gg];
-      }
-    }
-  }
-  __syncthreads();
-
-  // D: chunk partial = the four wave partials rescaled to the chunk maximum
-  const int rowf = (G * (hd + 2) + 3) & ~3;  // floats per chunk partial, 16-byte multiple
-  float* part = a.part + (size_t)(kv * a.nchunk + c) * rowf;
-  for (int i = tid; i < G * hd; i += kWg) {
-    const int gg = i / hd, d = i - gg * hd;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * kMaxG + gg) * 2]);
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = wml[(w * kMaxG + gg) * 2];
-      if (mw != -INFINITY) acc += wpart[(w * G + gg) * hd + d] * expf(mw - M);
-    }
-    part[gg * (hd + 2) + 2 + d] = acc;
-  }
-  if (tid < G) {
-    float M = -INFINITY, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * kMaxG + tid) * 2]);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = wml[(w * kMaxG + tid) * 2];
-      if (mw != -INFINITY) L += wml[(w * kMaxG + tid) * 2 + 1] * expf(mw - M);
-    }
-    *(float2*)(part + tid * (hd + 2)) = make_float2(M, L);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(&a.cnt[kv], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (old == (uint32_t)(c_hi - c_lo)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // merge (last chunk): chunk weights w[g][c] = exp(m_c - M_g) once, then the
-  // acc rows, staged into LDS in batches, weighted and summed
-  const int nact = c_hi - c_lo + 1;
-  const float* rows0 = a.part + (size_t)(kv * a.nchunk + c_lo) * rowf;
-  float* stage = tile;
-  const int per_batch = max(1, a.merge_floats / rowf);
-  lds_dma(rows0, stage, min(per_batch, nact) * rowf);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int gg = wave; gg < G; gg += 4) {
-    float M = -INFINITY;
-    for (int cc = lane; cc < nact; cc += 64) {
-      const float mv = cc < per_batch ? stage[cc * rowf + gg * (hd + 2)] : rows0[(size_t)cc * rowf + gg * (hd + 2)];
-      M = fmaxf(M, mv);
-    }
-    M = wave_max(M);
-    float L = 0.f;
-    for (int cc = lane; cc < nact; cc += 64) {
-      const float* pp = cc < per_batch ? stage + cc * rowf + gg * (hd + 2) : rows0 + (size_t)cc * rowf + gg * (hd + 2);
-      const float f = expf(pp[0] - M);
-      wts[gg * ncp + cc] = f;
-      L += pp[1] * f;
-    }
-    L = wave_sum(L);
-    if (lane == 0) wml[2 * gg] = 1.0f / L;
-  }
-  __syncthreads();
-  float o[8];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) o[q] = 0.f;
-  for (int b0 = 0; b0 < nact; b0 += per_batch) {
-    const int nb = min(per_batch, nact - b0);
-    if (b0 > 0) {
-      __syncthreads();  // previous batch consumed
-      lds_dma(rows0 + (size_t)b0 * rowf, stage, nb * rowf);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int i = tid + q * kWg;
-      if (i < G * hd) {
-        const int gg = i / hd, d = i - gg * hd;
-        const float* src = stage + gg * (hd + 2) + 2 + d;
-        const float* wv = wts + gg * ncp + b0;
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-        int cc = 0;
-        for (; cc + 4 <= nb; cc += 4) {
-          acc0 += src[cc * rowf] * wv[cc];
-          acc1 += src[(cc + 1) * rowf] * wv[cc + 1];
-          acc2 += src[(cc + 2) * rowf] * wv[cc + 2];
-          acc3 += src[(cc + 3) * rowf] * wv[cc + 3];
-        }
-        for (; cc < nb; ++cc) acc0 += src[cc * rowf] * wv[cc];
-        o[q] += (acc0 + acc1) + (acc2 + acc3);
-      }
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int i = tid + q * kWg;
-    if (i < G * hd) {
-      const int gg = i / hd, d = i - gg * hd;
-      a.out[(kv * G + gg) * hd + d] = o[q] * wml[2 * gg];
-    }
-  }
-  if (tid == 0) __hip_atomic_store(&a.cnt[kv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  attn_compute<G, KV16>(a, sm, kv, c, pos, kreg, &s_last,
+                        [&](int i, float v) { a.out[(size_t)kv * G * hd + i] = v; });
 }
 
 // ---------------------------------------------------------------------------
-// Token selection: ARGMAX_STAGE2 or the candidate sampler; bookkeeping.
-constexpr int kMaxGroups = 4096;
-
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  return z ^ (z >> 31);
-}
-
-// sort order: valid before invalid, then value descending, then group ascending
-__device__ __forceinline__ bool before(double va, uint32_t ga, double vb, uint32_t gb) {
-  const bool oka = !(ga >> 31), okb = !(gb >> 31);
-  if (oka != okb) return oka;
-  if (va != vb) return va > vb;
-  return (ga & 0x7fffffffu) < (gb & 0x7fffffffu);
-}
-
 __global__ __launch_bounds__(kWg) void k_select(const SelArgs a) {
-  DevState* st = a.st;
-  if (st->stopped) return;
-  const DevSampling& s = *a.samp;
-  const int tid = threadIdx.x;
-  __shared__ float vals[kWg];
-  __shared__ uint32_t idx[kWg];
-  __shared__ double sv[kMaxGroups];
-  __shared__ uint32_t sg[kMaxGroups];
-  __shared__ int s_int[4];
-  int token = 0;
-  const int groups = a.groups;
-
-  if (s.sample_mode == 0) {
-    float bv = kNegBig;
-    uint32_t bi = 0xffffffffu;
-    for (int g = tid; g < groups; g += kWg) {
-      const Candidate c = a.cand[g];
-      if (better(c.value, c.index, bv, bi)) {
-        bv = c.value;
-        bi = c.index;
-      }
-    }
-    vals[tid] = bv;
-    idx[tid] = bi;
-    __syncthreads();
-    for (int stride = 128; stride >= 1; stride >>= 1) {
-      if (tid < stride && better(vals[tid + stride], idx[tid + stride], vals[tid], idx[tid])) {
-        vals[tid] = vals[tid + stride];
-        idx[tid] = idx[tid + stride];
-      }
-      __syncthreads();
-    }
-    token = (int)idx[0];
-  } else {
-    int n2 = 1;
-    while (n2 < groups) n2 <<= 1;
-    // load + second penalty (sampling.ts:35-43)
-    int cnt = 0;
-    for (int i = tid; i < n2; i += kWg) {
-      double v = 0.0;
-      bool ok = false;
-      if (i < groups) {
-        const Candidate c = a.cand[i];
-        ok = isfinite(c.value) && c.index != 0xffffffffu;
-        v = (double)c.value;
-        if (ok && s.seen_penalty && c.index < (uint32_t)a.vocab && bit_test(a.seen_bits, c.index))
-          v = v > 0 ? v / s.repetition_penalty : v * s.repetition_penalty;
-      }
-      sv[i] = ok ? v : 0.0;
-      sg[i] = (uint32_t)i | (ok ? 0u : 0x80000000u);
-      cnt += ok ? 1 : 0;
-    }
-    vals[tid] = (float)cnt;
-    __syncthreads();
-    for (int stride = 128; stride >= 1; stride >>= 1) {
-      if (tid < stride) vals[tid] += vals[tid + stride];
-      __syncthreads();
-    }
-    const int n_valid = (int)vals[0];
-    // bitonic sort (stable via the group index key)
-    for (int k = 2; k <= n2; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < n2; i += kWg) {
-          const int ixj = i ^ j;
-          if (ixj > i) {
-            const bool asc = (i & k) == 0;
-            const bool swap = asc ? before(sv[ixj], sg[ixj], sv[i], sg[i]) : before(sv[i], sg[i], sv[ixj], sg[ixj]);
-            if (swap) {
-              const double tv = sv[i];
-              sv[i] = sv[ixj];
-              sv[ixj] = tv;
-              const uint32_t tg = sg[i];
-              sg[i] = sg[ixj];
-              sg[ixj] = tg;
-            }
-          }
-        }
-        __syncthreads();
-      }
-    }
-    const int lim = s.top_k > 0 ? min(s.top_k, n_valid) : n_valid;
-    auto id_at = [&](int i) -> int { return (int)a.cand[sg[i] & 0x7fffffffu].index; };
-    if (s.temperature <= 0.0) {
-      token = n_valid > 0 ? id_at(0) : 0;
-    } else {
-      // sampling.ts:53-75: probabilities in parallel, the running sums
-      // sequentially in the reference's order.
-      const double maxv = lim > 0 ? sv[0] : 0.0;
-      __syncthreads();
-      for (int i = tid; i < lim; i += kWg) sv[i] = exp((sv[i] - maxv) / s.temperature);
-      __syncthreads();
-      if (tid == 0) {
-        double total = 0.0;
-        for (int i = 0; i < lim; ++i) total += sv[i];
-        int cutoff = lim;
-        if (s.top_p < 1.0 && total > 0.0) {
-          double cdf = 0.0;
-          for (int i = 0; i < lim; ++i) {
-            cdf += sv[i] / total;
-            if (cdf >= s.top_p) {
-              cutoff = i + 1;
-              break;
-            }
-          }
-        }
-        double sample_total = 0.0;
-        for (int i = 0; i < cutoff; ++i) sample_total += sv[i];
-        const uint64_t z = mix64(s.seed + 0x9e3779b97f4a7c15ull * (uint64_t)(st->pos + 1));
-        const double u = (double)(z >> 11) * (1.0 / 9007199254740992.0);
-        double r = u * sample_total;
-        int pick = -1;
-        for (int i = 0; i < cutoff; ++i) {
-          r -= sv[i];
-          if (r <= 0) {
-            pick = i;
-            break;
-          }
-        }
-        if (pick < 0) pick = max(0, cutoff - 1);
-        s_int[2] = lim > 0 ? id_at(pick) : 0;
-      }
-      __syncthreads();
-      token = s_int[2];
-    }
-  }
-
-  if (tid == 0) {
-    const int pos = st->pos;
-    st->last_token = token;
-    if (pos + 1 <= a.ctx) a.hist[pos + 1] = token;
-    if (st->generating) {
-      const int ng = st->n_generated;
-      if (ng <= a.ctx) a.gen[ng] = token;
-      st->n_generated = ng + 1;
-      if (token >= 0 && token < a.vocab) {
-        a.pen_bits[token >> 5] |= 1u << (token & 31);
-        a.seen_bits[token >> 5] |= 1u << (token & 31);
-      }
-      bool eos = false;
-      for (int i = 0; i < s.n_eos && i < 16; ++i) eos |= (s.eos[i] == token);
-      if (eos || ng + 1 >= st->max_generated) st->stopped = 1;
-    }
-    st->pos = pos + 1;
-  }
+  __shared__ __align__(16) uint8_t ws[kSelectWorkspaceBytes];
+  if (a.st->stopped) return;
+  select_token(a, ws);
 }
 
 // ---------------------------------------------------------------------------

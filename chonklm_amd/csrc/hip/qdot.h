@@ -75,7 +75,7 @@ struct Frag<QT_Q5_1> {
   uint32_t d, m;
 };
 
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const unsigned short*)p; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *gbl((const unsigned short*)p); }
 
 template <int T>
 __device__ __forceinline__ Frag<T> load_unit(const QMat& w, int row, int u);
@@ -84,18 +84,18 @@ template <>
 __device__ __forceinline__ Frag<QT_Q4_K> load_unit<QT_Q4_K>(const QMat& w, int row, int u) {
   const size_t K = (size_t)w.k;
   Frag<QT_Q4_K> f;
-  f.qs = *(const uint4*)(w.s0 + row * (K / 2) + 16 * u);
-  f.hdr = *(const uint4*)(w.s1 + row * (K / 16) + 16 * (u >> 3));
+  f.qs = ldg4(w.s0 + row * (K / 2) + 16 * u);
+  f.hdr = ldg4(w.s1 + row * (K / 16) + 16 * (u >> 3));
   return f;
 }
 template <>
 __device__ __forceinline__ Frag<QT_Q5_K> load_unit<QT_Q5_K>(const QMat& w, int row, int u) {
   const size_t K = (size_t)w.k;
   Frag<QT_Q5_K> f;
-  f.qs = *(const uint4*)(w.s0 + row * (K / 2) + 16 * u);
-  f.hdr = *(const uint4*)(w.s1 + row * (K / 16) + 16 * (u >> 3));
+  f.qs = ldg4(w.s0 + row * (K / 2) + 16 * u);
+  f.hdr = ldg4(w.s1 + row * (K / 16) + 16 * (u >> 3));
   const int hh = u & 1;
-  f.qh = *(const uint4*)(w.s2 + row * (K / 8) + 32 * (u >> 3) + 16 * hh);
+  f.qh = ldg4(w.s2 + row * (K / 8) + 32 * (u >> 3) + 16 * hh);
   return f;
 }
 template <>
@@ -104,10 +104,10 @@ __device__ __forceinline__ Frag<QT_Q6_K> load_unit<QT_Q6_K>(const QMat& w, int r
   const int sb = u >> 3, c = u & 7, h = c >> 2, b = c & 3;
   Frag<QT_Q6_K> f;
   const uint8_t* ql = w.s0 + row * (K / 2) + 128 * sb + 64 * h + 8 * b;
-  f.qa = *(const uint2*)ql;
-  f.qb = *(const uint2*)(ql + 32);
-  f.qh = *(const uint2*)(w.s1 + row * (K / 4) + 64 * sb + 32 * h + 8 * b);
-  f.sc = *(const uint2*)(w.s2 + row * (K / 16) + 16 * sb + 8 * h);
+  f.qa = ldg2(ql);
+  f.qb = ldg2(ql + 32);
+  f.qh = ldg2(w.s1 + row * (K / 4) + 64 * sb + 32 * h + 8 * b);
+  f.sc = ldg2(w.s2 + row * (K / 16) + 16 * sb + 8 * h);
   f.d = ld_u16(w.s3 + 2 * (row * (K / 256) + sb));
   return f;
 }
@@ -115,9 +115,9 @@ template <>
 __device__ __forceinline__ Frag<QT_Q8_0> load_unit<QT_Q8_0>(const QMat& w, int row, int u) {
   const size_t K = (size_t)w.k;
   Frag<QT_Q8_0> f;
-  const uint4* q = (const uint4*)(w.s0 + row * K + 32 * u);
-  f.q0 = q[0];
-  f.q1 = q[1];
+  const uint8_t* q = w.s0 + row * K + 32 * u;
+  f.q0 = ldg4(q);
+  f.q1 = ldg4(q + 16);
   f.d = ld_u16(w.s1 + 2 * (row * (K / 32) + u));
   return f;
 }
@@ -125,8 +125,8 @@ template <>
 __device__ __forceinline__ Frag<QT_Q5_0> load_unit<QT_Q5_0>(const QMat& w, int row, int u) {
   const size_t K = (size_t)w.k;
   Frag<QT_Q5_0> f;
-  f.qs = *(const uint4*)(w.s0 + row * (K / 2) + 16 * u);
-  f.qh = *(const uint32_t*)(w.s1 + 4 * (row * (K / 32) + u));
+  f.qs = ldg4(w.s0 + row * (K / 2) + 16 * u);
+  f.qh = ldg1(w.s1 + 4 * (row * (K / 32) + u));
   f.d = ld_u16(w.s2 + 2 * (row * (K / 32) + u));
   return f;
 }
@@ -134,8 +134,8 @@ template <>
 __device__ __forceinline__ Frag<QT_Q5_1> load_unit<QT_Q5_1>(const QMat& w, int row, int u) {
   const size_t K = (size_t)w.k;
   Frag<QT_Q5_1> f;
-  f.qs = *(const uint4*)(w.s0 + row * (K / 2) + 16 * u);
-  f.qh = *(const uint32_t*)(w.s1 + 4 * (row * (K / 32) + u));
+  f.qs = ldg4(w.s0 + row * (K / 2) + 16 * u);
+  f.qh = ldg1(w.s1 + 4 * (row * (K / 32) + u));
   f.d = ld_u16(w.s2 + 2 * (row * (K / 32) + u));
   f.m = ld_u16(w.s3 + 2 * (row * (K / 32) + u));
   return f;

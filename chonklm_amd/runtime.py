@@ -99,6 +99,17 @@ class LlamaWgslEngine:
         check(lib().chonk_engine_read_logits(self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size), self._h)
         return out
 
+    def profile_step(self) -> list[tuple[str, float]]:
+        """Persistent step only: (phase, microseconds from the step's start to the
+        phase's last workgroup finishing) for one decode step."""
+        n_layers = self.info["layers"]
+        names = [f"L{i}.{p}" for i in range(n_layers) for p in ("qkv", "attn", "oproj", "gateup", "down")]
+        names.append("lmhead")
+        out = (C.c_double * len(names))()
+        n = C.c_int32()
+        check(lib().chonk_engine_profile_step(self._h, out, len(names), C.byref(n)), self._h)
+        return list(zip(names, list(out)[: n.value]))
+
     def read_buffer(self, which: int) -> np.ndarray:
         i = self.info
         sizes = {0: i["hidden"] * 4, 1: i["heads"] * i["head_dim"] * 4, 2: ((i["vocab"] + 255) // 256) * 8,

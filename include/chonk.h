@@ -84,7 +84,8 @@ typedef struct {
   int32_t qk_norm, interleaved_rope, kv_dtype;
   uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
   uint64_t device_bytes;            /* device memory held by the engine */
-  int32_t kernels_per_step;         /* kernel launches in one decode step */
+  int32_t kernels_per_step;         /* per-phase kernels of one decode step (chonk_engine_bench_kernel ids) */
+  int32_t persistent_step;          /* 1: a step runs as one persistent kernel launch */
 } chonk_engine_info;
 
 typedef struct {
@@ -171,6 +172,11 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
  * bytes per launch. */
 int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
                               size_t name_len, uint64_t* bytes);
+/* Persistent step only: runs one decode step with per-phase time stamps and
+ * returns, per phase (q|k|v, attention, o_proj, gate|up, down per layer, then
+ * lm_head), the time from the first workgroup's start to the last workgroup's
+ * end of that phase, in microseconds (the step's state is restored). */
+int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases);
 /* Writes `pos` synthetic positions into the K/V cache and sets the position,
  * so that long-context decode can be measured without a full prefill. */
 int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed);
