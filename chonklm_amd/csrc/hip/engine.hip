@@ -295,7 +295,6 @@ struct chonk_engine {
   int step_group = 0;
   void* tagged = nullptr;          // tagged activations, epoch and done counter (device memory)
   StepPhase* d_phases = nullptr;   // phase table (device memory)
-  void* step_uncached = nullptr;   // per-layer attention arrival counters (uncached pool)
   tagged_t *t_resid = nullptr, *t_attn = nullptr, *t_qkv = nullptr;  // last layer's buffers (readback)
   std::vector<std::string> phase_names;  // persistent step phases (profiling)
   StepDebug* step_dbg = nullptr;   // abort record of the persistent step
@@ -739,8 +738,12 @@ bool build_step(chonk_engine* e) {
       step_shared_bytes(std::max(H, std::max(qdim, F)), 0, G, c.hd, e->chunk, e->nchunk, (int)e->kv_elem);
   if (shmem > lds_limit() || step_occupancy(G, kv16, shmem) < 1) return false;
 
-  // tagged buffers: R0 | RFIN | per layer QKV, ATT, RMID, FF, REND, DO, DD | epoch, done
-  const size_t per_layer = (size_t)(qdim + 2 * kvdim) + qdim + H + F + H + (c.gemma ? 2 * H : 0);
+  // tagged buffers: R0 | RFIN | per layer QKV, ATT, RMID, FF, REND, DO, DD, attention partials | epoch, done
+  // (a partial row is written and read once per step, so a workgroup that
+  // merges several layers never meets a row it has read before)
+  const size_t rowf = (size_t)attn_rowf(G, c.hd);
+  const size_t part_layer = (size_t)c.kv_heads * e->nchunk * rowf;  // words
+  const size_t per_layer = (size_t)(qdim + 2 * kvdim) + qdim + H + F + H + (c.gemma ? 2 * H : 0) + part_layer;
   const size_t dbg_words = (sizeof(StepDebug) + 7) / 8;
   const size_t words = 2 * (size_t)H + per_layer * NL + 2 + dbg_words;
   HIP_OK(hipMalloc(&e->tagged, words * sizeof(tagged_t)));
@@ -754,7 +757,7 @@ bool build_step(chonk_engine* e) {
   tagged_t* r0 = take(H);
   tagged_t* rfin = take(H);
   struct TL {
-    tagged_t *qkv, *att, *rmid, *ff, *rend, *d_o, *d_down;
+    tagged_t *qkv, *att, *rmid, *ff, *rend, *d_o, *d_down, *part;
   };
   std::vector<TL> tl((size_t)NL);
   for (int i = 0; i < NL; ++i) {
@@ -765,24 +768,13 @@ bool build_step(chonk_engine* e) {
     tl[i].rend = take(H);
     tl[i].d_o = c.gemma ? take(H) : nullptr;
     tl[i].d_down = c.gemma ? take(H) : nullptr;
+    tl[i].part = take(part_layer);
   }
   uint32_t* epoch = (uint32_t*)take(1);
   uint32_t* done = (uint32_t*)take(1);
   e->step_dbg = (StepDebug*)take(dbg_words);
   const uint32_t one = 1;
   HIP_OK(hipMemcpy(epoch, &one, 4, hipMemcpyHostToDevice));
-  // per-layer attention arrival counters and chunk partials: within one step a
-  // partial row is written and read exactly once, so a workgroup that merges
-  // several layers never meets a row it has read before (its vector L1 is only
-  // invalidated at kernel start)
-  const size_t rowf = ((size_t)G * (c.hd + 2) + 3) & ~(size_t)3;
-  const size_t part_layer = (size_t)c.kv_heads * e->nchunk * rowf;  // floats
-  const size_t cnt_bytes = align256((size_t)NL * c.kv_heads * 4);
-  e->step_uncached = uncached_pool().take(e->device, cnt_bytes + (size_t)NL * part_layer * 4);
-  uint32_t* cnt = (uint32_t*)e->step_uncached;
-  float* parts = (float*)((uint8_t*)e->step_uncached + cnt_bytes);
-  HIP_OK(hipMemset(cnt, 0, (size_t)NL * c.kv_heads * 4));
-
   std::vector<StepPhase> ph;
   auto seg = [&](MvSeg& sg, const QMat& w, int n_out, int tile, int first) {
     sg.w = w;
@@ -830,16 +822,17 @@ bool build_step(chonk_engine* e) {
       }
       ph.push_back(p);
     }
-    {  // attention: the per-phase kernel's arguments with per-layer counters
+    {  // attention: the per-phase kernel's arguments with per-layer tagged partials
       StepPhase p{};
       p.kind = PH_ATTN;
       for (const Launch& L : e->kernels_logits)
         if (L.kind == Launch::ATTN && L.layer == i) p.at = L.at;
-      p.at.cnt = cnt + (size_t)i * c.kv_heads;
-      p.at.part = parts + (size_t)i * part_layer;
+      p.at.cnt = nullptr;
+      p.at.part = nullptr;
       p.n_tasks = c.kv_heads * e->nchunk;
       p.qkv_in = tl[i].qkv;
       p.attn_out = tl[i].att;
+      p.tpart = tl[i].part;
       ph.push_back(p);
     }
     {  // o projection
@@ -1002,7 +995,6 @@ void engine_free(chonk_engine* e) {
   e->weights.release();
   e->state.release();
   uncached_pool().give_back(e->device, e->uncached);
-  if (e->step_uncached) uncached_pool().give_back(e->device, e->step_uncached);
   if (e->tagged) (void)hipFree(e->tagged);
   if (e->d_phases) (void)hipFree(e->d_phases);
   if (e->h_state) (void)hipHostFree(e->h_state);

@@ -128,6 +128,168 @@ struct SegView {
   int n_out, tile, lpr, wg_begin;
 };
 
+// ---- matvec core (k_mv_* and the persistent step) --------------------------------
+
+// LDS of the integer-digit form of x at `base`: three digit planes of K bytes,
+// then bsc[K/32] and xs8[K/8] (3.625 K bytes in all); xs16[K/16] lies apart.
+__device__ __forceinline__ XqView xq_view(void* base, float* xs16, int K) {
+  XqView v;
+  v.plane = (const int8_t*)base;
+  v.bsc = (const float*)((char*)base + 3 * K);
+  v.xs8 = v.bsc + K / 32;
+  v.xs16 = xs16;
+  v.k = K;
+  return v;
+}
+
+// Fills the digit planes, block scales and run sums of x (fp32 in LDS, K a
+// multiple of 32). Called by all threads after a barrier that follows the last
+// write of x; a barrier must separate it from the first read of the planes.
+__device__ __forceinline__ void quantize_x(const float* xs, int K, void* base, float* xs16) {
+  int8_t* plane = (int8_t*)base;
+  float* bsc = (float*)((char*)base + 3 * K);
+  float* xs8 = bsc + K / 32;
+  // 8 consecutive threads cover one 32-element block (K / 4 is a multiple of 8)
+  for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg) {
+    const float4 v = reinterpret_cast<const float4*>(xs)[i4];
+    const float m = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    int e = 0;
+    (void)frexpf(m, &e);  // m < 2^e, so |x| * 2^(22-e) < 2^22
+    const int sh = min(22 - e, 126);
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = (int)rintf(ldexpf(vv[i], sh));
+      const int d0 = (int)(int8_t)q;
+      const int r1 = (q - d0) >> 8;
+      const int d1 = (int)(int8_t)r1;
+      const int d2 = (r1 - d1) >> 8;  // |d2| <= 65
+      w0 |= ((uint32_t)d0 & 255u) << (8 * i);
+      w1 |= ((uint32_t)d1 & 255u) << (8 * i);
+      w2 |= ((uint32_t)d2 & 255u) << (8 * i);
+    }
+    reinterpret_cast<uint32_t*>(plane)[i4] = w0;
+    reinterpret_cast<uint32_t*>(plane + K)[i4] = w1;
+    reinterpret_cast<uint32_t*>(plane + 2 * K)[i4] = w2;
+    const float s4 = (v.x + v.y) + (v.z + v.w);
+    const float s8 = s4 + dpp<0xb1>(s4);
+    const float s16 = s8 + dpp<0x4e>(s8);
+    if ((i4 & 1) == 0) xs8[i4 >> 1] = s8;
+    if ((i4 & 3) == 0) xs16[i4 >> 2] = s16;
+    // a non-finite block poisons its products as the fp32 sum would
+    if ((i4 & 7) == 0) bsc[i4 >> 3] = __builtin_isfinite(m) ? ldexpf(1.0f, -sh) : __int_as_float(0x7fc00000);
+  }
+}
+
+// A lane's share of a matvec task: lane group lg (of ng groups of lpr lanes)
+// owns virtual rows lg, lg + ng, ... (GLU: even rows gate, odd rows up); lane
+// li owns units li, li + lpr, ... of each row.
+struct MvLane {
+  int U, lpr, ng, lg, li, rows, ucount, t0;
+  bool glu;
+};
+
+__device__ __forceinline__ MvLane mv_lane(const SegView& g, int t0, int nt, bool glu) {
+  MvLane m;
+  m.U = g.w.k >> 5;
+  m.lpr = g.lpr;
+  const int shift = __builtin_ctz((unsigned)m.lpr);
+  m.ng = kWg >> shift;
+  m.lg = threadIdx.x >> shift;
+  m.li = threadIdx.x & (m.lpr - 1);
+  const int nv = nt > 0 ? (glu ? 2 * nt : nt) : 0;
+  m.rows = m.lg < nv ? (nv - m.lg + m.ng - 1) / m.ng : 0;
+  m.ucount = (m.U + m.lpr - 1) / m.lpr;
+  m.t0 = t0;
+  m.glu = glu;
+  return m;
+}
+
+// The lane walks its rows in batches of RB rows x UC units; the UC units' x
+// stays in registers for all rows. Fragments of the next batch are in flight
+// while the current one is reduced.
+template <int T, int UC>
+struct MvShape {
+  static constexpr int kPf = sizeof(Frag<T>) > 40 ? 2 : 4;
+  static constexpr int RB = kPf / UC > 0 ? kPf / UC : 1;
+  static constexpr int N = RB * UC;
+};
+
+// units held in registers per lane: 1 or 2 (more are walked in blocks of 2)
+__device__ __forceinline__ int mv_uc(const SegView& g) { return (g.w.k >> 5) <= g.lpr ? 1 : 2; }
+
+// Issues the weight loads of batch b (unit block jb, rows [rb*RB, rb*RB+RB)).
+template <int T, int UC>
+__device__ __forceinline__ void mv_fetch(const SegView& g, const MvLane& m, int b, Frag<T> (&f)[MvShape<T, UC>::N]) {
+  constexpr int RB = MvShape<T, UC>::RB;
+  const int nrb = max(1, (m.rows + RB - 1) / RB);
+  const int jb = b / nrb, rb = b - jb * nrb;
+#pragma unroll
+  for (int rr = 0; rr < RB; ++rr) {
+    const int r = rb * RB + rr;
+    const int v = m.lg + r * m.ng;
+#pragma unroll
+    for (int j = 0; j < UC; ++j) {
+      // past the last batch u >= U, so nothing is loaded
+      const int u = m.li + (jb * UC + j) * m.lpr;
+      if (r < m.rows && u < m.U) {
+        QMat w = g.w;
+        if (m.glu && (v & 1)) {
+          w.s0 = g.u0;
+          w.s1 = g.u1;
+          w.s2 = g.u2;
+          w.s3 = g.u3;
+        }
+        f[rr * UC + j] = load_unit<T>(w, m.t0 + (m.glu ? (v >> 1) : v), u);
+      }
+    }
+  }
+}
+
+// Dot products of the lane's rows once the digit planes are ready; cur holds
+// batch 0 (issued by mv_fetch before the input was). Row r's sum lands in
+// res[lg + r * ng].
+template <int T, int UC>
+__device__ __forceinline__ void mv_stream(const SegView& g, const MvLane& m, const XqView& x, float* res,
+                                          Frag<T> (&cur)[MvShape<T, UC>::N]) {
+  constexpr int RB = MvShape<T, UC>::RB, N = MvShape<T, UC>::N;
+  const int nrb = max(1, (m.rows + RB - 1) / RB);
+  const int nb = m.rows > 0 ? nrb * ((m.ucount + UC - 1) / UC) : 0;
+  XU xr[UC];
+  for (int b = 0; b < nb; ++b) {
+    const int jb = b / nrb, rb = b - jb * nrb;
+    if (rb == 0) {
+#pragma unroll
+      for (int j = 0; j < UC; ++j) {
+        const int u = m.li + (jb * UC + j) * m.lpr;
+        if (u < m.U) load_xu<T>(x, u, xr[j]);
+      }
+    }
+    Frag<T> nxt[N];
+    mv_fetch<T, UC>(g, m, b + 1, nxt);
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr) {
+      const int r = rb * RB + rr;
+      if (r < m.rows) {  // uniform in the lane group
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < UC; ++j) {
+          const int u = m.li + (jb * UC + j) * m.lpr;
+          if (u < m.U) acc += dot_q<T>(cur[rr * UC + j], u, xr[j]);
+        }
+        acc = group_sum_n(acc, m.lpr);
+        if (m.li == 0) {
+          float* d = res + m.lg + r * m.ng;
+          *d = jb == 0 ? acc : *d + acc;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < N; ++q) cur[q] = nxt[q];
+  }
+}
+
 constexpr int kMaxG = 8;
 
 __host__ __device__ constexpr int attn_tpp(int hd) { return hd / 64 > 2 ? hd / 64 : 2; }
@@ -236,15 +398,18 @@ __device__ __forceinline__ void v_walk(const void* tile, int hd, int d0, int pa,
   }
 }
 
-// Phases B-D and the merge of the decode attention for (kv head kv, chunk c)
-// at position pos, once the group's q heads, the new k/v, the norm weights
-// and the rotary table are in LDS, the chunk's valid V rows are in the LDS
-// tile and this thread's K slice is in kreg (layout of k_attention). The
-// last chunk of the head to arrive stores merged output element i of the
-// group (i = g * hd + d) with out(i, value).
-template <int G, bool KV16, class Out>
-__device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int kv, int c, int pos,
-                                             uint4 (&kreg)[KV16 ? 8 : 16], uint32_t* s_last, Out out) {
+// LDS layout of the decode attention (floats): q_s[G][hd] | k_new[hd] |
+// v_new[hd] | qn[hd] | kn[hd] | inv[hd] | wpart[4][G][hd] | wml[4][kMaxG][2] |
+// wts[G][ncp] | cpart[rowf] | tile (V rows, later merge staging).
+
+// Phases B-D of the decode attention for (kv head kv, chunk c) at position
+// pos, once the group's q heads, the new k/v, the norm weights and the rotary
+// table are in LDS, the chunk's valid V rows are in the LDS tile and this
+// thread's K slice is in kreg (layout of k_attention). Leaves the chunk
+// partial in cpart: for head g at g * (hd + 2), [max, sum, acc[hd]].
+template <int G, bool KV16>
+__device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv, int c, int pos,
+                                           uint4 (&kreg)[KV16 ? 8 : 16]) {
   const int hd = a.hd, half = hd / 2, CH = a.chunk;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -265,7 +430,8 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int k
   float* wpart = inv + hd;
   float* wml = wpart + 4 * G * hd;
   float* wts = wml + 8 * kMaxG;
-  float* tile = wts + G * ncp;
+  float* cpart = wts + G * ncp;
+  float* tile = cpart + attn_rowf(G, hd);
   const size_t head_base = (size_t)kv * a.ctx * hd;
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
   const int c_lo = start / CH, c_hi = pos / CH;
@@ -414,8 +580,6 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int k
   __syncthreads();
 
   // D: chunk partial = the four wave partials rescaled to the chunk maximum
-  const int rowf = (G * (hd + 2) + 3) & ~3;  // floats per chunk partial, 16-byte multiple
-  float* part = a.part + (size_t)(kv * a.nchunk + c) * rowf;
   for (int i = tid; i < G * hd; i += kWg) {
     const int gg = i / hd, d = i - gg * hd;
     float M = -INFINITY;
@@ -427,7 +591,7 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int k
       const float mw = wml[(w * kMaxG + gg) * 2];
       if (mw != -INFINITY) acc += wpart[(w * G + gg) * hd + d] * expf(mw - M);
     }
-    *gblw(part + gg * (hd + 2) + 2 + d) = acc;
+    cpart[gg * (hd + 2) + 2 + d] = acc;
   }
   if (tid < G) {
     float M = -INFINITY, L = 0.f;
@@ -438,9 +602,32 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int k
       const float mw = wml[(w * kMaxG + tid) * 2];
       if (mw != -INFINITY) L += wml[(w * kMaxG + tid) * 2 + 1] * expf(mw - M);
     }
-    *gblw(part + tid * (hd + 2)) = M;
-    *gblw(part + tid * (hd + 2) + 1) = L;
+    cpart[tid * (hd + 2)] = M;
+    cpart[tid * (hd + 2) + 1] = L;
   }
+  __syncthreads();
+}
+
+// attn_chunk, then the chunk partial to uncached memory; the last chunk of the
+// head to arrive (arrival counter a.cnt[kv]) merges all of them and stores
+// output element i of the group (i = g * hd + d) with out(i, value).
+template <int G, bool KV16, class Out>
+__device__ __forceinline__ void attn_compute(const AttnArgs& a, float* sm, int kv, int c, int pos,
+                                             uint4 (&kreg)[KV16 ? 8 : 16], uint32_t* s_last, Out out) {
+  attn_chunk<G, KV16>(a, sm, kv, c, pos, kreg);
+  const int hd = a.hd, CH = a.chunk;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ncp = (a.nchunk + 3) & ~3;
+  float* wml = sm + (5 * G + 5) * hd;
+  float* wts = wml + 8 * kMaxG;
+  const float* cpart = wts + G * ncp;
+  float* tile = (float*)cpart + attn_rowf(G, hd);
+  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+  const int c_lo = start / CH, c_hi = pos / CH;
+  const int rowf = attn_rowf(G, hd);  // floats per chunk partial, 16-byte multiple
+  float* part = a.part + (size_t)(kv * a.nchunk + c) * rowf;
+  for (int i = tid; i < G * (hd + 2); i += kWg) *gblw(part + i) = cpart[i];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {

@@ -87,6 +87,10 @@ struct AttnArgs {
   float eps, scale;
 };
 
+// Floats (or tagged words) per attention chunk partial: per head [max, sum,
+// acc[hd]], padded to a 16-byte multiple.
+__host__ __device__ constexpr int attn_rowf(int G, int hd) { return (G * (hd + 2) + 3) & ~3; }
+
 struct SelArgs {
   const Candidate* cand;
   int32_t groups;
@@ -131,11 +135,13 @@ struct StepPhase {
   const tagged_t* add;     // EPI_ADD: residual input [n_out]
   tagged_t* tout[3];       // per-segment tagged outputs (EPI_STORE / EPI_ADD / EPI_GLU_*)
   float* logits;           // EPI_LOGITS: plain logits [vocab]
-  // PH_ATTN: one task per (kv head, chunk); q|k|v come from qkv_in, the merged
-  // output goes to attn_out
+  // PH_ATTN: one task per (kv head, chunk); q|k|v come from qkv_in. Every
+  // chunk but the newest stores its partial in tpart ([kv][nchunk] rows of
+  // attn_rowf words); the newest chunk's task merges them into attn_out.
   AttnArgs at;
   const tagged_t* qkv_in;
   tagged_t* attn_out;
+  tagged_t* tpart;
 };
 
 // Record of the first wait that exceeded its time bound (diagnostics).

@@ -76,8 +76,39 @@ __device__ __forceinline__ MvLds mv_lds(float* smem, int K) {
   return l;
 }
 
+// The prologue's inputs, copied out of the kernel arguments once: every typed
+// variant of the matvec inlines the prologue, and reading the argument block
+// from all of them makes the compiler stage the whole block in scratch.
+struct MvPro {
+  const float *in, *delta, *w_delta, *w_norm;
+  float* res_out;
+  QMat embed;
+  const int32_t* hist;
+  DevState* st;
+  float embed_scale, eps;
+  int32_t pro, k, vocab;
+};
+
+__device__ __forceinline__ MvPro mv_pro(const MvArgs& a) {
+  MvPro p;
+  p.in = a.in;
+  p.delta = a.delta;
+  p.w_delta = a.w_delta;
+  p.w_norm = a.w_norm;
+  p.res_out = a.res_out;
+  p.embed = a.embed;
+  p.hist = a.hist;
+  p.st = a.st;
+  p.embed_scale = a.embed_scale;
+  p.eps = a.eps;
+  p.pro = a.pro;
+  p.k = a.k;
+  p.vocab = a.vocab;
+  return p;
+}
+
 // Issues the activation loads of the prologue (no waiting).
-__device__ __forceinline__ void mv_stage(const MvArgs& a, const MvLds& l) {
+__device__ __forceinline__ void mv_stage(const MvPro& a, const MvLds& l) {
   const int K = a.k;
   switch (a.pro) {
     case PRO_PLAIN: lds_dma(a.in, l.xs, K); break;
@@ -99,7 +130,7 @@ __device__ __forceinline__ void mv_stage(const MvArgs& a, const MvLds& l) {
 
 // Completes the prologue once the staged data has landed: xs becomes the
 // matvec input (normalised as the mode requires), xs16 its 16-element sums.
-__device__ void mv_finish(const MvArgs& a, const MvLds& l) {
+__device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
   const int K = a.k, tid = threadIdx.x;
   float* xs = l.xs;
   if (a.pro == PRO_EMBED_NORM) {
@@ -141,84 +172,24 @@ __device__ void mv_finish(const MvArgs& a, const MvLds& l) {
     for (int i = tid; i < K; i += kWg) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), l.wn[i]);
     __syncthreads();
   }
-  for (int j = tid; j < K / 16; j += kWg) {
-    const float4* p = (const float4*)(xs + 16 * j);
-    const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-    l.xs16[j] = ((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w)) +
-                ((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w));
-  }
+  quantize_x(xs, K, l.dl, l.xs16);  // dl / wd are free from here on
   __syncthreads();
 }
 
 // Rows [t0, t0 + nt) of the segment (2*nt interleaved gate/up rows when GLU).
-// Lane group lg of `lpr` lanes owns virtual rows lg, lg+ng, ...; lane li owns
-// units li, li+lpr, ... of each row. The lane's (row, unit) items are walked
-// row-major in batches of kPf fragments: the first batch is issued together
-// with the activation staging (weights do not depend on it) and each later
-// batch is loaded while the previous one is being reduced.
-template <int T, bool GLU>
-__device__ __forceinline__ bool mv_work(const MvArgs& a, const SegView& g, int t0, int nt, const MvLds& l) {
-  // prefetch depth: 4 fragments of <= 9 dwords, 2 of the larger Q5_K ones
-  constexpr int kPf = sizeof(Frag<T>) > 40 ? 2 : 4;
-  const int U = g.w.k >> 5;
-  const int lpr = g.lpr;
-  const int shift = __builtin_ctz((unsigned)lpr);
-  const int ng = kWg >> shift;
-  const int lg = threadIdx.x >> shift, li = threadIdx.x & (lpr - 1);
-  const int nv = nt > 0 ? (GLU ? 2 * nt : nt) : 0;
-  const int rows_lane = lg < nv ? (nv - lg + ng - 1) / ng : 0;
-  const int ucount = (U + lpr - 1) / lpr;  // units per lane (uniform in a lane group)
-  const int items = rows_lane * ucount;
-
-  auto load_item = [&](int ii, Frag<T>& f) {
-    const int r = ii / ucount, j = ii - r * ucount;
-    const int v = lg + r * ng, u = li + j * lpr;
-    if (ii < items && u < U) {
-      QMat m = g.w;
-      if (GLU && (v & 1)) {
-        m.s0 = g.u0;
-        m.s1 = g.u1;
-        m.s2 = g.u2;
-        m.s3 = g.u3;
-      }
-      f = load_unit<T>(m, t0 + (GLU ? (v >> 1) : v), u);
-    }
-  };
-
-  mv_stage(a, l);
-  Frag<T> cur[kPf];
-#pragma unroll
-  for (int q = 0; q < kPf; ++q) load_item(q, cur[q]);
+// The first weight batch is issued right after the activation staging
+// (weights do not depend on it); mv_stream walks the rest.
+template <int T, int UC, bool GLU>
+__device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0, int nt, const MvLds& l) {
+  const MvLane m = mv_lane(g, t0, nt, GLU);
+  Frag<T> cur[MvShape<T, UC>::N];
+  mv_fetch<T, UC>(g, m, 0, cur);
   const int stopped = __hip_atomic_load(&a.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (stopped) return false;
   mv_finish(a, l);
-
-  const float* xs = l.xs;
-  const float* xs16 = l.xs16;
-  float acc = 0.f;
-  for (int base = 0; base < items; base += kPf) {
-    Frag<T> nxt[kPf];
-#pragma unroll
-    for (int q = 0; q < kPf; ++q) load_item(base + kPf + q, nxt[q]);
-#pragma unroll
-    for (int q = 0; q < kPf; ++q) {
-      const int ii = base + q;
-      if (ii < items) {
-        const int r = ii / ucount, j = ii - r * ucount;
-        const int u = li + j * lpr;
-        if (u < U) acc += dot_unit<T>(cur[q], u, xs, xs16);
-        if (j == ucount - 1) {
-          acc = group_sum_n(acc, lpr);
-          if (li == 0) l.res[lg + r * ng] = acc;
-          acc = 0.f;
-        }
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kPf; ++q) cur[q] = nxt[q];
-  }
+  mv_stream<T, UC>(g, m, xq_view(l.dl, l.xs16, a.k), l.res, cur);
   return true;
 }
 
@@ -233,7 +204,16 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   // the type is uniform per workgroup, so every thread takes the same branch
   // (the staging and prologue inside hold barriers)
   bool live = false;
-  with_type(g.w.type, [&]<int T>() { live = mv_work<T, glu>(a, g, t0, nt, l); });
+  const MvPro p = mv_pro(a);
+  mv_stage(p, l);
+  const int uc = mv_uc(g);
+  with_type(g.w.type, [&]<int T>() {
+    if (uc == 1) {
+      live = mv_work<T, 1, glu>(p, g, t0, nt, l);
+    } else {
+      live = mv_work<T, 2, glu>(p, g, t0, nt, l);
+    }
+  });
   if (!live) return;
   __syncthreads();
 
@@ -340,7 +320,8 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   float* wpart = inv + hd;         // [4][G][hd] wave partials
   float* wml = wpart + 4 * G * hd; // [4][kMaxG][2] wave (max, sum)
   float* wts = wml + 8 * kMaxG;    // [G][ncp] merge weights
-  float* tile = wts + G * ncp;     // V rows [CH][hd] (kElem bytes each), later merge staging
+  // wts + G * ncp: [rowf] this chunk's partial
+  float* tile = wts + G * ncp + attn_rowf(G, hd);  // V rows [CH][hd] (kElem bytes each), later merge staging
   __shared__ uint32_t s_last;
 
   const float* kraw = a.qkv + a.heads * hd;
@@ -461,14 +442,14 @@ size_t mv_shared_bytes(int k, int max_tile_rows) {
 
 int attn_merge_floats(int group, int hd, int nchunk) {
   // stage up to 32 KiB of chunk partials per batch; the V tile area is reused
-  const int rowf = (group * (hd + 2) + 3) & ~3;
+  const int rowf = attn_rowf(group, hd);
   return std::min(nchunk * rowf, std::max(8192, rowf));
 }
 
 size_t attn_shared_bytes(int group, int hd, int chunk, int nchunk, int kv_elem) {
   const size_t tile = std::max((size_t)chunk * hd * kv_elem / 4, (size_t)attn_merge_floats(group, hd, nchunk));
   const size_t ncp = ((size_t)nchunk + 3) & ~(size_t)3;
-  return sizeof(float) * ((size_t)(5 * group + 5) * hd + 8 * kMaxG + (size_t)group * ncp + tile);
+  return sizeof(float) * ((size_t)(5 * group + 5) * hd + 8 * kMaxG + (size_t)group * ncp + attn_rowf(group, hd) + tile);
 }
 
 int attn_max_chunk(int hd) { return kWg / attn_tpp(hd); }

@@ -3,14 +3,15 @@
 // For every GGUF type there is
 //   * Frag<T>            the raw bytes of one unit (loaded with vector loads),
 //   * load_unit<T>()     issues the loads for (row, unit),
-//   * dot_unit<T>()      sum_i x[k_i] * w_i over the unit's 32 elements,
+//   * load_xu<T>() / dot_q<T>()  sum_i x[k_i] * w_i over the unit's 32 elements
+//                        against the integer-digit form of x (XqView),
 //   * dequant_unit<T>()  the 32 weights, bit-exact with the reference decode.
 //
 // Element placement inside a unit, and the exact fp32 operation order used by
 // dequant_unit, follow the reference's WGSL weight helpers
 // (src/lib/llama-wgsl-runtime.ts: q5_0 :2230-2246, q5_1 :2280-2289,
 // q8_0 :2321-2327, q4_k :2378-2410, q5_k :2479-2495, q6_k :2560-2580), which
-// in turn follow llama.cpp's dequantize_row_* block formats. dot_unit uses the
+// in turn follow llama.cpp's dequantize_row_* block formats. dot_q uses the
 // factored form d*sc*sum(x*q) - dmin*m*sum(x) and is only required to match
 // within fp32 rounding.
 #pragma once
@@ -157,147 +158,214 @@ __device__ __forceinline__ int unit_col(int u, int e) {
   }
 }
 
-// ---- dot products ------------------------------------------------------------
-// xs: activations in LDS; xs16: sums of xs over aligned 16-element runs.
+// ---- dot products --------------------------------------------------------------
+// The matvec input x is re-expressed per aligned 32-element block as integers
+// q = rint(x * 2^sh) with |q| <= 2^22, sh chosen from the block's largest |x|,
+// held as three planes of balanced base-256 digits (q = d0 + 256 d1 + 65536 d2,
+// each digit an int8). Dot products of the integer weight codes with the digit
+// planes are exact in int32 (v_dot4_i32_i8, four products per instruction);
+// one conversion per 8-16 elements brings them back to fp32. The representation
+// error is <= 2^-22 of the block's largest |x|, the order of fp32 rounding of
+// the reference's own sum.
+struct XqView {
+  const int8_t* plane;  // digit plane p at plane + p * k
+  const float* bsc;     // [k/32] 2^-sh of each block
+  const float* xs16;    // [k/16] fp32 sums of x over aligned 16-element runs
+  const float* xs8;     // [k/8]  fp32 sums of x over aligned 8-element runs
+  int k;
+};
+
+// x for one 32-element unit: digit words w[plane][word] (4 elements per word,
+// in the order the type's dot consumes them) and per-run scales and sums.
+struct XU {
+  int w[3][8];
+  float b[4];  // 2^-sh of the runs' blocks
+  float s[4];  // fp32 sums of x over the runs
+};
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// d0 + 256 d1 + 65536 d2 in fp32 (|d1 * 256 + d0| stays far inside int32)
+__device__ __forceinline__ float digits_f(int a0, int a1, int a2) {
+  return fmaf((float)a2, 65536.0f, (float)(a1 * 256 + a0));
+}
+
+__device__ __forceinline__ void ld_words4(const int8_t* p, int k, int off, XU& x, int at) {
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl) {
+    const int4 v = *(const int4*)(p + pl * k + off);
+    x.w[pl][at] = v.x;
+    x.w[pl][at + 1] = v.y;
+    x.w[pl][at + 2] = v.z;
+    x.w[pl][at + 3] = v.w;
+  }
+}
+__device__ __forceinline__ void ld_words2(const int8_t* p, int k, int off, XU& x, int at) {
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl) {
+    const int2 v = *(const int2*)(p + pl * k + off);
+    x.w[pl][at] = v.x;
+    x.w[pl][at + 1] = v.y;
+  }
+}
+
 template <int T>
-__device__ __forceinline__ float dot_unit(const Frag<T>& f, int u, const float* xs, const float* xs16);
-
-template <>
-__device__ __forceinline__ float dot_unit<QT_Q4_K>(const Frag<QT_Q4_K>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  const int sb = u >> 3, c = u & 7, g = c >> 1, hh = c & 1;
-  const int base = sb * 256 + 64 * g + 16 * hh;
-  const float4* xl = (const float4*)(xs + base);
-  const float4* xh = (const float4*)(xs + base + 32);
-  const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
-  float lo = 0.f, hi = 0.f;
+__device__ __forceinline__ void load_xu(const XqView& x, int u, XU& r) {
+  if constexpr (T == QT_Q4_K || T == QT_Q5_K) {
+    // elements base + [0,16) (sub-block 2g) and base + 32 + [0,16) (sub-block 2g+1)
+    const int sb = u >> 3, c = u & 7, g = c >> 1, hh = c & 1;
+    const int base = sb * 256 + 64 * g + 16 * hh;
+    ld_words4(x.plane, x.k, base, r, 0);
+    ld_words4(x.plane, x.k, base + 32, r, 4);
+    r.b[0] = x.bsc[base >> 5];
+    r.b[1] = x.bsc[(base >> 5) + 1];
+    r.s[0] = x.xs16[base >> 4];
+    r.s[1] = x.xs16[(base >> 4) + 2];
+  } else if constexpr (T == QT_Q6_K) {
+    // four 8-element runs base + 32 qd + [0,8)
+    const int sb = u >> 3, c = u & 7, h = c >> 2, b = c & 3;
+    const int base = sb * 256 + 128 * h + 8 * b;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const float4 a = xl[v], b = xh[v];
-    lo += a.x * nib_lo(q[v], 0) + a.y * nib_lo(q[v], 1) + a.z * nib_lo(q[v], 2) + a.w * nib_lo(q[v], 3);
-    hi += b.x * nib_hi(q[v], 0) + b.y * nib_hi(q[v], 1) + b.z * nib_hi(q[v], 2) + b.w * nib_hi(q[v], 3);
-  }
-  uint32_t sc0, m0, sc1, m1;
-  scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
-  scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
-  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
-  const float s_lo = xs16[base >> 4], s_hi = xs16[(base >> 4) + 2];
-  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * s_lo + (float)m1 * s_hi);
-}
-
-template <>
-__device__ __forceinline__ float dot_unit<QT_Q5_K>(const Frag<QT_Q5_K>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  const int sb = u >> 3, c = u & 7, g = c >> 1, hh = c & 1;
-  const int base = sb * 256 + 64 * g + 16 * hh;
-  const float4* xl = (const float4*)(xs + base);
-  const float4* xh = (const float4*)(xs + base + 32);
-  const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
-  const uint32_t h[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
-  float lo = 0.f, hi = 0.f;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const float4 a = xl[v], b = xh[v];
-    float ql[4], qhv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t hb = (h[v] >> (8 * i)) & 0xffu;
-      ql[i] = (float)(((q[v] >> (8 * i)) & 15u) + (((hb >> (2 * g)) & 1u) << 4));
-      qhv[i] = (float)(((q[v] >> (8 * i + 4)) & 15u) + (((hb >> (2 * g + 1)) & 1u) << 4));
+    for (int qd = 0; qd < 4; ++qd) {
+      ld_words2(x.plane, x.k, base + 32 * qd, r, 2 * qd);
+      r.b[qd] = x.bsc[(base + 32 * qd) >> 5];
+      r.s[qd] = x.xs8[(base + 32 * qd) >> 3];
     }
-    lo += a.x * ql[0] + a.y * ql[1] + a.z * ql[2] + a.w * ql[3];
-    hi += b.x * qhv[0] + b.y * qhv[1] + b.z * qhv[2] + b.w * qhv[3];
+  } else {
+    // Q8_0 / Q5_0 / Q5_1: the 32 elements of block u
+    ld_words4(x.plane, x.k, 32 * u, r, 0);
+    ld_words4(x.plane, x.k, 32 * u + 16, r, 4);
+    r.b[0] = x.bsc[u];
+    r.s[0] = x.xs16[2 * u] + x.xs16[2 * u + 1];
   }
+}
+
+// sum over the unit of x * w (w dequantized), for the unit's fragment
+template <int T>
+__device__ __forceinline__ float dot_q(const Frag<T>& f, int u, const XU& x);
+
+template <>
+__device__ __forceinline__ float dot_q<QT_Q4_K>(const Frag<QT_Q4_K>& f, int u, const XU& x) {
+  const int g = (u & 7) >> 1;
+  const int q[4] = {(int)f.qs.x, (int)f.qs.y, (int)f.qs.z, (int)f.qs.w};
+  int l0 = 0, l1 = 0, l2 = 0, h0 = 0, h1 = 0, h2 = 0;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int wl = q[v] & 0x0f0f0f0f, wh = (q[v] >> 4) & 0x0f0f0f0f;
+    l0 = sdot4(wl, x.w[0][v], l0);
+    l1 = sdot4(wl, x.w[1][v], l1);
+    l2 = sdot4(wl, x.w[2][v], l2);
+    h0 = sdot4(wh, x.w[0][4 + v], h0);
+    h1 = sdot4(wh, x.w[1][4 + v], h1);
+    h2 = sdot4(wh, x.w[2][4 + v], h2);
+  }
+  const float lo = digits_f(l0, l1, l2) * x.b[0], hi = digits_f(h0, h1, h2) * x.b[1];
   uint32_t sc0, m0, sc1, m1;
   scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
   scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
   const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
-  const float s_lo = xs16[base >> 4], s_hi = xs16[(base >> 4) + 2];
-  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * s_lo + (float)m1 * s_hi);
+  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * x.s[0] + (float)m1 * x.s[1]);
 }
 
 template <>
-__device__ __forceinline__ float dot_unit<QT_Q6_K>(const Frag<QT_Q6_K>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  const int sb = u >> 3, c = u & 7, h = c >> 2, b = c & 3;
-  const int base = sb * 256 + 128 * h + 8 * b;
-  const uint32_t qa[2] = {f.qa.x, f.qa.y}, qb[2] = {f.qb.x, f.qb.y}, qh[2] = {f.qh.x, f.qh.y};
+__device__ __forceinline__ float dot_q<QT_Q5_K>(const Frag<QT_Q5_K>& f, int u, const XU& x) {
+  const int g = (u & 7) >> 1;
+  const int q[4] = {(int)f.qs.x, (int)f.qs.y, (int)f.qs.z, (int)f.qs.w};
+  const int h[4] = {(int)f.qh.x, (int)f.qh.y, (int)f.qh.z, (int)f.qh.w};
+  int l0 = 0, l1 = 0, l2 = 0, h0 = 0, h1 = 0, h2 = 0;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int wl = (q[v] & 0x0f0f0f0f) | (((h[v] >> (2 * g)) & 0x01010101) << 4);
+    const int wh = ((q[v] >> 4) & 0x0f0f0f0f) | (((h[v] >> (2 * g + 1)) & 0x01010101) << 4);
+    l0 = sdot4(wl, x.w[0][v], l0);
+    l1 = sdot4(wl, x.w[1][v], l1);
+    l2 = sdot4(wl, x.w[2][v], l2);
+    h0 = sdot4(wh, x.w[0][4 + v], h0);
+    h1 = sdot4(wh, x.w[1][4 + v], h1);
+    h2 = sdot4(wh, x.w[2][4 + v], h2);
+  }
+  const float lo = digits_f(l0, l1, l2) * x.b[0], hi = digits_f(h0, h1, h2) * x.b[1];
+  uint32_t sc0, m0, sc1, m1;
+  scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
+  scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
+  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
+  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * x.s[0] + (float)m1 * x.s[1]);
+}
+
+template <>
+__device__ __forceinline__ float dot_q<QT_Q6_K>(const Frag<QT_Q6_K>& f, int u, const XU& x) {
+  // codes 0..63 (the -32 offset is applied through the run sums)
+  const int b = (u & 7) & 3;
+  const int qa[2] = {(int)f.qa.x, (int)f.qa.y}, qb[2] = {(int)f.qb.x, (int)f.qb.y};
+  const int qh[2] = {(int)f.qh.x, (int)f.qh.y};
   float acc = 0.f;
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
-    const uint32_t* src = (qd & 1) ? qb : qa;
+    const int* src = (qd & 1) ? qb : qa;
     const int shift = qd < 2 ? 0 : 4;
-    const float4* xv = (const float4*)(xs + base + 32 * qd);
-    float s = 0.f;
+    int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const float4 x4 = xv[half];
-      const uint32_t lo = src[half] >> shift, hb = qh[half] >> (2 * qd);
-      const float q0 = (float)((int)(((lo >> 0) & 15u) | (((hb >> 0) & 3u) << 4)) - 32);
-      const float q1 = (float)((int)(((lo >> 8) & 15u) | (((hb >> 8) & 3u) << 4)) - 32);
-      const float q2 = (float)((int)(((lo >> 16) & 15u) | (((hb >> 16) & 3u) << 4)) - 32);
-      const float q3 = (float)((int)(((lo >> 24) & 15u) | (((hb >> 24) & 3u) << 4)) - 32);
-      s += x4.x * q0 + x4.y * q1 + x4.z * q2 + x4.w * q3;
+      const int w = ((src[half] >> shift) & 0x0f0f0f0f) | (((qh[half] >> (2 * qd)) & 0x03030303) << 4);
+      a0 = sdot4(w, x.w[0][2 * qd + half], a0);
+      a1 = sdot4(w, x.w[1][2 * qd + half], a1);
+      a2 = sdot4(w, x.w[2][2 * qd + half], a2);
     }
+    const float s = digits_f(a0, a1, a2) * x.b[qd] - 32.0f * x.s[qd];
     // sc[8h + (l>>4) + 2qd] with l>>4 == b>>1; f.sc holds sc[8h .. 8h+7]
     const int si = (b >> 1) + 2 * qd;
     const uint32_t sw = si < 4 ? f.sc.x : f.sc.y;
-    const float scv = (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
-    acc += scv * s;
+    acc += (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * s;
   }
-  (void)xs16;
   return h2f(f.d) * acc;
 }
 
 template <>
-__device__ __forceinline__ float dot_unit<QT_Q8_0>(const Frag<QT_Q8_0>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  const float4* xv = (const float4*)(xs + 32 * u);
-  const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
-  float s = 0.f;
+__device__ __forceinline__ float dot_q<QT_Q8_0>(const Frag<QT_Q8_0>& f, int u, const XU& x) {
+  const int q[8] = {(int)f.q0.x, (int)f.q0.y, (int)f.q0.z, (int)f.q0.w,
+                    (int)f.q1.x, (int)f.q1.y, (int)f.q1.z, (int)f.q1.w};
+  int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
-    const float4 a = xv[v];
-    s += a.x * (float)(int8_t)(q[v] & 0xffu) + a.y * (float)(int8_t)((q[v] >> 8) & 0xffu) +
-         a.z * (float)(int8_t)((q[v] >> 16) & 0xffu) + a.w * (float)(int8_t)(q[v] >> 24);
+    a0 = sdot4(q[v], x.w[0][v], a0);
+    a1 = sdot4(q[v], x.w[1][v], a1);
+    a2 = sdot4(q[v], x.w[2][v], a2);
   }
-  (void)xs16;
-  return h2f(f.d) * s;
+  (void)u;
+  return h2f(f.d) * (digits_f(a0, a1, a2) * x.b[0]);
 }
 
-template <int T>
-__device__ __forceinline__ float dot_q5x(const uint4 qs, uint32_t qh, int u, const float* xs) {
-  const float4* xv = (const float4*)(xs + 32 * u);
-  const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-  float s = 0.f;
+// Q5_0 / Q5_1 codes 0..31: low nibbles (elements 0..15) and high nibbles
+// (16..31) of qs, fifth bit from qh; returns sum(x * code)
+__device__ __forceinline__ float dot_q5_codes(const uint4 qs, uint32_t qh, const XU& x) {
+  const int q[4] = {(int)qs.x, (int)qs.y, (int)qs.z, (int)qs.w};
+  int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const float4 a = xv[v], b = xv[v + 4];
-    float lo[4], hi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * v + i;
-      lo[i] = (float)((int)(((q[v] >> (8 * i)) & 15u) | (((qh >> j) & 1u) << 4)) - (T == QT_Q5_0 ? 16 : 0));
-      hi[i] = (float)((int)(((q[v] >> (8 * i + 4)) & 15u) | (((qh >> (j + 16)) & 1u) << 4)) - (T == QT_Q5_0 ? 16 : 0));
-    }
-    s += a.x * lo[0] + a.y * lo[1] + a.z * lo[2] + a.w * lo[3];
-    s += b.x * hi[0] + b.y * hi[1] + b.z * hi[2] + b.w * hi[3];
+    // bits 4v..4v+3 of qh (and 16+4v..) spread to bit 4 of bytes 0..3
+    const int hl = (int)((((qh >> (4 * v)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+    const int hh = (int)((((qh >> (16 + 4 * v)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+    const int wl = (q[v] & 0x0f0f0f0f) | hl, wh = ((q[v] >> 4) & 0x0f0f0f0f) | hh;
+    a0 = sdot4(wl, x.w[0][v], a0);
+    a1 = sdot4(wl, x.w[1][v], a1);
+    a2 = sdot4(wl, x.w[2][v], a2);
+    a0 = sdot4(wh, x.w[0][4 + v], a0);
+    a1 = sdot4(wh, x.w[1][4 + v], a1);
+    a2 = sdot4(wh, x.w[2][4 + v], a2);
   }
-  return s;
+  return digits_f(a0, a1, a2) * x.b[0];
 }
 
 template <>
-__device__ __forceinline__ float dot_unit<QT_Q5_0>(const Frag<QT_Q5_0>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  (void)xs16;
-  return h2f(f.d) * dot_q5x<QT_Q5_0>(f.qs, f.qh, u, xs);
+__device__ __forceinline__ float dot_q<QT_Q5_0>(const Frag<QT_Q5_0>& f, int u, const XU& x) {
+  (void)u;
+  return h2f(f.d) * (dot_q5_codes(f.qs, f.qh, x) - 16.0f * x.s[0]);
 }
 
 template <>
-__device__ __forceinline__ float dot_unit<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, const float* xs,
-                                                   const float* xs16) {
-  const float sx = xs16[2 * u] + xs16[2 * u + 1];
-  return h2f(f.d) * dot_q5x<QT_Q5_1>(f.qs, f.qh, u, xs) + h2f(f.m) * sx;
+__device__ __forceinline__ float dot_q<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, const XU& x) {
+  (void)u;
+  return h2f(f.d) * dot_q5_codes(f.qs, f.qh, x) + h2f(f.m) * x.s[0];
 }
 
 // ---- exact dequantization ------------------------------------------------------

@@ -40,56 +40,109 @@ struct WaitSite {
   int phase, task;
 };
 
-// Copies src[0, n) into dst (LDS) once every word carries `tag`. All threads
-// of the workgroup call it. Returns false when the step is aborted (this wait
-// exceeded its bound, or another workgroup's did).
-__device__ __forceinline__ bool poll_in(const tagged_t* src, int n, float* dst, uint32_t tag, DevState* st, StepDebug* dbg,
-                        const WaitSite& site, int pos) {
-  const uint64_t t0 = wall_clock64();
-  for (uint32_t it = 0;; ++it) {
-    int stale = 0;
-    for (int i = threadIdx.x; i < n; i += kWg) {
-      const uint64_t w = __hip_atomic_load(gbl(src + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      stale |= (uint32_t)(w >> 32) != tag;
-      dst[i] = __uint_as_float((uint32_t)w);
-    }
-    if (!__syncthreads_or(stale)) return true;
-    if ((it & 3) == 3) {
-      int flag = 0;
-      bool timeout = false;
-      if (threadIdx.x == 0) {
-        timeout = wall_clock64() - t0 > kPollTicks;
-        flag = timeout || __hip_atomic_load(gbl(&st->error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+// Up to three tagged ranges copied into LDS by one poll.
+struct PollSeg {
+  const tagged_t* src;
+  float* dst;
+  int n;
+};
+
+// Copies every segment's src[0, n) into its dst (LDS) once every word carries
+// `tag`. All threads of the workgroup call it. Returns false when the step is
+// aborted (this wait exceeded its bound, or another workgroup's did). Each
+// thread issues all of its loads of a pass before it waits, so a pass costs
+// one memory round trip whatever the number of segments.
+constexpr int kPollBatch = 4;  // words per thread per pass (more costs registers the step needs)
+
+template <int NS>
+__device__ __forceinline__ bool poll_segs(const PollSeg (&sg)[NS], uint32_t tag, DevState* st, StepDebug* dbg,
+                                          const WaitSite& site, int pos) {
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < NS; ++q) total += sg[q].n;
+  // element e of the concatenation: the last segment that starts at or before
+  // e (selects, not an indexed array, so everything stays in registers)
+  auto locate = [&](int e, const tagged_t*& src, float*& dst) {
+    src = sg[0].src + e;
+    dst = sg[0].dst + e;
+    int off = e;
+#pragma unroll
+    for (int r = 1; r < NS; ++r) {
+      off -= sg[r - 1].n;
+      if (off >= 0) {
+        src = sg[r].src + off;
+        dst = sg[r].dst + off;
       }
-      if (__syncthreads_or(flag)) {
-        if (threadIdx.x == 0 && timeout) {
-          uint32_t expect = 0;
-          if (__hip_atomic_compare_exchange_strong(&dbg->claimed, &expect, 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)) {
-            int idx = -1;
-            uint32_t seen = 0;
-            for (int i = 0; i < n && idx < 0; ++i) {
-              const uint64_t w = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              if ((uint32_t)(w >> 32) != tag) {
-                idx = i;
-                seen = (uint32_t)(w >> 32);
-              }
-            }
-            __hip_atomic_store(&dbg->wg, (int32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->phase, site.phase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->task, site.task, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->index, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->seen, seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->want, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->pos, pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&dbg->abort_time, (uint64_t)wall_clock64(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          __hip_atomic_store(&st->error, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  const uint64_t t0 = wall_clock64();
+  for (int base = 0; base < total; base += kWg * kPollBatch) {
+    for (uint32_t it = 0;; ++it) {
+      int stale = 0;
+      const int rem = total - base - (int)threadIdx.x;  // this thread's words: j * kWg < rem
+      uint64_t w[kPollBatch];
+#pragma unroll
+      for (int j = 0; j < kPollBatch; ++j) {
+        if (j * kWg < rem) {
+          const tagged_t* src;
+          float* dst;
+          locate(base + (int)threadIdx.x + j * kWg, src, dst);
+          w[j] = __hip_atomic_load(gbl(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        return false;
+      }
+#pragma unroll
+      for (int j = 0; j < kPollBatch; ++j) {
+        if (j * kWg < rem) {
+          const tagged_t* src;
+          float* dst;
+          locate(base + (int)threadIdx.x + j * kWg, src, dst);
+          stale |= (uint32_t)(w[j] >> 32) != tag;
+          *dst = __uint_as_float((uint32_t)w[j]);
+        }
+      }
+      if (!__syncthreads_or(stale)) break;
+      if ((it & 3) == 3) {
+        int flag = 0;
+        bool timeout = false;
+        if (threadIdx.x == 0) {
+          timeout = wall_clock64() - t0 > kPollTicks;
+          flag = timeout || __hip_atomic_load(gbl(&st->error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        }
+        if (__syncthreads_or(flag)) {
+          if (threadIdx.x == 0 && timeout) {
+            uint32_t expect = 0;
+            if (__hip_atomic_compare_exchange_strong(&dbg->claimed, &expect, 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)) {
+              int idx = -1;
+              uint32_t seen = 0;
+              for (int e = 0; e < total && idx < 0; ++e) {
+                const tagged_t* src;
+                float* dst;
+                locate(e, src, dst);
+                const uint64_t v = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((uint32_t)(v >> 32) != tag) {
+                  idx = e;
+                  seen = (uint32_t)(v >> 32);
+                }
+              }
+              __hip_atomic_store(&dbg->wg, (int32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->phase, site.phase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->task, site.task, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->index, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->seen, seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->want, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->pos, pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(&dbg->abort_time, (uint64_t)wall_clock64(), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __hip_atomic_store(&st->error, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          return false;
+        }
       }
     }
   }
+  return true;
 }
 
 // The task's segment of a matvec phase, picked field by field.
@@ -151,51 +204,29 @@ constexpr int kStepResFloats = 1024;  // matvec row results: >= 2 * tile (GLU) a
 // One matvec task: rows [t0, t0 + nt) of the task's segment. Order: norm
 // weights staged and the first weight fragments requested, then the input
 // polled, then the prologue, the streaming dot products and the epilogue.
-template <int T>
+template <int T, int UC>
 __device__ __forceinline__ bool mv_task(const StepArgs& a, const StepPhase& ph, const TaskSeg& ts, bool glu, int gtask,
                                         int pos, uint32_t tag, const StepMvLds& l, const WaitSite& ws) {
-  constexpr int kPf = sizeof(Frag<T>) > 40 ? 2 : 4;
   const SegView& g = ts.g;
   const int tid = threadIdx.x;
   const int K = ph.k;
-  const int U = g.w.k >> 5;
-  const int lpr = g.lpr;
-  const int shift = __builtin_ctz((unsigned)lpr);
-  const int ng = kWg >> shift;
-  const int lg = tid >> shift, li = tid & (lpr - 1);
   const int t0 = ts.task * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
-  const int nv = nt > 0 ? (glu ? 2 * nt : nt) : 0;
-  const int rows_lane = lg < nv ? (nv - lg + ng - 1) / ng : 0;
-  const int ucount = (U + lpr - 1) / lpr;
-  const int items = rows_lane * ucount;
-
-  auto load_item = [&](int ii, Frag<T>& f) {
-    const int r = ii / ucount, j = ii - r * ucount;
-    const int v = lg + r * ng, u = li + j * lpr;
-    if (ii < items && u < U) {
-      QMat m = g.w;
-      if (glu && (v & 1)) {
-        m.s0 = g.u0;
-        m.s1 = g.u1;
-        m.s2 = g.u2;
-        m.s3 = g.u3;
-      }
-      f = load_unit<T>(m, t0 + (glu ? (v >> 1) : v), u);
-    }
-  };
+  const MvLane m = mv_lane(g, t0, nt, glu);
 
   // 1. inputs that do not depend on the previous phase
   if (ph.pro != PRO_PLAIN) lds_dma(ph.w_norm, l.wn, K);
   if (ph.pro == PRO_RES_NORM) lds_dma(ph.w_delta, l.wd, K);
-  Frag<T> cur[kPf];
-#pragma unroll
-  for (int q = 0; q < kPf; ++q) load_item(q, cur[q]);
+  Frag<T> cur[MvShape<T, UC>::N];
+  mv_fetch<T, UC>(g, m, 0, cur);
 
   // 2. inputs of the previous phases
-  if (ph.pro != PRO_EMBED_NORM && !poll_in(ph.in, K, l.xs, tag, a.st, a.dbg, ws, pos)) return false;
-  if (ph.pro == PRO_RES_NORM && !poll_in(ph.delta, K, l.dl, tag, a.st, a.dbg, ws, pos)) return false;
-  if (ph.epi == EPI_ADD && nt > 0 && !poll_in(ph.add + t0, nt, l.addv, tag, a.st, a.dbg, ws, pos)) return false;
+  {
+    const PollSeg sg[3] = {{ph.in, l.xs, ph.pro != PRO_EMBED_NORM ? K : 0},
+                           {ph.delta, l.dl, ph.pro == PRO_RES_NORM ? K : 0},
+                           {ph.epi == EPI_ADD ? ph.add + t0 : ph.add, l.addv, ph.epi == EPI_ADD ? max(nt, 0) : 0}};
+    if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -228,40 +259,11 @@ __device__ __forceinline__ bool mv_task(const StepArgs& a, const StepPhase& ph, 
     for (int i = tid; i < K; i += kWg) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), l.wn[i]);
     __syncthreads();
   }
-  for (int j = tid; j < K / 16; j += kWg) {
-    const float4* p = (const float4*)(xs + 16 * j);
-    const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-    l.xs16[j] = ((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w)) +
-                ((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w));
-  }
+  quantize_x(xs, K, l.dl, l.xs16);  // dl / wd are free from here on
   __syncthreads();
 
-  // 4. dot products (mv_work)
-  {
-    const float* xs16 = l.xs16;
-    float acc = 0.f;
-    for (int base = 0; base < items; base += kPf) {
-      Frag<T> nxt[kPf];
-#pragma unroll
-      for (int q = 0; q < kPf; ++q) load_item(base + kPf + q, nxt[q]);
-#pragma unroll
-      for (int q = 0; q < kPf; ++q) {
-        const int ii = base + q;
-        if (ii < items) {
-          const int r = ii / ucount, j = ii - r * ucount;
-          const int u = li + j * lpr;
-          if (u < U) acc += dot_unit<T>(cur[q], u, xs, xs16);
-          if (j == ucount - 1) {
-            acc = group_sum_n(acc, lpr);
-            if (li == 0) l.res[lg + r * ng] = acc;
-            acc = 0.f;
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < kPf; ++q) cur[q] = nxt[q];
-    }
-  }
+  // 4. dot products
+  mv_stream<T, UC>(g, m, xq_view(l.dl, l.xs16, K), l.res, cur);
   __syncthreads();
 
   // 5. epilogue
@@ -345,19 +347,29 @@ __device__ __forceinline__ bool mv_dispatch(const StepArgs& a, const StepPhase& 
   if (ph.pro == PRO_EMBED_NORM) embed_into(a, pos, ph.k, l.xs);  // made visible by the task's first barrier
   const bool glu = ph.epi == EPI_GLU_SILU || ph.epi == EPI_GLU_GELU;
   bool ok = true;
-  with_type(ts.g.w.type, [&]<int T>() { ok = mv_task<T>(a, ph, ts, glu, t, pos, tag, l, ws); });
+  const int uc = mv_uc(ts.g);
+  with_type(ts.g.w.type, [&]<int T>() {
+    if (uc == 1) {
+      ok = mv_task<T, 1>(a, ph, ts, glu, t, pos, tag, l, ws);
+    } else {
+      ok = mv_task<T, 2>(a, ph, ts, glu, t, pos, tag, l, ws);
+    }
+  });
   return ok;
 }
 
-// One attention task: (kv head, chunk) = (t / nchunk, t % nchunk).
+// One attention task: (kv head, chunk) = (t / nchunk, t % nchunk). Every
+// chunk but the newest stores its partial (tagged); the newest chunk's task
+// merges the head's partials as they arrive and stores the head's output.
 template <int G, bool KV16>
 __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph, int t, int pos, uint32_t tag, float* sm,
-                          uint32_t* s_last, const WaitSite& ws) {
+                                          const WaitSite& ws) {
   const AttnArgs& at = ph.at;
   const int kv = t / at.nchunk, c = t - kv * at.nchunk;
   const int hd = at.hd, CH = at.chunk;
   const int start = (at.window != 0 && pos + 1 > at.window) ? pos + 1 - at.window : 0;
-  if (c < start / CH || c > pos / CH) return true;  // chunk outside [start, pos]
+  const int c_lo = start / CH, c_hi = pos / CH;
+  if (c < c_lo || c > c_hi) return true;  // chunk outside [start, pos]
   const int tid = threadIdx.x;
   const int tpp = at.tpp;
   const int my_p = tid / tpp, my_j = tid & (tpp - 1);
@@ -367,6 +379,7 @@ __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph
   constexpr int kVec = KV16 ? 8 : 16;
   const int nvec = dpt * kElem / 16;
   const int ncp = (at.nchunk + 3) & ~3;
+  const int rowf = attn_rowf(G, hd);
   float* q_s = sm;
   float* k_new = q_s + G * hd;
   float* v_new = k_new + hd;
@@ -376,7 +389,8 @@ __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph
   float* wpart = inv + hd;
   float* wml = wpart + 4 * G * hd;
   float* wts = wml + 8 * kMaxG;
-  float* tile = wts + G * ncp;
+  float* cpart = wts + G * ncp;
+  float* tile = cpart + rowf;
   const int p_begin = max(start - t_lo, 0);
   const int p_end = min(pos + 1 - t_lo, CH);
 
@@ -400,16 +414,102 @@ __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph
     lds_dma((const float*)((const uint8_t*)at.vc + (head_base + (size_t)(t_lo + p_begin) * hd) * kElem),
             (float*)((uint8_t*)tile + (size_t)p_begin * hd * kElem), (p_end - p_begin) * hd * kElem / 4);
 
-  // this step's q (group heads), k and v of the head
+  // this step's q (group heads), k and v of the head, in one polling pass
   const int qdim = at.heads * hd, kvdim = at.kv_heads * hd;
-  if (!poll_in(ph.qkv_in + (size_t)kv * G * hd, G * hd, q_s, tag, a.st, a.dbg, ws, pos)) return false;
-  if (!poll_in(ph.qkv_in + qdim + (size_t)kv * hd, hd, k_new, tag, a.st, a.dbg, ws, pos)) return false;
-  if (!poll_in(ph.qkv_in + qdim + kvdim + (size_t)kv * hd, hd, v_new, tag, a.st, a.dbg, ws, pos)) return false;
+  {
+    const PollSeg sg[3] = {{ph.qkv_in + (size_t)kv * G * hd, q_s, G * hd},
+                           {ph.qkv_in + qdim + (size_t)kv * hd, k_new, hd},
+                           {ph.qkv_in + qdim + kvdim + (size_t)kv * hd, v_new, hd}};
+    if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  attn_chunk<G, KV16>(at, sm, kv, c, pos, kreg);
+
+  // partial rows [kv][nchunk], rowf words each (padding words carry the tag too)
+  tagged_t* rows = ph.tpart + (size_t)kv * at.nchunk * rowf;
+  if (c != c_hi) {
+    for (int i = tid; i < rowf; i += kWg) tag_store(rows + (size_t)c * rowf + i, i < G * (hd + 2) ? cpart[i] : 0.0f, tag);
+    return true;
+  }
+
+  // merge of chunks c_lo..c_hi (this one last), in batches of LDS rows with a
+  // running maximum: per head [M, rescale of the earlier batches, L] in wml
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nact = c_hi - c_lo + 1;
+  const int cap = max(1, min(at.merge_floats / rowf, ncp));
+  float* stage = tile;
+  float o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = 0.f;
+  if (tid < G) {
+    wml[3 * tid] = -INFINITY;
+    wml[3 * tid + 2] = 0.0f;
+  }
+  for (int b0 = 0; b0 < nact; b0 += cap) {
+    const int nb = min(cap, nact - b0);
+    const int n_mem = min(nb, nact - 1 - b0);  // rows of other chunks in this batch
+    __syncthreads();  // the previous batch (or the V tile) is consumed
+    if (n_mem > 0) {
+      const PollSeg sg[1] = {{rows + (size_t)(c_lo + b0) * rowf, stage, n_mem * rowf}};
+      if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+    }
+    if (n_mem < nb)
+      for (int i = tid; i < G * (hd + 2); i += kWg) stage[(size_t)(nb - 1) * rowf + i] = cpart[i];
+    __syncthreads();
+    for (int gg = wave; gg < G; gg += 4) {
+      float mb = -INFINITY;
+      for (int cc = lane; cc < nb; cc += 64) mb = fmaxf(mb, stage[cc * rowf + gg * (hd + 2)]);
+      mb = wave_max(mb);
+      const float M0 = wml[3 * gg];
+      const float M = fmaxf(M0, mb);
+      float L = 0.f;
+      for (int cc = lane; cc < nb; cc += 64) {
+        const float* pp = stage + cc * rowf + gg * (hd + 2);
+        const float f = expf(pp[0] - M);
+        wts[gg * ncp + cc] = f;
+        L += pp[1] * f;
+      }
+      L = wave_sum(L);
+      if (lane == 0) {
+        const float r = M0 == -INFINITY ? 0.0f : expf(M0 - M);
+        wml[3 * gg] = M;
+        wml[3 * gg + 1] = r;
+        wml[3 * gg + 2] = wml[3 * gg + 2] * r + L;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = tid + q * kWg;
+      if (i < G * hd) {
+        const int gg = i / hd, d = i - gg * hd;
+        const float* src = stage + gg * (hd + 2) + 2 + d;
+        const float* wv = wts + gg * ncp;
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        int cc = 0;
+        for (; cc + 4 <= nb; cc += 4) {
+          acc0 += src[cc * rowf] * wv[cc];
+          acc1 += src[(cc + 1) * rowf] * wv[cc + 1];
+          acc2 += src[(cc + 2) * rowf] * wv[cc + 2];
+          acc3 += src[(cc + 3) * rowf] * wv[cc + 3];
+        }
+        for (; cc < nb; ++cc) acc0 += src[cc * rowf] * wv[cc];
+        o[q] = o[q] * wml[3 * gg + 1] + ((acc0 + acc1) + (acc2 + acc3));
+      }
+    }
+  }
   tagged_t* out = ph.attn_out + (size_t)kv * G * hd;
-  attn_compute<G, KV16>(at, sm, kv, c, pos, kreg, s_last, [&](int i, float v) { tag_store(out + i, v, tag); });
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = tid + q * kWg;
+    if (i < G * hd) {
+      const int gg = i / hd, d = i - gg * hd;
+      tag_store(out + gg * hd + d, o[q] * (1.0f / wml[3 * gg + 2]), tag);
+    }
+  }
   return true;
 }
 
@@ -439,7 +539,7 @@ __global__ __launch_bounds__(kWg, 1) void k_step(const StepArgs* __restrict__ ap
     for (; t < ph.n_tasks && ok; t += nwg) {
       const WaitSite ws{p, t};
       if (ph.kind == PH_ATTN) {
-        ok = attn_task<G, KV16>(a, ph, t, pos, tag, smem, &s_flag, ws);
+        ok = attn_task<G, KV16>(a, ph, t, pos, tag, smem, ws);
       } else {
         ok = mv_dispatch(a, ph, t, pos, tag, smem, ws);
       }
