@@ -6,6 +6,12 @@
 #include "kernels.h"
 #include "qdot.h"
 
+// Optional trace point inside the attention phases (k = 1, 2, 3 after B, C, D);
+// empty unless a profiling build defines it.
+#ifndef CHONK_ATTN_STAMP
+#define CHONK_ATTN_STAMP(k)
+#endif
+
 namespace chonk {
 namespace {
 
@@ -498,6 +504,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv,
     }
     __syncthreads();
   }
+  CHONK_ATTN_STAMP(1);
 
   // C: scores, wave-local softmax statistics, weighted V
   {
@@ -578,6 +585,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv,
     }
   }
   __syncthreads();
+  CHONK_ATTN_STAMP(2);
 
   // D: chunk partial = the four wave partials rescaled to the chunk maximum
   for (int i = tid; i < G * hd; i += kWg) {
@@ -606,6 +614,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv,
     cpart[tid * (hd + 2) + 1] = L;
   }
   __syncthreads();
+  CHONK_ATTN_STAMP(3);
 }
 
 // attn_chunk, then the chunk partial to uncached memory; the last chunk of the

@@ -49,12 +49,13 @@ struct PollSeg {
 
 // Copies every segment's src[0, n) into its dst (LDS) once every word carries
 // `tag`. All threads of the workgroup call it. Returns false when the step is
-// aborted (this wait exceeded its bound, or another workgroup's did). Each
-// thread issues all of its loads of a pass before it waits, so a pass costs
-// one memory round trip whatever the number of segments.
-constexpr int kPollBatch = 4;  // words per thread per pass (more costs registers the step needs)
-
-template <int NS>
+// aborted (this wait exceeded its bound, or another workgroup's did). A pass
+// over a window of B words per thread issues all of its loads before it
+// waits, so it costs one memory round trip; B is small where registers are
+// scarce. Every lane issues every load and store (past the end it reads and
+// stores the last word again), which keeps the code branch-free and the
+// compiler's wait counts exact.
+template <int NS, int B>
 __device__ __forceinline__ bool poll_segs(const PollSeg (&sg)[NS], uint32_t tag, DevState* st, StepDebug* dbg,
                                           const WaitSite& site, int pos) {
   int total = 0;
@@ -76,29 +77,24 @@ __device__ __forceinline__ bool poll_segs(const PollSeg (&sg)[NS], uint32_t tag,
     }
   };
   const uint64_t t0 = wall_clock64();
-  for (int base = 0; base < total; base += kWg * kPollBatch) {
+  for (int base = 0; base < total; base += B * kWg) {
     for (uint32_t it = 0;; ++it) {
       int stale = 0;
-      const int rem = total - base - (int)threadIdx.x;  // this thread's words: j * kWg < rem
-      uint64_t w[kPollBatch];
+      uint64_t w[B];
 #pragma unroll
-      for (int j = 0; j < kPollBatch; ++j) {
-        if (j * kWg < rem) {
-          const tagged_t* src;
-          float* dst;
-          locate(base + (int)threadIdx.x + j * kWg, src, dst);
-          w[j] = __hip_atomic_load(gbl(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+      for (int j = 0; j < B; ++j) {
+        const tagged_t* src;
+        float* dst;
+        locate(min(base + (int)threadIdx.x + j * kWg, total - 1), src, dst);
+        w[j] = __hip_atomic_load(gbl(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
 #pragma unroll
-      for (int j = 0; j < kPollBatch; ++j) {
-        if (j * kWg < rem) {
-          const tagged_t* src;
-          float* dst;
-          locate(base + (int)threadIdx.x + j * kWg, src, dst);
-          stale |= (uint32_t)(w[j] >> 32) != tag;
-          *dst = __uint_as_float((uint32_t)w[j]);
-        }
+      for (int j = 0; j < B; ++j) {
+        const tagged_t* src;
+        float* dst;
+        locate(min(base + (int)threadIdx.x + j * kWg, total - 1), src, dst);
+        stale |= (uint32_t)(w[j] >> 32) != tag;
+        *dst = __uint_as_float((uint32_t)w[j]);
       }
       if (!__syncthreads_or(stale)) break;
       if ((it & 3) == 3) {
@@ -225,7 +221,7 @@ __device__ __forceinline__ bool mv_task(const StepArgs& a, const StepPhase& ph, 
     const PollSeg sg[3] = {{ph.in, l.xs, ph.pro != PRO_EMBED_NORM ? K : 0},
                            {ph.delta, l.dl, ph.pro == PRO_RES_NORM ? K : 0},
                            {ph.epi == EPI_ADD ? ph.add + t0 : ph.add, l.addv, ph.epi == EPI_ADD ? max(nt, 0) : 0}};
-    if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+    if (!poll_segs<3, UC == 1 ? 4 : 12>(sg, tag, a.st, a.dbg, ws, pos)) return false;
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -420,7 +416,7 @@ __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph
     const PollSeg sg[3] = {{ph.qkv_in + (size_t)kv * G * hd, q_s, G * hd},
                            {ph.qkv_in + qdim + (size_t)kv * hd, k_new, hd},
                            {ph.qkv_in + qdim + kvdim + (size_t)kv * hd, v_new, hd}};
-    if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+    if (!poll_segs<3, 2>(sg, tag, a.st, a.dbg, ws, pos)) return false;
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -454,7 +450,7 @@ __device__ __forceinline__ bool attn_task(const StepArgs& a, const StepPhase& ph
     __syncthreads();  // the previous batch (or the V tile) is consumed
     if (n_mem > 0) {
       const PollSeg sg[1] = {{rows + (size_t)(c_lo + b0) * rowf, stage, n_mem * rowf}};
-      if (!poll_segs(sg, tag, a.st, a.dbg, ws, pos)) return false;
+      if (!poll_segs<1, 17>(sg, tag, a.st, a.dbg, ws, pos)) return false;
     }
     if (n_mem < nb)
       for (int i = tid; i < G * (hd + 2); i += kWg) stage[(size_t)(nb - 1) * rowf + i] = cpart[i];
