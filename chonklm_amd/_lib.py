@@ -129,6 +129,7 @@ SIGNATURES = [
     ("chonk_engine_generate_stepped", C.c_int,
      [P, I32P, C.c_size_t, C.c_int32, C.POINTER(SamplingC), P, P, I32P, C.c_size_t, C.POINTER(C.c_size_t),
       C.POINTER(GenStatsC)]),
+    ("chonk_engine_prefill", C.c_int, [P, I32P, C.c_size_t]),
     ("chonk_engine_conversation", C.c_int, [P, I32P, C.c_size_t, C.POINTER(C.c_size_t), I32P]),
     ("chonk_engine_reset", C.c_int, [P]),
     ("chonk_engine_reset_conversation", C.c_int, [P]),
@@ -144,6 +145,8 @@ SIGNATURES = [
     ("chonk_dequant", C.c_int, [C.c_int32, C.c_uint32, P, C.c_int64, C.c_int64, F32P]),
     ("chonk_matvec", C.c_int,
      [C.c_int32, C.c_uint32, P, C.c_int64, C.c_int64, F32P, F32P, C.c_int32, C.POINTER(C.c_double)]),
+    ("chonk_gemm", C.c_int,
+     [C.c_int32, C.c_uint32, P, C.c_int64, C.c_int64, F32P, C.c_int64, F32P, C.c_int32, C.POINTER(C.c_double)]),
     ("chonk_write_synthetic_gguf", C.c_int, [C.POINTER(SynthConfigC), C.c_char_p, C.c_int32]),
     ("chonk_write_shards", C.c_int, [C.c_char_p, C.c_char_p, C.c_uint64, C.c_char_p]),
 ]

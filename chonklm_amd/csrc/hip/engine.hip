@@ -37,6 +37,7 @@
 #include "../host/synth.h"
 #include "chonk.h"
 #include "kernels.h"
+#include "prefill.h"
 
 namespace chonk {
 namespace {
@@ -151,6 +152,7 @@ class Arena {
 struct DevMat {
   QMat q{};
   uint64_t gguf_bytes = 0;  // bytes of the N rows as stored in GGUF
+  int ws = 0;               // GEMM weight exponent: |W| * 2^ws stays below 2^14
 };
 
 // ---- model description (buildGgufLlamaManifest) ---------------------------------
@@ -315,6 +317,13 @@ struct chonk_engine {
   bool has_cached_next = false;
   int32_t cached_next = 0;
   uint64_t weight_bytes_per_token = 0;
+  // batched prompt processing: row buffers allocated on first use
+  bool batched_prefill = true;
+  void* pf_mem = nullptr;
+  float *pf_x = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr,
+        *pf_d = nullptr, *pf_xscale = nullptr;
+  _Float16 *pf_h = nullptr, *pf_l = nullptr;
+  int32_t* pf_tok = nullptr;
   // status
   std::atomic<bool> busy{false};
   bool lost = false;
@@ -422,6 +431,33 @@ void check_matrix(const GgufTensorInfo& t, int64_t K, int64_t N) {
   if (K > 32768) throw Error(CHONK_EINVAL, "tensor " + t.name + " row length above 32768 is not supported");
 }
 
+// Power of two that brings every dequantized weight of the tensor below 2^14
+// (bound from the blocks' fp16 scales), so that the GEMM's fp16 hi/lo split of
+// W * 2^ws neither overflows nor loses the low half to subnormals.
+int weight_exponent(uint32_t type, const uint8_t* raw, size_t n_blocks, size_t block_bytes) {
+  auto h = [&](size_t b, size_t off) {
+    uint16_t v;
+    std::memcpy(&v, raw + b * block_bytes + off, 2);
+    return std::fabs(f16_to_f32(v));
+  };
+  double bound = 0;
+  for (size_t b = 0; b < n_blocks; ++b) {
+    double v = 0;
+    switch (type) {
+      case GGML_Q4_K: v = 63.0 * 15 * h(b, 0) + 63.0 * h(b, 2); break;
+      case GGML_Q5_K: v = 63.0 * 31 * h(b, 0) + 63.0 * h(b, 2); break;
+      case GGML_Q6_K: v = 128.0 * 32 * h(b, 208); break;
+      case GGML_Q8_0: v = 128.0 * h(b, 0); break;
+      case GGML_Q5_0: v = 16.0 * h(b, 0); break;
+      case GGML_Q5_1: v = 31.0 * h(b, 0) + h(b, 2); break;
+      default: break;
+    }
+    if (std::isfinite(v)) bound = std::max(bound, v);
+  }
+  if (!(bound > 0)) return 0;
+  return std::max(-30, std::min(30, (int)std::floor(std::log2(16384.0 / bound))));
+}
+
 DevMat upload_matrix(Arena& arena, const ByteSource& src, const GgufFile& g, const GgufTensorInfo& t, int64_t K,
                      int64_t N) {
   check_matrix(t, K, N);
@@ -441,6 +477,7 @@ DevMat upload_matrix(Arena& arena, const ByteSource& src, const GgufFile& g, con
     *dst[i] = (const uint8_t*)p;
   }
   m.gguf_bytes = (uint64_t)(N * (K / tt.block_elems)) * tt.block_bytes;
+  m.ws = weight_exponent(t.type, raw.data(), (size_t)(N * (K / tt.block_elems)), tt.block_bytes);
   return m;
 }
 
@@ -997,6 +1034,7 @@ void engine_free(chonk_engine* e) {
   uncached_pool().give_back(e->device, e->uncached);
   if (e->tagged) (void)hipFree(e->tagged);
   if (e->d_phases) (void)hipFree(e->d_phases);
+  if (e->pf_mem) (void)hipFree(e->pf_mem);
   if (e->h_state) (void)hipHostFree(e->h_state);
   if (e->h_tok) (void)hipHostFree(e->h_tok);
   if (e->h_samp) (void)hipHostFree(e->h_samp);
@@ -1159,12 +1197,16 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   HIP_OK(hipDeviceSynchronize());
 
   HIP_OK(init_kernel_attributes());
+  HIP_OK(init_gemm_attributes());
   build_steps(e.get());
   e->step_logits = e->kernels_logits;
   e->step_plain = e->kernels_plain;
   // the persistent step is the default; CHONK_STEP=0 keeps the per-phase kernels
   const char* sv = std::getenv("CHONK_STEP");
   if (!(sv && sv[0] == '0')) build_step(e.get());
+  // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
+  const char* pv = std::getenv("CHONK_PREFILL");
+  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0);
   const char* ng = std::getenv("CHONK_NO_GRAPH");
   e->use_graph = !(ng && ng[0] == '1');
   for (const Launch& L : e->kernels_logits)
@@ -1293,6 +1335,157 @@ Error device_error(chonk_engine* e, const DevState& st) {
   return Error(CHONK_EHIP, msg);
 }
 
+// ---- batched prompt pass ------------------------------------------------------------
+
+constexpr int kPrefillRows = 512;  // prompt rows per pass (longer prompts take several)
+
+void prefill_alloc(chonk_engine* e) {
+  if (e->pf_mem) return;
+  const ModelCfg& c = e->cfg;
+  const size_t R = kPrefillRows;
+  const size_t H = c.hidden, qdim = (size_t)c.heads * c.hd, kvdim = (size_t)c.kv_heads * c.hd, F = c.ffn;
+  const size_t kmax = gemm_kpad((int)std::max(H, std::max(qdim, F)));
+  const size_t sizes[10] = {R * H * 4,    R * (qdim + 2 * kvdim) * 4, R * qdim * 4, R * F * 4, R * F * 4,
+                            R * F * 4,    R * H * 4,                  R * 4,        R * kmax * 2, R * kmax * 2};
+  size_t total = align256(R * 4);
+  for (size_t z : sizes) total += align256(z);
+  HIP_OK(hipMalloc(&e->pf_mem, total));
+  uint8_t* p = (uint8_t*)e->pf_mem;
+  void* out[10];
+  for (int i = 0; i < 10; ++i) {
+    out[i] = p;
+    p += align256(sizes[i]);
+  }
+  e->pf_x = (float*)out[0];
+  e->pf_qkv = (float*)out[1];
+  e->pf_att = (float*)out[2];
+  e->pf_g = (float*)out[3];
+  e->pf_u = (float*)out[4];
+  e->pf_act = (float*)out[5];
+  e->pf_d = (float*)out[6];
+  e->pf_xscale = (float*)out[7];
+  e->pf_h = (_Float16*)out[8];
+  e->pf_l = (_Float16*)out[9];
+  e->pf_tok = (int32_t*)p;
+}
+
+// K/V of every layer for tokens[0, n) at positions e->pos .. e->pos + n - 1,
+// computed as row batches (dequant-fused MFMA GEMMs, causal attention over the
+// cache). The host position and the device state are left to the caller; no
+// logits are produced (the reference's runToken(id, false) for each token).
+void prefill_rows(chonk_engine* e, const int32_t* tokens, int n) {
+  const ModelCfg& c = e->cfg;
+  if (n <= 0) return;
+  if ((int64_t)e->pos + n > c.ctx)
+    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+  prefill_alloc(e);
+  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn;
+  const int ldqkv = qdim + 2 * kvdim;
+  hipStream_t s = e->stream;
+  for (int off = 0; off < n; off += kPrefillRows) {
+    const int T = std::min(kPrefillRows, n - off);
+    const int p0 = e->pos + off;
+    HIP_OK(hipMemcpyAsync(e->pf_tok, tokens + off, (size_t)T * 4, hipMemcpyHostToDevice, s));
+    auto split = [&](const float* x, int ld, int k, const float* w) {
+      PfSplitArgs a{};
+      a.x = x;
+      a.ldx = ld;
+      a.k = k;
+      a.kpad = gemm_kpad(k);
+      a.w = w;
+      a.eps = c.eps;
+      a.xh = e->pf_h;
+      a.xl = e->pf_l;
+      a.xscale = e->pf_xscale;
+      HIP_OK(launch_pf_split(a, T, s));
+    };
+    auto gemm = [&](const DevMat& m, float* y, int ldy, int epi) {
+      GemmArgs g{};
+      g.w = m.q;
+      g.xh = e->pf_h;
+      g.xl = e->pf_l;
+      g.xscale = e->pf_xscale;
+      g.y = y;
+      g.ldy = ldy;
+      g.t = T;
+      g.kpad = gemm_kpad(m.q.k);
+      g.epi = epi;
+      g.ws = m.ws;
+      HIP_OK(launch_gemm(g, s));
+    };
+    HIP_OK(launch_pf_embed(e->embed.q, e->pf_tok, c.embed_scale, H, e->pf_x, T, s));
+    for (int i = 0; i < c.layers; ++i) {
+      const LayerDev& L = e->layers[i];
+      split(e->pf_x, H, H, L.in_norm);
+      gemm(L.q, e->pf_qkv, ldqkv, GEMM_STORE);
+      gemm(L.k, e->pf_qkv + qdim, ldqkv, GEMM_STORE);
+      gemm(L.v, e->pf_qkv + qdim + kvdim, ldqkv, GEMM_STORE);
+      PfRopeArgs r{};
+      r.qkv = e->pf_qkv;
+      r.ld = ldqkv;
+      r.p0 = p0;
+      r.hd = c.hd;
+      r.heads = c.heads;
+      r.kv_heads = c.kv_heads;
+      r.ctx = c.ctx;
+      r.interleaved = c.interleaved ? 1 : 0;
+      r.kv16 = e->kv_elem == 2 ? 1 : 0;
+      r.qn_w = c.qk_norm ? L.q_norm : nullptr;
+      r.kn_w = c.qk_norm ? L.k_norm : nullptr;
+      r.eps = c.qk_eps;
+      r.rope_inv = rope_table(e, c.layer[i].theta, c.hd);
+      r.kc = L.kc;
+      r.vc = L.vc;
+      HIP_OK(launch_pf_rope_kv(r, T, s));
+      if (i == c.layers - 1) break;  // only the last layer's K/V are needed from it
+      PfAttnArgs at{};
+      at.qkv = e->pf_qkv;
+      at.ld = ldqkv;
+      at.out = e->pf_att;
+      at.ldo = qdim;
+      at.heads = c.heads;
+      at.kv_heads = c.kv_heads;
+      at.hd = c.hd;
+      at.ctx = c.ctx;
+      at.p0 = p0;
+      at.window = c.layer[i].window;
+      at.kv16 = r.kv16;
+      at.scale = c.scale;
+      at.kc = L.kc;
+      at.vc = L.vc;
+      HIP_OK(launch_pf_attn(at, T, s));
+      split(e->pf_att, qdim, qdim, nullptr);
+      if (c.gemma) {
+        gemm(L.o, e->pf_d, H, GEMM_STORE);
+        HIP_OK(launch_pf_norm_add(e->pf_d, L.post_norm, c.eps, H, e->pf_x, T, s));
+      } else {
+        gemm(L.o, e->pf_x, H, GEMM_ADD);
+      }
+      split(e->pf_x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm);
+      gemm(L.gate, e->pf_g, F, GEMM_STORE);
+      gemm(L.up, e->pf_u, F, GEMM_STORE);
+      PfGluArgs gl{};
+      gl.g = e->pf_g;
+      gl.u = e->pf_u;
+      gl.act = e->pf_act;
+      gl.k = F;
+      gl.kpad = gemm_kpad(F);
+      gl.gelu = c.gemma ? 1 : 0;
+      gl.xh = e->pf_h;
+      gl.xl = e->pf_l;
+      gl.xscale = e->pf_xscale;
+      HIP_OK(launch_pf_glu_split(gl, T, s));
+      if (c.gemma) {
+        gemm(L.down, e->pf_d, H, GEMM_STORE);
+        HIP_OK(launch_pf_norm_add(e->pf_d, L.post_ffn_norm, c.eps, H, e->pf_x, T, s));
+      } else {
+        gemm(L.down, e->pf_x, H, GEMM_ADD);
+      }
+    }
+  }
+  HIP_OK(hipStreamSynchronize(s));
+}
+
 int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
                   size_t n_pen, const int32_t* seen, size_t n_seen) {
   if (e->pos >= e->cfg.ctx)
@@ -1396,8 +1589,15 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
   } else {
     std::vector<int32_t> suf(prompt + prefix, prompt + n_prompt);
     HIP_OK(hipMemcpy(e->hist + e->pos, suf.data(), suf.size() * 4, hipMemcpyHostToDevice));
-    upload_state_fields(e, st);
-    for (size_t i = 0; i + 1 < n_suffix; ++i) replay(e, false);
+    if (e->batched_prefill && n_suffix > 1) {
+      // all but the last prompt token as row batches, the last one as a step
+      prefill_rows(e, suf.data(), (int)n_suffix - 1);
+      st.pos = e->pos + (int)n_suffix - 1;
+      upload_state_fields(e, st);
+    } else {
+      upload_state_fields(e, st);
+      for (size_t i = 0; i + 1 < n_suffix; ++i) replay(e, false);
+    }
     replay(e, true);
     st = read_state(e);
     if (st.error) throw device_error(e, st);
@@ -1591,6 +1791,24 @@ int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, 
     const int32_t t = run_token(e, token, need_logits != 0, s, penalized, penalized ? n_penalized : 0, seen,
                                 seen ? n_seen : 0);
     if (out_token) *out_token = t;
+  });
+}
+
+int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n) {
+  return api(e, [&] {
+    if (n == 0) return;
+    if (!tokens) throw Error(CHONK_EINVAL, "tokens is null");
+    for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
+    if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
+      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+    HIP_OK(hipMemcpy(e->hist + e->pos, tokens, n * 4, hipMemcpyHostToDevice));
+    prefill_rows(e, tokens, (int)n);
+    e->pos += (int)n;
+    DevState st = read_state(e);
+    st.pos = e->pos;
+    upload_state_fields(e, st);
+    e->known_token_pos = -1;
+    e->logits_valid = false;
   });
 }
 
@@ -1954,6 +2172,98 @@ int chonk_matvec(int32_t device, uint32_t ggml_type, const void* blocks, int64_t
         if (avg_us) *avg_us = (double)ms * 1000.0 / reps;
       }
       HIP_OK(hipMemcpy(y, d_y, (size_t)n_rows * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      if (s) (void)hipStreamDestroy(s);
+      for (void* p : bufs) (void)hipFree(p);
+      throw;
+    }
+    (void)hipStreamDestroy(s);
+    for (void* p : bufs) (void)hipFree(p);
+  });
+}
+
+int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
+               const float* x, int64_t n_tokens, float* y, int32_t reps, double* avg_us) {
+  return api_free([&] {
+    TypeTraits t;
+    if (!type_traits(ggml_type, &t) || !t.quantized) throw Error(CHONK_EINVAL, "unsupported GGUF tensor type " + type_name(ggml_type));
+    if (n_rows <= 0 || row_len <= 0 || row_len % t.block_elems || row_len % 32 || row_len > 65536 || n_tokens <= 0 ||
+        n_tokens > 65536 || !blocks || !x || !y)
+      throw Error(CHONK_EINVAL, "bad gemm shape");
+    HIP_OK(hipSetDevice(device));
+    const Stripes st = repack(ggml_type, (const uint8_t*)blocks, n_rows, row_len);
+    QMat q{};
+    q.type = (int32_t)ggml_type;
+    q.n = (int32_t)n_rows;
+    q.k = (int32_t)row_len;
+    const int ws = weight_exponent(ggml_type, (const uint8_t*)blocks, (size_t)(n_rows * (row_len / t.block_elems)),
+                                   t.block_bytes);
+    const int kpad = gemm_kpad((int)row_len);
+    std::vector<void*> bufs;
+    auto dev = [&](size_t n) {
+      void* p;
+      HIP_OK(hipMalloc(&p, n));
+      bufs.push_back(p);
+      return p;
+    };
+    hipStream_t s = nullptr;
+    try {
+      const uint8_t** dst[4] = {&q.s0, &q.s1, &q.s2, &q.s3};
+      for (int i = 0; i < 4; ++i) {
+        if (st.s[i].empty()) continue;
+        void* p = dev(st.s[i].size());
+        HIP_OK(hipMemcpy(p, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+        *dst[i] = (const uint8_t*)p;
+      }
+      float* d_x = (float*)dev((size_t)n_tokens * row_len * 4);
+      float* d_y = (float*)dev((size_t)n_tokens * n_rows * 4);
+      _Float16* d_h = (_Float16*)dev((size_t)n_tokens * kpad * 2);
+      _Float16* d_l = (_Float16*)dev((size_t)n_tokens * kpad * 2);
+      float* d_s = (float*)dev((size_t)n_tokens * 4);
+      HIP_OK(hipMemcpy(d_x, x, (size_t)n_tokens * row_len * 4, hipMemcpyHostToDevice));
+      PfSplitArgs sa{};
+      sa.x = d_x;
+      sa.ldx = (int)row_len;
+      sa.k = (int)row_len;
+      sa.kpad = kpad;
+      sa.xh = d_h;
+      sa.xl = d_l;
+      sa.xscale = d_s;
+      GemmArgs g{};
+      g.w = q;
+      g.xh = d_h;
+      g.xl = d_l;
+      g.xscale = d_s;
+      g.y = d_y;
+      g.ldy = (int)n_rows;
+      g.t = (int)n_tokens;
+      g.kpad = kpad;
+      g.epi = GEMM_STORE;
+      g.ws = ws;
+      HIP_OK(init_kernel_attributes());
+      HIP_OK(init_gemm_attributes());
+      HIP_OK(hipStreamCreate(&s));
+      auto run = [&] {
+        HIP_OK(launch_pf_split(sa, (int)n_tokens, s));
+        HIP_OK(launch_gemm(g, s));
+      };
+      run();
+      HIP_OK(hipStreamSynchronize(s));
+      if (reps > 0) {
+        hipEvent_t e0, e1;
+        HIP_OK(hipEventCreate(&e0));
+        HIP_OK(hipEventCreate(&e1));
+        HIP_OK(hipEventRecord(e0, s));
+        for (int i = 0; i < reps; ++i) run();
+        HIP_OK(hipEventRecord(e1, s));
+        HIP_OK(hipEventSynchronize(e1));
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        if (avg_us) *avg_us = (double)ms * 1000.0 / reps;
+      }
+      HIP_OK(hipMemcpy(y, d_y, (size_t)n_tokens * n_rows * 4, hipMemcpyDeviceToHost));
     } catch (...) {
       if (s) (void)hipStreamDestroy(s);
       for (void* p : bufs) (void)hipFree(p);

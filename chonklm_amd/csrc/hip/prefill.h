@@ -1,0 +1,73 @@
+// Batched (many-token) kernels: operand split, dequant-fused MFMA GEMM and the
+// per-token glue of a prompt processed as T rows at once (prefill.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "device_common.h"
+
+namespace chonk {
+
+enum GemmEpi : int32_t { GEMM_STORE = 0, GEMM_ADD = 1 };
+
+// y[t][n] (=|+=) 2^-ws * xscale[t] * sum_k (xh + xl)[t][k] * (W 2^ws)[n][k]
+struct GemmArgs {
+  QMat w;                 // striped weights, N = w.n rows of K = w.k
+  const _Float16* xh;     // [t][kpad] activation planes, zero past K
+  const _Float16* xl;
+  const float* xscale;    // [t]
+  float* y;               // [t][ldy]
+  int32_t ldy, t, kpad, epi;
+  int32_t ws;             // weight exponent
+};
+
+struct PfSplitArgs {
+  const float* x;         // [rows][ldx]
+  int32_t ldx, k, kpad;
+  const float* w;         // RMSNorm weight [k], or null for a plain split
+  float eps;
+  _Float16 *xh, *xl;      // [rows][kpad]
+  float* xscale;          // [rows]
+};
+
+struct PfGluArgs {
+  const float *g, *u;     // [rows][k]
+  float* act;             // [rows][k]
+  int32_t k, kpad, gelu;
+  _Float16 *xh, *xl;
+  float* xscale;
+};
+
+struct PfRopeArgs {
+  float* qkv;             // [rows][ld]: q | k | v
+  int32_t ld, p0, hd, heads, kv_heads, ctx, interleaved, kv16;
+  const float *qn_w, *kn_w;  // per-head RMSNorm weights (null: none)
+  float eps;
+  const float* rope_inv;  // [hd/2]
+  void *kc, *vc;          // [kv_heads][ctx][hd]
+};
+
+struct PfAttnArgs {
+  const float* qkv;       // rotated q rows
+  int32_t ld;
+  float* out;             // [rows][ldo]
+  int32_t ldo, heads, kv_heads, hd, ctx, p0, window, kv16;
+  float scale;
+  const void *kc, *vc;
+};
+
+// K padded for the GEMM's activation planes.
+constexpr int gemm_kpad(int k) { return (k + 127) / 128 * 128; }
+
+size_t gemm_shared_bytes();
+hipError_t init_gemm_attributes();
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s);
+hipError_t launch_pf_embed(const QMat& embed, const int32_t* tok, float scale, int k, float* x, int rows,
+                           hipStream_t s);
+hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, float* x, int rows, hipStream_t s);
+hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s);
+hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s);
+hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s);
+
+}  // namespace chonk

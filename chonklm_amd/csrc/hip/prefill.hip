@@ -1,0 +1,473 @@
+// Batched (many-token) kernels for gfx950: the prompt is processed as T rows
+// at once instead of T decode steps (the reference prefills token by token,
+// llama-wgsl-runtime.ts:276-289; the K/V it leaves in the cache and the last
+// prompt token's logits are what must match).
+//
+// Linear layers are dequant-fused GEMMs on the matrix cores. fp16 MFMA keeps
+// fp32-class accuracy by splitting both operands into hi + lo halves:
+//   W * 2^ws = Wh + Wl,  x * 2^rs = xh + xl  (per token row),
+//   sum W x = 2^-(ws+rs) * (Wh xh + Wh xl + Wl xh)   (Wl xl ~ 2^-22, dropped)
+// with the weights dequantized bit-exactly (dequant_unit) into LDS tiles and
+// the products accumulated in fp32 by v_mfma_f32_16x16x16_f16.
+#include <hip/hip_runtime.h>
+
+#include "kernel_common.h"
+#include "kernels.h"
+#include "prefill.h"
+
+namespace chonk {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGM = 64;          // weight rows per workgroup tile
+constexpr int kGT = 64;          // token rows per workgroup tile
+constexpr int kGK = 128;         // K per stage (whole units for every type)
+constexpr int kGS = kGK + 8;     // LDS row stride in halves (bank spread)
+
+__device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// ---- operand split ----------------------------------------------------------------
+
+// One workgroup per token row: optional RMSNorm (x * inv) * w with the
+// reference's fp32 operation order, then the row scaled by a power of two so
+// that |x| < 2^14 and split into fp16 hi + lo planes (zero-padded to kpad).
+// mode 0: plain; 1: RMSNorm with w.
+__global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
+  __shared__ float red[8];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* x = a.x + (size_t)t * a.ldx;
+  float inv = 1.0f;
+  if (a.w) {
+    float ss = 0.f;
+    for (int i = tid; i < a.k; i += kWg) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+  }
+  float mx = 0.f;
+  for (int i = tid; i < a.k; i += kWg) {
+    const float v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
+    mx = fmaxf(mx, fabsf(v));
+  }
+  mx = wave_max(mx);
+  __syncthreads();
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+  int e = 0;
+  (void)frexpf(mx, &e);  // mx < 2^e
+  const int rs = max(min(14 - e, 60), -60);
+  _Float16* xh = a.xh + (size_t)t * a.kpad;
+  _Float16* xl = a.xl + (size_t)t * a.kpad;
+  for (int i = tid; i < a.kpad; i += kWg) {
+    float v = 0.f;
+    if (i < a.k) v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
+    const float s = ldexpf(v, rs);
+    const _Float16 h = (_Float16)s;
+    xh[i] = h;
+    xl[i] = (_Float16)(s - (float)h);
+  }
+  if (tid == 0) a.xscale[t] = __builtin_isfinite(mx) ? ldexpf(1.0f, -rs) : __int_as_float(0x7fc00000);
+}
+
+// ---- dequant-fused GEMM ----------------------------------------------------------
+
+// y[t][n] (=|+=) sum_k x[t][k] W[n][k] for a kGM x kGT tile. Four waves, each
+// a 32 x 32 quarter (2 x 2 MFMA tiles of 16 x 16, three products each).
+template <int T>
+__global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
+  extern __shared__ __align__(16) _Float16 gsm[];
+  _Float16* wh = gsm;
+  _Float16* wl = wh + kGM * kGS;
+  _Float16* xh = wl + kGM * kGS;
+  _Float16* xl = xh + kGT * kGS;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * kGT;
+  const int U = a.w.k >> 5;
+  const int nstage = (a.w.k + kGK - 1) / kGK;
+  // staging roles: weight unit (row wr, unit j of the stage); x quarter row
+  const int wr = tid >> 2, wj = tid & 3;
+  const int xt = tid >> 2, xq = tid & 3;
+  const bool w_ok = n0 + wr < a.w.n;
+  const bool x_ok = t0 + xt < a.t;
+  const float wsc = ldexpf(1.0f, a.ws);
+
+  float4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int rb = (wave & 1) * 32, tb = (wave >> 1) * 32;
+
+  Frag<T> f{};
+  uint4 xv[8];
+  auto fetch = [&](int s) {
+    const int u = s * 4 + wj;
+    if (w_ok && u < U) f = load_unit<T>(a.w, n0 + wr, u);
+    if (x_ok) {
+      const uint4* ph = (const uint4*)(a.xh + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
+      const uint4* pl = (const uint4*)(a.xl + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        xv[v] = ph[v];
+        xv[4 + v] = pl[v];
+      }
+    }
+  };
+  fetch(0);
+  for (int s = 0; s < nstage; ++s) {
+    __syncthreads();  // the previous stage's tiles are consumed
+    {
+      // weights: the unit's 32 values at their K offsets, hi and lo
+      const int u = s * 4 + wj;
+      float v[32];
+      if (w_ok && u < U) {
+        dequant_unit<T>(f, u, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e] = 0.f;
+      }
+      _Float16* rh = wh + wr * kGS;
+      _Float16* rl = wl + wr * kGS;
+#pragma unroll
+      for (int e = 0; e < 32; e += 4) {
+        const int kk = (u < U ? unit_col<T>(u, e) : 32 * u + e) - s * kGK;
+        half4_t h, l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sv = v[e + i] * wsc;
+          h[i] = (_Float16)sv;
+          l[i] = (_Float16)(sv - (float)h[i]);
+        }
+        *(half4_t*)(rh + kk) = h;
+        *(half4_t*)(rl + kk) = l;
+      }
+      // activations: 32 halves of each plane
+      uint4* dh = (uint4*)(xh + xt * kGS + xq * 32);
+      uint4* dl = (uint4*)(xl + xt * kGS + xq * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        dh[q] = x_ok ? xv[q] : make_uint4(0u, 0u, 0u, 0u);
+        dl[q] = x_ok ? xv[4 + q] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    __syncthreads();
+    if (s + 1 < nstage) fetch(s + 1);
+    const int col = lane & 15, kq = (lane >> 4) * 4;
+#pragma unroll
+    for (int ks = 0; ks < kGK / 16; ++ks) {
+      half4_t ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ah[i] = *(const half4_t*)(wh + (rb + 16 * i + col) * kGS + ks * 16 + kq);
+        al[i] = *(const half4_t*)(wl + (rb + 16 * i + col) * kGS + ks * 16 + kq);
+        bh[i] = *(const half4_t*)(xh + (tb + 16 * i + col) * kGS + ks * 16 + kq);
+        bl[i] = *(const half4_t*)(xl + (tb + 16 * i + col) * kGS + ks * 16 + kq);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma16(ah[i], bh[j], acc[i][j]);
+          acc[i][j] = mfma16(ah[i], bl[j], acc[i][j]);
+          acc[i][j] = mfma16(al[i], bh[j], acc[i][j]);
+        }
+    }
+  }
+  // lane holds rows 4 * (lane / 16) + 0..3 of each row tile, token lane % 16
+  const float wun = ldexpf(1.0f, -a.ws);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = t0 + tb + 16 * j + (lane & 15);
+    if (t >= a.t) continue;
+    const float sc = wun * a.xscale[t];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int n = n0 + rb + 16 * i + 4 * (lane >> 4);
+      float* y = a.y + (size_t)t * a.ldy + n;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (n + q >= a.w.n) break;
+        const float v = acc[i][j][q] * sc;
+        y[q] = a.epi == GEMM_ADD ? __fadd_rn(y[q], v) : v;
+      }
+    }
+  }
+}
+
+// ---- per-token glue ---------------------------------------------------------------
+
+// Embedding rows of the prompt tokens times the embedding scale.
+__global__ __launch_bounds__(kWg) void k_pf_embed(QMat embed, const int32_t* tok, float scale, int k, float* x) {
+  const int t = blockIdx.x;
+  const int id = tok[t];
+  with_type(embed.type, [&]<int TE>() {
+    for (int u = threadIdx.x; u < k / 32; u += kWg) {
+      const Frag<TE> f = load_unit<TE>(embed, id, u);
+      float v[32];
+      dequant_unit<TE>(f, u, v);
+#pragma unroll
+      for (int e = 0; e < 32; ++e) x[(size_t)t * k + unit_col<TE>(u, e)] = __fmul_rn(v[e], scale);
+    }
+  });
+}
+
+// x = clamp(x + RMSNorm(d) * w, +-65000) per token row (the Gemma-3 sandwich
+// residual, as the decode prologue PRO_RES_NORM computes it).
+__global__ __launch_bounds__(kWg) void k_pf_norm_add(const float* d, const float* w, float eps, int k, float* x) {
+  __shared__ float red[8];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* dr = d + (size_t)t * k;
+  float* xr = x + (size_t)t * k;
+  float ss = 0.f;
+  for (int i = tid; i < k; i += kWg) ss += dr[i] * dr[i];
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)k + eps);
+  for (int i = tid; i < k; i += kWg) {
+    const float nd = __fmul_rn(__fmul_rn(dr[i], inv), w[i]);
+    xr[i] = fminf(fmaxf(__fadd_rn(xr[i], nd), -65000.0f), 65000.0f);
+  }
+}
+
+// act = silu(g) * u or gelu_tanh(g) * u per element, then the split of the row
+// into fp16 planes (one workgroup per token row).
+__global__ __launch_bounds__(kWg) void k_pf_glu_split(PfGluArgs a) {
+  __shared__ float red[8];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* g = a.g + (size_t)t * a.k;
+  const float* u = a.u + (size_t)t * a.k;
+  float* y = a.act + (size_t)t * a.k;
+  float mx = 0.f;
+  for (int i = tid; i < a.k; i += kWg) {
+    const float v = a.gelu ? __fmul_rn(gelu_tanh(g[i]), u[i]) : silu_mul(g[i], u[i]);
+    y[i] = v;
+    mx = fmaxf(mx, fabsf(v));
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  (void)frexpf(mx, &e);
+  const int rs = max(min(14 - e, 60), -60);
+  _Float16* xh = a.xh + (size_t)t * a.kpad;
+  _Float16* xl = a.xl + (size_t)t * a.kpad;
+  for (int i = tid; i < a.kpad; i += kWg) {
+    const float s = i < a.k ? ldexpf(y[i], rs) : 0.f;
+    const _Float16 h = (_Float16)s;
+    xh[i] = h;
+    xl[i] = (_Float16)(s - (float)h);
+  }
+  if (tid == 0) a.xscale[t] = __builtin_isfinite(mx) ? ldexpf(1.0f, -rs) : __int_as_float(0x7fc00000);
+}
+
+// Per-head q/k RMSNorm and rotary embedding of every prompt row (position
+// p0 + t), the new k and v into the cache; one wave per head. Same operation
+// order as the decode attention's phase B.
+__global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = a.p0 + t;
+  const int hd = a.hd, half = hd / 2;
+  const int nh = a.heads + a.kv_heads;
+  float* row = a.qkv + (size_t)t * a.ld;
+  const size_t crow = (size_t)pos * hd;
+  for (int hh = wave; hh < nh; hh += 4) {
+    const bool is_k = hh >= a.heads;
+    const int kv = hh - a.heads;
+    float* x = is_k ? row + a.heads * hd + kv * hd : row + hh * hd;
+    float r = 1.0f;
+    if (a.qn_w) {
+      float ss = 0.f;
+      for (int d = lane; d < hd; d += 64) ss += x[d] * x[d];
+      ss = wave_sum(ss);
+      r = 1.0f / sqrtf(ss / (float)hd + a.eps);
+    }
+    const float* w = is_k ? a.kn_w : a.qn_w;
+    // all lanes read their pair before any lane writes
+    float y0[4], y1[4];
+    int ia[4], ib[4];
+    int nd = 0;
+    for (int d = lane; d < half; d += 64, ++nd) {
+      ia[nd] = a.interleaved ? 2 * d : d;
+      ib[nd] = a.interleaved ? 2 * d + 1 : d + half;
+      float x0 = x[ia[nd]], x1 = x[ib[nd]];
+      if (a.qn_w) {
+        x0 = __fmul_rn(__fmul_rn(x0, r), w[ia[nd]]);
+        x1 = __fmul_rn(__fmul_rn(x1, r), w[ib[nd]]);
+      }
+      const float ang = __fmul_rn((float)pos, a.rope_inv[d]);
+      const float co = cosf(ang), si = sinf(ang);
+      y0[nd] = __fsub_rn(__fmul_rn(x0, co), __fmul_rn(x1, si));
+      y1[nd] = __fadd_rn(__fmul_rn(x0, si), __fmul_rn(x1, co));
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int q = 0; q < nd; ++q) {
+      if (is_k) {
+        const size_t base = (size_t)kv * a.ctx * hd + crow;
+        if (a.kv16) {
+          ((__half*)a.kc)[base + ia[q]] = __float2half_rn(y0[q]);
+          ((__half*)a.kc)[base + ib[q]] = __float2half_rn(y1[q]);
+        } else {
+          ((float*)a.kc)[base + ia[q]] = y0[q];
+          ((float*)a.kc)[base + ib[q]] = y1[q];
+        }
+      } else {
+        x[ia[q]] = y0[q];
+        x[ib[q]] = y1[q];
+      }
+    }
+    if (is_k) {
+      const float* vsrc = row + (a.heads + a.kv_heads) * hd + kv * hd;
+      const size_t base = (size_t)kv * a.ctx * hd + crow;
+      for (int d = lane; d < hd; d += 64) {
+        if (a.kv16)
+          ((__half*)a.vc)[base + d] = __float2half_rn(vsrc[d]);
+        else
+          ((float*)a.vc)[base + d] = vsrc[d];
+      }
+    }
+  }
+}
+
+// Causal attention of every prompt row: one workgroup per (token, q head),
+// keys [start, p0 + t] of the cache in blocks of 256 (one per thread), an
+// online softmax across blocks. q is the rotated row left by k_pf_rope_kv.
+__global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
+  __shared__ float qs[256];
+  __shared__ float red[8];
+  __shared__ float wsh[kWg];
+  __shared__ float part[kWg];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int G = a.heads / a.kv_heads, kv = h / G;
+  const int hd = a.hd;
+  const int pos = a.p0 + t;
+  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+  const float* q = a.qkv + (size_t)t * a.ld + h * hd;
+  for (int d = tid; d < hd; d += kWg) qs[d] = q[d];
+  __syncthreads();
+  const size_t head_base = (size_t)kv * a.ctx * hd;
+  float M = -INFINITY, L = 0.f;
+  // output dims: thread tid owns dim (tid % hd) for key slice tid / hd
+  const int nsl = kWg / hd, my_d = tid % hd, my_sl = tid / hd;
+  float o = 0.f;
+  for (int b0 = start; b0 <= pos; b0 += kWg) {
+    const int p = b0 + tid;
+    float s = -INFINITY;
+    if (p <= pos) {
+      float acc = 0.f;
+      if (a.kv16) {
+        const __half* kr = (const __half*)a.kc + head_base + (size_t)p * hd;
+        for (int d = 0; d < hd; d += 8) {
+          const uint4 w4 = *(const uint4*)(kr + d);
+          const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc += qs[d + 2 * i] * h2f(w[i]);
+            acc += qs[d + 2 * i + 1] * h2f(w[i] >> 16);
+          }
+        }
+      } else {
+        const float* kr = (const float*)a.kc + head_base + (size_t)p * hd;
+        for (int d = 0; d < hd; ++d) acc += qs[d] * kr[d];
+      }
+      s = acc * a.scale;
+    }
+    float mb = wave_max(s);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
+    __syncthreads();
+    mb = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float e = p <= pos ? expf(s - mb) : 0.f;
+    wsh[tid] = e;
+    float lb = wave_sum(e);
+    __syncthreads();
+    if ((tid & 63) == 0) red[4 + (tid >> 6)] = lb;
+    __syncthreads();
+    lb = (red[4] + red[5]) + (red[6] + red[7]);
+    const float Mn = fmaxf(M, mb);
+    const float ro = M == -INFINITY ? 0.f : expf(M - Mn), rb = expf(mb - Mn);
+    // weighted V of this block for my dim over my slice of the keys
+    float ob = 0.f;
+    const int nk = min(kWg, pos + 1 - b0);
+    for (int kk = my_sl; kk < nk; kk += nsl) {
+      const size_t vi = head_base + (size_t)(b0 + kk) * hd + my_d;
+      const float vv = a.kv16 ? __half2float(((const __half*)a.vc)[vi]) : ((const float*)a.vc)[vi];
+      ob += wsh[kk] * vv;
+    }
+    part[tid] = ob;
+    __syncthreads();
+    if (tid < hd) {
+      float sb = 0.f;
+      for (int sl = 0; sl < nsl; ++sl) sb += part[sl * hd + tid];
+      o = o * ro + sb * rb;
+    }
+    L = L * ro + lb * rb;
+    M = Mn;
+    __syncthreads();
+  }
+  if (tid < hd) a.out[(size_t)t * a.ldo + h * hd + tid] = o * (1.0f / L);
+}
+
+}  // namespace
+
+// ---- host launchers ----------------------------------------------------------------
+
+size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM + 2 * kGT) * kGS; }
+
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT);
+  const size_t sh = gemm_shared_bytes();
+  switch (a.w.type) {
+    case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_K: hipLaunchKernelGGL(k_gemm<QT_Q5_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q6_K: hipLaunchKernelGGL(k_gemm<QT_Q6_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q8_0: hipLaunchKernelGGL(k_gemm<QT_Q8_0>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_0: hipLaunchKernelGGL(k_gemm<QT_Q5_0>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_1: hipLaunchKernelGGL(k_gemm<QT_Q5_1>, grid, dim3(kWg), sh, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t init_gemm_attributes() {
+  const size_t sh = gemm_shared_bytes();
+  const void* fns[6] = {(const void*)k_gemm<QT_Q4_K>, (const void*)k_gemm<QT_Q5_K>, (const void*)k_gemm<QT_Q6_K>,
+                        (const void*)k_gemm<QT_Q8_0>, (const void*)k_gemm<QT_Q5_0>, (const void*)k_gemm<QT_Q5_1>};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_split, dim3(rows), dim3(kWg), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_pf_embed(const QMat& embed, const int32_t* tok, float scale, int k, float* x, int rows,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_embed, dim3(rows), dim3(kWg), 0, s, embed, tok, scale, k, x);
+  return hipGetLastError();
+}
+hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, float* x, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_norm_add, dim3(rows), dim3(kWg), 0, s, d, w, eps, k, x);
+  return hipGetLastError();
+}
+hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_glu_split, dim3(rows), dim3(kWg), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_rope_kv, dim3(rows), dim3(kWg), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_pf_attn, dim3(rows, a.heads), dim3(kWg), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace chonk

@@ -79,6 +79,11 @@ class LlamaWgslEngine:
                                            C.cast(seen, C.POINTER(C.c_int32)), n_seen, C.byref(out)), self._h)
         return int(out.value)
 
+    def prefill(self, token_ids: Sequence[int]) -> None:
+        """runToken(id, false) for every id, computed as row batches (no logits)."""
+        arr, n = _i32_array(list(token_ids))
+        check(lib().chonk_engine_prefill(self._h, C.cast(arr, C.POINTER(C.c_int32)), n), self._h)
+
     def reset(self) -> None:
         check(lib().chonk_engine_reset(self._h), self._h)
 

@@ -8,6 +8,8 @@
  *   chonk_engine_create            loadLlamaWgslModel + LlamaWgslEngine.create
  *                                  (src/lib/llama-wgsl-runtime.ts:184-240, :669-919)
  *   chonk_engine_run_token         LlamaWgslEngine.runToken (:1025-1150)
+ *   chonk_engine_prefill           the prompt loop of generateLlamaWgsl (:281-288),
+ *                                  runToken(id, false) per token, as row batches
  *   chonk_engine_generate          generateLlamaWgsl (:242-314)
  *   chonk_engine_reset             LlamaWgslEngine.reset (:1011-1019)
  *   chonk_engine_reset_conversation resetLlamaWgslConversation (:320-324)
@@ -120,6 +122,13 @@ int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, 
                            const int32_t* penalized, size_t n_penalized, const int32_t* seen, size_t n_seen,
                            int32_t* out_token);
 
+/* Appends tokens[0, n) to the context without computing logits, with the
+ * result of n calls of run_token(token, need_logits = 0) (the reference's
+ * prompt loop, generateLlamaWgsl :281-288), computed as row batches: the
+ * linear layers as dequant-fused MFMA GEMMs and a causal attention over the
+ * cache. generate uses the same pass for all but the last prompt token. */
+int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n);
+
 /* generateLlamaWgsl: prefix reuse against the previous conversation, prompt
  * prefill, then up to max_new_tokens generated ids (stopping after an EOS
  * id), all on the device without a per-token host round trip. A negative
@@ -191,6 +200,12 @@ int chonk_dequant(int32_t device, uint32_t ggml_type, const void* blocks, int64_
  * and stores the mean microseconds in *avg_us. */
 int chonk_matvec(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
                  const float* x, float* y, int32_t reps, double* avg_us);
+/* Y[T,N] = X[T,K] W[N,K]^T with the batched pass's GEMM (fp16 hi/lo operand
+ * split on the matrix cores, fp32 accumulation); x and y are row-major. When
+ * reps > 0 also times `reps` launches (the operand split included) and
+ * stores the mean microseconds in *avg_us. */
+int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
+               const float* x, int64_t n_tokens, float* y, int32_t reps, double* avg_us);
 
 /* Model files --------------------------------------------------------------- */
 typedef struct {

@@ -195,3 +195,45 @@ def test_shard_directory_load(synth, tmp_path):
         need = i == len(prompt) - 1
         assert a.run_token(t, need) == b.run_token(t, need)
     np.testing.assert_array_equal(a.read_logits(), b.read_logits())
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_batched_prefill_matches_token_steps(name, synth):
+    """chonk_engine_prefill leaves the K/V rows, position and next-token logits
+    of the reference's token-by-token prompt loop (oracle)."""
+    w, loaded, ref = _pair(synth, name)
+    eng = loaded.engine
+    prompt = _prompt(w, seed=12, n=min(40, w.prompt_tokens + 9))
+    eng.prefill(prompt[:-1])
+    for t in prompt[:-1]:
+        ref.run_token(t, False)
+    assert eng.position == ref.position == len(prompt) - 1
+    n = eng.info["kv_heads"] * eng.info["head_dim"]
+    for layer in range(w.spec.layers):
+        for pos in (0, len(prompt) // 2, len(prompt) - 2):
+            for is_v in (False, True):
+                g = eng.read_kv(layer, is_v, pos)
+                r = ref.read_kv(layer, is_v, pos, n)
+                assert np.max(np.abs(g - r)) <= np.max(np.abs(r)) * 2e-3 + 1e-6, f"layer {layer} pos {pos} v={is_v}"
+    a = eng.run_token(prompt[-1], True)
+    b = ref.run_token(prompt[-1], True)
+    assert rel_err(eng.read_logits(), ref.logits()) <= 1e-3
+    assert a == b
+
+
+def test_batched_prefill_in_chunks_and_after_context(synth):
+    """A prompt longer than one 512-row pass, appended after earlier tokens."""
+    w, loaded, ref = _pair(synth, "tiny-llama-q8", max_context=1100)
+    eng = loaded.engine
+    head = _prompt(w, seed=13, n=5)
+    for t in head:
+        eng.run_token(t, False)
+        ref.run_token(t, False)
+    body = _prompt(w, seed=14, n=600)
+    eng.prefill(body)
+    for t in body:
+        ref.run_token(t, False)
+    a = eng.run_token(7, True)
+    b = ref.run_token(7, True)
+    assert rel_err(eng.read_logits(), ref.logits()) <= 1e-3
+    assert a == b
