@@ -52,6 +52,7 @@ struct PfAttnArgs {
   int32_t ld;
   float* out;             // [rows][ldo]
   int32_t ldo, heads, kv_heads, hd, ctx, p0, window, kv16;
+  int32_t rows;           // prompt rows of the pass (set by the launcher)
   float scale;
   const void *kc, *vc;
 };

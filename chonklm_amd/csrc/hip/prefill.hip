@@ -412,11 +412,168 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
   if (tid < hd) a.out[(size_t)t * a.ldo + h * hd + tid] = o * (1.0f / L);
 }
 
+// Causal attention of the prompt rows on the matrix cores (fp16 K/V cache):
+// one workgroup per (block of 64 / G tokens, kv head); its 64 query rows
+// (token, q head of the group) are four waves of 16. Per block of 64 keys:
+// S = Q K^T (q split into fp16 hi + lo, K exact), a running softmax per row
+// inside each wave, then O += P V (P split into hi + lo, V exact).
+constexpr int kFaKeys = 64;
+
+template <int HD>
+__global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
+  extern __shared__ __align__(16) _Float16 fsm[];
+  constexpr int KS = HD + 8, VS = kFaKeys + 8, PS = kFaKeys + 8;
+  _Float16* ks = fsm;                         // [64 keys][KS]
+  _Float16* vt = ks + kFaKeys * KS;           // [HD dims][VS]   (V transposed)
+  _Float16* pw = vt + HD * VS;                // [4 waves][2][16 rows][PS]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.heads / a.kv_heads, TW = 64 / G;
+  const int t0 = blockIdx.x * TW, kv = blockIdx.y;
+  const int col = lane & 15, quad = lane >> 4;
+  const __half* kc = (const __half*)a.kc + (size_t)kv * a.ctx * HD;
+  const __half* vc = (const __half*)a.vc + (size_t)kv * a.ctx * HD;
+
+  // this lane's A-operand row of Q (row 16 * wave + col), hi and lo halves
+  half4_t qh[HD / 16], ql[HD / 16];
+  {
+    const int r = 16 * wave + col, t = t0 + r / G;
+    const bool ok = r < TW * G && t < a.rows;
+    const float* q = a.qkv + (size_t)(ok ? t : 0) * a.ld + (kv * G + r % G) * HD;
+#pragma unroll
+    for (int k = 0; k < HD / 16; ++k) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ok ? q[16 * k + 4 * quad + i] : 0.f;
+        qh[k][i] = (_Float16)v;
+        ql[k][i] = (_Float16)(v - (float)qh[k][i]);
+      }
+    }
+  }
+  // rows of this lane's C values: 16 * wave + 4 * quad + i
+  int rpos[4], rstart[4];
+  bool rok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wave + 4 * quad + i, t = t0 + r / G;
+    rok[i] = r < TW * G && t < a.rows;
+    rpos[i] = a.p0 + t;
+    rstart[i] = (a.window != 0 && rpos[i] + 1 > a.window) ? rpos[i] + 1 - a.window : 0;
+  }
+  const int t_last = min(t0 + TW, a.rows) - 1;
+  const int pos_hi = a.p0 + t_last;
+  const int st_lo = (a.window != 0 && a.p0 + t0 + 1 > a.window) ? a.p0 + t0 + 1 - a.window : 0;
+
+  float m_run[4], l_run[4];
+  float4_t o[HD / 16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+#pragma unroll
+  for (int d = 0; d < HD / 16; ++d) o[d] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = st_lo / kFaKeys; kb <= pos_hi / kFaKeys; ++kb) {
+    const int k0 = kb * kFaKeys;
+    __syncthreads();  // the previous block's K / V^T are consumed
+    // K rows and V^T: 16-byte pieces (8 halves), keys past the cache clamped
+    for (int piece = tid; piece < kFaKeys * HD / 8; piece += kWg) {
+      const int key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
+      const size_t row = (size_t)min(k0 + key, a.ctx - 1) * HD;
+      const uint4 kv8 = *(const uint4*)(kc + row + d8);
+      *(uint4*)(ks + key * KS + d8) = kv8;
+      const uint4 vv8 = *(const uint4*)(vc + row + d8);
+      const _Float16* vh = (const _Float16*)&vv8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vt[(d8 + i) * VS + key] = vh[i];
+    }
+    __syncthreads();
+    // S for the wave's 16 rows x 64 keys (four 16 x 16 tiles)
+    float4_t s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < HD / 16; ++k) {
+        const half4_t b = *(const half4_t*)(ks + (16 * kt + col) * KS + 16 * k + 4 * quad);
+        s[kt] = mfma16(qh[k], b, s[kt]);
+        s[kt] = mfma16(ql[k], b, s[kt]);
+      }
+    }
+    // masked, scaled scores; block maximum per row (over the 16 lanes of a row group)
+    float mb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int key = k0 + 16 * kt + col;
+        const bool in = rok[i] && key >= rstart[i] && key <= rpos[i];
+        const float v = in ? s[kt][i] * a.scale : -INFINITY;
+        s[kt][i] = v;
+        m = fmaxf(m, v);
+      }
+      mb[i] = group_max<16>(m);
+    }
+    _Float16* ph = pw + (size_t)wave * 2 * 16 * PS;
+    _Float16* pl = ph + 16 * PS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float mn = fmaxf(m_run[i], mb[i]);
+      const float ro = (m_run[i] == -INFINITY) ? 0.f : expf(m_run[i] - mn);
+      float lb = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const float p = (mn == -INFINITY || s[kt][i] == -INFINITY) ? 0.f : expf(s[kt][i] - mn);
+        lb += p;
+        const _Float16 h = (_Float16)p;
+        ph[(4 * quad + i) * PS + 16 * kt + col] = h;
+        pl[(4 * quad + i) * PS + 16 * kt + col] = (_Float16)(p - (float)h);
+      }
+      lb = group_sum<16>(lb);
+      l_run[i] = l_run[i] * ro + lb;
+      m_run[i] = mn;
+#pragma unroll
+      for (int d = 0; d < HD / 16; ++d) o[d][i] *= ro;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's P rows are in LDS
+    __builtin_amdgcn_wave_barrier();
+    // O += P V over the block's 64 keys
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      const half4_t ah = *(const half4_t*)(ph + col * PS + 16 * kq + 4 * quad);
+      const half4_t al = *(const half4_t*)(pl + col * PS + 16 * kq + 4 * quad);
+#pragma unroll
+      for (int d = 0; d < HD / 16; ++d) {
+        const half4_t b = *(const half4_t*)(vt + (16 * d + col) * VS + 16 * kq + 4 * quad);
+        o[d] = mfma16(ah, b, o[d]);
+        o[d] = mfma16(al, b, o[d]);
+      }
+    }
+  }
+  // out[token][head * HD + dim] for the lane's rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (!rok[i]) continue;
+    const int r = 16 * wave + 4 * quad + i, t = t0 + r / G;
+    float* out = a.out + (size_t)t * a.ldo + (kv * G + r % G) * HD;
+    const float inv = 1.0f / l_run[i];
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d) out[16 * d + col] = o[d][i] * inv;
+  }
+}
+
 }  // namespace
 
 // ---- host launchers ----------------------------------------------------------------
 
 size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM + 2 * kGT) * kGS; }
+
+size_t fattn_shared_bytes(int hd) {
+  return sizeof(_Float16) * ((size_t)kFaKeys * (hd + 8) + (size_t)hd * (kFaKeys + 8) + 4 * 2 * 16 * (kFaKeys + 8));
+}
+
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT);
@@ -439,6 +596,14 @@ hipError_t init_gemm_attributes() {
                         (const void*)k_gemm<QT_Q8_0>, (const void*)k_gemm<QT_Q5_0>, (const void*)k_gemm<QT_Q5_1>};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh);
+    if (e != hipSuccess) return e;
+  }
+  const void* fa[4] = {(const void*)k_pf_fattn<32>, (const void*)k_pf_fattn<64>, (const void*)k_pf_fattn<128>,
+                       (const void*)k_pf_fattn<256>};
+  const int hds[4] = {32, 64, 128, 256};
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e =
+        hipFuncSetAttribute(fa[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)fattn_shared_bytes(hds[i]));
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -466,7 +631,23 @@ hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s) {
   return hipGetLastError();
 }
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
-  hipLaunchKernelGGL(k_pf_attn, dim3(rows, a.heads), dim3(kWg), 0, s, a);
+  const int G = a.heads / a.kv_heads;
+  if (!a.kv16 || G > 16) {
+    hipLaunchKernelGGL(k_pf_attn, dim3(rows, a.heads), dim3(kWg), 0, s, a);
+    return hipGetLastError();
+  }
+  PfAttnArgs b = a;
+  b.rows = rows;
+  const int tw = 64 / G;
+  const dim3 grid((rows + tw - 1) / tw, a.kv_heads);
+  const size_t sh = fattn_shared_bytes(a.hd);
+  switch (a.hd) {
+    case 32: hipLaunchKernelGGL(k_pf_fattn<32>, grid, dim3(kWg), sh, s, b); break;
+    case 64: hipLaunchKernelGGL(k_pf_fattn<64>, grid, dim3(kWg), sh, s, b); break;
+    case 128: hipLaunchKernelGGL(k_pf_fattn<128>, grid, dim3(kWg), sh, s, b); break;
+    case 256: hipLaunchKernelGGL(k_pf_fattn<256>, grid, dim3(kWg), sh, s, b); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
