@@ -321,7 +321,7 @@ struct chonk_engine {
   bool batched_prefill = true;
   void* pf_mem = nullptr;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr,
-        *pf_d = nullptr, *pf_xscale = nullptr;
+        *pf_d = nullptr, *pf_xscale = nullptr, *pf_part = nullptr;
   _Float16 *pf_h = nullptr, *pf_l = nullptr;
   int32_t* pf_tok = nullptr;
   // status
@@ -1335,38 +1335,223 @@ Error device_error(chonk_engine* e, const DevState& st) {
   return Error(CHONK_EHIP, msg);
 }
 
-// ---- batched prompt pass ------------------------------------------------------------
+// ---- row batches: prompt pass and batched decode ---------------------------------------
 
 constexpr int kPrefillRows = 512;  // prompt rows per pass (longer prompts take several)
+constexpr int64_t kPartFloats = (int64_t)4 << 20;  // K-split partial sums
+
+// Device buffers of a row batch (rows <= cap).
+struct RowBufs {
+  float *x = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr, *act = nullptr, *d = nullptr,
+        *xscale = nullptr, *part = nullptr;
+  _Float16 *h = nullptr, *l = nullptr;
+  int32_t* tok = nullptr;
+  int cap = 0;
+};
+
+// Sizes the buffers of `rows` rows for the engine's model; returns the bytes
+// needed and, with base != null, carves them from base.
+size_t row_bufs_layout(const ModelCfg& c, int rows, uint8_t* base, RowBufs* out) {
+  const size_t R = rows;
+  const size_t H = c.hidden, qdim = (size_t)c.heads * c.hd, kvdim = (size_t)c.kv_heads * c.hd, F = c.ffn;
+  const size_t kmax = gemm_kpad((int)std::max(H, std::max(qdim, F)));
+  const size_t sizes[12] = {R * H * 4, R * (qdim + 2 * kvdim) * 4, R * qdim * 4, R * F * 4, R * F * 4, R * F * 4,
+                            R * H * 4, R * 4, (size_t)kPartFloats * 4, R * kmax * 2, R * kmax * 2, R * 4};
+  size_t off = 0;
+  void* ptr[12];
+  for (int i = 0; i < 12; ++i) {
+    ptr[i] = base ? base + off : nullptr;
+    off += align256(sizes[i]);
+  }
+  if (out) {
+    out->x = (float*)ptr[0];
+    out->qkv = (float*)ptr[1];
+    out->att = (float*)ptr[2];
+    out->g = (float*)ptr[3];
+    out->u = (float*)ptr[4];
+    out->act = (float*)ptr[5];
+    out->d = (float*)ptr[6];
+    out->xscale = (float*)ptr[7];
+    out->part = (float*)ptr[8];
+    out->h = (_Float16*)ptr[9];
+    out->l = (_Float16*)ptr[10];
+    out->tok = (int32_t*)ptr[11];
+    out->cap = rows;
+  }
+  return off;
+}
+
+// K/V placement of a row batch: per-layer caches, optionally paged.
+struct RowKv {
+  std::vector<void*> kc, vc;
+  int ctx = 0;
+  const int32_t* pages = nullptr;
+  int max_pages = 0;
+};
+
+// Where the rows sit: positions p0 + row of sequence seq0, or per-row arrays.
+struct RowPlace {
+  int p0 = 0, seq0 = 0;
+  const int32_t* row_seq = nullptr;  // device [rows]
+  const int32_t* row_pos = nullptr;  // device [rows]
+};
+
+// The layers for rows 0..T-1 whose token ids are in b.tok: every layer's K/V
+// of the rows into the cache; with logits != null also the last layer's
+// attention and MLP and the final norm and lm_head of rows [lr0, lr0 + nlr)
+// into logits ([nlr][vocab]). Launches on s; does not synchronize.
+void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlace& pl, int T, float* logits, int lr0,
+              int nlr, hipStream_t s) {
+  const ModelCfg& c = e->cfg;
+  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn;
+  const int ldqkv = qdim + 2 * kvdim;
+  auto split = [&](const float* x, int ld, int k, const float* w, int rows) {
+    PfSplitArgs a{};
+    a.x = x;
+    a.ldx = ld;
+    a.k = k;
+    a.kpad = gemm_kpad(k);
+    a.w = w;
+    a.eps = c.eps;
+    a.xh = b.h;
+    a.xl = b.l;
+    a.xscale = b.xscale;
+    HIP_OK(launch_pf_split(a, rows, s));
+  };
+  auto gemm = [&](const DevMat& m, float* y, int ldy, int epi, int rows) {
+    GemmArgs g{};
+    g.w = m.q;
+    g.xh = b.h;
+    g.xl = b.l;
+    g.xscale = b.xscale;
+    g.y = y;
+    g.ldy = ldy;
+    g.t = rows;
+    g.kpad = gemm_kpad(m.q.k);
+    g.epi = epi;
+    g.ws = m.ws;
+    g.part = b.part;
+    g.part_cap = kPartFloats;
+    HIP_OK(launch_gemm(g, s));
+  };
+  auto kv_addr = [&](int i) {
+    KvAddr k{};
+    k.kc = kvs.kc[i];
+    k.vc = kvs.vc[i];
+    k.ctx = kvs.ctx;
+    k.pages = kvs.pages;
+    k.max_pages = kvs.max_pages;
+    k.seq0 = pl.seq0;
+    k.row_seq = pl.row_seq;
+    k.row_pos = pl.row_pos;
+    k.p0 = pl.p0;
+    return k;
+  };
+  HIP_OK(launch_pf_embed(e->embed.q, b.tok, c.embed_scale, H, b.x, T, s));
+  for (int i = 0; i < c.layers; ++i) {
+    const LayerDev& L = e->layers[i];
+    split(b.x, H, H, L.in_norm, T);
+    gemm(L.q, b.qkv, ldqkv, GEMM_STORE, T);
+    gemm(L.k, b.qkv + qdim, ldqkv, GEMM_STORE, T);
+    gemm(L.v, b.qkv + qdim + kvdim, ldqkv, GEMM_STORE, T);
+    PfRopeArgs r{};
+    r.qkv = b.qkv;
+    r.ld = ldqkv;
+    r.hd = c.hd;
+    r.heads = c.heads;
+    r.kv_heads = c.kv_heads;
+    r.interleaved = c.interleaved ? 1 : 0;
+    r.kv16 = e->kv_elem == 2 ? 1 : 0;
+    r.qn_w = c.qk_norm ? L.q_norm : nullptr;
+    r.kn_w = c.qk_norm ? L.k_norm : nullptr;
+    r.eps = c.qk_eps;
+    r.rope_inv = rope_table(e, c.layer[i].theta, c.hd);
+    r.kv = kv_addr(i);
+    HIP_OK(launch_pf_rope_kv(r, T, s));
+    if (i == c.layers - 1 && !logits) break;  // only the last layer's K/V are needed from it
+    PfAttnArgs at{};
+    at.qkv = b.qkv;
+    at.ld = ldqkv;
+    at.out = b.att;
+    at.ldo = qdim;
+    at.heads = c.heads;
+    at.kv_heads = c.kv_heads;
+    at.hd = c.hd;
+    at.window = c.layer[i].window;
+    at.kv16 = r.kv16;
+    at.scale = c.scale;
+    at.kv = r.kv;
+    HIP_OK(launch_pf_attn(at, T, s));
+    split(b.att, qdim, qdim, nullptr, T);
+    if (c.gemma) {
+      gemm(L.o, b.d, H, GEMM_STORE, T);
+      HIP_OK(launch_pf_norm_add(b.d, L.post_norm, c.eps, H, b.x, T, s));
+    } else {
+      gemm(L.o, b.x, H, GEMM_ADD, T);
+    }
+    split(b.x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm, T);
+    gemm(L.gate, b.g, F, GEMM_STORE, T);
+    gemm(L.up, b.u, F, GEMM_STORE, T);
+    PfGluArgs gl{};
+    gl.g = b.g;
+    gl.u = b.u;
+    gl.act = b.act;
+    gl.k = F;
+    gl.kpad = gemm_kpad(F);
+    gl.gelu = c.gemma ? 1 : 0;
+    gl.xh = b.h;
+    gl.xl = b.l;
+    gl.xscale = b.xscale;
+    HIP_OK(launch_pf_glu_split(gl, T, s));
+    if (c.gemma) {
+      gemm(L.down, b.d, H, GEMM_STORE, T);
+      HIP_OK(launch_pf_norm_add(b.d, L.post_ffn_norm, c.eps, H, b.x, T, s));
+    } else {
+      gemm(L.down, b.x, H, GEMM_ADD, T);
+    }
+  }
+  if (logits) {
+    split(b.x + (size_t)lr0 * H, H, H, e->final_norm, nlr);
+    gemm(e->lm_head, logits, c.vocab, GEMM_STORE, nlr);
+  }
+}
 
 void prefill_alloc(chonk_engine* e) {
   if (e->pf_mem) return;
-  const ModelCfg& c = e->cfg;
-  const size_t R = kPrefillRows;
-  const size_t H = c.hidden, qdim = (size_t)c.heads * c.hd, kvdim = (size_t)c.kv_heads * c.hd, F = c.ffn;
-  const size_t kmax = gemm_kpad((int)std::max(H, std::max(qdim, F)));
-  const size_t sizes[10] = {R * H * 4,    R * (qdim + 2 * kvdim) * 4, R * qdim * 4, R * F * 4, R * F * 4,
-                            R * F * 4,    R * H * 4,                  R * 4,        R * kmax * 2, R * kmax * 2};
-  size_t total = align256(R * 4);
-  for (size_t z : sizes) total += align256(z);
-  HIP_OK(hipMalloc(&e->pf_mem, total));
-  uint8_t* p = (uint8_t*)e->pf_mem;
-  void* out[10];
-  for (int i = 0; i < 10; ++i) {
-    out[i] = p;
-    p += align256(sizes[i]);
-  }
-  e->pf_x = (float*)out[0];
-  e->pf_qkv = (float*)out[1];
-  e->pf_att = (float*)out[2];
-  e->pf_g = (float*)out[3];
-  e->pf_u = (float*)out[4];
-  e->pf_act = (float*)out[5];
-  e->pf_d = (float*)out[6];
-  e->pf_xscale = (float*)out[7];
-  e->pf_h = (_Float16*)out[8];
-  e->pf_l = (_Float16*)out[9];
-  e->pf_tok = (int32_t*)p;
+  RowBufs b;
+  const size_t bytes = row_bufs_layout(e->cfg, kPrefillRows, nullptr, nullptr);
+  HIP_OK(hipMalloc(&e->pf_mem, bytes));
+  row_bufs_layout(e->cfg, kPrefillRows, (uint8_t*)e->pf_mem, &b);
+  e->pf_x = b.x;
+  e->pf_qkv = b.qkv;
+  e->pf_att = b.att;
+  e->pf_g = b.g;
+  e->pf_u = b.u;
+  e->pf_act = b.act;
+  e->pf_d = b.d;
+  e->pf_xscale = b.xscale;
+  e->pf_part = b.part;
+  e->pf_h = b.h;
+  e->pf_l = b.l;
+  e->pf_tok = b.tok;
+}
+
+RowBufs engine_row_bufs(const chonk_engine* e) {
+  RowBufs b;
+  b.x = e->pf_x;
+  b.qkv = e->pf_qkv;
+  b.att = e->pf_att;
+  b.g = e->pf_g;
+  b.u = e->pf_u;
+  b.act = e->pf_act;
+  b.d = e->pf_d;
+  b.xscale = e->pf_xscale;
+  b.part = e->pf_part;
+  b.h = e->pf_h;
+  b.l = e->pf_l;
+  b.tok = e->pf_tok;
+  b.cap = kPrefillRows;
+  return b;
 }
 
 // K/V of every layer for tokens[0, n) at positions e->pos .. e->pos + n - 1,
@@ -1379,111 +1564,21 @@ void prefill_rows(chonk_engine* e, const int32_t* tokens, int n) {
   if ((int64_t)e->pos + n > c.ctx)
     throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
   prefill_alloc(e);
-  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn;
-  const int ldqkv = qdim + 2 * kvdim;
-  hipStream_t s = e->stream;
+  const RowBufs b = engine_row_bufs(e);
+  RowKv kvs;
+  for (const LayerDev& L : e->layers) {
+    kvs.kc.push_back(L.kc);
+    kvs.vc.push_back(L.vc);
+  }
+  kvs.ctx = c.ctx;
   for (int off = 0; off < n; off += kPrefillRows) {
     const int T = std::min(kPrefillRows, n - off);
-    const int p0 = e->pos + off;
-    HIP_OK(hipMemcpyAsync(e->pf_tok, tokens + off, (size_t)T * 4, hipMemcpyHostToDevice, s));
-    auto split = [&](const float* x, int ld, int k, const float* w) {
-      PfSplitArgs a{};
-      a.x = x;
-      a.ldx = ld;
-      a.k = k;
-      a.kpad = gemm_kpad(k);
-      a.w = w;
-      a.eps = c.eps;
-      a.xh = e->pf_h;
-      a.xl = e->pf_l;
-      a.xscale = e->pf_xscale;
-      HIP_OK(launch_pf_split(a, T, s));
-    };
-    auto gemm = [&](const DevMat& m, float* y, int ldy, int epi) {
-      GemmArgs g{};
-      g.w = m.q;
-      g.xh = e->pf_h;
-      g.xl = e->pf_l;
-      g.xscale = e->pf_xscale;
-      g.y = y;
-      g.ldy = ldy;
-      g.t = T;
-      g.kpad = gemm_kpad(m.q.k);
-      g.epi = epi;
-      g.ws = m.ws;
-      HIP_OK(launch_gemm(g, s));
-    };
-    HIP_OK(launch_pf_embed(e->embed.q, e->pf_tok, c.embed_scale, H, e->pf_x, T, s));
-    for (int i = 0; i < c.layers; ++i) {
-      const LayerDev& L = e->layers[i];
-      split(e->pf_x, H, H, L.in_norm);
-      gemm(L.q, e->pf_qkv, ldqkv, GEMM_STORE);
-      gemm(L.k, e->pf_qkv + qdim, ldqkv, GEMM_STORE);
-      gemm(L.v, e->pf_qkv + qdim + kvdim, ldqkv, GEMM_STORE);
-      PfRopeArgs r{};
-      r.qkv = e->pf_qkv;
-      r.ld = ldqkv;
-      r.p0 = p0;
-      r.hd = c.hd;
-      r.heads = c.heads;
-      r.kv_heads = c.kv_heads;
-      r.ctx = c.ctx;
-      r.interleaved = c.interleaved ? 1 : 0;
-      r.kv16 = e->kv_elem == 2 ? 1 : 0;
-      r.qn_w = c.qk_norm ? L.q_norm : nullptr;
-      r.kn_w = c.qk_norm ? L.k_norm : nullptr;
-      r.eps = c.qk_eps;
-      r.rope_inv = rope_table(e, c.layer[i].theta, c.hd);
-      r.kc = L.kc;
-      r.vc = L.vc;
-      HIP_OK(launch_pf_rope_kv(r, T, s));
-      if (i == c.layers - 1) break;  // only the last layer's K/V are needed from it
-      PfAttnArgs at{};
-      at.qkv = e->pf_qkv;
-      at.ld = ldqkv;
-      at.out = e->pf_att;
-      at.ldo = qdim;
-      at.heads = c.heads;
-      at.kv_heads = c.kv_heads;
-      at.hd = c.hd;
-      at.ctx = c.ctx;
-      at.p0 = p0;
-      at.window = c.layer[i].window;
-      at.kv16 = r.kv16;
-      at.scale = c.scale;
-      at.kc = L.kc;
-      at.vc = L.vc;
-      HIP_OK(launch_pf_attn(at, T, s));
-      split(e->pf_att, qdim, qdim, nullptr);
-      if (c.gemma) {
-        gemm(L.o, e->pf_d, H, GEMM_STORE);
-        HIP_OK(launch_pf_norm_add(e->pf_d, L.post_norm, c.eps, H, e->pf_x, T, s));
-      } else {
-        gemm(L.o, e->pf_x, H, GEMM_ADD);
-      }
-      split(e->pf_x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm);
-      gemm(L.gate, e->pf_g, F, GEMM_STORE);
-      gemm(L.up, e->pf_u, F, GEMM_STORE);
-      PfGluArgs gl{};
-      gl.g = e->pf_g;
-      gl.u = e->pf_u;
-      gl.act = e->pf_act;
-      gl.k = F;
-      gl.kpad = gemm_kpad(F);
-      gl.gelu = c.gemma ? 1 : 0;
-      gl.xh = e->pf_h;
-      gl.xl = e->pf_l;
-      gl.xscale = e->pf_xscale;
-      HIP_OK(launch_pf_glu_split(gl, T, s));
-      if (c.gemma) {
-        gemm(L.down, e->pf_d, H, GEMM_STORE);
-        HIP_OK(launch_pf_norm_add(e->pf_d, L.post_ffn_norm, c.eps, H, e->pf_x, T, s));
-      } else {
-        gemm(L.down, e->pf_x, H, GEMM_ADD);
-      }
-    }
+    HIP_OK(hipMemcpyAsync(b.tok, tokens + off, (size_t)T * 4, hipMemcpyHostToDevice, e->stream));
+    RowPlace pl;
+    pl.p0 = e->pos + off;
+    run_rows(e, b, kvs, pl, T, nullptr, 0, 0, e->stream);
   }
-  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipStreamSynchronize(e->stream));
 }
 
 int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
@@ -2220,6 +2315,7 @@ int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n
       _Float16* d_h = (_Float16*)dev((size_t)n_tokens * kpad * 2);
       _Float16* d_l = (_Float16*)dev((size_t)n_tokens * kpad * 2);
       float* d_s = (float*)dev((size_t)n_tokens * 4);
+      float* d_part = (float*)dev((size_t)kPartFloats * 4);
       HIP_OK(hipMemcpy(d_x, x, (size_t)n_tokens * row_len * 4, hipMemcpyHostToDevice));
       PfSplitArgs sa{};
       sa.x = d_x;
@@ -2240,6 +2336,8 @@ int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n
       g.kpad = kpad;
       g.epi = GEMM_STORE;
       g.ws = ws;
+      g.part = d_part;
+      g.part_cap = kPartFloats;
       HIP_OK(init_kernel_attributes());
       HIP_OK(init_gemm_attributes());
       HIP_OK(hipStreamCreate(&s));
@@ -2314,3 +2412,167 @@ int chonk_write_shards(const char* gguf_path, const char* out_dir, uint64_t shar
 }
 
 }  // extern "C"
+
+// ---- batched decoding: independent sequences over one engine's weights ---------------
+
+struct chonk_batch {
+  chonk_engine* e = nullptr;
+  int max_seqs = 0, max_tokens = 0, max_pages = 0, rows_cap = 0;
+  void* kv_mem = nullptr;   // per layer: K pages | V pages, [page][kv_heads][64][hd] fp16
+  void* row_mem = nullptr;  // row buffers, page table, row arrays, logits
+  int32_t *pages = nullptr, *rseq = nullptr, *rpos = nullptr, *next = nullptr;
+  float* logits = nullptr;  // [max(max_seqs, 1)][vocab], rows of the last call
+  int last_rows = 0;
+  RowBufs b;
+  RowKv kvs;
+  std::vector<int> len;     // positions held by each sequence's pages
+};
+
+namespace chonk {
+namespace {
+
+void batch_free(chonk_batch* b) {
+  if (!b) return;
+  if (b->e) (void)hipSetDevice(b->e->device);
+  if (b->e && b->e->stream) (void)hipStreamSynchronize(b->e->stream);
+  if (b->kv_mem) (void)hipFree(b->kv_mem);
+  if (b->row_mem) (void)hipFree(b->row_mem);
+  delete b;
+}
+
+void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** out) {
+  const ModelCfg& c = e->cfg;
+  if (max_seqs <= 0 || max_seqs > 1024 || max_tokens <= 0 || max_tokens > c.ctx)
+    throw Error(CHONK_EINVAL, "batch needs 1..1024 sequences of 1.." + std::to_string(c.ctx) + " tokens");
+  if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
+  if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
+  std::unique_ptr<chonk_batch, void (*)(chonk_batch*)> b(new chonk_batch(), batch_free);
+  b->e = e;
+  b->max_seqs = max_seqs;
+  b->max_tokens = max_tokens;
+  b->max_pages = (max_tokens + kKvPage - 1) / kKvPage;
+  b->rows_cap = std::max(kPrefillRows, max_seqs);
+  b->len.assign((size_t)max_seqs, 0);
+  const size_t n_pages = (size_t)max_seqs * b->max_pages;
+  const size_t pool = align256(n_pages * c.kv_heads * kKvPage * c.hd * 2);
+  HIP_OK(hipMalloc(&b->kv_mem, pool * 2 * c.layers));
+  b->kvs.ctx = max_tokens;
+  b->kvs.max_pages = b->max_pages;
+  for (int i = 0; i < c.layers; ++i) {
+    b->kvs.kc.push_back((uint8_t*)b->kv_mem + pool * 2 * i);
+    b->kvs.vc.push_back((uint8_t*)b->kv_mem + pool * (2 * i + 1));
+  }
+  const size_t rb = row_bufs_layout(c, b->rows_cap, nullptr, nullptr);
+  const size_t tab = align256(n_pages * 4), arr = align256((size_t)b->rows_cap * 4);
+  const size_t lg = align256((size_t)max_seqs * c.vocab * 4);
+  HIP_OK(hipMalloc(&b->row_mem, rb + tab + 3 * arr + lg));
+  uint8_t* p = (uint8_t*)b->row_mem;
+  row_bufs_layout(c, b->rows_cap, p, &b->b);
+  p += rb;
+  b->pages = (int32_t*)p;
+  p += tab;
+  b->rseq = (int32_t*)p;
+  b->rpos = (int32_t*)(p + arr);
+  b->next = (int32_t*)(p + 2 * arr);
+  b->logits = (float*)(p + 3 * arr);
+  // sequence s owns physical pages [s * max_pages, (s + 1) * max_pages)
+  std::vector<int32_t> table(n_pages);
+  for (size_t i = 0; i < n_pages; ++i) table[i] = (int32_t)i;
+  HIP_OK(hipMemcpy(b->pages, table.data(), n_pages * 4, hipMemcpyHostToDevice));
+  b->kvs.pages = b->pages;
+  *out = b.release();
+}
+
+void batch_prefill(chonk_batch* b, int seq, const int32_t* tokens, size_t n, int32_t* next) {
+  chonk_engine* e = b->e;
+  if (seq < 0 || seq >= b->max_seqs) throw Error(CHONK_EINVAL, "sequence index out of range");
+  if (n == 0 || !tokens) throw Error(CHONK_EINVAL, "empty prompt");
+  if ((int64_t)n > b->max_tokens)
+    throw Error(CHONK_ECONTEXT, "batch sequence context exhausted at " + std::to_string(b->max_tokens) + " tokens");
+  for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
+  for (size_t off = 0; off < n; off += kPrefillRows) {
+    const int T = (int)std::min<size_t>(kPrefillRows, n - off);
+    const bool last = off + T == n;
+    HIP_OK(hipMemcpyAsync(b->b.tok, tokens + off, (size_t)T * 4, hipMemcpyHostToDevice, e->stream));
+    RowPlace pl;
+    pl.p0 = (int)off;
+    pl.seq0 = seq;
+    run_rows(e, b->b, b->kvs, pl, T, last ? b->logits : nullptr, T - 1, 1, e->stream);
+  }
+  HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, 1, b->next, e->stream));
+  HIP_OK(hipMemcpyAsync(e->h_tok, b->next, 4, hipMemcpyDeviceToHost, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  b->len[(size_t)seq] = (int)n;
+  b->last_rows = 1;
+  if (next) *next = *e->h_tok;
+}
+
+void batch_step(chonk_batch* b, const int32_t* seqs, const int32_t* tokens, size_t n, int32_t* next) {
+  chonk_engine* e = b->e;
+  if (n == 0 || !seqs || !tokens) throw Error(CHONK_EINVAL, "empty step");
+  if ((int64_t)n > b->max_seqs) throw Error(CHONK_EINVAL, "more rows than sequences");
+  std::vector<int32_t> pos(n);
+  std::vector<bool> used((size_t)b->max_seqs, false);
+  for (size_t i = 0; i < n; ++i) {
+    if (seqs[i] < 0 || seqs[i] >= b->max_seqs) throw Error(CHONK_EINVAL, "sequence index out of range");
+    if (used[(size_t)seqs[i]]) throw Error(CHONK_EINVAL, "a sequence appears twice in one step");
+    used[(size_t)seqs[i]] = true;
+    check_token(e, tokens[i]);
+    pos[i] = b->len[(size_t)seqs[i]];
+    if (pos[i] >= b->max_tokens)
+      throw Error(CHONK_ECONTEXT, "batch sequence context exhausted at " + std::to_string(b->max_tokens) + " tokens");
+  }
+  HIP_OK(hipMemcpyAsync(b->b.tok, tokens, n * 4, hipMemcpyHostToDevice, e->stream));
+  HIP_OK(hipMemcpyAsync(b->rseq, seqs, n * 4, hipMemcpyHostToDevice, e->stream));
+  HIP_OK(hipMemcpyAsync(b->rpos, pos.data(), n * 4, hipMemcpyHostToDevice, e->stream));
+  RowPlace pl;
+  pl.row_seq = b->rseq;
+  pl.row_pos = b->rpos;
+  run_rows(e, b->b, b->kvs, pl, (int)n, b->logits, 0, (int)n, e->stream);
+  HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, (int)n, b->next, e->stream));
+  std::vector<int32_t> out(n);
+  HIP_OK(hipMemcpyAsync(out.data(), b->next, n * 4, hipMemcpyDeviceToHost, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  for (size_t i = 0; i < n; ++i) b->len[(size_t)seqs[i]] += 1;
+  b->last_rows = (int)n;
+  if (next) std::copy(out.begin(), out.end(), next);
+}
+
+}  // namespace
+}  // namespace chonk
+
+int chonk_batch_create(chonk_engine* e, int32_t max_seqs, int32_t max_tokens, chonk_batch** out) {
+  if (!out) return CHONK_EINVAL;
+  *out = nullptr;
+  return api(e, [&] { batch_create(e, max_seqs, max_tokens, out); });
+}
+
+int chonk_batch_destroy(chonk_batch* b) {
+  if (!b) return CHONK_OK;
+  return api(b->e, [&] { batch_free(b); });
+}
+
+int chonk_batch_prefill(chonk_batch* b, int32_t seq, const int32_t* tokens, size_t n, int32_t* next_id) {
+  if (!b) return CHONK_EINVAL;
+  return api(b->e, [&] { batch_prefill(b, seq, tokens, n, next_id); });
+}
+
+int chonk_batch_step(chonk_batch* b, const int32_t* seqs, const int32_t* tokens, size_t n, int32_t* next_ids) {
+  if (!b) return CHONK_EINVAL;
+  return api(b->e, [&] { batch_step(b, seqs, tokens, n, next_ids); });
+}
+
+int chonk_batch_position(const chonk_batch* b, int32_t seq, int32_t* out_pos) {
+  if (!b || !out_pos || seq < 0 || seq >= b->max_seqs) return CHONK_EINVAL;
+  *out_pos = b->len[(size_t)seq];
+  return CHONK_OK;
+}
+
+int chonk_batch_read_logits(chonk_batch* b, int32_t row, float* out, size_t n) {
+  if (!b) return CHONK_EINVAL;
+  return api(b->e, [&] {
+    const size_t V = (size_t)b->e->cfg.vocab;
+    if (row < 0 || row >= b->last_rows || !out || n < V) throw Error(CHONK_EINVAL, "bad logits row or buffer");
+    HIP_OK(hipMemcpy(out, b->logits + (size_t)row * V, V * 4, hipMemcpyDeviceToHost));
+  });
+}

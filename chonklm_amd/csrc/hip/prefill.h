@@ -19,7 +19,25 @@ struct GemmArgs {
   float* y;               // [t][ldy]
   int32_t ldy, t, kpad, epi;
   int32_t ws;             // weight exponent
+  int32_t ksplit;         // K partitions (grid z); > 1 needs `part`
+  float* part;            // [ksplit][t][w.n] partial sums, reduced in order by the launcher
+  int64_t part_cap;       // floats available in part
 };
+
+// Where a row batch's K/V live: the engine's contiguous cache
+// ([kv_heads][ctx][hd] per layer, pages == null), or pages of 64 positions
+// ([page][kv_heads][64][hd]) through a per-sequence page table.
+struct KvAddr {
+  void *kc, *vc;
+  int32_t ctx;
+  const int32_t* pages;   // [seq][max_pages] physical page ids, or null
+  int32_t max_pages;
+  int32_t seq0;           // sequence of every row when row_seq is null
+  const int32_t* row_seq; // [rows] per-row sequence, or null
+  const int32_t* row_pos; // [rows] per-row position, or null (p0 + row)
+  int32_t p0;
+};
+constexpr int kKvPage = 64;
 
 struct PfSplitArgs {
   const float* x;         // [rows][ldx]
@@ -40,21 +58,21 @@ struct PfGluArgs {
 
 struct PfRopeArgs {
   float* qkv;             // [rows][ld]: q | k | v
-  int32_t ld, p0, hd, heads, kv_heads, ctx, interleaved, kv16;
+  int32_t ld, hd, heads, kv_heads, interleaved, kv16;
   const float *qn_w, *kn_w;  // per-head RMSNorm weights (null: none)
   float eps;
   const float* rope_inv;  // [hd/2]
-  void *kc, *vc;          // [kv_heads][ctx][hd]
+  KvAddr kv;
 };
 
 struct PfAttnArgs {
   const float* qkv;       // rotated q rows
   int32_t ld;
   float* out;             // [rows][ldo]
-  int32_t ldo, heads, kv_heads, hd, ctx, p0, window, kv16;
-  int32_t rows;           // prompt rows of the pass (set by the launcher)
+  int32_t ldo, heads, kv_heads, hd, window, kv16;
+  int32_t rows;           // rows of the pass (set by the launcher)
   float scale;
-  const void *kc, *vc;
+  KvAddr kv;
 };
 
 // K padded for the GEMM's activation planes.
@@ -62,6 +80,8 @@ constexpr int gemm_kpad(int k) { return (k + 127) / 128 * 128; }
 
 size_t gemm_shared_bytes();
 hipError_t init_gemm_attributes();
+// Picks the K split for a launch (at least ~256 workgroups when the partial
+// buffer allows) and launches the GEMM and, when split, the ordered reduction.
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_embed(const QMat& embed, const int32_t* tok, float scale, int k, float* x, int rows,
@@ -70,5 +90,7 @@ hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, 
 hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s);
+// Greedy id per row of logits [rows][vocab] (the reference's argmax ordering).
+hipError_t launch_row_argmax(const float* logits, int vocab, int rows, int32_t* out, hipStream_t s);
 
 }  // namespace chonk

@@ -11,6 +11,8 @@
 // the products accumulated in fp32 by v_mfma_f32_16x16x16_f16.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "kernel_common.h"
 #include "kernels.h"
 #include "prefill.h"
@@ -88,7 +90,10 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * kGT;
   const int U = a.w.k >> 5;
-  const int nstage = (a.w.k + kGK - 1) / kGK;
+  const int nst = (a.w.k + kGK - 1) / kGK;
+  // this workgroup's stages: part blockIdx.z of ksplit
+  const int s_lo = (int)((int64_t)nst * blockIdx.z / a.ksplit);
+  const int s_hi = (int)((int64_t)nst * (blockIdx.z + 1) / a.ksplit);
   // staging roles: weight unit (row wr, unit j of the stage); x quarter row
   const int wr = tid >> 2, wj = tid & 3;
   const int xt = tid >> 2, xq = tid & 3;
@@ -118,8 +123,8 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       }
     }
   };
-  fetch(0);
-  for (int s = 0; s < nstage; ++s) {
+  fetch(s_lo);
+  for (int s = s_lo; s < s_hi; ++s) {
     __syncthreads();  // the previous stage's tiles are consumed
     {
       // weights: the unit's 32 values at their K offsets, hi and lo
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       }
     }
     __syncthreads();
-    if (s + 1 < nstage) fetch(s + 1);
+    if (s + 1 < s_hi) fetch(s + 1);
     const int col = lane & 15, kq = (lane >> 4) * 4;
 #pragma unroll
     for (int ks = 0; ks < kGK / 16; ++ks) {
@@ -189,13 +194,29 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
     for (int i = 0; i < 2; ++i) {
       const int n = n0 + rb + 16 * i + 4 * (lane >> 4);
       float* y = a.y + (size_t)t * a.ldy + n;
+      float* pp = a.part + ((size_t)blockIdx.z * a.t + t) * a.w.n + n;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if (n + q >= a.w.n) break;
         const float v = acc[i][j][q] * sc;
-        y[q] = a.epi == GEMM_ADD ? __fadd_rn(y[q], v) : v;
+        if (a.ksplit > 1)
+          pp[q] = v;
+        else
+          y[q] = a.epi == GEMM_ADD ? __fadd_rn(y[q], v) : v;
       }
     }
+  }
+}
+
+// y[t][n] (=|+=) the K-split partial sums, added in split order.
+__global__ __launch_bounds__(kWg) void k_gemm_reduce(GemmArgs a) {
+  const int64_t total = (int64_t)a.t * a.w.n;
+  for (int64_t i = (int64_t)blockIdx.x * kWg + threadIdx.x; i < total; i += (int64_t)gridDim.x * kWg) {
+    float v = a.part[i];
+    for (int z = 1; z < a.ksplit; ++z) v += a.part[(int64_t)z * total + i];
+    const int64_t t = i / a.w.n, n = i - t * a.w.n;
+    float* y = a.y + t * a.ldy + n;
+    *y = a.epi == GEMM_ADD ? __fadd_rn(*y, v) : v;
   }
 }
 
@@ -265,16 +286,24 @@ __global__ __launch_bounds__(kWg) void k_pf_glu_split(PfGluArgs a) {
   if (tid == 0) a.xscale[t] = __builtin_isfinite(mx) ? ldexpf(1.0f, -rs) : __int_as_float(0x7fc00000);
 }
 
+__device__ __forceinline__ int row_pos(const KvAddr& k, int t) { return k.row_pos ? k.row_pos[t] : k.p0 + t; }
+__device__ __forceinline__ int row_seq(const KvAddr& k, int t) { return k.row_seq ? k.row_seq[t] : k.seq0; }
+// element offset of (sequence, kv head, position)'s K/V row
+__device__ __forceinline__ size_t kv_row(const KvAddr& k, int kv_heads, int hd, int seq, int kv, int pos) {
+  if (!k.pages) return ((size_t)kv * k.ctx + pos) * hd;
+  const int page = k.pages[(size_t)seq * k.max_pages + pos / kKvPage];
+  return (((size_t)page * kv_heads + kv) * kKvPage + (pos & (kKvPage - 1))) * hd;
+}
+
 // Per-head q/k RMSNorm and rotary embedding of every prompt row (position
 // p0 + t), the new k and v into the cache; one wave per head. Same operation
 // order as the decode attention's phase B.
 __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = a.p0 + t;
+  const int pos = row_pos(a.kv, t);
   const int hd = a.hd, half = hd / 2;
   const int nh = a.heads + a.kv_heads;
   float* row = a.qkv + (size_t)t * a.ld;
-  const size_t crow = (size_t)pos * hd;
   for (int hh = wave; hh < nh; hh += 4) {
     const bool is_k = hh >= a.heads;
     const int kv = hh - a.heads;
@@ -307,13 +336,13 @@ __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
     __builtin_amdgcn_wave_barrier();
     for (int q = 0; q < nd; ++q) {
       if (is_k) {
-        const size_t base = (size_t)kv * a.ctx * hd + crow;
+        const size_t base = kv_row(a.kv, a.kv_heads, hd, row_seq(a.kv, t), kv, pos);
         if (a.kv16) {
-          ((__half*)a.kc)[base + ia[q]] = __float2half_rn(y0[q]);
-          ((__half*)a.kc)[base + ib[q]] = __float2half_rn(y1[q]);
+          ((__half*)a.kv.kc)[base + ia[q]] = __float2half_rn(y0[q]);
+          ((__half*)a.kv.kc)[base + ib[q]] = __float2half_rn(y1[q]);
         } else {
-          ((float*)a.kc)[base + ia[q]] = y0[q];
-          ((float*)a.kc)[base + ib[q]] = y1[q];
+          ((float*)a.kv.kc)[base + ia[q]] = y0[q];
+          ((float*)a.kv.kc)[base + ib[q]] = y1[q];
         }
       } else {
         x[ia[q]] = y0[q];
@@ -322,12 +351,12 @@ __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
     }
     if (is_k) {
       const float* vsrc = row + (a.heads + a.kv_heads) * hd + kv * hd;
-      const size_t base = (size_t)kv * a.ctx * hd + crow;
+      const size_t base = kv_row(a.kv, a.kv_heads, hd, row_seq(a.kv, t), kv, pos);
       for (int d = lane; d < hd; d += 64) {
         if (a.kv16)
-          ((__half*)a.vc)[base + d] = __float2half_rn(vsrc[d]);
+          ((__half*)a.kv.vc)[base + d] = __float2half_rn(vsrc[d]);
         else
-          ((float*)a.vc)[base + d] = vsrc[d];
+          ((float*)a.kv.vc)[base + d] = vsrc[d];
       }
     }
   }
@@ -344,12 +373,12 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
   const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int G = a.heads / a.kv_heads, kv = h / G;
   const int hd = a.hd;
-  const int pos = a.p0 + t;
+  const int pos = row_pos(a.kv, t);
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
   const float* q = a.qkv + (size_t)t * a.ld + h * hd;
   for (int d = tid; d < hd; d += kWg) qs[d] = q[d];
   __syncthreads();
-  const size_t head_base = (size_t)kv * a.ctx * hd;
+  const size_t head_base = (size_t)kv * a.kv.ctx * hd;
   float M = -INFINITY, L = 0.f;
   // output dims: thread tid owns dim (tid % hd) for key slice tid / hd
   const int nsl = kWg / hd, my_d = tid % hd, my_sl = tid / hd;
@@ -360,7 +389,7 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
     if (p <= pos) {
       float acc = 0.f;
       if (a.kv16) {
-        const __half* kr = (const __half*)a.kc + head_base + (size_t)p * hd;
+        const __half* kr = (const __half*)a.kv.kc + head_base + (size_t)p * hd;
         for (int d = 0; d < hd; d += 8) {
           const uint4 w4 = *(const uint4*)(kr + d);
           const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
@@ -371,7 +400,7 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
           }
         }
       } else {
-        const float* kr = (const float*)a.kc + head_base + (size_t)p * hd;
+        const float* kr = (const float*)a.kv.kc + head_base + (size_t)p * hd;
         for (int d = 0; d < hd; ++d) acc += qs[d] * kr[d];
       }
       s = acc * a.scale;
@@ -395,7 +424,7 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
     const int nk = min(kWg, pos + 1 - b0);
     for (int kk = my_sl; kk < nk; kk += nsl) {
       const size_t vi = head_base + (size_t)(b0 + kk) * hd + my_d;
-      const float vv = a.kv16 ? __half2float(((const __half*)a.vc)[vi]) : ((const float*)a.vc)[vi];
+      const float vv = a.kv16 ? __half2float(((const __half*)a.kv.vc)[vi]) : ((const float*)a.kv.vc)[vi];
       ob += wsh[kk] * vv;
     }
     part[tid] = ob;
@@ -419,7 +448,7 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
 // inside each wave, then O += P V (P split into hi + lo, V exact).
 constexpr int kFaKeys = 64;
 
-template <int HD>
+template <int HD, bool PAGED>
 __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   extern __shared__ __align__(16) _Float16 fsm[];
   constexpr int KS = HD + 8, VS = kFaKeys + 8, PS = kFaKeys + 8;
@@ -428,11 +457,14 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   _Float16* pw = vt + HD * VS;                // [4 waves][2][16 rows][PS]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = a.heads / a.kv_heads, TW = 64 / G;
+  // rows of one workgroup share a sequence: one token per workgroup when
+  // every row has its own
+  const int G = a.heads / a.kv_heads, TW = a.kv.row_seq ? 1 : 64 / G;
   const int t0 = blockIdx.x * TW, kv = blockIdx.y;
   const int col = lane & 15, quad = lane >> 4;
-  const __half* kc = (const __half*)a.kc + (size_t)kv * a.ctx * HD;
-  const __half* vc = (const __half*)a.vc + (size_t)kv * a.ctx * HD;
+  const int seq = row_seq(a.kv, t0);
+  const __half* kc = (const __half*)a.kv.kc;
+  const __half* vc = (const __half*)a.kv.vc;
 
   // this lane's A-operand row of Q (row 16 * wave + col), hi and lo halves
   half4_t qh[HD / 16], ql[HD / 16];
@@ -457,12 +489,12 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   for (int i = 0; i < 4; ++i) {
     const int r = 16 * wave + 4 * quad + i, t = t0 + r / G;
     rok[i] = r < TW * G && t < a.rows;
-    rpos[i] = a.p0 + t;
+    rpos[i] = rok[i] ? row_pos(a.kv, t) : 0;
     rstart[i] = (a.window != 0 && rpos[i] + 1 > a.window) ? rpos[i] + 1 - a.window : 0;
   }
   const int t_last = min(t0 + TW, a.rows) - 1;
-  const int pos_hi = a.p0 + t_last;
-  const int st_lo = (a.window != 0 && a.p0 + t0 + 1 > a.window) ? a.p0 + t0 + 1 - a.window : 0;
+  const int pos_hi = row_pos(a.kv, t_last), pos_lo = row_pos(a.kv, t0);
+  const int st_lo = (a.window != 0 && pos_lo + 1 > a.window) ? pos_lo + 1 - a.window : 0;
 
   float m_run[4], l_run[4];
   float4_t o[HD / 16];
@@ -480,7 +512,13 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
     // K rows and V^T: 16-byte pieces (8 halves), keys past the cache clamped
     for (int piece = tid; piece < kFaKeys * HD / 8; piece += kWg) {
       const int key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
-      const size_t row = (size_t)min(k0 + key, a.ctx - 1) * HD;
+      size_t row;
+      if constexpr (PAGED) {
+        const int page = a.kv.pages[(size_t)seq * a.kv.max_pages + kb];
+        row = (((size_t)page * a.kv_heads + kv) * kKvPage + key) * HD;
+      } else {
+        row = ((size_t)kv * a.kv.ctx + min(k0 + key, a.kv.ctx - 1)) * HD;
+      }
       const uint4 kv8 = *(const uint4*)(kc + row + d8);
       *(uint4*)(ks + key * KS + d8) = kv8;
       const uint4 vv8 = *(const uint4*)(vc + row + d8);
@@ -564,6 +602,35 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   }
 }
 
+// Greedy id of each row of logits: the largest value, the lowest index on
+// ties, NaN never chosen (argmax's better(), llama-wgsl-runtime.ts:3645-3791).
+__global__ __launch_bounds__(kWg) void k_row_argmax(const float* logits, int vocab, int32_t* out) {
+  __shared__ float sv[kWg];
+  __shared__ uint32_t si[kWg];
+  const float* row = logits + (size_t)blockIdx.x * vocab;
+  float bv = kNegBig;
+  uint32_t bi = 0xffffffffu;
+  for (int i = threadIdx.x; i < vocab; i += kWg) {
+    const float v = row[i];
+    if (better(v, (uint32_t)i, bv, bi)) {
+      bv = v;
+      bi = (uint32_t)i;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int stride = kWg / 2; stride >= 1; stride >>= 1) {
+    if ((int)threadIdx.x < stride && better(sv[threadIdx.x + stride], si[threadIdx.x + stride], sv[threadIdx.x],
+                                            si[threadIdx.x])) {
+      sv[threadIdx.x] = sv[threadIdx.x + stride];
+      si[threadIdx.x] = si[threadIdx.x + stride];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = si[0] == 0xffffffffu ? 0 : (int32_t)si[0];
+}
+
 }  // namespace
 
 // ---- host launchers ----------------------------------------------------------------
@@ -575,8 +642,17 @@ size_t fattn_shared_bytes(int hd) {
 }
 
 
-hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT);
+hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
+  GemmArgs a = a0;
+  const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
+  const int nst = (a.w.k + kGK - 1) / kGK;
+  a.ksplit = 1;
+  if (a.part && tiles < 256) {
+    int ks = std::min(nst, (256 + tiles - 1) / tiles);
+    while (ks > 1 && (int64_t)ks * a.t * a.w.n > a.part_cap) --ks;
+    a.ksplit = ks;
+  }
+  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, a.ksplit);
   const size_t sh = gemm_shared_bytes();
   switch (a.w.type) {
     case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
@@ -586,6 +662,11 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     case QT_Q5_0: hipLaunchKernelGGL(k_gemm<QT_Q5_0>, grid, dim3(kWg), sh, s, a); break;
     case QT_Q5_1: hipLaunchKernelGGL(k_gemm<QT_Q5_1>, grid, dim3(kWg), sh, s, a); break;
     default: return hipErrorInvalidValue;
+  }
+  if (a.ksplit > 1) {
+    const int64_t total = (int64_t)a.t * a.w.n;
+    const int blocks = (int)std::min<int64_t>((total + kWg - 1) / kWg, 4096);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(kWg), 0, s, a);
   }
   return hipGetLastError();
 }
@@ -598,12 +679,14 @@ hipError_t init_gemm_attributes() {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh);
     if (e != hipSuccess) return e;
   }
-  const void* fa[4] = {(const void*)k_pf_fattn<32>, (const void*)k_pf_fattn<64>, (const void*)k_pf_fattn<128>,
-                       (const void*)k_pf_fattn<256>};
+  const void* fa[8] = {(const void*)k_pf_fattn<32, false>,  (const void*)k_pf_fattn<64, false>,
+                       (const void*)k_pf_fattn<128, false>, (const void*)k_pf_fattn<256, false>,
+                       (const void*)k_pf_fattn<32, true>,   (const void*)k_pf_fattn<64, true>,
+                       (const void*)k_pf_fattn<128, true>,  (const void*)k_pf_fattn<256, true>};
   const int hds[4] = {32, 64, 128, 256};
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     const hipError_t e =
-        hipFuncSetAttribute(fa[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)fattn_shared_bytes(hds[i]));
+        hipFuncSetAttribute(fa[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)fattn_shared_bytes(hds[i & 3]));
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -633,22 +716,37 @@ hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s) {
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
   const int G = a.heads / a.kv_heads;
   if (!a.kv16 || G > 16) {
+    if (a.kv.pages || a.kv.row_seq) return hipErrorInvalidValue;  // paged rows need the fp16 cache
     hipLaunchKernelGGL(k_pf_attn, dim3(rows, a.heads), dim3(kWg), 0, s, a);
     return hipGetLastError();
   }
   PfAttnArgs b = a;
   b.rows = rows;
-  const int tw = 64 / G;
+  const int tw = a.kv.row_seq ? 1 : 64 / G;
   const dim3 grid((rows + tw - 1) / tw, a.kv_heads);
   const size_t sh = fattn_shared_bytes(a.hd);
+  const bool paged = a.kv.pages != nullptr;
+#define CHONK_FA(H)                                                              \
+  if (paged)                                                                     \
+    hipLaunchKernelGGL((k_pf_fattn<H, true>), grid, dim3(kWg), sh, s, b);        \
+  else                                                                           \
+    hipLaunchKernelGGL((k_pf_fattn<H, false>), grid, dim3(kWg), sh, s, b);
   switch (a.hd) {
-    case 32: hipLaunchKernelGGL(k_pf_fattn<32>, grid, dim3(kWg), sh, s, b); break;
-    case 64: hipLaunchKernelGGL(k_pf_fattn<64>, grid, dim3(kWg), sh, s, b); break;
-    case 128: hipLaunchKernelGGL(k_pf_fattn<128>, grid, dim3(kWg), sh, s, b); break;
-    case 256: hipLaunchKernelGGL(k_pf_fattn<256>, grid, dim3(kWg), sh, s, b); break;
+    case 32: CHONK_FA(32) break;
+    case 64: CHONK_FA(64) break;
+    case 128: CHONK_FA(128) break;
+    case 256: CHONK_FA(256) break;
     default: return hipErrorInvalidValue;
   }
+#undef CHONK_FA
   return hipGetLastError();
 }
 
+}  // namespace chonk
+
+namespace chonk {
+hipError_t launch_row_argmax(const float* logits, int vocab, int rows, int32_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_row_argmax, dim3(rows), dim3(kWg), 0, s, logits, vocab, out);
+  return hipGetLastError();
+}
 }  // namespace chonk

@@ -185,6 +185,59 @@ def load_llama_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = Non
     return LoadedLlamaWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
 
 
+class LlamaWgslBatch:
+    """Independent sequences decoded together over one engine's weights (no
+    counterpart in the reference, which runs one sequence per engine): each
+    sequence has its own paged fp16 K/V cache; a step appends one token to any
+    subset of them and returns their greedy next ids (chonk_batch_*)."""
+
+    def __init__(self, engine: LlamaWgslEngine, max_seqs: int, max_tokens: int):
+        self.engine = engine
+        self.vocab = engine.info["vocab"]
+        h = C.c_void_p()
+        check(lib().chonk_batch_create(engine._h, int(max_seqs), int(max_tokens), C.byref(h)), engine._h)
+        self._h = h
+
+    def prefill(self, seq: int, token_ids: Sequence[int]) -> int:
+        arr, n = _i32_array(list(token_ids))
+        out = C.c_int32()
+        check(lib().chonk_batch_prefill(self._h, int(seq), C.cast(arr, C.POINTER(C.c_int32)), n, C.byref(out)),
+              self.engine._h)
+        return int(out.value)
+
+    def step(self, seqs: Sequence[int], token_ids: Sequence[int]) -> list[int]:
+        s_arr, n = _i32_array(list(seqs))
+        t_arr, m = _i32_array(list(token_ids))
+        if n != m:
+            raise ValueError("seqs and token_ids differ in length")
+        out = (C.c_int32 * max(1, n))()
+        check(lib().chonk_batch_step(self._h, C.cast(s_arr, C.POINTER(C.c_int32)), C.cast(t_arr, C.POINTER(C.c_int32)),
+                                     n, C.cast(out, C.POINTER(C.c_int32))), self.engine._h)
+        return [int(out[i]) for i in range(n)]
+
+    def position(self, seq: int) -> int:
+        v = C.c_int32()
+        check(lib().chonk_batch_position(self._h, int(seq), C.byref(v)))
+        return int(v.value)
+
+    def read_logits(self, row: int) -> np.ndarray:
+        out = np.empty(self.vocab, dtype=np.float32)
+        check(lib().chonk_batch_read_logits(self._h, int(row), out.ctypes.data_as(C.POINTER(C.c_float)), out.size),
+              self.engine._h)
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            check(lib().chonk_batch_destroy(self._h), self.engine._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def generate_llama_wgsl(loaded: LoadedLlamaWgslModel, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None,
                         temperature=None, top_p=None, top_k=None, repetition_penalty=None,
                         on_token: Optional[Callable[[dict], None]] = None,
@@ -276,6 +329,6 @@ def shard_gguf(gguf_path: str, out_dir: str, shard_size: int = 24 * 1024 * 1024,
 
 __all__ = [
     "ChonkError", "LlamaWgslEngine", "LoadedLlamaWgslModel", "ModelDef", "load_llama_wgsl_model",
-    "generate_llama_wgsl", "dispose_llama_wgsl", "reset_llama_wgsl_conversation", "write_synthetic_gguf",
+    "generate_llama_wgsl", "dispose_llama_wgsl", "LlamaWgslBatch", "reset_llama_wgsl_conversation", "write_synthetic_gguf",
     "shard_gguf",
 ]

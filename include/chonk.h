@@ -190,6 +190,25 @@ int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap
  * so that long-context decode can be measured without a full prefill. */
 int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed);
 
+/* Batched decoding (no counterpart in the reference, which runs one sequence
+ * per engine) -----------------------------------------------------------------
+ * Independent sequences over one engine's weights, each with its own paged
+ * fp16 K/V cache (pages of 64 positions); one step advances any subset of the
+ * sequences by one token, every linear layer a dequant-fused MFMA GEMM over
+ * the batch rows. Greedy selection (argmax, no repetition penalty). The
+ * engine's own conversation is not touched. */
+typedef struct chonk_batch chonk_batch;
+int chonk_batch_create(chonk_engine* e, int32_t max_seqs, int32_t max_tokens_per_seq, chonk_batch** out);
+int chonk_batch_destroy(chonk_batch* b);
+/* Starts sequence `seq` over: K/V of the prompt, and the greedy next id. */
+int chonk_batch_prefill(chonk_batch* b, int32_t seq, const int32_t* tokens, size_t n, int32_t* next_id);
+/* Appends tokens[i] to sequence seqs[i] (distinct) for i < n and returns each
+ * sequence's greedy next id in next_ids[i]. */
+int chonk_batch_step(chonk_batch* b, const int32_t* seqs, const int32_t* tokens, size_t n, int32_t* next_ids);
+int chonk_batch_position(const chonk_batch* b, int32_t seq, int32_t* out_pos);
+/* Logits of row `row` of the last prefill (row 0) or step. */
+int chonk_batch_read_logits(chonk_batch* b, int32_t row, float* out, size_t n);
+
 /* Kernel-level entry points (tests) ---------------------------------------
  * GGUF rows are given as raw block bytes in host memory; the call uploads
  * them with the engine's repacking, runs the kernel on `device`, and returns
