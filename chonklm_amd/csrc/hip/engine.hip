@@ -1481,7 +1481,10 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     at.kv16 = r.kv16;
     at.scale = c.scale;
     at.kv = r.kv;
-    HIP_OK(launch_pf_attn(at, T, s));
+    if (pl.row_seq && c.hd >= 64 && c.heads / c.kv_heads <= 8 && kvs.max_pages <= 64)
+      HIP_OK(launch_bd_attn(at, T, b.part, kPartFloats, s));
+    else
+      HIP_OK(launch_pf_attn(at, T, s));
     split(b.att, qdim, qdim, nullptr, T);
     if (c.gemma) {
       gemm(L.o, b.d, H, GEMM_STORE, T);
@@ -2426,6 +2429,7 @@ struct chonk_batch {
   RowBufs b;
   RowKv kvs;
   std::vector<int> len;     // positions held by each sequence's pages
+  std::map<int, hipGraphExec_t> step_graphs;  // one captured step per row count
 };
 
 namespace chonk {
@@ -2435,6 +2439,7 @@ void batch_free(chonk_batch* b) {
   if (!b) return;
   if (b->e) (void)hipSetDevice(b->e->device);
   if (b->e && b->e->stream) (void)hipStreamSynchronize(b->e->stream);
+  for (auto& g : b->step_graphs) (void)hipGraphExecDestroy(g.second);
   if (b->kv_mem) (void)hipFree(b->kv_mem);
   if (b->row_mem) (void)hipFree(b->row_mem);
   delete b;
@@ -2499,7 +2504,7 @@ void batch_prefill(chonk_batch* b, int seq, const int32_t* tokens, size_t n, int
     pl.seq0 = seq;
     run_rows(e, b->b, b->kvs, pl, T, last ? b->logits : nullptr, T - 1, 1, e->stream);
   }
-  HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, 1, b->next, e->stream));
+  HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, 1, b->b.part, b->next, e->stream));
   HIP_OK(hipMemcpyAsync(e->h_tok, b->next, 4, hipMemcpyDeviceToHost, e->stream));
   HIP_OK(hipStreamSynchronize(e->stream));
   b->len[(size_t)seq] = (int)n;
@@ -2525,11 +2530,39 @@ void batch_step(chonk_batch* b, const int32_t* seqs, const int32_t* tokens, size
   HIP_OK(hipMemcpyAsync(b->b.tok, tokens, n * 4, hipMemcpyHostToDevice, e->stream));
   HIP_OK(hipMemcpyAsync(b->rseq, seqs, n * 4, hipMemcpyHostToDevice, e->stream));
   HIP_OK(hipMemcpyAsync(b->rpos, pos.data(), n * 4, hipMemcpyHostToDevice, e->stream));
-  RowPlace pl;
-  pl.row_seq = b->rseq;
-  pl.row_pos = b->rpos;
-  run_rows(e, b->b, b->kvs, pl, (int)n, b->logits, 0, (int)n, e->stream);
-  HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, (int)n, b->next, e->stream));
+  // the step for n rows is captured once (inputs live in fixed device buffers);
+  // CHONK_NO_GRAPH=1 launches it directly (for profilers)
+  if (!e->use_graph) {
+    RowPlace pl;
+    pl.row_seq = b->rseq;
+    pl.row_pos = b->rpos;
+    run_rows(e, b->b, b->kvs, pl, (int)n, b->logits, 0, (int)n, e->stream);
+    HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, (int)n, b->b.part, b->next, e->stream));
+  }
+  auto it = b->step_graphs.find((int)n);
+  if (!e->use_graph) {
+  } else if (it == b->step_graphs.end()) {
+    RowPlace pl;
+    pl.row_seq = b->rseq;
+    pl.row_pos = b->rpos;
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    try {
+      run_rows(e, b->b, b->kvs, pl, (int)n, b->logits, 0, (int)n, e->stream);
+      HIP_OK(launch_row_argmax(b->logits, e->cfg.vocab, (int)n, b->b.part, b->next, e->stream));
+    } catch (...) {
+      (void)hipStreamEndCapture(e->stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    HIP_OK(hipStreamEndCapture(e->stream, &g));
+    hipGraphExec_t x = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_OK(ie);
+    it = b->step_graphs.emplace((int)n, x).first;
+  }
+  if (e->use_graph) HIP_OK(hipGraphLaunch(it->second, e->stream));
   std::vector<int32_t> out(n);
   HIP_OK(hipMemcpyAsync(out.data(), b->next, n * 4, hipMemcpyDeviceToHost, e->stream));
   HIP_OK(hipStreamSynchronize(e->stream));

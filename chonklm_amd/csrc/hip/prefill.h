@@ -90,7 +90,11 @@ hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, 
 hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s);
-// Greedy id per row of logits [rows][vocab] (the reference's argmax ordering).
-hipError_t launch_row_argmax(const float* logits, int vocab, int rows, int32_t* out, hipStream_t s);
+// Decode attention of rows with their own sequences (kv.row_seq) over paged
+// K/V: per-page partials in `part`, then a merge per (row, kv head).
+hipError_t launch_bd_attn(const PfAttnArgs& a, int rows, float* part, int64_t part_cap, hipStream_t s);
+// Greedy id per row of logits [rows][vocab] (the reference's argmax ordering);
+// scratch holds 64 floats per row.
+hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* scratch, int32_t* out, hipStream_t s);
 
 }  // namespace chonk

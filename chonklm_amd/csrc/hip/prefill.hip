@@ -602,15 +602,155 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   }
 }
 
+// Decode attention of batch rows over paged K/V: one workgroup per (page,
+// kv head, row) holds the row's G query heads against the page's (up to) 64
+// positions and leaves a partial [max, sum, acc[hd]] per head; k_bd_merge
+// combines a row's pages. Same arithmetic as the decode attention's chunks
+// and merge, with pages for chunks.
+template <int HD>
+__global__ __launch_bounds__(kWg) void k_bd_attn(PfAttnArgs a, float* part, int max_pages) {
+  __shared__ float q_s[8 * HD];
+  __shared__ float sc[8][kKvPage];
+  __shared__ float red[8][4];
+  __shared__ __align__(16) __half v_s[kKvPage * HD];
+  const int page = blockIdx.x, kv = blockIdx.y, r = blockIdx.z, tid = threadIdx.x;
+  const int G = a.heads / a.kv_heads;
+  const int pos = row_pos(a.kv, r);
+  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+  const int k0 = page * kKvPage;
+  if (k0 > pos || k0 + kKvPage <= start) return;  // page outside [start, pos]
+  const int seq = row_seq(a.kv, r);
+  const int phys = a.kv.pages[(size_t)seq * a.kv.max_pages + page];
+  const __half* kb = (const __half*)a.kv.kc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
+  const __half* vb = (const __half*)a.kv.vc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
+  const float* q = a.qkv + (size_t)r * a.ld + kv * G * HD;
+  lds_dma((const float*)vb, (float*)v_s, kKvPage * HD / 2);  // the page's V rows, in flight
+  for (int i = tid; i < G * HD; i += kWg) q_s[i] = q[i];
+  __syncthreads();
+  // scores: four threads per position, HD / 4 dims each
+  const int key = tid >> 2, part4 = tid & 3;
+  const bool valid = k0 + key >= start && k0 + key <= pos;
+  float s[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) s[g] = 0.f;
+  {
+    const __half* kr = kb + key * HD + part4 * (HD / 4);
+#pragma unroll
+    for (int d = 0; d < HD / 4; d += 8) {
+      const uint4 w4 = *(const uint4*)(kr + d);
+      const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+      float kf[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kf[2 * i] = h2f(w[i]);
+        kf[2 * i + 1] = h2f(w[i] >> 16);
+      }
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if (g < G) {
+          const float* qq = q_s + g * HD + part4 * (HD / 4) + d;
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc += qq[i] * kf[i];
+          s[g] += acc;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    if (g < G) {
+      const float v = group_sum<4>(s[g]);
+      if (part4 == 0) sc[g][key] = valid ? v * a.scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  // per head: max and exp over the page (one wave per head, lanes = positions)
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int g = wave; g < G; g += 4) {
+    const float v = sc[g][lane];
+    const float m = wave_max(v);
+    const float e = v == -INFINITY ? 0.f : expf(v - m);
+    sc[g][lane] = e;
+    const float l = wave_sum(e);
+    if (lane == 0) {
+      red[g][0] = m;
+      red[g][1] = l;
+    }
+  }
+  __syncthreads();
+  // weighted V: thread per (head, dim)
+  const int rowf = attn_rowf(G, HD);
+  float* out = part + (((size_t)r * a.kv_heads + kv) * max_pages + page) * rowf;
+  // only the page's valid positions (other slots may hold anything)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int kl = max(0, start - k0), kh = min(kKvPage - 1, pos - k0);
+  for (int i = tid; i < G * HD; i += kWg) {
+    const int g = i / HD, d = i - g * HD;
+    float acc = 0.f;
+    for (int k = kl; k <= kh; ++k) acc += sc[g][k] * __half2float(v_s[k * HD + d]);
+    out[g * (HD + 2) + 2 + d] = acc;
+  }
+  if (tid < G) {
+    out[tid * (HD + 2)] = red[tid][0];
+    out[tid * (HD + 2) + 1] = red[tid][1];
+  }
+}
+
+// out row r, heads of kv head blockIdx.x: the pages' partials merged (chunk
+// weights exp(m_j - M), normalised by the merged sum).
+template <int HD>
+__global__ __launch_bounds__(kWg) void k_bd_merge(PfAttnArgs a, const float* part, int max_pages) {
+  __shared__ float w[8][64];
+  __shared__ float inv[8];
+  const int kv = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = a.heads / a.kv_heads;
+  const int pos = row_pos(a.kv, r);
+  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+  const int j_lo = start / kKvPage, j_hi = pos / kKvPage;
+  const int n = j_hi - j_lo + 1;
+  const int rowf = attn_rowf(G, HD);
+  const float* base = part + (((size_t)r * a.kv_heads + kv) * max_pages + j_lo) * rowf;
+  for (int g = wave; g < G; g += 4) {
+    float M = -INFINITY;
+    for (int j = lane; j < n; j += 64) M = fmaxf(M, base[(size_t)j * rowf + g * (HD + 2)]);
+    M = wave_max(M);
+    float L = 0.f;
+    for (int j = lane; j < n; j += 64) {
+      const float f = expf(base[(size_t)j * rowf + g * (HD + 2)] - M);
+      if (j < 64) w[g][j] = f;
+      L += base[(size_t)j * rowf + g * (HD + 2) + 1] * f;
+    }
+    L = wave_sum(L);
+    if (lane == 0) inv[g] = 1.0f / L;
+  }
+  __syncthreads();
+  for (int i = tid; i < G * HD; i += kWg) {
+    const int g = i / HD, d = i - g * HD;
+    float acc = 0.f;
+    for (int j = 0; j < n; ++j) {
+      const float f = j < 64 ? w[g][j] : 0.f;
+      acc += base[(size_t)j * rowf + g * (HD + 2) + 2 + d] * f;
+    }
+    a.out[(size_t)r * a.ldo + (kv * G + g) * HD + d] = acc * inv[g];
+  }
+}
+
 // Greedy id of each row of logits: the largest value, the lowest index on
 // ties, NaN never chosen (argmax's better(), llama-wgsl-runtime.ts:3645-3791).
-__global__ __launch_bounds__(kWg) void k_row_argmax(const float* logits, int vocab, int32_t* out) {
+// Stage 1: kArgParts workgroups per row each reduce a slice to (value, id).
+constexpr int kArgParts = 32;
+
+__global__ __launch_bounds__(kWg) void k_row_argmax1(const float* logits, int vocab, float* pv, uint32_t* pi) {
   __shared__ float sv[kWg];
   __shared__ uint32_t si[kWg];
   const float* row = logits + (size_t)blockIdx.x * vocab;
+  const int per = (vocab + kArgParts - 1) / kArgParts;
+  const int lo = blockIdx.y * per, hi = min(vocab, lo + per);
   float bv = kNegBig;
   uint32_t bi = 0xffffffffu;
-  for (int i = threadIdx.x; i < vocab; i += kWg) {
+  for (int i = lo + threadIdx.x; i < hi; i += kWg) {
     const float v = row[i];
     if (better(v, (uint32_t)i, bv, bi)) {
       bv = v;
@@ -628,7 +768,28 @@ __global__ __launch_bounds__(kWg) void k_row_argmax(const float* logits, int voc
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = si[0] == 0xffffffffu ? 0 : (int32_t)si[0];
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x * kArgParts + blockIdx.y] = sv[0];
+    pi[blockIdx.x * kArgParts + blockIdx.y] = si[0];
+  }
+}
+
+// Stage 2: one wave per row over the row's kArgParts candidates.
+__global__ __launch_bounds__(64) void k_row_argmax2(const float* pv, const uint32_t* pi, int32_t* out) {
+  __shared__ float sv[64];
+  __shared__ uint32_t si[64];
+  const int r = blockIdx.x, l = threadIdx.x;
+  sv[l] = l < kArgParts ? pv[r * kArgParts + l] : kNegBig;
+  si[l] = l < kArgParts ? pi[r * kArgParts + l] : 0xffffffffu;
+  __syncthreads();
+  for (int stride = 32; stride >= 1; stride >>= 1) {
+    if (l < stride && better(sv[l + stride], si[l + stride], sv[l], si[l])) {
+      sv[l] = sv[l + stride];
+      si[l] = si[l + stride];
+    }
+    __syncthreads();
+  }
+  if (l == 0) out[r] = si[0] == 0xffffffffu ? 0 : (int32_t)si[0];
 }
 
 }  // namespace
@@ -745,8 +906,40 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
 }  // namespace chonk
 
 namespace chonk {
-hipError_t launch_row_argmax(const float* logits, int vocab, int rows, int32_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(k_row_argmax, dim3(rows), dim3(kWg), 0, s, logits, vocab, out);
+hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* scratch, int32_t* out, hipStream_t s) {
+  float* pv = scratch;
+  uint32_t* pi = (uint32_t*)(scratch + (size_t)rows * kArgParts);
+  hipLaunchKernelGGL(k_row_argmax1, dim3(rows, kArgParts), dim3(kWg), 0, s, logits, vocab, pv, pi);
+  hipLaunchKernelGGL(k_row_argmax2, dim3(rows), dim3(64), 0, s, pv, pi, out);
+  return hipGetLastError();
+}
+}  // namespace chonk
+
+namespace chonk {
+hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t part_cap, hipStream_t s) {
+  PfAttnArgs a = a0;
+  a.rows = rows;
+  const int G = a.heads / a.kv_heads;
+  const int mp = a.kv.max_pages;
+  if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || mp > 64 ||
+      (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap)
+    return hipErrorInvalidValue;
+  const dim3 g1(mp, a.kv_heads, rows), g2(a.kv_heads, rows);
+  switch (a.hd) {
+    case 64:
+      hipLaunchKernelGGL(k_bd_attn<64>, g1, dim3(kWg), 0, s, a, part, mp);
+      hipLaunchKernelGGL(k_bd_merge<64>, g2, dim3(kWg), 0, s, a, part, mp);
+      break;
+    case 128:
+      hipLaunchKernelGGL(k_bd_attn<128>, g1, dim3(kWg), 0, s, a, part, mp);
+      hipLaunchKernelGGL(k_bd_merge<128>, g2, dim3(kWg), 0, s, a, part, mp);
+      break;
+    case 256:
+      hipLaunchKernelGGL(k_bd_attn<256>, g1, dim3(kWg), 0, s, a, part, mp);
+      hipLaunchKernelGGL(k_bd_merge<256>, g2, dim3(kWg), 0, s, a, part, mp);
+      break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 }  // namespace chonk
