@@ -255,14 +255,19 @@ __device__ __forceinline__ void mv_fetch(const SegView& g, const MvLane& m, int 
 
 // Dot products of the lane's rows once the digit planes are ready; cur holds
 // batch 0 (issued by mv_fetch before the input was). Row r's sum lands in
-// res[lg + r * ng].
-template <int T, int UC>
+// res[lg + r * ng]. AHEAD batches are in flight while one is reduced (two for
+// long row streams such as the lm_head, whose batches would otherwise wait
+// on memory one at a time).
+template <int T, int UC, int AHEAD = 1>
 __device__ __forceinline__ void mv_stream(const SegView& g, const MvLane& m, const XqView& x, float* res,
                                           Frag<T> (&cur)[MvShape<T, UC>::N]) {
   constexpr int RB = MvShape<T, UC>::RB, N = MvShape<T, UC>::N;
   const int nrb = max(1, (m.rows + RB - 1) / RB);
   const int nb = m.rows > 0 ? nrb * ((m.ucount + UC - 1) / UC) : 0;
   XU xr[UC];
+  Frag<T> ahead[AHEAD > 1 ? AHEAD - 1 : 1][N];  // batches b + 1 .. b + AHEAD - 1
+#pragma unroll
+  for (int a = 0; a + 1 < AHEAD; ++a) mv_fetch<T, UC>(g, m, 1 + a, ahead[a]);
   for (int b = 0; b < nb; ++b) {
     const int jb = b / nrb, rb = b - jb * nrb;
     if (rb == 0) {
@@ -273,7 +278,7 @@ __device__ __forceinline__ void mv_stream(const SegView& g, const MvLane& m, con
       }
     }
     Frag<T> nxt[N];
-    mv_fetch<T, UC>(g, m, b + 1, nxt);
+    mv_fetch<T, UC>(g, m, b + AHEAD, nxt);
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr) {
       const int r = rb * RB + rr;
@@ -291,8 +296,19 @@ __device__ __forceinline__ void mv_stream(const SegView& g, const MvLane& m, con
         }
       }
     }
+    if constexpr (AHEAD > 1) {
 #pragma unroll
-    for (int q = 0; q < N; ++q) cur[q] = nxt[q];
+      for (int q = 0; q < N; ++q) cur[q] = ahead[0][q];
+#pragma unroll
+      for (int a = 0; a + 2 < AHEAD; ++a)
+#pragma unroll
+        for (int q = 0; q < N; ++q) ahead[a][q] = ahead[a + 1][q];
+#pragma unroll
+      for (int q = 0; q < N; ++q) ahead[AHEAD - 2][q] = nxt[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < N; ++q) cur[q] = nxt[q];
+    }
   }
 }
 

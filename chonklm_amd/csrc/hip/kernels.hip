@@ -179,7 +179,7 @@ __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
 // Rows [t0, t0 + nt) of the segment (2*nt interleaved gate/up rows when GLU).
 // The first weight batch is issued right after the activation staging
 // (weights do not depend on it); mv_stream walks the rest.
-template <int T, int UC, bool GLU>
+template <int T, int UC, bool GLU, int AHEAD>
 __device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0, int nt, const MvLds& l) {
   const MvLane m = mv_lane(g, t0, nt, GLU);
   Frag<T> cur[MvShape<T, UC>::N];
@@ -189,7 +189,7 @@ __device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0
   __syncthreads();
   if (stopped) return false;
   mv_finish(a, l);
-  mv_stream<T, UC>(g, m, xq_view(l.dl, l.xs16, a.k), l.res, cur);
+  mv_stream<T, UC, AHEAD>(g, m, xq_view(l.dl, l.xs16, a.k), l.res, cur);
   return true;
 }
 
@@ -201,6 +201,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
+  constexpr int ahead = EPI == EPI_LOGITS ? 2 : 1;  // the lm_head's long row streams
   // the type is uniform per workgroup, so every thread takes the same branch
   // (the staging and prologue inside hold barriers)
   bool live = false;
@@ -209,9 +210,9 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   const int uc = mv_uc(g);
   with_type(g.w.type, [&]<int T>() {
     if (uc == 1) {
-      live = mv_work<T, 1, glu>(p, g, t0, nt, l);
+      live = mv_work<T, 1, glu, ahead>(p, g, t0, nt, l);
     } else {
-      live = mv_work<T, 2, glu>(p, g, t0, nt, l);
+      live = mv_work<T, 2, glu, ahead>(p, g, t0, nt, l);
     }
   });
   if (!live) return;

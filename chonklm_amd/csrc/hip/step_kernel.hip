@@ -258,8 +258,11 @@ __device__ __forceinline__ bool mv_task(const StepArgs& a, const StepPhase& ph, 
   quantize_x(xs, K, l.dl, l.xs16);  // dl / wd are free from here on
   __syncthreads();
 
-  // 4. dot products
-  mv_stream<T, UC>(g, m, xq_view(l.dl, l.xs16, K), l.res, cur);
+  // 4. dot products (the lm_head's long row streams keep two batches in flight)
+  if (ph.epi == EPI_LOGITS)
+    mv_stream<T, UC, 2>(g, m, xq_view(l.dl, l.xs16, K), l.res, cur);
+  else
+    mv_stream<T, UC, 1>(g, m, xq_view(l.dl, l.xs16, K), l.res, cur);
   __syncthreads();
 
   // 5. epilogue
