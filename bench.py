@@ -14,7 +14,10 @@ Also reported:
   step_roofline weight + K/V bytes per token / ms per token vs 8 TB/s;
   q4k_matvec    the Q4_K gate|up matvec's GB/s;
   cpu_baseline  the oracle (CPU restatement of the reference WGSL
-                arithmetic) timed on a bounded sample of the same decode.
+                arithmetic) timed on a bounded sample of the same decode;
+  prefill_*     the prompt pass (row batches on the matrix cores);
+  batched_decode 64 sequences x 512-token prompts, greedy steps over all of
+                them at once (the batched configuration).
 """
 from __future__ import annotations
 
@@ -92,6 +95,32 @@ def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:
                       f"(synthetic K/V), oracle CPU restatement of the reference WGSL arithmetic, {el:.1f} s"}
 
 
+def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: int) -> dict:
+    """The batched-decode configuration: `seqs` independent sequences with a
+    `prompt`-token random prompt each, then greedy steps over all of them at
+    once (one MFMA GEMM per linear layer over the batch rows, paged fp16 K/V)."""
+    from chonklm_amd.runtime import LlamaWgslBatch
+
+    b = LlamaWgslBatch(eng, seqs, prompt + warmup + steps + 1)
+    rng = np.random.default_rng(7)
+    t0 = time.perf_counter()
+    cur = [b.prefill(s, rng.integers(0, vocab, prompt).tolist()) for s in range(seqs)]
+    prefill_s = time.perf_counter() - t0
+    rows = list(range(seqs))
+    for _ in range(warmup):
+        cur = b.step(rows, cur)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        cur = b.step(rows, cur)
+    el = time.perf_counter() - t1
+    b.close()
+    return {"sequences": seqs, "prompt_tokens": prompt, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(1000.0 * el / steps, 4),
+            "tokens_per_sec": round(seqs * steps / el, 1),
+            "prefill_tokens_per_sec": round(seqs * prompt / prefill_s, 1),
+            "note": "host-timed, step = one greedy token for every sequence"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,6 +136,7 @@ def main() -> int:
                     help="fill the K/V cache with synthetic values instead of prefilling the prompt "
                          "(profiling runs: the trace then holds decode steps only)")
     ap.add_argument("--model-cache", default=os.environ.get("CHONK_MODEL_CACHE", "/tmp/chonk_models"))
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode measurement")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first run 4 device-to-device copies of MIB MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -251,6 +281,8 @@ def main() -> int:
         "model_build_s": round(build_s, 1),
         "cpu_baseline": None,
     }
+    if not args.no_batched and info.get("kv_dtype", 0) == 0:
+        result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4)
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         result["cpu_baseline"] = cpu_baseline(path, w, pos0, args.cpu_seconds, threads)

@@ -1201,9 +1201,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   build_steps(e.get());
   e->step_logits = e->kernels_logits;
   e->step_plain = e->kernels_plain;
-  // the persistent step is the default; CHONK_STEP=0 keeps the per-phase kernels
+  // the per-phase kernels (one graph per step) are the default; CHONK_STEP=1
+  // selects the persistent step kernel
   const char* sv = std::getenv("CHONK_STEP");
-  if (!(sv && sv[0] == '0')) build_step(e.get());
+  if (sv && sv[0] == '1') build_step(e.get());
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
   e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0);
@@ -2461,6 +2462,7 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
   const size_t n_pages = (size_t)max_seqs * b->max_pages;
   const size_t pool = align256(n_pages * c.kv_heads * kKvPage * c.hd * 2);
   HIP_OK(hipMalloc(&b->kv_mem, pool * 2 * c.layers));
+  HIP_OK(hipMemset(b->kv_mem, 0, pool * 2 * c.layers));  // finite values in slots not yet written
   b->kvs.ctx = max_tokens;
   b->kvs.max_pages = b->max_pages;
   for (int i = 0; i < c.layers; ++i) {

@@ -509,7 +509,9 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   for (int kb = st_lo / kFaKeys; kb <= pos_hi / kFaKeys; ++kb) {
     const int k0 = kb * kFaKeys;
     __syncthreads();  // the previous block's K / V^T are consumed
-    // K rows and V^T: 16-byte pieces (8 halves), keys past the cache clamped
+    // K rows and V^T: 16-byte pieces (8 halves), keys past the cache clamped.
+    // Keys past the block's last position were never written (fresh pages can
+    // hold NaN bit patterns, and P = 0 times NaN is NaN): staged as zeros.
     for (int piece = tid; piece < kFaKeys * HD / 8; piece += kWg) {
       const int key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
       size_t row;
@@ -519,9 +521,10 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
       } else {
         row = ((size_t)kv * a.kv.ctx + min(k0 + key, a.kv.ctx - 1)) * HD;
       }
-      const uint4 kv8 = *(const uint4*)(kc + row + d8);
+      const bool live = k0 + key <= pos_hi;
+      const uint4 kv8 = live ? *(const uint4*)(kc + row + d8) : make_uint4(0u, 0u, 0u, 0u);
       *(uint4*)(ks + key * KS + d8) = kv8;
-      const uint4 vv8 = *(const uint4*)(vc + row + d8);
+      const uint4 vv8 = live ? *(const uint4*)(vc + row + d8) : make_uint4(0u, 0u, 0u, 0u);
       const _Float16* vh = (const _Float16*)&vv8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) vt[(d8 + i) * VS + key] = vh[i];
