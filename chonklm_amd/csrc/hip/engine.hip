@@ -287,6 +287,9 @@ struct chonk_engine {
   int32_t *hist = nullptr, *gen = nullptr;
   uint32_t *pen_bits = nullptr, *seen_bits = nullptr;
   int groups = 0, chunk = 0, nchunk = 0;
+  bool dec_attn = false;          // per-phase attention: k_attn_dec over dnchunk chunks
+  int dnchunk = 0;
+  tagged_t* dpart = nullptr;      // k_attn_dec chunk rows
   std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
   // per-phase kernels of one step (qkv, attn, oproj, gateup, down per layer; lm_head, select)
   std::vector<Launch> kernels_logits, kernels_plain;
@@ -625,6 +628,15 @@ void build_steps(chonk_engine* e) {
       t.tpp = attn_threads_per_position(c.hd, e->chunk, (int)e->kv_elem);
       L.shmem = attn_shared_bytes(G, c.hd, e->chunk, e->nchunk, e->kv_elem);
       L.grid = c.kv_heads * e->nchunk;
+      if (e->dec_attn) {
+        t.variant = 1;
+        t.tpart = e->dpart;
+        t.chunk = attn_dec_chunk();
+        t.nchunk = e->dnchunk;
+        t.merge_floats = attn_merge_floats(G, c.hd, e->dnchunk);
+        L.shmem = attn_dec_shared_bytes(G, c.hd, e->dnchunk);
+        L.grid = c.kv_heads * e->dnchunk;
+      }
       L.name = li + "attn";
       L.layer = i;
       steps.push_back(L);
@@ -866,6 +878,11 @@ bool build_step(chonk_engine* e) {
         if (L.kind == Launch::ATTN && L.layer == i) p.at = L.at;
       p.at.cnt = nullptr;
       p.at.part = nullptr;
+      // the step's own attention geometry (the per-phase kernel may use k_attn_dec's)
+      p.at.variant = 0;
+      p.at.chunk = e->chunk;
+      p.at.nchunk = e->nchunk;
+      p.at.merge_floats = attn_merge_floats(c.heads / c.kv_heads, c.hd, e->nchunk);
       p.n_tasks = c.kv_heads * e->nchunk;
       p.qkv_in = tl[i].qkv;
       p.attn_out = tl[i].att;
@@ -1118,6 +1135,17 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   }
   e->nchunk = (c.ctx + e->chunk - 1) / e->chunk;
   const int G = c.heads / c.kv_heads;
+  // the register-resident decode attention where it applies; CHONK_ATTN=chunked
+  // keeps k_attention
+  {
+    const char* av = std::getenv("CHONK_ATTN");
+    e->dec_attn = attn_dec_supported(G, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) &&
+                  !(av && std::strcmp(av, "chunked") == 0);
+    e->dnchunk = (c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk();
+    if (e->dec_attn &&
+        attn_dec_resident(e->device, G, c.hd, attn_dec_shared_bytes(G, c.hd, e->dnchunk)) < c.kv_heads * e->dnchunk)
+      e->dec_attn = false;
+  }
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
   size_t sbytes = 2 * align256(kv_bytes) * c.layers;
@@ -1125,6 +1153,9 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
             align256((size_t)c.ffn * 4) + align256((size_t)c.vocab * 4) +
             align256((size_t)e->groups * 8) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
             2 * align256((size_t)(c.ctx + 1) * 4) + 2 * align256(bits_words * 4);
+  const size_t dpart_bytes =
+      e->dec_attn ? (size_t)c.kv_heads * e->dnchunk * attn_rowf(G, c.hd) * sizeof(tagged_t) : 0;
+  sbytes += align256(dpart_bytes);
   e->state.reserve(sbytes);
 
   // weights
@@ -1173,12 +1204,13 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->cand = (Candidate*)e->state.take((size_t)e->groups * 8);
   {
     const size_t rowf = ((size_t)G * (c.hd + 2) + 3) & ~(size_t)3;
-    const size_t part_bytes = align256((size_t)c.kv_heads * e->nchunk * rowf * 4);
+    const size_t part_bytes = align256((size_t)c.kv_heads * std::max(e->nchunk, e->dnchunk) * rowf * 4);
     e->uncached = uncached_pool().take(e->device, part_bytes + align256((size_t)c.kv_heads * 4));
     e->part = (float*)e->uncached;
     e->cnt = (uint32_t*)((uint8_t*)e->uncached + part_bytes);
     HIP_OK(hipMemset(e->cnt, 0, (size_t)c.kv_heads * 4));
   }
+  if (e->dec_attn) e->dpart = (tagged_t*)e->state.take(dpart_bytes);
   e->st = (DevState*)e->state.take(sizeof(DevState));
   e->samp = (DevSampling*)e->state.take(sizeof(DevSampling));
   e->hist = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
@@ -1186,6 +1218,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->pen_bits = (uint32_t*)e->state.take(bits_words * 4);
   e->seen_bits = (uint32_t*)e->state.take(bits_words * 4);
   HIP_OK(hipMemset((void*)e->resA, 0, e->state.capacity() - 2 * align256(kv_bytes) * c.layers));
+  // chunk rows start with tag 0xffffffff, which no launch uses (epochs start at 0)
+  if (e->dpart) HIP_OK(hipMemset(e->dpart, 0xff, dpart_bytes));
   for (const LayerDev& L : e->layers) {
     HIP_OK(hipMemset(L.kc, 0, kv_bytes));
     HIP_OK(hipMemset(L.vc, 0, kv_bytes));

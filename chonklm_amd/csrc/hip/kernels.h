@@ -75,7 +75,9 @@ struct AttnArgs {
   void* kc;               // [kv_heads][C][hd], half or float
   void* vc;
   float* part;            // [kv_heads][nchunk] rows of G*(hd+2) floats padded to 4, uncached memory
-  uint32_t* cnt;          // [kv_heads], uncached memory, zero between launches
+  uint32_t* cnt;          // [kv_heads], uncached memory: k_attention's arrival counters (zero
+                          // between launches), k_attn_dec's per-head epochs
+  uint64_t* tpart;        // k_attn_dec: [kv_heads][nchunk] rows of tagged words
   float* out;             // [heads*hd]
   DevState* st;
   int32_t heads, kv_heads, hd, ctx, window, chunk, nchunk;
@@ -84,6 +86,7 @@ struct AttnArgs {
   int32_t merge_floats;   // LDS floats available for staging chunk partials
   int32_t spec_kv;        // request the chunk's K/V before the position is known
   int32_t tpp;            // threads per position in the score phase (power of two)
+  int32_t variant;        // 0: k_attention; 1: k_attn_dec (fp16 cache, 64-position chunks)
   float eps, scale;
 };
 
@@ -200,6 +203,16 @@ hipError_t init_kernel_attributes();
 size_t lds_limit();
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s);
+// The register-resident decode attention (attn_decode.hip): fp16 cache,
+// head_dim 64/128/256, GQA group <= 8 (group x head_dim <= 1536), at most 128
+// chunks of attn_dec_chunk() positions over the context.
+bool attn_dec_supported(int group, int hd, int ctx, int kv_f16);
+int attn_dec_chunk();
+size_t attn_dec_shared_bytes(int group, int hd, int nchunk);
+// Workgroups of k_attn_dec that fit on the device at once (its active chunks
+// wait for each other, so the whole grid must be resident).
+int attn_dec_resident(int device, int group, int hd, size_t shmem);
+hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s);
 hipError_t launch_select(const SelArgs& a, hipStream_t s);
 
 // Test / utility kernels

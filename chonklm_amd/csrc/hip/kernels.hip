@@ -508,6 +508,7 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
 }
 
 hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s) {
+  if (a.variant == 1) return launch_attn_dec(a, shmem, s);
   const int group = a.heads / a.kv_heads;
   const dim3 grid(a.kv_heads, a.nchunk);
 #define CHONK_ATTN_CASE(GG)                                                                  \
