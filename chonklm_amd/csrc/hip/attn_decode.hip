@@ -4,24 +4,27 @@
 //
 // One workgroup per (kv head, chunk of 64 positions); each wave owns 16
 // positions of the chunk and keeps them in registers:
-//   A  the position is requested first, then every load of the workgroup —
-//      q heads of the group, new k/v, norm weights into LDS; the wave's K rows
-//      (four lanes per position, HD/4 dims each) and V rows (HD/64 dims of
-//      each of the 16 positions per lane) into registers — and, while those
-//      are in flight, the lane's rotary cos/sin for the position.
+//   A  the position by a scalar load, then every load of the workgroup: the
+//      wave's K rows (four lanes per position, HD/4 dims each) and V rows
+//      (HD/64 dims of each of the 16 positions per lane) into registers, q
+//      heads of the group, new k/v and norm weights into LDS, and the rotary
+//      (cos, sin) of the position from the engine's table.
 //   B  every wave does the q RMSNorm + rotary of the group into its own LDS
-//      copy (no workgroup barrier); the wave holding the new position also
-//      does k, stores k/v to the cache and replaces its (stale) K/V registers
-//      of that position with the rounded new values.
+//      copy (no workgroup barrier).
 //   C  scores by quads of lanes, softmax statistics over the wave's 16
 //      positions, weights through LDS (broadcast reads), V walked from
-//      registers.
+//      registers — over the cached positions [start, pos); the new position
+//      is not in the cache yet.
 //   D  the four wave partials rescale to the chunk maximum and go to the
 //      chunk's row as tagged words {f32, u32 tag} (no wait); then every active
 //      chunk merges a slice of the output dims: it polls the rows' (max, sum)
 //      words and its dims' acc words until all carry this launch's tag, forms
 //      the weights exp(m_c - M) once per (head, chunk) with the lanes of one
-//      wave, and writes one weighted sum per output element. The chunks of a
+//      wave, and writes one weighted sum per output element. The new position
+//      joins every merge as one more term: while the rows travel, each chunk
+//      normalises, rotates and rounds k (and rounds v) itself, and the
+//      newest chunk stores both to the cache — so no chunk does more work
+//      than another before its row is out. The chunks of a
 //      launch wait for each other, so the engine uses this kernel only when
 //      its whole grid fits on the device at once; every wait is also bounded
 //      in time (DevState.error = 4 past the bound).
@@ -46,17 +49,12 @@ template <>
 struct VRow<1> {
   uint32_t w;
   __device__ void load(const __half* p) { w = (uint32_t)*gbl((const uint16_t*)p); }
-  __device__ void set(const float* f) { w = (uint32_t)__half_as_ushort(__float2half_rn(f[0])); }
   __device__ void get(float* f) const { f[0] = __half2float(__ushort_as_half((unsigned short)w)); }
 };
 template <>
 struct VRow<2> {
   uint32_t w;
   __device__ void load(const __half* p) { w = ldg1(p); }
-  __device__ void set(const float* f) {
-    w = (uint32_t)__half_as_ushort(__float2half_rn(f[0])) |
-        ((uint32_t)__half_as_ushort(__float2half_rn(f[1])) << 16);
-  }
   __device__ void get(float* f) const {
     f[0] = __half2float(__ushort_as_half((unsigned short)(w & 0xffffu)));
     f[1] = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
@@ -66,12 +64,6 @@ template <>
 struct VRow<4> {
   uint2 w;
   __device__ void load(const __half* p) { w = ldg2(p); }
-  __device__ void set(const float* f) {
-    w.x = (uint32_t)__half_as_ushort(__float2half_rn(f[0])) |
-          ((uint32_t)__half_as_ushort(__float2half_rn(f[1])) << 16);
-    w.y = (uint32_t)__half_as_ushort(__float2half_rn(f[2])) |
-          ((uint32_t)__half_as_ushort(__float2half_rn(f[3])) << 16);
-  }
   __device__ void get(float* f) const {
     f[0] = __half2float(__ushort_as_half((unsigned short)(w.x & 0xffffu)));
     f[1] = __half2float(__ushort_as_half((unsigned short)(w.x >> 16)));
@@ -79,6 +71,19 @@ struct VRow<4> {
     f[3] = __half2float(__ushort_as_half((unsigned short)(w.y >> 16)));
   }
 };
+
+__device__ __forceinline__ float2 ldg2f(const float2* p) {
+  const uint2 v = ldg2(p);
+  return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+}
+
+// A load through the scalar unit (own wait counter). For values that do not
+// change while the kernel reads them: written by an earlier kernel, or (the
+// epoch) advanced only after every workgroup that uses it has read it.
+template <class T>
+__device__ __forceinline__ T ld_scalar(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
 
 __device__ __forceinline__ void halves8(const uint4& v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -89,8 +94,12 @@ __device__ __forceinline__ void halves8(const uint4& v, float* f) {
   }
 }
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+// Two floats that are exact fp16 values, packed (truncating conversion).
+__device__ __forceinline__ uint32_t pkrtz(float a, float b) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+  uint32_t u;
+  __builtin_memcpy(&u, &h, 4);
+  return u;
 }
 
 // A wait for chunk rows is bounded (wall clock, 100 MHz): past the bound the
@@ -135,27 +144,14 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   float* wml = ew + 4 * G * kDecWave;
   float* area = wml + 8 * G;
 
-  // A: the position and the epoch first, then every load of the workgroup
+  // A: the position, stop flag and epoch by scalar loads (their own counter,
+  // so nothing below waits on them early), then the vector loads: the rotary
+  // frequencies, the wave's K/V rows, the LDS copies — with the rotary cos/sin
+  // computed while they are in flight
   DevState* st = a.st;
-  const int pos = __builtin_amdgcn_readfirstlane(
-      __hip_atomic_load(&st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  const int stopped = __builtin_amdgcn_readfirstlane(
-      __hip_atomic_load(&st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(
-      __hip_atomic_load(gbl(&a.cnt[kv]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  float inv[NPR];
-#pragma unroll
-  for (int j = 0; j < NPR; ++j) {
-    const int d = lane + 64 * j;
-    inv[j] = d < HALF ? a.rope_inv[d] : 0.f;
-  }
-  lds_dma(a.qkv + (size_t)kv * G * HD, q_s, G * HD);
-  lds_dma(a.qkv + (size_t)a.heads * HD + (size_t)kv * HD, kx, HD);
-  lds_dma(a.qkv + (size_t)(a.heads + a.kv_heads) * HD + (size_t)kv * HD, vx, HD);
-  if (a.qn_w) {
-    lds_dma(a.qn_w, nq, HD);
-    lds_dma(a.kn_w, nk, HD);
-  }
+  const int pos = ld_scalar(&st->pos);
+  const int stopped = ld_scalar(&st->stopped);
+  const uint32_t tag = ld_scalar(&a.cnt[kv]);
   const int t_lo = c * kDecChunk;
   const int kp = kDecWave * wave + (lane >> 2);  // this lane's K position in the chunk
   const int kd0 = (lane & 3) * DPT;
@@ -174,13 +170,23 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     }
   };
   if (a.spec_kv) load_kv();
-  // rotary cos/sin of the lane's pairs while the loads are in flight
+  lds_dma(a.qkv + (size_t)kv * G * HD, q_s, G * HD);
+  lds_dma(a.qkv + (size_t)a.heads * HD + (size_t)kv * HD, kx, HD);
+  lds_dma(a.qkv + (size_t)(a.heads + a.kv_heads) * HD + (size_t)kv * HD, vx, HD);
+  if (a.qn_w) {
+    lds_dma(a.qn_w, nq, HD);
+    lds_dma(a.kn_w, nk, HD);
+  }
+  // rotary (cos, sin) of the lane's pairs at the position
   float co[NPR], si[NPR];
+  {
+    const int pc = min(pos, a.ctx - 1);
 #pragma unroll
-  for (int j = 0; j < NPR; ++j) {
-    const float ang = __fmul_rn((float)pos, inv[j]);
-    co[j] = cosf(ang);
-    si[j] = sinf(ang);
+    for (int j = 0; j < NPR; ++j) {
+      const float2 v = ldg2f(a.rope_cs + (size_t)pc * HALF + min(lane + 64 * j, HALF - 1));
+      co[j] = v.x;
+      si[j] = v.y;
+    }
   }
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
   const int c_lo = start / kDecChunk, c_hi = pos / kDecChunk;
@@ -194,76 +200,63 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     return;
   }
   if (!active) return;
-  const int p_new = pos - t_lo;  // in this chunk only when c == c_hi
 
-  // B: every wave normalises and rotates the group's q heads into its own copy;
-  // the wave holding the new position also does k, stores k/v to the cache and
-  // replaces its (stale) K/V registers of that position
-  auto rope_head = [&](const float* x, const float* w, float* y, bool round16, size_t kv_row) {
-    float r = 1.0f;
+  // B: every wave normalises and rotates the group's q heads into its own copy
+  // (all heads in one pass, so the reductions overlap)
+  int ia[NPR], ib[NPR];
+#pragma unroll
+  for (int j = 0; j < NPR; ++j) {
+    const int d = min(lane + 64 * j, HALF - 1);
+    ia[j] = a.interleaved ? 2 * d : d;
+    ib[j] = a.interleaved ? 2 * d + 1 : d + HALF;
+  }
+  {
+    float x0[G][NPR], x1[G][NPR];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < NPR; ++j) {
+        x0[h][j] = q_s[h * HD + ia[j]];
+        x1[h][j] = q_s[h * HD + ib[j]];
+      }
     if (a.qn_w) {
-      float ss = 0.f;
+      float ss[G];
 #pragma unroll
-      for (int d = lane; d < HD; d += 64) ss += x[d] * x[d];
-      ss = wave_sum(ss);
-      r = 1.0f / sqrtf(ss / (float)HD + a.eps);
-    }
+      for (int h = 0; h < G; ++h) {
+        ss[h] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NPR; ++j) {
-      const int d = lane + 64 * j;
-      if (d < HALF) {
-        const int ia = a.interleaved ? 2 * d : d;
-        const int ib = a.interleaved ? 2 * d + 1 : d + HALF;
-        float x0 = x[ia], x1 = x[ib];
-        if (a.qn_w) {
-          x0 = __fmul_rn(__fmul_rn(x0, r), w[ia]);
-          x1 = __fmul_rn(__fmul_rn(x1, r), w[ib]);
+        for (int j = 0; j < NPR; ++j)
+          if (lane + 64 * j < HALF) ss[h] += x0[h][j] * x0[h][j] + x1[h][j] * x1[h][j];
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) ss[h] = wave_sum(ss[h]);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float r = 1.0f / sqrtf(ss[h] / (float)HD + a.eps);
+#pragma unroll
+        for (int j = 0; j < NPR; ++j) {
+          x0[h][j] = __fmul_rn(__fmul_rn(x0[h][j], r), nq[ia[j]]);
+          x1[h][j] = __fmul_rn(__fmul_rn(x1[h][j], r), nq[ib[j]]);
         }
-        float y0 = __fsub_rn(__fmul_rn(x0, co[j]), __fmul_rn(x1, si[j]));
-        float y1 = __fadd_rn(__fmul_rn(x0, si[j]), __fmul_rn(x1, co[j]));
-        if (round16) {
-          const __half h0 = __float2half_rn(y0), h1 = __float2half_rn(y1);
-          *gblw((unsigned short*)a.kc + kv_row + ia) = __half_as_ushort(h0);
-          *gblw((unsigned short*)a.kc + kv_row + ib) = __half_as_ushort(h1);
-          y0 = __half2float(h0);
-          y1 = __half2float(h1);
-        }
-        y[ia] = y0;
-        y[ib] = y1;
       }
     }
-  };
 #pragma unroll
-  for (int g = 0; g < G; ++g) rope_head(q_s + g * HD, nq, qw + g * HD, false, 0);
-  if (c == c_hi && p_new / kDecWave == wave) {
-    const size_t row = ((size_t)kv * a.ctx + pos) * HD;
-    rope_head(kx, nk, kx, true, row);
+    for (int h = 0; h < G; ++h)
 #pragma unroll
-    for (int d = lane; d < HD; d += 64) {
-      const __half vh = __float2half_rn(vx[d]);
-      *gblw((unsigned short*)a.vc + row + d) = __half_as_ushort(vh);
-      vx[d] = __half2float(vh);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rounded k/v are in LDS
-    __builtin_amdgcn_wave_barrier();
-    if (kp == p_new) {
-#pragma unroll
-      for (int v = 0; v < NKV; ++v) {
-        const float* kk = kx + kd0 + 8 * v;
-        kr[v] = make_uint4(pack2(kk[0], kk[1]), pack2(kk[2], kk[3]), pack2(kk[4], kk[5]), pack2(kk[6], kk[7]));
-      }
-    }
-    const int pn = p_new % kDecWave;
-#pragma unroll
-    for (int p = 0; p < kDecWave; ++p)
-      if (p == pn) vr[p].set(vx + lane * DPL);
+      for (int j = 0; j < NPR; ++j)
+        if (lane + 64 * j < HALF) {
+          qw[h * HD + ia[j]] = __fsub_rn(__fmul_rn(x0[h][j], co[j]), __fmul_rn(x1[h][j], si[j]));
+          qw[h * HD + ib[j]] = __fadd_rn(__fmul_rn(x0[h][j], si[j]), __fmul_rn(x1[h][j], co[j]));
+        }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's q copy is in LDS
   __builtin_amdgcn_wave_barrier();
 
   // C: scores, the wave's softmax statistics, weighted V
   const int tk = t_lo + kp;
-  const bool kvalid = tk >= start && tk <= pos;
+  // the new position is not in the registers (its row is written by this
+  // launch): the merge adds it
+  const bool kvalid = tk >= start && tk < pos;
   float s[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) s[g] = 0.f;
@@ -307,9 +300,9 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       const int p = 4 * p4 + i;
       float vf[DPL];
       vr[p].get(vf);
-      // positions outside [start, pos] carry weight 0; their (unwritten)
-      // rows must not reach the sum
-      const bool ok = p0 + p >= start && p0 + p <= pos;
+      // positions outside [start, pos) carry weight 0; their (possibly
+      // unwritten) rows must not reach the sum
+      const bool ok = p0 + p >= start && p0 + p < pos;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float wt = i == 0 ? w4[g].x : i == 1 ? w4[g].y : i == 2 ? w4[g].z : w4[g].w;
@@ -372,6 +365,50 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   float* colv = ml + 2 * G * nact;   // [G][nd][nact]
   float* wts = colv + G * SD * nact; // [G][nact], then 1/L per head in wml
   const int n_ml = 2 * G * nact, n_col = G * nd * nact, total = n_ml + n_col;
+  // the new position, while the rows are on their way: wave 0 normalises,
+  // rotates and rounds k, wave 1 rounds v (the newest chunk also stores both
+  // to the cache); every chunk adds the position to its merge
+  const size_t kv_row = ((size_t)kv * a.ctx + pos) * HD;
+  if (wave == 0) {
+    float x0[NPR], x1[NPR];
+#pragma unroll
+    for (int j = 0; j < NPR; ++j) {
+      x0[j] = kx[ia[j]];
+      x1[j] = kx[ib[j]];
+    }
+    if (a.qn_w) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NPR; ++j)
+        if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
+      ss = wave_sum(ss);
+      const float r = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+      for (int j = 0; j < NPR; ++j) {
+        x0[j] = __fmul_rn(__fmul_rn(x0[j], r), nk[ia[j]]);
+        x1[j] = __fmul_rn(__fmul_rn(x1[j], r), nk[ib[j]]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NPR; ++j)
+      if (lane + 64 * j < HALF) {
+        const __half h0 = __float2half_rn(__fsub_rn(__fmul_rn(x0[j], co[j]), __fmul_rn(x1[j], si[j])));
+        const __half h1 = __float2half_rn(__fadd_rn(__fmul_rn(x0[j], si[j]), __fmul_rn(x1[j], co[j])));
+        if (c == c_hi) {
+          *gblw((unsigned short*)a.kc + kv_row + ia[j]) = __half_as_ushort(h0);
+          *gblw((unsigned short*)a.kc + kv_row + ib[j]) = __half_as_ushort(h1);
+        }
+        kx[ia[j]] = __half2float(h0);
+        kx[ib[j]] = __half2float(h1);
+      }
+  } else if (wave == 1) {
+#pragma unroll
+    for (int d = lane; d < HD; d += 64) {
+      const __half vh = __float2half_rn(vx[d]);
+      if (c == c_hi) *gblw((unsigned short*)a.vc + kv_row + d) = __half_as_ushort(vh);
+      vx[d] = __half2float(vh);
+    }
+  }
   constexpr int NW = 4;  // words per thread per pass
   const uint64_t t0 = wall_clock64();
   bool late = false;
@@ -415,7 +452,13 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       }
     }
   }
+  // (the poll's barriers also publish the rounded k and v)
   for (int g = wave; g < G; g += 4) {
+    // the new position's score with the wave's own copy of q head g
+    float sn = 0.f;
+#pragma unroll
+    for (int d = lane; d < HD; d += 64) sn += qw[g * HD + d] * kx[d];
+    sn = wave_sum(sn) * a.scale;
     float mv[2], lv[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -423,7 +466,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       mv[j] = cc < nact ? ml[(g * nact + cc) * 2] : -INFINITY;
       lv[j] = cc < nact ? ml[(g * nact + cc) * 2 + 1] : 0.f;
     }
-    const float M = wave_max(fmaxf(mv[0], mv[1]));
+    const float M = fmaxf(wave_max(fmaxf(mv[0], mv[1])), sn);
     float L = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -432,8 +475,12 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       if (cc < nact) wts[g * nact + cc] = f;
       L += lv[j] * f;
     }
-    L = wave_sum(L);
-    if (lane == 0) wml[2 * g] = 1.0f / L;
+    const float fn = expf(sn - M);
+    L = wave_sum(L) + fn;
+    if (lane == 0) {
+      wml[2 * g] = 1.0f / L;
+      wml[2 * g + 1] = fn;
+    }
   }
   __syncthreads();
   for (int i = tid; i < G * nd; i += kWg) {
@@ -449,7 +496,8 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       a3 += src[cc + 3] * wv[cc + 3];
     }
     for (; cc < nact; ++cc) a0 += src[cc] * wv[cc];
-    a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = ((a0 + a1) + (a2 + a3)) * wml[2 * g];
+    const float acc = ((a0 + a1) + (a2 + a3)) + wml[2 * g + 1] * vx[d_lo + dd];
+    a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = acc * wml[2 * g];
   }
   if (late && tid == 0) st->error = 4;
   // every producer of this launch has read the tag once all rows carry it:
@@ -477,6 +525,16 @@ size_t attn_dec_shared_bytes(int group, int hd, int nchunk) {
 }
 
 namespace {
+// cs[p][d] = (cos, sin) of the rotary angle p * inv[d], the expression the
+// decode and prompt kernels evaluate inline.
+__global__ __launch_bounds__(kWg) void k_rope_cs(const float* inv, int half, int ctx, float2* cs) {
+  const int64_t i = (int64_t)blockIdx.x * kWg + threadIdx.x;
+  if (i >= (int64_t)ctx * half) return;
+  const int p = (int)(i / half), d = (int)(i % half);
+  const float ang = __fmul_rn((float)p, inv[d]);
+  cs[i] = make_float2(cosf(ang), sinf(ang));
+}
+
 template <int G, int HD>
 const void* dec_fn() {
   return (const void*)k_attn_dec<G, HD>;
@@ -508,6 +566,12 @@ int attn_dec_resident(int device, int group, int hd, size_t shmem) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, kWg, shmem) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
   return per_cu * cus;
+}
+
+hipError_t launch_rope_cs(const float* inv, int half, int ctx, float2* cs, hipStream_t s) {
+  const int64_t n = (int64_t)ctx * half;
+  hipLaunchKernelGGL(k_rope_cs, dim3((unsigned)((n + kWg - 1) / kWg)), dim3(kWg), 0, s, inv, half, ctx, cs);
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s) {

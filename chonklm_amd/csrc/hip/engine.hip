@@ -291,6 +291,7 @@ struct chonk_engine {
   int dnchunk = 0;
   tagged_t* dpart = nullptr;      // k_attn_dec chunk rows
   std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
+  std::vector<std::pair<uint32_t, float2*>> rope_cs;     // theta -> [ctx][hd/2] (cos, sin)
   // per-phase kernels of one step (qkv, attn, oproj, gateup, down per layer; lm_head, select)
   std::vector<Launch> kernels_logits, kernels_plain;
   // what a step replays: the per-phase kernels, or the single persistent step kernel
@@ -534,6 +535,21 @@ const float* rope_table(chonk_engine* e, uint32_t theta, int hd) {
   return p;
 }
 
+// (cos, sin) of every position's rotary angles for one theta, computed on the
+// device with the kernels' own expression (so the values are those the
+// kernels would compute inline).
+const float2* rope_cs_table(chonk_engine* e, uint32_t theta, int hd) {
+  for (const auto& t : e->rope_cs)
+    if (t.first == theta) return t.second;
+  const float* inv = rope_table(e, theta, hd);
+  float2* p = nullptr;
+  HIP_OK(hipMalloc(&p, (size_t)e->cfg.ctx * (hd / 2) * sizeof(float2)));
+  e->rope_cs.emplace_back(theta, p);
+  HIP_OK(launch_rope_cs(inv, hd / 2, e->cfg.ctx, p, e->stream));
+  HIP_OK(hipStreamSynchronize(e->stream));
+  return p;
+}
+
 void build_steps(chonk_engine* e) {
   const ModelCfg& c = e->cfg;
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, G = c.heads / c.kv_heads;
@@ -631,6 +647,7 @@ void build_steps(chonk_engine* e) {
       if (e->dec_attn) {
         t.variant = 1;
         t.tpart = e->dpart;
+        t.rope_cs = rope_cs_table(e, c.layer[i].theta, c.hd);
         t.chunk = attn_dec_chunk();
         t.nchunk = e->dnchunk;
         t.merge_floats = attn_merge_floats(G, c.hd, e->dnchunk);
@@ -1052,6 +1069,7 @@ void engine_free(chonk_engine* e) {
   if (e->tagged) (void)hipFree(e->tagged);
   if (e->d_phases) (void)hipFree(e->d_phases);
   if (e->pf_mem) (void)hipFree(e->pf_mem);
+  for (auto& t : e->rope_cs) (void)hipFree(t.second);
   if (e->h_state) (void)hipHostFree(e->h_state);
   if (e->h_tok) (void)hipHostFree(e->h_tok);
   if (e->h_samp) (void)hipHostFree(e->h_samp);

@@ -78,6 +78,7 @@ struct AttnArgs {
   uint32_t* cnt;          // [kv_heads], uncached memory: k_attention's arrival counters (zero
                           // between launches), k_attn_dec's per-head epochs
   uint64_t* tpart;        // k_attn_dec: [kv_heads][nchunk] rows of tagged words
+  const float2* rope_cs;  // k_attn_dec: [ctx][hd/2] (cos, sin) of the rotary angles
   float* out;             // [heads*hd]
   DevState* st;
   int32_t heads, kv_heads, hd, ctx, window, chunk, nchunk;
@@ -213,6 +214,8 @@ size_t attn_dec_shared_bytes(int group, int hd, int nchunk);
 // wait for each other, so the whole grid must be resident).
 int attn_dec_resident(int device, int group, int hd, size_t shmem);
 hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s);
+// cs[p][d] = (cos, sin)(p * inv[d]) for p < ctx, d < half.
+hipError_t launch_rope_cs(const float* inv, int half, int ctx, float2* cs, hipStream_t s);
 hipError_t launch_select(const SelArgs& a, hipStream_t s);
 
 // Test / utility kernels
