@@ -1400,7 +1400,16 @@ struct RowBufs {
   _Float16 *h = nullptr, *l = nullptr;
   int32_t* tok = nullptr;
   int cap = 0;
+  int64_t part_cap = 0;  // floats in part
 };
+
+// Floats of the partial-sum buffer for `rows` rows: room for every deferred
+// GEMM result of a layer without a K split, and at least kPartFloats.
+int64_t row_part_floats(const ModelCfg& c, int rows) {
+  const int64_t R = rows;
+  const int64_t qkv = (int64_t)(c.heads + 2 * c.kv_heads) * c.hd;
+  return std::max<int64_t>({kPartFloats, R * qkv, 2 * R * c.ffn, R * c.hidden});
+}
 
 // Sizes the buffers of `rows` rows for the engine's model; returns the bytes
 // needed and, with base != null, carves them from base.
@@ -1409,7 +1418,7 @@ size_t row_bufs_layout(const ModelCfg& c, int rows, uint8_t* base, RowBufs* out)
   const size_t H = c.hidden, qdim = (size_t)c.heads * c.hd, kvdim = (size_t)c.kv_heads * c.hd, F = c.ffn;
   const size_t kmax = gemm_kpad((int)std::max(H, std::max(qdim, F)));
   const size_t sizes[12] = {R * H * 4, R * (qdim + 2 * kvdim) * 4, R * qdim * 4, R * F * 4, R * F * 4, R * F * 4,
-                            R * H * 4, R * 4, (size_t)kPartFloats * 4, R * kmax * 2, R * kmax * 2, R * 4};
+                            R * H * 4, R * 4, (size_t)row_part_floats(c, rows) * 4, R * kmax * 2, R * kmax * 2, R * 4};
   size_t off = 0;
   void* ptr[12];
   for (int i = 0; i < 12; ++i) {
@@ -1430,6 +1439,7 @@ size_t row_bufs_layout(const ModelCfg& c, int rows, uint8_t* base, RowBufs* out)
     out->l = (_Float16*)ptr[10];
     out->tok = (int32_t*)ptr[11];
     out->cap = rows;
+    out->part_cap = row_part_floats(c, rows);
   }
   return off;
 }
@@ -1458,7 +1468,9 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
   const ModelCfg& c = e->cfg;
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn;
   const int ldqkv = qdim + 2 * kvdim;
-  auto split = [&](const float* x, int ld, int k, const float* w, int rows) {
+  // split of x into the GEMM operand planes, after the pending residual update
+  // (x += add, or the Gemma-3 sandwich with add_w) when add.p is set
+  auto split = [&](const float* x, int ld, int k, const float* w, int rows, PartSum add, const float* add_w) {
     PfSplitArgs a{};
     a.x = x;
     a.ldx = ld;
@@ -1469,23 +1481,24 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     a.xh = b.h;
     a.xl = b.l;
     a.xscale = b.xscale;
+    a.add = add;
+    a.add_w = add_w;
     HIP_OK(launch_pf_split(a, rows, s));
   };
-  auto gemm = [&](const DevMat& m, float* y, int ldy, int epi, int rows) {
+  // GEMM of the operand planes with the result left as partial sums in
+  // part[off, off + cap) (the consumer kernel adds them)
+  auto gemm = [&](const DevMat& m, int rows, int64_t off, int64_t cap) {
     GemmArgs g{};
     g.w = m.q;
     g.xh = b.h;
     g.xl = b.l;
     g.xscale = b.xscale;
-    g.y = y;
-    g.ldy = ldy;
     g.t = rows;
     g.kpad = gemm_kpad(m.q.k);
-    g.epi = epi;
     g.ws = m.ws;
-    g.part = b.part;
-    g.part_cap = kPartFloats;
-    HIP_OK(launch_gemm(g, s));
+    PartSum ps{};
+    HIP_OK(launch_gemm_deferred(g, b.part + off, cap, &ps, s));
+    return ps;
   };
   auto kv_addr = [&](int i) {
     KvAddr k{};
@@ -1500,14 +1513,20 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     k.p0 = pl.p0;
     return k;
   };
+  const int64_t P = b.part_cap;
+  // the partial-sum buffer shared out in proportion to each result's size
+  const int64_t pq = P * qdim / ldqkv, pk = P * kvdim / ldqkv;
   HIP_OK(launch_pf_embed(e->embed.q, b.tok, c.embed_scale, H, b.x, T, s));
+  PartSum pending{};                // the previous layer's ffn_down, not yet added to x
+  const float* pending_w = nullptr; // its Gemma-3 post-ffn norm
   for (int i = 0; i < c.layers; ++i) {
     const LayerDev& L = e->layers[i];
-    split(b.x, H, H, L.in_norm, T);
-    gemm(L.q, b.qkv, ldqkv, GEMM_STORE, T);
-    gemm(L.k, b.qkv + qdim, ldqkv, GEMM_STORE, T);
-    gemm(L.v, b.qkv + qdim + kvdim, ldqkv, GEMM_STORE, T);
+    split(b.x, H, H, L.in_norm, T, pending, pending_w);
+    pending = PartSum{};
     PfRopeArgs r{};
+    r.pq = gemm(L.q, T, 0, pq);
+    r.pk = gemm(L.k, T, pq, pk);
+    r.pv = gemm(L.v, T, pq + pk, P - pq - pk);
     r.qkv = b.qkv;
     r.ld = ldqkv;
     r.hd = c.hd;
@@ -1535,22 +1554,16 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     at.scale = c.scale;
     at.kv = r.kv;
     if (pl.row_seq && c.hd >= 64 && c.heads / c.kv_heads <= 8 && kvs.max_pages <= 64)
-      HIP_OK(launch_bd_attn(at, T, b.part, kPartFloats, s));
+      HIP_OK(launch_bd_attn(at, T, b.part, P, s));
     else
       HIP_OK(launch_pf_attn(at, T, s));
-    split(b.att, qdim, qdim, nullptr, T);
-    if (c.gemma) {
-      gemm(L.o, b.d, H, GEMM_STORE, T);
-      HIP_OK(launch_pf_norm_add(b.d, L.post_norm, c.eps, H, b.x, T, s));
-    } else {
-      gemm(L.o, b.x, H, GEMM_ADD, T);
-    }
-    split(b.x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm, T);
-    gemm(L.gate, b.g, F, GEMM_STORE, T);
-    gemm(L.up, b.u, F, GEMM_STORE, T);
+    split(b.att, qdim, qdim, nullptr, T, PartSum{}, nullptr);
+    const PartSum po = gemm(L.o, T, 0, P);
+    // x += o (Gemma-3: x = clamp(x + RMSNorm(o) * post_norm)), then the ffn norm
+    split(b.x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm, T, po, c.gemma ? L.post_norm : nullptr);
     PfGluArgs gl{};
-    gl.g = b.g;
-    gl.u = b.u;
+    gl.pg = gemm(L.gate, T, 0, P / 2);
+    gl.pu = gemm(L.up, T, P / 2, P - P / 2);
     gl.act = b.act;
     gl.k = F;
     gl.kpad = gemm_kpad(F);
@@ -1559,16 +1572,27 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     gl.xl = b.l;
     gl.xscale = b.xscale;
     HIP_OK(launch_pf_glu_split(gl, T, s));
-    if (c.gemma) {
-      gemm(L.down, b.d, H, GEMM_STORE, T);
-      HIP_OK(launch_pf_norm_add(b.d, L.post_ffn_norm, c.eps, H, b.x, T, s));
-    } else {
-      gemm(L.down, b.x, H, GEMM_ADD, T);
-    }
+    pending = gemm(L.down, T, 0, P);
+    pending_w = c.gemma ? L.post_ffn_norm : nullptr;
   }
   if (logits) {
-    split(b.x + (size_t)lr0 * H, H, H, e->final_norm, nlr);
-    gemm(e->lm_head, logits, c.vocab, GEMM_STORE, nlr);
+    PartSum add = pending;
+    if (add.p) add.p += (int64_t)lr0 * add.n;  // rows [lr0, lr0 + nlr) of the result
+    split(b.x + (size_t)lr0 * H, H, H, e->final_norm, nlr, add, pending_w);
+    GemmArgs g{};
+    g.w = e->lm_head.q;
+    g.xh = b.h;
+    g.xl = b.l;
+    g.xscale = b.xscale;
+    g.y = logits;
+    g.ldy = c.vocab;
+    g.t = nlr;
+    g.kpad = gemm_kpad(e->lm_head.q.k);
+    g.epi = GEMM_STORE;
+    g.ws = e->lm_head.ws;
+    g.part = b.part;
+    g.part_cap = P;
+    HIP_OK(launch_gemm(g, s));
   }
 }
 
@@ -1607,6 +1631,7 @@ RowBufs engine_row_bufs(const chonk_engine* e) {
   b.l = e->pf_l;
   b.tok = e->pf_tok;
   b.cap = kPrefillRows;
+  b.part_cap = row_part_floats(e->cfg, kPrefillRows);
   return b;
 }
 

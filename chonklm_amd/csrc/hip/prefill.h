@@ -22,6 +22,7 @@ struct GemmArgs {
   int32_t ksplit;         // K partitions (grid z); > 1 needs `part`
   float* part;            // [ksplit][t][w.n] partial sums, reduced in order by the launcher
   int64_t part_cap;       // floats available in part
+  int32_t defer;          // 1: always leave partials in part (launch_gemm_deferred)
 };
 
 // Where a row batch's K/V live: the engine's contiguous cache
@@ -39,6 +40,14 @@ struct KvAddr {
 };
 constexpr int kKvPage = 64;
 
+// A GEMM result left as K-split partial sums: value(t, j) = sum over z < ks
+// of p[z * zs + t * n + j], added in z order (the consumer kernel adds them).
+struct PartSum {
+  const float* p;         // null: absent
+  int32_t n, ks;
+  int64_t zs;
+};
+
 struct PfSplitArgs {
   const float* x;         // [rows][ldx]
   int32_t ldx, k, kpad;
@@ -46,10 +55,14 @@ struct PfSplitArgs {
   float eps;
   _Float16 *xh, *xl;      // [rows][kpad]
   float* xscale;          // [rows]
+  // residual update first (x must then be writable): x += add, or with
+  // add_w (the Gemma-3 sandwich) x = clamp(x + RMSNorm(add) * add_w, +-65000)
+  PartSum add;
+  const float* add_w;
 };
 
 struct PfGluArgs {
-  const float *g, *u;     // [rows][k]
+  PartSum pg, pu;         // gate and up rows [rows][k] (deferred GEMM results)
   float* act;             // [rows][k]
   int32_t k, kpad, gelu;
   _Float16 *xh, *xl;
@@ -57,7 +70,8 @@ struct PfGluArgs {
 };
 
 struct PfRopeArgs {
-  float* qkv;             // [rows][ld]: q | k | v
+  float* qkv;             // [rows][ld]: q | k | v (gathered from pq, pk, pv when given)
+  PartSum pq, pk, pv;
   int32_t ld, hd, heads, kv_heads, interleaved, kv16;
   const float *qn_w, *kn_w;  // per-head RMSNorm weights (null: none)
   float eps;
@@ -83,6 +97,10 @@ hipError_t init_gemm_attributes();
 // Picks the K split for a launch (at least ~256 workgroups when the partial
 // buffer allows) and launches the GEMM and, when split, the ordered reduction.
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// The GEMM with its result left as partial sums in `region` (capacity in
+// floats): the K split is chosen as in launch_gemm within the region, and no
+// reduction is launched; *out describes the partials for the consumer.
+hipError_t launch_gemm_deferred(const GemmArgs& a, float* region, int64_t region_cap, PartSum* out, hipStream_t s);
 hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_embed(const QMat& embed, const int32_t* tok, float scale, int k, float* x, int rows,
                            hipStream_t s);

@@ -32,6 +32,35 @@ __device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+constexpr int kMaxDeferSplit = 16;  // K split of a deferred GEMM (loads of a sum issued together)
+
+// Row t of a deferred result, elements j0 + kWg * e for e < 4 (zero past n):
+// every load of the four sums is issued before any is added, so a call costs
+// one memory round trip; the sums add the partials in split order.
+__device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float (&v)[4]) {
+  const float* q = P.p + (int64_t)t * P.n;
+  if (P.ks == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = j0 + kWg * e < P.n ? q[j0 + kWg * e] : 0.f;
+    return;
+  }
+  float w[4][kMaxDeferSplit];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = min(j0 + kWg * e, P.n - 1);
+#pragma unroll
+    for (int z = 0; z < kMaxDeferSplit; ++z) w[e][z] = z < P.ks ? q[(int64_t)z * P.zs + j] : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a = w[e][0];
+#pragma unroll
+    for (int z = 1; z < kMaxDeferSplit; ++z)
+      if (z < P.ks) a += w[e][z];
+    v[e] = j0 + kWg * e < P.n ? a : 0.f;
+  }
+}
+
 // ---- operand split ----------------------------------------------------------------
 
 // One workgroup per token row: optional RMSNorm (x * inv) * w with the
@@ -42,6 +71,42 @@ __global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
   __shared__ float red[8];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float* x = a.x + (size_t)t * a.ldx;
+  if (a.add.p) {
+    float* xw = const_cast<float*>(x);
+    if (a.add_w) {
+      // the branch output goes through x's row first (x is rewritten below)
+      float ss = 0.f;
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+        float d[4];
+        part_row4(a.add, t, i0, d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += d[e] * d[e];
+      }
+      ss = block_sum(ss, red);
+      const float inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+        float d[4];
+        part_row4(a.add, t, i0, d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = i0 + kWg * e;
+          if (i < a.k) {
+            const float nd = __fmul_rn(__fmul_rn(d[e], inv), a.add_w[i]);
+            xw[i] = fminf(fmaxf(__fadd_rn(xw[i], nd), -65000.0f), 65000.0f);
+          }
+        }
+      }
+    } else {
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+        float d[4];
+        part_row4(a.add, t, i0, d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + kWg * e < a.k) xw[i0 + kWg * e] = __fadd_rn(xw[i0 + kWg * e], d[e]);
+      }
+    }
+    __syncthreads();  // the updated row is read back below
+  }
   float inv = 1.0f;
   if (a.w) {
     float ss = 0.f;
@@ -199,7 +264,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       for (int q = 0; q < 4; ++q) {
         if (n + q >= a.w.n) break;
         const float v = acc[i][j][q] * sc;
-        if (a.ksplit > 1)
+        if (a.ksplit > 1 || a.defer)
           pp[q] = v;
         else
           y[q] = a.epi == GEMM_ADD ? __fadd_rn(y[q], v) : v;
@@ -259,14 +324,21 @@ __global__ __launch_bounds__(kWg) void k_pf_norm_add(const float* d, const float
 __global__ __launch_bounds__(kWg) void k_pf_glu_split(PfGluArgs a) {
   __shared__ float red[8];
   const int t = blockIdx.x, tid = threadIdx.x;
-  const float* g = a.g + (size_t)t * a.k;
-  const float* u = a.u + (size_t)t * a.k;
   float* y = a.act + (size_t)t * a.k;
   float mx = 0.f;
-  for (int i = tid; i < a.k; i += kWg) {
-    const float v = a.gelu ? __fmul_rn(gelu_tanh(g[i]), u[i]) : silu_mul(g[i], u[i]);
-    y[i] = v;
-    mx = fmaxf(mx, fabsf(v));
+  for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+    float gv[4], uv[4];
+    part_row4(a.pg, t, i0, gv);
+    part_row4(a.pu, t, i0, uv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = i0 + kWg * e;
+      if (i < a.k) {
+        const float v = a.gelu ? __fmul_rn(gelu_tanh(gv[e]), uv[e]) : silu_mul(gv[e], uv[e]);
+        y[i] = v;
+        mx = fmaxf(mx, fabsf(v));
+      }
+    }
   }
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
@@ -304,6 +376,24 @@ __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
   const int hd = a.hd, half = hd / 2;
   const int nh = a.heads + a.kv_heads;
   float* row = a.qkv + (size_t)t * a.ld;
+  if (a.pq.p) {
+    // the row from the projections' partial sums
+    const int qd = a.heads * hd, kd = a.kv_heads * hd;
+    const PartSum* src[3] = {&a.pq, &a.pk, &a.pv};
+    const int off[3] = {0, qd, qd + kd};
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const PartSum& P = *src[m];
+      for (int i0 = tid; i0 < P.n; i0 += 4 * kWg) {
+        float v[4];
+        part_row4(P, t, i0, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + kWg * e < P.n) row[off[m] + i0 + kWg * e] = v[e];
+      }
+    }
+    __syncthreads();
+  }
   for (int hh = wave; hh < nh; hh += 4) {
     const bool is_k = hh >= a.heads;
     const int kv = hh - a.heads;
@@ -832,6 +922,34 @@ hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
     const int blocks = (int)std::min<int64_t>((total + kWg - 1) / kWg, 4096);
     hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(kWg), 0, s, a);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t region_cap, PartSum* out, hipStream_t s) {
+  GemmArgs a = a0;
+  if ((int64_t)a.t * a.w.n > region_cap) return hipErrorInvalidValue;
+  const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
+  const int nst = (a.w.k + kGK - 1) / kGK;
+  int ks = tiles < 256 ? std::min(std::min(nst, kMaxDeferSplit), (256 + tiles - 1) / tiles) : 1;
+  while (ks > 1 && (int64_t)ks * a.t * a.w.n > region_cap) --ks;
+  a.ksplit = ks;
+  a.part = region;
+  a.defer = 1;
+  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, ks);
+  const size_t sh = gemm_shared_bytes();
+  switch (a.w.type) {
+    case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_K: hipLaunchKernelGGL(k_gemm<QT_Q5_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q6_K: hipLaunchKernelGGL(k_gemm<QT_Q6_K>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q8_0: hipLaunchKernelGGL(k_gemm<QT_Q8_0>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_0: hipLaunchKernelGGL(k_gemm<QT_Q5_0>, grid, dim3(kWg), sh, s, a); break;
+    case QT_Q5_1: hipLaunchKernelGGL(k_gemm<QT_Q5_1>, grid, dim3(kWg), sh, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  out->p = region;
+  out->n = a.w.n;
+  out->ks = ks;
+  out->zs = (int64_t)a.t * a.w.n;
   return hipGetLastError();
 }
 
