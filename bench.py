@@ -74,9 +74,12 @@ def kernel_symbol(cls: str, info: dict) -> str:
     dec = (kv16 == "true" and hd in (64, 128, 256) and 1 <= g <= 8 and g * hd <= 1536
            and (info["context"] + 63) // 64 <= 128 and os.environ.get("CHONK_ATTN") != "chunked")
     attn = f"k_attn_dec<{g}, {hd}>" if dec else f"k_attention<{g}, {kv16}>"
-    return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "gateup": "k_mv_swiglu",
-            "qkv": "k_mv_store",
-            "oproj": "k_mv_add", "down": "k_mv_add", "lmhead": "k_mv_logits"}.get(cls, cls)
+    if os.environ.get("CHONK_MV") == "generic":
+        mv = {"gateup": "k_mv_swiglu", "qkv": "k_mv_store", "oproj": "k_mv_add", "down": "k_mv_add"}
+    else:  # one-row-per-lane-group kernels (layers after the first; llama/qwen3 prologues)
+        mv = {"gateup": "k_mvr_swiglu_norm", "qkv": "k_mvr_store_norm", "oproj": "k_mvr_add_plain",
+              "down": "k_mvr_add_plain"}
+    return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
 
 
 def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:

@@ -522,6 +522,37 @@ void plan_seg(MvSeg& sg, const QMat& w, int n_out, bool glu, int wg_begin) {
 
 int seg_wgs(const MvSeg& sg) { return (sg.n_out + sg.tile - 1) / sg.tile; }
 
+// Geometry of the one-row-per-lane-group matvec (k_mvr_*): the smallest lane
+// count that keeps a lane at <= kRowUnits units, widened (up to a wave) while
+// the segment has fewer than 192 workgroups.
+void plan_seg_row(MvSeg& sg, int wg_begin) {
+  const int U = sg.w.k / 32;
+  int lpr = pick_lpr(U);
+  while (lpr < 64 && (U + lpr - 1) / lpr > kRowUnits) lpr *= 2;
+  while (lpr < 64 && (sg.n_out + kWg / lpr - 1) / (kWg / lpr) < 192) lpr *= 2;
+  sg.lpr = lpr;
+  sg.tile = kWg / lpr;
+  sg.wg_begin = wg_begin;
+}
+
+// Moves a decode-step matvec onto the row kernels when its shape allows
+// (CHONK_MV=generic keeps every launch on the generic kernels).
+void use_row_kernel(MvArgs& a) {
+  static const bool off = [] {
+    const char* v = std::getenv("CHONK_MV");
+    return v && std::string(v) == "generic";
+  }();
+  if (off || a.epi == EPI_LOGITS) return;
+  for (int i = 0; i < a.nseg; ++i)
+    if (a.seg[i].w.k / 32 > kRowUnits * 64) return;
+  int wg = 0;
+  for (int i = 0; i < a.nseg; ++i) {
+    plan_seg_row(a.seg[i], wg);
+    wg += seg_wgs(a.seg[i]);
+  }
+  a.row_kernel = 1;
+}
+
 // Rotary inverse frequencies theta^(-2d/hd) in f32, evaluated once on the host
 // with the reference's operation order (rope_angle, llama-wgsl-runtime.ts:2884-2887).
 const float* rope_table(chonk_engine* e, uint32_t theta, int hd) {
@@ -566,7 +597,8 @@ void build_steps(chonk_engine* e) {
     a.cand = e->cand;
     return a;
   };
-  auto finish = [&](Launch& L, const MvArgs& a, int max_rows) {
+  auto finish = [&](Launch& L, MvArgs& a, int max_rows) {
+    use_row_kernel(a);
     L.kind = Launch::MV;
     L.mv = a;
     L.grid = 0;

@@ -11,6 +11,15 @@
 #ifndef CHONK_ATTN_STAMP
 #define CHONK_ATTN_STAMP(k)
 #endif
+// Optional trace points of the matvec kernels: CHONK_MV_T(tr, k) records phase
+// k of this workgroup into the uint64_t tr[8], CHONK_MV_TRACE_END(tr, tag)
+// publishes them; both empty unless a profiling build defines them.
+#ifndef CHONK_MV_T
+#define CHONK_MV_T(tr, k) (void)(tr)
+#endif
+#ifndef CHONK_MV_TRACE_END
+#define CHONK_MV_TRACE_END(tr, tag) (void)(tr)
+#endif
 
 namespace chonk {
 namespace {

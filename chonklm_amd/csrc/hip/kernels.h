@@ -61,6 +61,7 @@ struct MvArgs {
   const int32_t* hist;
   int32_t vocab;
   int32_t advance_pos;    // WG0 advances st->pos when done (steps without logits)
+  int32_t row_kernel;     // 1: one output row per lane group (k_mvr_*, planned by plan_seg_row)
   const uint32_t* pen_bits;
   const DevSampling* samp;
   Candidate* cand;
@@ -202,6 +203,8 @@ int pick_lpr(int units);
 hipError_t init_kernel_attributes();
 // Dynamic LDS bytes a launch may request after init_kernel_attributes().
 size_t lds_limit();
+// Units of 32 weights a lane of the one-row-per-lane-group matvec handles at most.
+constexpr int kRowUnits = 4;
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s);
 // The register-resident decode attention (attn_decode.hip): fp16 cache,

@@ -180,16 +180,20 @@ __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
 // The first weight batch is issued right after the activation staging
 // (weights do not depend on it); mv_stream walks the rest.
 template <int T, int UC, bool GLU, int AHEAD>
-__device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0, int nt, const MvLds& l) {
+__device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0, int nt, const MvLds& l,
+                                        uint64_t (&tr)[8]) {
   const MvLane m = mv_lane(g, t0, nt, GLU);
   Frag<T> cur[MvShape<T, UC>::N];
   mv_fetch<T, UC>(g, m, 0, cur);
   const int stopped = __hip_atomic_load(&a.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  CHONK_MV_T(tr, 1);
   if (stopped) return false;
   mv_finish(a, l);
+  CHONK_MV_T(tr, 2);
   mv_stream<T, UC, AHEAD>(g, m, xq_view(l.dl, l.xs16, a.k), l.res, cur);
+  CHONK_MV_T(tr, 3);
   return true;
 }
 
@@ -205,14 +209,16 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   // the type is uniform per workgroup, so every thread takes the same branch
   // (the staging and prologue inside hold barriers)
   bool live = false;
+  uint64_t tr[8];
+  CHONK_MV_T(tr, 0);
   const MvPro p = mv_pro(a);
   mv_stage(p, l);
   const int uc = mv_uc(g);
   with_type(g.w.type, [&]<int T>() {
     if (uc == 1) {
-      live = mv_work<T, 1, glu, ahead>(p, g, t0, nt, l);
+      live = mv_work<T, 1, glu, ahead>(p, g, t0, nt, l, tr);
     } else {
-      live = mv_work<T, 2, glu, ahead>(p, g, t0, nt, l);
+      live = mv_work<T, 2, glu, ahead>(p, g, t0, nt, l, tr);
     }
   });
   if (!live) return;
@@ -273,7 +279,96 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
     }
   }
   if (a.advance_pos && blockIdx.x == 0 && tid == 0) a.st->pos = a.st->pos + 1;
+  CHONK_MV_T(tr, 4);
+  CHONK_MV_TRACE_END(tr, EPI * 65536 + a.k);
 }
+
+// One output row per lane group: lane group lg of lpr lanes owns row t0 + lg
+// (GLU: both the gate and the up row), lane li owns units li, li + lpr, ...
+// (at most kRowUnits). Every address is computed once, the weight loads are
+// issued unconditionally (ragged lanes load a valid unit and drop its
+// product), the prologue mode is fixed at compile time and the owning lane
+// stores the row's result directly: a short straight path for the decode
+// step, whose matvecs are bound by instruction latency rather than bytes.
+template <int EPI, int PRO>
+__device__ __forceinline__ void mv_row_body(const MvArgs& a) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
+  const MvLds l = mv_lds(smem, a.k);
+  const SegView g = seg_view(a);
+  const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
+  const int nt = min(g.tile, g.n_out - t0);
+  const int lpr = g.lpr;
+  const int lg = (int)threadIdx.x >> __builtin_ctz((unsigned)lpr);
+  const int li = (int)threadIdx.x & (lpr - 1);
+  const bool owner = li == 0 && lg < nt;
+  const int row = t0 + min(lg, nt - 1);
+  const int U = a.k >> 5;
+  MvPro p = mv_pro(a);
+  p.pro = PRO;
+  mv_stage(p, l);
+  float addv = 0.f;
+  if constexpr (EPI == EPI_ADD) addv = g.add[row];
+  float rg = 0.f, ru = 0.f;
+  bool live = false;
+  with_type(g.w.type, [&]<int T>() {
+    QMat wu = g.w;
+    wu.s0 = g.u0;
+    wu.s1 = g.u1;
+    wu.s2 = g.u2;
+    wu.s3 = g.u3;
+    Frag<T> fg[kRowUnits], fu[glu ? kRowUnits : 1];
+#pragma unroll
+    for (int j = 0; j < kRowUnits; ++j) {
+      if (j * lpr < U) {  // uniform
+        const int u = min(li + j * lpr, U - 1);
+        fg[j] = load_unit<T>(g.w, row, u);
+        if constexpr (glu) fu[j] = load_unit<T>(wu, row, u);
+      }
+    }
+    const int stopped = __hip_atomic_load(&p.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (stopped) return;
+    mv_finish(p, l);
+    const XqView xv = xq_view(l.dl, l.xs16, a.k);
+    float ag = 0.f, au = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRowUnits; ++j) {
+      const int u = li + j * lpr;
+      if (j * lpr < U && u < U) {
+        XU xr;
+        load_xu<T>(xv, u, xr);
+        ag += dot_q<T>(fg[j], u, xr);
+        if constexpr (glu) au += dot_q<T>(fu[j], u, xr);
+      }
+    }
+    rg = group_sum_n(ag, lpr);
+    if constexpr (glu) ru = group_sum_n(au, lpr);
+    live = true;
+  });
+  if (!live) return;
+  if (owner) {
+    if constexpr (EPI == EPI_STORE) g.out[row] = rg;
+    if constexpr (EPI == EPI_ADD) g.out[row] = __fadd_rn(addv, rg);
+    if constexpr (EPI == EPI_GLU_SILU) g.out[row] = silu_mul(rg, ru);
+    if constexpr (EPI == EPI_GLU_GELU) g.out[row] = __fmul_rn(gelu_tanh(rg), ru);
+  }
+  if (a.advance_pos && blockIdx.x == 0 && threadIdx.x == 0) a.st->pos = a.st->pos + 1;
+}
+
+#define CHONK_MVR(NAME, EPI, PRO) \
+  __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO>(a); }
+CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN)
+CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM)
+CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM)
+CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM)
+CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN)
+CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM)
+CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM)
+CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM)
+CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM)
+#undef CHONK_MVR
 
 __global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
 __global__ __launch_bounds__(kWg) void k_mv_add(const MvArgs a) { matvec_body<EPI_ADD>(a); }
@@ -476,7 +571,10 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[21] = {
+  const void* fns[30] = {
+      (const void*)k_mvr_store_plain,        (const void*)k_mvr_store_norm,         (const void*)k_mvr_store_embed,
+      (const void*)k_mvr_store_resnorm,      (const void*)k_mvr_add_plain,          (const void*)k_mvr_swiglu_norm,
+      (const void*)k_mvr_swiglu_resnorm,     (const void*)k_mvr_geglu_norm,         (const void*)k_mvr_geglu_resnorm,
       (const void*)k_mv_store,               (const void*)k_mv_add,                 (const void*)k_mv_swiglu,
       (const void*)k_mv_geglu,               (const void*)k_mv_logits,              (const void*)k_attention<1, true>,
       (const void*)k_attention<2, true>,     (const void*)k_attention<3, true>,     (const void*)k_attention<4, true>,
@@ -496,6 +594,23 @@ hipError_t init_kernel_attributes() {
 }
 
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s) {
+  if (a.row_kernel) {
+    void (*k)(const MvArgs) = nullptr;
+    switch (a.epi * 8 + a.pro) {
+      case EPI_STORE * 8 + PRO_PLAIN: k = k_mvr_store_plain; break;
+      case EPI_STORE * 8 + PRO_NORM: k = k_mvr_store_norm; break;
+      case EPI_STORE * 8 + PRO_EMBED_NORM: k = k_mvr_store_embed; break;
+      case EPI_STORE * 8 + PRO_RES_NORM: k = k_mvr_store_resnorm; break;
+      case EPI_ADD * 8 + PRO_PLAIN: k = k_mvr_add_plain; break;
+      case EPI_GLU_SILU * 8 + PRO_NORM: k = k_mvr_swiglu_norm; break;
+      case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;
+      case EPI_GLU_GELU * 8 + PRO_NORM: k = k_mvr_geglu_norm; break;
+      case EPI_GLU_GELU * 8 + PRO_RES_NORM: k = k_mvr_geglu_resnorm; break;
+      default: return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kWg), shmem, s, a);
+    return hipGetLastError();
+  }
   switch (a.epi) {
     case EPI_STORE: hipLaunchKernelGGL(k_mv_store, dim3(grid), dim3(kWg), shmem, s, a); break;
     case EPI_ADD: hipLaunchKernelGGL(k_mv_add, dim3(grid), dim3(kWg), shmem, s, a); break;
