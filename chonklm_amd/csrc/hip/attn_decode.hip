@@ -143,6 +143,8 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   float* ew = nk + HD + 4 * G * HD;
   float* wml = ew + 4 * G * kDecWave;
   float* area = wml + 8 * G;
+  uint64_t tr[8];
+  CHONK_MV_T(tr, 0);
 
   // A: the position, stop flag and epoch by scalar loads (their own counter,
   // so nothing below waits on them early), then the vector loads: the rotary
@@ -194,6 +196,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   if (active && !a.spec_kv) load_kv();
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  CHONK_MV_T(tr, 1);
   if (stopped) return;
   if (pos >= a.ctx) {
     if (tid == 0) st->error = 1;
@@ -321,6 +324,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     }
   }
   __syncthreads();
+  CHONK_MV_T(tr, 2);
 
   // D: chunk partial [max, sum, acc[HD]] per head, to the chunk's row
   const int rowf = attn_rowf(G, HD);
@@ -452,6 +456,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       }
     }
   }
+  CHONK_MV_T(tr, 3);
   // (the poll's barriers also publish the rounded k and v)
   for (int g = wave; g < G; g += 4) {
     // the new position's score with the wave's own copy of q head g
@@ -500,6 +505,8 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = acc * wml[2 * g];
   }
   if (late && tid == 0) st->error = 4;
+  CHONK_MV_T(tr, 4);
+  CHONK_MV_TRACE_END(tr, 7 * 65536 + c);
   // every producer of this launch has read the tag once all rows carry it:
   // the newest chunk advances the epoch for the next launch
   if (c != c_hi) return;

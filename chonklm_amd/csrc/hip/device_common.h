@@ -96,6 +96,10 @@ __device__ __forceinline__ uint2 ldg2(const void* p) {
   return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ uint32_t ldg1(const void* p) { return *gbl((const uint32_t*)p); }
+__device__ __forceinline__ float4 ldg4f(const float* p) {
+  const uint4 v = ldg4(p);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
 
 // Group candidate written by the lm_head epilogue (ARGMAX_STAGE1 output).
 struct Candidate {

@@ -543,6 +543,8 @@ void use_row_kernel(MvArgs& a) {
     return v && std::string(v) == "generic";
   }();
   if (off || a.epi == EPI_LOGITS) return;
+  // the register-resident plain / norm prologues hold at most 4 float4 per thread
+  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) return;
   for (int i = 0; i < a.nseg; ++i)
     if (a.seg[i].w.k / 32 > kRowUnits * 64) return;
   int wg = 0;

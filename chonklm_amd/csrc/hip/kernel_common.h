@@ -157,16 +157,14 @@ __device__ __forceinline__ XqView xq_view(void* base, float* xs16, int K) {
   return v;
 }
 
-// Fills the digit planes, block scales and run sums of x (fp32 in LDS, K a
-// multiple of 32). Called by all threads after a barrier that follows the last
-// write of x; a barrier must separate it from the first read of the planes.
-__device__ __forceinline__ void quantize_x(const float* xs, int K, void* base, float* xs16) {
+// Digit planes, block scale and run sums of the four elements 4*i4 .. 4*i4+3
+// of x. The 8 consecutive threads that hold one 32-element block call it
+// together (their lanes must be active together).
+__device__ __forceinline__ void quantize4(const float4 v, int i4, int K, void* base, float* xs16) {
   int8_t* plane = (int8_t*)base;
   float* bsc = (float*)((char*)base + 3 * K);
   float* xs8 = bsc + K / 32;
-  // 8 consecutive threads cover one 32-element block (K / 4 is a multiple of 8)
-  for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg) {
-    const float4 v = reinterpret_cast<const float4*>(xs)[i4];
+  {
     const float m = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     int e = 0;
     (void)frexpf(m, &e);  // m < 2^e, so |x| * 2^(22-e) < 2^22
@@ -195,6 +193,15 @@ __device__ __forceinline__ void quantize_x(const float* xs, int K, void* base, f
     // a non-finite block poisons its products as the fp32 sum would
     if ((i4 & 7) == 0) bsc[i4 >> 3] = __builtin_isfinite(m) ? ldexpf(1.0f, -sh) : __int_as_float(0x7fc00000);
   }
+}
+
+// Fills the digit planes, block scales and run sums of x (fp32 in LDS, K a
+// multiple of 32). Called by all threads after a barrier that follows the last
+// write of x; a barrier must separate it from the first read of the planes.
+__device__ __forceinline__ void quantize_x(const float* xs, int K, void* base, float* xs16) {
+  // 8 consecutive threads cover one 32-element block (K / 4 is a multiple of 8)
+  for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg)
+    quantize4(reinterpret_cast<const float4*>(xs)[i4], i4, K, base, xs16);
 }
 
 // A lane's share of a matvec task: lane group lg (of ng groups of lpr lanes)

@@ -304,9 +304,29 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   const bool owner = li == 0 && lg < nt;
   const int row = t0 + min(lg, nt - 1);
   const int U = a.k >> 5;
+  uint64_t tr[8];
+  CHONK_MV_T(tr, 0);
   MvPro p = mv_pro(a);
   p.pro = PRO;
-  mv_stage(p, l);
+  // plain and norm prologues keep x (and the norm weight) in registers: thread
+  // t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
+  constexpr bool reg_pro = PRO == PRO_PLAIN || PRO == PRO_NORM;
+  const int n4 = a.k >> 2;
+  float4 xv[4], wv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xv[r] = wv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (reg_pro) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i4 = (int)threadIdx.x + kWg * r;
+      if (i4 < n4) {
+        xv[r] = ldg4f(p.in + 4 * i4);
+        if constexpr (PRO == PRO_NORM) wv[r] = ldg4f(p.w_norm + 4 * i4);
+      }
+    }
+  } else {
+    mv_stage(p, l);
+  }
   float addv = 0.f;
   if constexpr (EPI == EPI_ADD) addv = g.add[row];
   float rg = 0.f, ru = 0.f;
@@ -328,9 +348,39 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     }
     const int stopped = __hip_atomic_load(&p.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    if constexpr (!reg_pro) __syncthreads();
+    CHONK_MV_T(tr, 1);
     if (stopped) return;
-    mv_finish(p, l);
+    if constexpr (reg_pro) {
+      if constexpr (PRO == PRO_NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((int)threadIdx.x + kWg * r < n4)
+            ss += (xv[r].x * xv[r].x + xv[r].y * xv[r].y) + (xv[r].z * xv[r].z + xv[r].w * xv[r].w);
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) l.red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = (l.red[0] + l.red[1]) + (l.red[2] + l.red[3]);
+        const float inv = 1.0f / sqrtf(ss / (float)a.k + p.eps);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          xv[r].x = __fmul_rn(__fmul_rn(xv[r].x, inv), wv[r].x);
+          xv[r].y = __fmul_rn(__fmul_rn(xv[r].y, inv), wv[r].y);
+          xv[r].z = __fmul_rn(__fmul_rn(xv[r].z, inv), wv[r].z);
+          xv[r].w = __fmul_rn(__fmul_rn(xv[r].w, inv), wv[r].w);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i4 = (int)threadIdx.x + kWg * r;
+        if (i4 < n4) quantize4(xv[r], i4, a.k, l.dl, l.xs16);
+      }
+      __syncthreads();
+    } else {
+      mv_finish(p, l);
+    }
+    CHONK_MV_T(tr, 2);
     const XqView xv = xq_view(l.dl, l.xs16, a.k);
     float ag = 0.f, au = 0.f;
 #pragma unroll
@@ -345,6 +395,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     }
     rg = group_sum_n(ag, lpr);
     if constexpr (glu) ru = group_sum_n(au, lpr);
+    CHONK_MV_T(tr, 3);
     live = true;
   });
   if (!live) return;
@@ -355,6 +406,8 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     if constexpr (EPI == EPI_GLU_GELU) g.out[row] = __fmul_rn(gelu_tanh(rg), ru);
   }
   if (a.advance_pos && blockIdx.x == 0 && threadIdx.x == 0) a.st->pos = a.st->pos + 1;
+  CHONK_MV_T(tr, 4);
+  CHONK_MV_TRACE_END(tr, EPI * 65536 + a.k);
 }
 
 #define CHONK_MVR(NAME, EPI, PRO) \
