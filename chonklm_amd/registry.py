@@ -95,6 +95,10 @@ WORKLOADS: dict[str, Workload] = {
                                          head_dim=64, ffn=512, vocab=1200, context_length=4096,
                                          rope_theta=1000000.0, norm_eps=1e-6, seed=7),
                  max_context=160, eos_ids=[1199], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-qwen3-hd128", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=2, heads=4,
+                                               kv_heads=2, head_dim=128, ffn=512, vocab=900, context_length=4096,
+                                               rope_theta=1000000.0, norm_eps=1e-6, seed=19),
+                 max_context=400, eos_ids=[899], prompt_tokens=150, decode_tokens=40),
         Workload("tiny-llama", SynthSpec(arch="llama", recipe="q4_k_m", hidden=192, layers=3, heads=6, kv_heads=2,
                                          ffn=512, vocab=1000, context_length=4096, rope_theta=100000.0,
                                          norm_eps=1e-5, seed=11),

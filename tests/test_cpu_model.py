@@ -33,7 +33,7 @@ def _oracle(synth, name, kv_f16=True):
                                 eos_ids=w.eos_ids, threads=4)
 
 
-@pytest.mark.parametrize("name", TINY)
+@pytest.mark.parametrize("name", TINY + ["tiny-qwen3-hd128"])
 def test_logits_match_float64_decoder(name, synth):
     w, path, ref = _oracle(synth, name)
     dec = NumpyDecoder(path, w.spec.vocab, w.max_context, kv_f16=True)

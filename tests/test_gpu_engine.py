@@ -1,7 +1,8 @@
 """GPU engine parity against the oracle on small synthetic decoders.
 
 Each tiny workload exercises a different type mix and architecture branch:
-tiny-qwen3 (Q4_K/Q6_K, qk-norm, split RoPE), tiny-llama (Q5_0/Q8_0/Q4_K
+tiny-qwen3 (Q4_K/Q6_K, qk-norm, split RoPE), tiny-qwen3-hd128 (head_dim 128,
+150-token prompts: decode attention over several 64-position chunks), tiny-llama (Q5_0/Q8_0/Q4_K
 fallbacks, interleaved RoPE, head_dim 32, GQA 3), tiny-llama-q8 (Q8_0
 everywhere), tiny-gemma3 (gemma3 sandwich norms, GELU-tanh, sliding window,
 Q8_0 tied lm_head, top-k/temperature sampling). Bars: identical token ids;
@@ -19,7 +20,7 @@ from tests.conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 
-TINY = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
+TINY = ["tiny-qwen3", "tiny-qwen3-hd128", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
 
 
 def _pair(synth, name, kv="f16", **over):
