@@ -34,20 +34,21 @@ __device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
 
 constexpr int kMaxDeferSplit = 16;  // K split of a deferred GEMM (loads of a sum issued together)
 
-// Row t of a deferred result, elements j0 + kWg * e for e < 4 (zero past n):
+// Row t of a deferred result, elements j0 + S * e for e < 4 (zero past n):
 // every load of the four sums is issued before any is added, so a call costs
 // one memory round trip; the sums add the partials in split order.
+template <int S = kWg>
 __device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float (&v)[4]) {
   const float* q = P.p + (int64_t)t * P.n;
   if (P.ks == 1) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = j0 + kWg * e < P.n ? q[j0 + kWg * e] : 0.f;
+    for (int e = 0; e < 4; ++e) v[e] = j0 + S * e < P.n ? q[j0 + S * e] : 0.f;
     return;
   }
   float w[4][kMaxDeferSplit];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int j = min(j0 + kWg * e, P.n - 1);
+    const int j = min(j0 + S * e, P.n - 1);
 #pragma unroll
     for (int z = 0; z < kMaxDeferSplit; ++z) w[e][z] = z < P.ks ? q[(int64_t)z * P.zs + j] : 0.f;
   }
@@ -57,8 +58,49 @@ __device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float
 #pragma unroll
     for (int z = 1; z < kMaxDeferSplit; ++z)
       if (z < P.ks) a += w[e][z];
-    v[e] = j0 + kWg * e < P.n ? a : 0.f;
+    v[e] = j0 + S * e < P.n ? a : 0.f;
   }
+}
+
+// Element j of row t of a deferred result (the partials added in split order).
+__device__ __forceinline__ float part_at(const PartSum& P, int t, int j) {
+  const float* q = P.p + (int64_t)t * P.n + j;
+  if (P.ks == 1) return q[0];
+  float w[kMaxDeferSplit];
+#pragma unroll
+  for (int z = 0; z < kMaxDeferSplit; ++z) w[z] = z < P.ks ? q[(int64_t)z * P.zs] : 0.f;
+  float a = w[0];
+#pragma unroll
+  for (int z = 1; z < kMaxDeferSplit; ++z)
+    if (z < P.ks) a += w[z];
+  return a;
+}
+
+// The per-row glue kernels run one workgroup of kRowT threads per token row
+// (a batch of decode rows is a few dozen workgroups; wide ones keep each
+// row's deferred partial sums to one or two rounds of loads).
+constexpr int kRowT = 1024;
+constexpr int kRowW = kRowT / 64;
+
+__device__ __forceinline__ float rowt_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float a = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowW; w += 4) a += (red[w] + red[w + 1]) + (red[w + 2] + red[w + 3]);
+  return a;
+}
+__device__ __forceinline__ float rowt_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float a = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowW; ++w) a = fmaxf(a, red[w]);
+  return a;
 }
 
 // ---- operand split ----------------------------------------------------------------
@@ -67,8 +109,8 @@ __device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float
 // reference's fp32 operation order, then the row scaled by a power of two so
 // that |x| < 2^14 and split into fp16 hi + lo planes (zero-padded to kpad).
 // mode 0: plain; 1: RMSNorm with w.
-__global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
-  __shared__ float red[8];
+__global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
+  __shared__ float red[kRowW];
   const int t = blockIdx.x, tid = threadIdx.x;
   const float* x = a.x + (size_t)t * a.ldx;
   if (a.add.p) {
@@ -76,20 +118,20 @@ __global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
     if (a.add_w) {
       // the branch output goes through x's row first (x is rewritten below)
       float ss = 0.f;
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
         float d[4];
-        part_row4(a.add, t, i0, d);
+        part_row4<kRowT>(a.add, t, i0, d);
 #pragma unroll
         for (int e = 0; e < 4; ++e) ss += d[e] * d[e];
       }
-      ss = block_sum(ss, red);
+      ss = rowt_sum(ss, red);
       const float inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
         float d[4];
-        part_row4(a.add, t, i0, d);
+        part_row4<kRowT>(a.add, t, i0, d);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int i = i0 + kWg * e;
+          const int i = i0 + kRowT * e;
           if (i < a.k) {
             const float nd = __fmul_rn(__fmul_rn(d[e], inv), a.add_w[i]);
             xw[i] = fminf(fmaxf(__fadd_rn(xw[i], nd), -65000.0f), 65000.0f);
@@ -97,12 +139,12 @@ __global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
         }
       }
     } else {
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
         float d[4];
-        part_row4(a.add, t, i0, d);
+        part_row4<kRowT>(a.add, t, i0, d);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (i0 + kWg * e < a.k) xw[i0 + kWg * e] = __fadd_rn(xw[i0 + kWg * e], d[e]);
+          if (i0 + kRowT * e < a.k) xw[i0 + kRowT * e] = __fadd_rn(xw[i0 + kRowT * e], d[e]);
       }
     }
     __syncthreads();  // the updated row is read back below
@@ -110,26 +152,22 @@ __global__ __launch_bounds__(kWg) void k_pf_split(PfSplitArgs a) {
   float inv = 1.0f;
   if (a.w) {
     float ss = 0.f;
-    for (int i = tid; i < a.k; i += kWg) ss += x[i] * x[i];
-    ss = block_sum(ss, red);
+    for (int i = tid; i < a.k; i += kRowT) ss += x[i] * x[i];
+    ss = rowt_sum(ss, red);
     inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
   }
   float mx = 0.f;
-  for (int i = tid; i < a.k; i += kWg) {
+  for (int i = tid; i < a.k; i += kRowT) {
     const float v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
     mx = fmaxf(mx, fabsf(v));
   }
-  mx = wave_max(mx);
-  __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+  mx = rowt_max(mx, red);
   int e = 0;
   (void)frexpf(mx, &e);  // mx < 2^e
   const int rs = max(min(14 - e, 60), -60);
   _Float16* xh = a.xh + (size_t)t * a.kpad;
   _Float16* xl = a.xl + (size_t)t * a.kpad;
-  for (int i = tid; i < a.kpad; i += kWg) {
+  for (int i = tid; i < a.kpad; i += kRowT) {
     float v = 0.f;
     if (i < a.k) v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
     const float s = ldexpf(v, rs);
@@ -321,18 +359,18 @@ __global__ __launch_bounds__(kWg) void k_pf_norm_add(const float* d, const float
 
 // act = silu(g) * u or gelu_tanh(g) * u per element, then the split of the row
 // into fp16 planes (one workgroup per token row).
-__global__ __launch_bounds__(kWg) void k_pf_glu_split(PfGluArgs a) {
-  __shared__ float red[8];
+__global__ __launch_bounds__(kRowT) void k_pf_glu_split(PfGluArgs a) {
+  __shared__ float red[kRowW];
   const int t = blockIdx.x, tid = threadIdx.x;
   float* y = a.act + (size_t)t * a.k;
   float mx = 0.f;
-  for (int i0 = tid; i0 < a.k; i0 += 4 * kWg) {
+  for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
     float gv[4], uv[4];
-    part_row4(a.pg, t, i0, gv);
-    part_row4(a.pu, t, i0, uv);
+    part_row4<kRowT>(a.pg, t, i0, gv);
+    part_row4<kRowT>(a.pu, t, i0, uv);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = i0 + kWg * e;
+      const int i = i0 + kRowT * e;
       if (i < a.k) {
         const float v = a.gelu ? __fmul_rn(gelu_tanh(gv[e]), uv[e]) : silu_mul(gv[e], uv[e]);
         y[i] = v;
@@ -340,16 +378,13 @@ __global__ __launch_bounds__(kWg) void k_pf_glu_split(PfGluArgs a) {
       }
     }
   }
-  mx = wave_max(mx);
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  mx = rowt_max(mx, red);
   int e = 0;
   (void)frexpf(mx, &e);
   const int rs = max(min(14 - e, 60), -60);
   _Float16* xh = a.xh + (size_t)t * a.kpad;
   _Float16* xl = a.xl + (size_t)t * a.kpad;
-  for (int i = tid; i < a.kpad; i += kWg) {
+  for (int i = tid; i < a.kpad; i += kRowT) {
     const float s = i < a.k ? ldexpf(y[i], rs) : 0.f;
     const _Float16 h = (_Float16)s;
     xh[i] = h;
@@ -368,86 +403,87 @@ __device__ __forceinline__ size_t kv_row(const KvAddr& k, int kv_heads, int hd, 
 }
 
 // Per-head q/k RMSNorm and rotary embedding of every prompt row (position
-// p0 + t), the new k and v into the cache; one wave per head. Same operation
-// order as the decode attention's phase B.
+// p0 + t), the new k and v into the cache. One wave per (row, head): workgroup
+// (t, y) holds heads 4y .. 4y + 3 of the q heads followed by the kv heads. A
+// lane owns rotary pairs p = lane + 64 j and gathers their two elements (and,
+// for a kv head, its v dims) straight from the projections' partial sums, every
+// load issued at once. Same operation order as the decode attention's phase B.
+// The rotated q goes to the q part of the row for the attention kernels.
 __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NP = 2;  // pairs per lane: head_dim <= 256
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hh = blockIdx.y * 4 + wave;
+  const int nh = a.heads + a.kv_heads;
+  if (hh >= nh) return;
   const int pos = row_pos(a.kv, t);
   const int hd = a.hd, half = hd / 2;
-  const int nh = a.heads + a.kv_heads;
+  const bool is_k = hh >= a.heads;
+  const int kv = hh - a.heads;
   float* row = a.qkv + (size_t)t * a.ld;
-  if (a.pq.p) {
-    // the row from the projections' partial sums
-    const int qd = a.heads * hd, kd = a.kv_heads * hd;
-    const PartSum* src[3] = {&a.pq, &a.pk, &a.pv};
-    const int off[3] = {0, qd, qd + kd};
+  const int col = is_k ? a.heads * hd + kv * hd : hh * hd;  // the head's columns in the q|k|v row
+  const PartSum& P = is_k ? a.pk : a.pq;
+  const int pcol = is_k ? kv * hd : hh * hd;                 // ... in its projection's result
+  int ia[NP], ib[NP];
+  float x0[NP], x1[NP];
 #pragma unroll
-    for (int m = 0; m < 3; ++m) {
-      const PartSum& P = *src[m];
-      for (int i0 = tid; i0 < P.n; i0 += 4 * kWg) {
-        float v[4];
-        part_row4(P, t, i0, v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (i0 + kWg * e < P.n) row[off[m] + i0 + kWg * e] = v[e];
-      }
+  for (int j = 0; j < NP; ++j) {
+    const int d = min(lane + 64 * j, half - 1);
+    ia[j] = a.interleaved ? 2 * d : d;
+    ib[j] = a.interleaved ? 2 * d + 1 : d + half;
+    if (P.p) {
+      x0[j] = part_at(P, t, pcol + ia[j]);
+      x1[j] = part_at(P, t, pcol + ib[j]);
+    } else {
+      x0[j] = row[col + ia[j]];
+      x1[j] = row[col + ib[j]];
     }
-    __syncthreads();
   }
-  for (int hh = wave; hh < nh; hh += 4) {
-    const bool is_k = hh >= a.heads;
-    const int kv = hh - a.heads;
-    float* x = is_k ? row + a.heads * hd + kv * hd : row + hh * hd;
-    float r = 1.0f;
+  float r = 1.0f;
+  if (a.qn_w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+      if (lane + 64 * j < half) ss += x0[j] * x0[j] + x1[j] * x1[j];
+    ss = wave_sum(ss);
+    r = 1.0f / sqrtf(ss / (float)hd + a.eps);
+  }
+  const float* w = is_k ? a.kn_w : a.qn_w;
+  size_t base = 0;
+  if (is_k) base = kv_row(a.kv, a.kv_heads, hd, row_seq(a.kv, t), kv, pos);
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int d = lane + 64 * j;
+    if (d >= half) continue;
+    float v0 = x0[j], v1 = x1[j];
     if (a.qn_w) {
-      float ss = 0.f;
-      for (int d = lane; d < hd; d += 64) ss += x[d] * x[d];
-      ss = wave_sum(ss);
-      r = 1.0f / sqrtf(ss / (float)hd + a.eps);
+      v0 = __fmul_rn(__fmul_rn(v0, r), w[ia[j]]);
+      v1 = __fmul_rn(__fmul_rn(v1, r), w[ib[j]]);
     }
-    const float* w = is_k ? a.kn_w : a.qn_w;
-    // all lanes read their pair before any lane writes
-    float y0[4], y1[4];
-    int ia[4], ib[4];
-    int nd = 0;
-    for (int d = lane; d < half; d += 64, ++nd) {
-      ia[nd] = a.interleaved ? 2 * d : d;
-      ib[nd] = a.interleaved ? 2 * d + 1 : d + half;
-      float x0 = x[ia[nd]], x1 = x[ib[nd]];
-      if (a.qn_w) {
-        x0 = __fmul_rn(__fmul_rn(x0, r), w[ia[nd]]);
-        x1 = __fmul_rn(__fmul_rn(x1, r), w[ib[nd]]);
-      }
-      const float ang = __fmul_rn((float)pos, a.rope_inv[d]);
-      const float co = cosf(ang), si = sinf(ang);
-      y0[nd] = __fsub_rn(__fmul_rn(x0, co), __fmul_rn(x1, si));
-      y1[nd] = __fadd_rn(__fmul_rn(x0, si), __fmul_rn(x1, co));
-    }
-    __builtin_amdgcn_wave_barrier();
-    for (int q = 0; q < nd; ++q) {
-      if (is_k) {
-        const size_t base = kv_row(a.kv, a.kv_heads, hd, row_seq(a.kv, t), kv, pos);
-        if (a.kv16) {
-          ((__half*)a.kv.kc)[base + ia[q]] = __float2half_rn(y0[q]);
-          ((__half*)a.kv.kc)[base + ib[q]] = __float2half_rn(y1[q]);
-        } else {
-          ((float*)a.kv.kc)[base + ia[q]] = y0[q];
-          ((float*)a.kv.kc)[base + ib[q]] = y1[q];
-        }
-      } else {
-        x[ia[q]] = y0[q];
-        x[ib[q]] = y1[q];
-      }
-    }
+    const float ang = __fmul_rn((float)pos, a.rope_inv[d]);
+    const float co = cosf(ang), si = sinf(ang);
+    const float y0 = __fsub_rn(__fmul_rn(v0, co), __fmul_rn(v1, si));
+    const float y1 = __fadd_rn(__fmul_rn(v0, si), __fmul_rn(v1, co));
     if (is_k) {
-      const float* vsrc = row + (a.heads + a.kv_heads) * hd + kv * hd;
-      const size_t base = kv_row(a.kv, a.kv_heads, hd, row_seq(a.kv, t), kv, pos);
-      for (int d = lane; d < hd; d += 64) {
-        if (a.kv16)
-          ((__half*)a.kv.vc)[base + d] = __float2half_rn(vsrc[d]);
-        else
-          ((float*)a.kv.vc)[base + d] = vsrc[d];
+      if (a.kv16) {
+        ((__half*)a.kv.kc)[base + ia[j]] = __float2half_rn(y0);
+        ((__half*)a.kv.kc)[base + ib[j]] = __float2half_rn(y1);
+      } else {
+        ((float*)a.kv.kc)[base + ia[j]] = y0;
+        ((float*)a.kv.kc)[base + ib[j]] = y1;
       }
+    } else {
+      row[col + ia[j]] = y0;
+      row[col + ib[j]] = y1;
+    }
+  }
+  if (is_k) {
+    const int vcol = (a.heads + a.kv_heads) * hd + kv * hd;
+    for (int d = lane; d < hd; d += 64) {
+      const float v = a.pv.p ? part_at(a.pv, t, kv * hd + d) : row[vcol + d];
+      if (a.kv16)
+        ((__half*)a.kv.vc)[base + d] = __float2half_rn(v);
+      else
+        ((float*)a.kv.vc)[base + d] = v;
     }
   }
 }
@@ -975,7 +1011,7 @@ hipError_t init_gemm_attributes() {
 }
 
 hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s) {
-  hipLaunchKernelGGL(k_pf_split, dim3(rows), dim3(kWg), 0, s, a);
+  hipLaunchKernelGGL(k_pf_split, dim3(rows), dim3(kRowT), 0, s, a);
   return hipGetLastError();
 }
 hipError_t launch_pf_embed(const QMat& embed, const int32_t* tok, float scale, int k, float* x, int rows,
@@ -988,11 +1024,13 @@ hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, 
   return hipGetLastError();
 }
 hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s) {
-  hipLaunchKernelGGL(k_pf_glu_split, dim3(rows), dim3(kWg), 0, s, a);
+  hipLaunchKernelGGL(k_pf_glu_split, dim3(rows), dim3(kRowT), 0, s, a);
   return hipGetLastError();
 }
 hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s) {
-  hipLaunchKernelGGL(k_pf_rope_kv, dim3(rows), dim3(kWg), 0, s, a);
+  const int nh = a.heads + a.kv_heads;
+  if (a.hd > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pf_rope_kv, dim3(rows, (nh + 3) / 4), dim3(kWg), 0, s, a);
   return hipGetLastError();
 }
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
