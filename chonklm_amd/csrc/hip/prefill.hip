@@ -966,7 +966,9 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
   if ((int64_t)a.t * a.w.n > region_cap) return hipErrorInvalidValue;
   const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
-  int ks = tiles < 256 ? std::min(std::min(nst, kMaxDeferSplit), (256 + tiles - 1) / tiles) : 1;
+  // split K until about two workgroups per CU are busy
+  constexpr int target = 512;
+  int ks = tiles < target ? std::min(std::min(nst, kMaxDeferSplit), (target + tiles - 1) / tiles) : 1;
   while (ks > 1 && (int64_t)ks * a.t * a.w.n > region_cap) --ks;
   a.ksplit = ks;
   a.part = region;
