@@ -123,8 +123,8 @@ def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: 
     el = time.perf_counter() - t1
     b.close()
     return {"sequences": seqs, "prompt_tokens": prompt, "steps": steps, "warmup": warmup,
-            "ms_per_step": round(1000.0 * el / steps, 4),
-            "tokens_per_sec": round(seqs * steps / el, 1),
+            "ms_per_step": round(1000.0 * el / steps, 4) if steps else None,
+            "tokens_per_sec": round(seqs * steps / el, 1) if steps else None,
             "prefill_tokens_per_sec": round(seqs * prompt / prefill_s, 1),
             "note": "host-timed, step = one greedy token for every sequence"}
 
@@ -145,6 +145,10 @@ def main() -> int:
                          "(profiling runs: the trace then holds decode steps only)")
     ap.add_argument("--model-cache", default=os.environ.get("CHONK_MODEL_CACHE", "/tmp/chonk_models"))
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode measurement")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only the batched-decode measurement (profiling runs: per-step kernel time is the "
+                         "difference of two runs with different --batched-steps)")
+    ap.add_argument("--batched-steps", type=int, default=32)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first run 4 device-to-device copies of MIB MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -181,6 +185,13 @@ def main() -> int:
     eng = loaded.engine
     info = eng.info
     prompt = np.random.default_rng(1234).integers(0, w.spec.vocab, w.prompt_tokens).tolist()
+
+    if args.batched_only:
+        bd = batched_decode(eng, w.spec.vocab, 64, 512, args.batched_steps, 4)
+        print(json.dumps({"metric": "batched decode tokens/s (64 sequences), 1xMI355X", "batched_decode": bd,
+                          "config": {"workload": w.name}}))
+        eng.dispose()
+        return 0
 
     if args.fake_prefill:
         eng.fake_context(w.prompt_tokens, seed=1)
