@@ -488,21 +488,32 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     }
   }
   __syncthreads();
-  for (int i = tid; i < G * nd; i += kWg) {
-    const int g = i / nd, dd = i - g * nd;
-    const float* src = colv + (size_t)(g * nd + dd) * nact;
-    const float* wv = wts + g * nact;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int cc = 0;
-    for (; cc + 4 <= nact; cc += 4) {
-      a0 += src[cc] * wv[cc];
-      a1 += src[cc + 1] * wv[cc + 1];
-      a2 += src[cc + 2] * wv[cc + 2];
-      a3 += src[cc + 3] * wv[cc + 3];
+  // the weighted sum over the chunks of each output element of the slice, by
+  // tpi lanes per element (every tpi-th chunk each, then a DPP sum): the
+  // workgroup's lanes spread over the G * nd elements
+  const int n_el = G * nd;
+  int tpi = 1;
+  while (tpi < 64 && 2 * tpi * n_el <= kWg && tpi < nact) tpi *= 2;
+  for (int base = 0; base < n_el * tpi; base += kWg) {
+    const int q = base + tid;
+    const int i = q / tpi, sub = q & (tpi - 1);
+    if (i < n_el) {
+      const int g = i / nd, dd = i - g * nd;
+      const float* src = colv + (size_t)(g * nd + dd) * nact;
+      const float* wv = wts + g * nact;
+      float a0 = 0.f, a1 = 0.f;
+      int cc = sub;
+      for (; cc + tpi < nact; cc += 2 * tpi) {
+        a0 += src[cc] * wv[cc];
+        a1 += src[cc + tpi] * wv[cc + tpi];
+      }
+      if (cc < nact) a0 += src[cc] * wv[cc];
+      const float sum = group_sum_n(a0 + a1, tpi);
+      if (sub == 0) {
+        const float acc = sum + wml[2 * g + 1] * vx[d_lo + dd];
+        a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = acc * wml[2 * g];
+      }
     }
-    for (; cc < nact; ++cc) a0 += src[cc] * wv[cc];
-    const float acc = ((a0 + a1) + (a2 + a3)) + wml[2 * g + 1] * vx[d_lo + dd];
-    a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = acc * wml[2 * g];
   }
   if (late && tid == 0) st->error = 4;
   CHONK_MV_T(tr, 4);

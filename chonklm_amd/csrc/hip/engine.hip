@@ -523,13 +523,13 @@ void plan_seg(MvSeg& sg, const QMat& w, int n_out, bool glu, int wg_begin) {
 int seg_wgs(const MvSeg& sg) { return (sg.n_out + sg.tile - 1) / sg.tile; }
 
 // Geometry of the one-row-per-lane-group matvec (k_mvr_*): the smallest lane
-// count that keeps a lane at <= kRowUnits units, widened (up to a wave) while
-// the segment has fewer than 192 workgroups.
-void plan_seg_row(MvSeg& sg, int wg_begin) {
+// count that keeps a lane at <= `units` units, widened (up to a wave) while the
+// segment has fewer than `min_wgs` workgroups.
+void plan_seg_row(MvSeg& sg, int wg_begin, int units, int min_wgs) {
   const int U = sg.w.k / 32;
-  int lpr = pick_lpr(U);
-  while (lpr < 64 && (U + lpr - 1) / lpr > kRowUnits) lpr *= 2;
-  while (lpr < 64 && (sg.n_out + kWg / lpr - 1) / (kWg / lpr) < 192) lpr *= 2;
+  int lpr = 4;
+  while (lpr < 64 && (U + lpr - 1) / lpr > units) lpr *= 2;
+  while (lpr < 64 && (sg.n_out + kWg / lpr - 1) / (kWg / lpr) < min_wgs) lpr *= 2;
   sg.lpr = lpr;
   sg.tile = kWg / lpr;
   sg.wg_begin = wg_begin;
@@ -547,9 +547,13 @@ void use_row_kernel(MvArgs& a) {
   if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) return;
   for (int i = 0; i < a.nseg; ++i)
     if (a.seg[i].w.k / 32 > kRowUnits * 64) return;
+  // one unit per lane and >= 192 workgroups per segment; the three-segment
+  // q|k|v launch runs faster with two units per lane and half the workgroups
+  // (measured on the Qwen3-0.6B shapes)
+  const bool multi = a.nseg > 1;
   int wg = 0;
   for (int i = 0; i < a.nseg; ++i) {
-    plan_seg_row(a.seg[i], wg);
+    plan_seg_row(a.seg[i], wg, multi ? 2 : 1, multi ? 96 : 192);
     wg += seg_wgs(a.seg[i]);
   }
   a.row_kernel = 1;
