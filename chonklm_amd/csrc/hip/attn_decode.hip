@@ -355,6 +355,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     tag_put(row + tid * (HD + 2) + 1, L, tag);
   }
 
+  CHONK_MV_T(tr, 3);
   // merge, shared by the active chunks: chunk ci merges dims [ci*SD, ci*SD+SD)
   // of every head of the group. It polls the (max, sum) words of every row and
   // its dims' acc words until all carry this launch's tag (one pass costs one
@@ -413,6 +414,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       vx[d] = __half2float(vh);
     }
   }
+  CHONK_MV_T(tr, 4);
   constexpr int NW = 4;  // words per thread per pass
   const uint64_t t0 = wall_clock64();
   bool late = false;
@@ -456,7 +458,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       }
     }
   }
-  CHONK_MV_T(tr, 3);
+  CHONK_MV_T(tr, 5);
   // (the poll's barriers also publish the rounded k and v)
   for (int g = wave; g < G; g += 4) {
     // the new position's score with the wave's own copy of q head g
@@ -516,8 +518,8 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     }
   }
   if (late && tid == 0) st->error = 4;
-  CHONK_MV_T(tr, 4);
-  CHONK_MV_TRACE_END(tr, 7 * 65536 + c);
+  CHONK_MV_T(tr, 6);
+  CHONK_MV_TRACE_END(tr, 7 * 65536);
   // every producer of this launch has read the tag once all rows carry it:
   // the newest chunk advances the epoch for the next launch
   if (c != c_hi) return;

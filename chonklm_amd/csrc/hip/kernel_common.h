@@ -27,15 +27,29 @@ namespace {
 constexpr float kNegBig = -3.402823e38f;  // the WGSL literal -3.402823e38
 
 // Cross-lane steps without the LDS crossbar: DPP quad/row permutations inside
-// 16-lane rows, a swizzle across the two rows of a 32-lane half, and scalar
-// lane reads across halves. Every lane of an aligned group of N lanes ends with
-// the same value. Lanes of a group must be active together.
+// 16-lane rows, then gfx950's permlane swaps across the rows of a 32-lane half
+// (v_permlane16_swap) and across the halves (v_permlane32_swap) — VALU ops,
+// where a ds_swizzle would take a trip through the LDS unit. Every lane of an
+// aligned group of N lanes ends with the same value. Lanes of a group must be
+// active together.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 __device__ __forceinline__ float swz_xor16(float v) {
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+// (a, b) = (v of this lane, v of lane ^ 16) and (v of this lane, v of lane ^ 32)
+// as the two halves of one swap (each lane receives both)
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float lane_of(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -47,8 +61,16 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 4) v += dpp<0x4e>(v);   // quad_perm 2,3,0,1
   if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror
   if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror
-  if constexpr (N >= 32) v += swz_xor16(v);
-  if constexpr (N >= 64) v = lane_of(v, 0) + lane_of(v, 32);
+  if constexpr (N >= 32) {
+    float a, b;
+    swap16(v, a, b);
+    v = a + b;
+  }
+  if constexpr (N >= 64) {
+    float a, b;
+    swap32(v, a, b);
+    v = a + b;
+  }
   return v;
 }
 template <int N>
@@ -57,8 +79,16 @@ __device__ __forceinline__ float group_max(float v) {
   if constexpr (N >= 4) v = fmaxf(v, dpp<0x4e>(v));
   if constexpr (N >= 8) v = fmaxf(v, dpp<0x141>(v));
   if constexpr (N >= 16) v = fmaxf(v, dpp<0x140>(v));
-  if constexpr (N >= 32) v = fmaxf(v, swz_xor16(v));
-  if constexpr (N >= 64) v = fmaxf(lane_of(v, 0), lane_of(v, 32));
+  if constexpr (N >= 32) {
+    float a, b;
+    swap16(v, a, b);
+    v = fmaxf(a, b);
+  }
+  if constexpr (N >= 64) {
+    float a, b;
+    swap32(v, a, b);
+    v = fmaxf(a, b);
+  }
   return v;
 }
 // runtime group width (power of two in [1, 64])
