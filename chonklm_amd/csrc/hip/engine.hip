@@ -1297,7 +1297,9 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   if (sv && sv[0] == '1') build_step(e.get());
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
-  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0);
+  // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
+  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) &&
+                       std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) <= 4096;
   const char* ng = std::getenv("CHONK_NO_GRAPH");
   e->use_graph = !(ng && ng[0] == '1');
   for (const Launch& L : e->kernels_logits)
@@ -2401,7 +2403,7 @@ int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n
   return api_free([&] {
     TypeTraits t;
     if (!type_traits(ggml_type, &t) || !t.quantized) throw Error(CHONK_EINVAL, "unsupported GGUF tensor type " + type_name(ggml_type));
-    if (n_rows <= 0 || row_len <= 0 || row_len % t.block_elems || row_len % 32 || row_len > 65536 || n_tokens <= 0 ||
+    if (n_rows <= 0 || row_len <= 0 || row_len % t.block_elems || row_len % 32 || row_len > 4096 || n_tokens <= 0 ||
         n_tokens > 65536 || !blocks || !x || !y)
       throw Error(CHONK_EINVAL, "bad gemm shape");
     HIP_OK(hipSetDevice(device));
@@ -2565,6 +2567,8 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
   const ModelCfg& c = e->cfg;
   if (max_seqs <= 0 || max_seqs > 1024 || max_tokens <= 0 || max_tokens > c.ctx)
     throw Error(CHONK_EINVAL, "batch needs 1..1024 sequences of 1.." + std::to_string(c.ctx) + " tokens");
+  if (std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) > 4096)
+    throw Error(CHONK_EINVAL, "batched decoding needs hidden, q and ffn widths of at most 4096");
   if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
   if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
   std::unique_ptr<chonk_batch, void (*)(chonk_batch*)> b(new chonk_batch(), batch_free);

@@ -110,70 +110,73 @@ __device__ __forceinline__ float rowt_max(float v, float* red) {
 // that |x| < 2^14 and split into fp16 hi + lo planes (zero-padded to kpad).
 // mode 0: plain; 1: RMSNorm with w.
 __global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
+  // the row lives in registers: element tid + kRowT * e of this thread is v[e]
+  // (rows of at most 4 * kRowT elements; the launcher checks)
   __shared__ float red[kRowW];
   const int t = blockIdx.x, tid = threadIdx.x;
-  const float* x = a.x + (size_t)t * a.ldx;
-  if (a.add.p) {
-    float* xw = const_cast<float*>(x);
-    if (a.add_w) {
-      // the branch output goes through x's row first (x is rewritten below)
-      float ss = 0.f;
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
-        float d[4];
-        part_row4<kRowT>(a.add, t, i0, d);
+  float* xw = const_cast<float*>(a.x + (size_t)t * a.ldx);
+  float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ss += d[e] * d[e];
-      }
+  for (int e = 0; e < 4; ++e) {
+    const int i = tid + kRowT * e;
+    v[e] = i < a.k ? xw[i] : 0.f;
+  }
+  if (a.add.p) {
+    float d[4];
+    part_row4<kRowT>(a.add, t, tid, d);
+    if (a.add_w) {
+      // the branch output goes through RMSNorm first (the Gemma-3 sandwich)
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += d[e] * d[e];
       ss = rowt_sum(ss, red);
       const float inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
-        float d[4];
-        part_row4<kRowT>(a.add, t, i0, d);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = i0 + kRowT * e;
-          if (i < a.k) {
-            const float nd = __fmul_rn(__fmul_rn(d[e], inv), a.add_w[i]);
-            xw[i] = fminf(fmaxf(__fadd_rn(xw[i], nd), -65000.0f), 65000.0f);
-          }
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int i = tid + kRowT * e;
+        if (i < a.k) v[e] = fminf(fmaxf(__fadd_rn(v[e], __fmul_rn(__fmul_rn(d[e], inv), a.add_w[i])), -65000.0f), 65000.0f);
       }
     } else {
-      for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
-        float d[4];
-        part_row4<kRowT>(a.add, t, i0, d);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (i0 + kRowT * e < a.k) xw[i0 + kRowT * e] = __fadd_rn(xw[i0 + kRowT * e], d[e]);
-      }
+      for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(v[e], d[e]);
     }
-    __syncthreads();  // the updated row is read back below
+    // the updated residual row
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = tid + kRowT * e;
+      if (i < a.k) xw[i] = v[e];
+    }
   }
-  float inv = 1.0f;
   if (a.w) {
     float ss = 0.f;
-    for (int i = tid; i < a.k; i += kRowT) ss += x[i] * x[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[e] * v[e];
     ss = rowt_sum(ss, red);
-    inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+    const float inv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = tid + kRowT * e;
+      if (i < a.k) v[e] = __fmul_rn(__fmul_rn(v[e], inv), a.w[i]);
+    }
   }
   float mx = 0.f;
-  for (int i = tid; i < a.k; i += kRowT) {
-    const float v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
-    mx = fmaxf(mx, fabsf(v));
-  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(v[e]));
   mx = rowt_max(mx, red);
-  int e = 0;
-  (void)frexpf(mx, &e);  // mx < 2^e
-  const int rs = max(min(14 - e, 60), -60);
+  int ex = 0;
+  (void)frexpf(mx, &ex);  // mx < 2^ex
+  const int rs = max(min(14 - ex, 60), -60);
   _Float16* xh = a.xh + (size_t)t * a.kpad;
   _Float16* xl = a.xl + (size_t)t * a.kpad;
-  for (int i = tid; i < a.kpad; i += kRowT) {
-    float v = 0.f;
-    if (i < a.k) v = a.w ? __fmul_rn(__fmul_rn(x[i], inv), a.w[i]) : x[i];
-    const float s = ldexpf(v, rs);
-    const _Float16 h = (_Float16)s;
-    xh[i] = h;
-    xl[i] = (_Float16)(s - (float)h);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = tid + kRowT * e;
+    if (i < a.kpad) {
+      const float sv = ldexpf(v[e], rs);  // zero past k
+      const _Float16 h = (_Float16)sv;
+      xh[i] = h;
+      xl[i] = (_Float16)(sv - (float)h);
+    }
   }
   if (tid == 0) a.xscale[t] = __builtin_isfinite(mx) ? ldexpf(1.0f, -rs) : __int_as_float(0x7fc00000);
 }
@@ -360,35 +363,39 @@ __global__ __launch_bounds__(kWg) void k_pf_norm_add(const float* d, const float
 // act = silu(g) * u or gelu_tanh(g) * u per element, then the split of the row
 // into fp16 planes (one workgroup per token row).
 __global__ __launch_bounds__(kRowT) void k_pf_glu_split(PfGluArgs a) {
+  // element tid + kRowT * e of the row is v[e] (at most 4 * kRowT elements)
   __shared__ float red[kRowW];
   const int t = blockIdx.x, tid = threadIdx.x;
   float* y = a.act + (size_t)t * a.k;
+  float gv[4], uv[4], v[4];
+  part_row4<kRowT>(a.pg, t, tid, gv);
+  part_row4<kRowT>(a.pu, t, tid, uv);
   float mx = 0.f;
-  for (int i0 = tid; i0 < a.k; i0 += 4 * kRowT) {
-    float gv[4], uv[4];
-    part_row4<kRowT>(a.pg, t, i0, gv);
-    part_row4<kRowT>(a.pu, t, i0, uv);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = i0 + kRowT * e;
-      if (i < a.k) {
-        const float v = a.gelu ? __fmul_rn(gelu_tanh(gv[e]), uv[e]) : silu_mul(gv[e], uv[e]);
-        y[i] = v;
-        mx = fmaxf(mx, fabsf(v));
-      }
+  for (int e = 0; e < 4; ++e) {
+    const int i = tid + kRowT * e;
+    v[e] = 0.f;
+    if (i < a.k) {
+      v[e] = a.gelu ? __fmul_rn(gelu_tanh(gv[e]), uv[e]) : silu_mul(gv[e], uv[e]);
+      y[i] = v[e];
+      mx = fmaxf(mx, fabsf(v[e]));
     }
   }
   mx = rowt_max(mx, red);
-  int e = 0;
-  (void)frexpf(mx, &e);
-  const int rs = max(min(14 - e, 60), -60);
+  int ex = 0;
+  (void)frexpf(mx, &ex);
+  const int rs = max(min(14 - ex, 60), -60);
   _Float16* xh = a.xh + (size_t)t * a.kpad;
   _Float16* xl = a.xl + (size_t)t * a.kpad;
-  for (int i = tid; i < a.kpad; i += kRowT) {
-    const float s = i < a.k ? ldexpf(y[i], rs) : 0.f;
-    const _Float16 h = (_Float16)s;
-    xh[i] = h;
-    xl[i] = (_Float16)(s - (float)h);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = tid + kRowT * e;
+    if (i < a.kpad) {
+      const float sv = ldexpf(v[e], rs);
+      const _Float16 h = (_Float16)sv;
+      xh[i] = h;
+      xl[i] = (_Float16)(sv - (float)h);
+    }
   }
   if (tid == 0) a.xscale[t] = __builtin_isfinite(mx) ? ldexpf(1.0f, -rs) : __int_as_float(0x7fc00000);
 }
@@ -1013,6 +1020,7 @@ hipError_t init_gemm_attributes() {
 }
 
 hipError_t launch_pf_split(const PfSplitArgs& a, int rows, hipStream_t s) {
+  if (a.kpad > 4 * kRowT) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pf_split, dim3(rows), dim3(kRowT), 0, s, a);
   return hipGetLastError();
 }
@@ -1026,6 +1034,7 @@ hipError_t launch_pf_norm_add(const float* d, const float* w, float eps, int k, 
   return hipGetLastError();
 }
 hipError_t launch_pf_glu_split(const PfGluArgs& a, int rows, hipStream_t s) {
+  if (a.kpad > 4 * kRowT) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pf_glu_split, dim3(rows), dim3(kRowT), 0, s, a);
   return hipGetLastError();
 }

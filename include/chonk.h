@@ -220,7 +220,8 @@ int chonk_dequant(int32_t device, uint32_t ggml_type, const void* blocks, int64_
 int chonk_matvec(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
                  const float* x, float* y, int32_t reps, double* avg_us);
 /* Y[T,N] = X[T,K] W[N,K]^T with the batched pass's GEMM (fp16 hi/lo operand
- * split on the matrix cores, fp32 accumulation); x and y are row-major. When
+ * split on the matrix cores, fp32 accumulation); x and y are row-major;
+ * K <= 4096 and T <= 65536 (CHONK_EINVAL otherwise). When
  * reps > 0 also times `reps` launches (the operand split included) and
  * stores the mean microseconds in *avg_us. */
 int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n_rows, int64_t row_len,
