@@ -216,6 +216,13 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
 
   Frag<T> f{};
   uint4 xv[8];
+  // the per-row operand scales of the epilogue, requested up front
+  float xsc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = t0 + tb + 16 * j + (lane & 15);
+    xsc[j] = t < a.t ? a.xscale[t] : 0.f;
+  }
   auto fetch = [&](int s) {
     const int u = s * 4 + wj;
     if (w_ok && u < U) f = load_unit<T>(a.w, n0 + wr, u);
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   for (int j = 0; j < 2; ++j) {
     const int t = t0 + tb + 16 * j + (lane & 15);
     if (t >= a.t) continue;
-    const float sc = wun * a.xscale[t];
+    const float sc = wun * xsc[j];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int n = n0 + rb + 16 * i + 4 * (lane >> 4);
