@@ -197,7 +197,10 @@ __device__ __forceinline__ bool mv_work(const MvPro& a, const SegView& g, int t0
   return true;
 }
 
-template <int EPI>
+// TT >= 0: the weight type is known at compile time (the lm_head kernels, one
+// per type, so that each allocates only the registers its type needs); AH > 0
+// overrides the number of weight batches in flight.
+template <int EPI, int TT = -1, int AH = 0>
 __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   extern __shared__ __align__(16) float smem[];
   const MvLds l = mv_lds(smem, a.k);
@@ -205,7 +208,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
-  constexpr int ahead = EPI == EPI_LOGITS ? 2 : 1;  // the lm_head's long row streams
+  constexpr int ahead = AH > 0 ? AH : (EPI == EPI_LOGITS ? 2 : 1);  // the lm_head's long row streams
   // the type is uniform per workgroup, so every thread takes the same branch
   // (the staging and prologue inside hold barriers)
   bool live = false;
@@ -214,13 +217,17 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   const MvPro p = mv_pro(a);
   mv_stage(p, l);
   const int uc = mv_uc(g);
-  with_type(g.w.type, [&]<int T>() {
+  auto work = [&]<int T>() {
     if (uc == 1) {
       live = mv_work<T, 1, glu, ahead>(p, g, t0, nt, l, tr);
     } else {
       live = mv_work<T, 2, glu, ahead>(p, g, t0, nt, l, tr);
     }
-  });
+  };
+  if constexpr (TT >= 0)
+    work.template operator()<TT>();
+  else
+    with_type(g.w.type, work);
   if (!live) return;
   __syncthreads();
 
@@ -428,6 +435,12 @@ __global__ __launch_bounds__(kWg) void k_mv_add(const MvArgs a) { matvec_body<EP
 __global__ __launch_bounds__(kWg) void k_mv_swiglu(const MvArgs a) { matvec_body<EPI_GLU_SILU>(a); }
 __global__ __launch_bounds__(kWg) void k_mv_geglu(const MvArgs a) { matvec_body<EPI_GLU_GELU>(a); }
 __global__ __launch_bounds__(kWg) void k_mv_logits(const MvArgs a) { matvec_body<EPI_LOGITS>(a); }
+// (Q6_K keeps one batch of rows ahead: with two its fragments take 228
+// registers and the 151936-row lm_head ran 4% slower)
+template <int T>
+__global__ __launch_bounds__(kWg) void k_mv_logits_t(const MvArgs a) {
+  matvec_body<EPI_LOGITS, T, T == QT_Q6_K ? 1 : 2>(a);
+}
 
 // ---------------------------------------------------------------------------
 // GQA decode attention, one workgroup per (kv head, chunk of positions).
@@ -624,7 +637,9 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[30] = {
+  const void* fns[36] = {
+      (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
+      (const void*)k_mv_logits_t<QT_Q8_0>,   (const void*)k_mv_logits_t<QT_Q5_0>,   (const void*)k_mv_logits_t<QT_Q5_1>,
       (const void*)k_mvr_store_plain,        (const void*)k_mvr_store_norm,         (const void*)k_mvr_store_embed,
       (const void*)k_mvr_store_resnorm,      (const void*)k_mvr_add_plain,          (const void*)k_mvr_swiglu_norm,
       (const void*)k_mvr_swiglu_resnorm,     (const void*)k_mvr_geglu_norm,         (const void*)k_mvr_geglu_resnorm,
@@ -669,7 +684,18 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
     case EPI_ADD: hipLaunchKernelGGL(k_mv_add, dim3(grid), dim3(kWg), shmem, s, a); break;
     case EPI_GLU_SILU: hipLaunchKernelGGL(k_mv_swiglu, dim3(grid), dim3(kWg), shmem, s, a); break;
     case EPI_GLU_GELU: hipLaunchKernelGGL(k_mv_geglu, dim3(grid), dim3(kWg), shmem, s, a); break;
-    case EPI_LOGITS: hipLaunchKernelGGL(k_mv_logits, dim3(grid), dim3(kWg), shmem, s, a); break;
+    case EPI_LOGITS:
+      // one segment, a type known here: the per-type lm_head kernel
+      switch (a.nseg == 1 ? a.seg[0].w.type : -1) {
+        case QT_Q4_K: hipLaunchKernelGGL(k_mv_logits_t<QT_Q4_K>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        case QT_Q5_K: hipLaunchKernelGGL(k_mv_logits_t<QT_Q5_K>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        case QT_Q6_K: hipLaunchKernelGGL(k_mv_logits_t<QT_Q6_K>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        case QT_Q8_0: hipLaunchKernelGGL(k_mv_logits_t<QT_Q8_0>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        case QT_Q5_0: hipLaunchKernelGGL(k_mv_logits_t<QT_Q5_0>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        case QT_Q5_1: hipLaunchKernelGGL(k_mv_logits_t<QT_Q5_1>, dim3(grid), dim3(kWg), shmem, s, a); break;
+        default: hipLaunchKernelGGL(k_mv_logits, dim3(grid), dim3(kWg), shmem, s, a); break;
+      }
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
