@@ -11,7 +11,8 @@
 //   context_length, rope.freq_base, attention.layer_norm_rms_epsilon},
 //   gemma3.attention.sliding_window.
 // Type recipe (Q4_K_M): llama.cpp's llama_tensor_get_type as restated in the
-// header of synth.h.
+// header of synth.h. Architecture gpt2 follows the GPT runtime's manifest
+// (src/lib/gpt-wgsl-runtime.ts:274-356; gpt2_plan below).
 #include "synth.h"
 
 #include <algorithm>
@@ -92,9 +93,44 @@ uint32_t recipe_tensor_type(const std::string& recipe, const std::string& role, 
   return fallback_type(t, row_len);
 }
 
+// The tensor plan of a GPT-2 decoder as the reference's GPT runtime reads it
+// (src/lib/gpt-wgsl-runtime.ts:274-356): learned position table, LayerNorm
+// weights and biases, fused q|k|v and biases on every linear layer, a separate
+// output matrix.
+std::vector<TensorPlan> gpt2_plan(const SynthConfig& c) {
+  const uint64_t H = (uint64_t)c.hidden, F = (uint64_t)c.ffn;
+  std::vector<TensorPlan> plan;
+  plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H, recipe_tensor_type(c.recipe, "output", -1, c.layers, H),
+                  0.f, c.weight_std});
+  plan.push_back({"position_embd.weight", (uint64_t)c.context_length, H, GGML_F32, 0.f, c.weight_std});
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    auto lin = [&](const std::string& role, uint64_t n, uint64_t k) {
+      plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f, c.weight_std});
+      plan.push_back({p + role + ".bias", 1, n, GGML_F32, 0.f, c.weight_std});
+    };
+    auto ln = [&](const std::string& role) {
+      plan.push_back({p + role + ".weight", 1, H, GGML_F32, 1.f, c.norm_std});
+      plan.push_back({p + role + ".bias", 1, H, GGML_F32, 0.f, c.norm_std});
+    };
+    ln("attn_norm");
+    lin("attn_qkv", 3 * H, H);
+    lin("attn_output", H, H);
+    ln("ffn_norm");
+    lin("ffn_up", F, H);
+    lin("ffn_down", H, F);
+  }
+  plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, c.norm_std});
+  plan.push_back({"output_norm.bias", 1, H, GGML_F32, 0.f, c.norm_std});
+  plan.push_back({"output.weight", (uint64_t)c.vocab, H, recipe_tensor_type(c.recipe, "output", -1, c.layers, H), 0.f,
+                  c.weight_std});
+  return plan;
+}
+
 void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_threads) {
   const std::string& a = c.arch;
-  if (a != "llama" && a != "qwen3" && a != "gemma3") throw std::runtime_error("synthetic writer: unsupported arch " + a);
+  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2")
+    throw std::runtime_error("synthetic writer: unsupported arch " + a);
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0)
     throw std::runtime_error("synthetic writer: non-positive dimension");
   if (c.heads % c.kv_heads != 0) throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
@@ -107,10 +143,11 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
   const float n_std = c.norm_std;
 
   std::vector<TensorPlan> plan;
+  if (a == "gpt2") plan = gpt2_plan(c);
   // tied embeddings: token_embd doubles as the output projection ("output" role)
-  plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H,
+  if (a != "gpt2") plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H,
                   recipe_tensor_type(c.recipe, "output", -1, c.layers, H), 0.f, w_std});
-  for (int i = 0; i < c.layers; ++i) {
+  for (int i = 0; i < (a == "gpt2" ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     auto lin = [&](const std::string& role, uint64_t n, uint64_t k) {
       plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f, w_std});
@@ -132,7 +169,7 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     lin("ffn_down", H, F);
     if (gemma) norm("post_ffw_norm", H);
   }
-  plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
+  if (a != "gpt2") plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
 
   GgufWriter w;
   w.set_string("general.architecture", a);
@@ -143,14 +180,17 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
   w.set_u32(a + ".block_count", (uint32_t)c.layers);
   w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
   w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
-  w.set_u32(a + ".attention.head_count_kv", (uint32_t)c.kv_heads);
+  if (a == "gpt2") w.set_f32("gpt2.attention.layer_norm_epsilon", c.norm_eps);
+  if (a != "gpt2") w.set_u32(a + ".attention.head_count_kv", (uint32_t)c.kv_heads);
   if (c.head_dim > 0) {
     w.set_u32(a + ".attention.key_length", (uint32_t)head_dim);
     w.set_u32(a + ".attention.value_length", (uint32_t)head_dim);
   }
-  w.set_u32(a + ".rope.dimension_count", (uint32_t)head_dim);
-  w.set_f32(a + ".rope.freq_base", c.rope_theta);
-  w.set_f32(a + ".attention.layer_norm_rms_epsilon", c.norm_eps);
+  if (a != "gpt2") {
+    w.set_u32(a + ".rope.dimension_count", (uint32_t)head_dim);
+    w.set_f32(a + ".rope.freq_base", c.rope_theta);
+    w.set_f32(a + ".attention.layer_norm_rms_epsilon", c.norm_eps);
+  }
   w.set_u32(a + ".vocab_size", (uint32_t)c.vocab);
   if (gemma) w.set_u32("gemma3.attention.sliding_window", (uint32_t)c.sliding_window);
 

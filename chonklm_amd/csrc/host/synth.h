@@ -24,7 +24,7 @@
 namespace chonk {
 
 struct SynthConfig {
-  std::string arch = "llama";  // llama | qwen3 | gemma3
+  std::string arch = "llama";  // llama | qwen3 | gemma3 | gpt2
   std::string name;
   int hidden = 576;
   int layers = 30;

@@ -90,6 +90,10 @@ WORKLOADS: dict[str, Workload] = {
                  eos_ids=[1, 106], prompt_tokens=1024, decode_tokens=128, temperature=0.8, top_k=40,
                  description="Gemma-3-270M-shaped decoder, Q4_K_M (Q8_0 lm_head), 1024-token prompt, "
                              "top-k 40 / T 0.8 sampling, 128 tokens"),
+        Workload("gpt2-124m-q4_k_m", SynthSpec(arch="gpt2", recipe="q4_k_m", hidden=768, layers=12, heads=12,
+                                               kv_heads=12, ffn=3072, vocab=50257, context_length=1024, seed=29),
+                 max_context=1024, eos_ids=[50256], prompt_tokens=512, decode_tokens=128,
+                 description="GPT-2-124M-shaped decoder (gpt2 runtime), Q4_K_M, 512-token prompt, greedy 128"),
         # small decoders for oracle parity (each exercises a different type mix)
         Workload("tiny-qwen3", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=2,
                                          head_dim=64, ffn=512, vocab=1200, context_length=4096,
@@ -99,6 +103,9 @@ WORKLOADS: dict[str, Workload] = {
                                                kv_heads=2, head_dim=128, ffn=512, vocab=900, context_length=4096,
                                                rope_theta=1000000.0, norm_eps=1e-6, seed=19),
                  max_context=400, eos_ids=[899], prompt_tokens=150, decode_tokens=40),
+        Workload("tiny-gpt2", SynthSpec(arch="gpt2", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=4,
+                                        ffn=1024, vocab=800, context_length=256, norm_eps=1e-5, seed=23),
+                 max_context=160, eos_ids=[799], prompt_tokens=24, decode_tokens=24),
         Workload("tiny-llama", SynthSpec(arch="llama", recipe="q4_k_m", hidden=192, layers=3, heads=6, kv_heads=2,
                                          ffn=512, vocab=1000, context_length=4096, rope_theta=100000.0,
                                          norm_eps=1e-5, seed=11),

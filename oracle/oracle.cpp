@@ -391,6 +391,9 @@ struct Layer {
   uint32_t theta_u32;
   std::vector<float> in_norm, post_norm, pre_ffn_norm, post_ffn_norm, q_norm, k_norm;
   Matrix q, k, v, o, gate, up, down;
+  // GPT-2: fused q|k|v, LayerNorm biases (in_norm / post_norm hold the weights), linear biases
+  Matrix qkv;
+  std::vector<float> in_norm_b, post_norm_b, qkv_b, o_b, up_b, down_b;
   std::vector<float> kcache, vcache;  // [kv_heads][C][hd]
 };
 
@@ -401,6 +404,8 @@ struct orc_model {
   Pool* pool = nullptr;
   // hyper-parameters (buildGgufLlamaManifest, llama-wgsl-runtime.ts:326-425)
   bool gemma = false, interleaved = false, qk_norm = false, kv_f16 = false;
+  bool gpt = false;                         // GGUF architecture gpt2 (gpt-wgsl-runtime.ts)
+  std::vector<float> pos_embd, final_norm_b;  // GPT-2: [context][hidden] position table, final LayerNorm bias
   int hidden = 0, ffn = 0, vocab = 0, n_layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float norm_eps = 1e-5f, qk_eps = 1e-5f, attn_scale = 0, embed_scale = 1;
   Matrix embed, lm_head;
@@ -408,7 +413,7 @@ struct orc_model {
   std::vector<Layer> layers;
   int pos = 0;
   // scratch of the last step
-  std::vector<float> hA, hB, hC, norm, q, k, v, qn, attn, gate, up, ff, logits, scores;
+  std::vector<float> hA, hB, hC, norm, q, k, v, qn, attn, gate, up, ff, logits, scores, qkv;
   std::vector<uint8_t> candidates;
   std::vector<float> last_residual;
 };
@@ -600,11 +605,68 @@ std::vector<float> floats(orc_model* m, const std::string& name, size_t n) {
   return out;
 }
 
+// manifestFromGguf + the engine's buffers (gpt-wgsl-runtime.ts:274-356, :540-640)
+void build_gpt(orc_model* m, const orc_model_def* def) {
+  const Gguf& g = m->g;
+  m->gpt = true;
+  m->hidden = (int)num(g, "gpt2.embedding_length", 0, true);
+  m->n_layers = (int)num(g, "gpt2.block_count", 0, true);
+  m->ffn = (int)num(g, "gpt2.feed_forward_length", 0, true);
+  m->heads = (int)num(g, "gpt2.attention.head_count", 0, true);
+  const int gguf_ctx = (int)num(g, "gpt2.context_length", 0, true);
+  m->norm_eps = (float)num(g, "gpt2.attention.layer_norm_epsilon", 1e-5, false);
+  if (m->hidden % m->heads) throw std::runtime_error("GPT WGSL: hidden is not divisible by heads");
+  m->hd = m->hidden / m->heads;
+  if (m->hd != 64) throw std::runtime_error("GPT WGSL: only 64-wide GPT-2 heads are implemented");
+  m->kv_heads = m->heads;
+  auto te = g.tensors.find("token_embd.weight");
+  if (te == g.tensors.end() || te->second.shape.size() != 2) throw std::runtime_error("GPT WGSL: missing token_embd.weight");
+  m->vocab = (int)te->second.shape[1];
+  if ((m->vocab + 255) / 256 > 256) throw std::runtime_error("GPT WGSL argmax supports at most 65536 vocab entries");
+  m->ctx = std::min(def->max_context, gguf_ctx);
+  m->attn_scale = (float)(1.0 / std::sqrt((double)m->hd));  // INV_SQRT_HEAD_DIM (:1066)
+  m->kv_f16 = def->kv_f16 != 0;
+  m->embed = matrix(m, "token_embd.weight", (uint64_t)m->hidden, (uint64_t)m->vocab);
+  m->lm_head = matrix(m, "output.weight", (uint64_t)m->hidden, (uint64_t)m->vocab);
+  m->pos_embd = floats(m, "position_embd.weight", (size_t)gguf_ctx * m->hidden);
+  m->final_norm = floats(m, "output_norm.weight", m->hidden);
+  m->final_norm_b = floats(m, "output_norm.bias", m->hidden);
+  const int H = m->hidden;
+  for (int i = 0; i < m->n_layers; ++i) {
+    Layer L;
+    const std::string p = "blk." + std::to_string(i) + ".";
+    L.heads = L.kv_heads = m->heads;
+    L.qdim = L.kvdim = H;
+    L.ffn = m->ffn;
+    L.window = 0;
+    L.theta_u32 = 0;
+    L.in_norm = floats(m, p + "attn_norm.weight", H);
+    L.in_norm_b = floats(m, p + "attn_norm.bias", H);
+    L.post_norm = floats(m, p + "ffn_norm.weight", H);
+    L.post_norm_b = floats(m, p + "ffn_norm.bias", H);
+    L.qkv = matrix(m, p + "attn_qkv.weight", H, 3 * (uint64_t)H);
+    L.qkv_b = floats(m, p + "attn_qkv.bias", 3 * (size_t)H);
+    L.o = matrix(m, p + "attn_output.weight", H, H);
+    L.o_b = floats(m, p + "attn_output.bias", H);
+    L.up = matrix(m, p + "ffn_up.weight", H, m->ffn);
+    L.up_b = floats(m, p + "ffn_up.bias", m->ffn);
+    L.down = matrix(m, p + "ffn_down.weight", m->ffn, H);
+    L.down_b = floats(m, p + "ffn_down.bias", H);
+    L.kcache.assign((size_t)H * m->ctx, 0.0f);
+    L.vcache.assign((size_t)H * m->ctx, 0.0f);
+    m->layers.push_back(std::move(L));
+  }
+}
+
 void build(orc_model* m, const orc_model_def* def) {
   const Gguf& g = m->g;
   auto it = g.kv.find("general.architecture");
   if (it == g.kv.end() || it->second.type != 8) throw std::runtime_error("GGUF metadata general.architecture is missing or not a string");
   const std::string arch = it->second.str;
+  if (arch == "gpt2") {
+    build_gpt(m, def);
+    return;
+  }
   if (arch != "qwen3" && arch != "llama" && arch != "gemma3")
     throw std::runtime_error("Llama GGUF WGSL does not support architecture " + arch);
   m->gemma = arch == "gemma3";
@@ -667,6 +729,125 @@ void build(orc_model* m, const orc_model_def* def) {
   if (m->gemma && !m->qk_norm) throw std::runtime_error("Gemma WGSL layer is missing required weights");
 }
 
+// LAYER_NORM_WGSL (gpt-wgsl-runtime.ts:1658-1706): 256 threads, sum and sum of
+// squares strided then 128..1 trees; variance = max(E[x^2] - mean^2, 0).
+void layer_norm(const float* in, const float* w, const float* b, float* out, int n, float eps) {
+  float ps[256], pq[256];
+  for (int t = 0; t < 256; ++t) {
+    float sum = 0.0f, sq = 0.0f;
+    for (int i = t; i < n; i += 256) {
+      const float v = in[i];
+      sum = sum + v;
+      const float v2 = v * v;
+      sq = sq + v2;
+    }
+    ps[t] = sum;
+    pq[t] = sq;
+  }
+  for (int st = 128; st >= 1; st >>= 1)
+    for (int t = 0; t < st; ++t) {
+      ps[t] = ps[t] + ps[t + st];
+      pq[t] = pq[t] + pq[t + st];
+    }
+  const float mean = ps[0] / (float)n;
+  const float m2 = mean * mean;
+  const float variance = std::max(pq[0] / (float)n - m2, 0.0f);
+  const float inv_std = 1.0f / std::sqrt(variance + eps);
+  for (int i = 0; i < n; ++i) {
+    const float v = (in[i] - mean) * inv_std;
+    const float vw = v * w[i];
+    out[i] = vw + b[i];
+  }
+}
+
+// SANITIZE_WGSL (:1726-1746)
+inline float sanitize(float v) { return v != v ? 0.0f : std::min(std::max(v, -10000.0f), 10000.0f); }
+
+// GPT-2 attention: ATTENTION_SCORE_WGSL (:1773-1813, 64-thread tree per
+// position) and ATTENTION_VALUE_WGSL (:1815-1845: exp weights summed
+// unnormalised, divided once by max(denom, 1e-20)).
+void attention_gpt(orc_model* m, Layer& L, int pos, const float* q, float* out) {
+  const int hd = m->hd, C = m->ctx;
+  std::vector<float>& scores = m->scores;
+  scores.assign((size_t)L.heads * C, 0.0f);
+  m->pool->run(L.heads, [&](int64_t hb, int64_t he) {
+    float partial[64];
+    for (int64_t head = hb; head < he; ++head) {
+      for (int t = 0; t <= pos; ++t) {
+        const float* kr = L.kcache.data() + ((size_t)head * C + t) * hd;
+        for (int d = 0; d < 64; ++d) partial[d] = q[head * hd + d] * kr[d];
+        for (int st = 32; st >= 1; st >>= 1)
+          for (int d = 0; d < st; ++d) partial[d] = partial[d] + partial[d + st];
+        scores[(size_t)head * C + t] = partial[0] * m->attn_scale;
+      }
+      const float* sc = scores.data() + (size_t)head * C;
+      float mx = -3.402823e38f;
+      for (int t = 0; t <= pos; ++t) mx = std::fmax(mx, sc[t]);
+      for (int d = 0; d < hd; ++d) {
+        float denom = 0.0f, acc = 0.0f;
+        for (int t = 0; t <= pos; ++t) {
+          const float p = std::exp(sc[t] - mx);
+          denom = denom + p;
+          const float pv = p * L.vcache[((size_t)head * C + t) * hd + d];
+          acc = acc + pv;
+        }
+        out[head * hd + d] = acc / std::max(denom, 1e-20f);
+      }
+    }
+  });
+}
+
+// ARGMAX_STAGE1/2 of the GPT-2 runtime (:1896-2004): trees keeping the left
+// slot unless the right one is strictly greater (so NaN in the left slot stays
+// and ties go by tree position), padding -3.402823e38 with index 0; the
+// penalty applies to the listed ids whenever it is not 1.
+void argmax_gpt(const float* logits, int64_t vocab, const std::vector<int32_t>& sorted_ids, float pen,
+                uint8_t* pairs, int32_t* token) {
+  const int64_t groups = (vocab + 255) / 256;
+  float cv[256];
+  uint32_t ci[256];
+  for (int64_t gidx = 0; gidx < groups; ++gidx) {
+    float vals[256];
+    uint32_t idx[256];
+    for (int t = 0; t < 256; ++t) {
+      const int64_t i = gidx * 256 + t;
+      if (i < vocab) {
+        float v = logits[i];
+        if (!sorted_ids.empty() && std::binary_search(sorted_ids.begin(), sorted_ids.end(), (int32_t)i))
+          v = v > 0.0f ? v / pen : v * pen;
+        vals[t] = v;
+        idx[t] = (uint32_t)i;
+      } else {
+        vals[t] = kNegBig;
+        idx[t] = 0u;
+      }
+    }
+    for (int st = 128; st >= 1; st >>= 1)
+      for (int t = 0; t < st; ++t)
+        if (vals[t + st] > vals[t]) {
+          vals[t] = vals[t + st];
+          idx[t] = idx[t + st];
+        }
+    cv[gidx] = vals[0];
+    ci[gidx] = idx[0];
+    if (pairs) {
+      std::memcpy(pairs + 8 * gidx, &vals[0], 4);
+      std::memcpy(pairs + 8 * gidx + 4, &idx[0], 4);
+    }
+  }
+  for (int64_t t = groups; t < 256; ++t) {
+    cv[t] = kNegBig;
+    ci[t] = 0u;
+  }
+  for (int st = 128; st >= 1; st >>= 1)
+    for (int t = 0; t < st; ++t)
+      if (cv[t + st] > cv[t]) {
+        cv[t] = cv[t + st];
+        ci[t] = ci[t + st];
+      }
+  *token = (int32_t)ci[0];
+}
+
 void embedding(orc_model* m, int32_t token, float* out) {
   // GGUF_*_EMBEDDING_WGSL (:2615-2866): dequant(token row) * EMBEDDING_SCALE
   if (token < 0 || token >= m->vocab) throw std::runtime_error("token id " + std::to_string(token) + " outside embedding table");
@@ -718,6 +899,7 @@ orc_model* orc_model_load(const char* path, const orc_model_def* def, char* err,
     m->ff.assign(m->ffn, 0);
     m->logits.assign(m->vocab, 0);
     m->candidates.assign((size_t)(m->vocab + 255) / 256 * 8, 0);
+    if (m->gpt) m->qkv.assign(3 * (size_t)H, 0);
     return m;
   } catch (const std::exception& e) {
     if (err && err_len) std::snprintf(err, err_len, "%s", e.what());
@@ -734,6 +916,8 @@ void orc_model_free(orc_model* m) {
 }
 
 int orc_model_context(const orc_model* m) { return m->ctx; }
+int orc_model_is_gpt(const orc_model* m) { return m->gpt ? 1 : 0; }
+int orc_model_vocab(const orc_model* m) { return m->vocab; }
 int orc_model_position(const orc_model* m) { return m->pos; }
 
 void orc_model_reset(orc_model* m) {
@@ -895,10 +1079,69 @@ int32_t orc_sample_candidates(const uint8_t* pairs, int64_t n_groups, const orc_
   return !lim.empty() ? (int32_t)lim[0].id : 0;
 }
 
+// GptWgslEngine.runToken (gpt-wgsl-runtime.ts:749-840)
+static int32_t run_token_gpt(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
+                             const int32_t* penalized, int64_t n_penalized, const int32_t* seen, int64_t n_seen,
+                             double uniform) {
+  if (m->pos >= m->ctx) throw std::runtime_error("GPT WGSL context exhausted at " + std::to_string(m->ctx) + " tokens");
+  const int H = m->hidden, pos = m->pos, C = m->ctx;
+  Pool& pool = *m->pool;
+  float* hidden = m->hA.data();
+  embedding(m, token, hidden);
+  for (int h = 0; h < H; ++h) hidden[h] = hidden[h] + m->pos_embd[(size_t)pos * H + h];  // ADD_POSITION (:1639-1656)
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    Layer& L = m->layers[li];
+    layer_norm(hidden, L.in_norm.data(), L.in_norm_b.data(), m->norm.data(), H, m->norm_eps);
+    matvec(pool, L.qkv.type, L.qkv.data, L.qkv.n, L.qkv.k, m->norm.data(), m->qkv.data());
+    for (int i = 0; i < 3 * H; ++i) m->qkv[i] = m->qkv[i] + L.qkv_b[i];
+    for (int hh = 0; hh < L.heads; ++hh)  // STORE_KV (:1748-1771)
+      for (int d = 0; d < m->hd; ++d) {
+        const size_t ci = ((size_t)hh * C + pos) * m->hd + d;
+        L.kcache[ci] = kv_round(m, m->qkv[H + hh * m->hd + d]);
+        L.vcache[ci] = kv_round(m, m->qkv[2 * H + hh * m->hd + d]);
+      }
+    attention_gpt(m, L, pos, m->qkv.data(), m->attn.data());
+    matvec(pool, L.o.type, L.o.data, L.o.n, L.o.k, m->attn.data(), m->hB.data());
+    for (int i = 0; i < H; ++i) m->hB[i] = m->hB[i] + L.o_b[i];
+    for (int i = 0; i < H; ++i) hidden[i] = sanitize(hidden[i] + m->hB[i]);
+    layer_norm(hidden, L.post_norm.data(), L.post_norm_b.data(), m->norm.data(), H, m->norm_eps);
+    matvec(pool, L.up.type, L.up.data, L.up.n, L.up.k, m->norm.data(), m->ff.data());
+    for (int i = 0; i < L.ffn; ++i) m->ff[i] = gelu_tanh(m->ff[i] + L.up_b[i]);
+    matvec(pool, L.down.type, L.down.data, L.down.n, L.down.k, m->ff.data(), m->hB.data());
+    for (int i = 0; i < H; ++i) m->hB[i] = m->hB[i] + L.down_b[i];
+    for (int i = 0; i < H; ++i) hidden[i] = sanitize(hidden[i] + m->hB[i]);
+  }
+  m->last_residual.assign(hidden, hidden + H);
+  int32_t best = 0;
+  if (need_logits) {
+    layer_norm(hidden, m->final_norm.data(), m->final_norm_b.data(), m->norm.data(), H, m->norm_eps);
+    matvec(pool, m->lm_head.type, m->lm_head.data, (uint64_t)m->vocab, m->lm_head.k, m->norm.data(),
+           m->logits.data());
+    // the penalty list is the last maxContext seen ids whenever the penalty is not 1 (:785-796)
+    const double rp = s ? s->repetition_penalty : 1.0;
+    std::vector<int32_t> ids;
+    if (rp != 1.0 && n_penalized > 0) {
+      const int64_t keep = std::min<int64_t>(n_penalized, m->ctx);
+      ids.assign(penalized + (n_penalized - keep), penalized + n_penalized);
+      std::sort(ids.begin(), ids.end());
+    }
+    const float pen = (float)(uint32_t)std::floor(rp * 1000 + 0.5) / 1000.0f;
+    argmax_gpt(m->logits.data(), m->vocab, ids, pen, m->candidates.data(), &best);
+    const bool sampling = s && (s->temperature > 0 || s->top_p < 1 || s->top_k > 0);
+    if (sampling) best = orc_sample_candidates(m->candidates.data(), (m->vocab + 255) / 256, s, seen, n_seen, uniform);
+  }
+  m->pos += 1;
+  return best;
+}
+
 int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
                         const int32_t* penalized, int64_t n_penalized, const int32_t* seen, int64_t n_seen,
                         double uniform, int32_t* out_token, char* err, size_t err_len) {
   try {
+    if (m->gpt) {
+      *out_token = run_token_gpt(m, token, need_logits, s, penalized, n_penalized, seen, n_seen, uniform);
+      return 0;
+    }
     if (m->pos >= m->ctx)
       throw std::runtime_error("Llama WGSL context exhausted at " + std::to_string(m->ctx) + " tokens");
     const int H = m->hidden, pos = m->pos;

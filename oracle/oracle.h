@@ -59,10 +59,15 @@ typedef struct {
 orc_model* orc_model_load(const char* gguf_path, const orc_model_def* def, char* err, size_t err_len);
 void orc_model_free(orc_model* m);
 int orc_model_context(const orc_model* m);
+/* 1 for a GGUF of architecture gpt2 (gpt-wgsl-runtime.ts), else 0. */
+int orc_model_is_gpt(const orc_model* m);
+/* Vocabulary of the loaded model (ModelDef.vocab, or token_embd's rows for gpt2). */
+int orc_model_vocab(const orc_model* m);
 int orc_model_position(const orc_model* m);
 void orc_model_reset(orc_model* m);
 
-/* runToken (llama-wgsl-runtime.ts:1025-1150). `uniform` is the sampler's
+/* runToken (llama-wgsl-runtime.ts:1025-1150; for gpt2 GptWgslEngine.runToken,
+ * gpt-wgsl-runtime.ts:749-840). `uniform` is the sampler's
  * U in [0,1) (replaces Math.random). Returns 0, or -1 with err filled. */
 int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
                         const int32_t* penalized, int64_t n_penalized, const int32_t* seen, int64_t n_seen,

@@ -48,6 +48,8 @@ def lib():
         L.orc_model_load.argtypes = [C.c_char_p, C.POINTER(_Def), C.c_char_p, C.c_size_t]
         L.orc_model_free.argtypes = [P]
         L.orc_model_context.argtypes = [P]
+        L.orc_model_is_gpt.argtypes = [P]
+        L.orc_model_vocab.argtypes = [P]
         L.orc_model_position.argtypes = [P]
         L.orc_model_reset.argtypes = [P]
         L.orc_model_run_token.argtypes = [P, C.c_int32, C.c_int32, C.POINTER(_Samp), I32P, C.c_int64, I32P,
@@ -107,7 +109,8 @@ def sample_candidates(pairs: np.ndarray, temperature: float, top_p: float, top_k
 
 
 class OracleModel:
-    """CPU restatement of LlamaWgslEngine + generateLlamaWgsl."""
+    """CPU restatement of LlamaWgslEngine + generateLlamaWgsl, or for a gpt2
+    GGUF of GptWgslEngine + generateGptWgsl (gpt-wgsl-runtime.ts)."""
 
     def __init__(self, path: str, vocab: int, layers: int, max_context: int, kv_f16: bool = True,
                  threads: int = 8, eos_ids: Sequence[int] = (), default_repetition_penalty: Optional[float] = None):
@@ -116,7 +119,8 @@ class OracleModel:
         self._h = lib().orc_model_load(str(path).encode(), C.byref(d), err, 512)
         if not self._h:
             raise RuntimeError(err.value.decode())
-        self.vocab = vocab
+        self.gpt = bool(lib().orc_model_is_gpt(self._h))
+        self.vocab = int(lib().orc_model_vocab(self._h))
         self.max_context = max_context
         self.eos_ids = set(eos_ids)
         self.default_repetition_penalty = default_repetition_penalty
@@ -179,7 +183,9 @@ class OracleModel:
     def generate(self, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None, temperature=None,
                  top_p=None, top_k=None, repetition_penalty=None, seed: int = 0,
                  margins: Optional[list] = None) -> list[int]:
-        """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314)."""
+        """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314); generateGptWgsl
+        (gpt-wgsl-runtime.ts:182-249) for gpt2, which also runs the token after
+        the last generated one and refuses an empty prompt with no cached token."""
         prompt = list(prompt_ids)
         mx = min(128 if max_new_tokens is None else max_new_tokens, self.max_context - len(prompt))
         t = 0.0 if temperature is None else temperature
@@ -197,6 +203,8 @@ class OracleModel:
             prefix = 0
         suffix = prompt[prefix:]
         next_id = 0
+        if not suffix and self.gpt and self.cached_next_id is None:
+            raise RuntimeError("GPT WGSL has no cached next token for an empty prompt")
         if not suffix and self.cached_next_id is not None:
             next_id = self.cached_next_id
         else:
@@ -211,7 +219,7 @@ class OracleModel:
             generated.append(next_id)
             if next_id in self.eos_ids:
                 break
-            if step + 1 >= mx:
+            if step + 1 >= mx and not self.gpt:
                 break
             ids = prompt + generated
             next_id = self.run_token(next_id, True, t, tp, tk, rp, ids, ids, seed)

@@ -140,3 +140,79 @@ class NumpyDecoder:
         self.pos += 1
         self.last_hidden = x
         return self.lm[: self.vocab] @ self._rms(x, self.final_norm)
+
+
+class NumpyGpt2:
+    """Float64 GPT-2 decoder (the reference's GPT runtime, src/lib/gpt-wgsl-runtime.ts:749-840):
+    token + learned position embedding; per layer LayerNorm -> fused q|k|v + bias ->
+    multi-head attention -> output projection + bias -> residual, clamped to +-10000 (NaN -> 0);
+    LayerNorm -> up + bias -> GELU-tanh -> down + bias -> residual, clamped; final LayerNorm ->
+    output matrix. Closed forms in float64 (variance as the mean of squared deviations)."""
+
+    def __init__(self, path: str, max_context: int, kv_f16: bool = False):
+        g: Gguf = read_gguf(path)
+        p = "gpt2."
+        self.L = int(g.kv[p + "block_count"])
+        self.H = int(g.kv[p + "embedding_length"])
+        self.nh = int(g.kv[p + "attention.head_count"])
+        self.hd = self.H // self.nh
+        self.eps = float(np.float32(g.kv.get(p + "attention.layer_norm_epsilon", 1e-5)))
+        self.ctx = min(max_context, int(g.kv[p + "context_length"]))
+        self.kv_f16 = kv_f16
+        f = lambda n: matrix(g, n).astype(np.float64)
+        self.emb = f("token_embd.weight")
+        self.vocab = self.emb.shape[0]
+        self.pe = f("position_embd.weight")
+        self.lm = f("output.weight")
+        self.fn_w, self.fn_b = f("output_norm.weight"), f("output_norm.bias")
+        self.layers = []
+        for i in range(self.L):
+            b = f"blk.{i}."
+            self.layers.append({k: f(b + k) for k in (
+                "attn_norm.weight", "attn_norm.bias", "attn_qkv.weight", "attn_qkv.bias", "attn_output.weight",
+                "attn_output.bias", "ffn_norm.weight", "ffn_norm.bias", "ffn_up.weight", "ffn_up.bias",
+                "ffn_down.weight", "ffn_down.bias")})
+        self.reset()
+
+    def reset(self):
+        self.pos = 0
+        self.K = np.zeros((self.L, self.nh, self.ctx, self.hd))
+        self.V = np.zeros((self.L, self.nh, self.ctx, self.hd))
+
+    def _ln(self, x, w, b):
+        mu = x.mean()
+        return (x - mu) / np.sqrt(((x - mu) ** 2).mean() + self.eps) * w + b
+
+    @staticmethod
+    def _gelu(x):
+        c = 0.7978845608028654
+        g = 0.5 * x * (1 + np.tanh(c * (x + 0.044715 * x ** 3)))
+        return np.where(np.isnan(x), 0.0, np.where(x > 10, x, np.where(x < -10, 0.0, g)))
+
+    @staticmethod
+    def _sanitize(x):
+        return np.where(np.isnan(x), 0.0, np.clip(x, -10000.0, 10000.0))
+
+    def step(self, token: int) -> np.ndarray:
+        H, hd, nh = self.H, self.hd, self.nh
+        x = self.emb[token] + self.pe[self.pos]
+        for i, lay in enumerate(self.layers):
+            n = self._ln(x, lay["attn_norm.weight"], lay["attn_norm.bias"])
+            qkv = lay["attn_qkv.weight"] @ n + lay["attn_qkv.bias"]
+            q, k, v = qkv[:H].reshape(nh, hd), qkv[H:2 * H].reshape(nh, hd), qkv[2 * H:].reshape(nh, hd)
+            if self.kv_f16:
+                k = k.astype(np.float16).astype(np.float64)
+                v = v.astype(np.float16).astype(np.float64)
+            self.K[i, :, self.pos] = k
+            self.V[i, :, self.pos] = v
+            out = np.empty((nh, hd))
+            for h in range(nh):
+                s = self.K[i, h, :self.pos + 1] @ q[h] / np.sqrt(hd)
+                pr = np.exp(s - s.max())
+                out[h] = (pr / pr.sum()) @ self.V[i, h, :self.pos + 1]
+            x = self._sanitize(x + lay["attn_output.weight"] @ out.reshape(-1) + lay["attn_output.bias"])
+            n = self._ln(x, lay["ffn_norm.weight"], lay["ffn_norm.bias"])
+            u = self._gelu(lay["ffn_up.weight"] @ n + lay["ffn_up.bias"])
+            x = self._sanitize(x + lay["ffn_down.weight"] @ u + lay["ffn_down.bias"])
+        self.pos += 1
+        return self.lm @ self._ln(x, self.fn_w, self.fn_b)

@@ -20,7 +20,7 @@ from chonklm_amd import WORKLOADS
 from oracle.oracle import OracleModel
 from tests import ggufpy
 from tests.conftest import rel_err
-from tests.numpy_ref import NumpyDecoder
+from tests.numpy_ref import NumpyDecoder, NumpyGpt2
 
 TINY = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "greedy_golden.json").read_text())
@@ -126,3 +126,37 @@ def test_context_exhaustion_message(synth):
         ref.run_token(t + 1, False)
     with pytest.raises(RuntimeError, match="context exhausted at 4 tokens"):
         ref.run_token(1, True)
+
+
+def test_gpt2_logits_match_float64_decoder(synth):
+    """The oracle's GPT-2 path (gpt-wgsl-runtime.ts:749-840: LayerNorm with bias, fused q|k|v,
+    biases, GELU-tanh, +-10000 residual clamp, learned positions) against the float64 decoder."""
+    w, path, ref = _oracle(synth, "tiny-gpt2")
+    assert ref.gpt and ref.vocab == w.spec.vocab
+    dec = NumpyGpt2(path, w.max_context, kv_f16=True)
+    prompt = np.random.default_rng(6).integers(0, w.spec.vocab, 10).tolist()
+    tok = prompt[0]
+    for i in range(len(prompt) + 8):
+        if i < len(prompt):
+            tok = prompt[i]
+        a = ref.run_token(tok, True)
+        want = dec.step(tok)
+        assert rel_err(ref.logits(), want) <= 1e-4, f"step {i}"
+        if i >= len(prompt) - 1:
+            tok = a
+
+
+def test_gpt2_generate_loop(synth):
+    """generateGptWgsl (:182-249): one runToken past the last generated token, and an empty
+    prompt needs a cached next token."""
+    w, path, ref = _oracle(synth, "tiny-gpt2")
+    prompt = np.random.default_rng(7).integers(0, w.spec.vocab, 9).tolist()
+    ids = ref.generate(prompt, 6)
+    assert len(ids) <= 6
+    if w.eos_ids[0] not in ids:
+        assert ref.position == len(prompt) + len(ids)
+        assert ref.cached_next_id is not None
+    ref.reset()
+    ref.cached_token_ids, ref.cached_next_id = [], None
+    with pytest.raises(RuntimeError, match="no cached next token"):
+        ref.generate([], 3)
