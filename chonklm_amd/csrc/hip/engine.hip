@@ -169,6 +169,8 @@ struct LayerCfg {
 struct ModelCfg {
   std::string arch;
   bool gemma = false, interleaved = false, qk_norm = false;
+  bool gpt = false;  // GGUF architecture gpt2: the reference's GPT runtime (gpt-wgsl-runtime.ts)
+  int pos_rows = 0;  // gpt2: rows of the learned position table (gpt2.context_length)
   int hidden = 0, ffn = 0, vocab = 0, layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float eps = 1e-5f, qk_eps = 1e-5f, scale = 0, embed_scale = 1;
   std::vector<LayerCfg> layer;
@@ -188,6 +190,34 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
   c.arch = a->str;
   if (c.arch == "openelm")
     throw Error(CHONK_EINVAL, "architecture openelm (fused qkv, per-layer heads) is not supported by this engine yet");
+  if (c.arch == "gpt2") {
+    // manifestFromGguf (gpt-wgsl-runtime.ts:274-356)
+    c.gpt = true;
+    c.layers = (int)meta_number(g, "gpt2.block_count", nullptr);
+    c.hidden = (int)meta_number(g, "gpt2.embedding_length", nullptr);
+    c.ffn = (int)meta_number(g, "gpt2.feed_forward_length", nullptr);
+    c.heads = (int)meta_number(g, "gpt2.attention.head_count", nullptr);
+    c.pos_rows = (int)meta_number(g, "gpt2.context_length", nullptr);
+    const double eps_default = 1e-5;
+    c.eps = (float)meta_number(g, "gpt2.attention.layer_norm_epsilon", &eps_default);
+    if (c.heads <= 0 || c.hidden % c.heads)
+      throw Error(CHONK_EINVAL, "GPT WGSL: hidden " + std::to_string(c.hidden) + " is not divisible by heads");
+    c.hd = c.hidden / c.heads;
+    if (c.hd != 64)
+      throw Error(CHONK_EINVAL, "GPT WGSL: only 64-wide GPT-2 heads are implemented, got " + std::to_string(c.hd));
+    c.kv_heads = c.heads;
+    const GgufTensorInfo* te = g.find("token_embd.weight");
+    if (!te || te->shape.size() != 2) throw Error(CHONK_EINVAL, "GPT WGSL: missing token_embd.weight");
+    c.vocab = (int)te->shape[1];
+    if ((c.vocab + 255) / 256 > 256)
+      throw Error(CHONK_EINVAL, "GPT WGSL argmax supports at most 65536 vocab entries, got " + std::to_string(c.vocab));
+    c.ctx = std::min(def.max_context, c.pos_rows);
+    c.scale = (float)(1.0 / std::sqrt((double)c.hd));  // INV_SQRT_HEAD_DIM (:1066)
+    c.layer.assign(c.layers, LayerCfg{0, 0});           // no rotary embedding
+    if (c.layers <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
+      throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+    return c;
+  }
   if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3")
     throw Error(CHONK_EINVAL, "Llama GGUF WGSL does not support architecture " + c.arch);
   c.gemma = c.arch == "gemma3";
@@ -237,6 +267,10 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
 
 struct LayerDev {
   DevMat q, k, v, o, gate, up, down;
+  DevMat qkv;  // gpt2: fused q|k|v
+  // gpt2: LayerNorm biases (in_norm / post_norm hold the weights) and linear biases
+  float *in_norm_b = nullptr, *post_norm_b = nullptr, *qkv_b = nullptr, *o_b = nullptr, *up_b = nullptr,
+        *down_b = nullptr;
   float *in_norm = nullptr, *post_norm = nullptr, *pre_ffn_norm = nullptr, *post_ffn_norm = nullptr;
   float *q_norm = nullptr, *k_norm = nullptr;
   void *kc = nullptr, *vc = nullptr;
@@ -274,6 +308,7 @@ struct chonk_engine {
   std::vector<LayerDev> layers;
   DevMat embed, lm_head;
   float* final_norm = nullptr;
+  float *final_norm_b = nullptr, *pos_embd = nullptr;  // gpt2: final LayerNorm bias, position table
   size_t kv_elem = 2;
   // activations
   float *resA = nullptr, *resB = nullptr, *delta = nullptr, *qkv = nullptr, *attn = nullptr, *ff = nullptr,
@@ -542,11 +577,18 @@ void use_row_kernel(MvArgs& a) {
     const char* v = std::getenv("CHONK_MV");
     return v && std::string(v) == "generic";
   }();
-  if (off || a.epi == EPI_LOGITS) return;
+  // GPT-2's prologues and epilogues (LayerNorm, biases, GELU, clamped residual)
+  // exist only in the row kernels
+  bool needs_row = a.epi == EPI_GELU || a.pro == PRO_LN || a.pro == PRO_EMBED_LN || a.sanitize;
+  for (int i = 0; i < a.nseg; ++i) needs_row = needs_row || a.seg[i].bias;
+  if ((off && !needs_row) || a.epi == EPI_LOGITS) return;
   // the register-resident plain / norm prologues hold at most 4 float4 per thread
   if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) return;
   for (int i = 0; i < a.nseg; ++i)
-    if (a.seg[i].w.k / 32 > kRowUnits * 64) return;
+    if (a.seg[i].w.k / 32 > kRowUnits * 64) {
+      if (needs_row) throw Error(CHONK_EINVAL, "GPT-2 layers need rows of at most 8192 weights");
+      return;
+    }
   // one unit per lane and >= 192 workgroups per segment; the three-segment
   // q|k|v launch runs faster with two units per lane and half the workgroups
   // (measured on the Qwen3-0.6B shapes)
@@ -565,7 +607,8 @@ const float* rope_table(chonk_engine* e, uint32_t theta, int hd) {
   for (const auto& t : e->rope_tables)
     if (t.first == theta) return t.second;
   std::vector<float> inv((size_t)hd / 2);
-  for (int d = 0; d < hd / 2; ++d) inv[d] = std::pow((float)theta, (-2.0f * (float)d) / (float)hd);
+  // theta 0: no rotary embedding (GPT-2): every angle is 0
+  for (int d = 0; d < hd / 2; ++d) inv[d] = theta == 0 ? 0.0f : std::pow((float)theta, (-2.0f * (float)d) / (float)hd);
   float* p = (float*)e->weights.take(inv.size() * 4);
   HIP_OK(hipMemcpy(p, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
   e->rope_tables.emplace_back(theta, p);
@@ -615,8 +658,33 @@ void build_steps(chonk_engine* e) {
   for (int i = 0; i < c.layers; ++i) {
     LayerDev& Ld = e->layers[i];
     const std::string li = "L" + std::to_string(i) + ".";
-    // qkv
-    {
+    // qkv (gpt2: one fused matrix with bias, LayerNorm prologue; embedding +
+    // position on layer 0)
+    if (c.gpt) {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = H;
+      a.nseg = 1;
+      plan_seg(a.seg[0], Ld.qkv.q, 3 * H, false, 0);
+      a.seg[0].out = e->qkv;
+      a.seg[0].bias = Ld.qkv_b;
+      a.epi = EPI_STORE;
+      a.w_norm = Ld.in_norm;
+      a.norm_b = Ld.in_norm_b;
+      if (i == 0) {
+        a.pro = PRO_EMBED_LN;
+        a.pos_embd = e->pos_embd;
+        a.res_out = e->resA;
+      } else {
+        a.pro = PRO_LN;
+        a.in = e->resA;
+      }
+      finish(L, a, a.seg[0].tile);
+      L.name = li + "qkv";
+      L.weight_bytes = Ld.qkv.gguf_bytes + (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
+      L.layer = i;
+      steps.push_back(L);
+    } else {
       Launch L;
       MvArgs a = mv_base();
       a.k = H;
@@ -713,14 +781,36 @@ void build_steps(chonk_engine* e) {
         a.seg[0].out = e->resB;
         a.seg[0].add = e->resA;
       }
+      if (c.gpt) {
+        a.seg[0].bias = Ld.o_b;
+        a.sanitize = 1;
+      }
       finish(L, a, a.seg[0].tile);
       L.name = li + "oproj";
       L.weight_bytes = Ld.o.gguf_bytes;
       L.layer = i;
       steps.push_back(L);
     }
-    // gate|up
-    {
+    // gate|up (gpt2: up with bias, GELU-tanh, LayerNorm prologue)
+    if (c.gpt) {
+      Launch L;
+      MvArgs a = mv_base();
+      a.k = H;
+      a.nseg = 1;
+      plan_seg(a.seg[0], Ld.up.q, c.ffn, false, 0);
+      a.seg[0].out = e->ff;
+      a.seg[0].bias = Ld.up_b;
+      a.epi = EPI_GELU;
+      a.pro = PRO_LN;
+      a.in = e->resB;
+      a.w_norm = Ld.post_norm;
+      a.norm_b = Ld.post_norm_b;
+      finish(L, a, a.seg[0].tile);
+      L.name = li + "gateup";
+      L.weight_bytes = Ld.up.gguf_bytes;
+      L.layer = i;
+      steps.push_back(L);
+    } else {
       Launch L;
       MvArgs a = mv_base();
       a.k = H;
@@ -764,6 +854,10 @@ void build_steps(chonk_engine* e) {
         a.seg[0].out = e->resA;
         a.seg[0].add = e->resB;
       }
+      if (c.gpt) {
+        a.seg[0].bias = Ld.down_b;
+        a.sanitize = 1;
+      }
       finish(L, a, a.seg[0].tile);
       L.name = li + "down";
       L.weight_bytes = Ld.down.gguf_bytes;
@@ -788,7 +882,12 @@ void build_steps(chonk_engine* e) {
     sg.out = e->logits;
     a.epi = EPI_LOGITS;
     a.w_norm = e->final_norm;
-    if (c.gemma) {
+    a.gpt_argmax = c.gpt ? 1 : 0;
+    if (c.gpt) {
+      a.pro = PRO_LN;
+      a.in = e->resA;
+      a.norm_b = e->final_norm_b;
+    } else if (c.gemma) {
       a.pro = PRO_RES_NORM;
       a.in = e->resB;
       a.delta = e->delta;
@@ -808,6 +907,7 @@ void build_steps(chonk_engine* e) {
     L.kind = Launch::SEL;
     SelArgs& s = L.sel;
     s.cand = e->cand;
+    s.gpt_argmax = c.gpt ? 1 : 0;
     s.groups = e->groups;
     s.vocab = c.vocab;
     s.ctx = c.ctx;
@@ -832,6 +932,7 @@ bool build_step(chonk_engine* e) {
   const ModelCfg& c = e->cfg;
   const int G = c.heads / c.kv_heads;
   const bool kv16 = e->kv_elem == 2;
+  if (c.gpt) return false;  // the persistent step runs the llama-family layer only
   if (!step_supported(G, kv16)) return false;
   int cus = 0;
   HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
@@ -1153,7 +1254,25 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   mat_bytes("token_embd.weight", H, c.vocab);
   if (!tied) mat_bytes(lm_name, H, c.vocab);
   vec_bytes(H);
-  for (int i = 0; i < c.layers; ++i) {
+  if (c.gpt) {
+    if (tied) throw Error(CHONK_EINVAL, "GPT WGSL GGUF missing tensor output.weight");
+    vec_bytes(H);                                // final LayerNorm bias
+    vec_bytes((int64_t)c.pos_rows * H);          // position table
+    vec_bytes(c.hd / 2);                         // (zero) rotary table
+    for (int i = 0; i < c.layers; ++i) {
+      const std::string p = "blk." + std::to_string(i) + ".";
+      mat_bytes(p + "attn_qkv.weight", H, 3 * (int64_t)H);
+      mat_bytes(p + "attn_output.weight", H, H);
+      mat_bytes(p + "ffn_up.weight", H, c.ffn);
+      mat_bytes(p + "ffn_down.weight", c.ffn, H);
+      for (int v = 0; v < 4; ++v) vec_bytes(H);  // LayerNorm weights and biases
+      vec_bytes(3 * (int64_t)H);
+      vec_bytes(H);
+      vec_bytes(c.ffn);
+      vec_bytes(H);
+    }
+  }
+  for (int i = 0; i < (c.gpt ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     mat_bytes(p + "attn_q.weight", H, qdim);
     mat_bytes(p + "attn_k.weight", H, kvdim);
@@ -1218,7 +1337,31 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->embed = upload_matrix(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
   e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
   e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
-  for (int i = 0; i < c.layers; ++i) {
+  if (c.gpt) {
+    // GptWgslEngine buffers (gpt-wgsl-runtime.ts:540-640)
+    e->final_norm_b = upload_floats(e->weights, *src, g, "output_norm.bias", H);
+    e->pos_embd = upload_floats(e->weights, *src, g, "position_embd.weight", (int64_t)c.pos_rows * H);
+    for (int i = 0; i < c.layers; ++i) {
+      const std::string p = "blk." + std::to_string(i) + ".";
+      LayerDev L;
+      L.in_norm = upload_floats(e->weights, *src, g, p + "attn_norm.weight", H);
+      L.in_norm_b = upload_floats(e->weights, *src, g, p + "attn_norm.bias", H);
+      L.post_norm = upload_floats(e->weights, *src, g, p + "ffn_norm.weight", H);
+      L.post_norm_b = upload_floats(e->weights, *src, g, p + "ffn_norm.bias", H);
+      L.qkv = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_qkv.weight"), H, 3 * (int64_t)H);
+      L.qkv_b = upload_floats(e->weights, *src, g, p + "attn_qkv.bias", 3 * (int64_t)H);
+      L.o = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_output.weight"), H, H);
+      L.o_b = upload_floats(e->weights, *src, g, p + "attn_output.bias", H);
+      L.up = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_up.weight"), H, c.ffn);
+      L.up_b = upload_floats(e->weights, *src, g, p + "ffn_up.bias", c.ffn);
+      L.down = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_down.weight"), c.ffn, H);
+      L.down_b = upload_floats(e->weights, *src, g, p + "ffn_down.bias", H);
+      L.kc = e->state.take(kv_bytes);
+      L.vc = e->state.take(kv_bytes);
+      e->layers.push_back(L);
+    }
+  }
+  for (int i = 0; i < (c.gpt ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     LayerDev L;
     L.in_norm = upload_floats(e->weights, *src, g, p + "attn_norm.weight", H);
@@ -1246,8 +1389,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   }
   uint64_t wpt = e->lm_head.gguf_bytes + e->embed.gguf_bytes / c.vocab + (uint64_t)H * 4;
   for (const LayerDev& L : e->layers)
-    wpt += L.q.gguf_bytes + L.k.gguf_bytes + L.v.gguf_bytes + L.o.gguf_bytes + L.gate.gguf_bytes + L.up.gguf_bytes +
-           L.down.gguf_bytes + (uint64_t)H * 4 * (c.gemma ? 4 : 2) + (c.qk_norm ? 2ull * c.hd * 4 : 0);
+    wpt += L.q.gguf_bytes + L.k.gguf_bytes + L.v.gguf_bytes + L.qkv.gguf_bytes + L.o.gguf_bytes + L.gate.gguf_bytes +
+           L.up.gguf_bytes + L.down.gguf_bytes + (uint64_t)H * 4 * (c.gemma || c.gpt ? 4 : 2) +
+           (c.qk_norm ? 2ull * c.hd * 4 : 0) + (c.gpt ? 4ull * (5 * (uint64_t)H + c.ffn) : 0);
+  if (c.gpt) wpt += 8ull * H;  // final LayerNorm bias, the position row
   e->weight_bytes_per_token = wpt;
 
   e->resA = (float*)e->state.take((size_t)H * 4);
@@ -1298,7 +1443,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
   // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
-  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) &&
+  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt &&
                        std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) <= 4096;
   const char* ng = std::getenv("CHONK_NO_GRAPH");
   e->use_graph = !(ng && ng[0] == '1');
@@ -1705,13 +1850,15 @@ void prefill_rows(chonk_engine* e, const int32_t* tokens, int n) {
 int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
                   size_t n_pen, const int32_t* seen, size_t n_seen) {
   if (e->pos >= e->cfg.ctx)
-    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+    throw Error(CHONK_ECONTEXT, std::string(e->cfg.gpt ? "GPT" : "Llama") + " WGSL context exhausted at " +
+                                    std::to_string(e->cfg.ctx) + " tokens");
   check_token(e, token);
   put_token(e, e->pos, token);
   if (need_logits) {
     // argmax(): the penalty list is the last `context` ids (:1649-1653)
     const double rp = s ? s->repetition_penalty : 1.0;
-    const bool stage1 = rp > 1 && n_pen > 0;
+    // (the GPT-2 runtime applies the list whenever the penalty is not 1, :785-796)
+    const bool stage1 = (e->cfg.gpt ? rp != 1.0 : rp > 1) && n_pen > 0;
     const size_t keep = std::min(n_pen, (size_t)e->cfg.ctx);
     if (stage1) upload_bits(e, e->pen_bits, pen + (n_pen - keep), keep);
     const DevSampling d = make_sampling(e, s, stage1, n_seen > 0);
@@ -1897,6 +2044,9 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
   }
   int32_t next = 0;
   const size_t n_suffix = n_prompt - (size_t)prefix;
+  const bool gpt = e->cfg.gpt;
+  if (n_suffix == 0 && gpt && !e->has_cached_next)
+    throw Error(CHONK_EINVAL, "GPT WGSL has no cached next token for an empty prompt");
   if (n_suffix == 0 && e->has_cached_next) {
     next = e->cached_next;
   } else {
@@ -1916,7 +2066,9 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
     ids.push_back(next);
     if (cb) cb(user, 1, next);
     if (is_eos(next)) break;
-    if (step + 1 >= max) break;
+    // (generateGptWgsl, gpt-wgsl-runtime.ts:228-245, also runs the token after
+    // the last generated one: its result is the cached next id)
+    if (step + 1 >= max && !gpt) break;
     next = run_token(e, next, true, &s, ids.data(), ids.size(), ids.data(), ids.size());
   }
   const double t_end = now_ms();
@@ -2016,7 +2168,14 @@ int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n) {
     if (!tokens) throw Error(CHONK_EINVAL, "tokens is null");
     for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
     if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
-      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+      throw Error(CHONK_ECONTEXT, std::string(e->cfg.gpt ? "GPT" : "Llama") + " WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+    if (!e->batched_prefill) {
+      // token by token through the decode step (gpt2, or CHONK_PREFILL=token)
+      for (size_t i = 0; i < n; ++i) run_token(e, tokens[i], false, nullptr, nullptr, 0, nullptr, 0);
+      e->known_token_pos = -1;
+      e->logits_valid = false;
+      return;
+    }
     HIP_OK(hipMemcpy(e->hist + e->pos, tokens, n * 4, hipMemcpyHostToDevice));
     prefill_rows(e, tokens, (int)n);
     e->pos += (int)n;
@@ -2034,7 +2193,11 @@ int chonk_engine_generate(chonk_engine* e, const int32_t* prompt, size_t n_promp
   return api(e, [&] {
     if (!prompt && n_prompt) throw Error(CHONK_EINVAL, "null prompt");
     std::vector<int32_t> ids;
-    generate(e, prompt, n_prompt, max_new_tokens, s, &ids, stats);
+    // GPT-2 follows generateGptWgsl from the host (one more step at the end)
+    if (e->cfg.gpt)
+      generate_stepped(e, prompt, n_prompt, max_new_tokens, s, nullptr, nullptr, &ids, stats);
+    else
+      generate(e, prompt, n_prompt, max_new_tokens, s, &ids, stats);
     const size_t n = std::min(ids.size(), out_cap);
     if (out_ids && n) std::memcpy(out_ids, ids.data(), n * 4);
     if (n_out) *n_out = ids.size();
@@ -2569,6 +2732,7 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
     throw Error(CHONK_EINVAL, "batch needs 1..1024 sequences of 1.." + std::to_string(c.ctx) + " tokens");
   if (std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) > 4096)
     throw Error(CHONK_EINVAL, "batched decoding needs hidden, q and ffn widths of at most 4096");
+  if (c.gpt) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not gpt2");
   if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
   if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
   std::unique_ptr<chonk_batch, void (*)(chonk_batch*)> b(new chonk_batch(), batch_free);

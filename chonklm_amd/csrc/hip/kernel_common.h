@@ -170,6 +170,7 @@ struct SegView {
   const uint8_t *u0, *u1, *u2, *u3;  // GLU up-matrix streams
   float* out;
   const float* add;
+  const float* bias;
   int n_out, tile, lpr, wg_begin;
 };
 
@@ -811,7 +812,28 @@ __device__ __forceinline__ void select_token(const SelArgs& a, uint8_t* ws) {
   int token = 0;
   const int groups = a.groups;
 
-  if (s.sample_mode == 0) {
+  if (s.sample_mode == 0 && a.gpt_argmax) {
+    // the GPT-2 runtime's ARGMAX_STAGE2 (gpt-wgsl-runtime.ts:1961-2004): one
+    // slot per group (at most 256), padding (-3.402823e38, 0), a tree that
+    // keeps the left slot unless the right one is strictly greater
+    if (tid < groups) {
+      const Candidate c = a.cand[tid];
+      vals[tid] = c.value;
+      idx[tid] = c.index;
+    } else {
+      vals[tid] = kNegBig;
+      idx[tid] = 0u;
+    }
+    __syncthreads();
+    for (int stride = 128; stride >= 1; stride >>= 1) {
+      if (tid < stride && vals[tid + stride] > vals[tid]) {
+        vals[tid] = vals[tid + stride];
+        idx[tid] = idx[tid + stride];
+      }
+      __syncthreads();
+    }
+    token = (int)idx[0];
+  } else if (s.sample_mode == 0) {
     float bv = kNegBig;
     uint32_t bi = 0xffffffffu;
     for (int g = tid; g < groups; g += kWg) {

@@ -23,6 +23,8 @@ enum ProMode : int32_t {
   PRO_NORM = 1,          // xs = rmsnorm(in) * w_norm
   PRO_EMBED_NORM = 2,    // r = embed(hist[pos]) * scale; WG0 writes r; xs = rmsnorm(r) * w_norm
   PRO_RES_NORM = 3,      // r = clamp(in + rmsnorm(delta) * w_delta, +-65000); WG0 writes r; xs = rmsnorm(r) * w_norm
+  PRO_LN = 5,            // xs = layernorm(in) * w_norm + norm_b (GPT-2)
+  PRO_EMBED_LN = 6,      // r = embed(hist[pos]) + pos_embd[pos]; WG0 writes r; xs = layernorm(r) * w_norm + norm_b
 };
 
 enum EpiMode : int32_t {
@@ -31,6 +33,7 @@ enum EpiMode : int32_t {
   EPI_GLU_SILU = 2, // out[n] = silu(gate_n) * up_n
   EPI_GLU_GELU = 3, // out[n] = gelu_tanh(gate_n) * up_n
   EPI_LOGITS = 4,   // logits[n] = acc; group candidate per 256 rows
+  EPI_GELU = 5,     // out[n] = gelu_tanh(acc + bias[n]) (GPT-2 MLP up projection)
 };
 
 struct MvSeg {
@@ -38,6 +41,7 @@ struct MvSeg {
   QMat w2;           // GLU: up
   float* out;
   const float* add;  // EPI_ADD residual input
+  const float* bias; // added to each row's sum first when set (GPT-2 linear biases)
   int32_t n_out;     // output rows
   int32_t tile;      // output rows per workgroup
   int32_t lpr;       // lanes per row (power of two, <= 64)
@@ -62,6 +66,10 @@ struct MvArgs {
   int32_t vocab;
   int32_t advance_pos;    // WG0 advances st->pos when done (steps without logits)
   int32_t row_kernel;     // 1: one output row per lane group (k_mvr_*, planned by plan_seg_row)
+  const float* norm_b;    // PRO_LN / PRO_EMBED_LN: LayerNorm bias
+  const float* pos_embd;  // PRO_EMBED_LN: learned position table [context][k]
+  int32_t sanitize;       // EPI_ADD: NaN -> 0, clamp to +-10000 (GPT-2 residual)
+  int32_t gpt_argmax;     // EPI_LOGITS: the GPT-2 runtime's group argmax (strict >, left slot kept)
   const uint32_t* pen_bits;
   const DevSampling* samp;
   Candidate* cand;
@@ -98,6 +106,7 @@ __host__ __device__ constexpr int attn_rowf(int G, int hd) { return (G * (hd + 2
 
 struct SelArgs {
   const Candidate* cand;
+  int32_t gpt_argmax;     // greedy stage 2 with the GPT-2 runtime's tree (strict >, left slot kept)
   int32_t groups;
   int32_t vocab;
   int32_t ctx;

@@ -50,6 +50,7 @@ __device__ __forceinline__ SegView seg_view(const MvArgs& a) {
   v.u3 = CHONK_PICK(w2.s3);
   v.out = CHONK_PICK(out);
   v.add = CHONK_PICK(add);
+  v.bias = CHONK_PICK(bias);
   v.n_out = CHONK_PICK(n_out);
   v.tile = CHONK_PICK(tile);
   v.lpr = CHONK_PICK(lpr);
@@ -80,7 +81,7 @@ __device__ __forceinline__ MvLds mv_lds(float* smem, int K) {
 // variant of the matvec inlines the prologue, and reading the argument block
 // from all of them makes the compiler stage the whole block in scratch.
 struct MvPro {
-  const float *in, *delta, *w_delta, *w_norm;
+  const float *in, *delta, *w_delta, *w_norm, *norm_b, *pos_embd;
   float* res_out;
   QMat embed;
   const int32_t* hist;
@@ -95,6 +96,8 @@ __device__ __forceinline__ MvPro mv_pro(const MvArgs& a) {
   p.delta = a.delta;
   p.w_delta = a.w_delta;
   p.w_norm = a.w_norm;
+  p.norm_b = a.norm_b;
+  p.pos_embd = a.pos_embd;
   p.res_out = a.res_out;
   p.embed = a.embed;
   p.hist = a.hist;
@@ -122,6 +125,15 @@ __device__ __forceinline__ void mv_stage(const MvPro& a, const MvLds& l) {
       lds_dma(a.w_delta, l.wd, K);
       lds_dma(a.w_norm, l.wn, K);
       break;
+    case PRO_LN:
+      lds_dma(a.in, l.xs, K);
+      lds_dma(a.w_norm, l.wn, K);
+      lds_dma(a.norm_b, l.wd, K);
+      break;
+    case PRO_EMBED_LN:  // the row depends on the token
+      lds_dma(a.w_norm, l.wn, K);
+      lds_dma(a.norm_b, l.wd, K);
+      break;
     default:  // PRO_EMBED_NORM: the row depends on the token; only the norm weight is staged
       lds_dma(a.w_norm, l.wn, K);
       break;
@@ -133,8 +145,9 @@ __device__ __forceinline__ void mv_stage(const MvPro& a, const MvLds& l) {
 __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
   const int K = a.k, tid = threadIdx.x;
   float* xs = l.xs;
-  if (a.pro == PRO_EMBED_NORM) {
-    int tok = a.hist[a.st->pos];
+  if (a.pro == PRO_EMBED_NORM || a.pro == PRO_EMBED_LN) {
+    const int pos = a.st->pos;
+    int tok = a.hist[pos];
     if (tok < 0 || tok >= a.vocab) {
       if (tid == 0 && blockIdx.x == 0) a.st->error = 2;
       tok = 0;
@@ -150,6 +163,11 @@ __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
       }
     });
     __syncthreads();
+    if (a.pro == PRO_EMBED_LN) {
+      // ADD_POSITION (gpt-wgsl-runtime.ts:1639-1656)
+      for (int i = tid; i < K; i += kWg) xs[i] = __fadd_rn(xs[i], a.pos_embd[(size_t)pos * K + i]);
+      __syncthreads();
+    }
   } else if (a.pro == PRO_RES_NORM) {
     float ss = 0.f;
     for (int i = tid; i < K; i += kWg) ss += l.dl[i] * l.dl[i];
@@ -161,7 +179,27 @@ __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
     }
     __syncthreads();
   }
-  if (a.pro != PRO_PLAIN) {
+  if (a.pro == PRO_LN || a.pro == PRO_EMBED_LN) {
+    // LAYER_NORM_WGSL (gpt-wgsl-runtime.ts:1658-1706): mean and E[x^2] in one
+    // pass, variance max(E[x^2] - mean^2, 0), ((x - mean) * inv_std) * w + b
+    if (a.pro == PRO_EMBED_LN && blockIdx.x == 0) {
+      for (int i = tid; i < K; i += kWg) a.res_out[i] = xs[i];
+    }
+    float sm = 0.f, sq = 0.f;
+    for (int i = tid; i < K; i += kWg) {
+      sm += xs[i];
+      sq += xs[i] * xs[i];
+    }
+    sm = block_sum(sm, l.red);
+    sq = block_sum(sq, l.red);
+    const float mean = sm / (float)K;
+    const float var = fmaxf(__fsub_rn(sq / (float)K, __fmul_rn(mean, mean)), 0.0f);
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    __syncthreads();  // every thread has read xs for the sums
+    for (int i = tid; i < K; i += kWg)
+      xs[i] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xs[i], mean), inv), l.wn[i]), l.wd[i]);
+    __syncthreads();
+  } else if (a.pro != PRO_PLAIN) {
     if ((a.pro == PRO_EMBED_NORM || a.pro == PRO_RES_NORM) && blockIdx.x == 0) {
       for (int i = tid; i < K; i += kWg) a.res_out[i] = xs[i];
     }
@@ -251,7 +289,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
       float* vals = res + 256;
       uint32_t* idx = (uint32_t*)(vals + 256);
       float v = kNegBig;
-      uint32_t id = 0xffffffffu;
+      uint32_t id = a.gpt_argmax ? 0u : 0xffffffffu;
       const int row = t0 + tid;
       if (tid < nt && row < a.vocab) {
         v = res[tid];
@@ -265,11 +303,13 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
       vals[tid] = v;
       idx[tid] = id;
       __syncthreads();
+      // (the GPT-2 runtime's ARGMAX_STAGE1, gpt-wgsl-runtime.ts:1896-1959,
+      // keeps the left slot unless the right one is strictly greater)
       for (int stride = 128; stride >= 1; stride >>= 1) {
         if (tid < stride) {
           const float ov = vals[tid + stride];
           const uint32_t oi = idx[tid + stride];
-          if (better(ov, oi, vals[tid], idx[tid])) {
+          if (a.gpt_argmax ? ov > vals[tid] : better(ov, oi, vals[tid], idx[tid])) {
             vals[tid] = ov;
             idx[tid] = oi;
           }
@@ -334,8 +374,9 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   } else {
     mv_stage(p, l);
   }
-  float addv = 0.f;
+  float addv = 0.f, biasv = 0.f;
   if constexpr (EPI == EPI_ADD) addv = g.add[row];
+  if (g.bias) biasv = g.bias[row];
   float rg = 0.f, ru = 0.f;
   bool live = false;
   with_type(g.w.type, [&]<int T>() {
@@ -407,10 +448,16 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   });
   if (!live) return;
   if (owner) {
+    if (g.bias) rg = __fadd_rn(rg, biasv);
     if constexpr (EPI == EPI_STORE) g.out[row] = rg;
-    if constexpr (EPI == EPI_ADD) g.out[row] = __fadd_rn(addv, rg);
+    if constexpr (EPI == EPI_ADD) {
+      float y = __fadd_rn(addv, rg);
+      if (a.sanitize) y = y != y ? 0.0f : fminf(fmaxf(y, -10000.0f), 10000.0f);  // SANITIZE (gpt-wgsl-runtime.ts:1726-1746)
+      g.out[row] = y;
+    }
     if constexpr (EPI == EPI_GLU_SILU) g.out[row] = silu_mul(rg, ru);
     if constexpr (EPI == EPI_GLU_GELU) g.out[row] = __fmul_rn(gelu_tanh(rg), ru);
+    if constexpr (EPI == EPI_GELU) g.out[row] = gelu_tanh(rg);
   }
   if (a.advance_pos && blockIdx.x == 0 && threadIdx.x == 0) a.st->pos = a.st->pos + 1;
   CHONK_MV_T(tr, 4);
@@ -428,6 +475,9 @@ CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM)
 CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM)
 CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM)
 CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM)
+CHONK_MVR(k_mvr_store_ln, EPI_STORE, PRO_LN)
+CHONK_MVR(k_mvr_store_embed_ln, EPI_STORE, PRO_EMBED_LN)
+CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN)
 #undef CHONK_MVR
 
 __global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
@@ -637,7 +687,8 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[36] = {
+  const void* fns[39] = {
+      (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
       (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
       (const void*)k_mv_logits_t<QT_Q8_0>,   (const void*)k_mv_logits_t<QT_Q5_0>,   (const void*)k_mv_logits_t<QT_Q5_1>,
       (const void*)k_mvr_store_plain,        (const void*)k_mvr_store_norm,         (const void*)k_mvr_store_embed,
@@ -674,6 +725,9 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
       case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;
       case EPI_GLU_GELU * 8 + PRO_NORM: k = k_mvr_geglu_norm; break;
       case EPI_GLU_GELU * 8 + PRO_RES_NORM: k = k_mvr_geglu_resnorm; break;
+      case EPI_STORE * 8 + PRO_LN: k = k_mvr_store_ln; break;
+      case EPI_STORE * 8 + PRO_EMBED_LN: k = k_mvr_store_embed_ln; break;
+      case EPI_GELU * 8 + PRO_LN: k = k_mvr_gelu_ln; break;
       default: return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k, dim3(grid), dim3(kWg), shmem, s, a);

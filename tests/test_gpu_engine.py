@@ -247,3 +247,40 @@ def test_batched_prefill_in_chunks_and_after_context(synth):
     b = ref.run_token(7, True)
     assert rel_err(eng.read_logits(), ref.logits()) <= 1e-3
     assert a == b
+
+
+def test_gpt2_step_logits_and_tokens(synth):
+    """The GPT-2 runtime (gpt-wgsl-runtime.ts:749-840) on the device: LayerNorm prologues,
+    fused q|k|v with bias, attention without rotary, bias + clamped residual epilogues,
+    GELU-tanh MLP, its argmax tree; token ids identical and logits within 1e-3."""
+    w, loaded, ref = _pair(synth, "tiny-gpt2")
+    eng = loaded.engine
+    assert eng.info["vocab"] == ref.vocab
+    prompt = _prompt(w)
+    tok = prompt[0]
+    for i in range(len(prompt) + 12):
+        need = i >= len(prompt) - 1
+        if i < len(prompt):
+            tok = prompt[i]
+        a = eng.run_token(tok, need)
+        b = ref.run_token(tok, need)
+        if need:
+            e = rel_err(eng.read_logits(), ref.logits())
+            assert e <= 1e-3, f"step {i}: logits rel err {e:.3e}"
+            assert a == b, f"step {i}: token {a} != {b}"
+            tok = a
+    assert eng.position == ref.position == len(prompt) + 12
+
+
+@pytest.mark.parametrize("temperature,top_k,rp", [(0.0, 0, 1.0), (0.8, 40, 1.0), (0.0, 0, 1.3)])
+def test_gpt2_generate_matches_oracle(synth, temperature, top_k, rp):
+    """generateGptWgsl (:182-249): ids, position (one step past the last id) and the cached
+    next id match the oracle, greedy, sampled and with a repetition penalty."""
+    w, loaded, ref = _pair(synth, "tiny-gpt2")
+    prompt = _prompt(w, seed=3)
+    out = generate_llama_wgsl(loaded, prompt, w.decode_tokens, temperature=temperature, top_k=top_k,
+                              repetition_penalty=rp, seed=5)
+    want = ref.generate(prompt, w.decode_tokens, temperature=temperature, top_k=top_k, repetition_penalty=rp, seed=5)
+    assert out["ids"] == want
+    assert loaded.engine.position == ref.position
+    assert loaded.cached_next_id == ref.cached_next_id
