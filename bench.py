@@ -159,7 +159,7 @@ def main() -> int:
               "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
         return 2
 
-    from chonklm_amd import WORKLOADS, generate_llama_wgsl, load_llama_wgsl_model
+    from chonklm_amd import WORKLOADS, generate_llama_wgsl, load_gpt_wgsl_model, load_llama_wgsl_model
 
     if args.calibrate_copy:
         import torch
@@ -181,7 +181,7 @@ def main() -> int:
     ctx = w.prompt_tokens + 1 + args.warmup + args.steps + 8
     md = w.model_def(path)
     md.max_context = ctx
-    loaded = load_llama_wgsl_model(md)
+    loaded = (load_gpt_wgsl_model if md.runtime == "gpt-webgpu" else load_llama_wgsl_model)(md)
     eng = loaded.engine
     info = eng.info
     prompt = np.random.default_rng(1234).integers(0, w.spec.vocab, w.prompt_tokens).tolist()
@@ -300,7 +300,7 @@ def main() -> int:
         "model_build_s": round(build_s, 1),
         "cpu_baseline": None,
     }
-    if not args.no_batched and info.get("kv_dtype", 0) == 0:
+    if not args.no_batched and info.get("kv_dtype", 0) == 0 and info.get("architecture") != 3:
         result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4)
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)

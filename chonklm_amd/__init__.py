@@ -1,4 +1,5 @@
-"""chonklm_amd — MI355X-native decode path of the llama-webgpu runtime.
+"""chonklm_amd — MI355X-native decode path of the llama-webgpu runtime (and the gpt-webgpu
+runtime on the same kernels).
 
 The compute lives in libchonk.so (HIP kernels for gfx950 + C++ engine behind
 the C ABI in include/chonk.h); this package is the host-side mirror of the
@@ -8,8 +9,13 @@ from .registry import ModelDef, Workload, WORKLOADS
 from .runtime import (
     ChonkError,
     LlamaWgslEngine,
+    LoadedGptWgslModel,
     LoadedLlamaWgslModel,
+    dispose_gpt_wgsl,
     dispose_llama_wgsl,
+    generate_gpt_wgsl,
+    load_gpt_wgsl_model,
+    reset_gpt_wgsl_conversation,
     generate_llama_wgsl,
     load_llama_wgsl_model,
     reset_llama_wgsl_conversation,
@@ -20,5 +26,6 @@ from .runtime import (
 __all__ = [
     "ModelDef", "Workload", "WORKLOADS", "ChonkError", "LlamaWgslEngine", "LoadedLlamaWgslModel",
     "dispose_llama_wgsl", "generate_llama_wgsl", "load_llama_wgsl_model", "reset_llama_wgsl_conversation",
-    "shard_gguf", "write_synthetic_gguf",
+    "shard_gguf", "write_synthetic_gguf", "LoadedGptWgslModel", "load_gpt_wgsl_model", "generate_gpt_wgsl",
+    "reset_gpt_wgsl_conversation", "dispose_gpt_wgsl",
 ]

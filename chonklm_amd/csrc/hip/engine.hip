@@ -2141,7 +2141,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->kv_heads = c.kv_heads;
   out->head_dim = c.hd;
   out->context = c.ctx;
-  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : 2;
+  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : 3;
   out->qk_norm = c.qk_norm;
   out->interleaved_rope = c.interleaved;
   out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;

@@ -524,7 +524,8 @@ napi_value Info(napi_env env, napi_callback_info info) {
            {"heads", (double)ei.heads},         {"kvHeads", (double)ei.kv_heads},
            {"headDim", (double)ei.head_dim},    {"context", (double)ei.context},
            {"weightBytesPerToken", (double)ei.weight_bytes_per_token},
-           {"deviceBytes", (double)ei.device_bytes}, {"kernelsPerStep", (double)ei.kernels_per_step}};
+           {"deviceBytes", (double)ei.device_bytes}, {"kernelsPerStep", (double)ei.kernels_per_step},
+           {"architecture", (double)ei.architecture}};
   for (const auto& x : f) {
     napi_create_double(env, x.v, &v);
     napi_set_named_property(env, obj, x.k, v);

@@ -4,7 +4,7 @@
 
 export interface ModelDef {
   id: string;
-  runtime: string; // must be "llama-webgpu"
+  runtime: string; // "llama-webgpu" (llama / qwen3 / gemma3 files) or "gpt-webgpu" (gpt2 files)
   eosIds: number[];
   vocab: number;
   layers: number;
@@ -78,6 +78,27 @@ export declare function generateLlamaWgsl(
 
 export declare function disposeLlamaWgsl(loaded: LoadedLlamaWgslModel): void;
 export declare function resetLlamaWgslConversation(loaded: LoadedLlamaWgslModel): void;
+
+/** LoadedGptWgslModel (src/lib/gpt-wgsl-runtime.ts:120-128). */
+export interface LoadedGptWgslModel extends Omit<LoadedLlamaWgslModel, "runtime"> {
+  runtime: "gpt-webgpu";
+}
+
+export declare function loadGptWgslModel(
+  model: ModelDef,
+  onProgress?: ProgressCallback,
+  onStep?: LoadStepCallback,
+  options?: { tokenizer?: Tokenizer; device?: number },
+): Promise<LoadedGptWgslModel>;
+
+export declare function generateGptWgsl(
+  loaded: LoadedGptWgslModel,
+  promptIds: number[],
+  opts?: GenerateOptions,
+): Promise<{ text: string; ids: number[]; tokensPerSec: number }>;
+
+export declare function disposeGptWgsl(loaded: LoadedGptWgslModel): void;
+export declare function resetGptWgslConversation(loaded: LoadedGptWgslModel): void;
 
 export {
   loadLlamaWgslModel as loadPleiasWgslModel,

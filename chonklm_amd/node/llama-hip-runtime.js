@@ -88,6 +88,45 @@ async function loadLlamaWgslModel(model, onProgress, onStep, options) {
     throw new Error(`loadLlamaWgslModel: ${model.id} is not configured for the Llama WGSL runtime`);
   }
   if (!model.gguf) throw new Error(`Llama WGSL ${model.id} is missing gguf path`);
+  const engine = await openEngine(model, onProgress, onStep, options);
+  if (engine.info.architecture === ARCH_GPT2) {
+    engine.dispose();
+    throw new Error('Llama GGUF WGSL does not support architecture gpt2');
+  }
+  if (onStep) onStep({ step: 'ready', detail: 'Llama HIP runtime ready' });
+  return loadedRecord('llama-webgpu', model, engine, options);
+}
+
+// loadGptWgslModel (src/lib/gpt-wgsl-runtime.ts:130-180). The engine runs the gpt2
+// architecture of the GGUF file (LayerNorm with bias, learned positions, biased linears,
+// GELU-tanh MLP, clamped residual, its argmax rule and generate loop).
+async function loadGptWgslModel(model, onProgress, onStep, options) {
+  if (model.runtime !== 'gpt-webgpu') throw new Error(`loadGptWgslModel: unsupported model ${model.id}`);
+  if (!model.gguf) throw new Error(`GPT WGSL model ${model.id} missing 'gguf' URL`);
+  const engine = await openEngine(model, onProgress, onStep, options);
+  if (engine.info.architecture !== ARCH_GPT2) {
+    engine.dispose();
+    throw new Error(`loadGptWgslModel: ${model.id} is not a gpt2 GGUF file`);
+  }
+  if (onStep) onStep({ step: 'ready', detail: 'GPT HIP runtime ready' });
+  return loadedRecord('gpt-webgpu', model, engine, options);
+}
+
+const ARCH_GPT2 = 3;  // chonk_engine_info.architecture
+
+function loadedRecord(runtime, model, engine, options) {
+  return {
+    runtime,
+    def: model,
+    tokenizer: (options && options.tokenizer) || idsOnlyTokenizer,
+    engine,
+    ep: 'hip',
+    cachedTokenIds: [],
+    cachedNextId: null,
+  };
+}
+
+async function openEngine(model, onProgress, onStep, options) {
   const file = modelFilePath(model, model.gguf);
   if (onStep) onStep({ step: 'runtime', detail: 'opening the HIP device' });
   if (onProgress) onProgress({ loaded: 0, total: 0, file });
@@ -104,17 +143,7 @@ async function loadLlamaWgslModel(model, onProgress, onStep, options) {
     },
     file,
   );
-  const engine = new LlamaWgslEngine(handle, model);
-  if (onStep) onStep({ step: 'ready', detail: 'Llama HIP runtime ready' });
-  return {
-    runtime: 'llama-webgpu',
-    def: model,
-    tokenizer: (options && options.tokenizer) || idsOnlyTokenizer,
-    engine,
-    ep: 'hip',
-    cachedTokenIds: [],
-    cachedNextId: null,
-  };
+  return new LlamaWgslEngine(handle, model);
 }
 
 // generateLlamaWgsl (:242-314). Without onToken / shouldStop the whole loop
@@ -162,6 +191,12 @@ module.exports = {
   generateLlamaWgsl,
   disposeLlamaWgsl,
   resetLlamaWgslConversation,
+  // GPT-2 runtime (src/lib/gpt-wgsl-runtime.ts:130-260); generation follows the GPT loop
+  // inside the engine when the file is gpt2
+  loadGptWgslModel,
+  generateGptWgsl: generateLlamaWgsl,
+  disposeGptWgsl: disposeLlamaWgsl,
+  resetGptWgslConversation: resetLlamaWgslConversation,
   // PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
   loadPleiasWgslModel: loadLlamaWgslModel,
   generatePleiasWgsl: generateLlamaWgsl,

@@ -63,8 +63,9 @@ class Workload:
     description: str = ""
 
     def model_def(self, path: str, kv_dtype: str = "f16", device: int = 0) -> ModelDef:
+        runtime = "gpt-webgpu" if self.spec.arch == "gpt2" else "llama-webgpu"
         return ModelDef(id=self.name, vocab=self.spec.vocab, layers=self.spec.layers, max_context=self.max_context,
-                        eos_ids=list(self.eos_ids), path=path, kv_dtype=kv_dtype, device=device)
+                        eos_ids=list(self.eos_ids), path=path, kv_dtype=kv_dtype, device=device, runtime=runtime)
 
 
 SMOLLM2 = dict(arch="llama", hidden=576, layers=30, heads=9, kv_heads=3, ffn=1536, vocab=49152,

@@ -180,6 +180,9 @@ def load_llama_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = Non
     if on_step:
         on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
     engine = LlamaWgslEngine(model)
+    if engine.info["architecture"] == 3:
+        engine.dispose()
+        raise ValueError("Llama GGUF WGSL does not support architecture gpt2")
     if on_step:
         on_step({"step": "ready", "detail": "Llama HIP runtime ready"})
     return LoadedLlamaWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
@@ -298,6 +301,52 @@ def reset_llama_wgsl_conversation(loaded: LoadedLlamaWgslModel) -> None:
     check(lib().chonk_engine_reset_conversation(loaded.engine._h), loaded.engine._h)
     loaded.cached_token_ids = []
     loaded.cached_next_id = None
+
+
+# ---- GPT-2 runtime (src/lib/gpt-wgsl-runtime.ts) ------------------------------------
+# The same engine runs the gpt2 architecture (LayerNorm with bias, learned positions,
+# biased linears, GELU-tanh MLP, clamped residual, its argmax rule and generate loop); the
+# architecture comes from the GGUF file, the runtime tag from the model definition.
+
+@dataclass
+class LoadedGptWgslModel(LoadedLlamaWgslModel):
+    """LoadedGptWgslModel (gpt-wgsl-runtime.ts:120-128)."""
+
+    runtime: str = "gpt-webgpu"
+
+
+def load_gpt_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = None,
+                        on_step: Optional[Callable] = None, tokenizer: object = None) -> LoadedGptWgslModel:
+    """loadGptWgslModel (:130-180): rejects a definition not tagged for the GPT runtime and a
+    GGUF file whose architecture is not gpt2."""
+    if model.runtime != "gpt-webgpu":
+        raise ValueError(f"loadGptWgslModel: unsupported model {model.id}")
+    if on_step:
+        on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
+    engine = LlamaWgslEngine(model)
+    if engine.info["architecture"] != 3:
+        engine.dispose()
+        raise ValueError(f"loadGptWgslModel: {model.id} is not a gpt2 GGUF file")
+    if on_step:
+        on_step({"step": "ready", "detail": "GPT HIP runtime ready"})
+    return LoadedGptWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
+
+
+def generate_gpt_wgsl(loaded: LoadedGptWgslModel, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None,
+                      **kw) -> dict:
+    """generateGptWgsl (:182-249): the engine follows the GPT loop (an empty suffix needs a
+    cached next id; one more step runs after the last generated token)."""
+    return generate_llama_wgsl(loaded, prompt_ids, max_new_tokens, **kw)
+
+
+def reset_gpt_wgsl_conversation(loaded: LoadedGptWgslModel) -> None:
+    """resetGptWgslConversation (:251-255)."""
+    reset_llama_wgsl_conversation(loaded)
+
+
+def dispose_gpt_wgsl(loaded: LoadedGptWgslModel) -> None:
+    """disposeGptWgsl (:257-260)."""
+    dispose_llama_wgsl(loaded)
 
 
 # PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)

@@ -82,7 +82,7 @@ typedef struct {
 
 typedef struct {
   int32_t hidden, ffn, vocab, layers, heads, kv_heads, head_dim, context;
-  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3 */
+  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3, 3 gpt2 */
   int32_t qk_norm, interleaved_rope, kv_dtype;
   uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
   uint64_t device_bytes;            /* device memory held by the engine */
@@ -229,7 +229,7 @@ int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n
 
 /* Model files --------------------------------------------------------------- */
 typedef struct {
-  const char* arch;      /* "llama" | "qwen3" | "gemma3" */
+  const char* arch;      /* "llama" | "qwen3" | "gemma3" | "gpt2" */
   const char* recipe;    /* "q4_k_m" | "q8_0" | "q4_k" | "q6_k" | "q5_0" */
   int32_t hidden, layers, heads, kv_heads, head_dim, ffn, vocab, context_length;
   float rope_theta, norm_eps;

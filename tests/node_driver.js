@@ -18,7 +18,8 @@ async function main() {
     }
   } else if (job.kind === 'generate') {
     const steps = [];
-    const loaded = await rt.loadLlamaWgslModel(job.model, null, (s) => steps.push(s.step));
+    const load = job.model.runtime === 'gpt-webgpu' ? rt.loadGptWgslModel : rt.loadLlamaWgslModel;
+    const loaded = await load(job.model, null, (s) => steps.push(s.step));
     out.steps = steps;
     out.runs = [];
     for (const g of job.generate) {

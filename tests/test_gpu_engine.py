@@ -13,7 +13,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from chonklm_amd import WORKLOADS, ChonkError, generate_llama_wgsl, load_llama_wgsl_model
+from chonklm_amd import (WORKLOADS, ChonkError, generate_gpt_wgsl, generate_llama_wgsl, load_gpt_wgsl_model,
+                         load_llama_wgsl_model)
 from chonklm_amd.runtime import LlamaWgslEngine, reset_llama_wgsl_conversation
 from oracle.oracle import OracleModel
 from tests.conftest import rel_err
@@ -29,7 +30,7 @@ def _pair(synth, name, kv="f16", **over):
     md = w.model_def(path, kv_dtype=kv)
     for k, v in over.items():
         setattr(md, k, v)
-    loaded = load_llama_wgsl_model(md)
+    loaded = (load_gpt_wgsl_model if md.runtime == "gpt-webgpu" else load_llama_wgsl_model)(md)
     ref = OracleModel(path, w.spec.vocab, w.spec.layers, md.max_context, kv_f16=(kv == "f16"), eos_ids=w.eos_ids)
     return w, loaded, ref
 
@@ -278,9 +279,26 @@ def test_gpt2_generate_matches_oracle(synth, temperature, top_k, rp):
     next id match the oracle, greedy, sampled and with a repetition penalty."""
     w, loaded, ref = _pair(synth, "tiny-gpt2")
     prompt = _prompt(w, seed=3)
-    out = generate_llama_wgsl(loaded, prompt, w.decode_tokens, temperature=temperature, top_k=top_k,
-                              repetition_penalty=rp, seed=5)
+    out = generate_gpt_wgsl(loaded, prompt, w.decode_tokens, temperature=temperature, top_k=top_k,
+                            repetition_penalty=rp, seed=5)
     want = ref.generate(prompt, w.decode_tokens, temperature=temperature, top_k=top_k, repetition_penalty=rp, seed=5)
     assert out["ids"] == want
     assert loaded.engine.position == ref.position
     assert loaded.cached_next_id == ref.cached_next_id
+
+
+def test_gpt2_loader_tags(synth):
+    """loadGptWgslModel refuses a definition not tagged gpt-webgpu; the Llama loader refuses a
+    gpt2 file (gpt-wgsl-runtime.ts:135-137, llama-wgsl-runtime.ts architecture check)."""
+    w = WORKLOADS["tiny-gpt2"]
+    md = w.model_def(synth("tiny-gpt2"))
+    loaded = load_gpt_wgsl_model(md)
+    assert loaded.runtime == "gpt-webgpu" and loaded.engine.info["architecture"] == 3
+    dispose_gpt = __import__("chonklm_amd").dispose_gpt_wgsl
+    dispose_gpt(loaded)
+    md.runtime = "llama-webgpu"
+    with pytest.raises(ValueError, match="does not support architecture gpt2"):
+        load_llama_wgsl_model(md)
+    q = WORKLOADS["tiny-qwen3"].model_def(synth("tiny-qwen3"))
+    with pytest.raises(ValueError, match="loadGptWgslModel: unsupported model"):
+        load_gpt_wgsl_model(q)

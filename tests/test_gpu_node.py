@@ -60,3 +60,23 @@ def test_node_generate_matches_oracle(synth):
     assert np.allclose(st["logitsHead"], ref2.logits()[:8], rtol=1e-3, atol=1e-4)
     assert out["busy"] in ("EBUSY", None)  # two queued calls may also run back to back
     assert "disposed" in out["afterDispose"]
+
+
+def test_node_gpt2_generate_matches_oracle(synth):
+    """loadGptWgslModel / generateGptWgsl (gpt-wgsl-runtime.ts:130-249) through the addon on a
+    gpt2 file: ids, cachedNextId (the step after the last id also runs) as the oracle."""
+    w = WORKLOADS["tiny-gpt2"]
+    path = synth("tiny-gpt2")
+    rng = np.random.default_rng(37)
+    p1 = rng.integers(0, w.spec.vocab, 12).tolist()
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, w.max_context, kv_f16=True, eos_ids=w.eos_ids)
+    want1 = ref.generate(p1, 9)
+    cache1 = (list(ref.cached_token_ids), ref.cached_next_id)
+    md = model(path, runtime="gpt-webgpu", vocab=w.spec.vocab, layers=w.spec.layers, maxContext=w.max_context,
+               eosIds=w.eos_ids, kvDtype="float16")
+    out = run_driver({"kind": "generate", "model": md, "prompt": p1[:4], "generate": [
+        {"prompt": p1, "opts": {"maxNewTokens": 9}},
+    ]}, timeout=300)
+    r = out["runs"]
+    assert r[0]["ids"] == want1 and (r[0]["cached"], r[0]["next"]) == cache1
+    assert r[0]["position"] == ref.position
