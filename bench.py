@@ -76,6 +76,8 @@ def kernel_symbol(cls: str, info: dict) -> str:
     attn = f"k_attn_dec<{g}, {hd}>" if dec else f"k_attention<{g}, {kv16}>"
     if os.environ.get("CHONK_MV") == "generic":
         mv = {"gateup": "k_mv_swiglu", "qkv": "k_mv_store", "oproj": "k_mv_add", "down": "k_mv_add"}
+    elif info.get("architecture") == 3:  # gpt2 row kernels (LayerNorm prologues, biases)
+        mv = {"gateup": "k_mvr_gelu_ln", "qkv": "k_mvr_store_ln", "oproj": "k_mvr_add_bias", "down": "k_mvr_add_bias"}
     else:  # one-row-per-lane-group kernels (layers after the first; llama/qwen3 prologues)
         mv = {"gateup": "k_mvr_swiglu_norm", "qkv": "k_mvr_store_norm", "oproj": "k_mvr_add_plain",
               "down": "k_mvr_add_plain"}

@@ -337,7 +337,9 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
 // product), the prologue mode is fixed at compile time and the owning lane
 // stores the row's result directly: a short straight path for the decode
 // step, whose matvecs are bound by instruction latency rather than bytes.
-template <int EPI, int PRO>
+// GB: the GPT-2 epilogue terms (a per-row bias and the residual sanitize) are compiled in;
+// the llama-family kernels carry neither
+template <int EPI, int PRO, bool GB>
 __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   extern __shared__ __align__(16) float smem[];
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
@@ -376,7 +378,9 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   }
   float addv = 0.f, biasv = 0.f;
   if constexpr (EPI == EPI_ADD) addv = g.add[row];
-  if (g.bias) biasv = g.bias[row];
+  if constexpr (GB) {
+    if (g.bias) biasv = g.bias[row];
+  }
   float rg = 0.f, ru = 0.f;
   bool live = false;
   with_type(g.w.type, [&]<int T>() {
@@ -448,11 +452,13 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   });
   if (!live) return;
   if (owner) {
-    if (g.bias) rg = __fadd_rn(rg, biasv);
+    if constexpr (GB) {
+      if (g.bias) rg = __fadd_rn(rg, biasv);
+    }
     if constexpr (EPI == EPI_STORE) g.out[row] = rg;
     if constexpr (EPI == EPI_ADD) {
       float y = __fadd_rn(addv, rg);
-      if (a.sanitize) y = y != y ? 0.0f : fminf(fmaxf(y, -10000.0f), 10000.0f);  // SANITIZE (gpt-wgsl-runtime.ts:1726-1746)
+      if (GB && a.sanitize) y = y != y ? 0.0f : fminf(fmaxf(y, -10000.0f), 10000.0f);  // SANITIZE (gpt-wgsl-runtime.ts:1726-1746)
       g.out[row] = y;
     }
     if constexpr (EPI == EPI_GLU_SILU) g.out[row] = silu_mul(rg, ru);
@@ -464,20 +470,22 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   CHONK_MV_TRACE_END(tr, EPI * 65536 + a.k);
 }
 
-#define CHONK_MVR(NAME, EPI, PRO) \
-  __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO>(a); }
-CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN)
-CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM)
-CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM)
-CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM)
-CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN)
-CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM)
-CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM)
-CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM)
-CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM)
-CHONK_MVR(k_mvr_store_ln, EPI_STORE, PRO_LN)
-CHONK_MVR(k_mvr_store_embed_ln, EPI_STORE, PRO_EMBED_LN)
-CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN)
+#define CHONK_MVR(NAME, EPI, PRO, GB) \
+  __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO, GB>(a); }
+CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN, false)
+CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM, false)
+CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, false)
+CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM, false)
+CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN, false)
+CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM, false)
+CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM, false)
+CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM, false)
+CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM, false)
+// gpt2: LayerNorm prologues, biases, GELU-tanh, the sanitized residual add
+CHONK_MVR(k_mvr_store_ln, EPI_STORE, PRO_LN, true)
+CHONK_MVR(k_mvr_store_embed_ln, EPI_STORE, PRO_EMBED_LN, true)
+CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN, true)
+CHONK_MVR(k_mvr_add_bias, EPI_ADD, PRO_PLAIN, true)
 #undef CHONK_MVR
 
 __global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
@@ -687,7 +695,8 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[39] = {
+  const void* fns[40] = {
+      (const void*)k_mvr_add_bias,
       (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
       (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
       (const void*)k_mv_logits_t<QT_Q8_0>,   (const void*)k_mv_logits_t<QT_Q5_0>,   (const void*)k_mv_logits_t<QT_Q5_1>,
@@ -715,12 +724,17 @@ hipError_t init_kernel_attributes() {
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s) {
   if (a.row_kernel) {
     void (*k)(const MvArgs) = nullptr;
+    bool gb = a.sanitize != 0;
+    for (int i = 0; i < a.nseg; ++i) gb = gb || a.seg[i].bias != nullptr;
+    const bool ln = a.pro == PRO_LN || a.pro == PRO_EMBED_LN;
+    // bias / sanitize need a GB kernel: the GPT-2 set below
+    if (gb && !ln && !(a.epi == EPI_ADD && a.pro == PRO_PLAIN)) return hipErrorInvalidValue;
     switch (a.epi * 8 + a.pro) {
       case EPI_STORE * 8 + PRO_PLAIN: k = k_mvr_store_plain; break;
       case EPI_STORE * 8 + PRO_NORM: k = k_mvr_store_norm; break;
       case EPI_STORE * 8 + PRO_EMBED_NORM: k = k_mvr_store_embed; break;
       case EPI_STORE * 8 + PRO_RES_NORM: k = k_mvr_store_resnorm; break;
-      case EPI_ADD * 8 + PRO_PLAIN: k = k_mvr_add_plain; break;
+      case EPI_ADD * 8 + PRO_PLAIN: k = gb ? k_mvr_add_bias : k_mvr_add_plain; break;
       case EPI_GLU_SILU * 8 + PRO_NORM: k = k_mvr_swiglu_norm; break;
       case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;
       case EPI_GLU_GELU * 8 + PRO_NORM: k = k_mvr_geglu_norm; break;
