@@ -302,3 +302,25 @@ def test_gpt2_loader_tags(synth):
     q = WORKLOADS["tiny-qwen3"].model_def(synth("tiny-qwen3"))
     with pytest.raises(ValueError, match="loadGptWgslModel: unsupported model"):
         load_gpt_wgsl_model(q)
+
+
+def test_gpt2_errors_and_empty_prompt(synth):
+    """GPT errors keep the reference's wording (gpt-wgsl-runtime.ts:218, :752); an empty
+    suffix after a finished run continues from the cached next id, as the oracle does."""
+    w, loaded, ref = _pair(synth, "tiny-gpt2")
+    with pytest.raises(ChonkError, match="GPT WGSL has no cached next token for an empty prompt"):
+        generate_gpt_wgsl(loaded, [], 4)
+    prompt = _prompt(w, seed=11, n=10)
+    a = generate_gpt_wgsl(loaded, prompt, 5)["ids"]
+    b = ref.generate(prompt, 5)
+    assert a == b
+    # the same prompt + ids again: empty suffix, continue from cachedNextId
+    a2 = generate_gpt_wgsl(loaded, prompt + a, 4)["ids"]
+    b2 = ref.generate(prompt + b, 4)
+    assert a2 == b2 and loaded.cached_next_id == ref.cached_next_id
+    eng = loaded.engine
+    eng.reset()
+    for t in range(w.max_context):
+        eng.run_token(t % w.spec.vocab, False)
+    with pytest.raises(ChonkError, match=f"GPT WGSL context exhausted at {w.max_context} tokens"):
+        eng.run_token(1, True)
