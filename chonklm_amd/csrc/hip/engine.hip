@@ -583,7 +583,12 @@ void use_row_kernel(MvArgs& a) {
   for (int i = 0; i < a.nseg; ++i) needs_row = needs_row || a.seg[i].bias;
   if ((off && !needs_row) || a.epi == EPI_LOGITS) return;
   // the register-resident plain / norm prologues hold at most 4 float4 per thread
-  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) return;
+  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) {
+    if (needs_row)
+      throw Error(CHONK_EINVAL, "GPT-2 layers need a feed-forward width of at most " + std::to_string(4 * 4 * kWg) +
+                                    ", got " + std::to_string(a.k));
+    return;
+  }
   for (int i = 0; i < a.nseg; ++i)
     if (a.seg[i].w.k / 32 > kRowUnits * 64) {
       if (needs_row) throw Error(CHONK_EINVAL, "GPT-2 layers need rows of at most 8192 weights");

@@ -324,3 +324,19 @@ def test_gpt2_errors_and_empty_prompt(synth):
         eng.run_token(t % w.spec.vocab, False)
     with pytest.raises(ChonkError, match=f"GPT WGSL context exhausted at {w.max_context} tokens"):
         eng.run_token(1, True)
+
+
+def test_gpt2_wide_ffn_refused(tmp_path):
+    """A gpt2 file whose feed-forward width exceeds the row kernels' 4096 is refused at
+    load with an explicit error (no silent fallback to kernels without bias terms)."""
+    import dataclasses
+
+    from chonklm_amd import write_synthetic_gguf
+
+    base = WORKLOADS["tiny-gpt2"]
+    w = dataclasses.replace(base, name="tiny-gpt2-wide", spec=dataclasses.replace(base.spec, ffn=5120, layers=1))
+    path = str(tmp_path / "wide.gguf")
+    write_synthetic_gguf(w, path)
+    md = w.model_def(path)
+    with pytest.raises(ChonkError, match="feed-forward width of at most 4096, got 5120"):
+        load_gpt_wgsl_model(md)
