@@ -583,10 +583,9 @@ void use_row_kernel(MvArgs& a) {
   for (int i = 0; i < a.nseg; ++i) needs_row = needs_row || a.seg[i].bias;
   if ((off && !needs_row) || a.epi == EPI_LOGITS) return;
   // the register-resident plain / norm prologues hold at most 4 float4 per thread
-  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg) {
-    if (needs_row)
-      throw Error(CHONK_EINVAL, "GPT-2 layers need a feed-forward width of at most " + std::to_string(4 * 4 * kWg) +
-                                    ", got " + std::to_string(a.k));
+  // (GPT-2's wider ffn_down rows take the LDS-staged variant of its row kernel)
+  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg && !(needs_row && a.pro == PRO_PLAIN)) {
+    if (needs_row) throw Error(CHONK_EINVAL, "GPT-2 rows wider than 4096 need the plain prologue");
     return;
   }
   for (int i = 0; i < a.nseg; ++i)

@@ -337,9 +337,10 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
 // product), the prologue mode is fixed at compile time and the owning lane
 // stores the row's result directly: a short straight path for the decode
 // step, whose matvecs are bound by instruction latency rather than bytes.
-// GB: the GPT-2 epilogue terms (a per-row bias and the residual sanitize) are compiled in;
-// the llama-family kernels carry neither
-template <int EPI, int PRO, bool GB>
+// GB: 0 llama family; 1 GPT-2 epilogue terms (a per-row bias and the residual sanitize)
+// compiled in; 2 as 1 with the input staged through LDS (rows wider than the 4096 that the
+// register-resident prologue holds)
+template <int EPI, int PRO, int GB>
 __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   extern __shared__ __align__(16) float smem[];
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
@@ -359,7 +360,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   p.pro = PRO;
   // plain and norm prologues keep x (and the norm weight) in registers: thread
   // t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
-  constexpr bool reg_pro = PRO == PRO_PLAIN || PRO == PRO_NORM;
+  constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM) && GB != 2;
   const int n4 = a.k >> 2;
   float4 xv[4], wv[4];
 #pragma unroll
@@ -472,20 +473,21 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
 
 #define CHONK_MVR(NAME, EPI, PRO, GB) \
   __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO, GB>(a); }
-CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN, false)
-CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM, false)
-CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, false)
-CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM, false)
-CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN, false)
-CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM, false)
-CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM, false)
-CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM, false)
-CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM, false)
+CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN, 0)
+CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM, 0)
+CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, 0)
+CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM, 0)
+CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN, 0)
+CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM, 0)
+CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM, 0)
+CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM, 0)
+CHONK_MVR(k_mvr_geglu_resnorm, EPI_GLU_GELU, PRO_RES_NORM, 0)
 // gpt2: LayerNorm prologues, biases, GELU-tanh, the sanitized residual add
-CHONK_MVR(k_mvr_store_ln, EPI_STORE, PRO_LN, true)
-CHONK_MVR(k_mvr_store_embed_ln, EPI_STORE, PRO_EMBED_LN, true)
-CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN, true)
-CHONK_MVR(k_mvr_add_bias, EPI_ADD, PRO_PLAIN, true)
+CHONK_MVR(k_mvr_store_ln, EPI_STORE, PRO_LN, 1)
+CHONK_MVR(k_mvr_store_embed_ln, EPI_STORE, PRO_EMBED_LN, 1)
+CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN, 1)
+CHONK_MVR(k_mvr_add_bias, EPI_ADD, PRO_PLAIN, 1)
+CHONK_MVR(k_mvr_add_bias_wide, EPI_ADD, PRO_PLAIN, 2)
 #undef CHONK_MVR
 
 __global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
@@ -695,8 +697,8 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[40] = {
-      (const void*)k_mvr_add_bias,
+  const void* fns[41] = {
+      (const void*)k_mvr_add_bias,           (const void*)k_mvr_add_bias_wide,
       (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
       (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
       (const void*)k_mv_logits_t<QT_Q8_0>,   (const void*)k_mv_logits_t<QT_Q5_0>,   (const void*)k_mv_logits_t<QT_Q5_1>,
@@ -734,7 +736,9 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
       case EPI_STORE * 8 + PRO_NORM: k = k_mvr_store_norm; break;
       case EPI_STORE * 8 + PRO_EMBED_NORM: k = k_mvr_store_embed; break;
       case EPI_STORE * 8 + PRO_RES_NORM: k = k_mvr_store_resnorm; break;
-      case EPI_ADD * 8 + PRO_PLAIN: k = gb ? k_mvr_add_bias : k_mvr_add_plain; break;
+      case EPI_ADD * 8 + PRO_PLAIN:
+        k = !gb ? k_mvr_add_plain : a.k > 4 * 4 * kWg ? k_mvr_add_bias_wide : k_mvr_add_bias;
+        break;
       case EPI_GLU_SILU * 8 + PRO_NORM: k = k_mvr_swiglu_norm; break;
       case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;
       case EPI_GLU_GELU * 8 + PRO_NORM: k = k_mvr_geglu_norm; break;
