@@ -186,7 +186,7 @@ def main() -> int:
     loaded = (load_gpt_wgsl_model if md.runtime == "gpt-webgpu" else load_llama_wgsl_model)(md)
     eng = loaded.engine
     info = eng.info
-    prompt = np.random.default_rng(1234).integers(0, w.spec.vocab, w.prompt_tokens).tolist()
+    prompt = w.prompt(1234)
 
     if args.batched_only:
         bd = batched_decode(eng, w.spec.vocab, 64, 512, args.batched_steps, 4)

@@ -132,6 +132,7 @@ SIGNATURES = [
     ("chonk_engine_prefill", C.c_int, [P, I32P, C.c_size_t]),
     ("chonk_engine_conversation", C.c_int, [P, I32P, C.c_size_t, C.POINTER(C.c_size_t), I32P]),
     ("chonk_engine_reset", C.c_int, [P]),
+    ("chonk_engine_debug_fail_next_launch", C.c_int, [P]),
     ("chonk_engine_reset_conversation", C.c_int, [P]),
     ("chonk_engine_position", C.c_int, [P, I32P]),
     ("chonk_engine_read_logits", C.c_int, [P, F32P, C.c_size_t]),

@@ -366,6 +366,7 @@ struct chonk_engine {
   // status
   std::atomic<bool> busy{false};
   bool lost = false;
+  bool fail_next_launch = false;  // test hook: the next launch reports a HIP error
   std::string err;
 };
 
@@ -1462,7 +1463,17 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
 // One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
 // cannot trace graph launches) the same launches issued one by one.
+// The test hook's stand-in for a failed launch: the same error path as a HIP
+// error returned by the runtime (the caller marks the engine lost).
+void check_injected_failure(chonk_engine* e, const char* where) {
+  if (!e->fail_next_launch) return;
+  e->fail_next_launch = false;
+  throw Error(CHONK_EHIP, std::string("HIP error hipErrorLaunchFailure (injected by "
+                                      "chonk_engine_debug_fail_next_launch) at ") + where);
+}
+
 void replay(chonk_engine* e, bool logits) {
+  check_injected_failure(e, "hipGraphLaunch");
   if (e->use_graph) {
     HIP_OK(hipGraphLaunch(logits ? e->exec_logits : e->exec_plain, e->stream));
   } else {
@@ -1497,7 +1508,9 @@ DevSampling make_sampling(chonk_engine* e, const chonk_sampling* s, bool stage1,
   d.top_k = top_k;
   d.seed = s ? s->seed : 0;
   d.sample_mode = (temperature > 0 || top_p < 1 || top_k > 0) ? 1 : 0;  // needsSamplingReadback
-  d.stage1_penalty = stage1 && rp > 1 ? 1 : 0;
+  // the caller decides: llama applies the list when rp > 1 (:1649-1661), the
+  // GPT-2 runtime whenever rp != 1 (gpt-wgsl-runtime.ts:789-798)
+  d.stage1_penalty = stage1 ? 1 : 0;
   d.stage1_pen = (float)js_round(rp * 1000) / 1000.0f;
   d.repetition_penalty = std::max(rp, 1e-6);
   d.seen_penalty = seen && d.repetition_penalty != 1 ? 1 : 0;
@@ -1829,6 +1842,7 @@ RowBufs engine_row_bufs(const chonk_engine* e) {
 // cache). The host position and the device state are left to the caller; no
 // logits are produced (the reference's runToken(id, false) for each token).
 void prefill_rows(chonk_engine* e, const int32_t* tokens, int n) {
+  check_injected_failure(e, "the prompt pass");
   const ModelCfg& c = e->cfg;
   if (n <= 0) return;
   if ((int64_t)e->pos + n > c.ctx)
@@ -1897,13 +1911,16 @@ double now_ms() {
 
 // generateLlamaWgsl's option defaults (:255-262): temperature 0, topP 1,
 // topK 0, repetitionPenalty = opts ?? def.defaultRepetitionPenalty ?? 1
-// (a non-positive or non-finite value means "not given").
+// (a non-positive or non-finite value means "not given"). generateGptWgsl
+// takes opts.repetitionPenalty ?? 1 and ignores the definition's default
+// (gpt-wgsl-runtime.ts:198-203).
 chonk_sampling effective_sampling(const chonk_engine* e, const chonk_sampling* s_in) {
   chonk_sampling s{};
   s.temperature = 0;
   s.top_p = 1;
   s.top_k = 0;
-  s.repetition_penalty = e->def.default_repetition_penalty > 0 ? e->def.default_repetition_penalty : 1.0;
+  s.repetition_penalty =
+      (!e->cfg.gpt && e->def.default_repetition_penalty > 0) ? e->def.default_repetition_penalty : 1.0;
   if (s_in) {
     s.temperature = s_in->temperature;
     s.top_p = s_in->top_p;
@@ -2231,6 +2248,10 @@ int chonk_engine_conversation(chonk_engine* e, int32_t* ids, size_t cap, size_t*
 }
 
 int chonk_engine_reset(chonk_engine* e) { return api(e, [&] { engine_reset(e); }); }
+
+int chonk_engine_debug_fail_next_launch(chonk_engine* e) {
+  return api(e, [&] { e->fail_next_launch = true; });
+}
 
 int chonk_engine_reset_conversation(chonk_engine* e) {
   return api(e, [&] {

@@ -99,10 +99,11 @@ class ShardSource : public ByteSource {
       const std::string path = dir_ + "/" + s.name;
       struct stat st;
       if (::stat(path.c_str(), &st) != 0) throw std::runtime_error("missing shard " + path);
-      // cache.ts:568-573 rejects a shard whose byte size differs from the manifest.
+      // cache.ts:568-573 rejects a shard whose byte size differs from the manifest,
+      // with this wording
       if ((uint64_t)st.st_size != s.size) {
-        throw std::runtime_error("shard size mismatch for " + path + ": expected " + std::to_string(s.size) +
-                                 " got " + std::to_string((uint64_t)st.st_size));
+        throw std::runtime_error("shard " + path + ": expected " + std::to_string(s.size) + " bytes, got " +
+                                 std::to_string((uint64_t)st.st_size));
       }
     }
     if (expect != m_.total_size) throw std::runtime_error("shard manifest totalSize mismatch for " + dir_);

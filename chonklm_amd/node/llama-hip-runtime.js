@@ -150,8 +150,16 @@ async function openEngine(model, onProgress, onStep, options) {
 // runs on the device; with them it is stepped one token at a time and the
 // callbacks run on this thread between steps, as in the reference.
 async function generateLlamaWgsl(loaded, promptIds, opts) {
-  const o = opts || {};
-  const s = samplingOf(o, loaded.def);
+  return generateWith(loaded, promptIds, opts || {}, samplingOf(opts, loaded.def));
+}
+
+// generateGptWgsl (gpt-wgsl-runtime.ts:182-249): repetitionPenalty is
+// opts.repetitionPenalty ?? 1; the definition's default is not consulted (:198-203).
+async function generateGptWgsl(loaded, promptIds, opts) {
+  return generateWith(loaded, promptIds, opts || {}, samplingOf(opts, null));
+}
+
+async function generateWith(loaded, promptIds, o, s) {
   const maxArg = o.maxNewTokens === undefined || o.maxNewTokens === null ? -1 : Math.max(0, Math.floor(o.maxNewTokens));
   const generated = [];
   let cumulative = '';
@@ -194,7 +202,7 @@ module.exports = {
   // GPT-2 runtime (src/lib/gpt-wgsl-runtime.ts:130-260); generation follows the GPT loop
   // inside the engine when the file is gpt2
   loadGptWgslModel,
-  generateGptWgsl: generateLlamaWgsl,
+  generateGptWgsl,
   disposeGptWgsl: disposeLlamaWgsl,
   resetGptWgslConversation: resetLlamaWgslConversation,
   // PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)

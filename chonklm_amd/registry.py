@@ -62,6 +62,12 @@ class Workload:
     top_p: float = 1.0
     description: str = ""
 
+    def prompt(self, seed: int = 1234, n: Optional[int] = None) -> list[int]:
+        """Seeded uniform token ids: the workload's prompt (n defaults to prompt_tokens)."""
+        import numpy as np
+
+        return np.random.default_rng(seed).integers(0, self.spec.vocab, self.prompt_tokens if n is None else n).tolist()
+
     def model_def(self, path: str, kv_dtype: str = "f16", device: int = 0) -> ModelDef:
         runtime = "gpt-webgpu" if self.spec.arch == "gpt2" else "llama-webgpu"
         return ModelDef(id=self.name, vocab=self.spec.vocab, layers=self.spec.layers, max_context=self.max_context,

@@ -27,7 +27,8 @@
  * An engine is not re-entrant: a call made while another call on the same
  * engine is in progress returns CHONK_EBUSY (the reference's `active` guard,
  * :1221-1224). Engines on different threads are independent.
- * A HIP error marks the engine lost; later calls fail fast with CHONK_ELOST
+ * A HIP error marks the engine lost; later calls that touch the device
+ * (position, info and destroy still answer) fail fast with CHONK_ELOST
  * (the LFM runtime's deviceLost behaviour, lfm-wgsl-runtime.ts:704-707,
  * :729-731).
  */
@@ -157,6 +158,13 @@ int chonk_engine_conversation(chonk_engine* e, int32_t* ids, size_t cap, size_t*
 int chonk_engine_reset(chonk_engine* e);
 int chonk_engine_reset_conversation(chonk_engine* e);
 int chonk_engine_position(const chonk_engine* e, int32_t* out_pos);
+
+/* Test hook (no counterpart in the reference, which cannot force a device
+ * error): the engine's next kernel launch reports a HIP error. That call
+ * returns CHONK_EHIP, the engine is marked lost, and every later call on it
+ * that touches the device returns CHONK_ELOST (the LFM runtime's deviceLost rule,
+ * lfm-wgsl-runtime.ts:704-707, :729-731); destroy still frees it. */
+int chonk_engine_debug_fail_next_launch(chonk_engine* e);
 
 /* Logits of the last step that computed them (vocab floats). */
 int chonk_engine_read_logits(chonk_engine* e, float* out, size_t n);

@@ -238,16 +238,113 @@ class Pool {
   bool stop_ = false;
 };
 
-// One output row of the GGUF matvec (llama-wgsl-runtime.ts:2412-2442).
-float matvec_row(uint32_t type, const uint8_t* w, uint64_t row, uint64_t K, const float* x) {
-  float partial[128];
-  for (uint32_t t = 0; t < 128; ++t) {
-    float sum = 0.0f;
-    for (uint64_t k = t; k < K; k += 128) {
-      const float prod = x[k] * weight_at(type, w, row, k, K);
-      sum = sum + prod;
+// Every weight of one row, block by block, with the float operations of
+// weight_at in the same order (the block's scales decoded once): out[k] ==
+// weight_at(type, d, row, k, K) bit for bit for every k.
+void decode_row(uint32_t type, const uint8_t* d, uint64_t row, uint64_t K, float* out) {
+  switch (type) {
+    case 0:
+    case 1:
+      for (uint64_t k = 0; k < K; ++k) out[k] = weight_at(type, d, row, k, K);
+      return;
+    case 6:
+    case 7: {
+      const uint64_t bb = type == 6 ? 22 : 24, qo = type == 6 ? 6 : 8, ho = type == 6 ? 2 : 4;
+      for (uint64_t b = 0; b < K / 32; ++b) {
+        const uint64_t base = (row * (K / 32) + b) * bb;
+        const float dd = f16_at(d, base);
+        const float mm = type == 7 ? f16_at(d, base + 2) : 0.0f;
+        const uint32_t qh = u32_at(d, base + ho);
+        for (uint32_t j = 0; j < 32; ++j) {
+          const uint32_t qb = byte_at(d, base + qo + (j & 15));
+          const uint32_t qv = (j >= 16 ? qb >> 4 : qb & 15u) | (((qh >> j) & 1u) << 4);
+          if (type == 6) {
+            out[b * 32 + j] = dd * (float)((int32_t)qv - 16);
+          } else {
+            const float prod = dd * (float)qv;
+            out[b * 32 + j] = prod + mm;
+          }
+        }
+      }
+      return;
     }
-    partial[t] = sum;
+    case 8:
+      for (uint64_t b = 0; b < K / 32; ++b) {
+        const uint64_t base = (row * (K / 32) + b) * 34;
+        const float dd = f16_at(d, base);
+        for (uint32_t j = 0; j < 32; ++j) out[b * 32 + j] = (float)i8_at(d, base + 2 + j) * dd;
+      }
+      return;
+    case 12:
+    case 13: {
+      const uint64_t bb = type == 12 ? 144 : 176;
+      for (uint64_t sb = 0; sb < K / 256; ++sb) {
+        const uint64_t base = (row * (K / 256) + sb) * bb;
+        const float dd = f16_at(d, base), dmin = f16_at(d, base + 2);
+        for (uint32_t j = 0; j < 8; ++j) {  // 32-element sub-block j = 2 * group64 + high
+          uint32_t sc, m;
+          scale_min(j, d, base + 4, &sc, &m);
+          const float a = dd * (float)sc;
+          const float c = dmin * (float)m;
+          const uint32_t g = j >> 1;
+          const bool high = (j & 1) != 0;
+          for (uint32_t l = 0; l < 32; ++l) {
+            uint32_t q;
+            if (type == 12) {
+              const uint32_t qb = byte_at(d, base + 16 + g * 32 + l);
+              q = high ? qb >> 4 : qb & 15u;
+            } else {
+              const uint32_t qb = byte_at(d, base + 48 + g * 32 + l);
+              const uint32_t mask = (high ? 2u : 1u) << (g * 2);
+              q = (high ? qb >> 4 : qb & 15u) + ((byte_at(d, base + 16 + l) & mask) != 0 ? 16u : 0u);
+            }
+            const float b = a * (float)q;
+            out[sb * 256 + g * 64 + (high ? 32 : 0) + l] = b - c;
+          }
+        }
+      }
+      return;
+    }
+    case 14:
+      for (uint64_t sb = 0; sb < K / 256; ++sb) {
+        const uint64_t base = (row * (K / 256) + sb) * 210;
+        const float dd = f16_at(d, base + 208);
+        for (uint32_t i = 0; i < 256; ++i) {
+          const uint32_t half = i >> 7, local = i & 127, lane = local & 31, quarter = local >> 5;
+          const uint32_t ql = byte_at(d, base + half * 64 + lane + ((quarter & 1) ? 32 : 0));
+          const uint32_t lo = quarter < 2 ? ql & 15u : ql >> 4;
+          const uint32_t qh = (byte_at(d, base + 128 + half * 32 + lane) >> (quarter * 2)) & 3u;
+          const int32_t q = (int32_t)(lo | (qh << 4)) - 32;
+          const float a = dd * (float)i8_at(d, base + 192 + half * 8 + (lane >> 4) + quarter * 2);
+          out[sb * 256 + i] = a * (float)q;
+        }
+      }
+      return;
+  }
+  for (uint64_t k = 0; k < K; ++k) out[k] = NAN;
+}
+
+// One output row of the GGUF matvec (llama-wgsl-runtime.ts:2412-2442): lane
+// t of 128 sums x[k] * w(n, k) over k = t, t + 128, ... in increasing k
+// (sum = sum + input[k] * w, :2420-2422), then the stride 64..1 tree. The 128
+// lane sums advance together over each 128-wide slice of k, which is the same
+// per-lane order.
+float matvec_row(uint32_t type, const uint8_t* w, uint64_t row, uint64_t K, const float* x) {
+  thread_local std::vector<float> wrow;
+  if (wrow.size() < K) wrow.resize(K);
+  decode_row(type, w, row, K, wrow.data());
+  const float* wr = wrow.data();
+  float partial[128];
+  for (uint32_t t = 0; t < 128; ++t) partial[t] = 0.0f;
+  uint64_t kb = 0;
+  for (; kb + 128 <= K; kb += 128)
+    for (uint32_t t = 0; t < 128; ++t) {
+      const float prod = x[kb + t] * wr[kb + t];
+      partial[t] = partial[t] + prod;
+    }
+  for (uint32_t t = 0; kb + t < K; ++t) {
+    const float prod = x[kb + t] * wr[kb + t];
+    partial[t] = partial[t] + prod;
   }
   for (uint32_t stride = 64; stride >= 1; stride >>= 1)
     for (uint32_t t = 0; t < stride; ++t) partial[t] = partial[t] + partial[t + stride];
@@ -537,15 +634,21 @@ void attention(orc_model* m, Layer& L, int pos, const float* q, float* out) {
       for (int t = start; t <= pos; ++t) mx = std::fmax(mx, sc[t]);
       float denom = 0.0f;
       for (int t = start; t <= pos; ++t) denom = denom + std::exp(sc[t] - mx);
-      for (int d = 0; d < hd; ++d) {
-        float acc = 0.0f;
-        for (int t = start; t <= pos; ++t) {
-          const float p = std::exp(sc[t] - mx) / denom;
-          const float pv = p * L.vcache[((size_t)kvh * C + t) * hd + d];
-          acc = acc + pv;
+      // every output dim d evaluates p_t = exp(s_t - max) / denom with the same
+      // operands, so p_t is computed once; acc[d] still sums over t in order
+      thread_local std::vector<float> pt;
+      pt.resize((size_t)C);
+      for (int t = start; t <= pos; ++t) pt[t] = std::exp(sc[t] - mx) / denom;
+      float acc[256];
+      for (int d = 0; d < hd; ++d) acc[d] = 0.0f;
+      for (int t = start; t <= pos; ++t) {
+        const float* vr = L.vcache.data() + ((size_t)kvh * C + t) * hd;
+        for (int d = 0; d < hd; ++d) {
+          const float pv = pt[t] * vr[d];
+          acc[d] = acc[d] + pv;
         }
-        out[head * hd + d] = acc;
       }
+      for (int d = 0; d < hd; ++d) out[head * hd + d] = acc[d];
     }
   });
 }
@@ -579,8 +682,8 @@ Matrix matrix(orc_model* m, const std::string& name, uint64_t k, uint64_t n) {
   const Tensor& t = it->second;
   if (t.type == 0 || t.type == 1)
     throw std::runtime_error("Llama WGSL tensor " + name + " is not a supported GGUF quantized tensor");
-  BlockGeom bg;
-  geom(t.type, &bg);
+  BlockGeom bg{1, 1};
+  if (!geom(t.type, &bg)) throw std::runtime_error("unsupported GGUF tensor type in " + name);
   if (k % (uint64_t)bg.elems) throw std::runtime_error("row length not a multiple of the block size for " + name);
   if (t.shape.empty() || t.shape[0] != k) throw std::runtime_error("tensor " + name + " row length mismatch");
   uint64_t rows = t.nbytes / (k / bg.elems * bg.bytes);
@@ -868,6 +971,13 @@ int orc_dequant(uint32_t type, const uint8_t* blocks, int64_t n, float* out) {
   return 0;
 }
 
+int orc_decode_rows(uint32_t type, const uint8_t* blocks, int64_t n_rows, int64_t row_len, float* out) {
+  BlockGeom g;
+  if (!geom(type, &g) || row_len % g.elems || n_rows < 0) return -1;
+  for (int64_t r = 0; r < n_rows; ++r) decode_row(type, blocks, (uint64_t)r, (uint64_t)row_len, out + r * row_len);
+  return 0;
+}
+
 int orc_matvec(uint32_t type, const uint8_t* blocks, int64_t n_rows, int64_t row_len, const float* x, float* y,
                int n_threads) {
   BlockGeom g;
@@ -952,6 +1062,21 @@ int orc_model_fake_context(orc_model* m, int pos, uint64_t seed) {
         }
   }
   m->pos = pos;
+  return 0;
+}
+
+int orc_argmax_gpt(const float* logits, int64_t vocab, const int32_t* penalized, int64_t n_penalized,
+                   double repetition_penalty, uint8_t* candidate_pairs, int32_t* token) {
+  // the GPT-2 runtime's stage 1/2 (gpt-wgsl-runtime.ts:1882-2004); its penalty list
+  // applies whenever the penalty is not 1 (:789-798)
+  if (vocab <= 0 || (vocab + 255) / 256 > 256) return -1;
+  std::vector<int32_t> ids;
+  if (repetition_penalty != 1.0 && n_penalized > 0) {
+    ids.assign(penalized, penalized + n_penalized);
+    std::sort(ids.begin(), ids.end());
+  }
+  const float pen = (float)(uint32_t)std::floor(repetition_penalty * 1000 + 0.5) / 1000.0f;
+  argmax_gpt(logits, vocab, ids, pen, candidate_pairs, token);
   return 0;
 }
 

@@ -33,6 +33,10 @@ extern "C" {
  * 14 Q6_K, 0 F32, 1 F16). Returns 0 on success. */
 int orc_dequant(uint32_t type, const uint8_t* blocks, int64_t n, float* out);
 
+/* The same decode row by row, as the oracle's matvec takes it (block scales
+ * decoded once per block); equal to orc_dequant element for element. */
+int orc_decode_rows(uint32_t type, const uint8_t* blocks, int64_t n_rows, int64_t row_len, float* out);
+
 /* y[N] = W[N,K] x[K] in the WGSL order: 128 strided partial sums then a
  * stride 64..1 tree (llama-wgsl-runtime.ts:2412-2442). */
 int orc_matvec(uint32_t type, const uint8_t* blocks, int64_t n_rows, int64_t row_len, const float* x,
@@ -91,6 +95,11 @@ int orc_model_fake_context(orc_model* m, int pos, uint64_t seed);
  * per 256-id group) and the greedy token. */
 int orc_argmax(const float* logits, int64_t vocab, const int32_t* penalized, int64_t n_penalized,
                double repetition_penalty, uint8_t* candidate_pairs, int32_t* token);
+
+/* The GPT-2 runtime's ARGMAX_STAGE1/2 (strict-greater trees, padding index
+ * 0, penalty whenever it is not 1; at most 65536 ids). */
+int orc_argmax_gpt(const float* logits, int64_t vocab, const int32_t* penalized, int64_t n_penalized,
+                   double repetition_penalty, uint8_t* candidate_pairs, int32_t* token);
 
 /* sampleFromCandidateBuffer (sampling.ts:23-76) with Math.random() -> uniform. */
 int32_t orc_sample_candidates(const uint8_t* candidate_pairs, int64_t n_groups, const orc_sampling* s,

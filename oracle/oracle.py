@@ -44,6 +44,7 @@ def lib():
         I32P = C.POINTER(C.c_int32)
         L.orc_dequant.argtypes = [C.c_uint32, P, C.c_int64, P]
         L.orc_matvec.argtypes = [C.c_uint32, P, C.c_int64, C.c_int64, P, P, C.c_int]
+        L.orc_decode_rows.argtypes = [C.c_uint32, P, C.c_int64, C.c_int64, P]
         L.orc_model_load.restype = P
         L.orc_model_load.argtypes = [C.c_char_p, C.POINTER(_Def), C.c_char_p, C.c_size_t]
         L.orc_model_free.argtypes = [P]
@@ -60,6 +61,7 @@ def lib():
         L.orc_sample_candidates.restype = C.c_int32
         L.orc_sample_candidates.argtypes = [P, C.c_int64, C.POINTER(_Samp), I32P, C.c_int64, C.c_double]
         L.orc_argmax.argtypes = [P, C.c_int64, I32P, C.c_int64, C.c_double, P, I32P]
+        L.orc_argmax_gpt.argtypes = [P, C.c_int64, I32P, C.c_int64, C.c_double, P, I32P]
         L.orc_uniform.restype = C.c_double
         L.orc_uniform.argtypes = [C.c_uint64, C.c_uint64]
         _L = L
@@ -71,6 +73,15 @@ def dequant(type_id: int, blocks: bytes | np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     if lib().orc_dequant(type_id, raw.ctypes.data, n, out.ctypes.data) != 0:
         raise ValueError("bad dequant arguments")
+    return out
+
+
+def decode_rows(type_id: int, blocks: bytes | np.ndarray, n_rows: int, row_len: int) -> np.ndarray:
+    """Row-wise block decode used inside the oracle's matvec (must equal dequant)."""
+    raw = np.frombuffer(bytes(blocks), dtype=np.uint8)
+    out = np.empty(n_rows * row_len, dtype=np.float32)
+    if lib().orc_decode_rows(type_id, raw.ctypes.data, n_rows, row_len, out.ctypes.data) != 0:
+        raise ValueError("bad decode arguments")
     return out
 
 
@@ -93,6 +104,19 @@ def argmax(logits: np.ndarray, penalized: Sequence[int] = (), repetition_penalty
     tok = C.c_int32()
     lib().orc_argmax(lg.ctypes.data, lg.size, arr, len(penalized), repetition_penalty, pairs.ctypes.data,
                      C.byref(tok))
+    return int(tok.value), pairs
+
+
+def argmax_gpt(logits: np.ndarray, penalized: Sequence[int] = (), repetition_penalty: float = 1.0):
+    """The GPT-2 runtime's argmax: (token, candidate pairs as uint8[groups*8])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    groups = (lg.size + 255) // 256
+    pairs = np.zeros(groups * 8, dtype=np.uint8)
+    arr = (C.c_int32 * max(1, len(penalized)))(*penalized)
+    tok = C.c_int32()
+    if lib().orc_argmax_gpt(lg.ctypes.data, lg.size, arr, len(penalized), repetition_penalty, pairs.ctypes.data,
+                            C.byref(tok)) != 0:
+        raise ValueError("vocab outside 1..65536")
     return int(tok.value), pairs
 
 

@@ -22,18 +22,34 @@ async function main() {
     const loaded = await load(job.model, null, (s) => steps.push(s.step));
     out.steps = steps;
     out.runs = [];
+    const gen = job.model.runtime === 'gpt-webgpu' ? rt.generateGptWgsl : rt.generateLlamaWgsl;
     for (const g of job.generate) {
       const seen = [];
       const opts = Object.assign({}, g.opts || {});
-      if (g.stepped) opts.onToken = (info) => seen.push(info.id);
+      let busyInCallback = null;
+      if (g.stepped) {
+        opts.onToken = (info) => {
+          // the stepped loop holds the engine while onToken runs on this thread, so a
+          // synchronous engine call from here must be refused (the reference's active guard)
+          if (g.busyProbe && seen.length === 0) {
+            try {
+              loaded.engine.reset();
+              busyInCallback = 'no error';
+            } catch (e) {
+              busyInCallback = e.code || String(e.message);
+            }
+          }
+          seen.push(info.id);
+        };
+      }
       if (g.stopAfter !== undefined) {
         let n = 0;
         opts.shouldStop = () => n++ >= g.stopAfter;
       }
       if (g.reset) rt.resetLlamaWgslConversation(loaded);
-      const r = await rt.generateLlamaWgsl(loaded, g.prompt, opts);
+      const r = await gen(loaded, g.prompt, opts);
       out.runs.push({ ids: r.ids, seen, cached: loaded.cachedTokenIds, next: loaded.cachedNextId,
-                      position: loaded.engine.position, tps: r.tokensPerSec });
+                      position: loaded.engine.position, tps: r.tokensPerSec, busy: busyInCallback });
     }
     // raw engine API: prefill + step, logits readback
     loaded.engine.reset();

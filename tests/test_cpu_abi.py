@@ -95,3 +95,19 @@ def test_null_arguments():
     assert lib().chonk_engine_destroy(None) == 0
     h = C.c_void_p()
     assert lib().chonk_engine_create(C.byref(_def()), None, C.byref(h)) == _lib.CHONK_EINVAL
+
+
+def test_shard_size_mismatch_uses_the_reference_wording(synth, tmp_path):
+    """A shard whose byte size differs from its manifest entry is refused before any device
+    work, with fetchShardCached's message (cache.ts:568-573)."""
+    from chonklm_amd import shard_gguf
+
+    out = tmp_path / "shards"
+    shard_gguf(synth("tiny-qwen3"), str(out), shard_size=65536)
+    victim = sorted(out.glob("*.bin"))[1]
+    size = victim.stat().st_size
+    victim.write_bytes(victim.read_bytes()[: size - 10])
+    rc, msg = _create(out)
+    assert rc == _lib.CHONK_EIO
+    assert f"shard {victim}: expected {size} bytes, got {size - 10}" in msg
+

@@ -273,10 +273,12 @@ def test_gpt2_step_logits_and_tokens(synth):
     assert eng.position == ref.position == len(prompt) + 12
 
 
-@pytest.mark.parametrize("temperature,top_k,rp", [(0.0, 0, 1.0), (0.8, 40, 1.0), (0.0, 0, 1.3)])
+@pytest.mark.parametrize("temperature,top_k,rp", [(0.0, 0, 1.0), (0.8, 40, 1.0), (0.0, 0, 1.3), (0.0, 0, 0.8),
+                                                  (0.8, 40, 0.8)])
 def test_gpt2_generate_matches_oracle(synth, temperature, top_k, rp):
     """generateGptWgsl (:182-249): ids, position (one step past the last id) and the cached
-    next id match the oracle, greedy, sampled and with a repetition penalty."""
+    next id match the oracle, greedy, sampled and with a repetition penalty; a penalty below
+    1 applies in ARGMAX_STAGE1 too (the GPT runtime penalizes whenever it is not 1, :789-798)."""
     w, loaded, ref = _pair(synth, "tiny-gpt2")
     prompt = _prompt(w, seed=3)
     out = generate_gpt_wgsl(loaded, prompt, w.decode_tokens, temperature=temperature, top_k=top_k,
@@ -285,6 +287,14 @@ def test_gpt2_generate_matches_oracle(synth, temperature, top_k, rp):
     assert out["ids"] == want
     assert loaded.engine.position == ref.position
     assert loaded.cached_next_id == ref.cached_next_id
+
+
+def test_gpt2_ignores_definition_default_penalty(synth):
+    """generateGptWgsl takes opts.repetitionPenalty ?? 1 (gpt-wgsl-runtime.ts:198-203): a
+    definition's defaultRepetitionPenalty is not applied, unlike generateLlamaWgsl's."""
+    w, loaded, ref = _pair(synth, "tiny-gpt2", default_repetition_penalty=1.6)
+    prompt = _prompt(w, seed=6)
+    assert generate_gpt_wgsl(loaded, prompt, 12)["ids"] == ref.generate(prompt, 12, repetition_penalty=1.0)
 
 
 def test_gpt2_loader_tags(synth):
