@@ -74,6 +74,7 @@ class EngineInfoC(C.Structure):
         ("device_bytes", C.c_uint64),
         ("kernels_per_step", C.c_int32),
         ("persistent_step", C.c_int32),
+        ("noalloc_prefill_rows", C.c_int32),
     ]
 
 
@@ -130,6 +131,7 @@ SIGNATURES = [
      [P, I32P, C.c_size_t, C.c_int32, C.POINTER(SamplingC), P, P, I32P, C.c_size_t, C.POINTER(C.c_size_t),
       C.POINTER(GenStatsC)]),
     ("chonk_engine_prefill", C.c_int, [P, I32P, C.c_size_t]),
+    ("chonk_engine_prefill_noalloc", C.c_int, [P, I32P, C.c_size_t]),
     ("chonk_engine_conversation", C.c_int, [P, I32P, C.c_size_t, C.POINTER(C.c_size_t), I32P]),
     ("chonk_engine_reset", C.c_int, [P]),
     ("chonk_engine_debug_fail_next_launch", C.c_int, [P]),

@@ -39,6 +39,13 @@
 #include "kernels.h"
 #include "prefill.h"
 
+// Row buffers of the no-allocation prompt pass (chonk_engine_prefill_noalloc):
+// one array per GPU the library runs on, held until the process ends. Host
+// code never uses this name as an address: the device address comes from
+// hipGetSymbolAddress, once per device (scratch_address).
+constexpr size_t kNoAllocScratchBytes = (size_t)48 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace chonk {
 namespace {
 
@@ -358,6 +365,8 @@ struct chonk_engine {
   uint64_t weight_bytes_per_token = 0;
   // batched prompt processing: row buffers allocated on first use
   bool batched_prefill = true;
+  uint8_t* scratch = nullptr;  // device address of this GPU's no-allocation prompt-pass scratch
+  int noalloc_rows = 0;        // rows one chonk_engine_prefill_noalloc call may take (0: none)
   void* pf_mem = nullptr;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr,
         *pf_d = nullptr, *pf_xscale = nullptr, *pf_part = nullptr;
@@ -541,6 +550,24 @@ float* upload_floats(Arena& arena, const ByteSource& src, const GgufFile& g, con
   HIP_OK(hipMemcpy(p, f.data(), (size_t)n * 4, hipMemcpyHostToDevice));
   return p;
 }
+
+// Device address of `scratch` on `device`, looked up once per device with
+// that device current (the caller has made it current).
+uint8_t* scratch_address(int device) {
+  static std::mutex* mu = new std::mutex();
+  static std::map<int, uint8_t*>* addr = new std::map<int, uint8_t*>();
+  std::lock_guard<std::mutex> l(*mu);
+  auto it = addr->find(device);
+  if (it != addr->end()) return it->second;
+  void* p = nullptr;
+  HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  if (!p) throw Error(CHONK_EHIP, "hipGetSymbolAddress returned no address for the prompt-pass scratch");
+  (*addr)[device] = (uint8_t*)p;
+  return (uint8_t*)p;
+}
+
+// Rows of one no-allocation prompt pass for this model (defined with the row buffers).
+int noalloc_rows_for(const ModelCfg& c);
 
 int target_wgs() { return 512; }
 
@@ -1450,6 +1477,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
   e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt &&
                        std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) <= 4096;
+  // the no-allocation prompt pass: as many rows (a multiple of 16, at most one
+  // full pass) as fit the scratch with this model's row buffers
+  e->scratch = scratch_address(e->device);
+  e->noalloc_rows = e->batched_prefill ? noalloc_rows_for(c) : 0;
   const char* ng = std::getenv("CHONK_NO_GRAPH");
   e->use_graph = !(ng && ng[0] == '1');
   for (const Launch& L : e->kernels_logits)
@@ -1461,8 +1492,6 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   *out = e.release();
 }
 
-// One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
-// cannot trace graph launches) the same launches issued one by one.
 // The test hook's stand-in for a failed launch: the same error path as a HIP
 // error returned by the runtime (the caller marks the engine lost).
 void check_injected_failure(chonk_engine* e, const char* where) {
@@ -1472,6 +1501,8 @@ void check_injected_failure(chonk_engine* e, const char* where) {
                                       "chonk_engine_debug_fail_next_launch) at ") + where);
 }
 
+// One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
+// cannot trace graph launches) the same launches issued one by one.
 void replay(chonk_engine* e, bool logits) {
   check_injected_failure(e, "hipGraphLaunch");
   if (e->use_graph) {
@@ -1798,6 +1829,14 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
   }
 }
 
+// The largest multiple of 16 rows, at most one full pass, whose row buffers fit
+// the no-allocation scratch (0 when not even 16 rows fit).
+int noalloc_rows_for(const ModelCfg& c) {
+  for (int r = kPrefillRows; r >= 16; r -= 16)
+    if (row_bufs_layout(c, r, nullptr, nullptr) <= kNoAllocScratchBytes) return r;
+  return 0;
+}
+
 void prefill_alloc(chonk_engine* e) {
   if (e->pf_mem) return;
   RowBufs b;
@@ -1841,22 +1880,29 @@ RowBufs engine_row_bufs(const chonk_engine* e) {
 // computed as row batches (dequant-fused MFMA GEMMs, causal attention over the
 // cache). The host position and the device state are left to the caller; no
 // logits are produced (the reference's runToken(id, false) for each token).
+void prefill_rows_in(chonk_engine* e, const RowBufs& b, const int32_t* tokens, int n);
+
 void prefill_rows(chonk_engine* e, const int32_t* tokens, int n) {
+  if (n <= 0) return;
+  prefill_alloc(e);
+  prefill_rows_in(e, engine_row_bufs(e), tokens, n);
+}
+
+// The same pass with row buffers b (passes of at most b.cap rows).
+void prefill_rows_in(chonk_engine* e, const RowBufs& b, const int32_t* tokens, int n) {
   check_injected_failure(e, "the prompt pass");
   const ModelCfg& c = e->cfg;
   if (n <= 0) return;
   if ((int64_t)e->pos + n > c.ctx)
     throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
-  prefill_alloc(e);
-  const RowBufs b = engine_row_bufs(e);
   RowKv kvs;
   for (const LayerDev& L : e->layers) {
     kvs.kc.push_back(L.kc);
     kvs.vc.push_back(L.vc);
   }
   kvs.ctx = c.ctx;
-  for (int off = 0; off < n; off += kPrefillRows) {
-    const int T = std::min(kPrefillRows, n - off);
+  for (int off = 0; off < n; off += b.cap) {
+    const int T = std::min(b.cap, n - off);
     HIP_OK(hipMemcpyAsync(b.tok, tokens + off, (size_t)T * 4, hipMemcpyHostToDevice, e->stream));
     RowPlace pl;
     pl.p0 = e->pos + off;
@@ -2170,6 +2216,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->device_bytes = e->weights.capacity() + e->state.capacity();
   out->kernels_per_step = (int32_t)e->kernels_logits.size();
   out->persistent_step = e->use_step ? 1 : 0;
+  out->noalloc_prefill_rows = e->noalloc_rows;
   return CHONK_OK;
 }
 
@@ -2199,6 +2246,37 @@ int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n) {
     }
     HIP_OK(hipMemcpy(e->hist + e->pos, tokens, n * 4, hipMemcpyHostToDevice));
     prefill_rows(e, tokens, (int)n);
+    e->pos += (int)n;
+    DevState st = read_state(e);
+    st.pos = e->pos;
+    upload_state_fields(e, st);
+    e->known_token_pos = -1;
+    e->logits_valid = false;
+  });
+}
+
+int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t n) {
+  return api(e, [&] {
+    if (n == 0) return;
+    if (!tokens) throw Error(CHONK_EINVAL, "tokens is null");
+    if (e->noalloc_rows <= 0)
+      throw Error(CHONK_EINVAL, std::string("chonk_engine_prefill_noalloc: this model has no row-batch prompt pass ") +
+                                    "that fits the " + std::to_string(kNoAllocScratchBytes >> 20) +
+                                    " MiB scratch (gpt2, rows wider than 4096, or CHONK_PREFILL=token)");
+    if (n > (size_t)e->noalloc_rows)
+      throw Error(CHONK_EINVAL, "chonk_engine_prefill_noalloc takes at most " + std::to_string(e->noalloc_rows) +
+                                    " tokens per call for this model (its " +
+                                    std::to_string(kNoAllocScratchBytes >> 20) + " MiB scratch), got " +
+                                    std::to_string(n));
+    for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
+    if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
+      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+    // every row buffer is written before it is read (the operand split writes
+    // its own zero padding), so the previous call's contents need no clearing
+    RowBufs b;
+    row_bufs_layout(e->cfg, e->noalloc_rows, e->scratch, &b);
+    HIP_OK(hipMemcpy(e->hist + e->pos, tokens, n * 4, hipMemcpyHostToDevice));
+    prefill_rows_in(e, b, tokens, (int)n);
     e->pos += (int)n;
     DevState st = read_state(e);
     st.pos = e->pos;

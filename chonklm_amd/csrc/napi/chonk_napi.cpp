@@ -525,6 +525,7 @@ napi_value Info(napi_env env, napi_callback_info info) {
            {"headDim", (double)ei.head_dim},    {"context", (double)ei.context},
            {"weightBytesPerToken", (double)ei.weight_bytes_per_token},
            {"deviceBytes", (double)ei.device_bytes}, {"kernelsPerStep", (double)ei.kernels_per_step},
+           {"noallocPrefillRows", (double)ei.noalloc_prefill_rows},
            {"architecture", (double)ei.architecture}};
   for (const auto& x : f) {
     napi_create_double(env, x.v, &v);

@@ -84,6 +84,12 @@ class LlamaWgslEngine:
         arr, n = _i32_array(list(token_ids))
         check(lib().chonk_engine_prefill(self._h, C.cast(arr, C.POINTER(C.c_int32)), n), self._h)
 
+    def prefill_noalloc(self, token_ids: Sequence[int]) -> None:
+        """prefill() with the row buffers in the library's per-GPU scratch (no device
+        allocation); at most info['noalloc_prefill_rows'] tokens per call."""
+        arr, n = _i32_array(list(token_ids))
+        check(lib().chonk_engine_prefill_noalloc(self._h, C.cast(arr, C.POINTER(C.c_int32)), n), self._h)
+
     def reset(self) -> None:
         check(lib().chonk_engine_reset(self._h), self._h)
 

@@ -89,6 +89,7 @@ typedef struct {
   uint64_t device_bytes;            /* device memory held by the engine */
   int32_t kernels_per_step;         /* per-phase kernels of one decode step (chonk_engine_bench_kernel ids) */
   int32_t persistent_step;          /* 1: a step runs as one persistent kernel launch */
+  int32_t noalloc_prefill_rows;     /* most tokens one chonk_engine_prefill_noalloc call takes (0: none) */
 } chonk_engine_info;
 
 typedef struct {
@@ -129,6 +130,20 @@ int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, 
  * linear layers as dequant-fused MFMA GEMMs and a causal attention over the
  * cache. generate uses the same pass for all but the last prompt token. */
 int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n);
+
+/* chonk_engine_prefill without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The row buffers of the pass come from one 48 MiB device array per GPU,
+ * reserved when the library is loaded on that GPU and held until the process
+ * ends, instead of the ~50-60 MB that chonk_engine_prefill allocates on its
+ * first call. One call takes at most chonk_engine_info.noalloc_prefill_rows
+ * tokens (one pass; CHONK_EINVAL beyond that, or when the model's row buffers
+ * do not fit). Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (two engines on two threads) race and must be
+ * serialized by the caller. Results equal chonk_engine_prefill's to fp32
+ * rounding (passes of a different row count change the GEMMs' K split). */
+int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t n);
 
 /* generateLlamaWgsl: prefix reuse against the previous conversation, prompt
  * prefill, then up to max_new_tokens generated ids (stopping after an EOS
