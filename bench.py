@@ -84,11 +84,22 @@ def kernel_symbol(cls: str, info: dict) -> str:
     return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
 
 
+def host_cpus() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:
-    """Oracle decode steps at the benchmark's context, fake K/V, greedy."""
+    """Oracle decode steps at the benchmark's context (fake K/V, greedy), plus a few
+    prompt steps without logits at two contexts, from which the reference's own figure
+    generated / (prefill + decode) (llama-wgsl-runtime.ts:266, :312-313) is estimated
+    for the whole workload (per-token cost taken as linear in the position)."""
     from oracle.oracle import OracleModel
 
-    ref = OracleModel(path, w.spec.vocab, w.spec.layers, pos + 64, kv_f16=True, threads=threads)
+    ctx = max(pos + 64, w.prompt_tokens + w.decode_tokens + 8)
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=threads)
     ref.fake_context(pos, seed=1)
     tok = 1
     n = 0
@@ -99,10 +110,77 @@ def cpu_baseline(path: str, w, pos: int, seconds: float, threads: int) -> dict:
         el = time.perf_counter() - t0
         if el >= seconds or n >= 64:
             break
+    decode_s = el / n
+    # prompt steps (runToken(id, false): no lm_head) at the start and in the middle of the prompt
+    samples = []
+    for p0 in (0, w.prompt_tokens // 2):
+        ref.reset()
+        ref.fake_context(p0, seed=2)
+        t1 = time.perf_counter()
+        for i in range(4):
+            ref.run_token(1 + i, False)
+        samples.append((p0 + 2, (time.perf_counter() - t1) / 4))
     ref.close()
+    (x0, c0), (x1, c1) = samples
+    slope = (c1 - c0) / max(x1 - x0, 1)
+    prefill_est = sum(max(c0 + slope * (p - x0), 0.0) for p in range(w.prompt_tokens - 1))
+    decode_est = w.decode_tokens * decode_s
     return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "host_cpus": host_cpus(),
+            "reference_formula_tokens_per_sec": round(w.decode_tokens / (prefill_est + decode_est), 4),
+            "reference_formula_note": f"generated / (prefill + decode) for {w.prompt_tokens} prompt + "
+                                      f"{w.decode_tokens} generated tokens, estimated from the sampled per-token "
+                                      f"costs (prompt steps {c0 * 1e3:.0f} ms at position {x0}, {c1 * 1e3:.0f} ms at "
+                                      f"{x1}; decode {decode_s * 1e3:.0f} ms at {pos})",
             "sample": f"{n} greedy decode steps of the same model at context {pos}..{pos + n} "
-                      f"(synthetic K/V), oracle CPU restatement of the reference WGSL arithmetic, {el:.1f} s"}
+                      f"(synthetic K/V) and 8 prompt steps, oracle CPU restatement of the reference WGSL "
+                      f"arithmetic on {threads} threads ({host_cpus()} host CPUs visible), {el:.1f} s of decode"}
+
+
+def kernel_cold_warm(eng, info: dict, reps: int) -> dict:
+    """Per-launch HIP-event times of representative step kernels with the caches flushed
+    (cold: >= 512 MiB written first, evicting L2 and the 256 MB Infinity Cache) and right
+    after an identical launch (warm), each over `reps` launches, with their GB/s."""
+    n = info["kernels_per_step"]
+    names = {}
+    for kid in range(n - 1):
+        name, _, nbytes = eng.bench_kernel(kid, 1)
+        names[name] = (kid, nbytes)
+    last = info["layers"] - 1
+    want = {"attn (last layer)": f"L{last}.attn", "gate|up Q4_K (layer 1)": "L1.gateup",
+            "q|k|v (layer 1)": "L1.qkv", "down (layer 1)": "L1.down", "lm_head": "lmhead"}
+    out = {}
+    for label, key in want.items():
+        if key not in names:
+            continue
+        kid, nbytes = names[key]
+        cold, warm = eng.bench_kernel_cold(kid, reps)
+        out[label] = {"kernel": key, "bytes": int(nbytes), "cold_us": round(cold, 3), "warm_us": round(warm, 3),
+                      "cold_gb_s": round(nbytes / cold / 1e3, 1), "warm_gb_s": round(nbytes / warm / 1e3, 1)}
+    return out
+
+
+def q4k_matvec_bandwidth(rows: int = 262144, k: int = 2048, reps: int = 20) -> dict:
+    """A Q4_K matvec too large for the Infinity Cache (rows x k Q4_K = 302 MB): every launch
+    streams the matrix from HBM; GB/s of its GGUF bytes over the mean of `reps` launches."""
+    import ctypes as C
+
+    from chonklm_amd._lib import check, lib
+
+    nb = rows * (k // 256)
+    rng = np.random.default_rng(5)
+    blocks = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    blocks[:, 0:4] = np.array([0x00, 0x20, 0x00, 0x20], dtype=np.uint8)  # d = dmin = 2^-7 (f16)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    us = C.c_double()
+    check(lib().chonk_matvec(0, 12, blocks.ctypes.data, rows, k, x.ctypes.data_as(C.POINTER(C.c_float)),
+                             y.ctypes.data_as(C.POINTER(C.c_float)), reps, C.byref(us)))
+    nbytes = nb * 144
+    return {"rows": rows, "k": k, "bytes": nbytes, "us_per_launch": round(us.value, 2),
+            "achieved": round(nbytes / us.value / 1e3, 1), "unit": "GB/s",
+            "frac": round(nbytes / us.value / 1e3 / HBM_PEAK_GBS, 4),
+            "note": "generic Q4_K matvec kernel, 256-row tiles; matrix larger than the Infinity Cache"}
 
 
 def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: int) -> dict:
@@ -140,6 +218,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--cold-reps", type=int, default=100,
+                    help="launches per kernel for the cold / warm per-launch timing (0 skips it)")
     ap.add_argument("--no-kernel-times", action="store_true",
                     help="skip the per-kernel timing pass (profiling runs)")
     ap.add_argument("--fake-prefill", action="store_true",
@@ -265,9 +345,9 @@ def main() -> int:
             "prompt_tokens": w.prompt_tokens,
             "context_at_timed_start": pos0 + args.warmup,
             "context_at_end": pos_end,
-            "kv_cache": "f16",
+            "kv_cache": "f16" if info.get("kv_dtype", 0) == 0 else "f32",
             "persistent_step": bool(info.get("persistent_step")),
-            "weights": "Q4_K_M GGUF (Q4_K / Q6_K), random N(0,0.02)",
+            "weights": f"{w.spec.recipe.upper()} GGUF (llama.cpp type recipe), random N(0,0.02)",
         },
         "roofline": {
             "bound": "hbm",
@@ -302,10 +382,26 @@ def main() -> int:
         "model_build_s": round(build_s, 1),
         "cpu_baseline": None,
     }
+    if w.temperature > 0 or w.top_k > 0:
+        # the timed steps above select greedily; the configuration's own sampling runs
+        # through the device-driven generate loop (candidate sampler in the select kernel)
+        from chonklm_amd.runtime import reset_llama_wgsl_conversation
+
+        reset_llama_wgsl_conversation(loaded)
+        g = generate_llama_wgsl(loaded, prompt, w.decode_tokens, temperature=w.temperature, top_k=w.top_k,
+                                top_p=w.top_p, seed=9)
+        n_gen = len(g["ids"])
+        result["sampled_decode"] = {
+            "temperature": w.temperature, "top_k": w.top_k, "generated": n_gen,
+            "tokens_per_sec": round((n_gen - 1) / (g["decodeMs"] / 1000.0), 1) if n_gen > 1 else None,
+            "note": "generateLlamaWgsl with the configuration's sampling; decode wall time after the prompt"}
+    if args.cold_reps > 0 and not args.no_kernel_times:
+        result["kernel_cold_warm"] = kernel_cold_warm(eng, info, args.cold_reps)
+        result["q4k_matvec_hbm"] = q4k_matvec_bandwidth()
     if not args.no_batched and info.get("kv_dtype", 0) == 0 and info.get("architecture") != 3:
         result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4)
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
+        threads = min(16, host_cpus())  # the GPU box's CPU share is 16 threads
         result["cpu_baseline"] = cpu_baseline(path, w, pos0, args.cpu_seconds, threads)
     loaded.engine.dispose()
     print(json.dumps(result), flush=True)

@@ -151,6 +151,8 @@ SIGNATURES = [
     ("chonk_engine_bench_kernel", C.c_int,
      [P, C.c_int32, C.c_int32, C.POINTER(C.c_double), C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64)]),
     ("chonk_engine_fake_context", C.c_int, [P, C.c_int32, C.c_uint64]),
+    ("chonk_engine_bench_kernel_cold", C.c_int,
+     [P, C.c_int32, C.c_int32, C.c_uint64, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     ("chonk_dequant", C.c_int, [C.c_int32, C.c_uint32, P, C.c_int64, C.c_int64, F32P]),
     ("chonk_matvec", C.c_int,
      [C.c_int32, C.c_uint32, P, C.c_int64, C.c_int64, F32P, F32P, C.c_int32, C.POINTER(C.c_double)]),

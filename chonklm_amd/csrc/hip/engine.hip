@@ -376,6 +376,8 @@ struct chonk_engine {
   std::atomic<bool> busy{false};
   bool lost = false;
   bool fail_next_launch = false;  // test hook: the next launch reports a HIP error
+  void* flush = nullptr;          // benchmark: buffer written between cold launches
+  size_t flush_bytes = 0;
   std::string err;
 };
 
@@ -1240,6 +1242,7 @@ void engine_free(chonk_engine* e) {
   if (e->tagged) (void)hipFree(e->tagged);
   if (e->d_phases) (void)hipFree(e->d_phases);
   if (e->pf_mem) (void)hipFree(e->pf_mem);
+  if (e->flush) (void)hipFree(e->flush);
   for (auto& t : e->rope_cs) (void)hipFree(t.second);
   if (e->h_state) (void)hipHostFree(e->h_state);
   if (e->h_tok) (void)hipHostFree(e->h_tok);
@@ -2548,6 +2551,57 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
       }
       *bytes = by;
     }
+  });
+}
+
+int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t reps, uint64_t flush_bytes,
+                                   double* cold_us, double* warm_us) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (kernel_id < 0 || kernel_id >= (int32_t)e->kernels_logits.size() || reps <= 0)
+      throw Error(CHONK_EINVAL, "bad kernel id or repetitions");
+    const Launch& L = e->kernels_logits[(size_t)kernel_id];
+    if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
+    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    flush_bytes = std::max<uint64_t>(flush_bytes, (uint64_t)512 << 20);
+    if (e->flush_bytes < flush_bytes) {
+      if (e->flush) HIP_OK(hipFree(e->flush));
+      e->flush = nullptr;
+      e->flush_bytes = 0;
+      HIP_OK(hipMalloc(&e->flush, flush_bytes));
+      e->flush_bytes = flush_bytes;
+    }
+    const DevState saved = read_state(e);
+    DevState st = saved;
+    st.stopped = 0;
+    st.generating = 0;
+    upload_state_fields(e, st);
+    Launch run = L;
+    if (run.kind == Launch::MV) run.mv.advance_pos = 0;
+    hipEvent_t a, b;
+    HIP_OK(hipEventCreate(&a));
+    HIP_OK(hipEventCreate(&b));
+    double sum[2] = {0, 0};
+    enqueue(run, e->stream);
+    for (int mode = 0; mode < 2; ++mode)  // 0 cold: caches flushed before the launch; 1 warm: launched twice, the second timed
+      for (int i = 0; i < reps; ++i) {
+        if (mode == 0)
+          HIP_OK(hipMemsetAsync(e->flush, i & 0xff, e->flush_bytes, e->stream));
+        else
+          enqueue(run, e->stream);
+        HIP_OK(hipEventRecord(a, e->stream));
+        enqueue(run, e->stream);
+        HIP_OK(hipEventRecord(b, e->stream));
+        HIP_OK(hipEventSynchronize(b));
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, a, b));
+        sum[mode] += ms;
+      }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    upload_state_fields(e, saved);
+    if (cold_us) *cold_us = sum[0] * 1000.0 / reps;
+    if (warm_us) *warm_us = sum[1] * 1000.0 / reps;
   });
 }
 

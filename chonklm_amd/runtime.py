@@ -135,6 +135,13 @@ class LlamaWgslEngine:
                                          out.ctypes.data_as(C.POINTER(C.c_float))), self._h)
         return out
 
+    def bench_kernel_cold(self, kernel_id: int, reps: int, flush_bytes: int = 768 << 20) -> tuple[float, float]:
+        """(cold, warm) mean microseconds of one launch of a step kernel, caches flushed or not."""
+        cold, warm = C.c_double(), C.c_double()
+        check(lib().chonk_engine_bench_kernel_cold(self._h, kernel_id, reps, flush_bytes, C.byref(cold),
+                                                   C.byref(warm)), self._h)
+        return float(cold.value), float(warm.value)
+
     def fake_context(self, pos: int, seed: int = 1) -> None:
         check(lib().chonk_engine_fake_context(self._h, pos, seed), self._h)
 

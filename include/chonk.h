@@ -204,6 +204,12 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
  * bytes per launch. */
 int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
                               size_t name_len, uint64_t* bytes);
+/* The same kernel timed launch by launch with HIP events, `reps` times with
+ * the caches flushed first (a write of max(flush_bytes, 512 MiB) to a
+ * benchmark buffer evicts L2 and the 256 MB Infinity Cache: *cold_us) and
+ * `reps` times right after an identical launch (*warm_us). */
+int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t reps, uint64_t flush_bytes,
+                                   double* cold_us, double* warm_us);
 /* Persistent step only: runs one decode step with per-phase time stamps and
  * returns, per phase (q|k|v, attention, o_proj, gate|up, down per layer, then
  * lm_head), the time from the first workgroup's start to the last workgroup's
