@@ -973,15 +973,23 @@ bool build_step(chonk_engine* e) {
   if (cus <= 0) return false;
   const int grid = cus;
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn, NL = c.layers;
-  const size_t shmem =
-      step_shared_bytes(std::max(H, std::max(qdim, F)), 0, G, c.hd, e->chunk, e->nchunk, (int)e->kv_elem);
+  // attention chunk of the step: the largest that keeps a task's K/V rows,
+  // rotary table and norm weights within one prefetch slot
+  int schunk = 0;
+  for (int ch = attn_max_chunk(c.hd); ch >= 16 && !schunk; ch >>= 1) {
+    AttnSlot L;
+    if (attn_slot_layout(c.hd, ch, (int)e->kv_elem, &L) <= kStepSlotBytes) schunk = ch;
+  }
+  if (!schunk) return false;
+  const int snchunk = (c.ctx + schunk - 1) / schunk;
+  const size_t shmem = step_shared_bytes(std::max(H, std::max(qdim, F)), 0, G, c.hd, schunk, snchunk, (int)e->kv_elem);
   if (shmem > lds_limit() || step_occupancy(G, kv16, shmem) < 1) return false;
 
   // tagged buffers: R0 | RFIN | per layer QKV, ATT, RMID, FF, REND, DO, DD, attention partials | epoch, done
   // (a partial row is written and read once per step, so a workgroup that
   // merges several layers never meets a row it has read before)
   const size_t rowf = (size_t)attn_rowf(G, c.hd);
-  const size_t part_layer = (size_t)c.kv_heads * e->nchunk * rowf;  // words
+  const size_t part_layer = (size_t)c.kv_heads * snchunk * rowf;  // words
   const size_t per_layer = (size_t)(qdim + 2 * kvdim) + qdim + H + F + H + (c.gemma ? 2 * H : 0) + part_layer;
   const size_t dbg_words = (sizeof(StepDebug) + 7) / 8;
   const size_t words = 2 * (size_t)H + per_layer * NL + 2 + dbg_words;
@@ -1070,10 +1078,11 @@ bool build_step(chonk_engine* e) {
       p.at.part = nullptr;
       // the step's own attention geometry (the per-phase kernel may use k_attn_dec's)
       p.at.variant = 0;
-      p.at.chunk = e->chunk;
-      p.at.nchunk = e->nchunk;
-      p.at.merge_floats = attn_merge_floats(c.heads / c.kv_heads, c.hd, e->nchunk);
-      p.n_tasks = c.kv_heads * e->nchunk;
+      p.at.chunk = schunk;
+      p.at.nchunk = snchunk;
+      p.at.merge_floats = attn_merge_floats(c.heads / c.kv_heads, c.hd, snchunk);
+      p.at.tpp = attn_threads_per_position(c.hd, schunk, (int)e->kv_elem);
+      p.n_tasks = c.kv_heads * snchunk;
       p.qkv_in = tl[i].qkv;
       p.attn_out = tl[i].att;
       p.tpart = tl[i].part;
@@ -1151,14 +1160,105 @@ bool build_step(chonk_engine* e) {
   for (const StepPhase& p : ph)
     for (int si = 0; si < p.nseg && p.kind == PH_MV; ++si)
       if (2 * p.seg[si].tile > 1024) throw Error(CHONK_EINVAL, "persistent step: matvec tile too large");
-  // device copies: the phase table, then the two argument blocks (with / without logits)
+  // every task before the lm_head must find its rows and norm weights in one slot
+  for (const StepPhase& p : ph) {
+    if (p.kind != PH_MV || p.epi == EPI_LOGITS) continue;
+    const bool glu = p.epi == EPI_GLU_SILU || p.epi == EPI_GLU_GELU;
+    const int norms = p.pro == PRO_PLAIN ? 0 : (p.pro == PRO_RES_NORM ? 2 : 1);
+    for (int si = 0; si < p.nseg; ++si) {
+      const MvSeg& sg = p.seg[si];
+      for (int t0 = 0; t0 < sg.n_out; t0 += sg.tile) {
+        MvSlot sl;
+        if (mv_slot_layout(sg.w.type, p.k, t0, std::min(sg.tile, sg.n_out - t0), glu ? 2 : 1, norms, &sl) >
+            kStepSlotBytes) {
+          (void)hipFree(e->tagged);
+          e->tagged = nullptr;
+          return false;
+        }
+      }
+    }
+  }
+  // each workgroup's task list: task t of a phase runs on workgroup t mod grid
+  int max_tasks = 0;
+  for (int b = 0; b < grid; ++b) {
+    int n = 0;
+    for (const StepPhase& p : ph) n += p.n_tasks > b ? (p.n_tasks - b + grid - 1) / grid : 0;
+    max_tasks = std::max(max_tasks, n);
+  }
+  const int stride = max_tasks + kStepDescRing;  // end records cover the descriptor prefetch
+  std::vector<StepTask> tasks((size_t)grid * stride);
+  for (StepTask& d : tasks) d.phase = INT32_MAX;
+  for (int b = 0; b < grid; ++b) {
+    StepTask* out = tasks.data() + (size_t)b * stride;
+    for (int pi = 0; pi < (int)ph.size(); ++pi) {
+      const StepPhase& p = ph[(size_t)pi];
+      for (int t = b; t < p.n_tasks; t += grid) {
+        StepTask d{};
+        d.phase = pi;
+        d.t = t;
+        if (p.kind == PH_ATTN) {
+          d.kind = STASK_ATTN;
+        } else if (p.epi == EPI_LOGITS) {
+          d.kind = STASK_LM;
+        } else {
+          d.kind = STASK_MV;
+          const int si = (p.nseg > 2 && t >= p.seg[2].wg_begin) ? 2 : (p.nseg > 1 && t >= p.seg[1].wg_begin) ? 1 : 0;
+          const MvSeg& sg = p.seg[si];
+          const int task = t - sg.wg_begin;
+          d.type = sg.w.type;
+          d.k = p.k;
+          d.lpr = sg.lpr;
+          d.uc = (p.k >> 5) <= sg.lpr ? 1 : 2;
+          d.t0 = task * sg.tile;
+          d.nt = std::min(sg.tile, sg.n_out - d.t0);
+          d.glu = p.epi == EPI_GLU_SILU || p.epi == EPI_GLU_GELU;
+          d.pro = p.pro;
+          d.epi = p.epi;
+          if (p.pro == PRO_EMBED_NORM || p.pro == PRO_RES_NORM) {
+            const int S = (p.k + p.n_tasks - 1) / p.n_tasks;
+            d.res_lo = std::min(p.k, t * S);
+            d.res_hi = std::min(p.k, d.res_lo + S);
+          }
+          d.in = p.in;
+          d.delta = p.delta;
+          d.add = p.epi == EPI_ADD ? p.add + d.t0 : nullptr;
+          d.out = p.tout[si] + d.t0;
+          d.res_out = p.res_out;
+          MvSlot sl;
+          mv_slot_layout(d.type, p.k, d.t0, d.nt, d.glu ? 2 : 1,
+                         p.pro == PRO_PLAIN ? 0 : (p.pro == PRO_RES_NORM ? 2 : 1), &sl);
+          d.wn = sl.wn;
+          d.wd = sl.wd;
+          auto dma = [&](const void* src, int dst, int n16) {
+            if (d.n_dma >= kStepMaxDma) throw Error(CHONK_EINVAL, "persistent step: too many slot copies");
+            d.dma[d.n_dma++] = StepDma{(const uint8_t*)src, dst, n16};
+          };
+          if (sl.wn >= 0) dma(p.w_norm, sl.wn, p.k / 4);
+          if (sl.wd >= 0) dma(p.w_delta, sl.wd, p.k / 4);
+          const uint8_t* const src[2][4] = {{sg.w.s0, sg.w.s1, sg.w.s2, sg.w.s3}, {sg.w2.s0, sg.w2.s1, sg.w2.s2, sg.w2.s3}};
+          for (int j = 0; j < 2; ++j)
+            for (int q = 0; q < 4; ++q) {
+              d.data[j][q] = sl.data[j][q];
+              if (sl.n16[j][q] > 0) dma(src[j][q] + sl.src0[j][q], sl.dst[j][q], sl.n16[j][q]);
+            }
+        }
+        *out++ = d;
+      }
+    }
+  }
+  // device copies: the phase table, the task lists, then the argument blocks (with / without logits, traced)
   const size_t ph_bytes = align256(ph.size() * sizeof(StepPhase));
-  HIP_OK(hipMalloc((void**)&e->d_phases, ph_bytes + 3 * align256(sizeof(StepArgs))));
+  const size_t task_bytes = align256(tasks.size() * sizeof(StepTask));
+  HIP_OK(hipMalloc((void**)&e->d_phases, ph_bytes + task_bytes + 3 * align256(sizeof(StepArgs))));
   HIP_OK(hipMemcpy(e->d_phases, ph.data(), ph.size() * sizeof(StepPhase), hipMemcpyHostToDevice));
-  StepArgs* d_args = (StepArgs*)((uint8_t*)e->d_phases + ph_bytes);
+  StepTask* d_tasks = (StepTask*)((uint8_t*)e->d_phases + ph_bytes);
+  HIP_OK(hipMemcpy(d_tasks, tasks.data(), tasks.size() * sizeof(StepTask), hipMemcpyHostToDevice));
+  StepArgs* d_args = (StepArgs*)((uint8_t*)d_tasks + task_bytes);
 
   StepArgs a{};
   a.phases = e->d_phases;
+  a.tasks = d_tasks;
+  a.task_stride = stride;
   a.st = e->st;
   a.epoch = epoch;
   a.done = done;
@@ -2160,6 +2260,44 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
 
 // ---- C ABI ------------------------------------------------------------------------
 
+namespace chonk {
+namespace {
+// One persistent step with wall-clock stamps; returns the raw trace.
+std::vector<uint64_t> trace_step(chonk_engine* e, int* np_out, int* grid_out) {
+  if (!e->use_step) throw Error(CHONK_EINVAL, "the engine does not run the persistent step");
+  const ModelCfg& c = e->cfg;
+  if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+  const Launch& L = e->step_logits[0];
+  const int np = L.step.n_phases, grid = L.grid;
+  const size_t words = (size_t)(np + 1) * grid + (size_t)np * grid * kStepStamps;
+  uint64_t* tr = nullptr;
+  HIP_OK(hipMalloc(&tr, words * 8));
+  Launch run = L;
+  run.step.trace = tr;
+  StepArgs* slot = (StepArgs*)((uint8_t*)L.d_step + 2 * align256(sizeof(StepArgs)));
+  HIP_OK(hipMemcpy(slot, &run.step, sizeof(StepArgs), hipMemcpyHostToDevice));
+  run.d_step = slot;
+  const DevState saved = read_state(e);
+  DevState st = saved;
+  st.stopped = 0;
+  st.generating = 0;
+  upload_state_fields(e, st);
+  enqueue(run, e->stream);  // warm
+  HIP_OK(hipMemsetAsync(tr, 0, words * 8, e->stream));
+  upload_state_fields(e, st);
+  enqueue(run, e->stream);
+  HIP_OK(hipStreamSynchronize(e->stream));
+  std::vector<uint64_t> h(words);
+  HIP_OK(hipMemcpy(h.data(), tr, words * 8, hipMemcpyDeviceToHost));
+  (void)hipFree(tr);
+  upload_state_fields(e, saved);
+  *np_out = np;
+  *grid_out = grid;
+  return h;
+}
+}  // namespace
+}  // namespace chonk
+
 extern "C" {
 
 const char* chonk_last_error(void) { return g_last_error.c_str(); }
@@ -2466,35 +2604,23 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
   });
 }
 
+int chonk_engine_profile_step_raw(chonk_engine* e, uint64_t* out, size_t cap, int32_t* n_phases, int32_t* n_wg) {
+  return api(e, [&] {
+    int np = 0, grid = 0;
+    const std::vector<uint64_t> h = trace_step(e, &np, &grid);
+    if (out) std::memcpy(out, h.data(), std::min(cap, h.size()) * 8);
+    if (n_phases) *n_phases = np;
+    if (n_wg) *n_wg = grid;
+  });
+}
+
+
 int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases) {
   return api(e, [&] {
-    if (!e->use_step) throw Error(CHONK_EINVAL, "the engine does not run the persistent step");
-    const ModelCfg& c = e->cfg;
-    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
-    const Launch& L = e->step_logits[0];
-    const int np = L.step.n_phases, grid = L.grid;
+    int np = 0, grid = 0;
+    const std::vector<uint64_t> h = trace_step(e, &np, &grid);
     const size_t words = (size_t)(np + 1) * grid;
-    uint64_t* tr = nullptr;
-    HIP_OK(hipMalloc(&tr, words * 8));
-    Launch run = L;
-    run.step.trace = tr;
-    StepArgs* slot = (StepArgs*)((uint8_t*)L.d_step + 2 * align256(sizeof(StepArgs)));
-    HIP_OK(hipMemcpy(slot, &run.step, sizeof(StepArgs), hipMemcpyHostToDevice));
-    run.d_step = slot;
-    const DevState saved = read_state(e);
-    DevState st = saved;
-    st.stopped = 0;
-    st.generating = 0;
-    upload_state_fields(e, st);
-    enqueue(run, e->stream);  // warm
-    HIP_OK(hipMemsetAsync(tr, 0, words * 8, e->stream));
-    upload_state_fields(e, st);
-    enqueue(run, e->stream);
-    HIP_OK(hipStreamSynchronize(e->stream));
-    std::vector<uint64_t> h(words);
-    HIP_OK(hipMemcpy(h.data(), tr, words * 8, hipMemcpyDeviceToHost));
-    (void)hipFree(tr);
-    upload_state_fields(e, saved);
+    (void)words;
     uint64_t t0 = ~0ull;
     for (int w = 0; w < grid; ++w) t0 = std::min(t0, h[(size_t)np * grid + w]);
     for (int p = 0; p < np && p < cap; ++p) {

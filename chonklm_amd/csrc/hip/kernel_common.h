@@ -122,7 +122,7 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 }
 
 __device__ __forceinline__ bool bit_test(const uint32_t* bits, uint32_t id) {
-  return (bits[id >> 5] >> (id & 31u)) & 1u;
+  return (*gbl(bits + (id >> 5)) >> (id & 31u)) & 1u;
 }
 
 __device__ __forceinline__ void st_relaxed(float* p, float v) {
@@ -478,7 +478,9 @@ __device__ __forceinline__ void v_walk(const void* tile, int hd, int d0, int pa,
 // partial in cpart: for head g at g * (hd + 2), [max, sum, acc[hd]].
 template <int G, bool KV16>
 __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv, int c, int pos,
-                                           uint4 (&kreg)[KV16 ? 8 : 16]) {
+                                           uint4 (&kreg)[KV16 ? 8 : 16], const float* inv_in = nullptr,
+                                           const float* qn_in = nullptr, const float* kn_in = nullptr,
+                                           void* vtile = nullptr) {
   const int hd = a.hd, half = hd / 2, CH = a.chunk;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -500,10 +502,15 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv,
   float* wml = wpart + 4 * G * hd;
   float* wts = wml + 8 * kMaxG;
   float* cpart = wts + G * ncp;
-  float* tile = cpart + attn_rowf(G, hd);
+  // the rotary table, norm weights and V rows come from sm, or from the
+  // caller's copies (the persistent step's prefetch slot)
+  float* tile = vtile ? (float*)vtile : cpart + attn_rowf(G, hd);
+  if (inv_in) inv = (float*)inv_in;
+  if (qn_in) qn = (float*)qn_in;
+  if (kn_in) kn = (float*)kn_in;
   const size_t head_base = (size_t)kv * a.ctx * hd;
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-  const int c_lo = start / CH, c_hi = pos / CH;
+  const int c_hi = pos / CH;
   const int p_begin = max(start - t_lo, 0);
   const int p_end = min(pos + 1 - t_lo, CH);
   const int p_new = pos - t_lo;

@@ -168,8 +168,55 @@ struct StepDebug {
   uint64_t start[1024];    // per-workgroup start time of the last step
 };
 
+// Wall-clock stamps per persistent-step task when tracing: matvec: start,
+// input arrived, prologue done, input quantized, dot products done, next slot
+// requested, epilogue stored, end; attention: start, input arrived, K rows
+// loaded, chunk done, next slot requested, partial stored or heads merged,
+// next slot requested (merging chunk), end.
+constexpr int kStepStamps = 8;
+
+// One task of a workgroup's list in the persistent step, resolved on the host
+// from the phase table: a matvec task carries its rows, the slot layout of
+// its weight rows and norm weights, the direct-to-LDS copies that fill that
+// slot and the addresses of its tagged inputs and outputs, so the device
+// reads one record per task instead of walking the phase's segments.
+enum StepTaskKind : int32_t {
+  STASK_MV = 0,    // matvec task whose rows and norm weights are in the slot
+  STASK_ATTN = 1,  // attention task (kv head, chunk) = (t / nchunk, t % nchunk)
+  STASK_LM = 2,    // lm_head task: rows streamed from memory, group argmax
+};
+struct StepDma {
+  const uint8_t* src;
+  int32_t dst, n16;  // slot offset, 16-byte units
+};
+constexpr int kStepMaxDma = 10;  // two norm weights + two matrices of up to four streams
+struct alignas(16) StepTask {
+  int32_t phase;         // index in the phase table; >= n_phases ends the list
+  int32_t t;             // task index within the phase
+  int32_t kind;          // StepTaskKind
+  int32_t type, uc, k, lpr;
+  int32_t t0, nt, glu;   // rows [t0, t0 + nt) of the segment
+  int32_t pro, epi;
+  int32_t res_lo, res_hi;  // residual slice stored by this task (PRO_EMBED_NORM / PRO_RES_NORM)
+  int32_t n_dma;
+  int32_t wn, wd;        // slot offsets of the norm weights (-1: none)
+  int32_t data[2][4];    // slot offset of row t0 of each (matrix, stream) (-1: none)
+  int32_t pad[3];
+  const tagged_t* in;    // [k] unless PRO_EMBED_NORM
+  const tagged_t* delta; // [k] for PRO_RES_NORM
+  const tagged_t* add;   // EPI_ADD: residual words of rows [t0, t0 + nt)
+  tagged_t* out;         // output words of rows [t0, t0 + nt)
+  tagged_t* res_out;     // residual words [k] (the task stores [res_lo, res_hi))
+  StepDma dma[kStepMaxDma];
+  int32_t pad2[2];
+};
+static_assert(sizeof(StepTask) == 320, "StepTask is copied in 16-byte units");
+constexpr int kStepDescRing = 8;  // task records a workgroup keeps in LDS (prefetched ahead)
+
 struct StepArgs {
   const StepPhase* phases;
+  const StepTask* tasks;   // [grid][task_stride]: each workgroup's tasks in order, then end records
+  int32_t task_stride;
   int32_t n_phases;
   int32_t logits;          // 1: the step ends with token selection
   DevState* st;
@@ -186,8 +233,82 @@ struct StepArgs {
   Candidate* cand;
   SelArgs sel;
   StepDebug* dbg;
-  uint64_t* trace;         // optional [n_phases + 1][grid] wall-clock stamps: phase ends, then start
+  uint64_t* trace;         // optional wall-clock stamps: [n_phases + 1][grid] phase ends, then start;
+                           // then [n_phases][grid][kStepStamps] per task (see k_step)
 };
+
+// Each task of the persistent step finds the inputs that do not depend on the
+// previous phases (norm weights, its weight rows, its K/V chunk) in an LDS
+// slot filled by direct-to-LDS loads issued during the workgroup's previous
+// task; two slots of kStepSlotBytes alternate.
+constexpr int kStepSlotBytes = 36 * 1024;
+
+// Bytes per row of stream s of a [N][K] matrix of `type` in the striped layout
+// (device_common.h); 0 for a stream the type does not use.
+__host__ __device__ constexpr int stripe_row_bytes(int type, int k, int s) {
+  switch (type) {
+    case QT_Q4_K: return s == 0 ? k / 2 : s == 1 ? k / 16 : 0;
+    case QT_Q5_K: return s == 0 ? k / 2 : s == 1 ? k / 16 : s == 2 ? k / 8 : 0;
+    case QT_Q6_K: return s == 0 ? k / 2 : s == 1 ? k / 4 : s == 2 ? k / 16 : k / 128;
+    case QT_Q8_0: return s == 0 ? k : s == 1 ? k / 16 : 0;
+    case QT_Q5_0: return s == 0 ? k / 2 : s == 1 ? k / 8 : s == 2 ? k / 16 : 0;
+    case QT_Q5_1: return s == 0 ? k / 2 : s == 1 ? k / 8 : k / 16;
+  }
+  return 0;
+}
+
+// Slot layout of a matvec task over rows [t0, t0 + nt) of a K-column matrix
+// (two matrices for GLU): the norm weights (K floats each) first, then each
+// stream's row range as a 16-byte-aligned copy. data[m][s] is the slot offset
+// of row t0's first byte of stream s of matrix m; returns the slot bytes used.
+struct MvSlot {
+  int wn, wd;        // norm weight / residual-norm weight offsets (-1: none)
+  int data[2][4];    // per matrix and stream: offset of row t0 (-1: none)
+  int dst[2][4];     // slot offset of the copy (16-aligned)
+  int src0[2][4];    // first byte (16-aligned) of the copied range within the stream
+  int n16[2][4];     // 16-byte units copied
+};
+__host__ __device__ inline int mv_slot_layout(int type, int k, int t0, int nt, int nmat, int n_norms, MvSlot* m) {
+  int off = 0;
+  m->wn = n_norms > 0 ? off : -1;
+  off += n_norms > 0 ? 4 * k : 0;
+  m->wd = n_norms > 1 ? off : -1;
+  off += n_norms > 1 ? 4 * k : 0;
+  for (int j = 0; j < 2; ++j)
+    for (int s = 0; s < 4; ++s) {
+      const int rb = stripe_row_bytes(type, k, s);
+      if (j >= nmat || rb == 0 || nt <= 0) {
+        m->data[j][s] = -1;
+        m->dst[j][s] = 0;
+        m->src0[j][s] = 0;
+        m->n16[j][s] = 0;
+        continue;
+      }
+      const int b0 = t0 * rb, b1 = (t0 + nt) * rb;
+      const int a0 = b0 & ~15, a1 = (b1 + 15) & ~15;
+      m->src0[j][s] = a0;
+      m->n16[j][s] = (a1 - a0) / 16;
+      m->dst[j][s] = off;
+      m->data[j][s] = off + (b0 - a0);
+      off += a1 - a0;
+    }
+  return off;
+}
+
+// Slot layout of an attention task: rotary inverse frequencies [hd/2], q / k
+// norm weights [hd] each, then K and V rows of the chunk indexed by chunk
+// position (only the positions the task reads are copied).
+struct AttnSlot {
+  int inv, qn, kn, k, v;
+};
+__host__ __device__ inline int attn_slot_layout(int hd, int chunk, int kv_elem, AttnSlot* s) {
+  s->inv = 0;
+  s->qn = (hd / 2 * 4 + 15) & ~15;
+  s->kn = s->qn + hd * 4;
+  s->k = s->kn + hd * 4;
+  s->v = s->k + chunk * hd * kv_elem;
+  return s->v + chunk * hd * kv_elem;
+}
 
 // Dynamic LDS bytes of the persistent step for this model.
 size_t step_shared_bytes(int max_k, int max_tile_rows, int group, int hd, int chunk, int nchunk, int kv_elem);

@@ -522,9 +522,8 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   DevState* st = a.st;
   const int kv = blockIdx.x, c = blockIdx.y;
   const int hd = a.hd, half = hd / 2, CH = a.chunk;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tpp = a.tpp, P = 64 / tpp;
+  const int tid = threadIdx.x;
+  const int tpp = a.tpp;
   const int my_p = tid / tpp, my_j = tid & (tpp - 1);
   const int dpt = hd / tpp;
   const int t_lo = c * CH;  // positions of this chunk: t_lo + p, p < CH
@@ -592,8 +591,6 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
   if (c < c_lo || c > c_hi) return;
   const int p_begin = max(start - t_lo, 0);  // valid positions: [p_begin, p_end)
   const int p_end = min(pos + 1 - t_lo, CH);
-  const int p_new = pos - t_lo;              // in range only in the last chunk
-  const bool own_new = (c == c_hi);
   if (!a.spec_kv) {
     load_chunk(p_begin, p_end);
     __builtin_amdgcn_s_waitcnt(0);

@@ -215,6 +215,13 @@ int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t r
  * lm_head), the time from the first workgroup's start to the last workgroup's
  * end of that phase, in microseconds (the step's state is restored). */
 int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases);
+/* Persistent step only: the raw wall-clock trace (100 MHz ticks) of one step:
+ * [n_phases + 1][n_wg] phase ends then workgroup starts, followed by
+ * [n_phases][n_wg][8] per task: start, input arrived, prologue done, input
+ * quantized, dot products done, next slot requested, epilogue stored, end
+ * (attention: start, input arrived, K rows loaded, chunk done, next slot
+ * requested, partial stored or heads merged, next slot requested, end). */
+int chonk_engine_profile_step_raw(chonk_engine* e, uint64_t* out, size_t cap, int32_t* n_phases, int32_t* n_wg);
 /* Writes `pos` synthetic positions into the K/V cache and sets the position,
  * so that long-context decode can be measured without a full prefill. */
 int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed);

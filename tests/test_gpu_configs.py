@@ -7,7 +7,8 @@
   tests/golden/make_config_golden.py (the oracle runs the reference's
   token-by-token loop, llama-wgsl-runtime.ts:242-314, in the build
   container; the fixture is keyed by the GGUF file's SHA-256).
-* Decode steps at the configurations' contexts against the oracle run live:
+* Decode steps at the configurations' contexts against the oracle run live,
+  through the per-phase graph and through the persistent step kernel:
   logits within 1e-3 (max |d| / max |ref|) and identical ids. The K/V cache
   holds the same synthetic positions on both sides (SmolLM2: the real prompt),
   so these steps run the kernels at their configuration geometry: decode
@@ -81,8 +82,16 @@ def test_config_generate_matches_golden(synth, name):
     loaded.engine.dispose()
 
 
+@pytest.fixture(params=["graph", "persistent"])
+def step_mode(request, monkeypatch):
+    """Both decode-step executions: the per-phase kernels replayed as one graph
+    (default) and the persistent step kernel (CHONK_STEP=1)."""
+    monkeypatch.setenv("CHONK_STEP", "1" if request.param == "persistent" else "0")
+    return request.param
+
+
 @pytest.mark.parametrize("name", CONFIGS)
-def test_config_steps_match_oracle(synth, name):
+def test_config_steps_match_oracle(synth, name, step_mode):
     w = WORKLOADS[name]
     path = synth(name)
     ctx = w.prompt_tokens + 16
@@ -90,6 +99,7 @@ def test_config_steps_match_oracle(synth, name):
     md.max_context = ctx
     loaded = load_llama_wgsl_model(md)
     eng = loaded.engine
+    assert eng.info["persistent_step"] == (1 if step_mode == "persistent" else 0)
     ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
     prompt = w.prompt(1234)
     samp = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, seed=9)
