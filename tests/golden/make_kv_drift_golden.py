@@ -7,7 +7,8 @@ build's default cache is fp16. For the Qwen3-0.6B Q4_K_M configuration
 loop twice in lockstep over the same token stream, once with an fp32 cache
 (the reference's semantics, whose choices drive the stream) and once with
 fp16 rounding on store. Every step records the fp32 run's token, its top-1 /
-top-2 logit margin, and the drift max|l16 - l32| / max|l32| of the logits.
+top-2 logit margin, the drift max|l16 - l32| / max|l32| of the logits, and
+whether the fp16 run picks the same token.
 
 Run: python tests/golden/make_kv_drift_golden.py   (~25 min on 8 cores)
 """

@@ -1,0 +1,91 @@
+"""The fp16 K/V cache against the reference's fp32 K/V at the configurations' contexts.
+
+The reference stores K and V in fp32 (llama-wgsl-runtime.ts:830-831); this
+build's cache is fp16 by default, fp32 on request. tests/golden/kv_drift_golden.json
+(written by tests/golden/make_kv_drift_golden.py) holds, for the Qwen3-0.6B
+Q4_K_M configuration (2048-token prompt, greedy) and the Gemma-3-270M Q4_K_M
+configuration (1024-token prompt, top-k 40 / T 0.8, seed 9), the token stream of
+the oracle run with an fp32 cache (the reference's semantics), the top-1/top-2
+logit margin at every step, the logit drift of an fp16-cache run fed the same
+stream and whether its pick agrees.
+
+On the GPU both caches are fed that stream (teacher forcing, so one divergent
+pick does not change the later contexts):
+
+* fp32 cache: every pick equals the fp32 oracle's (both configurations);
+* fp16 cache, greedy Qwen3: every pick of the 128 steps equals the fp32
+  oracle's, so the default cache reproduces the reference's greedy output at
+  2K context;
+* fp16 cache, sampled Gemma-3: the fp16 oracle itself picks differently from
+  the fp32 oracle at 3 of 128 steps. A sampled pick moves when a candidate
+  group's winner changes or when the draw sits near a cumulative-probability
+  boundary, both of which logits within the parity bar can cause, so the GPU's
+  fp16 picks are held to at most 3 + 2 disagreements with the fp32 oracle.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+from pathlib import Path
+
+import pytest
+
+from chonklm_amd import WORKLOADS, load_llama_wgsl_model
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "kv_drift_golden.json").read_text())
+
+
+def _sha256(path: str) -> str:
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for block in iter(lambda: f.read(1 << 22), b""):
+            h.update(block)
+    return h.hexdigest()
+
+
+def _stream_picks(synth, name: str, kv: str) -> tuple[list[int], dict]:
+    w = WORKLOADS[name]
+    path = synth(name)
+    g = GOLDEN[name]
+    if _sha256(path) != g["sha256"]:
+        pytest.fail(f"{name}: synthetic GGUF writer output changed; rerun tests/golden/make_kv_drift_golden.py")
+    ids = g["ids_fp32_kv"]
+    md = w.model_def(path, kv_dtype=kv)
+    md.max_context = w.prompt_tokens + len(ids) + 8
+    loaded = load_llama_wgsl_model(md)
+    eng = loaded.engine
+    prompt = w.prompt(g["prompt_seed"])
+    eng.prefill(prompt[:-1])
+    hist = list(prompt)
+    tok = prompt[-1]
+    picks = []
+    for want in ids:
+        picks.append(eng.run_token(tok, True, penalized_token_ids=hist, seen_ids=hist, **g["sampling"]))
+        tok = want  # the fp32 oracle's stream
+        hist.append(want)
+    eng.dispose()
+    return picks, g
+
+
+@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m"])
+def test_fp32_cache_follows_fp32_oracle(synth, name):
+    picks, g = _stream_picks(synth, name, "f32")
+    bad = [i for i, (a, b) in enumerate(zip(picks, g["ids_fp32_kv"])) if a != b]
+    assert not bad, (f"{name}: fp32-cache picks differ from the fp32 oracle at steps {bad[:8]} "
+                     f"(oracle margins there {[round(g['margins_fp32_kv'][i], 6) for i in bad[:8]]})")
+
+
+@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m"])
+def test_fp16_cache_drift_against_fp32_oracle(synth, name):
+    picks, g = _stream_picks(synth, name, "f16")
+    assert max(g["drift_fp16_vs_fp32"]) < 1e-3
+    bad = [i for i, (a, b) in enumerate(zip(picks, g["ids_fp32_kv"])) if a != b]
+    if g["sampling"]["temperature"] == 0:
+        assert all(g["same_token_fp16"])
+        assert not bad, f"{name}: greedy picks with the fp16 cache differ from the fp32 reference at steps {bad[:8]}"
+    else:
+        oracle_flips = sum(not x for x in g["same_token_fp16"])
+        assert len(bad) <= oracle_flips + 2, (f"{name}: fp16-cache picks differ from the fp32 oracle at {len(bad)} "
+                                              f"steps {bad[:8]} (the fp16 oracle at {oracle_flips})")
