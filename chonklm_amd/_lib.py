@@ -106,6 +106,9 @@ class SynthConfigC(C.Structure):
         ("seed", C.c_uint64),
         ("weight_std", C.c_float),
         ("norm_std", C.c_float),
+        ("layer_heads", C.POINTER(C.c_int32)),
+        ("layer_kv_heads", C.POINTER(C.c_int32)),
+        ("layer_ffn", C.POINTER(C.c_int32)),
     ]
 
 

@@ -171,11 +171,14 @@ struct TensorRef {
 struct LayerCfg {
   uint32_t theta = 10000;
   int window = 0;
+  int heads = 0, kv_heads = 0, ffn = 0;  // openelm varies them per layer
 };
 
 struct ModelCfg {
   std::string arch;
   bool gemma = false, interleaved = false, qk_norm = false;
+  bool openelm = false;  // fused attn_qkv, per-layer heads / kv heads / feed-forward width
+  int gmax = 1;          // largest GQA group of any layer
   bool gpt = false;  // GGUF architecture gpt2: the reference's GPT runtime (gpt-wgsl-runtime.ts)
   int pos_rows = 0;  // gpt2: rows of the learned position table (gpt2.context_length)
   int hidden = 0, ffn = 0, vocab = 0, layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
@@ -190,13 +193,24 @@ double meta_number(const GgufFile& g, const std::string& key, const double* fall
   throw Error(CHONK_EINVAL, "GGUF metadata " + key + " is missing or not numeric");
 }
 
+// A numeric array of metadata (ggufNumberArray, llama-wgsl-runtime.ts:474-486).
+std::vector<int> meta_array(const GgufFile& g, const std::string& key) {
+  const GgufValue* v = g.value(key);
+  if (!v || v->type != GV_ARRAY) throw Error(CHONK_EINVAL, "GGUF metadata " + key + " is missing or not a numeric array");
+  std::vector<int> out;
+  for (size_t i = 0; i < v->array.size(); ++i) {
+    if (!v->array[i].is_number())
+      throw Error(CHONK_EINVAL, "GGUF metadata " + key + "[" + std::to_string(i) + "] is not numeric");
+    out.push_back((int)v->array[i].number);
+  }
+  return out;
+}
+
 ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
   ModelCfg c;
   const GgufValue* a = g.value("general.architecture");
   if (!a || a->type != GV_STRING) throw Error(CHONK_EINVAL, "GGUF metadata general.architecture is missing or not a string");
   c.arch = a->str;
-  if (c.arch == "openelm")
-    throw Error(CHONK_EINVAL, "architecture openelm (fused qkv, per-layer heads) is not supported by this engine yet");
   if (c.arch == "gpt2") {
     // manifestFromGguf (gpt-wgsl-runtime.ts:274-356)
     c.gpt = true;
@@ -220,21 +234,34 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
       throw Error(CHONK_EINVAL, "GPT WGSL argmax supports at most 65536 vocab entries, got " + std::to_string(c.vocab));
     c.ctx = std::min(def.max_context, c.pos_rows);
     c.scale = (float)(1.0 / std::sqrt((double)c.hd));  // INV_SQRT_HEAD_DIM (:1066)
-    c.layer.assign(c.layers, LayerCfg{0, 0});           // no rotary embedding
+    c.layer.assign(c.layers, LayerCfg{0, 0, c.heads, c.kv_heads, c.ffn});  // no rotary embedding
     if (c.layers <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
       throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
     return c;
   }
-  if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3")
+  if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3" && c.arch != "openelm")
     throw Error(CHONK_EINVAL, "Llama GGUF WGSL does not support architecture " + c.arch);
   c.gemma = c.arch == "gemma3";
+  c.openelm = c.arch == "openelm";
   c.interleaved = c.arch == "llama";
   const std::string p = c.arch + ".";
   c.layers = (int)meta_number(g, p + "block_count", nullptr);
   c.hidden = (int)meta_number(g, p + "embedding_length", nullptr);
-  c.heads = (int)meta_number(g, p + "attention.head_count", nullptr);
-  c.kv_heads = (int)meta_number(g, p + "attention.head_count_kv", nullptr);
-  c.ffn = (int)meta_number(g, p + "feed_forward_length", nullptr);
+  // openelm: per-layer arrays, the scalars are their maxima (buildGgufLlamaManifest, :373-380)
+  std::vector<int> lh, lkv, lff;
+  if (c.openelm) {
+    lh = meta_array(g, p + "attention.head_count");
+    lkv = meta_array(g, p + "attention.head_count_kv");
+    lff = meta_array(g, p + "feed_forward_length");
+    if (lh.empty() || lkv.empty() || lff.empty()) throw Error(CHONK_EINVAL, "openelm per-layer metadata arrays are empty");
+    c.heads = *std::max_element(lh.begin(), lh.end());
+    c.kv_heads = *std::max_element(lkv.begin(), lkv.end());
+    c.ffn = *std::max_element(lff.begin(), lff.end());
+  } else {
+    c.heads = (int)meta_number(g, p + "attention.head_count", nullptr);
+    c.kv_heads = (int)meta_number(g, p + "attention.head_count_kv", nullptr);
+    c.ffn = (int)meta_number(g, p + "feed_forward_length", nullptr);
+  }
   const double hd_default = std::floor((double)c.hidden / std::max(1, c.heads));
   c.hd = (int)meta_number(g, p + "attention.key_length", &hd_default);
   c.vocab = def.vocab;
@@ -251,18 +278,33 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
   const double theta = c.gemma ? 10000.0 : meta_number(g, p + "rope.freq_base", &theta_default);
   const double gtheta = c.gemma ? meta_number(g, "gemma3.rope.freq_base", &gtheta_default) : 0;
   const int window = c.gemma ? (int)meta_number(g, "gemma3.attention.sliding_window", &win_default) : 0;
+  // validateLayerArray (:1815-1821)
+  for (const auto* v : {&lh, &lkv, &lff})
+    if (c.openelm && (int)v->size() != c.layers)
+      throw Error(CHONK_EINVAL, "Llama WGSL manifest layer array length " + std::to_string(v->size()) + " != layers " +
+                                    std::to_string(c.layers));
   for (int i = 0; i < c.layers; ++i) {
     LayerCfg L;
     const double th = c.gemma ? (i % 6 == 5 ? gtheta : 10000.0) : theta;
     L.theta = (uint32_t)std::llround(th);
     L.window = c.gemma ? (i % 6 == 5 ? 0 : window) : 0;
+    L.heads = c.openelm ? lh[(size_t)i] : c.heads;
+    L.kv_heads = c.openelm ? lkv[(size_t)i] : c.kv_heads;
+    L.ffn = c.openelm ? lff[(size_t)i] : c.ffn;
     c.layer.push_back(L);
   }
   // limits of this engine's kernels
   if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
     throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
-  if (c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8)
-    throw Error(CHONK_EINVAL, "GQA group size must divide heads and be at most 8");
+  for (const LayerCfg& L : c.layer) {
+    if (L.heads <= 0 || L.kv_heads <= 0 || L.ffn <= 0)
+      throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+    if (L.heads % L.kv_heads != 0 || L.heads / L.kv_heads > 8)
+      throw Error(CHONK_EINVAL, "GQA group size must divide heads and be at most 8");
+    c.gmax = std::max(c.gmax, L.heads / L.kv_heads);
+  }
+  // the packed q|k|v path normalises q and k (llama-wgsl-runtime.ts:1071-1084)
+  if (c.openelm && !c.qk_norm) throw Error(CHONK_EINVAL, "Llama WGSL layer is missing attention projection weights");
   if (c.hd != 32 && c.hd != 64 && c.hd != 128 && c.hd != 256)
     throw Error(CHONK_EINVAL, "head_dim " + std::to_string(c.hd) + " is not supported (32, 64, 128 or 256)");
   if ((c.vocab + 255) / 256 > 4096) throw Error(CHONK_EINVAL, "vocab above 1048576 is not supported");
@@ -666,7 +708,7 @@ const float2* rope_cs_table(chonk_engine* e, uint32_t theta, int hd) {
 
 void build_steps(chonk_engine* e) {
   const ModelCfg& c = e->cfg;
-  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, G = c.heads / c.kv_heads;
+  const int H = c.hidden;
   auto mv_base = [&]() {
     MvArgs a{};
     a.st = e->st;
@@ -692,6 +734,8 @@ void build_steps(chonk_engine* e) {
   for (int i = 0; i < c.layers; ++i) {
     LayerDev& Ld = e->layers[i];
     const std::string li = "L" + std::to_string(i) + ".";
+    const LayerCfg& lc = c.layer[i];
+    const int qdim = lc.heads * c.hd, kvdim = lc.kv_heads * c.hd, G = lc.heads / lc.kv_heads;
     // qkv (gpt2: one fused matrix with bias, LayerNorm prologue; embedding +
     // position on layer 0)
     if (c.gpt) {
@@ -722,13 +766,20 @@ void build_steps(chonk_engine* e) {
       Launch L;
       MvArgs a = mv_base();
       a.k = H;
-      a.nseg = 3;
-      plan_seg(a.seg[0], Ld.q.q, qdim, false, 0);
-      a.seg[0].out = e->qkv;
-      plan_seg(a.seg[1], Ld.k.q, kvdim, false, seg_wgs(a.seg[0]));
-      a.seg[1].out = e->qkv + qdim;
-      plan_seg(a.seg[2], Ld.v.q, kvdim, false, a.seg[1].wg_begin + seg_wgs(a.seg[1]));
-      a.seg[2].out = e->qkv + qdim + kvdim;
+      if (c.openelm) {
+        // one fused matrix whose rows are q | k | v (attn.qkv_proj, :359, :1071-1074)
+        a.nseg = 1;
+        plan_seg(a.seg[0], Ld.qkv.q, qdim + 2 * kvdim, false, 0);
+        a.seg[0].out = e->qkv;
+      } else {
+        a.nseg = 3;
+        plan_seg(a.seg[0], Ld.q.q, qdim, false, 0);
+        a.seg[0].out = e->qkv;
+        plan_seg(a.seg[1], Ld.k.q, kvdim, false, seg_wgs(a.seg[0]));
+        a.seg[1].out = e->qkv + qdim;
+        plan_seg(a.seg[2], Ld.v.q, kvdim, false, a.seg[1].wg_begin + seg_wgs(a.seg[1]));
+        a.seg[2].out = e->qkv + qdim + kvdim;
+      }
       a.epi = EPI_STORE;
       a.w_norm = Ld.in_norm;
       if (i == 0) {
@@ -744,9 +795,12 @@ void build_steps(chonk_engine* e) {
         a.pro = PRO_NORM;
         a.in = e->resA;
       }
-      finish(L, a, std::max(a.seg[0].tile, std::max(a.seg[1].tile, a.seg[2].tile)));
+      int max_tile = 0;
+      for (int si = 0; si < a.nseg; ++si) max_tile = std::max(max_tile, a.seg[si].tile);
+      finish(L, a, max_tile);
       L.name = li + "qkv";
-      L.weight_bytes = Ld.q.gguf_bytes + Ld.k.gguf_bytes + Ld.v.gguf_bytes + (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
+      L.weight_bytes = Ld.q.gguf_bytes + Ld.k.gguf_bytes + Ld.v.gguf_bytes + Ld.qkv.gguf_bytes +
+                       (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
       L.layer = i;
       steps.push_back(L);
     }
@@ -764,8 +818,8 @@ void build_steps(chonk_engine* e) {
       t.cnt = e->cnt;
       t.out = e->attn;
       t.st = e->st;
-      t.heads = c.heads;
-      t.kv_heads = c.kv_heads;
+      t.heads = lc.heads;
+      t.kv_heads = lc.kv_heads;
       t.hd = c.hd;
       t.ctx = c.ctx;
       t.window = c.layer[i].window;
@@ -783,7 +837,7 @@ void build_steps(chonk_engine* e) {
       t.spec_kv = (t.window == 0 && c.ctx <= 4096) ? 1 : 0;
       t.tpp = attn_threads_per_position(c.hd, e->chunk, (int)e->kv_elem);
       L.shmem = attn_shared_bytes(G, c.hd, e->chunk, e->nchunk, e->kv_elem);
-      L.grid = c.kv_heads * e->nchunk;
+      L.grid = lc.kv_heads * e->nchunk;
       if (e->dec_attn) {
         t.variant = 1;
         t.tpart = e->dpart;
@@ -792,7 +846,7 @@ void build_steps(chonk_engine* e) {
         t.nchunk = e->dnchunk;
         t.merge_floats = attn_merge_floats(G, c.hd, e->dnchunk);
         L.shmem = attn_dec_shared_bytes(G, c.hd, e->dnchunk);
-        L.grid = c.kv_heads * e->dnchunk;
+        L.grid = lc.kv_heads * e->dnchunk;
       }
       L.name = li + "attn";
       L.layer = i;
@@ -831,7 +885,7 @@ void build_steps(chonk_engine* e) {
       MvArgs a = mv_base();
       a.k = H;
       a.nseg = 1;
-      plan_seg(a.seg[0], Ld.up.q, c.ffn, false, 0);
+      plan_seg(a.seg[0], Ld.up.q, lc.ffn, false, 0);
       a.seg[0].out = e->ff;
       a.seg[0].bias = Ld.up_b;
       a.epi = EPI_GELU;
@@ -849,7 +903,7 @@ void build_steps(chonk_engine* e) {
       MvArgs a = mv_base();
       a.k = H;
       a.nseg = 1;
-      plan_seg(a.seg[0], Ld.gate.q, c.ffn, true, 0);
+      plan_seg(a.seg[0], Ld.gate.q, lc.ffn, true, 0);
       a.seg[0].w2 = Ld.up.q;
       a.seg[0].out = e->ff;
       a.epi = c.gemma ? EPI_GLU_GELU : EPI_GLU_SILU;
@@ -875,7 +929,7 @@ void build_steps(chonk_engine* e) {
     {
       Launch L;
       MvArgs a = mv_base();
-      a.k = c.ffn;
+      a.k = lc.ffn;
       a.nseg = 1;
       plan_seg(a.seg[0], Ld.down.q, H, false, 0);
       a.pro = PRO_PLAIN;
@@ -967,6 +1021,7 @@ bool build_step(chonk_engine* e) {
   const int G = c.heads / c.kv_heads;
   const bool kv16 = e->kv_elem == 2;
   if (c.gpt) return false;  // the persistent step runs the llama-family layer only
+  if (c.openelm) return false;  // and one head geometry for every layer
   if (!step_supported(G, kv16)) return false;
   int cus = 0;
   HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
@@ -1409,13 +1464,19 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   }
   for (int i = 0; i < (c.gpt ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
-    mat_bytes(p + "attn_q.weight", H, qdim);
-    mat_bytes(p + "attn_k.weight", H, kvdim);
-    mat_bytes(p + "attn_v.weight", H, kvdim);
-    mat_bytes(p + "attn_output.weight", qdim, H);
-    mat_bytes(p + "ffn_gate.weight", H, c.ffn);
-    mat_bytes(p + "ffn_up.weight", H, c.ffn);
-    mat_bytes(p + "ffn_down.weight", c.ffn, H);
+    const LayerCfg& lc = c.layer[i];
+    const int lq = lc.heads * c.hd, lkv = lc.kv_heads * c.hd;
+    if (c.openelm) {
+      mat_bytes(p + "attn_qkv.weight", H, lq + 2 * lkv);
+    } else {
+      mat_bytes(p + "attn_q.weight", H, lq);
+      mat_bytes(p + "attn_k.weight", H, lkv);
+      mat_bytes(p + "attn_v.weight", H, lkv);
+    }
+    mat_bytes(p + "attn_output.weight", lq, H);
+    mat_bytes(p + "ffn_gate.weight", H, lc.ffn);
+    mat_bytes(p + "ffn_up.weight", H, lc.ffn);
+    mat_bytes(p + "ffn_down.weight", lc.ffn, H);
     vec_bytes(H);
     vec_bytes(H);
     if (c.gemma) {
@@ -1444,17 +1505,20 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     if (v >= 16 && v <= attn_max_chunk(c.hd) && (v & (v - 1)) == 0) e->chunk = v;
   }
   e->nchunk = (c.ctx + e->chunk - 1) / e->chunk;
-  const int G = c.heads / c.kv_heads;
-  // the register-resident decode attention where it applies; CHONK_ATTN=chunked
-  // keeps k_attention
+  const int G = c.gmax;  // partial rows are sized for the largest group
+  // the register-resident decode attention where it applies (every layer's
+  // group); CHONK_ATTN=chunked keeps k_attention
   {
     const char* av = std::getenv("CHONK_ATTN");
-    e->dec_attn = attn_dec_supported(G, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) &&
-                  !(av && std::strcmp(av, "chunked") == 0);
+    e->dec_attn = !(av && std::strcmp(av, "chunked") == 0);
     e->dnchunk = (c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk();
-    if (e->dec_attn &&
-        attn_dec_resident(e->device, G, c.hd, attn_dec_shared_bytes(G, c.hd, e->dnchunk)) < c.kv_heads * e->dnchunk)
-      e->dec_attn = false;
+    for (const LayerCfg& lc : c.layer) {
+      const int lg = lc.heads / lc.kv_heads;
+      if (e->dec_attn && (!attn_dec_supported(lg, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) ||
+                          attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, e->dnchunk)) <
+                              lc.kv_heads * e->dnchunk))
+        e->dec_attn = false;
+    }
   }
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
@@ -1509,13 +1573,19 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       L.q_norm = upload_floats(e->weights, *src, g, p + "attn_q_norm.weight", c.hd);
       L.k_norm = upload_floats(e->weights, *src, g, p + "attn_k_norm.weight", c.hd);
     }
-    L.q = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_q.weight"), H, qdim);
-    L.k = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_k.weight"), H, kvdim);
-    L.v = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_v.weight"), H, kvdim);
-    L.o = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_output.weight"), qdim, H);
-    L.gate = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_gate.weight"), H, c.ffn);
-    L.up = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_up.weight"), H, c.ffn);
-    L.down = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_down.weight"), c.ffn, H);
+    const LayerCfg& lc = c.layer[i];
+    const int lq = lc.heads * c.hd, lkv = lc.kv_heads * c.hd;
+    if (c.openelm) {
+      L.qkv = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_qkv.weight"), H, lq + 2 * lkv);
+    } else {
+      L.q = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_q.weight"), H, lq);
+      L.k = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_k.weight"), H, lkv);
+      L.v = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_v.weight"), H, lkv);
+    }
+    L.o = upload_matrix(e->weights, *src, g, tensor(g, p + "attn_output.weight"), lq, H);
+    L.gate = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_gate.weight"), H, lc.ffn);
+    L.up = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_up.weight"), H, lc.ffn);
+    L.down = upload_matrix(e->weights, *src, g, tensor(g, p + "ffn_down.weight"), lc.ffn, H);
     if (L.gate.q.type != L.up.q.type)
       throw Error(CHONK_EINVAL, "ffn_gate and ffn_up of layer " + std::to_string(i) + " have different types");
     L.kc = e->state.take(kv_bytes);
@@ -1802,8 +1872,7 @@ struct RowPlace {
 void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlace& pl, int T, float* logits, int lr0,
               int nlr, hipStream_t s) {
   const ModelCfg& c = e->cfg;
-  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn;
-  const int ldqkv = qdim + 2 * kvdim;
+  const int H = c.hidden;
   // split of x into the GEMM operand planes, after the pending residual update
   // (x += add, or the Gemma-3 sandwich with add_w) when add.p is set
   auto split = [&](const float* x, int ld, int k, const float* w, int rows, PartSum add, const float* add_w) {
@@ -1850,24 +1919,36 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     return k;
   };
   const int64_t P = b.part_cap;
-  // the partial-sum buffer shared out in proportion to each result's size
-  const int64_t pq = P * qdim / ldqkv, pk = P * kvdim / ldqkv;
   HIP_OK(launch_pf_embed(e->embed.q, b.tok, c.embed_scale, H, b.x, T, s));
   PartSum pending{};                // the previous layer's ffn_down, not yet added to x
   const float* pending_w = nullptr; // its Gemma-3 post-ffn norm
   for (int i = 0; i < c.layers; ++i) {
     const LayerDev& L = e->layers[i];
+    const LayerCfg& lc = c.layer[i];
+    const int qdim = lc.heads * c.hd, kvdim = lc.kv_heads * c.hd, F = lc.ffn;
+    const int ldqkv = qdim + 2 * kvdim;
     split(b.x, H, H, L.in_norm, T, pending, pending_w);
     pending = PartSum{};
     PfRopeArgs r{};
-    r.pq = gemm(L.q, T, 0, pq);
-    r.pk = gemm(L.k, T, pq, pk);
-    r.pv = gemm(L.v, T, pq + pk, P - pq - pk);
+    if (c.openelm) {
+      // one fused q|k|v result; k and v are column ranges of it
+      r.pq = gemm(L.qkv, T, 0, P);
+      r.pk = r.pq;
+      r.pk.p += qdim;
+      r.pv = r.pq;
+      r.pv.p += qdim + kvdim;
+    } else {
+      // the partial-sum buffer shared out in proportion to each result's size
+      const int64_t pq = P * qdim / ldqkv, pk = P * kvdim / ldqkv;
+      r.pq = gemm(L.q, T, 0, pq);
+      r.pk = gemm(L.k, T, pq, pk);
+      r.pv = gemm(L.v, T, pq + pk, P - pq - pk);
+    }
     r.qkv = b.qkv;
     r.ld = ldqkv;
     r.hd = c.hd;
-    r.heads = c.heads;
-    r.kv_heads = c.kv_heads;
+    r.heads = lc.heads;
+    r.kv_heads = lc.kv_heads;
     r.interleaved = c.interleaved ? 1 : 0;
     r.kv16 = e->kv_elem == 2 ? 1 : 0;
     r.qn_w = c.qk_norm ? L.q_norm : nullptr;
@@ -1882,14 +1963,14 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     at.ld = ldqkv;
     at.out = b.att;
     at.ldo = qdim;
-    at.heads = c.heads;
-    at.kv_heads = c.kv_heads;
+    at.heads = lc.heads;
+    at.kv_heads = lc.kv_heads;
     at.hd = c.hd;
     at.window = c.layer[i].window;
     at.kv16 = r.kv16;
     at.scale = c.scale;
     at.kv = r.kv;
-    if (pl.row_seq && c.hd >= 64 && c.heads / c.kv_heads <= 8 && kvs.max_pages <= 64)
+    if (pl.row_seq && c.hd >= 64 && lc.heads / lc.kv_heads <= 8 && kvs.max_pages <= 64)
       HIP_OK(launch_bd_attn(at, T, b.part, P, s));
     else
       HIP_OK(launch_pf_attn(at, T, s));
@@ -2349,7 +2430,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->kv_heads = c.kv_heads;
   out->head_dim = c.hd;
   out->context = c.ctx;
-  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : 3;
+  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : c.arch == "gpt2" ? 3 : 4;
   out->qk_norm = c.qk_norm;
   out->interleaved_rope = c.interleaved;
   out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;
@@ -2556,7 +2637,7 @@ int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed) {
     const ModelCfg& c = e->cfg;
     if (pos < 0 || pos >= c.ctx) throw Error(CHONK_EINVAL, "position outside the context");
     for (int i = 0; i < c.layers; ++i)
-      HIP_OK(launch_fill_kv(e->layers[i].kc, e->layers[i].vc, c.kv_heads, c.ctx, c.hd, pos, e->kv_elem == 2,
+      HIP_OK(launch_fill_kv(e->layers[i].kc, e->layers[i].vc, c.layer[i].kv_heads, c.ctx, c.hd, pos, e->kv_elem == 2,
                             seed + 1000003ull * i, e->stream));
     DevState st{};
     st.pos = pos;
@@ -2672,8 +2753,9 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
         const int pos = e->pos;
         const int w = L.at.window;
         const int start = (w != 0 && pos + 1 > w) ? pos + 1 - w : 0;
-        by += 2ull * c.kv_heads * c.hd * (uint64_t)(pos + 1 - start) * e->kv_elem;
-        by += (uint64_t)(c.heads + 2 * c.kv_heads) * c.hd * 4 + (uint64_t)c.heads * c.hd * 4;
+        const uint64_t nh = (uint64_t)L.at.heads, nkv = (uint64_t)L.at.kv_heads;
+        by += 2ull * nkv * c.hd * (uint64_t)(pos + 1 - start) * e->kv_elem;
+        by += (nh + 2 * nkv) * c.hd * 4 + nh * c.hd * 4;
       }
       *bytes = by;
     }
@@ -2959,6 +3041,11 @@ int chonk_write_synthetic_gguf(const chonk_synth_config* c, const char* path, in
     s.seed = c->seed;
     s.weight_std = c->weight_std > 0 ? c->weight_std : 0.02f;
     s.norm_std = c->norm_std > 0 ? c->norm_std : 0.02f;
+    if (c->layers > 0) {
+      if (c->layer_heads) s.layer_heads.assign(c->layer_heads, c->layer_heads + c->layers);
+      if (c->layer_kv_heads) s.layer_kv_heads.assign(c->layer_kv_heads, c->layer_kv_heads + c->layers);
+      if (c->layer_ffn) s.layer_ffn.assign(c->layer_ffn, c->layer_ffn + c->layers);
+    }
     try {
       write_synthetic_gguf(s, path, n_threads);
     } catch (const std::exception& x) {
@@ -3018,6 +3105,7 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
   if (c.gpt) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not gpt2");
   if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
   if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
+  if (c.openelm) throw Error(CHONK_EINVAL, "batched decoding needs one head geometry for every layer (not openelm)");
   std::unique_ptr<chonk_batch, void (*)(chonk_batch*)> b(new chonk_batch(), batch_free);
   b->e = e;
   b->max_seqs = max_seqs;

@@ -1,5 +1,5 @@
 // Reference (non-imatrix) GGUF block quantizers used to build synthetic
-// models: Q8_0, Q5_0, Q5_1, Q4_K and Q6_K.
+// models: Q8_0, Q5_0, Q5_1, Q4_K, Q5_K and Q6_K.
 //
 // These restate the published algorithm of llama.cpp's ggml-quants.c
 // (quantize_row_*_ref, make_qkx2_quants, make_qx_quants, nearest_int) in code
@@ -284,6 +284,72 @@ void quant_q4_k(const float* x, uint8_t* y, int64_t nblocks) {
   }
 }
 
+// Q5_K: Q4_K's super-block with 5-bit values (0..31), the fifth bits in
+// qh[32]: value 32n + j of the 64-value group n sets bit 2n of qh[j], value
+// 32n + 32 + j bit 2n + 1; block d, dmin, scales[12], qh[32], qs[128].
+void quant_q5_k(const float* x, uint8_t* y, int64_t nblocks) {
+  uint8_t L[256], Laux[32];
+  float weights[32], mins[8], scales[8];
+  for (int64_t b = 0; b < nblocks; ++b, x += 256, y += 176) {
+    uint8_t* sc = y + 4;
+    uint8_t* qh = y + 16;
+    uint8_t* qs = y + 48;
+    std::memset(y, 0, 176);
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+      float sum_x2 = 0;
+      for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+      const float av_x = std::sqrt(sum_x2 / 32);
+      for (int l = 0; l < 32; ++l) weights[l] = av_x + std::fabs(x[32 * j + l]);
+      scales[j] = fit_scale_min(32, 31, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15);
+      if (scales[j] > max_scale) max_scale = scales[j];
+      if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    for (int j = 0; j < 8; ++j) {
+      uint8_t ls = (uint8_t)std::min(63, nearest_int(inv_scale * scales[j]));
+      uint8_t lm = (uint8_t)std::min(63, nearest_int(inv_min * mins[j]));
+      if (j < 4) {
+        sc[j] = ls;
+        sc[j + 4] = lm;
+      } else {
+        sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+        sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+        sc[j - 0] |= (uint8_t)((lm >> 4) << 6);
+      }
+    }
+    put_f16(y, max_scale / 63.f);
+    put_f16(y + 2, max_min / 63.f);
+    const float dd = get_f16(y), dmn = get_f16(y + 2);
+    for (int j = 0; j < 8; ++j) {
+      uint8_t s, m;
+      scale_min_k4(j, sc, &s, &m);
+      const float d = dd * s;
+      if (!d) continue;
+      const float dm = dmn * m;
+      for (int ii = 0; ii < 32; ++ii) {
+        int l = nearest_int((x[32 * j + ii] + dm) / d);
+        L[32 * j + ii] = (uint8_t)std::max(0, std::min(31, l));
+      }
+    }
+    for (int n = 0; n < 4; ++n) {
+      for (int j = 0; j < 32; ++j) {
+        int l1 = L[64 * n + j], l2 = L[64 * n + j + 32];
+        if (l1 > 15) {
+          l1 -= 16;
+          qh[j] |= (uint8_t)(1u << (2 * n));
+        }
+        if (l2 > 15) {
+          l2 -= 16;
+          qh[j] |= (uint8_t)(2u << (2 * n));
+        }
+        qs[32 * n + j] = (uint8_t)(l1 | (l2 << 4));
+      }
+    }
+  }
+}
+
 void quant_q6_k(const float* x, uint8_t* y, int64_t nblocks) {
   int8_t L[256];
   float scales[16];
@@ -353,6 +419,7 @@ bool quantize_rows(uint32_t type, const float* src, uint8_t* dst, int64_t n_elem
     case GGML_Q5_0: quant_q5_0(src, dst, nb); return true;
     case GGML_Q5_1: quant_q5_1(src, dst, nb); return true;
     case GGML_Q4_K: quant_q4_k(src, dst, nb); return true;
+    case GGML_Q5_K: quant_q5_k(src, dst, nb); return true;
     case GGML_Q6_K: quant_q6_k(src, dst, nb); return true;
     default: return false;  // Q5_K: decode-only here
   }

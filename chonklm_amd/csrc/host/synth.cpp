@@ -9,7 +9,9 @@
 //   <arch>.{block_count, embedding_length, feed_forward_length,
 //   attention.head_count, attention.head_count_kv, attention.key_length,
 //   context_length, rope.freq_base, attention.layer_norm_rms_epsilon},
-//   gemma3.attention.sliding_window.
+//   gemma3.attention.sliding_window. Architecture openelm has one fused
+//   blk.N.attn_qkv per layer (rows q | k | v) and per-layer head, kv-head and
+//   feed-forward counts as metadata arrays (:331-416).
 // Type recipe (Q4_K_M): llama.cpp's llama_tensor_get_type as restated in the
 // header of synth.h. Architecture gpt2 follows the GPT runtime's manifest
 // (src/lib/gpt-wgsl-runtime.ts:274-356; gpt2_plan below).
@@ -89,6 +91,8 @@ uint32_t recipe_tensor_type(const std::string& recipe, const std::string& role, 
     t = row_len % 256 != 0 ? GGML_Q8_0 : GGML_Q6_K;
   } else if (role == "attn_v" || role == "ffn_down") {
     if (use_more_bits(layer, n_layers)) t = GGML_Q6_K;
+  } else if (role == "attn_qkv") {
+    t = GGML_Q5_K;
   }
   return fallback_type(t, row_len);
 }
@@ -129,16 +133,29 @@ std::vector<TensorPlan> gpt2_plan(const SynthConfig& c) {
 
 void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_threads) {
   const std::string& a = c.arch;
-  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2")
+  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2" && a != "openelm")
     throw std::runtime_error("synthetic writer: unsupported arch " + a);
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0)
     throw std::runtime_error("synthetic writer: non-positive dimension");
-  if (c.heads % c.kv_heads != 0) throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
+  const bool openelm = a == "openelm";
+  auto per_layer = [&](const std::vector<int>& v, int fallback, const char* what) {
+    if (v.empty()) return std::vector<int>((size_t)c.layers, fallback);
+    if (!openelm) throw std::runtime_error(std::string("synthetic writer: per-layer ") + what + " needs arch openelm");
+    if ((int)v.size() != c.layers) throw std::runtime_error(std::string("synthetic writer: ") + what + " length != layers");
+    for (int x : v)
+      if (x <= 0) throw std::runtime_error("synthetic writer: non-positive dimension");
+    return v;
+  };
+  const std::vector<int> lh = per_layer(c.layer_heads, c.heads, "heads");
+  const std::vector<int> lkv = per_layer(c.layer_kv_heads, c.kv_heads, "kv_heads");
+  const std::vector<int> lff = per_layer(c.layer_ffn, c.ffn, "ffn");
+  for (int i = 0; i < c.layers; ++i)
+    if (lh[(size_t)i] % lkv[(size_t)i] != 0) throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
+  if (openelm && c.head_dim <= 0) throw std::runtime_error("synthetic writer: openelm needs head_dim");
   const int head_dim = c.head_dim > 0 ? c.head_dim : c.hidden / c.heads;
-  const uint64_t H = (uint64_t)c.hidden, F = (uint64_t)c.ffn;
-  const uint64_t qdim = (uint64_t)c.heads * head_dim, kvdim = (uint64_t)c.kv_heads * head_dim;
+  const uint64_t H = (uint64_t)c.hidden;
   const bool gemma = a == "gemma3";
-  const bool qk_norm = a == "qwen3" || gemma;
+  const bool qk_norm = a == "qwen3" || gemma || openelm;
   const float w_std = c.weight_std;
   const float n_std = c.norm_std;
 
@@ -153,10 +170,16 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
       plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f, w_std});
     };
     auto norm = [&](const std::string& role, uint64_t n) { plan.push_back({p + role + ".weight", 1, n, GGML_F32, 1.f, n_std}); };
+    const uint64_t qdim = (uint64_t)lh[(size_t)i] * head_dim, kvdim = (uint64_t)lkv[(size_t)i] * head_dim;
+    const uint64_t F = (uint64_t)lff[(size_t)i];
     norm("attn_norm", H);
-    lin("attn_q", qdim, H);
-    lin("attn_k", kvdim, H);
-    lin("attn_v", kvdim, H);
+    if (openelm) {
+      lin("attn_qkv", qdim + 2 * kvdim, H);
+    } else {
+      lin("attn_q", qdim, H);
+      lin("attn_k", kvdim, H);
+      lin("attn_v", kvdim, H);
+    }
     lin("attn_output", H, qdim);
     if (qk_norm) {
       norm("attn_q_norm", (uint64_t)head_dim);
@@ -178,10 +201,17 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
   w.set_u32(a + ".context_length", (uint32_t)c.context_length);
   w.set_u32(a + ".embedding_length", (uint32_t)c.hidden);
   w.set_u32(a + ".block_count", (uint32_t)c.layers);
-  w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
-  w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
+  if (openelm) {
+    auto u32s = [](const std::vector<int>& v) { return std::vector<uint32_t>(v.begin(), v.end()); };
+    w.set_u32_array(a + ".feed_forward_length", u32s(lff));
+    w.set_u32_array(a + ".attention.head_count", u32s(lh));
+    w.set_u32_array(a + ".attention.head_count_kv", u32s(lkv));
+  } else {
+    w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
+    w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
+    if (a != "gpt2") w.set_u32(a + ".attention.head_count_kv", (uint32_t)c.kv_heads);
+  }
   if (a == "gpt2") w.set_f32("gpt2.attention.layer_norm_epsilon", c.norm_eps);
-  if (a != "gpt2") w.set_u32(a + ".attention.head_count_kv", (uint32_t)c.kv_heads);
   if (c.head_dim > 0) {
     w.set_u32(a + ".attention.key_length", (uint32_t)head_dim);
     w.set_u32(a + ".attention.value_length", (uint32_t)head_dim);

@@ -11,6 +11,7 @@
 //     its row length is not a multiple of 256;
 //   * attn_v and ffn_down are Q6_K on layers where
 //     i < n/8 || i >= 7n/8 || (i - n/8) % 3 == 2;
+//   * a fused attn_qkv is Q5_K;
 //   * any K-quant whose row length is not a multiple of 256 falls back:
 //     Q4_K -> Q5_0, Q6_K -> Q8_0, Q5_K -> Q5_1;
 //   * 1-D norm weights stay F32.
@@ -20,11 +21,12 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 namespace chonk {
 
 struct SynthConfig {
-  std::string arch = "llama";  // llama | qwen3 | gemma3 | gpt2
+  std::string arch = "llama";  // llama | qwen3 | gemma3 | gpt2 | openelm
   std::string name;
   int hidden = 576;
   int layers = 30;
@@ -41,6 +43,10 @@ struct SynthConfig {
   uint64_t seed = 1;
   float weight_std = 0.02f;
   float norm_std = 0.02f;
+  // openelm: per-layer head, kv-head and feed-forward counts (empty: the
+  // scalars above for every layer); written as the arrays
+  // openelm.attention.head_count, .head_count_kv and .feed_forward_length
+  std::vector<int> layer_heads, layer_kv_heads, layer_ffn;
 };
 
 uint32_t recipe_tensor_type(const std::string& recipe, const std::string& role, int layer, int n_layers,

@@ -47,6 +47,11 @@ class SynthSpec:
     norm_eps: float = 1e-5
     sliding_window: int = 0
     seed: int = 1234
+    # openelm: per-layer head / kv-head / feed-forward counts (heads, kv_heads
+    # and ffn above are then their maxima)
+    layer_heads: Optional[list[int]] = None
+    layer_kv_heads: Optional[list[int]] = None
+    layer_ffn: Optional[list[int]] = None
 
 
 @dataclass
@@ -81,6 +86,15 @@ QWEN3 = dict(arch="qwen3", hidden=1024, layers=28, heads=16, kv_heads=8, head_di
 GEMMA3 = dict(arch="gemma3", hidden=640, layers=18, heads=4, kv_heads=1, head_dim=256, ffn=2048, vocab=262144,
               context_length=32768, rope_theta=1000000.0, norm_eps=1e-6, sliding_window=512)
 
+# OpenELM-270M-shaped: per-layer query / kv heads as the reference registry
+# lists them (registry.ts:55-58, 589-630; groups of 4), feed-forward widths
+# from multipliers 0.5..4.0 of the hidden size rounded to multiples of 256
+OPENELM_270M = dict(arch="openelm", hidden=1280, layers=16, heads=20, kv_heads=5, head_dim=64, ffn=5120, vocab=32000,
+                    context_length=2048, rope_theta=10000.0, norm_eps=1e-6,
+                    layer_heads=[12] * 5 + [16] * 7 + [20] * 4, layer_kv_heads=[3] * 5 + [4] * 7 + [5] * 4,
+                    layer_ffn=[768, 1024, 1280, 1536, 1792, 2048, 2560, 2816, 3072, 3328, 3584, 3840, 4352, 4608,
+                               4864, 5120])
+
 WORKLOADS: dict[str, Workload] = {
     w.name: w
     for w in [
@@ -101,6 +115,10 @@ WORKLOADS: dict[str, Workload] = {
                                                kv_heads=12, ffn=3072, vocab=50257, context_length=1024, seed=29),
                  max_context=1024, eos_ids=[50256], prompt_tokens=512, decode_tokens=128,
                  description="GPT-2-124M-shaped decoder (gpt2 runtime), Q4_K_M, 512-token prompt, greedy 128"),
+        Workload("openelm-270m-q4_k_m", SynthSpec(recipe="q4_k_m", seed=37, **OPENELM_270M), max_context=512,
+                 eos_ids=[2], prompt_tokens=32, decode_tokens=128,
+                 description="OpenELM-270M-shaped decoder (fused q|k|v, per-layer heads 12-20 / kv heads 3-5 / "
+                             "feed-forward 768-5120), Q4_K_M, 32-token prompt, greedy 128"),
         # small decoders for oracle parity (each exercises a different type mix)
         Workload("tiny-qwen3", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=2,
                                          head_dim=64, ffn=512, vocab=1200, context_length=4096,
@@ -121,6 +139,12 @@ WORKLOADS: dict[str, Workload] = {
                                             ffn=384, vocab=700, context_length=4096, rope_theta=100000.0,
                                             norm_eps=1e-5, seed=13),
                  max_context=160, eos_ids=[2], prompt_tokens=16, decode_tokens=24),
+        Workload("tiny-openelm", SynthSpec(arch="openelm", recipe="q4_k_m", hidden=256, layers=4, heads=4,
+                                           kv_heads=2, head_dim=64, ffn=768, vocab=1000, context_length=2048,
+                                           rope_theta=10000.0, norm_eps=1e-6, seed=31,
+                                           layer_heads=[2, 3, 4, 4], layer_kv_heads=[1, 1, 1, 2],
+                                           layer_ffn=[256, 384, 512, 768]),
+                 max_context=160, eos_ids=[2], prompt_tokens=24, decode_tokens=32),
         Workload("tiny-gemma3", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=320, layers=7, heads=4,
                                           kv_heads=1, head_dim=128, ffn=512, vocab=1500, context_length=4096,
                                           rope_theta=1000000.0, norm_eps=1e-6, sliding_window=16, seed=17),

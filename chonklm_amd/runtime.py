@@ -396,6 +396,13 @@ def write_synthetic_gguf(workload: Workload | str, path: str, threads: int = 8) 
     c.hidden, c.layers, c.heads, c.kv_heads = sp.hidden, sp.layers, sp.heads, sp.kv_heads
     c.head_dim, c.ffn, c.vocab, c.context_length = sp.head_dim, sp.ffn, sp.vocab, sp.context_length
     c.rope_theta, c.norm_eps, c.sliding_window, c.seed = sp.rope_theta, sp.norm_eps, sp.sliding_window, sp.seed
+    keep = []
+    for fld in ("layer_heads", "layer_kv_heads", "layer_ffn"):
+        vals = getattr(sp, fld)
+        if vals is not None:
+            arr = (C.c_int32 * len(vals))(*vals)
+            keep.append(arr)
+            setattr(c, fld, C.cast(arr, C.POINTER(C.c_int32)))
     check(lib().chonk_write_synthetic_gguf(C.byref(c), str(path).encode(), int(threads)))
     return str(path)
 

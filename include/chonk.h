@@ -83,7 +83,7 @@ typedef struct {
 
 typedef struct {
   int32_t hidden, ffn, vocab, layers, heads, kv_heads, head_dim, context;
-  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3, 3 gpt2 */
+  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3, 3 gpt2, 4 openelm */
   int32_t qk_norm, interleaved_rope, kv_dtype;
   uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
   uint64_t device_bytes;            /* device memory held by the engine */
@@ -265,7 +265,7 @@ int chonk_gemm(int32_t device, uint32_t ggml_type, const void* blocks, int64_t n
 
 /* Model files --------------------------------------------------------------- */
 typedef struct {
-  const char* arch;      /* "llama" | "qwen3" | "gemma3" | "gpt2" */
+  const char* arch;      /* "llama" | "qwen3" | "gemma3" | "gpt2" | "openelm" */
   const char* recipe;    /* "q4_k_m" | "q8_0" | "q4_k" | "q6_k" | "q5_0" */
   int32_t hidden, layers, heads, kv_heads, head_dim, ffn, vocab, context_length;
   float rope_theta, norm_eps;
@@ -273,6 +273,11 @@ typedef struct {
   uint64_t seed;
   float weight_std;      /* 0 -> 0.02 */
   float norm_std;        /* 0 -> 0.02 */
+  /* openelm: per-layer head, kv-head and feed-forward counts, `layers` entries
+   * each (null: heads / kv_heads / ffn for every layer) */
+  const int32_t* layer_heads;
+  const int32_t* layer_kv_heads;
+  const int32_t* layer_ffn;
 } chonk_synth_config;
 
 /* Writes a seeded random-init decoder as GGUF (see the recipe in synth.h). */

@@ -467,6 +467,21 @@ void load_gguf(const char* path, Gguf* g) {
       throw std::runtime_error("tensor " + kv.first + " extends past end of file");
 }
 
+// ggufNumberArray (llama-wgsl-runtime.ts:474-486)
+std::vector<int> num_array(const Gguf& g, const std::string& k) {
+  auto it = g.kv.find(k);
+  if (it == g.kv.end() || it->second.type != 9)
+    throw std::runtime_error("GGUF metadata " + k + " is missing or not a numeric array");
+  std::vector<int> out;
+  for (size_t i = 0; i < it->second.arr.size(); ++i) {
+    const Value& v = it->second.arr[i];
+    if (v.type == 8 || v.type == 9 || v.type == 7)
+      throw std::runtime_error("GGUF metadata " + k + "[" + std::to_string(i) + "] is not numeric");
+    out.push_back((int)v.num);
+  }
+  return out;
+}
+
 double num(const Gguf& g, const std::string& k, double fallback, bool required) {
   auto it = g.kv.find(k);
   if (it != g.kv.end() && it->second.type != 8 && it->second.type != 9) return it->second.num;
@@ -502,6 +517,7 @@ struct orc_model {
   // hyper-parameters (buildGgufLlamaManifest, llama-wgsl-runtime.ts:326-425)
   bool gemma = false, interleaved = false, qk_norm = false, kv_f16 = false;
   bool gpt = false;                         // GGUF architecture gpt2 (gpt-wgsl-runtime.ts)
+  bool openelm = false;                     // fused attn_qkv, per-layer heads / kv heads / ffn
   std::vector<float> pos_embd, final_norm_b;  // GPT-2: [context][hidden] position table, final LayerNorm bias
   int hidden = 0, ffn = 0, vocab = 0, n_layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float norm_eps = 1e-5f, qk_eps = 1e-5f, attn_scale = 0, embed_scale = 1;
@@ -770,15 +786,31 @@ void build(orc_model* m, const orc_model_def* def) {
     build_gpt(m, def);
     return;
   }
-  if (arch != "qwen3" && arch != "llama" && arch != "gemma3")
+  if (arch != "qwen3" && arch != "llama" && arch != "gemma3" && arch != "openelm")
     throw std::runtime_error("Llama GGUF WGSL does not support architecture " + arch);
   m->gemma = arch == "gemma3";
+  m->openelm = arch == "openelm";
   m->interleaved = arch == "llama";
   m->n_layers = (int)num(g, arch + ".block_count", 0, true);
   m->hidden = (int)num(g, arch + ".embedding_length", 0, true);
-  m->heads = (int)num(g, arch + ".attention.head_count", 0, true);
-  m->kv_heads = (int)num(g, arch + ".attention.head_count_kv", 0, true);
-  m->ffn = (int)num(g, arch + ".feed_forward_length", 0, true);
+  // openelm: per-layer arrays whose maxima are the model's heads / kvHeads /
+  // intermediate (buildGgufLlamaManifest, :373-380; validateLayerArray, :1815-1821)
+  std::vector<int> lh, lkv, lff;
+  if (m->openelm) {
+    lh = num_array(g, arch + ".attention.head_count");
+    lkv = num_array(g, arch + ".attention.head_count_kv");
+    lff = num_array(g, arch + ".feed_forward_length");
+    for (const auto* v : {&lh, &lkv, &lff})
+      if ((int)v->size() != m->n_layers || v->empty())
+        throw std::runtime_error("Llama WGSL manifest layer array length != layers");
+    m->heads = *std::max_element(lh.begin(), lh.end());
+    m->kv_heads = *std::max_element(lkv.begin(), lkv.end());
+    m->ffn = *std::max_element(lff.begin(), lff.end());
+  } else {
+    m->heads = (int)num(g, arch + ".attention.head_count", 0, true);
+    m->kv_heads = (int)num(g, arch + ".attention.head_count_kv", 0, true);
+    m->ffn = (int)num(g, arch + ".feed_forward_length", 0, true);
+  }
   m->hd = (int)num(g, arch + ".attention.key_length", std::floor((double)m->hidden / m->heads), false);
   if (m->hd > 256) throw std::runtime_error("head_dim above 256 is not supported");
   m->vocab = def->vocab;
@@ -800,11 +832,11 @@ void build(orc_model* m, const orc_model_def* def) {
   for (int i = 0; i < m->n_layers; ++i) {
     Layer L;
     const std::string p = "blk." + std::to_string(i) + ".";
-    L.heads = m->heads;
-    L.kv_heads = m->kv_heads;
-    L.qdim = m->heads * m->hd;
-    L.kvdim = m->kv_heads * m->hd;
-    L.ffn = m->ffn;
+    L.heads = m->openelm ? lh[(size_t)i] : m->heads;
+    L.kv_heads = m->openelm ? lkv[(size_t)i] : m->kv_heads;
+    L.qdim = L.heads * m->hd;
+    L.kvdim = L.kv_heads * m->hd;
+    L.ffn = m->openelm ? lff[(size_t)i] : m->ffn;
     const double th = m->gemma ? (i % 6 == 5 ? gtheta : 10000.0) : theta;
     L.theta_u32 = (uint32_t)std::llround(th);  // Math.round(layer.ropeTheta)
     L.window = m->gemma ? (i % 6 == 5 ? 0 : window) : 0;
@@ -818,18 +850,28 @@ void build(orc_model* m, const orc_model_def* def) {
       L.q_norm = floats(m, p + "attn_q_norm.weight", m->hd);
       L.k_norm = floats(m, p + "attn_k_norm.weight", m->hd);
     }
-    L.q = matrix(m, p + "attn_q.weight", m->hidden, L.qdim);
-    L.k = matrix(m, p + "attn_k.weight", m->hidden, L.kvdim);
-    L.v = matrix(m, p + "attn_v.weight", m->hidden, L.kvdim);
+    if (m->openelm) {
+      // attn.qkv_proj aliased to attn_qkv (:359), rows q | k | v (:797)
+      L.qkv = matrix(m, p + "attn_qkv.weight", m->hidden, (uint64_t)L.qdim + 2 * L.kvdim);
+    } else {
+      L.q = matrix(m, p + "attn_q.weight", m->hidden, L.qdim);
+      L.k = matrix(m, p + "attn_k.weight", m->hidden, L.kvdim);
+      L.v = matrix(m, p + "attn_v.weight", m->hidden, L.kvdim);
+    }
     L.o = matrix(m, p + "attn_output.weight", L.qdim, m->hidden);
-    L.gate = matrix(m, p + "ffn_gate.weight", m->hidden, m->ffn);
-    L.up = matrix(m, p + "ffn_up.weight", m->hidden, m->ffn);
-    L.down = matrix(m, p + "ffn_down.weight", m->ffn, m->hidden);
+    L.gate = matrix(m, p + "ffn_gate.weight", m->hidden, L.ffn);
+    L.up = matrix(m, p + "ffn_up.weight", m->hidden, L.ffn);
+    L.down = matrix(m, p + "ffn_down.weight", L.ffn, m->hidden);
     L.kcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
     L.vcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
     m->layers.push_back(std::move(L));
   }
   if (m->gemma && !m->qk_norm) throw std::runtime_error("Gemma WGSL layer is missing required weights");
+  // the packed q|k|v path runs only with q/k norms (:1071-1084)
+  if (m->openelm && !m->qk_norm) throw std::runtime_error("Llama WGSL layer is missing attention projection weights");
+  for (const Layer& L : m->layers)
+    if (L.heads <= 0 || L.kv_heads <= 0 || L.heads % L.kv_heads != 0)
+      throw std::runtime_error("layer heads must be a positive multiple of kv heads");
 }
 
 // LAYER_NORM_WGSL (gpt-wgsl-runtime.ts:1658-1706): 256 threads, sum and sum of
@@ -1010,6 +1052,7 @@ orc_model* orc_model_load(const char* path, const orc_model_def* def, char* err,
     m->logits.assign(m->vocab, 0);
     m->candidates.assign((size_t)(m->vocab + 255) / 256 * 8, 0);
     if (m->gpt) m->qkv.assign(3 * (size_t)H, 0);
+    if (m->openelm) m->qkv.assign((size_t)qdim + 2 * kvdim, 0);
     return m;
   } catch (const std::exception& e) {
     if (err && err_len) std::snprintf(err, err_len, "%s", e.what());
@@ -1300,9 +1343,18 @@ int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const 
       } else {
         // :1069-1103
         rms_norm(residual, L.in_norm.data(), m->norm.data(), H, m->norm_eps);
-        matvec(pool, L.q.type, L.q.data, L.q.n, L.q.k, m->norm.data(), m->q.data());
-        matvec(pool, L.k.type, L.k.data, L.k.n, L.k.k, m->norm.data(), m->k.data());
-        matvec(pool, L.v.type, L.v.data, L.v.n, L.v.k, m->norm.data(), m->v.data());
+        if (m->openelm) {
+          // q4Matvec(norm, qkvProj, qkv), then qkvNormRopeStore (:1071-1074, :3025-3120),
+          // whose arithmetic is qkNormRopeStore's over the packed row
+          matvec(pool, L.qkv.type, L.qkv.data, L.qkv.n, L.qkv.k, m->norm.data(), m->qkv.data());
+          std::copy(m->qkv.begin(), m->qkv.begin() + L.qdim, m->q.begin());
+          std::copy(m->qkv.begin() + L.qdim, m->qkv.begin() + L.qdim + L.kvdim, m->k.begin());
+          std::copy(m->qkv.begin() + L.qdim + L.kvdim, m->qkv.begin() + L.qdim + 2 * L.kvdim, m->v.begin());
+        } else {
+          matvec(pool, L.q.type, L.q.data, L.q.n, L.q.k, m->norm.data(), m->q.data());
+          matvec(pool, L.k.type, L.k.data, L.k.n, L.k.k, m->norm.data(), m->k.data());
+          matvec(pool, L.v.type, L.v.data, L.v.n, L.v.k, m->norm.data(), m->v.data());
+        }
         const float* qa;
         if (m->qk_norm) {
           qk_rope_store(m, L, pos, true, m->qn.data());

@@ -26,7 +26,7 @@ sys.path.insert(0, str(ROOT))
 from chonklm_amd import WORKLOADS, write_synthetic_gguf  # noqa: E402
 from tests.numpy_ref import NumpyDecoder  # noqa: E402
 
-MODELS = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
+MODELS = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3", "tiny-openelm"]
 STEPS = 24
 
 

@@ -5,7 +5,9 @@ Vectorised restatement of the decoder the reference runs
 (pre-norm, GQA attention with optional per-head q/k RMSNorm, RoPE interleaved
 for GGUF arch "llama" and split-half otherwise, SwiGLU) and gemma3 layers
 (sandwich norms, +-65000 residual clamp, GELU-tanh, sqrt(hidden) embedding
-scale, sliding window on layers i % 6 != 5). Everything is float64 except the
+scale, sliding window on layers i % 6 != 5) and openelm layers (one fused
+q|k|v matrix, per-layer head / kv-head / feed-forward counts from metadata
+arrays, q/k RMSNorm, split-half RoPE). Everything is float64 except the
 dequantized weights (exact float32 values) and, optionally, a binary16 K/V
 cache. Closed forms only: no reduction-order mimicry.
 """
@@ -27,8 +29,11 @@ class NumpyDecoder:
         p = arch + "."
         self.L = int(g.kv[p + "block_count"])
         self.H = int(g.kv[p + "embedding_length"])
-        self.nh = int(g.kv[p + "attention.head_count"])
-        self.nkv = int(g.kv[p + "attention.head_count_kv"])
+        self.openelm = arch == "openelm"
+        hc, kvc = g.kv[p + "attention.head_count"], g.kv[p + "attention.head_count_kv"]
+        self.lnh = [int(x) for x in hc] if self.openelm else [int(hc)] * self.L
+        self.lnkv = [int(x) for x in kvc] if self.openelm else [int(kvc)] * self.L
+        self.nh, self.nkv = max(self.lnh), max(self.lnkv)
         self.hd = int(g.kv.get(p + "attention.key_length", self.H // self.nh))
         self.eps = float(np.float32(g.kv.get(p + "attention.layer_norm_rms_epsilon", 1e-5)))
         self.vocab = vocab
@@ -50,8 +55,13 @@ class NumpyDecoder:
         for i in range(self.L):
             b = f"blk.{i}."
             get = lambda n: matrix(g, b + n).astype(np.float64)
-            lay = dict(q=get("attn_q.weight"), k=get("attn_k.weight"), v=get("attn_v.weight"),
-                       o=get("attn_output.weight"), gate=get("ffn_gate.weight"), up=get("ffn_up.weight"),
+            if self.openelm:
+                qkv = get("attn_qkv.weight")
+                qd, kd = self.lnh[i] * self.hd, self.lnkv[i] * self.hd
+                lay = dict(q=qkv[:qd], k=qkv[qd:qd + kd], v=qkv[qd + kd:qd + 2 * kd])
+            else:
+                lay = dict(q=get("attn_q.weight"), k=get("attn_k.weight"), v=get("attn_v.weight"))
+            lay.update(o=get("attn_output.weight"), gate=get("ffn_gate.weight"), up=get("ffn_up.weight"),
                        down=get("ffn_down.weight"), in_norm=get("attn_norm.weight"))
             if self.gemma:
                 lay.update(post=get("post_attention_norm.weight"), pre_ffn=get("ffn_norm.weight"),
@@ -90,11 +100,12 @@ class NumpyDecoder:
         return y
 
     def step(self, token: int) -> np.ndarray:
-        H, hd, nh, nkv = self.H, self.hd, self.nh, self.nkv
+        H, hd = self.H, self.hd
         x = self.emb[token] * (np.sqrt(H) if self.gemma else 1.0)
         if self.gemma:
             x = x * 1.0
         for i, lay in enumerate(self.layers):
+            nh, nkv = self.lnh[i], self.lnkv[i]
             n = self._rms(x, lay["in_norm"])
             q = (lay["q"] @ n).reshape(nh, hd)
             k = (lay["k"] @ n).reshape(nkv, hd)
@@ -107,8 +118,8 @@ class NumpyDecoder:
             if self.kv_f16:
                 k = k.astype(np.float16).astype(np.float64)
                 v = v.astype(np.float16).astype(np.float64)
-            self.K[i, :, self.pos] = k
-            self.V[i, :, self.pos] = v
+            self.K[i, :nkv, self.pos] = k
+            self.V[i, :nkv, self.pos] = v
             w = self.window[i]
             start = self.pos + 1 - w if (w and self.pos + 1 > w) else 0
             grp = nh // nkv

@@ -22,7 +22,7 @@ from tests import ggufpy
 from tests.conftest import rel_err
 from tests.numpy_ref import NumpyDecoder, NumpyGpt2
 
-TINY = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
+TINY = ["tiny-qwen3", "tiny-llama", "tiny-llama-q8", "tiny-gemma3", "tiny-openelm"]
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "greedy_golden.json").read_text())
 
 
@@ -66,19 +66,25 @@ def test_greedy_ids_match_golden(name, synth):
     assert ids[:n] == g["ids"][:n]
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-gemma3"])
+def _layer_heads(w, layer):
+    sp = w.spec
+    return ((sp.layer_heads or [sp.heads] * sp.layers)[layer], (sp.layer_kv_heads or [sp.kv_heads] * sp.layers)[layer])
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-gemma3", "tiny-openelm"])
 def test_kv_rows_match_float64_decoder(name, synth):
     w, path, ref = _oracle(synth, name)
     dec = NumpyDecoder(path, w.spec.vocab, w.max_context, kv_f16=True)
     for t in np.random.default_rng(6).integers(0, w.spec.vocab, 7).tolist():
         ref.run_token(t, False)
         dec.step(t)
-    n = w.spec.kv_heads * dec.hd
     for layer in range(w.spec.layers):
+        nkv = _layer_heads(w, layer)[1]
+        n = nkv * dec.hd
         for pos in (0, 3, 6):
             for is_v in (False, True):
                 got = ref.read_kv(layer, is_v, pos, n)
-                want = (dec.V if is_v else dec.K)[layer, :, pos].reshape(-1)
+                want = (dec.V if is_v else dec.K)[layer, :nkv, pos].reshape(-1)
                 # both round to binary16; allow one ulp where fp32 and fp64 straddle a rounding edge
                 assert np.max(np.abs(got - want)) <= np.max(np.abs(want)) * 2e-3 + 1e-6
 
@@ -90,9 +96,8 @@ def test_first_position_attention_returns_value_row(name, synth):
     ref.run_token(17, True)
     g = ggufpy.read_gguf(path)
     arch = g.kv["general.architecture"]
-    nh = int(g.kv[arch + ".attention.head_count"])
-    nkv = int(g.kv[arch + ".attention.head_count_kv"])
-    hdim = int(g.kv.get(arch + ".attention.key_length", int(g.kv[arch + ".embedding_length"]) // nh))
+    nh, nkv = _layer_heads(w, w.spec.layers - 1)  # the last layer's (openelm varies them per layer)
+    hdim = int(g.kv.get(arch + ".attention.key_length", int(g.kv[arch + ".embedding_length"]) // w.spec.heads))
     attn = ref.read(5, nh * hdim).reshape(nh, hdim)
     v = ref.read_kv(w.spec.layers - 1, True, 0, nkv * hdim).reshape(nkv, hdim)
     for h in range(nh):

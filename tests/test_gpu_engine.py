@@ -5,7 +5,8 @@ tiny-qwen3 (Q4_K/Q6_K, qk-norm, split RoPE), tiny-qwen3-hd128 (head_dim 128,
 150-token prompts: decode attention over several 64-position chunks), tiny-llama (Q5_0/Q8_0/Q4_K
 fallbacks, interleaved RoPE, head_dim 32, GQA 3), tiny-llama-q8 (Q8_0
 everywhere), tiny-gemma3 (gemma3 sandwich norms, GELU-tanh, sliding window,
-Q8_0 tied lm_head, top-k/temperature sampling). Bars: identical token ids;
+Q8_0 tied lm_head, top-k/temperature sampling), tiny-openelm (fused q|k|v in
+Q5_K, per-layer head / kv-head / feed-forward counts, GQA groups 2-4). Bars: identical token ids;
 logits max|d| / max|ref| <= 1e-3 at every step.
 """
 from __future__ import annotations
@@ -21,7 +22,12 @@ from tests.conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 
-TINY = ["tiny-qwen3", "tiny-qwen3-hd128", "tiny-llama", "tiny-llama-q8", "tiny-gemma3"]
+TINY = ["tiny-qwen3", "tiny-qwen3-hd128", "tiny-llama", "tiny-llama-q8", "tiny-gemma3", "tiny-openelm"]
+
+
+def _layer_kv_heads(w, layer):
+    """K/V heads of one layer (openelm varies them per layer)."""
+    return (w.spec.layer_kv_heads or [w.spec.kv_heads] * w.spec.layers)[layer]
 
 
 def _pair(synth, name, kv="f16", **over):
@@ -51,7 +57,9 @@ def step_mode(request, monkeypatch):
 @pytest.mark.parametrize("name", TINY)
 def test_step_logits_and_tokens(name, synth, step_mode):
     w, loaded, ref = _pair(synth, name)
-    assert loaded.engine.info["persistent_step"] == (1 if step_mode == "persistent" else 0)
+    # the persistent step runs one head geometry for every layer (not openelm)
+    persistent = step_mode == "persistent" and w.spec.arch != "openelm"
+    assert loaded.engine.info["persistent_step"] == (1 if persistent else 0)
     eng = loaded.engine
     prompt = _prompt(w)
     toks_g, toks_r = [], []
@@ -219,11 +227,11 @@ def test_batched_prefill_matches_token_steps(name, synth):
     for t in prompt[:-1]:
         ref.run_token(t, False)
     assert eng.position == ref.position == len(prompt) - 1
-    n = eng.info["kv_heads"] * eng.info["head_dim"]
     for layer in range(w.spec.layers):
+        n = _layer_kv_heads(w, layer) * eng.info["head_dim"]
         for pos in (0, len(prompt) // 2, len(prompt) - 2):
             for is_v in (False, True):
-                g = eng.read_kv(layer, is_v, pos)
+                g = eng.read_kv(layer, is_v, pos)[:n]
                 r = ref.read_kv(layer, is_v, pos, n)
                 assert np.max(np.abs(g - r)) <= np.max(np.abs(r)) * 2e-3 + 1e-6, f"layer {layer} pos {pos} v={is_v}"
     a = eng.run_token(prompt[-1], True)
@@ -352,6 +360,28 @@ def test_gpt2_wide_ffn_matches_oracle(tmp_path):
     eng = loaded.engine
     tok = 5
     for i in range(10):
+        a = eng.run_token(tok, True)
+        b = ref.run_token(tok, True)
+        e = rel_err(eng.read_logits(), ref.logits())
+        assert e <= 1e-3, f"step {i}: logits rel err {e:.3e}"
+        assert a == b, f"step {i}: token {a} != {b}"
+        tok = a
+
+
+def test_openelm_270m_shape_steps_match_oracle(synth):
+    """The OpenELM-270M shape: per-layer GQA of 12/16/20 query heads over 3/4/5 kv heads, a
+    Q5_K fused q|k|v, feed-forward widths 768..5120 (ffn_down rows above 4096 take the generic
+    matvec; the prompt runs through the batched pass): prompt then 8 greedy steps, logits
+    within 1e-3 and identical ids."""
+    w, loaded, ref = _pair(synth, "openelm-270m-q4_k_m")
+    eng = loaded.engine
+    assert eng.info["architecture"] == 4
+    prompt = _prompt(w, seed=21, n=32)
+    eng.prefill(prompt[:-1])
+    for t in prompt[:-1]:
+        ref.run_token(t, False)
+    tok = prompt[-1]
+    for i in range(8):
         a = eng.run_token(tok, True)
         b = ref.run_token(tok, True)
         e = rel_err(eng.read_logits(), ref.logits())
