@@ -10,7 +10,8 @@ and K/V cache resident in HBM; timed with HIP events on the engine stream).
 
 Also reported:
   roofline      the kernel class with the most time per step, its algorithmic
-                bytes per launch / mean launch time vs 8 TB/s;
+                bytes per launch / mean launch time (every layer's launch of the
+                class back to back, HIP events) vs 8 TB/s;
   step_roofline weight + K/V bytes per token / ms per token vs 8 TB/s;
   q4k_matvec    the Q4_K gate|up matvec's GB/s;
   cpu_baseline  the oracle (CPU restatement of the reference WGSL
@@ -217,7 +218,8 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3-0.6b-q4_k_m")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernel-rounds", type=int, default=1,
+                    help="back-to-back passes over each kernel class (one launch per layer) timed with HIP events")
     ap.add_argument("--cold-reps", type=int, default=100,
                     help="launches per kernel for the cold / warm per-launch timing (0 skips it)")
     ap.add_argument("--no-kernel-times", action="store_true",
@@ -293,15 +295,21 @@ def main() -> int:
     tok_s = 1000.0 / ms_per_step
     pos_end = eng.position
 
-    # per-kernel launch times (HIP events, same arguments as in the step)
+    # per-launch durations (HIP events on the engine stream): each kernel class (one
+    # launch per layer, e.g. every layer's attention) launched back to back, so every
+    # launch meets its weights / K/V rows as cold as in the step; bytes at this position
     n_kernels = info["kernels_per_step"]
     classes: dict[str, dict] = {}
-    for kid in range(0 if args.no_kernel_times else n_kernels - 1):  # select advances the position
-        name, us, nbytes = eng.bench_kernel(kid, args.kernel_reps)
-        c = classes.setdefault(kernel_class(name), {"launches": 0, "us": 0.0, "bytes": 0})
-        c["launches"] += 1
-        c["us"] += us
-        c["bytes"] += nbytes
+    if not args.no_kernel_times and not info.get("persistent_step"):
+        ids_of: dict[str, list[int]] = {}
+        for kid in range(n_kernels - 1):  # the select kernel moves no bulk data
+            name, _, nbytes = eng.bench_kernel(kid, 0)
+            ids_of.setdefault(kernel_class(name), []).append(kid)
+            c = classes.setdefault(kernel_class(name), {"launches": 0, "us": 0.0, "bytes": 0})
+            c["launches"] += 1
+            c["bytes"] += nbytes
+        for cls, ids in ids_of.items():
+            classes[cls]["us"] = eng.time_kernels(ids, args.kernel_rounds) * len(ids)
     if not classes:
         classes["none"] = {"launches": 1, "us": float("nan"), "bytes": 0}
     gu = classes.get("gateup")
@@ -372,7 +380,7 @@ def main() -> int:
             "kernel": "gateup (Q4_K, fused RMSNorm + SwiGLU)",
             "achieved": round(gu["bytes"] / gu["us"] / 1e3, 1), "unit": "GB/s",
             "us_per_launch": round(gu["us"] / gu["launches"], 3)},
-        # the step's phases timed as standalone kernels (HIP events, 20 launches each)
+        # per-step time of each kernel class (HIP events over back-to-back passes of the class)
         "kernels": {k: {"launches": v["launches"], "us_per_step": round(v["us"], 2),
                         "gb_s": round(v["bytes"] / v["us"] / 1e3, 1)} for k, v in classes.items()},
         "kernel_sum_us": round(sum(v["us"] for v in classes.values()), 2),

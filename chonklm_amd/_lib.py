@@ -152,6 +152,7 @@ SIGNATURES = [
     ("chonk_batch_step", C.c_int, [P, I32P, I32P, C.c_size_t, I32P]),
     ("chonk_batch_position", C.c_int, [P, C.c_int32, I32P]),
     ("chonk_batch_read_logits", C.c_int, [P, C.c_int32, F32P, C.c_size_t]),
+    ("chonk_engine_time_kernels", C.c_int, [P, I32P, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     ("chonk_engine_bench_kernel", C.c_int,
      [P, C.c_int32, C.c_int32, C.POINTER(C.c_double), C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64)]),
     ("chonk_engine_fake_context", C.c_int, [P, C.c_int32, C.c_uint64]),

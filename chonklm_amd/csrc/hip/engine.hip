@@ -2685,6 +2685,45 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
   });
 }
 
+int chonk_engine_time_kernels(chonk_engine* e, const int32_t* ids, int32_t n_ids, int32_t rounds,
+                              double* us_per_launch) {
+  return api(e, [&] {
+    const ModelCfg& c = e->cfg;
+    if (!ids || n_ids <= 0 || rounds <= 0 || !us_per_launch) throw Error(CHONK_EINVAL, "bad kernel list or rounds");
+    std::vector<Launch> run;
+    for (int i = 0; i < n_ids; ++i) {
+      if (ids[i] < 0 || ids[i] >= (int32_t)e->kernels_logits.size()) throw Error(CHONK_EINVAL, "bad kernel id");
+      Launch L = e->kernels_logits[(size_t)ids[i]];
+      if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
+      if (L.kind == Launch::MV) L.mv.advance_pos = 0;
+      run.push_back(L);
+    }
+    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    const DevState saved = read_state(e);
+    DevState st = saved;
+    st.stopped = 0;
+    st.generating = 0;
+    upload_state_fields(e, st);
+    hipEvent_t a, b;
+    HIP_OK(hipEventCreate(&a));
+    HIP_OK(hipEventCreate(&b));
+    double total_ms = 0;
+    for (int r = 0; r < rounds; ++r) {
+      HIP_OK(hipEventRecord(a, e->stream));
+      for (const Launch& L : run) enqueue(L, e->stream);
+      HIP_OK(hipEventRecord(b, e->stream));
+      HIP_OK(hipEventSynchronize(b));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, a, b));
+      total_ms += ms;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    upload_state_fields(e, saved);
+    *us_per_launch = total_ms * 1000.0 / ((double)rounds * n_ids);
+  });
+}
+
 int chonk_engine_profile_step_raw(chonk_engine* e, uint64_t* out, size_t cap, int32_t* n_phases, int32_t* n_wg) {
   return api(e, [&] {
     int np = 0, grid = 0;
@@ -2717,11 +2756,14 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
                               size_t name_len, uint64_t* bytes) {
   return api(e, [&] {
     const ModelCfg& c = e->cfg;
-    if (kernel_id < 0 || kernel_id >= (int32_t)e->kernels_logits.size() || reps <= 0)
+    if (kernel_id < 0 || kernel_id >= (int32_t)e->kernels_logits.size() || reps < 0)
       throw Error(CHONK_EINVAL, "bad kernel id or repetitions");
     const Launch& L = e->kernels_logits[(size_t)kernel_id];
-    if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
+    if (reps > 0 && L.kind == Launch::SEL)
+      throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
     if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    if (avg_us) *avg_us = 0.0;
+    if (reps > 0) {
     const DevState saved = read_state(e);
     DevState st = saved;
     st.stopped = 0;
@@ -2743,6 +2785,7 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
     (void)hipEventDestroy(b);
     upload_state_fields(e, saved);
     if (avg_us) *avg_us = (double)ms * 1000.0 / reps;
+    }
     if (name && name_len) std::snprintf(name, name_len, "%s", L.name.c_str());
     if (bytes) {
       uint64_t by = L.weight_bytes;

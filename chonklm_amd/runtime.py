@@ -167,6 +167,13 @@ class LlamaWgslEngine:
         check(lib().chonk_engine_bench_decode(self._h, warmup, steps, C.byref(ms)), self._h)
         return float(ms.value)
 
+    def time_kernels(self, ids: list[int], rounds: int = 1) -> float:
+        """Mean microseconds per launch of the step kernels `ids` launched back to back."""
+        arr = (C.c_int32 * len(ids))(*ids)
+        us = C.c_double()
+        check(lib().chonk_engine_time_kernels(self._h, arr, len(ids), rounds, C.byref(us)), self._h)
+        return float(us.value)
+
     def bench_kernel(self, kernel_id: int, reps: int) -> tuple[str, float, int]:
         us = C.c_double()
         name = C.create_string_buffer(64)

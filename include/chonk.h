@@ -201,7 +201,7 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
  * `reps` times back-to-back with the arguments it has in the step, timed with
  * HIP events on the engine stream. kernel_id indexes the step's launch list;
  * name receives its label (e.g. "L3.gateup q4_k"); bytes its algorithmic
- * bytes per launch. */
+ * bytes per launch. reps = 0 launches nothing (name and bytes only). */
 int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, double* avg_us, char* name,
                               size_t name_len, uint64_t* bytes);
 /* The same kernel timed launch by launch with HIP events, `reps` times with
@@ -210,6 +210,13 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
  * `reps` times right after an identical launch (*warm_us). */
 int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t reps, uint64_t flush_bytes,
                                    double* cold_us, double* warm_us);
+/* Mean duration (microseconds) of one launch of the step kernels ids[0..n_ids)
+ * when the list is launched back to back, `rounds` times, with the arguments
+ * they have in the step, timed with HIP events on the engine stream. A list
+ * of one phase of every layer (e.g. each layer's attention) meets its weights
+ * and K/V rows as cold as the step does, unlike repeats of one launch. */
+int chonk_engine_time_kernels(chonk_engine* e, const int32_t* ids, int32_t n_ids, int32_t rounds,
+                              double* us_per_launch);
 /* Persistent step only: runs one decode step with per-phase time stamps and
  * returns, per phase (q|k|v, attention, o_proj, gate|up, down per layer, then
  * lm_head), the time from the first workgroup's start to the last workgroup's
