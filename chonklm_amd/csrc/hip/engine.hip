@@ -25,6 +25,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -1905,6 +1906,36 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     HIP_OK(launch_gemm_deferred(g, b.part + off, cap, &ps, s));
     return ps;
   };
+  // one launch over two or three matrices of one type and K whose results are
+  // column ranges of one partial-sum row (segments start on 64-row tiles);
+  // returns false (nothing launched) when the matrices do not qualify
+  auto gemm_fused = [&](std::initializer_list<const DevMat*> ms, int rows, PartSum* out) {
+    std::vector<const DevMat*> m(ms);
+    for (size_t i = 1; i < m.size(); ++i)
+      if (m[i]->q.type != m[0]->q.type || m[i]->q.k != m[0]->q.k || m[i - 1]->q.n % 64 != 0) return false;
+    GemmArgs g{};
+    g.w = m[0]->q;
+    g.w2 = m[1]->q;
+    g.w3 = m.size() > 2 ? m[2]->q : m[1]->q;
+    g.n1 = m[0]->q.n;
+    g.n2 = g.n1 + m[1]->q.n;
+    g.n_all = g.n2 + (m.size() > 2 ? m[2]->q.n : 0);
+    g.xh = b.h;
+    g.xl = b.l;
+    g.xscale = b.xscale;
+    g.t = rows;
+    g.kpad = gemm_kpad(m[0]->q.k);
+    g.ws = m[0]->ws;
+    for (const DevMat* d : m) g.ws = std::min(g.ws, d->ws);  // every matrix stays below 2^14
+    HIP_OK(launch_gemm_deferred(g, b.part, b.part_cap, out, s));
+    return true;
+  };
+  // column range [c0, c0 + n) of a fused result
+  auto columns = [](PartSum p, int c0, int n) {
+    p.p += c0;
+    p.n = n;
+    return p;
+  };
   auto kv_addr = [&](int i) {
     KvAddr k{};
     k.kc = kvs.kc[i];
@@ -1930,13 +1961,17 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     split(b.x, H, H, L.in_norm, T, pending, pending_w);
     pending = PartSum{};
     PfRopeArgs r{};
+    PartSum fused{};
     if (c.openelm) {
       // one fused q|k|v result; k and v are column ranges of it
-      r.pq = gemm(L.qkv, T, 0, P);
-      r.pk = r.pq;
-      r.pk.p += qdim;
-      r.pv = r.pq;
-      r.pv.p += qdim + kvdim;
+      const PartSum f = gemm(L.qkv, T, 0, P);
+      r.pq = columns(f, 0, qdim);
+      r.pk = columns(f, qdim, kvdim);
+      r.pv = columns(f, qdim + kvdim, kvdim);
+    } else if (gemm_fused({&L.q, &L.k, &L.v}, T, &fused)) {
+      r.pq = columns(fused, 0, qdim);
+      r.pk = columns(fused, qdim, kvdim);
+      r.pv = columns(fused, qdim + kvdim, kvdim);
     } else {
       // the partial-sum buffer shared out in proportion to each result's size
       const int64_t pq = P * qdim / ldqkv, pk = P * kvdim / ldqkv;
@@ -1979,8 +2014,14 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     // x += o (Gemma-3: x = clamp(x + RMSNorm(o) * post_norm)), then the ffn norm
     split(b.x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm, T, po, c.gemma ? L.post_norm : nullptr);
     PfGluArgs gl{};
-    gl.pg = gemm(L.gate, T, 0, P / 2);
-    gl.pu = gemm(L.up, T, P / 2, P - P / 2);
+    PartSum gu{};
+    if (gemm_fused({&L.gate, &L.up}, T, &gu)) {
+      gl.pg = columns(gu, 0, F);
+      gl.pu = columns(gu, F, F);
+    } else {
+      gl.pg = gemm(L.gate, T, 0, P / 2);
+      gl.pu = gemm(L.up, T, P / 2, P - P / 2);
+    }
     gl.act = b.act;
     gl.k = F;
     gl.kpad = gemm_kpad(F);
@@ -1994,7 +2035,7 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
   }
   if (logits) {
     PartSum add = pending;
-    if (add.p) add.p += (int64_t)lr0 * add.n;  // rows [lr0, lr0 + nlr) of the result
+    if (add.p) add.p += (int64_t)lr0 * add.ld;  // rows [lr0, lr0 + nlr) of the result
     split(b.x + (size_t)lr0 * H, H, H, e->final_norm, nlr, add, pending_w);
     GemmArgs g{};
     g.w = e->lm_head.q;

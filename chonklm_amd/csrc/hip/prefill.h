@@ -13,6 +13,11 @@ enum GemmEpi : int32_t { GEMM_STORE = 0, GEMM_ADD = 1 };
 // y[t][n] (=|+=) 2^-ws * xscale[t] * sum_k (xh + xl)[t][k] * (W 2^ws)[n][k]
 struct GemmArgs {
   QMat w;                 // striped weights, N = w.n rows of K = w.k
+  // a fused launch over up to three matrices of one type and K (e.g. q | k | v):
+  // output rows [0, n1) come from w, [n1, n2) from w2, [n2, n_all) from w3; the
+  // segment starts are multiples of the 64-row tile. n_all = 0: w alone.
+  QMat w2, w3;
+  int32_t n1, n2, n_all, pad0;
   const _Float16* xh;     // [t][kpad] activation planes, zero past K
   const _Float16* xl;
   const float* xscale;    // [t]
@@ -44,8 +49,9 @@ constexpr int kKvPage = 64;
 // of p[z * zs + t * n + j], added in z order (the consumer kernel adds them).
 struct PartSum {
   const float* p;         // null: absent
-  int32_t n, ks;
-  int64_t zs;
+  int32_t n, ks;          // valid columns, K splits
+  int64_t zs;             // floats between splits
+  int32_t ld, pad0;       // floats between rows (>= n: a column range of a fused result)
 };
 
 struct PfSplitArgs {

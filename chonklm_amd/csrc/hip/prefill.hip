@@ -39,7 +39,7 @@ constexpr int kMaxDeferSplit = 16;  // K split of a deferred GEMM (loads of a su
 // one memory round trip; the sums add the partials in split order.
 template <int S = kWg>
 __device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float (&v)[4]) {
-  const float* q = P.p + (int64_t)t * P.n;
+  const float* q = P.p + (int64_t)t * P.ld;
   if (P.ks == 1) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = j0 + S * e < P.n ? q[j0 + S * e] : 0.f;
@@ -64,7 +64,7 @@ __device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float
 
 // Element j of row t of a deferred result (the partials added in split order).
 __device__ __forceinline__ float part_at(const PartSum& P, int t, int j) {
-  const float* q = P.p + (int64_t)t * P.n + j;
+  const float* q = P.p + (int64_t)t * P.ld + j;
   if (P.ks == 1) return q[0];
   float w[kMaxDeferSplit];
 #pragma unroll
@@ -195,6 +195,19 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * kGT;
+  const int N = a.n_all ? a.n_all : a.w.n;
+  // the tile's matrix of a fused launch (segments start on tile boundaries)
+  const int seg = a.n_all ? (n0 >= a.n2 ? 2 : (n0 >= a.n1 ? 1 : 0)) : 0;
+  const int sb = seg == 2 ? a.n2 : (seg == 1 ? a.n1 : 0);
+  // picked field by field (a selected struct copy would live in scratch)
+  QMat wm = a.w;
+#define CHONK_PICK_W(f) wm.f = seg == 2 ? a.w3.f : (seg == 1 ? a.w2.f : a.w.f)
+  CHONK_PICK_W(s0);
+  CHONK_PICK_W(s1);
+  CHONK_PICK_W(s2);
+  CHONK_PICK_W(s3);
+  CHONK_PICK_W(n);
+#undef CHONK_PICK_W
   const int U = a.w.k >> 5;
   const int nst = (a.w.k + kGK - 1) / kGK;
   // this workgroup's stages: part blockIdx.z of ksplit
@@ -203,7 +216,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   // staging roles: weight unit (row wr, unit j of the stage); x quarter row
   const int wr = tid >> 2, wj = tid & 3;
   const int xt = tid >> 2, xq = tid & 3;
-  const bool w_ok = n0 + wr < a.w.n;
+  const bool w_ok = n0 + wr < N;
   const bool x_ok = t0 + xt < a.t;
   const float wsc = ldexpf(1.0f, a.ws);
 
@@ -225,7 +238,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   }
   auto fetch = [&](int s) {
     const int u = s * 4 + wj;
-    if (w_ok && u < U) f = load_unit<T>(a.w, n0 + wr, u);
+    if (w_ok && u < U) f = load_unit<T>(wm, n0 - sb + wr, u);
     if (x_ok) {
       const uint4* ph = (const uint4*)(a.xh + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
       const uint4* pl = (const uint4*)(a.xl + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
@@ -307,10 +320,10 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
     for (int i = 0; i < 2; ++i) {
       const int n = n0 + rb + 16 * i + 4 * (lane >> 4);
       float* y = a.y + (size_t)t * a.ldy + n;
-      float* pp = a.part + ((size_t)blockIdx.z * a.t + t) * a.w.n + n;
+      float* pp = a.part + ((size_t)blockIdx.z * a.t + t) * N + n;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        if (n + q >= a.w.n) break;
+        if (n + q >= N) break;
         const float v = acc[i][j][q] * sc;
         if (a.ksplit > 1 || a.defer)
           pp[q] = v;
@@ -977,17 +990,25 @@ hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
 
 hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t region_cap, PartSum* out, hipStream_t s) {
   GemmArgs a = a0;
-  if ((int64_t)a.t * a.w.n > region_cap) return hipErrorInvalidValue;
-  const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
+  const int N = a.n_all ? a.n_all : a.w.n;
+  if (a.n_all) {
+    // fused segments: one type and K, starts on tile boundaries, in order
+    if (a.n1 <= 0 || a.n1 % kGM || a.n2 < a.n1 || a.n2 % kGM || a.n_all < a.n2 || a.w2.type != a.w.type ||
+        a.w3.type != a.w.type || a.w2.k != a.w.k || a.w3.k != a.w.k || a.w.n != a.n1 ||
+        (a.n2 > a.n1 && a.w2.n != a.n2 - a.n1) || (a.n_all > a.n2 && a.w3.n != a.n_all - a.n2))
+      return hipErrorInvalidValue;
+  }
+  if ((int64_t)a.t * N > region_cap) return hipErrorInvalidValue;
+  const int tiles = ((N + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
   // split K until about two workgroups per CU are busy
   constexpr int target = 512;
   int ks = tiles < target ? std::min(std::min(nst, kMaxDeferSplit), (target + tiles - 1) / tiles) : 1;
-  while (ks > 1 && (int64_t)ks * a.t * a.w.n > region_cap) --ks;
+  while (ks > 1 && (int64_t)ks * a.t * N > region_cap) --ks;
   a.ksplit = ks;
   a.part = region;
   a.defer = 1;
-  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, ks);
+  const dim3 grid((N + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, ks);
   const size_t sh = gemm_shared_bytes();
   switch (a.w.type) {
     case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
@@ -999,9 +1020,10 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
     default: return hipErrorInvalidValue;
   }
   out->p = region;
-  out->n = a.w.n;
+  out->n = N;
+  out->ld = N;
   out->ks = ks;
-  out->zs = (int64_t)a.t * a.w.n;
+  out->zs = (int64_t)a.t * N;
   return hipGetLastError();
 }
 
