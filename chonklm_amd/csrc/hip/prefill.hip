@@ -8,7 +8,7 @@
 //   W * 2^ws = Wh + Wl,  x * 2^rs = xh + xl  (per token row),
 //   sum W x = 2^-(ws+rs) * (Wh xh + Wh xl + Wl xh)   (Wl xl ~ 2^-22, dropped)
 // with the weights dequantized bit-exactly (dequant_unit) into LDS tiles and
-// the products accumulated in fp32 by v_mfma_f32_16x16x16_f16.
+// the products accumulated in fp32 by gfx950's v_mfma_f32_16x16x32_f16.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -28,8 +28,11 @@ constexpr int kGT = 64;          // token rows per workgroup tile
 constexpr int kGK = 128;         // K per stage (whole units for every type)
 constexpr int kGS = kGK + 8;     // LDS row stride in halves (bank spread)
 
-__device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+// gfx950's double-K shape: lane l holds row (or column) l % 16 and 8 consecutive
+// k of the 32 (the same k for both operands, so the product is the dot over k)
+__device__ __forceinline__ float4_t mfma32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 constexpr int kMaxDeferSplit = 16;  // K split of a deferred GEMM (loads of a sum issued together)
@@ -288,24 +291,24 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
     }
     __syncthreads();
     if (s + 1 < s_hi) fetch(s + 1);
-    const int col = lane & 15, kq = (lane >> 4) * 4;
+    const int col = lane & 15, kq = (lane >> 4) * 8;
 #pragma unroll
-    for (int ks = 0; ks < kGK / 16; ++ks) {
-      half4_t ah[2], al[2], bh[2], bl[2];
+    for (int ks = 0; ks < kGK / 32; ++ks) {
+      half8_t ah[2], al[2], bh[2], bl[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        ah[i] = *(const half4_t*)(wh + (rb + 16 * i + col) * kGS + ks * 16 + kq);
-        al[i] = *(const half4_t*)(wl + (rb + 16 * i + col) * kGS + ks * 16 + kq);
-        bh[i] = *(const half4_t*)(xh + (tb + 16 * i + col) * kGS + ks * 16 + kq);
-        bl[i] = *(const half4_t*)(xl + (tb + 16 * i + col) * kGS + ks * 16 + kq);
+        ah[i] = *(const half8_t*)(wh + (rb + 16 * i + col) * kGS + ks * 32 + kq);
+        al[i] = *(const half8_t*)(wl + (rb + 16 * i + col) * kGS + ks * 32 + kq);
+        bh[i] = *(const half8_t*)(xh + (tb + 16 * i + col) * kGS + ks * 32 + kq);
+        bl[i] = *(const half8_t*)(xl + (tb + 16 * i + col) * kGS + ks * 32 + kq);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          acc[i][j] = mfma16(ah[i], bh[j], acc[i][j]);
-          acc[i][j] = mfma16(ah[i], bl[j], acc[i][j]);
-          acc[i][j] = mfma16(al[i], bh[j], acc[i][j]);
+          acc[i][j] = mfma32(ah[i], bh[j], acc[i][j]);
+          acc[i][j] = mfma32(ah[i], bl[j], acc[i][j]);
+          acc[i][j] = mfma32(al[i], bh[j], acc[i][j]);
         }
     }
   }
@@ -620,16 +623,16 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   const __half* vc = (const __half*)a.kv.vc;
 
   // this lane's A-operand row of Q (row 16 * wave + col), hi and lo halves
-  half4_t qh[HD / 16], ql[HD / 16];
+  half8_t qh[HD / 32], ql[HD / 32];
   {
     const int r = 16 * wave + col, t = t0 + r / G;
     const bool ok = r < TW * G && t < a.rows;
     const float* q = a.qkv + (size_t)(ok ? t : 0) * a.ld + (kv * G + r % G) * HD;
 #pragma unroll
-    for (int k = 0; k < HD / 16; ++k) {
+    for (int k = 0; k < HD / 32; ++k) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = ok ? q[16 * k + 4 * quad + i] : 0.f;
+      for (int i = 0; i < 8; ++i) {
+        const float v = ok ? q[32 * k + 8 * quad + i] : 0.f;
         qh[k][i] = (_Float16)v;
         ql[k][i] = (_Float16)(v - (float)qh[k][i]);
       }
@@ -689,10 +692,10 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
     for (int kt = 0; kt < 4; ++kt) {
       s[kt] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < HD / 16; ++k) {
-        const half4_t b = *(const half4_t*)(ks + (16 * kt + col) * KS + 16 * k + 4 * quad);
-        s[kt] = mfma16(qh[k], b, s[kt]);
-        s[kt] = mfma16(ql[k], b, s[kt]);
+      for (int k = 0; k < HD / 32; ++k) {
+        const half8_t b = *(const half8_t*)(ks + (16 * kt + col) * KS + 32 * k + 8 * quad);
+        s[kt] = mfma32(qh[k], b, s[kt]);
+        s[kt] = mfma32(ql[k], b, s[kt]);
       }
     }
     // masked, scaled scores; block maximum per row (over the 16 lanes of a row group)
@@ -735,14 +738,14 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
     __builtin_amdgcn_wave_barrier();
     // O += P V over the block's 64 keys
 #pragma unroll
-    for (int kq = 0; kq < 4; ++kq) {
-      const half4_t ah = *(const half4_t*)(ph + col * PS + 16 * kq + 4 * quad);
-      const half4_t al = *(const half4_t*)(pl + col * PS + 16 * kq + 4 * quad);
+    for (int kq = 0; kq < kFaKeys / 32; ++kq) {
+      const half8_t ah = *(const half8_t*)(ph + col * PS + 32 * kq + 8 * quad);
+      const half8_t al = *(const half8_t*)(pl + col * PS + 32 * kq + 8 * quad);
 #pragma unroll
       for (int d = 0; d < HD / 16; ++d) {
-        const half4_t b = *(const half4_t*)(vt + (16 * d + col) * VS + 16 * kq + 4 * quad);
-        o[d] = mfma16(ah, b, o[d]);
-        o[d] = mfma16(al, b, o[d]);
+        const half8_t b = *(const half8_t*)(vt + (16 * d + col) * VS + 32 * kq + 8 * quad);
+        o[d] = mfma32(ah, b, o[d]);
+        o[d] = mfma32(al, b, o[d]);
       }
     }
   }
