@@ -173,6 +173,7 @@ struct LayerCfg {
   uint32_t theta = 10000;
   int window = 0;
   int heads = 0, kv_heads = 0, ffn = 0;  // openelm varies them per layer
+  bool conv = false;                     // lfm2: a gated short-convolution layer instead of attention
 };
 
 struct ModelCfg {
@@ -181,6 +182,7 @@ struct ModelCfg {
   bool openelm = false;  // fused attn_qkv, per-layer heads / kv heads / feed-forward width
   int gmax = 1;          // largest GQA group of any layer
   bool gpt = false;  // GGUF architecture gpt2: the reference's GPT runtime (gpt-wgsl-runtime.ts)
+  bool lfm = false;  // GGUF architecture lfm2: the reference's LFM runtime (lfm-wgsl-runtime.ts)
   int pos_rows = 0;  // gpt2: rows of the learned position table (gpt2.context_length)
   int hidden = 0, ffn = 0, vocab = 0, layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float eps = 1e-5f, qk_eps = 1e-5f, scale = 0, embed_scale = 1;
@@ -238,6 +240,66 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
     c.layer.assign(c.layers, LayerCfg{0, 0, c.heads, c.kv_heads, c.ffn});  // no rotary embedding
     if (c.layers <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
       throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+    return c;
+  }
+  if (c.arch == "lfm2") {
+    // The LFM runtime (lfm-wgsl-runtime.ts:313-340, :457-580) fixes the
+    // LFM2.5-350M shape in code; here the dimensions come from the file and the
+    // constants stay the reference's: eps 1e-5 on every RMSNorm (:1567-1639,
+    // :1763), rope base 1e6 with split halves (:1739-1742), three conv taps
+    // (:1641-1672), the embedding as lm_head (:512-519), context = the
+    // definition's maxContext (:461). A layer holding shortconv.conv.weight is
+    // a convolution layer (lfm2.attention.head_count_kv is 0 there).
+    c.lfm = true;
+    c.layers = (int)meta_number(g, "lfm2.block_count", nullptr);
+    c.hidden = (int)meta_number(g, "lfm2.embedding_length", nullptr);
+    c.ffn = (int)meta_number(g, "lfm2.feed_forward_length", nullptr);
+    c.heads = (int)meta_number(g, "lfm2.attention.head_count", nullptr);
+    std::vector<int> lkv;
+    const GgufValue* kv = g.value("lfm2.attention.head_count_kv");
+    if (kv && kv->type == GV_ARRAY) {
+      lkv = meta_array(g, "lfm2.attention.head_count_kv");
+      if ((int)lkv.size() != c.layers)
+        throw Error(CHONK_EINVAL, "LFM GGUF lfm2.attention.head_count_kv has " + std::to_string(lkv.size()) +
+                                      " entries for " + std::to_string(c.layers) + " layers");
+    } else {
+      lkv.assign((size_t)std::max(0, c.layers), (int)meta_number(g, "lfm2.attention.head_count_kv", nullptr));
+    }
+    const double hd_default = std::floor((double)c.hidden / std::max(1, c.heads));
+    c.hd = (int)meta_number(g, "lfm2.attention.key_length", &hd_default);
+    c.vocab = def.vocab;
+    c.ctx = def.max_context;
+    c.eps = c.qk_eps = 1e-5f;
+    c.qk_norm = true;
+    c.scale = (float)(1.0 / std::sqrt((double)c.hd));
+    c.kv_heads = 0;
+    for (int i = 0; i < c.layers; ++i) {
+      LayerCfg L;
+      L.theta = 1000000;
+      L.conv = g.find("blk." + std::to_string(i) + ".shortconv.conv.weight") != nullptr;
+      L.heads = c.heads;
+      L.kv_heads = L.conv ? c.heads : lkv[(size_t)i];  // (a convolution layer has no heads; kept valid)
+      L.ffn = c.ffn;
+      if (!L.conv) c.kv_heads = std::max(c.kv_heads, L.kv_heads);
+      c.layer.push_back(L);
+    }
+    if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.ctx <= 0)
+      throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+    if (c.kv_heads <= 0) throw Error(CHONK_EINVAL, "LFM GGUF has no attention layer");
+    for (LayerCfg& L : c.layer) {
+      if (L.conv) L.kv_heads = c.kv_heads;
+      if (L.kv_heads <= 0 || L.heads % L.kv_heads != 0 || L.heads / L.kv_heads > 8)
+        throw Error(CHONK_EINVAL, "GQA group size must divide heads and be at most 8");
+      c.gmax = std::max(c.gmax, L.heads / L.kv_heads);
+    }
+    if (c.hd != 32 && c.hd != 64 && c.hd != 128 && c.hd != 256)
+      throw Error(CHONK_EINVAL, "head_dim " + std::to_string(c.hd) + " is not supported (32, 64, 128 or 256)");
+    // the convolution prologue holds a row of at most 4096 channels in registers;
+    // the class-major lm_head gives each of the 256 argmax slots one workgroup
+    if (c.hidden > 4096 || c.hidden % 4 != 0)
+      throw Error(CHONK_EINVAL, "LFM hidden size must be a multiple of 4 and at most 4096");
+    if (c.vocab > 65536)
+      throw Error(CHONK_EINVAL, "LFM argmax supports at most 65536 vocab entries, got " + std::to_string(c.vocab));
     return c;
   }
   if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3" && c.arch != "openelm")
@@ -317,6 +379,9 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
 
 struct LayerDev {
   DevMat q, k, v, o, gate, up, down;
+  DevMat conv_in, conv_out;  // lfm2 convolution layer: in_proj (rows B | C | x) and out_proj
+  float* conv_w = nullptr;   // [hidden][3] taps
+  float *conv_s1 = nullptr, *conv_s2 = nullptr;  // B * x two positions and one position back
   DevMat qkv;  // gpt2: fused q|k|v
   // gpt2: LayerNorm biases (in_norm / post_norm hold the weights) and linear biases
   float *in_norm_b = nullptr, *post_norm_b = nullptr, *qkv_b = nullptr, *o_b = nullptr, *up_b = nullptr,
@@ -363,6 +428,7 @@ struct chonk_engine {
   // activations
   float *resA = nullptr, *resB = nullptr, *delta = nullptr, *qkv = nullptr, *attn = nullptr, *ff = nullptr,
         *logits = nullptr, *part = nullptr;
+  float* conv_proj = nullptr;  // lfm2: [3 * hidden] in_proj output of the current convolution layer
   Candidate* cand = nullptr;
   uint32_t* cnt = nullptr;
   void* uncached = nullptr;       // part + cnt, from the uncached pool
@@ -596,6 +662,67 @@ float* upload_floats(Arena& arena, const ByteSource& src, const GgufFile& g, con
   return p;
 }
 
+// The LFM loader's checks (lfm-wgsl-runtime.ts:313-431): a missing tensor, a
+// linear tensor that is not Q8_0 / Q4_K / Q6_K, a float tensor that is not
+// F32 / F16, each with the reference's wording.
+const GgufTensorInfo& lfm_tensor(const GgufFile& g, const std::string& name) {
+  const GgufTensorInfo* t = g.find(name);
+  if (!t) throw Error(CHONK_EINVAL, "LFM GGUF missing tensor " + name);
+  return *t;
+}
+
+const GgufTensorInfo& lfm_linear(const GgufFile& g, const std::string& name) {
+  const GgufTensorInfo& t = lfm_tensor(g, name);
+  if (t.type != GGML_Q8_0 && t.type != GGML_Q4_K && t.type != GGML_Q6_K)
+    throw Error(CHONK_EINVAL, "unsupported LFM GGUF linear tensor " + name + ": " + type_name(t.type));
+  return t;
+}
+
+float* lfm_floats(Arena& arena, const ByteSource& src, const GgufFile& g, const std::string& name, int64_t n) {
+  const GgufTensorInfo& t = lfm_tensor(g, name);
+  if (t.type != GGML_F32 && t.type != GGML_F16)
+    throw Error(CHONK_EINVAL, "LFM GGUF tensor " + name + " is " + type_name(t.type) + ", expected F32/F16");
+  return upload_floats(arena, src, g, name, n);
+}
+
+// Rows of the class-major lm_head copy: 256 classes (id mod 256) of
+// ceil(V / 256) rows each.
+int64_t class_rows(int64_t V) { return 256 * ((V + 255) / 256); }
+
+// The vocab x K matrix `t` stored class-major for the lm_head: physical row
+// c * R + j holds id j * 256 + c (R = ceil(V / 256); rows past V are zero
+// blocks, which decode to 0), so that one workgroup of R rows sees one
+// residue class in id order (TOPK256_WGSL's slot, lfm-wgsl-runtime.ts:1925-1947).
+DevMat upload_class_major(Arena& arena, const ByteSource& src, const GgufFile& g, const GgufTensorInfo& t,
+                          int64_t K, int64_t V) {
+  check_matrix(t, K, V);
+  std::vector<uint8_t> raw = read_tensor(src, g, t);
+  TypeTraits tt;
+  type_traits(t.type, &tt);
+  const size_t row_bytes = (size_t)(K / tt.block_elems) * tt.block_bytes;
+  const int64_t R = (V + 255) / 256, N = 256 * R;
+  std::vector<uint8_t> perm((size_t)N * row_bytes, 0);
+  for (int64_t c = 0; c < 256; ++c)
+    for (int64_t j = 0; j < R; ++j) {
+      const int64_t id = j * 256 + c;
+      if (id < V) std::memcpy(perm.data() + (size_t)(c * R + j) * row_bytes, raw.data() + (size_t)id * row_bytes, row_bytes);
+    }
+  const Stripes st = repack(t.type, perm.data(), N, K);
+  DevMat m;
+  m.q.type = (int32_t)t.type;
+  m.q.n = (int32_t)N;
+  m.q.k = (int32_t)K;
+  const uint8_t** dst[4] = {&m.q.s0, &m.q.s1, &m.q.s2, &m.q.s3};
+  for (int i = 0; i < 4; ++i) {
+    if (st.s[i].empty()) continue;
+    void* p = arena.take(st.s[i].size());
+    HIP_OK(hipMemcpy(p, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+    *dst[i] = (const uint8_t*)p;
+  }
+  m.gguf_bytes = (uint64_t)V * row_bytes;
+  return m;
+}
+
 // Device address of `scratch` on `device`, looked up once per device with
 // that device current (the caller has made it current).
 uint8_t* scratch_address(int device) {
@@ -653,17 +780,19 @@ void use_row_kernel(MvArgs& a) {
   // GPT-2's prologues and epilogues (LayerNorm, biases, GELU, clamped residual)
   // exist only in the row kernels
   bool needs_row = a.epi == EPI_GELU || a.pro == PRO_LN || a.pro == PRO_EMBED_LN || a.sanitize;
+  // (so are the lfm2 convolution prologue and state shift)
+  needs_row = needs_row || a.pro == PRO_CONV || a.conv_commit;
   for (int i = 0; i < a.nseg; ++i) needs_row = needs_row || a.seg[i].bias;
   if ((off && !needs_row) || a.epi == EPI_LOGITS) return;
   // the register-resident plain / norm prologues hold at most 4 float4 per thread
   // (GPT-2's wider ffn_down rows take the LDS-staged variant of its row kernel)
   if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg && !(needs_row && a.pro == PRO_PLAIN)) {
-    if (needs_row) throw Error(CHONK_EINVAL, "GPT-2 rows wider than 4096 need the plain prologue");
+    if (needs_row) throw Error(CHONK_EINVAL, "row-kernel prologues hold at most 4096 elements (the plain one excepted)");
     return;
   }
   for (int i = 0; i < a.nseg; ++i)
     if (a.seg[i].w.k / 32 > kRowUnits * 64) {
-      if (needs_row) throw Error(CHONK_EINVAL, "GPT-2 layers need rows of at most 8192 weights");
+      if (needs_row) throw Error(CHONK_EINVAL, "the row kernels take rows of at most 8192 weights");
       return;
     }
   // one unit per lane and >= 192 workgroups per segment; the three-segment
@@ -737,9 +866,61 @@ void build_steps(chonk_engine* e) {
     const std::string li = "L" + std::to_string(i) + ".";
     const LayerCfg& lc = c.layer[i];
     const int qdim = lc.heads * c.hd, kvdim = lc.kv_heads * c.hd, G = lc.heads / lc.kv_heads;
+    if (lc.conv) {
+      // LfmWgslEngine.runToken's convolution branch (lfm-wgsl-runtime.ts:740-744):
+      // in_proj with the operator norm as prologue, then out_proj whose
+      // prologue is CONV_BLOCK over this token's B | C | x and the layer's state
+      // (shifted afterwards by the gate|up launch) and whose epilogue adds the
+      // residual (opAddNorm's add)
+      {
+        Launch L;
+        MvArgs a = mv_base();
+        a.k = H;
+        a.nseg = 1;
+        plan_seg(a.seg[0], Ld.conv_in.q, 3 * H, false, 0);
+        a.seg[0].out = e->conv_proj;
+        a.epi = EPI_STORE;
+        a.w_norm = Ld.in_norm;
+        if (i == 0) {
+          a.pro = PRO_EMBED_NORM;
+          a.res_out = e->resA;
+        } else {
+          a.pro = PRO_NORM;
+          a.in = e->resA;
+        }
+        finish(L, a, a.seg[0].tile);
+        L.name = li + "inproj";
+        L.weight_bytes = Ld.conv_in.gguf_bytes + (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
+        L.layer = i;
+        steps.push_back(L);
+      }
+      {
+        Launch L;
+        MvArgs a = mv_base();
+        a.k = H;
+        a.nseg = 1;
+        plan_seg(a.seg[0], Ld.conv_out.q, H, false, 0);
+        a.pro = PRO_CONV;
+        a.conv_proj = e->conv_proj;
+        a.conv_w = Ld.conv_w;
+        a.conv_s1 = Ld.conv_s1;
+        a.conv_s2 = Ld.conv_s2;
+        a.conv_n = H;
+        a.epi = EPI_ADD;
+        a.seg[0].out = e->resB;
+        a.seg[0].add = e->resA;
+        finish(L, a, a.seg[0].tile);
+        L.name = li + "outproj";
+        L.weight_bytes = Ld.conv_out.gguf_bytes;
+        L.layer = i;
+        steps.push_back(L);
+      }
+    }
     // qkv (gpt2: one fused matrix with bias, LayerNorm prologue; embedding +
     // position on layer 0)
-    if (c.gpt) {
+    if (lc.conv) {
+      // (no attention in a convolution layer)
+    } else if (c.gpt) {
       Launch L;
       MvArgs a = mv_base();
       a.k = H;
@@ -806,7 +987,7 @@ void build_steps(chonk_engine* e) {
       steps.push_back(L);
     }
     // attention
-    {
+    if (!lc.conv) {
       Launch L;
       L.kind = Launch::ATTN;
       AttnArgs& t = L.at;
@@ -854,7 +1035,7 @@ void build_steps(chonk_engine* e) {
       steps.push_back(L);
     }
     // o projection
-    {
+    if (!lc.conv) {
       Launch L;
       MvArgs a = mv_base();
       a.k = qdim;
@@ -920,6 +1101,14 @@ void build_steps(chonk_engine* e) {
         a.in = e->resB;
         a.w_norm = Ld.post_norm;
       }
+      if (lc.conv) {
+        // every reader of the old state (out_proj) has finished: shift it
+        a.conv_commit = 1;
+        a.conv_proj = e->conv_proj;
+        a.conv_s1 = Ld.conv_s1;
+        a.conv_s2 = Ld.conv_s2;
+        a.conv_n = H;
+      }
       finish(L, a, 2 * a.seg[0].tile);
       L.name = li + "gateup";
       L.weight_bytes = Ld.gate.gguf_bytes + Ld.up.gguf_bytes;
@@ -969,6 +1158,12 @@ void build_steps(chonk_engine* e) {
     sg.tile = 256;
     sg.wg_begin = 0;
     sg.out = e->logits;
+    if (c.lfm) {
+      // class-major rows: workgroup c computes ids c, c + 256, ... (TOPK256's slot c)
+      sg.n_out = (int)class_rows(c.vocab);
+      sg.tile = sg.n_out / 256;
+      a.lfm_classes = 1;
+    }
     a.epi = EPI_LOGITS;
     a.w_norm = e->final_norm;
     a.gpt_argmax = c.gpt ? 1 : 0;
@@ -996,7 +1191,8 @@ void build_steps(chonk_engine* e) {
     L.kind = Launch::SEL;
     SelArgs& s = L.sel;
     s.cand = e->cand;
-    s.gpt_argmax = c.gpt ? 1 : 0;
+    // (ARGMAX_WGSL's stage over the 256 slots is the same strict-greater tree, lfm-wgsl-runtime.ts:1903-1922)
+    s.gpt_argmax = c.gpt || c.lfm ? 1 : 0;
     s.groups = e->groups;
     s.vocab = c.vocab;
     s.ctx = c.ctx;
@@ -1022,7 +1218,7 @@ bool build_step(chonk_engine* e) {
   const int G = c.heads / c.kv_heads;
   const bool kv16 = e->kv_elem == 2;
   if (c.gpt) return false;  // the persistent step runs the llama-family layer only
-  if (c.openelm) return false;  // and one head geometry for every layer
+  if (c.openelm || c.lfm) return false;  // and one head geometry, attention in every layer
   if (!step_supported(G, kv16)) return false;
   int cus = 0;
   HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
@@ -1442,8 +1638,15 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     wbytes += stripes_bytes(t.type, N, K);
   };
   auto vec_bytes = [&](int64_t n) { wbytes += align256((size_t)n * 4); };
-  mat_bytes("token_embd.weight", H, c.vocab);
-  if (!tied) mat_bytes(lm_name, H, c.vocab);
+  if (c.lfm) {
+    // the embedding, its class-major copy as lm_head, token_embd_norm
+    const GgufTensorInfo& te = lfm_linear(g, "token_embd.weight");
+    check_matrix(te, H, c.vocab);
+    wbytes += stripes_bytes(te.type, c.vocab, H) + stripes_bytes(te.type, class_rows(c.vocab), H);
+  } else {
+    mat_bytes("token_embd.weight", H, c.vocab);
+    if (!tied) mat_bytes(lm_name, H, c.vocab);
+  }
   vec_bytes(H);
   if (c.gpt) {
     if (tied) throw Error(CHONK_EINVAL, "GPT WGSL GGUF missing tensor output.weight");
@@ -1463,7 +1666,37 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       vec_bytes(H);
     }
   }
-  for (int i = 0; i < (c.gpt ? 0 : c.layers); ++i) {
+  for (int i = 0; i < (c.lfm ? c.layers : 0); ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    const LayerCfg& lc = c.layer[i];
+    auto lin = [&](const std::string& name, int64_t K, int64_t N) {
+      const GgufTensorInfo& t = lfm_linear(g, p + name);
+      check_matrix(t, K, N);
+      wbytes += stripes_bytes(t.type, N, K);
+    };
+    if (lc.conv) {
+      const GgufTensorInfo& cw = lfm_tensor(g, p + "shortconv.conv.weight");
+      if (cw.shape.size() != 2 || cw.shape[0] != 3 || (int64_t)cw.shape[1] != H)
+        throw Error(CHONK_EINVAL, "LFM GGUF tensor " + cw.name + " must be [3, " + std::to_string(H) + "]");
+      lin("shortconv.in_proj.weight", H, 3 * (int64_t)H);
+      lin("shortconv.out_proj.weight", H, H);
+      vec_bytes(3 * (int64_t)H);
+    } else {
+      lin("attn_q.weight", H, lc.heads * c.hd);
+      lin("attn_k.weight", H, lc.kv_heads * c.hd);
+      lin("attn_v.weight", H, lc.kv_heads * c.hd);
+      lin("attn_output.weight", lc.heads * c.hd, H);
+      vec_bytes(c.hd);
+      vec_bytes(c.hd);
+      vec_bytes(c.hd / 2);
+    }
+    lin("ffn_gate.weight", H, lc.ffn);
+    lin("ffn_up.weight", H, lc.ffn);
+    lin("ffn_down.weight", lc.ffn, H);
+    vec_bytes(H);
+    vec_bytes(H);
+  }
+  for (int i = 0; i < (c.gpt || c.lfm ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     const LayerCfg& lc = c.layer[i];
     const int lq = lc.heads * c.hd, lkv = lc.kv_heads * c.hd;
@@ -1493,7 +1726,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->weights.reserve(wbytes);
 
   // state arena: K/V cache + activations + bookkeeping
-  e->groups = (c.vocab + 255) / 256;
+  // (lfm2: one argmax slot per residue class, TOPK256_WGSL)
+  e->groups = c.lfm ? 256 : (c.vocab + 255) / 256;
+  int kv_layers = 0, conv_layers = 0;  // layers holding a K/V cache / a convolution state
+  for (const LayerCfg& lc : c.layer) (lc.conv ? conv_layers : kv_layers) += 1;
   // attention chunk: the smallest power of two >= 16 giving at most ~512
   // workgroups and at most 32 chunks over the whole context (the last chunk to
   // finish merges all chunks), capped by the kernel's limit for hd
@@ -1515,6 +1751,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     e->dnchunk = (c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk();
     for (const LayerCfg& lc : c.layer) {
       const int lg = lc.heads / lc.kv_heads;
+      if (lc.conv) continue;
       if (e->dec_attn && (!attn_dec_supported(lg, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) ||
                           attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, e->dnchunk)) <
                               lc.kv_heads * e->dnchunk))
@@ -1523,7 +1760,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   }
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
-  size_t sbytes = 2 * align256(kv_bytes) * c.layers;
+  size_t sbytes = 2 * align256(kv_bytes) * kv_layers;
+  sbytes += c.lfm ? align256((size_t)3 * H * 4) + 2 * align256((size_t)H * 4) * conv_layers : 0;
   sbytes += 3 * align256((size_t)H * 4) + align256((size_t)(qdim + 2 * kvdim) * 4) + align256((size_t)qdim * 4) +
             align256((size_t)c.ffn * 4) + align256((size_t)c.vocab * 4) +
             align256((size_t)e->groups * 8) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
@@ -1535,8 +1773,44 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
   // weights
   e->embed = upload_matrix(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
-  e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
-  e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
+  if (c.lfm) {
+    // LfmWgslEngine.create (:501-580): the embedding doubles as the lm_head
+    e->lm_head = upload_class_major(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
+    e->final_norm = lfm_floats(e->weights, *src, g, "token_embd_norm.weight", H);
+  } else {
+    e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
+    e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
+  }
+  for (int i = 0; i < (c.lfm ? c.layers : 0); ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    const LayerCfg& lc = c.layer[i];
+    LayerDev L;
+    auto lin = [&](const std::string& name, int64_t K, int64_t N) {
+      return upload_matrix(e->weights, *src, g, lfm_linear(g, p + name), K, N);
+    };
+    L.in_norm = lfm_floats(e->weights, *src, g, p + "attn_norm.weight", H);
+    L.post_norm = lfm_floats(e->weights, *src, g, p + "ffn_norm.weight", H);
+    if (lc.conv) {
+      L.conv_w = lfm_floats(e->weights, *src, g, p + "shortconv.conv.weight", 3 * (int64_t)H);
+      L.conv_in = lin("shortconv.in_proj.weight", H, 3 * (int64_t)H);
+      L.conv_out = lin("shortconv.out_proj.weight", H, H);
+    } else {
+      L.q_norm = lfm_floats(e->weights, *src, g, p + "attn_q_norm.weight", c.hd);
+      L.k_norm = lfm_floats(e->weights, *src, g, p + "attn_k_norm.weight", c.hd);
+      L.q = lin("attn_q.weight", H, lc.heads * c.hd);
+      L.k = lin("attn_k.weight", H, lc.kv_heads * c.hd);
+      L.v = lin("attn_v.weight", H, lc.kv_heads * c.hd);
+      L.o = lin("attn_output.weight", lc.heads * c.hd, H);
+      L.kc = e->state.take(kv_bytes);
+      L.vc = e->state.take(kv_bytes);
+    }
+    L.gate = lin("ffn_gate.weight", H, lc.ffn);
+    L.up = lin("ffn_up.weight", H, lc.ffn);
+    L.down = lin("ffn_down.weight", lc.ffn, H);
+    if (L.gate.q.type != L.up.q.type)
+      throw Error(CHONK_EINVAL, "ffn_gate and ffn_up of layer " + std::to_string(i) + " have different types");
+    e->layers.push_back(L);
+  }
   if (c.gpt) {
     // GptWgslEngine buffers (gpt-wgsl-runtime.ts:540-640)
     e->final_norm_b = upload_floats(e->weights, *src, g, "output_norm.bias", H);
@@ -1561,7 +1835,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       e->layers.push_back(L);
     }
   }
-  for (int i = 0; i < (c.gpt ? 0 : c.layers); ++i) {
+  for (int i = 0; i < (c.gpt || c.lfm ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     LayerDev L;
     L.in_norm = upload_floats(e->weights, *src, g, p + "attn_norm.weight", H);
@@ -1597,7 +1871,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   for (const LayerDev& L : e->layers)
     wpt += L.q.gguf_bytes + L.k.gguf_bytes + L.v.gguf_bytes + L.qkv.gguf_bytes + L.o.gguf_bytes + L.gate.gguf_bytes +
            L.up.gguf_bytes + L.down.gguf_bytes + (uint64_t)H * 4 * (c.gemma || c.gpt ? 4 : 2) +
-           (c.qk_norm ? 2ull * c.hd * 4 : 0) + (c.gpt ? 4ull * (5 * (uint64_t)H + c.ffn) : 0);
+           (c.qk_norm && !L.conv_w ? 2ull * c.hd * 4 : 0) + (c.gpt ? 4ull * (5 * (uint64_t)H + c.ffn) : 0) +
+           L.conv_in.gguf_bytes + L.conv_out.gguf_bytes + (L.conv_w ? 12ull * H : 0);
   if (c.gpt) wpt += 8ull * H;  // final LayerNorm bias, the position row
   e->weight_bytes_per_token = wpt;
 
@@ -1609,6 +1884,15 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->ff = (float*)e->state.take((size_t)c.ffn * 4);
   e->logits = (float*)e->state.take((size_t)c.vocab * 4);
   e->cand = (Candidate*)e->state.take((size_t)e->groups * 8);
+  if (c.lfm) {
+    // the convolution states start at zero with the rest of this region
+    e->conv_proj = (float*)e->state.take((size_t)3 * H * 4);
+    for (size_t i = 0; i < e->layers.size(); ++i) {
+      if (!c.layer[i].conv) continue;
+      e->layers[i].conv_s1 = (float*)e->state.take((size_t)H * 4);
+      e->layers[i].conv_s2 = (float*)e->state.take((size_t)H * 4);
+    }
+  }
   {
     const size_t rowf = ((size_t)G * (c.hd + 2) + 3) & ~(size_t)3;
     const size_t part_bytes = align256((size_t)c.kv_heads * std::max(e->nchunk, e->dnchunk) * rowf * 4);
@@ -1624,10 +1908,11 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   e->gen = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
   e->pen_bits = (uint32_t*)e->state.take(bits_words * 4);
   e->seen_bits = (uint32_t*)e->state.take(bits_words * 4);
-  HIP_OK(hipMemset((void*)e->resA, 0, e->state.capacity() - 2 * align256(kv_bytes) * c.layers));
+  HIP_OK(hipMemset((void*)e->resA, 0, e->state.capacity() - 2 * align256(kv_bytes) * kv_layers));
   // chunk rows start with tag 0xffffffff, which no launch uses (epochs start at 0)
   if (e->dpart) HIP_OK(hipMemset(e->dpart, 0xff, dpart_bytes));
   for (const LayerDev& L : e->layers) {
+    if (!L.kc) continue;
     HIP_OK(hipMemset(L.kc, 0, kv_bytes));
     HIP_OK(hipMemset(L.vc, 0, kv_bytes));
   }
@@ -1649,7 +1934,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
   // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
-  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt &&
+  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt && !c.lfm &&
                        std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) <= 4096;
   // the no-allocation prompt pass: as many rows (a multiple of 16, at most one
   // full pass) as fit the scratch with this model's row buffers
@@ -1713,6 +1998,9 @@ DevSampling make_sampling(chonk_engine* e, const chonk_sampling* s, bool stage1,
   d.top_k = top_k;
   d.seed = s ? s->seed : 0;
   d.sample_mode = (temperature > 0 || top_p < 1 || top_k > 0) ? 1 : 0;  // needsSamplingReadback
+  // the LFM runtime also takes the candidate path for any penalty other than 1
+  // (needsCandidateReadback, sampling.ts:18-21; lfm-wgsl-runtime.ts:787-806)
+  if (e->cfg.lfm && rp != 1.0) d.sample_mode = 1;
   // the caller decides: llama applies the list when rp > 1 (:1649-1661), the
   // GPT-2 runtime whenever rp != 1 (gpt-wgsl-runtime.ts:789-798)
   d.stage1_penalty = stage1 ? 1 : 0;
@@ -1751,6 +2039,13 @@ void put_token(chonk_engine* e, int position, int32_t token) {
   e->known_token = token;
 }
 
+// The context error in the wording of the engine's runtime
+// (llama-wgsl-runtime.ts:1032, gpt-wgsl-runtime.ts:751-753, lfm-wgsl-runtime.ts:732-734).
+Error context_exhausted(const chonk_engine* e) {
+  const char* name = e->cfg.gpt ? "GPT" : e->cfg.lfm ? "LFM" : "Llama";
+  return Error(CHONK_ECONTEXT, std::string(name) + " WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+}
+
 void check_token(const chonk_engine* e, int32_t token) {
   if (token < 0 || token >= e->cfg.vocab)
     throw Error(CHONK_EINVAL, "token id " + std::to_string(token) + " outside embedding table");
@@ -1760,8 +2055,14 @@ void engine_reset(chonk_engine* e) {
   HIP_OK(hipStreamSynchronize(e->stream));
   const size_t kv_bytes = (size_t)e->cfg.kv_heads * e->cfg.hd * e->cfg.ctx * e->kv_elem;
   for (const LayerDev& L : e->layers) {
-    HIP_OK(hipMemsetAsync(L.kc, 0, kv_bytes, e->stream));
-    HIP_OK(hipMemsetAsync(L.vc, 0, kv_bytes, e->stream));
+    if (L.kc) {
+      HIP_OK(hipMemsetAsync(L.kc, 0, kv_bytes, e->stream));
+      HIP_OK(hipMemsetAsync(L.vc, 0, kv_bytes, e->stream));
+    }
+    if (L.conv_s1) {  // LfmWgslEngine.reset clears each convolution state (:711-724)
+      HIP_OK(hipMemsetAsync(L.conv_s1, 0, (size_t)e->cfg.hidden * 4, e->stream));
+      HIP_OK(hipMemsetAsync(L.conv_s2, 0, (size_t)e->cfg.hidden * 4, e->stream));
+    }
   }
   DevState s{};
   upload_state_fields(e, s);
@@ -2119,7 +2420,7 @@ void prefill_rows_in(chonk_engine* e, const RowBufs& b, const int32_t* tokens, i
   const ModelCfg& c = e->cfg;
   if (n <= 0) return;
   if ((int64_t)e->pos + n > c.ctx)
-    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    throw context_exhausted(e);
   RowKv kvs;
   for (const LayerDev& L : e->layers) {
     kvs.kc.push_back(L.kc);
@@ -2139,15 +2440,15 @@ void prefill_rows_in(chonk_engine* e, const RowBufs& b, const int32_t* tokens, i
 int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_sampling* s, const int32_t* pen,
                   size_t n_pen, const int32_t* seen, size_t n_seen) {
   if (e->pos >= e->cfg.ctx)
-    throw Error(CHONK_ECONTEXT, std::string(e->cfg.gpt ? "GPT" : "Llama") + " WGSL context exhausted at " +
-                                    std::to_string(e->cfg.ctx) + " tokens");
+    throw context_exhausted(e);
   check_token(e, token);
   put_token(e, e->pos, token);
   if (need_logits) {
     // argmax(): the penalty list is the last `context` ids (:1649-1653)
     const double rp = s ? s->repetition_penalty : 1.0;
     // (the GPT-2 runtime applies the list whenever the penalty is not 1, :785-796)
-    const bool stage1 = (e->cfg.gpt ? rp != 1.0 : rp > 1) && n_pen > 0;
+    // (the LFM runtime has no penalty list: its penalty acts on the candidates)
+    const bool stage1 = !e->cfg.lfm && (e->cfg.gpt ? rp != 1.0 : rp > 1) && n_pen > 0;
     const size_t keep = std::min(n_pen, (size_t)e->cfg.ctx);
     if (stage1) upload_bits(e, e->pen_bits, pen + (n_pen - keep), keep);
     const DevSampling d = make_sampling(e, s, stage1, n_seen > 0);
@@ -2182,16 +2483,16 @@ double now_ms() {
 
 // generateLlamaWgsl's option defaults (:255-262): temperature 0, topP 1,
 // topK 0, repetitionPenalty = opts ?? def.defaultRepetitionPenalty ?? 1
-// (a non-positive or non-finite value means "not given"). generateGptWgsl
-// takes opts.repetitionPenalty ?? 1 and ignores the definition's default
-// (gpt-wgsl-runtime.ts:198-203).
+// (a non-positive or non-finite value means "not given"). generateGptWgsl and
+// generateLfmWgsl take opts.repetitionPenalty ?? 1 and ignore the definition's
+// default (gpt-wgsl-runtime.ts:198-203, lfm-wgsl-runtime.ts:236-241).
 chonk_sampling effective_sampling(const chonk_engine* e, const chonk_sampling* s_in) {
   chonk_sampling s{};
   s.temperature = 0;
   s.top_p = 1;
   s.top_k = 0;
   s.repetition_penalty =
-      (!e->cfg.gpt && e->def.default_repetition_penalty > 0) ? e->def.default_repetition_penalty : 1.0;
+      (!e->cfg.gpt && !e->cfg.lfm && e->def.default_repetition_penalty > 0) ? e->def.default_repetition_penalty : 1.0;
   if (s_in) {
     s.temperature = s_in->temperature;
     s.top_p = s_in->top_p;
@@ -2219,11 +2520,11 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
   }
   const size_t n_suffix = n_prompt - (size_t)prefix;
   if ((int64_t)e->pos + (int64_t)n_suffix > c.ctx)
-    throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    throw context_exhausted(e);
   auto is_eos = [&](int32_t id) { return std::find(e->eos.begin(), e->eos.end(), id) != e->eos.end(); };
 
   // penalty list = prompt (+ generated ids, appended on the device)
-  const bool stage1 = s.repetition_penalty > 1;
+  const bool stage1 = !c.lfm && s.repetition_penalty > 1;
   DevSampling d = make_sampling(e, &s, stage1, true);
   if (stage1 || d.seen_penalty) {
     upload_bits(e, e->pen_bits, prompt, n_prompt);
@@ -2295,6 +2596,18 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
       HIP_OK(hipMemcpy(generated.data(), e->gen, generated.size() * 4, hipMemcpyDeviceToHost));
     e->pos = st.pos;
     next = generated.empty() ? next : generated.back();
+    if (c.lfm && !generated.empty() && !is_eos(generated.back())) {
+      // generateLfmWgsl also runs the last generated id (lfm-wgsl-runtime.ts:288-300):
+      // its pick is the cached next id; the device holds that id at hist[pos]
+      st.generating = 0;
+      st.stopped = 0;
+      upload_state_fields(e, st);
+      replay(e, true);
+      st = read_state(e);
+      if (st.error) throw device_error(e, st);
+      e->pos = st.pos;
+      next = st.last_token;
+    }
   }
   // leave the device in API mode
   st.generating = 0;
@@ -2336,7 +2649,7 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
   }
   int32_t next = 0;
   const size_t n_suffix = n_prompt - (size_t)prefix;
-  const bool gpt = e->cfg.gpt;
+  const bool gpt = e->cfg.gpt, lfm = e->cfg.lfm;
   if (n_suffix == 0 && gpt && !e->has_cached_next)
     throw Error(CHONK_EINVAL, "GPT WGSL has no cached next token for an empty prompt");
   if (n_suffix == 0 && e->has_cached_next) {
@@ -2358,9 +2671,10 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
     ids.push_back(next);
     if (cb) cb(user, 1, next);
     if (is_eos(next)) break;
-    // (generateGptWgsl, gpt-wgsl-runtime.ts:228-245, also runs the token after
-    // the last generated one: its result is the cached next id)
-    if (step + 1 >= max && !gpt) break;
+    // (generateGptWgsl, gpt-wgsl-runtime.ts:228-245, and generateLfmWgsl,
+    // lfm-wgsl-runtime.ts:288-300, also run the token after the last generated
+    // one: its result is the cached next id)
+    if (step + 1 >= max && !gpt && !lfm) break;
     next = run_token(e, next, true, &s, ids.data(), ids.size(), ids.data(), ids.size());
   }
   const double t_end = now_ms();
@@ -2388,7 +2702,7 @@ namespace {
 std::vector<uint64_t> trace_step(chonk_engine* e, int* np_out, int* grid_out) {
   if (!e->use_step) throw Error(CHONK_EINVAL, "the engine does not run the persistent step");
   const ModelCfg& c = e->cfg;
-  if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+  if (e->pos >= c.ctx) throw context_exhausted(e);
   const Launch& L = e->step_logits[0];
   const int np = L.step.n_phases, grid = L.grid;
   const size_t words = (size_t)(np + 1) * grid + (size_t)np * grid * kStepStamps;
@@ -2471,7 +2785,8 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->kv_heads = c.kv_heads;
   out->head_dim = c.hd;
   out->context = c.ctx;
-  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : c.arch == "gpt2" ? 3 : 4;
+  out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : c.arch == "gpt2" ? 3
+                      : c.arch == "openelm" ? 4 : 5;
   out->qk_norm = c.qk_norm;
   out->interleaved_rope = c.interleaved;
   out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;
@@ -2499,7 +2814,7 @@ int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n) {
     if (!tokens) throw Error(CHONK_EINVAL, "tokens is null");
     for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
     if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
-      throw Error(CHONK_ECONTEXT, std::string(e->cfg.gpt ? "GPT" : "Llama") + " WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+      throw context_exhausted(e);
     if (!e->batched_prefill) {
       // token by token through the decode step (gpt2, or CHONK_PREFILL=token)
       for (size_t i = 0; i < n; ++i) run_token(e, tokens[i], false, nullptr, nullptr, 0, nullptr, 0);
@@ -2533,7 +2848,7 @@ int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t 
                                     std::to_string(n));
     for (size_t i = 0; i < n; ++i) check_token(e, tokens[i]);
     if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
-      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
+      throw context_exhausted(e);
     // every row buffer is written before it is read (the operand split writes
     // its own zero padding), so the previous call's contents need no clearing
     RowBufs b;
@@ -2655,6 +2970,7 @@ int chonk_engine_read_kv(chonk_engine* e, int32_t layer, int32_t is_value, int32
     if (layer < 0 || layer >= c.layers || pos < 0 || pos >= c.ctx || !out) throw Error(CHONK_EINVAL, "bad layer/position");
     HIP_OK(hipStreamSynchronize(e->stream));
     const LayerDev& L = e->layers[layer];
+    if (!L.kc) throw Error(CHONK_EINVAL, "layer " + std::to_string(layer) + " is a convolution layer (no K/V cache)");
     const uint8_t* base = (const uint8_t*)(is_value ? L.vc : L.kc);
     std::vector<uint8_t> row((size_t)c.hd * e->kv_elem);
     for (int h = 0; h < c.kv_heads; ++h) {
@@ -2678,7 +2994,8 @@ int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed) {
     const ModelCfg& c = e->cfg;
     if (pos < 0 || pos >= c.ctx) throw Error(CHONK_EINVAL, "position outside the context");
     for (int i = 0; i < c.layers; ++i)
-      HIP_OK(launch_fill_kv(e->layers[i].kc, e->layers[i].vc, c.layer[i].kv_heads, c.ctx, c.hd, pos, e->kv_elem == 2,
+      if (e->layers[i].kc)  // (lfm2 convolution layers keep only their zero state)
+        HIP_OK(launch_fill_kv(e->layers[i].kc, e->layers[i].vc, c.layer[i].kv_heads, c.ctx, c.hd, pos, e->kv_elem == 2,
                             seed + 1000003ull * i, e->stream));
     DevState st{};
     st.pos = pos;
@@ -2695,7 +3012,7 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
     const ModelCfg& c = e->cfg;
     if (n_warmup < 0 || n_steps <= 0) throw Error(CHONK_EINVAL, "bad step counts");
     if ((int64_t)e->pos + n_warmup + n_steps > c.ctx)
-      throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+      throw context_exhausted(e);
     DevSampling d = make_sampling(e, nullptr, false, false);
     upload_sampling(e, d);
     // the history slot at the current position must hold a token
@@ -2739,7 +3056,7 @@ int chonk_engine_time_kernels(chonk_engine* e, const int32_t* ids, int32_t n_ids
       if (L.kind == Launch::MV) L.mv.advance_pos = 0;
       run.push_back(L);
     }
-    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    if (e->pos >= c.ctx) throw context_exhausted(e);
     const DevState saved = read_state(e);
     DevState st = saved;
     st.stopped = 0;
@@ -2802,7 +3119,7 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
     const Launch& L = e->kernels_logits[(size_t)kernel_id];
     if (reps > 0 && L.kind == Launch::SEL)
       throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
-    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    if (e->pos >= c.ctx) throw context_exhausted(e);
     if (avg_us) *avg_us = 0.0;
     if (reps > 0) {
     const DevState saved = read_state(e);
@@ -2854,7 +3171,7 @@ int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t r
       throw Error(CHONK_EINVAL, "bad kernel id or repetitions");
     const Launch& L = e->kernels_logits[(size_t)kernel_id];
     if (L.kind == Launch::SEL) throw Error(CHONK_EINVAL, "the select kernel advances the position; not timed alone");
-    if (e->pos >= c.ctx) throw Error(CHONK_ECONTEXT, "Llama WGSL context exhausted at " + std::to_string(c.ctx) + " tokens");
+    if (e->pos >= c.ctx) throw context_exhausted(e);
     flush_bytes = std::max<uint64_t>(flush_bytes, (uint64_t)512 << 20);
     if (e->flush_bytes < flush_bytes) {
       if (e->flush) HIP_OK(hipFree(e->flush));
@@ -3187,6 +3504,7 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
   if (std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) > 4096)
     throw Error(CHONK_EINVAL, "batched decoding needs hidden, q and ffn widths of at most 4096");
   if (c.gpt) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not gpt2");
+  if (c.lfm) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not lfm2");
   if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
   if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
   if (c.openelm) throw Error(CHONK_EINVAL, "batched decoding needs one head geometry for every layer (not openelm)");

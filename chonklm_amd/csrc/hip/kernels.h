@@ -25,6 +25,7 @@ enum ProMode : int32_t {
   PRO_RES_NORM = 3,      // r = clamp(in + rmsnorm(delta) * w_delta, +-65000); WG0 writes r; xs = rmsnorm(r) * w_norm
   PRO_LN = 5,            // xs = layernorm(in) * w_norm + norm_b (GPT-2)
   PRO_EMBED_LN = 6,      // r = embed(hist[pos]) + pos_embd[pos]; WG0 writes r; xs = layernorm(r) * w_norm + norm_b
+  PRO_CONV = 7,          // xs = C * (s1 * w0 + s2 * w1 + (B * x) * w2), B | C | x = conv_proj (lfm2)
 };
 
 enum EpiMode : int32_t {
@@ -32,7 +33,7 @@ enum EpiMode : int32_t {
   EPI_ADD = 1,      // out[n] = add[n] + acc
   EPI_GLU_SILU = 2, // out[n] = silu(gate_n) * up_n
   EPI_GLU_GELU = 3, // out[n] = gelu_tanh(gate_n) * up_n
-  EPI_LOGITS = 4,   // logits[n] = acc; group candidate per 256 rows
+  EPI_LOGITS = 4,   // logits[n] = acc; group candidate per 256 rows (lfm2: per residue class mod 256)
   EPI_GELU = 5,     // out[n] = gelu_tanh(acc + bias[n]) (GPT-2 MLP up projection)
 };
 
@@ -74,6 +75,16 @@ struct MvArgs {
   const DevSampling* samp;
   Candidate* cand;
   DevState* st;
+  // lfm2 short convolution: the PRO_CONV prologue reads the state, a later
+  // launch of the same layer (conv_commit) shifts it once every reader is done
+  const float* conv_proj;  // [3 * conv_n] this token's in_proj rows B | C | x
+  const float* conv_w;     // [conv_n][3] depthwise taps
+  float* conv_s1;          // [conv_n] B * x two positions back
+  float* conv_s2;          // [conv_n] B * x one position back
+  int32_t conv_n;          // channels (the hidden size)
+  int32_t conv_commit;     // WG0 sets s1 = s2, s2 = B * x
+  int32_t lfm_classes;     // EPI_LOGITS: rows stored class-major, workgroup c computes ids c, c + 256, ...
+  int32_t pad_lfm;
 };
 
 struct AttnArgs {

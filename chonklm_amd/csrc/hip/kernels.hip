@@ -289,8 +289,10 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
       float* vals = res + 256;
       uint32_t* idx = (uint32_t*)(vals + 256);
       float v = kNegBig;
-      uint32_t id = a.gpt_argmax ? 0u : 0xffffffffu;
-      const int row = t0 + tid;
+      uint32_t id = (a.gpt_argmax || a.lfm_classes) ? 0u : 0xffffffffu;
+      // lfm2: the rows are stored class-major, so workgroup c holds ids c,
+      // c + 256, ... in order and its candidate is TOPK256_WGSL's slot c
+      const int row = a.lfm_classes ? tid * 256 + ((int)blockIdx.x - g.wg_begin) : t0 + tid;
       if (tid < nt && row < a.vocab) {
         v = res[tid];
         g.out[row] = v;
@@ -299,6 +301,12 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
           v = v > 0.0f ? __fdiv_rn(v, p) : __fmul_rn(v, p);
         }
         id = (uint32_t)row;
+        // (the slot's scan starts from (-3.402823e38, 0) and only a strictly
+        // greater logit replaces it: NaN and values at or below it never do)
+        if (a.lfm_classes && !(v > kNegBig)) {
+          v = kNegBig;
+          id = 0u;
+        }
       }
       vals[tid] = v;
       idx[tid] = id;
@@ -330,6 +338,36 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   CHONK_MV_TRACE_END(tr, EPI * 65536 + a.k);
 }
 
+// CONV_BLOCK_WGSL (lfm-wgsl-runtime.ts:1641-1672) for channels 4*i4 .. 4*i4+3:
+// cur = B * x, conv = (s1 * w0 + s2 * w1) + cur * w2, out = C * conv, every
+// product and sum rounded once as written. proj holds B | C | x (n channels
+// each); the taps are [n][3], so four channels' twelve taps are three float4.
+__device__ __forceinline__ float4 conv_block4(const float* proj, const float* s1, const float* s2, const float* w,
+                                              int n, int i4) {
+  const float4 B = ldg4f(proj + 4 * i4), C = ldg4f(proj + n + 4 * i4), X = ldg4f(proj + 2 * n + 4 * i4);
+  const float4 p1 = ldg4f(s1 + 4 * i4), p2 = ldg4f(s2 + 4 * i4);
+  const float4 wa = ldg4f(w + 12 * i4), wb = ldg4f(w + 12 * i4 + 4), wc = ldg4f(w + 12 * i4 + 8);
+  auto ch = [](float b, float c, float x, float q1, float q2, float w0, float w1, float w2) {
+    const float cur = __fmul_rn(b, x);
+    const float conv = __fadd_rn(__fadd_rn(__fmul_rn(q1, w0), __fmul_rn(q2, w1)), __fmul_rn(cur, w2));
+    return __fmul_rn(c, conv);
+  };
+  return make_float4(ch(B.x, C.x, X.x, p1.x, p2.x, wa.x, wa.y, wa.z), ch(B.y, C.y, X.y, p1.y, p2.y, wa.w, wb.x, wb.y),
+                     ch(B.z, C.z, X.z, p1.z, p2.z, wb.z, wb.w, wc.x), ch(B.w, C.w, X.w, p1.w, p2.w, wc.y, wc.z, wc.w));
+}
+
+// The state shift of CONV_BLOCK_WGSL (state[s] = p1, state[s+1] = p2,
+// state[s+2] = cur: only the last two are ever read back), run by one
+// workgroup of a launch that follows every reader of the old state.
+__device__ __forceinline__ void conv_commit(const float* proj, float* s1, float* s2, int n) {
+  for (int i = (int)threadIdx.x; i < n; i += kWg) {
+    const float cur = __fmul_rn(proj[i], proj[2 * n + i]);
+    const float prev = s2[i];
+    s1[i] = prev;
+    s2[i] = cur;
+  }
+}
+
 // One output row per lane group: lane group lg of lpr lanes owns row t0 + lg
 // (GLU: both the gate and the up row), lane li owns units li, li + lpr, ...
 // (at most kRowUnits). Every address is computed once, the weight loads are
@@ -358,9 +396,9 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   CHONK_MV_T(tr, 0);
   MvPro p = mv_pro(a);
   p.pro = PRO;
-  // plain and norm prologues keep x (and the norm weight) in registers: thread
-  // t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
-  constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM) && GB != 2;
+  // plain, norm and convolution prologues keep x (and the norm weight) in
+  // registers: thread t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
+  constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM || PRO == PRO_CONV) && GB != 2;
   const int n4 = a.k >> 2;
   float4 xv[4], wv[4];
 #pragma unroll
@@ -370,8 +408,12 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     for (int r = 0; r < 4; ++r) {
       const int i4 = (int)threadIdx.x + kWg * r;
       if (i4 < n4) {
-        xv[r] = ldg4f(p.in + 4 * i4);
-        if constexpr (PRO == PRO_NORM) wv[r] = ldg4f(p.w_norm + 4 * i4);
+        if constexpr (PRO == PRO_CONV) {
+          xv[r] = conv_block4(a.conv_proj, a.conv_s1, a.conv_s2, a.conv_w, a.k, i4);
+        } else {
+          xv[r] = ldg4f(p.in + 4 * i4);
+          if constexpr (PRO == PRO_NORM) wv[r] = ldg4f(p.w_norm + 4 * i4);
+        }
       }
     }
   } else {
@@ -452,6 +494,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     live = true;
   });
   if (!live) return;
+  if (a.conv_commit && blockIdx.x == 0) conv_commit(a.conv_proj, a.conv_s1, a.conv_s2, a.conv_n);
   if (owner) {
     if constexpr (GB) {
       if (g.bias) rg = __fadd_rn(rg, biasv);
@@ -478,6 +521,7 @@ CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM, 0)
 CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, 0)
 CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM, 0)
 CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN, 0)
+CHONK_MVR(k_mvr_add_conv, EPI_ADD, PRO_CONV, 0)
 CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM, 0)
 CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM, 0)
 CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM, 0)
@@ -694,7 +738,8 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[41] = {
+  const void* fns[42] = {
+      (const void*)k_mvr_add_conv,
       (const void*)k_mvr_add_bias,           (const void*)k_mvr_add_bias_wide,
       (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
       (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
@@ -735,6 +780,10 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
       case EPI_STORE * 8 + PRO_RES_NORM: k = k_mvr_store_resnorm; break;
       case EPI_ADD * 8 + PRO_PLAIN:
         k = !gb ? k_mvr_add_plain : a.k > 4 * 4 * kWg ? k_mvr_add_bias_wide : k_mvr_add_bias;
+        break;
+      case EPI_ADD * 8 + PRO_CONV:
+        if (gb || a.k > 4 * 4 * kWg) return hipErrorInvalidValue;
+        k = k_mvr_add_conv;
         break;
       case EPI_GLU_SILU * 8 + PRO_NORM: k = k_mvr_swiglu_norm; break;
       case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;

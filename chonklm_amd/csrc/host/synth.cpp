@@ -11,7 +11,12 @@
 //   context_length, rope.freq_base, attention.layer_norm_rms_epsilon},
 //   gemma3.attention.sliding_window. Architecture openelm has one fused
 //   blk.N.attn_qkv per layer (rows q | k | v) and per-layer head, kv-head and
-//   feed-forward counts as metadata arrays (:331-416).
+//   feed-forward counts as metadata arrays (:331-416). Architecture lfm2
+//   follows the LFM runtime's loader (src/lib/lfm-wgsl-runtime.ts:505-560):
+//   blk.N.shortconv.{conv, in_proj, out_proj}.weight on convolution layers,
+//   blk.N.attn_{q, k, v, output, q_norm, k_norm}.weight on attention layers,
+//   token_embd_norm.weight as the final norm; the layer kinds are written as
+//   lfm2.attention.head_count_kv, one entry per layer, 0 on convolution layers.
 // Type recipe (Q4_K_M): llama.cpp's llama_tensor_get_type as restated in the
 // header of synth.h. Architecture gpt2 follows the GPT runtime's manifest
 // (src/lib/gpt-wgsl-runtime.ts:274-356; gpt2_plan below).
@@ -53,6 +58,10 @@ inline float normal_at(uint64_t stream, uint64_t i) {
   const double u2 = (b >> 11) * (1.0 / 9007199254740992.0);        // [0, 1)
   return (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
 }
+
+// Standard deviation of the synthetic short-convolution taps: large enough that
+// the convolution branch moves the residual stream.
+constexpr float kLfmConvStd = 0.5f;
 
 bool use_more_bits(int i, int n) { return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2; }
 
@@ -133,29 +142,32 @@ std::vector<TensorPlan> gpt2_plan(const SynthConfig& c) {
 
 void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_threads) {
   const std::string& a = c.arch;
-  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2" && a != "openelm")
+  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2" && a != "openelm" && a != "lfm2")
     throw std::runtime_error("synthetic writer: unsupported arch " + a);
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0)
     throw std::runtime_error("synthetic writer: non-positive dimension");
-  const bool openelm = a == "openelm";
-  auto per_layer = [&](const std::vector<int>& v, int fallback, const char* what) {
+  const bool openelm = a == "openelm", lfm = a == "lfm2";
+  auto per_layer = [&](const std::vector<int>& v, int fallback, const char* what, bool zero_ok) {
     if (v.empty()) return std::vector<int>((size_t)c.layers, fallback);
-    if (!openelm) throw std::runtime_error(std::string("synthetic writer: per-layer ") + what + " needs arch openelm");
+    if (!openelm && !(lfm && zero_ok))
+      throw std::runtime_error(std::string("synthetic writer: per-layer ") + what + " needs arch openelm");
     if ((int)v.size() != c.layers) throw std::runtime_error(std::string("synthetic writer: ") + what + " length != layers");
     for (int x : v)
-      if (x <= 0) throw std::runtime_error("synthetic writer: non-positive dimension");
+      if (x < 0 || (x == 0 && !(lfm && zero_ok))) throw std::runtime_error("synthetic writer: non-positive dimension");
     return v;
   };
-  const std::vector<int> lh = per_layer(c.layer_heads, c.heads, "heads");
-  const std::vector<int> lkv = per_layer(c.layer_kv_heads, c.kv_heads, "kv_heads");
-  const std::vector<int> lff = per_layer(c.layer_ffn, c.ffn, "ffn");
+  const std::vector<int> lh = per_layer(c.layer_heads, c.heads, "heads", false);
+  // lfm2: 0 kv heads marks a short-convolution layer
+  const std::vector<int> lkv = per_layer(c.layer_kv_heads, c.kv_heads, "kv_heads", true);
+  const std::vector<int> lff = per_layer(c.layer_ffn, c.ffn, "ffn", false);
   for (int i = 0; i < c.layers; ++i)
-    if (lh[(size_t)i] % lkv[(size_t)i] != 0) throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
+    if (lkv[(size_t)i] > 0 && lh[(size_t)i] % lkv[(size_t)i] != 0)
+      throw std::runtime_error("synthetic writer: heads not a multiple of kv_heads");
   if (openelm && c.head_dim <= 0) throw std::runtime_error("synthetic writer: openelm needs head_dim");
   const int head_dim = c.head_dim > 0 ? c.head_dim : c.hidden / c.heads;
   const uint64_t H = (uint64_t)c.hidden;
   const bool gemma = a == "gemma3";
-  const bool qk_norm = a == "qwen3" || gemma || openelm;
+  const bool qk_norm = a == "qwen3" || gemma || openelm || lfm;
   const float w_std = c.weight_std;
   const float n_std = c.norm_std;
 
@@ -173,6 +185,17 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     const uint64_t qdim = (uint64_t)lh[(size_t)i] * head_dim, kvdim = (uint64_t)lkv[(size_t)i] * head_dim;
     const uint64_t F = (uint64_t)lff[(size_t)i];
     norm("attn_norm", H);
+    if (lfm && lkv[(size_t)i] == 0) {
+      // short convolution: in_proj rows B | C | x, a 3-tap depthwise filter per channel
+      plan.push_back({p + "shortconv.conv.weight", H, 3, GGML_F32, 0.f, kLfmConvStd});
+      lin("shortconv.in_proj", 3 * H, H);
+      lin("shortconv.out_proj", H, H);
+      norm("ffn_norm", H);
+      lin("ffn_gate", F, H);
+      lin("ffn_up", F, H);
+      lin("ffn_down", H, F);
+      continue;
+    }
     if (openelm) {
       lin("attn_qkv", qdim + 2 * kvdim, H);
     } else {
@@ -192,7 +215,7 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     lin("ffn_down", H, F);
     if (gemma) norm("post_ffw_norm", H);
   }
-  if (a != "gpt2") plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
+  if (a != "gpt2") plan.push_back({lfm ? "token_embd_norm.weight" : "output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
 
   GgufWriter w;
   w.set_string("general.architecture", a);
@@ -201,7 +224,12 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
   w.set_u32(a + ".context_length", (uint32_t)c.context_length);
   w.set_u32(a + ".embedding_length", (uint32_t)c.hidden);
   w.set_u32(a + ".block_count", (uint32_t)c.layers);
-  if (openelm) {
+  if (lfm) {
+    w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
+    w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
+    w.set_u32_array(a + ".attention.head_count_kv", std::vector<uint32_t>(lkv.begin(), lkv.end()));
+    w.set_u32(a + ".shortconv.l_cache", 3u);
+  } else if (openelm) {
     auto u32s = [](const std::vector<int>& v) { return std::vector<uint32_t>(v.begin(), v.end()); };
     w.set_u32_array(a + ".feed_forward_length", u32s(lff));
     w.set_u32_array(a + ".attention.head_count", u32s(lh));

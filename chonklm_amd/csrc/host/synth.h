@@ -26,7 +26,7 @@
 namespace chonk {
 
 struct SynthConfig {
-  std::string arch = "llama";  // llama | qwen3 | gemma3 | gpt2 | openelm
+  std::string arch = "llama";  // llama | qwen3 | gemma3 | gpt2 | openelm | lfm2
   std::string name;
   int hidden = 576;
   int layers = 30;
@@ -45,7 +45,9 @@ struct SynthConfig {
   float norm_std = 0.02f;
   // openelm: per-layer head, kv-head and feed-forward counts (empty: the
   // scalars above for every layer); written as the arrays
-  // openelm.attention.head_count, .head_count_kv and .feed_forward_length
+  // openelm.attention.head_count, .head_count_kv and .feed_forward_length.
+  // lfm2: layer_kv_heads alone, 0 marking a short-convolution layer (written as
+  // lfm2.attention.head_count_kv)
   std::vector<int> layer_heads, layer_kv_heads, layer_ffn;
 };
 

@@ -4,7 +4,7 @@
 
 export interface ModelDef {
   id: string;
-  runtime: string; // "llama-webgpu" (llama / qwen3 / gemma3 files) or "gpt-webgpu" (gpt2 files)
+  runtime: string; // "llama-webgpu" (llama / qwen3 / gemma3 / openelm files), "gpt-webgpu" (gpt2), "lfm2-webgpu" (lfm2)
   eosIds: number[];
   vocab: number;
   layers: number;
@@ -99,6 +99,27 @@ export declare function generateGptWgsl(
 
 export declare function disposeGptWgsl(loaded: LoadedGptWgslModel): void;
 export declare function resetGptWgslConversation(loaded: LoadedGptWgslModel): void;
+
+/** LoadedLfmWgslModel (src/lib/lfm-wgsl-runtime.ts:159-167). */
+export interface LoadedLfmWgslModel extends Omit<LoadedLlamaWgslModel, "runtime"> {
+  runtime: "lfm2-webgpu";
+}
+
+export declare function loadLfmWgslModel(
+  model: ModelDef,
+  onProgress?: ProgressCallback,
+  onStep?: LoadStepCallback,
+  options?: { tokenizer?: Tokenizer; device?: number },
+): Promise<LoadedLfmWgslModel>;
+
+export declare function generateLfmWgsl(
+  loaded: LoadedLfmWgslModel,
+  promptIds: number[],
+  opts?: GenerateOptions,
+): Promise<{ text: string; ids: number[]; tokensPerSec: number }>;
+
+export declare function disposeLfmWgsl(loaded: LoadedLfmWgslModel): void;
+export declare function resetLfmWgslConversation(loaded: LoadedLfmWgslModel): void;
 
 export {
   loadLlamaWgslModel as loadPleiasWgslModel,

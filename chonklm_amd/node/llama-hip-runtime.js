@@ -89,9 +89,10 @@ async function loadLlamaWgslModel(model, onProgress, onStep, options) {
   }
   if (!model.gguf) throw new Error(`Llama WGSL ${model.id} is missing gguf path`);
   const engine = await openEngine(model, onProgress, onStep, options);
-  if (engine.info.architecture === ARCH_GPT2) {
+  if (engine.info.architecture === ARCH_GPT2 || engine.info.architecture === ARCH_LFM2) {
+    const arch = engine.info.architecture === ARCH_GPT2 ? 'gpt2' : 'lfm2';
     engine.dispose();
-    throw new Error('Llama GGUF WGSL does not support architecture gpt2');
+    throw new Error(`Llama GGUF WGSL does not support architecture ${arch}`);
   }
   if (onStep) onStep({ step: 'ready', detail: 'Llama HIP runtime ready' });
   return loadedRecord('llama-webgpu', model, engine, options);
@@ -112,7 +113,26 @@ async function loadGptWgslModel(model, onProgress, onStep, options) {
   return loadedRecord('gpt-webgpu', model, engine, options);
 }
 
-const ARCH_GPT2 = 3;  // chonk_engine_info.architecture
+// loadLfmWgslModel (src/lib/lfm-wgsl-runtime.ts:169-217). The engine runs the lfm2
+// architecture of the GGUF file (gated short-convolution layers beside GQA attention
+// layers, the embedding as lm_head, TOPK256 candidates and the LFM generate loop).
+async function loadLfmWgslModel(model, onProgress, onStep, options) {
+  if (model.runtime !== 'lfm2-webgpu') throw new Error(`loadLfmWgslModel: unsupported model ${model.id}`);
+  if (!model.gguf) throw new Error(`LFM GGUF model ${model.id} missing gguf path`);
+  const engine = await openEngine(model, onProgress, onStep, options);
+  if (engine.info.architecture !== ARCH_LFM2) {
+    const arch = ARCH_NAMES[engine.info.architecture];
+    engine.dispose();
+    throw new Error(`unsupported LFM GGUF architecture: ${arch}`);
+  }
+  if (onStep) onStep({ step: 'ready', detail: 'LFM HIP runtime ready' });
+  return loadedRecord('lfm2-webgpu', model, engine, options);
+}
+
+// chonk_engine_info.architecture
+const ARCH_GPT2 = 3;
+const ARCH_LFM2 = 5;
+const ARCH_NAMES = ['llama', 'qwen3', 'gemma3', 'gpt2', 'openelm', 'lfm2'];
 
 function loadedRecord(runtime, model, engine, options) {
   return {
@@ -156,6 +176,13 @@ async function generateLlamaWgsl(loaded, promptIds, opts) {
 // generateGptWgsl (gpt-wgsl-runtime.ts:182-249): repetitionPenalty is
 // opts.repetitionPenalty ?? 1; the definition's default is not consulted (:198-203).
 async function generateGptWgsl(loaded, promptIds, opts) {
+  return generateWith(loaded, promptIds, opts || {}, samplingOf(opts, null));
+}
+
+// generateLfmWgsl (lfm-wgsl-runtime.ts:219-306): repetitionPenalty is
+// opts.repetitionPenalty ?? 1 (:236-241); the engine runs one more step after the last
+// generated id, whose pick is the cached next id.
+async function generateLfmWgsl(loaded, promptIds, opts) {
   return generateWith(loaded, promptIds, opts || {}, samplingOf(opts, null));
 }
 
@@ -205,6 +232,11 @@ module.exports = {
   generateGptWgsl,
   disposeGptWgsl: disposeLlamaWgsl,
   resetGptWgslConversation: resetLlamaWgslConversation,
+  // LFM2 runtime (src/lib/lfm-wgsl-runtime.ts:169-316)
+  loadLfmWgslModel,
+  generateLfmWgsl,
+  disposeLfmWgsl: disposeLlamaWgsl,
+  resetLfmWgslConversation: resetLlamaWgslConversation,
   // PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
   loadPleiasWgslModel: loadLlamaWgslModel,
   generatePleiasWgsl: generateLlamaWgsl,

@@ -74,7 +74,7 @@ class Workload:
         return np.random.default_rng(seed).integers(0, self.spec.vocab, self.prompt_tokens if n is None else n).tolist()
 
     def model_def(self, path: str, kv_dtype: str = "f16", device: int = 0) -> ModelDef:
-        runtime = "gpt-webgpu" if self.spec.arch == "gpt2" else "llama-webgpu"
+        runtime = {"gpt2": "gpt-webgpu", "lfm2": "lfm2-webgpu"}.get(self.spec.arch, "llama-webgpu")
         return ModelDef(id=self.name, vocab=self.spec.vocab, layers=self.spec.layers, max_context=self.max_context,
                         eos_ids=list(self.eos_ids), path=path, kv_dtype=kv_dtype, device=device, runtime=runtime)
 
@@ -94,6 +94,16 @@ OPENELM_270M = dict(arch="openelm", hidden=1280, layers=16, heads=20, kv_heads=5
                     layer_heads=[12] * 5 + [16] * 7 + [20] * 4, layer_kv_heads=[3] * 5 + [4] * 7 + [5] * 4,
                     layer_ffn=[768, 1024, 1280, 1536, 1792, 2048, 2560, 2816, 3072, 3328, 3584, 3840, 4352, 4608,
                                4864, 5120])
+
+# LFM2.5-350M-shaped (registry.ts:61-112; the runtime's fixed shape,
+# lfm-wgsl-runtime.ts:457-462): convolution and attention layers in the
+# registry's order, 8 kv heads on the attention layers (0 marks a convolution
+# layer, as lfm2.attention.head_count_kv does)
+LFM2_TYPES = ["conv", "conv", "attention", "conv", "conv", "attention", "conv", "conv", "attention", "conv",
+              "attention", "conv", "attention", "conv", "attention", "conv"]
+LFM2_350M = dict(arch="lfm2", hidden=1024, layers=16, heads=16, kv_heads=8, head_dim=64, ffn=4608, vocab=65536,
+                 context_length=128000, rope_theta=1000000.0, norm_eps=1e-5,
+                 layer_kv_heads=[8 if t == "attention" else 0 for t in LFM2_TYPES])
 
 WORKLOADS: dict[str, Workload] = {
     w.name: w
@@ -119,6 +129,13 @@ WORKLOADS: dict[str, Workload] = {
                  eos_ids=[2], prompt_tokens=32, decode_tokens=128,
                  description="OpenELM-270M-shaped decoder (fused q|k|v, per-layer heads 12-20 / kv heads 3-5 / "
                              "feed-forward 768-5120), Q4_K_M, 32-token prompt, greedy 128"),
+        Workload("lfm2.5-350m-q4_k_m", SynthSpec(recipe="q4_k_m", seed=41, **LFM2_350M), max_context=4096,
+                 eos_ids=[7, 2], prompt_tokens=32, decode_tokens=128,
+                 description="LFM2.5-350M-shaped hybrid decoder (10 short-convolution and 6 attention layers, "
+                             "lfm2 runtime), Q4_K_M, 32-token prompt, greedy 128"),
+        Workload("lfm2.5-350m-q8_0", SynthSpec(recipe="q8_0", seed=41, **LFM2_350M), max_context=4096,
+                 eos_ids=[7, 2], prompt_tokens=32, decode_tokens=128,
+                 description="LFM2.5-350M-shaped hybrid decoder (lfm2 runtime), Q8_0, 32-token prompt, greedy 128"),
         # small decoders for oracle parity (each exercises a different type mix)
         Workload("tiny-qwen3", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=2,
                                          head_dim=64, ffn=512, vocab=1200, context_length=4096,
@@ -145,6 +162,14 @@ WORKLOADS: dict[str, Workload] = {
                                            layer_heads=[2, 3, 4, 4], layer_kv_heads=[1, 1, 1, 2],
                                            layer_ffn=[256, 384, 512, 768]),
                  max_context=160, eos_ids=[2], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-lfm2", SynthSpec(arch="lfm2", recipe="q4_k_m", hidden=256, layers=4, heads=4, kv_heads=2,
+                                        head_dim=64, ffn=512, vocab=1024, context_length=4096,
+                                        rope_theta=1000000.0, norm_eps=1e-5, seed=43, layer_kv_heads=[0, 2, 0, 2]),
+                 max_context=160, eos_ids=[7, 2], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-lfm2-q8", SynthSpec(arch="lfm2", recipe="q8_0", hidden=192, layers=3, heads=6, kv_heads=2,
+                                           head_dim=32, ffn=384, vocab=700, context_length=4096,
+                                           rope_theta=1000000.0, norm_eps=1e-5, seed=47, layer_kv_heads=[0, 0, 2]),
+                 max_context=160, eos_ids=[7, 2], prompt_tokens=16, decode_tokens=24),
         Workload("tiny-gemma3", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=320, layers=7, heads=4,
                                           kv_heads=1, head_dim=128, ffn=512, vocab=1500, context_length=4096,
                                           rope_theta=1000000.0, norm_eps=1e-6, sliding_window=16, seed=17),

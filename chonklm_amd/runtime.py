@@ -140,7 +140,8 @@ class LlamaWgslEngine:
 
     def read_buffer(self, which: int) -> np.ndarray:
         i = self.info
-        sizes = {0: i["hidden"] * 4, 1: i["heads"] * i["head_dim"] * 4, 2: ((i["vocab"] + 255) // 256) * 8,
+        slots = 256 if i["architecture"] == 5 else (i["vocab"] + 255) // 256  # lfm2: one per residue class
+        sizes = {0: i["hidden"] * 4, 1: i["heads"] * i["head_dim"] * 4, 2: slots * 8,
                  3: (i["heads"] + 2 * i["kv_heads"]) * i["head_dim"] * 4}
         buf = np.empty(sizes[which], dtype=np.uint8)
         check(lib().chonk_engine_read_buffer(self._h, which, buf.ctypes.data, buf.size), self._h)
@@ -217,9 +218,10 @@ def load_llama_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = Non
     if on_step:
         on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
     engine = LlamaWgslEngine(model)
-    if engine.info["architecture"] == 3:
+    arch = {3: "gpt2", 5: "lfm2"}.get(engine.info["architecture"])
+    if arch:
         engine.dispose()
-        raise ValueError("Llama GGUF WGSL does not support architecture gpt2")
+        raise ValueError(f"Llama GGUF WGSL does not support architecture {arch}")
     if on_step:
         on_step({"step": "ready", "detail": "Llama HIP runtime ready"})
     return LoadedLlamaWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
@@ -386,6 +388,54 @@ def dispose_gpt_wgsl(loaded: LoadedGptWgslModel) -> None:
     dispose_llama_wgsl(loaded)
 
 
+# ---- LFM2 runtime (src/lib/lfm-wgsl-runtime.ts) -----------------------------------
+# The same engine runs the lfm2 architecture (gated short-convolution layers beside
+# GQA attention layers, the embedding as lm_head, TOPK256 candidates, its generate
+# loop); the architecture comes from the GGUF file, the runtime tag from the model
+# definition.
+
+@dataclass
+class LoadedLfmWgslModel(LoadedLlamaWgslModel):
+    """LoadedLfmWgslModel (lfm-wgsl-runtime.ts:159-167)."""
+
+    runtime: str = "lfm2-webgpu"
+
+
+def load_lfm_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = None,
+                        on_step: Optional[Callable] = None, tokenizer: object = None) -> LoadedLfmWgslModel:
+    """loadLfmWgslModel (:169-217): rejects a definition not tagged for the LFM runtime and
+    a GGUF file whose architecture is not lfm2 (openGgufLfmSource, :318-322)."""
+    if model.runtime != "lfm2-webgpu":
+        raise ValueError(f"loadLfmWgslModel: unsupported model {model.id}")
+    if on_step:
+        on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
+    engine = LlamaWgslEngine(model)
+    if engine.info["architecture"] != 5:
+        arch = {0: "llama", 1: "qwen3", 2: "gemma3", 3: "gpt2", 4: "openelm"}.get(engine.info["architecture"])
+        engine.dispose()
+        raise ValueError(f"unsupported LFM GGUF architecture: {arch}")
+    if on_step:
+        on_step({"step": "ready", "detail": "LFM HIP runtime ready"})
+    return LoadedLfmWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
+
+
+def generate_lfm_wgsl(loaded: LoadedLfmWgslModel, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None,
+                      **kw) -> dict:
+    """generateLfmWgsl (:219-306): the engine follows the LFM loop (one more step runs after
+    the last generated token; repetitionPenalty defaults to 1, not to the definition's)."""
+    return generate_llama_wgsl(loaded, prompt_ids, max_new_tokens, **kw)
+
+
+def reset_lfm_wgsl_conversation(loaded: LoadedLfmWgslModel) -> None:
+    """resetLfmWgslConversation (:312-316)."""
+    reset_llama_wgsl_conversation(loaded)
+
+
+def dispose_lfm_wgsl(loaded: LoadedLfmWgslModel) -> None:
+    """disposeLfmWgsl (:308-310)."""
+    dispose_llama_wgsl(loaded)
+
+
 # PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
 load_pleias_wgsl_model = load_llama_wgsl_model
 generate_pleias_wgsl = generate_llama_wgsl
@@ -423,5 +473,6 @@ def shard_gguf(gguf_path: str, out_dir: str, shard_size: int = 24 * 1024 * 1024,
 __all__ = [
     "ChonkError", "LlamaWgslEngine", "LoadedLlamaWgslModel", "ModelDef", "load_llama_wgsl_model",
     "generate_llama_wgsl", "dispose_llama_wgsl", "LlamaWgslBatch", "reset_llama_wgsl_conversation", "write_synthetic_gguf",
-    "shard_gguf",
+    "shard_gguf", "LoadedLfmWgslModel", "load_lfm_wgsl_model", "generate_lfm_wgsl", "reset_lfm_wgsl_conversation",
+    "dispose_lfm_wgsl",
 ]

@@ -507,6 +507,11 @@ struct Layer {
   Matrix qkv;
   std::vector<float> in_norm_b, post_norm_b, qkv_b, o_b, up_b, down_b;
   std::vector<float> kcache, vcache;  // [kv_heads][C][hd]
+  // LFM2 short-convolution layer (lfm-wgsl-runtime.ts:69-78): in_proj rows
+  // B | C | x, the [hidden][3] depthwise taps and the [hidden][3] state
+  bool conv = false;
+  Matrix conv_in, conv_out;
+  std::vector<float> conv_w, conv_state;
 };
 
 }  // namespace
@@ -518,6 +523,7 @@ struct orc_model {
   bool gemma = false, interleaved = false, qk_norm = false, kv_f16 = false;
   bool gpt = false;                         // GGUF architecture gpt2 (gpt-wgsl-runtime.ts)
   bool openelm = false;                     // fused attn_qkv, per-layer heads / kv heads / ffn
+  bool lfm = false;                         // GGUF architecture lfm2 (lfm-wgsl-runtime.ts)
   std::vector<float> pos_embd, final_norm_b;  // GPT-2: [context][hidden] position table, final LayerNorm bias
   int hidden = 0, ffn = 0, vocab = 0, n_layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float norm_eps = 1e-5f, qk_eps = 1e-5f, attn_scale = 0, embed_scale = 1;
@@ -526,7 +532,7 @@ struct orc_model {
   std::vector<Layer> layers;
   int pos = 0;
   // scratch of the last step
-  std::vector<float> hA, hB, hC, norm, q, k, v, qn, attn, gate, up, ff, logits, scores, qkv;
+  std::vector<float> hA, hB, hC, norm, q, k, v, qn, attn, gate, up, ff, logits, scores, qkv, proj, conv_mid;
   std::vector<uint8_t> candidates;
   std::vector<float> last_residual;
 };
@@ -777,6 +783,101 @@ void build_gpt(orc_model* m, const orc_model_def* def) {
   }
 }
 
+// The LFM runtime's GGUF loader and engine buffers (lfm-wgsl-runtime.ts:313-455,
+// :501-580). The reference fixes the LFM2.5-350M shape in code (hidden 1024,
+// intermediate 4608, 16 heads, head_dim 64, 65536 ids, eps 1e-5, rope base
+// 1e6, three conv taps); here the dimensions come from the file's metadata and
+// the constants stay the reference's. A layer is a convolution layer when it
+// holds shortconv.conv.weight (lfm2.attention.head_count_kv is 0 there).
+Matrix lfm_linear(orc_model* m, const std::string& name, uint64_t k, uint64_t n) {
+  auto it = m->g.tensors.find(name);
+  if (it == m->g.tensors.end()) throw std::runtime_error("LFM GGUF missing tensor " + name);
+  const uint32_t t = it->second.type;
+  if (t != 8 && t != 12 && t != 14)  // ggufLinearKind (:422-427): Q8_0, Q4_K, Q6_K
+    throw std::runtime_error("unsupported LFM GGUF linear tensor " + name);
+  return matrix(m, name, k, n);
+}
+
+std::vector<float> lfm_floats(orc_model* m, const std::string& name, size_t n) {
+  auto it = m->g.tensors.find(name);
+  if (it == m->g.tensors.end()) throw std::runtime_error("LFM GGUF missing tensor " + name);
+  if (it->second.type != 0 && it->second.type != 1)
+    throw std::runtime_error("LFM GGUF tensor " + name + " is not F32/F16");
+  return floats(m, name, n);
+}
+
+void build_lfm(orc_model* m, const orc_model_def* def) {
+  const Gguf& g = m->g;
+  m->lfm = true;
+  m->n_layers = (int)num(g, "lfm2.block_count", 0, true);
+  m->hidden = (int)num(g, "lfm2.embedding_length", 0, true);
+  m->ffn = (int)num(g, "lfm2.feed_forward_length", 0, true);
+  m->heads = (int)num(g, "lfm2.attention.head_count", 0, true);
+  std::vector<int> lkv;
+  auto kv_it = g.kv.find("lfm2.attention.head_count_kv");
+  if (kv_it != g.kv.end() && kv_it->second.type == 9) {
+    lkv = num_array(g, "lfm2.attention.head_count_kv");
+    if ((int)lkv.size() != m->n_layers) throw std::runtime_error("LFM GGUF head_count_kv length != layers");
+  } else {
+    lkv.assign((size_t)m->n_layers, (int)num(g, "lfm2.attention.head_count_kv", 0, true));
+  }
+  m->hd = (int)num(g, "lfm2.attention.key_length", std::floor((double)m->hidden / m->heads), false);
+  if (m->hd > 256) throw std::runtime_error("head_dim above 256 is not supported");
+  m->vocab = def->vocab;
+  m->ctx = def->max_context;                 // LfmWgslEngine.maxContext (:461)
+  m->norm_eps = 1e-5f;                       // RMS_NORM_WGSL / ADD_RMS_NORM_WGSL (:1567-1639)
+  m->qk_eps = 1e-5f;                         // QK_NORM_ROPE_STORE_WGSL (:1763)
+  m->qk_norm = true;
+  m->attn_scale = (float)(1.0 / std::sqrt((double)m->hd));  // 0.125 at head_dim 64 (:1834)
+  m->embed_scale = 1.0f;
+  m->kv_f16 = def->kv_f16 != 0;
+  const int H = m->hidden;
+  m->embed = lfm_linear(m, "token_embd.weight", (uint64_t)H, (uint64_t)m->vocab);
+  m->lm_head = m->embed;                     // the lm_head is the embedding (:512-519)
+  m->final_norm = lfm_floats(m, "token_embd_norm.weight", H);
+  m->kv_heads = 0;
+  for (int i = 0; i < m->n_layers; ++i) {
+    Layer L;
+    const std::string p = "blk." + std::to_string(i) + ".";
+    L.conv = g.tensors.count(p + "shortconv.conv.weight") != 0;
+    L.heads = m->heads;
+    L.kv_heads = L.conv ? 0 : lkv[(size_t)i];
+    L.qdim = L.heads * m->hd;
+    L.kvdim = L.kv_heads * m->hd;
+    L.ffn = m->ffn;
+    L.theta_u32 = 1000000;                   // rope_angle's pow(1000000.0, ...) (:1739-1742)
+    L.window = 0;
+    L.in_norm = lfm_floats(m, p + "attn_norm.weight", H);
+    L.post_norm = lfm_floats(m, p + "ffn_norm.weight", H);
+    L.gate = lfm_linear(m, p + "ffn_gate.weight", H, m->ffn);
+    L.up = lfm_linear(m, p + "ffn_up.weight", H, m->ffn);
+    L.down = lfm_linear(m, p + "ffn_down.weight", m->ffn, H);
+    if (L.conv) {
+      const Tensor& cw = g.tensors.at(p + "shortconv.conv.weight");
+      if (cw.shape.size() != 2 || cw.shape[0] != 3 || cw.shape[1] != (uint64_t)H)
+        throw std::runtime_error("LFM conv weight " + p + "shortconv.conv.weight is not [3, hidden]");
+      L.conv_w = lfm_floats(m, p + "shortconv.conv.weight", 3 * (size_t)H);
+      L.conv_in = lfm_linear(m, p + "shortconv.in_proj.weight", H, 3 * (uint64_t)H);
+      L.conv_out = lfm_linear(m, p + "shortconv.out_proj.weight", H, H);
+      L.conv_state.assign(3 * (size_t)H, 0.0f);
+    } else {
+      if (L.kv_heads <= 0 || L.heads % L.kv_heads != 0)
+        throw std::runtime_error("layer heads must be a positive multiple of kv heads");
+      m->kv_heads = std::max(m->kv_heads, L.kv_heads);
+      L.q_norm = lfm_floats(m, p + "attn_q_norm.weight", m->hd);
+      L.k_norm = lfm_floats(m, p + "attn_k_norm.weight", m->hd);
+      L.q = lfm_linear(m, p + "attn_q.weight", H, L.qdim);
+      L.k = lfm_linear(m, p + "attn_k.weight", H, L.kvdim);
+      L.v = lfm_linear(m, p + "attn_v.weight", H, L.kvdim);
+      L.o = lfm_linear(m, p + "attn_output.weight", L.qdim, H);
+      L.kcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
+      L.vcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
+    }
+    m->layers.push_back(std::move(L));
+  }
+  if (m->kv_heads == 0) throw std::runtime_error("LFM GGUF has no attention layer");
+}
+
 void build(orc_model* m, const orc_model_def* def) {
   const Gguf& g = m->g;
   auto it = g.kv.find("general.architecture");
@@ -784,6 +885,10 @@ void build(orc_model* m, const orc_model_def* def) {
   const std::string arch = it->second.str;
   if (arch == "gpt2") {
     build_gpt(m, def);
+    return;
+  }
+  if (arch == "lfm2") {
+    build_lfm(m, def);
     return;
   }
   if (arch != "qwen3" && arch != "llama" && arch != "gemma3" && arch != "openelm")
@@ -1050,7 +1155,11 @@ orc_model* orc_model_load(const char* path, const orc_model_def* def, char* err,
     m->up.assign(m->ffn, 0);
     m->ff.assign(m->ffn, 0);
     m->logits.assign(m->vocab, 0);
-    m->candidates.assign((size_t)(m->vocab + 255) / 256 * 8, 0);
+    m->candidates.assign((size_t)(m->lfm ? 256 : (m->vocab + 255) / 256) * 8, 0);
+    if (m->lfm) {
+      m->proj.assign(3 * (size_t)H, 0);
+      m->conv_mid.assign(H, 0);
+    }
     if (m->gpt) m->qkv.assign(3 * (size_t)H, 0);
     if (m->openelm) m->qkv.assign((size_t)qdim + 2 * kvdim, 0);
     return m;
@@ -1078,6 +1187,7 @@ void orc_model_reset(orc_model* m) {
   for (auto& L : m->layers) {
     std::fill(L.kcache.begin(), L.kcache.end(), 0.0f);
     std::fill(L.vcache.begin(), L.vcache.end(), 0.0f);
+    std::fill(L.conv_state.begin(), L.conv_state.end(), 0.0f);  // LfmWgslEngine.reset (:711-724)
   }
 }
 
@@ -1302,10 +1412,162 @@ static int32_t run_token_gpt(orc_model* m, int32_t token, int32_t need_logits, c
   return best;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Q8_MATVEC_WGSL (lfm-wgsl-runtime.ts:1225-1276) over the 36-byte repacked
+// blocks: sum = sum + input[k] * q8 * scale, i.e. (x * q) * d with the scale
+// widened exactly from binary16 (packQ8_0ForGpu, :433-455); 128 strided lane
+// sums, then the stride 64..1 tree.
+float matvec_row_lfm_q8(const uint8_t* w, uint64_t row, uint64_t K, const float* x) {
+  float partial[128];
+  for (int t = 0; t < 128; ++t) partial[t] = 0.0f;
+  for (uint64_t k = 0; k < K; ++k) {
+    const uint64_t base = (row * (K / 32) + (k >> 5)) * 34;
+    const float xq = x[k] * (float)i8_at(w, base + 2 + (k & 31));
+    const float prod = xq * f16_at(w, base);
+    partial[k & 127] = partial[k & 127] + prod;
+  }
+  for (int st = 64; st >= 1; st >>= 1)
+    for (int t = 0; t < st; ++t) partial[t] = partial[t] + partial[t + st];
+  return partial[0];
+}
+
+// The LFM runtime's linear layer: Q8_0 in the order above, Q4_K / Q6_K as
+// sum + input[k] * dequant(w) (Q4K_MATVEC_WGSL :1398-1444, Q6K_MATVEC_WGSL
+// :1446-1492), which is the llama runtime's matvec.
+void matvec_lfm(Pool& pool, const Matrix& W, uint64_t N, const float* x, float* y) {
+  if (W.type != 8) {
+    matvec(pool, W.type, W.data, N, W.k, x, y);
+    return;
+  }
+  pool.run((int64_t)N, [&](int64_t b, int64_t e) {
+    for (int64_t n = b; n < e; ++n) y[n] = matvec_row_lfm_q8(W.data, (uint64_t)n, W.k, x);
+  });
+}
+
+// TOPK256_WGSL (:1925-1947), also the first stage of ARGMAX_WGSL (:1880-1923):
+// slot t keeps the first strictly greater logit among ids t, t + 256, ...,
+// starting from (-3.402823e38, 0); NaN never replaces it.
+void lfm_top256(const float* logits, int64_t vocab, uint8_t* pairs) {
+  for (int t = 0; t < 256; ++t) {
+    float mx = kNegBig;
+    uint32_t id = 0;
+    for (int64_t i = t; i < vocab; i += 256)
+      if (logits[i] > mx) {
+        mx = logits[i];
+        id = (uint32_t)i;
+      }
+    std::memcpy(pairs + 8 * t, &mx, 4);
+    std::memcpy(pairs + 8 * t + 4, &id, 4);
+  }
+}
+
+// ARGMAX_WGSL's second stage (:1903-1922): a stride 128..1 tree keeping the
+// left slot unless the right one is strictly greater.
+int32_t lfm_argmax(const uint8_t* pairs) {
+  float v[256];
+  uint32_t id[256];
+  for (int t = 0; t < 256; ++t) {
+    std::memcpy(&v[t], pairs + 8 * t, 4);
+    std::memcpy(&id[t], pairs + 8 * t + 4, 4);
+  }
+  for (int st = 128; st >= 1; st >>= 1)
+    for (int t = 0; t < st; ++t)
+      if (v[t + st] > v[t]) {
+        v[t] = v[t + st];
+        id[t] = id[t + st];
+      }
+  return (int32_t)id[0];
+}
+
+// CONV_BLOCK_WGSL (:1641-1672): cur = B * x; the two previous values of the
+// channel's state and cur through the three taps; state shifted; out = C * conv.
+void lfm_conv_block(Layer& L, const float* proj, float* out, int H) {
+  for (int h = 0; h < H; ++h) {
+    const float a = proj[h], b = proj[H + h], c = proj[2 * H + h];
+    const float cur = a * c;
+    float* st = L.conv_state.data() + 3 * (size_t)h;
+    const float* w = L.conv_w.data() + 3 * (size_t)h;
+    const float p1 = st[1], p2 = st[2];
+    const float t0 = p1 * w[0], t1 = p2 * w[1], t2 = cur * w[2];
+    const float conv = (t0 + t1) + t2;
+    st[0] = p1;
+    st[1] = p2;
+    st[2] = cur;
+    out[h] = b * conv;
+  }
+}
+
+// LfmWgslEngine.runToken (:727-809)
+int32_t run_token_lfm(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s, const int32_t* seen,
+                      int64_t n_seen, double uniform) {
+  if (m->pos >= m->ctx) throw std::runtime_error("LFM WGSL context exhausted at " + std::to_string(m->ctx) + " tokens");
+  const int H = m->hidden, pos = m->pos;
+  Pool& pool = *m->pool;
+  float* hA = m->hA.data();
+  float* hB = m->hB.data();
+  embedding(m, token, hA);  // EMBEDDING_{Q8,Q4K,Q6K}_WGSL (:1301-1323, :1494-1540): the dequantized row
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    Layer& L = m->layers[li];
+    rms_norm(hA, L.in_norm.data(), m->norm.data(), H, m->norm_eps);
+    if (L.conv) {
+      matvec_lfm(pool, L.conv_in, 3 * (uint64_t)H, m->norm.data(), m->proj.data());
+      lfm_conv_block(L, m->proj.data(), m->conv_mid.data(), H);
+      matvec_lfm(pool, L.conv_out, (uint64_t)H, m->conv_mid.data(), hB);
+    } else {
+      matvec_lfm(pool, L.q, (uint64_t)L.qdim, m->norm.data(), m->q.data());
+      matvec_lfm(pool, L.k, (uint64_t)L.kvdim, m->norm.data(), m->k.data());
+      matvec_lfm(pool, L.v, (uint64_t)L.kvdim, m->norm.data(), m->v.data());
+      qk_rope_store(m, L, pos, true, m->qn.data());  // QK_NORM_ROPE_STORE_WGSL (:1709-1786)
+      attention(m, L, pos, m->qn.data(), m->attn.data());  // ATTENTION_SCORE / _VALUE_WGSL (:1788-1878)
+      matvec_lfm(pool, L.o, (uint64_t)H, m->attn.data(), hB);
+    }
+    add_rms_norm(hA, hB, L.post_norm.data(), m->norm.data(), H, m->norm_eps);  // opAddNorm: hB = hA + hB
+    matvec_lfm(pool, L.gate, (uint64_t)L.ffn, m->norm.data(), m->gate.data());
+    matvec_lfm(pool, L.up, (uint64_t)L.ffn, m->norm.data(), m->up.data());
+    for (int i = 0; i < L.ffn; ++i) m->ff[i] = silu_mul(m->gate[i], m->up[i]);
+    matvec_lfm(pool, L.down, (uint64_t)H, m->ff.data(), hA);  // mlpDown writes hiddenA
+    for (int i = 0; i < H; ++i) hA[i] = hB[i] + hA[i];       // ffnAdd: hiddenA = hiddenB + hiddenA
+  }
+  m->last_residual.assign(hA, hA + H);
+  int32_t best = 0;
+  if (need_logits) {
+    rms_norm(hA, m->final_norm.data(), m->norm.data(), H, m->norm_eps);
+    matvec_lfm(pool, m->lm_head, (uint64_t)m->vocab, m->norm.data(), m->logits.data());
+    lfm_top256(m->logits.data(), m->vocab, m->candidates.data());
+    // needsCandidateReadback (sampling.ts:18-21): sampling, or a penalty that is not 1
+    const bool cand = s && (s->temperature > 0 || s->top_p < 1 || s->top_k > 0 || s->repetition_penalty != 1);
+    best = cand ? orc_sample_candidates(m->candidates.data(), 256, s, seen, n_seen, uniform)
+                : lfm_argmax(m->candidates.data());
+  }
+  m->pos += 1;
+  return best;
+}
+
+}  // namespace
+
+extern "C" {
+
+int orc_model_is_lfm(const orc_model* m) { return m->lfm ? 1 : 0; }
+
+int orc_lfm_select(const float* logits, int64_t vocab, uint8_t* candidate_pairs, int32_t* token) {
+  uint8_t pairs[256 * 8];
+  lfm_top256(logits, vocab, pairs);
+  if (candidate_pairs) std::memcpy(candidate_pairs, pairs, sizeof pairs);
+  if (token) *token = lfm_argmax(pairs);
+  return 0;
+}
+
 int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
                         const int32_t* penalized, int64_t n_penalized, const int32_t* seen, int64_t n_seen,
                         double uniform, int32_t* out_token, char* err, size_t err_len) {
   try {
+    if (m->lfm) {
+      *out_token = run_token_lfm(m, token, need_logits, s, seen, n_seen, uniform);
+      return 0;
+    }
     if (m->gpt) {
       *out_token = run_token_gpt(m, token, need_logits, s, penalized, n_penalized, seen, n_seen, uniform);
       return 0;

@@ -65,13 +65,16 @@ void orc_model_free(orc_model* m);
 int orc_model_context(const orc_model* m);
 /* 1 for a GGUF of architecture gpt2 (gpt-wgsl-runtime.ts), else 0. */
 int orc_model_is_gpt(const orc_model* m);
+/* 1 for a GGUF of architecture lfm2 (lfm-wgsl-runtime.ts), else 0. */
+int orc_model_is_lfm(const orc_model* m);
 /* Vocabulary of the loaded model (ModelDef.vocab, or token_embd's rows for gpt2). */
 int orc_model_vocab(const orc_model* m);
 int orc_model_position(const orc_model* m);
 void orc_model_reset(orc_model* m);
 
 /* runToken (llama-wgsl-runtime.ts:1025-1150; for gpt2 GptWgslEngine.runToken,
- * gpt-wgsl-runtime.ts:749-840). `uniform` is the sampler's
+ * gpt-wgsl-runtime.ts:749-840; for lfm2 LfmWgslEngine.runToken,
+ * lfm-wgsl-runtime.ts:727-809, which takes no penalty list). `uniform` is the sampler's
  * U in [0,1) (replaces Math.random). Returns 0, or -1 with err filled. */
 int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
                         const int32_t* penalized, int64_t n_penalized, const int32_t* seen, int64_t n_seen,
@@ -79,7 +82,7 @@ int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const 
 
 /* Buffers of the last step. which: 0 logits[vocab], 1 residual[hidden]
  * (final hidden before the last norm), 2 final normed hidden[hidden],
- * 3 candidates (vocab/256 x {value f32, index u32}) as raw 8-byte pairs,
+ * 3 candidates (vocab/256 x {value f32, index u32}, 256 for lfm2) as raw 8-byte pairs,
  * 4 q after rope (last layer) [heads*hd], 5 attention output (last layer). */
 int orc_model_read(const orc_model* m, int which, void* out, int64_t n_bytes);
 
@@ -100,6 +103,12 @@ int orc_argmax(const float* logits, int64_t vocab, const int32_t* penalized, int
  * 0, penalty whenever it is not 1; at most 65536 ids). */
 int orc_argmax_gpt(const float* logits, int64_t vocab, const int32_t* penalized, int64_t n_penalized,
                    double repetition_penalty, uint8_t* candidate_pairs, int32_t* token);
+
+/* The LFM runtime's selection over a logits vector: TOPK256_WGSL's 256
+ * candidates (slot t: the first strictly greatest of ids t, t + 256, ...,
+ * starting from (-3.402823e38, 0)) and ARGMAX_WGSL's token (a strict-greater
+ * tree over those slots), lfm-wgsl-runtime.ts:1880-1947. */
+int orc_lfm_select(const float* logits, int64_t vocab, uint8_t* candidate_pairs, int32_t* token);
 
 /* sampleFromCandidateBuffer (sampling.ts:23-76) with Math.random() -> uniform. */
 int32_t orc_sample_candidates(const uint8_t* candidate_pairs, int64_t n_groups, const orc_sampling* s,

@@ -50,6 +50,8 @@ def lib():
         L.orc_model_free.argtypes = [P]
         L.orc_model_context.argtypes = [P]
         L.orc_model_is_gpt.argtypes = [P]
+        L.orc_model_is_lfm.argtypes = [P]
+        L.orc_lfm_select.argtypes = [P, C.c_int64, P, I32P]
         L.orc_model_vocab.argtypes = [P]
         L.orc_model_position.argtypes = [P]
         L.orc_model_reset.argtypes = [P]
@@ -120,6 +122,15 @@ def argmax_gpt(logits: np.ndarray, penalized: Sequence[int] = (), repetition_pen
     return int(tok.value), pairs
 
 
+def lfm_select(logits: np.ndarray):
+    """The LFM runtime's TOPK256 / ARGMAX: (greedy token, 256 candidate pairs as uint8[2048])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    pairs = np.zeros(256 * 8, dtype=np.uint8)
+    tok = C.c_int32()
+    lib().orc_lfm_select(lg.ctypes.data, lg.size, pairs.ctypes.data, C.byref(tok))
+    return int(tok.value), pairs
+
+
 def uniform(seed: int, step: int) -> float:
     return float(lib().orc_uniform(seed & 0xFFFFFFFFFFFFFFFF, step))
 
@@ -133,8 +144,9 @@ def sample_candidates(pairs: np.ndarray, temperature: float, top_p: float, top_k
 
 
 class OracleModel:
-    """CPU restatement of LlamaWgslEngine + generateLlamaWgsl, or for a gpt2
-    GGUF of GptWgslEngine + generateGptWgsl (gpt-wgsl-runtime.ts)."""
+    """CPU restatement of LlamaWgslEngine + generateLlamaWgsl, for a gpt2 GGUF
+    of GptWgslEngine + generateGptWgsl (gpt-wgsl-runtime.ts), for an lfm2 GGUF
+    of LfmWgslEngine + generateLfmWgsl (lfm-wgsl-runtime.ts)."""
 
     def __init__(self, path: str, vocab: int, layers: int, max_context: int, kv_f16: bool = True,
                  threads: int = 8, eos_ids: Sequence[int] = (), default_repetition_penalty: Optional[float] = None):
@@ -144,6 +156,7 @@ class OracleModel:
         if not self._h:
             raise RuntimeError(err.value.decode())
         self.gpt = bool(lib().orc_model_is_gpt(self._h))
+        self.lfm = bool(lib().orc_model_is_lfm(self._h))
         self.vocab = int(lib().orc_model_vocab(self._h))
         self.max_context = max_context
         self.eos_ids = set(eos_ids)
@@ -209,13 +222,17 @@ class OracleModel:
                  margins: Optional[list] = None) -> list[int]:
         """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314); generateGptWgsl
         (gpt-wgsl-runtime.ts:182-249) for gpt2, which also runs the token after
-        the last generated one and refuses an empty prompt with no cached token."""
+        the last generated one and refuses an empty prompt with no cached token;
+        generateLfmWgsl (lfm-wgsl-runtime.ts:219-306) for lfm2, which runs the
+        token after the last generated one, starts an empty prompt with no
+        cached token from id 0 and ignores the definition's default penalty."""
         prompt = list(prompt_ids)
         mx = min(128 if max_new_tokens is None else max_new_tokens, self.max_context - len(prompt))
         t = 0.0 if temperature is None else temperature
         tp = 1.0 if top_p is None else top_p
         tk = 0 if top_k is None else top_k
-        rp = repetition_penalty if repetition_penalty is not None else (self.default_repetition_penalty or 1.0)
+        rp = repetition_penalty if repetition_penalty is not None else (
+            1.0 if self.lfm else (self.default_repetition_penalty or 1.0))
         n = 0
         while n < min(len(self.cached_token_ids), len(prompt)) and self.cached_token_ids[n] == prompt[n]:
             n += 1
@@ -243,7 +260,7 @@ class OracleModel:
             generated.append(next_id)
             if next_id in self.eos_ids:
                 break
-            if step + 1 >= mx and not self.gpt:
+            if step + 1 >= mx and not self.gpt and not self.lfm:
                 break
             ids = prompt + generated
             next_id = self.run_token(next_id, True, t, tp, tk, rp, ids, ids, seed)

@@ -18,11 +18,13 @@ async function main() {
     }
   } else if (job.kind === 'generate') {
     const steps = [];
-    const load = job.model.runtime === 'gpt-webgpu' ? rt.loadGptWgslModel : rt.loadLlamaWgslModel;
+    const load = { 'gpt-webgpu': rt.loadGptWgslModel, 'lfm2-webgpu': rt.loadLfmWgslModel }[job.model.runtime] ||
+      rt.loadLlamaWgslModel;
     const loaded = await load(job.model, null, (s) => steps.push(s.step));
     out.steps = steps;
     out.runs = [];
-    const gen = job.model.runtime === 'gpt-webgpu' ? rt.generateGptWgsl : rt.generateLlamaWgsl;
+    const gen = { 'gpt-webgpu': rt.generateGptWgsl, 'lfm2-webgpu': rt.generateLfmWgsl }[job.model.runtime] ||
+      rt.generateLlamaWgsl;
     for (const g of job.generate) {
       const seen = [];
       const opts = Object.assign({}, g.opts || {});

@@ -227,3 +227,104 @@ class NumpyGpt2:
             x = self._sanitize(x + lay["ffn_down.weight"] @ u + lay["ffn_down.bias"])
         self.pos += 1
         return self.lm @ self._ln(x, self.fn_w, self.fn_b)
+
+
+class NumpyLfm2:
+    """Float64 LFM2 decoder (the reference's LFM runtime, src/lib/lfm-wgsl-runtime.ts:727-809).
+
+    Per layer: RMSNorm (eps 1e-5) -> either a gated short convolution
+    (in_proj -> B, C, x; y_t = C * sum_j w_j (B*x)_{t-2+j} over the last three
+    positions; out_proj) or GQA attention (q/k/v, per-head q/k RMSNorm, split-half
+    RoPE with base 1e6, softmax(q.K / sqrt(hd)) V, output projection); residual;
+    RMSNorm -> SwiGLU -> residual. Final RMSNorm (token_embd_norm) and the tied
+    embedding as lm_head. A layer is a convolution layer when it holds
+    shortconv.conv.weight. Closed forms in float64: the convolution is evaluated
+    from a list of every position's B*x, not from a shifted state."""
+
+    def __init__(self, path: str, vocab: int, max_context: int, kv_f16: bool = False):
+        g: Gguf = read_gguf(path)
+        p = "lfm2."
+        self.L = int(g.kv[p + "block_count"])
+        self.H = int(g.kv[p + "embedding_length"])
+        self.nh = int(g.kv[p + "attention.head_count"])
+        kv = g.kv[p + "attention.head_count_kv"]
+        self.lnkv = [int(x) for x in kv] if isinstance(kv, (list, tuple)) else [int(kv)] * self.L
+        self.hd = int(g.kv.get(p + "attention.key_length", self.H // self.nh))
+        self.eps = 1e-5
+        self.vocab = vocab
+        self.ctx = max_context
+        self.kv_f16 = kv_f16
+        f = lambda n: matrix(g, n).astype(np.float64)
+        self.emb = f("token_embd.weight")
+        self.final_norm = f("token_embd_norm.weight")
+        self.layers = []
+        for i in range(self.L):
+            b = f"blk.{i}."
+            lay = dict(in_norm=f(b + "attn_norm.weight"), post=f(b + "ffn_norm.weight"), gate=f(b + "ffn_gate.weight"),
+                       up=f(b + "ffn_up.weight"), down=f(b + "ffn_down.weight"))
+            lay["conv"] = (b + "shortconv.conv.weight") in g.tensors
+            if lay["conv"]:
+                lay.update(w=f(b + "shortconv.conv.weight").reshape(self.H, 3), inp=f(b + "shortconv.in_proj.weight"),
+                           out=f(b + "shortconv.out_proj.weight"))
+            else:
+                lay.update(q=f(b + "attn_q.weight"), k=f(b + "attn_k.weight"), v=f(b + "attn_v.weight"),
+                           o=f(b + "attn_output.weight"), qn=f(b + "attn_q_norm.weight"),
+                           kn=f(b + "attn_k_norm.weight"))
+            self.layers.append(lay)
+        self.reset()
+
+    def reset(self):
+        self.pos = 0
+        self.K = [[] for _ in range(self.L)]
+        self.V = [[] for _ in range(self.L)]
+        self.bx = [[] for _ in range(self.L)]  # every position's B * x, per convolution layer
+
+    def _rms(self, x, w):
+        return x / np.sqrt(np.mean(x * x) + self.eps) * w
+
+    def _rope(self, x):
+        half = self.hd // 2
+        ang = self.pos * np.power(1e6, -2.0 * np.arange(half) / self.hd)
+        co, si = np.cos(ang), np.sin(ang)
+        a, b = x[:, :half], x[:, half:]
+        return np.concatenate([a * co - b * si, a * si + b * co], axis=1)
+
+    def step(self, token: int) -> np.ndarray:
+        H, hd = self.H, self.hd
+        x = self.emb[token].copy()
+        for i, lay in enumerate(self.layers):
+            n = self._rms(x, lay["in_norm"])
+            if lay["conv"]:
+                pr = lay["inp"] @ n
+                B, C, xx = pr[:H], pr[H:2 * H], pr[2 * H:]
+                self.bx[i].append(B * xx)
+                hist = ([np.zeros(H)] * 2 + self.bx[i])[-3:]  # positions t-2, t-1, t (zeros before 0)
+                conv = sum(lay["w"][:, j] * hist[j] for j in range(3))
+                o = lay["out"] @ (C * conv)
+            else:
+                nkv = self.lnkv[i]
+                q = (lay["q"] @ n).reshape(self.nh, hd)
+                k = (lay["k"] @ n).reshape(nkv, hd)
+                v = (lay["v"] @ n).reshape(nkv, hd)
+                q = self._rope(np.stack([self._rms(h, lay["qn"]) for h in q]))
+                k = self._rope(np.stack([self._rms(h, lay["kn"]) for h in k]))
+                if self.kv_f16:
+                    k = k.astype(np.float16).astype(np.float64)
+                    v = v.astype(np.float16).astype(np.float64)
+                self.K[i].append(k)
+                self.V[i].append(v)
+                KK, VV = np.stack(self.K[i]), np.stack(self.V[i])  # [t, nkv, hd]
+                grp = self.nh // nkv
+                att = np.empty((self.nh, hd))
+                for h in range(self.nh):
+                    s = KK[:, h // grp] @ q[h] / np.sqrt(hd)
+                    pw = np.exp(s - s.max())
+                    att[h] = (pw / pw.sum()) @ VV[:, h // grp]
+                o = lay["o"] @ att.reshape(-1)
+            x = x + o
+            n = self._rms(x, lay["post"])
+            gte, up = lay["gate"] @ n, lay["up"] @ n
+            x = x + lay["down"] @ (gte / (1 + np.exp(-gte)) * up)
+        self.pos += 1
+        self.last_hidden = x
+        return self.emb[: self.vocab] @ self._rms(x, self.final_norm)

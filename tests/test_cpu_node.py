@@ -54,7 +54,9 @@ def test_exports_and_load_errors(tmp_path):
     assert out["exports"] == sorted(["LlamaWgslEngine", "loadLlamaWgslModel", "generateLlamaWgsl",
                                      "disposeLlamaWgsl", "resetLlamaWgslConversation", "loadPleiasWgslModel",
                                      "generatePleiasWgsl", "disposePleiasWgsl", "loadGptWgslModel",
-                                     "generateGptWgsl", "disposeGptWgsl", "resetGptWgslConversation"])
+                                     "generateGptWgsl", "disposeGptWgsl", "resetGptWgslConversation",
+                                     "loadLfmWgslModel", "generateLfmWgsl", "disposeLfmWgsl",
+                                     "resetLfmWgslConversation"])
     e = out["errors"]
     assert not e[0]["ok"] and "is not configured for the Llama WGSL runtime" in e[0]["message"]
     assert e[1]["code"] == "EIO" and "missing.gguf" in e[1]["message"]

@@ -84,3 +84,28 @@ def test_node_gpt2_generate_matches_oracle(synth):
     r = out["runs"]
     assert r[0]["ids"] == want1 and (r[0]["cached"], r[0]["next"]) == cache1
     assert r[0]["position"] == ref.position
+
+
+def test_node_lfm2_generate_matches_oracle(synth):
+    """loadLfmWgslModel / generateLfmWgsl (lfm-wgsl-runtime.ts:169-306) through the addon on an
+    lfm2 file: ids and cachedNextId (the step after the last id also runs) as the oracle,
+    greedy and sampled; the definition's default penalty is not applied."""
+    w = WORKLOADS["tiny-lfm2"]
+    path = synth("tiny-lfm2")
+    rng = np.random.default_rng(41)
+    p1 = rng.integers(0, w.spec.vocab, 12).tolist()
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, w.max_context, kv_f16=True, eos_ids=w.eos_ids)
+    want1 = ref.generate(p1, 9)
+    cache1 = (list(ref.cached_token_ids), ref.cached_next_id)
+    ref.reset()
+    ref.cached_token_ids, ref.cached_next_id = [], None
+    want2 = ref.generate(p1, 10, temperature=0.8, top_k=20, seed=5)
+    md = model(path, runtime="lfm2-webgpu", vocab=w.spec.vocab, layers=w.spec.layers, maxContext=w.max_context,
+               eosIds=w.eos_ids, kvDtype="float16", defaultRepetitionPenalty=1.5)
+    out = run_driver({"kind": "generate", "model": md, "prompt": p1[:4], "generate": [
+        {"prompt": p1, "opts": {"maxNewTokens": 9}},
+        {"prompt": p1, "opts": {"maxNewTokens": 10, "temperature": 0.8, "topK": 20, "seed": 5}, "reset": True},
+    ]}, timeout=300)
+    r = out["runs"]
+    assert r[0]["ids"] == want1 and (r[0]["cached"], r[0]["next"]) == cache1
+    assert r[1]["ids"] == want2
