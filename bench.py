@@ -81,7 +81,9 @@ def kernel_symbol(cls: str, info: dict) -> str:
         mv = {"gateup": "k_mvr_gelu_ln", "qkv": "k_mvr_store_ln", "oproj": "k_mvr_add_bias", "down": "k_mvr_add_bias"}
     else:  # one-row-per-lane-group kernels (layers after the first; llama/qwen3 prologues)
         mv = {"gateup": "k_mvr_swiglu_norm", "qkv": "k_mvr_store_norm", "oproj": "k_mvr_add_plain",
-              "down": "k_mvr_add_plain"}
+              "down": "k_mvr_add_plain", "inproj": "k_mvr_store_norm", "outproj": "k_mvr_add_conv"}
+    if info["ffn"] > 4096 and "down" in mv and os.environ.get("CHONK_MV") != "generic":
+        mv["down"] = "k_mvr_add_bias_wide"  # rows above 4096 stage the input through LDS
     return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
 
 
@@ -243,7 +245,8 @@ def main() -> int:
               "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
         return 2
 
-    from chonklm_amd import WORKLOADS, generate_llama_wgsl, load_gpt_wgsl_model, load_llama_wgsl_model
+    from chonklm_amd import (WORKLOADS, generate_llama_wgsl, load_gpt_wgsl_model, load_lfm_wgsl_model,
+                             load_llama_wgsl_model)
 
     if args.calibrate_copy:
         import torch
@@ -265,7 +268,8 @@ def main() -> int:
     ctx = w.prompt_tokens + 1 + args.warmup + args.steps + 8
     md = w.model_def(path)
     md.max_context = ctx
-    loaded = (load_gpt_wgsl_model if md.runtime == "gpt-webgpu" else load_llama_wgsl_model)(md)
+    loaded = {"gpt-webgpu": load_gpt_wgsl_model, "lfm2-webgpu": load_lfm_wgsl_model}.get(
+        md.runtime, load_llama_wgsl_model)(md)
     eng = loaded.engine
     info = eng.info
     prompt = w.prompt(1234)
@@ -318,7 +322,9 @@ def main() -> int:
     kvdim = info["kv_heads"] * info["head_dim"]
     mean_pos = (pos0 + args.warmup + pos_end) / 2.0
     kv_elem = 2 if info.get("kv_dtype", 0) == 0 else 4
-    kv_bytes = 2 * info["layers"] * kvdim * (mean_pos + 1) * kv_elem
+    # (lfm2: only the attention layers hold a K/V cache)
+    kv_layers = sum(1 for k in (w.spec.layer_kv_heads or [1] * info["layers"]) if k > 0)
+    kv_bytes = 2 * kv_layers * kvdim * (mean_pos + 1) * kv_elem
     step_bytes = info["weight_bytes_per_token"] + kv_bytes
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
@@ -406,7 +412,7 @@ def main() -> int:
     if args.cold_reps > 0 and not args.no_kernel_times:
         result["kernel_cold_warm"] = kernel_cold_warm(eng, info, args.cold_reps)
         result["q4k_matvec_hbm"] = q4k_matvec_bandwidth()
-    if not args.no_batched and info.get("kv_dtype", 0) == 0 and info.get("architecture") != 3:
+    if not args.no_batched and info.get("kv_dtype", 0) == 0 and info.get("architecture") not in (3, 5):
         result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4)
     if not args.no_cpu_baseline:
         threads = min(16, host_cpus())  # the GPU box's CPU share is 16 threads

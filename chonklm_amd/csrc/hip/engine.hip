@@ -784,9 +784,11 @@ void use_row_kernel(MvArgs& a) {
   needs_row = needs_row || a.pro == PRO_CONV || a.conv_commit;
   for (int i = 0; i < a.nseg; ++i) needs_row = needs_row || a.seg[i].bias;
   if ((off && !needs_row) || a.epi == EPI_LOGITS) return;
-  // the register-resident plain / norm prologues hold at most 4 float4 per thread
-  // (GPT-2's wider ffn_down rows take the LDS-staged variant of its row kernel)
-  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg && !(needs_row && a.pro == PRO_PLAIN)) {
+  // the register-resident plain / norm prologues hold at most 4 float4 per thread;
+  // wider rows of the plain prologue with the residual add (ffn_down) take the
+  // LDS-staged variant of the row kernel
+  const bool wide_ok = a.pro == PRO_PLAIN && a.epi == EPI_ADD;
+  if ((a.pro == PRO_PLAIN || a.pro == PRO_NORM) && a.k > 4 * 4 * kWg && !wide_ok) {
     if (needs_row) throw Error(CHONK_EINVAL, "row-kernel prologues hold at most 4096 elements (the plain one excepted)");
     return;
   }

@@ -779,7 +779,8 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
       case EPI_STORE * 8 + PRO_EMBED_NORM: k = k_mvr_store_embed; break;
       case EPI_STORE * 8 + PRO_RES_NORM: k = k_mvr_store_resnorm; break;
       case EPI_ADD * 8 + PRO_PLAIN:
-        k = !gb ? k_mvr_add_plain : a.k > 4 * 4 * kWg ? k_mvr_add_bias_wide : k_mvr_add_bias;
+        // (rows wider than the register-resident prologue's 4096 stage the input through LDS)
+        k = a.k > 4 * 4 * kWg ? k_mvr_add_bias_wide : !gb ? k_mvr_add_plain : k_mvr_add_bias;
         break;
       case EPI_ADD * 8 + PRO_CONV:
         if (gb || a.k > 4 * 4 * kWg) return hipErrorInvalidValue;
