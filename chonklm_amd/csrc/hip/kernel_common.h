@@ -235,6 +235,28 @@ __device__ __forceinline__ void quantize_x(const float* xs, int K, void* base, f
     quantize4(reinterpret_cast<const float4*>(xs)[i4], i4, K, base, xs16);
 }
 
+// Stores elements 4*i4 .. 4*i4+3 of x into the fp32 unit layout of type T
+// (qdot.h: X[v * U + u], run sums S[u]). Lane pairs hold consecutive i4 (the
+// caller's threads cover i4 in order, K a multiple of 32), and both lanes of a
+// pair call it together: the even lane stores the pair's 8-element sum.
+template <int T>
+__device__ __forceinline__ void xf_put(const float4 v, int i4, int U, float4* X, float* S) {
+  int u, e;
+  unit_of_col<T>(4 * i4, u, e);
+  X[(e >> 2) * U + u] = v;
+  const float s4 = (v.x + v.y) + (v.z + v.w);
+  const float s8 = s4 + dpp<0xb1>(s4);
+  if ((i4 & 1) == 0) S[4 * u + (e >> 3)] = s8;
+}
+
+// The same from the fp32 vector xs[K] in LDS. All threads call it after a
+// barrier that follows the last write of xs; a barrier must separate it from
+// the first read of X / S.
+template <int T>
+__device__ __forceinline__ void xf_build(const float* xs, int K, float4* X, float* S) {
+  for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg) xf_put<T>(reinterpret_cast<const float4*>(xs)[i4], i4, K >> 5, X, S);
+}
+
 // A lane's share of a matvec task: lane group lg (of ng groups of lpr lanes)
 // owns virtual rows lg, lg + ng, ... (GLU: even rows gate, odd rows up); lane
 // li owns units li, li + lpr, ... of each row.

@@ -141,8 +141,9 @@ __device__ __forceinline__ void mv_stage(const MvPro& a, const MvLds& l) {
 }
 
 // Completes the prologue once the staged data has landed: xs becomes the
-// matvec input (normalised as the mode requires), xs16 its 16-element sums.
-__device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
+// matvec input, normalised as the mode requires (ends with a barrier after
+// the last write of xs, or with none when xs is the staged input itself).
+__device__ __forceinline__ void mv_norm(const MvPro& a, const MvLds& l) {
   const int K = a.k, tid = threadIdx.x;
   float* xs = l.xs;
   if (a.pro == PRO_EMBED_NORM || a.pro == PRO_EMBED_LN) {
@@ -210,7 +211,12 @@ __device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
     for (int i = tid; i < K; i += kWg) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), l.wn[i]);
     __syncthreads();
   }
-  quantize_x(xs, K, l.dl, l.xs16);  // dl / wd are free from here on
+}
+
+// mv_norm, then the integer-digit form of xs (dl) and its 16-element sums.
+__device__ __forceinline__ void mv_finish(const MvPro& a, const MvLds& l) {
+  mv_norm(a, l);
+  quantize_x(l.xs, a.k, l.dl, l.xs16);  // dl / wd are free from here on
   __syncthreads();
 }
 
@@ -392,6 +398,8 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   const bool owner = li == 0 && lg < nt;
   const int row = t0 + min(lg, nt - 1);
   const int U = a.k >> 5;
+  // x in the fp32 unit layout (qdot.h): X in dl, the run sums in wd
+  float4* xfx = reinterpret_cast<float4*>(l.dl);
   uint64_t tr[8];
   CHONK_MV_T(tr, 0);
   MvPro p = mv_pro(a);
@@ -456,6 +464,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
         ss = wave_sum(ss);
         if ((threadIdx.x & 63) == 0) l.red[threadIdx.x >> 6] = ss;
         __syncthreads();
+        CHONK_MV_T(tr, 5);
         ss = (l.red[0] + l.red[1]) + (l.red[2] + l.red[3]);
         const float inv = 1.0f / sqrtf(ss / (float)a.k + p.eps);
 #pragma unroll
@@ -469,23 +478,25 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i4 = (int)threadIdx.x + kWg * r;
-        if (i4 < n4) quantize4(xv[r], i4, a.k, l.dl, l.xs16);
+        if (i4 < n4) xf_put<T>(xv[r], i4, U, xfx, l.wd);
       }
       __syncthreads();
     } else {
-      mv_finish(p, l);
+      mv_norm(p, l);
+      xf_build<T>(l.xs, a.k, xfx, l.wd);
+      __syncthreads();
     }
     CHONK_MV_T(tr, 2);
-    const XqView xv = xq_view(l.dl, l.xs16, a.k);
     float ag = 0.f, au = 0.f;
 #pragma unroll
     for (int j = 0; j < kRowUnits; ++j) {
       const int u = li + j * lpr;
       if (j * lpr < U && u < U) {
-        XU xr;
-        load_xu<T>(xv, u, xr);
-        ag += dot_q<T>(fg[j], u, xr);
-        if constexpr (glu) au += dot_q<T>(fu[j], u, xr);
+        XF xr;
+        load_xf(xfx, (const float4*)l.wd, U, u, xr);
+        if (j == 0) CHONK_MV_T(tr, 6);
+        ag += dot_f<T>(fg[j], u, xr);
+        if constexpr (glu) au += dot_f<T>(fu[j], u, xr);
       }
     }
     rg = group_sum_n(ag, lpr);

@@ -368,6 +368,161 @@ __device__ __forceinline__ float dot_q<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, c
   return h2f(f.d) * dot_q5_codes(f.qs, f.qh, x) + h2f(f.m) * x.s[0];
 }
 
+// ---- fp32 activation form (decode row kernels) ----------------------------------
+// The row kernels keep x in fp32 and skip the integer-digit conversion, whose
+// per-workgroup cost (every workgroup converts the whole vector) dominates a
+// decode matvec. Layout in LDS, U = K/32 units, unit-local element order
+// e = 0..31 as in unit_col:
+//   X[v * U + u]  float4: elements 4v .. 4v+3 of unit u (v = 0..7)
+//   S[u]          float4: sums of x over the unit's 8-element runs e in [8k, 8k+8)
+// Lanes of a row group read consecutive units, so every 16-byte LDS read of a
+// wave touches consecutive slots. The sums give each type's factored offset
+// term (Q4_K/Q5_K halves, Q6_K quarters, Q8_0/Q5_x whole blocks).
+
+// Unit u and unit-local element e of row column c (inverse of unit_col).
+template <int T>
+__device__ __forceinline__ void unit_of_col(int c, int& u, int& e) {
+  if constexpr (T == QT_Q4_K || T == QT_Q5_K) {
+    const int r = c & 255, r2 = r & 63, r3 = r2 & 31;
+    u = (c >> 8) * 8 + 2 * (r >> 6) + (r3 >> 4);
+    e = (r2 >> 5) * 16 + (r3 & 15);
+  } else if constexpr (T == QT_Q6_K) {
+    const int r = c & 255, r2 = r & 127, r3 = r2 & 31;
+    u = (c >> 8) * 8 + 4 * (r >> 7) + (r3 >> 3);
+    e = 8 * (r2 >> 5) + (r3 & 7);
+  } else {
+    u = c >> 5;
+    e = c & 31;
+  }
+}
+
+// x for one unit: the eight float4 and the four run sums.
+struct XF {
+  float4 x[8];
+  float4 s;
+};
+
+__device__ __forceinline__ void load_xf(const float4* X, const float4* S, int U, int u, XF& r) {
+#pragma unroll
+  for (int v = 0; v < 8; ++v) r.x[v] = X[v * U + u];
+  r.s = S[u];
+}
+
+__device__ __forceinline__ float ub(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+__device__ __forceinline__ float sb(uint32_t w, int i) { return (float)(int)(int8_t)((w >> (8 * i)) & 0xffu); }
+__device__ __forceinline__ float dot4u(float4 a, uint32_t w) {
+  return (a.x * ub(w, 0) + a.y * ub(w, 1)) + (a.z * ub(w, 2) + a.w * ub(w, 3));
+}
+
+// sum over the unit of x * w (w dequantized) in fp32, factored as the
+// integer-digit dot_q: d * sc * sum(x * q) - dmin * m * sum(x) and the like.
+template <int T>
+__device__ __forceinline__ float dot_f(const Frag<T>& f, int u, const XF& x);
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q4_K>(const Frag<QT_Q4_K>& f, int u, const XF& x) {
+  const int g = (u & 7) >> 1;
+  const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    lo += dot4u(x.x[v], q[v] & 0x0f0f0f0fu);
+    hi += dot4u(x.x[4 + v], (q[v] >> 4) & 0x0f0f0f0fu);
+  }
+  uint32_t sc0, m0, sc1, m1;
+  scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
+  scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
+  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
+  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * (x.s.x + x.s.y) + (float)m1 * (x.s.z + x.s.w));
+}
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q5_K>(const Frag<QT_Q5_K>& f, int u, const XF& x) {
+  const int g = (u & 7) >> 1;
+  const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
+  const uint32_t h[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t wl = (q[v] & 0x0f0f0f0fu) | (((h[v] >> (2 * g)) & 0x01010101u) << 4);
+    const uint32_t wh = ((q[v] >> 4) & 0x0f0f0f0fu) | (((h[v] >> (2 * g + 1)) & 0x01010101u) << 4);
+    lo += dot4u(x.x[v], wl);
+    hi += dot4u(x.x[4 + v], wh);
+  }
+  uint32_t sc0, m0, sc1, m1;
+  scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
+  scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
+  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
+  return d * ((float)sc0 * lo + (float)sc1 * hi) - dmin * ((float)m0 * (x.s.x + x.s.y) + (float)m1 * (x.s.z + x.s.w));
+}
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q6_K>(const Frag<QT_Q6_K>& f, int u, const XF& x) {
+  // codes 0..63, the -32 offset through the run sums
+  const int b = u & 3;
+  const uint32_t qa[2] = {f.qa.x, f.qa.y}, qb[2] = {f.qb.x, f.qb.y}, qh[2] = {f.qh.x, f.qh.y};
+  const float sr[4] = {x.s.x, x.s.y, x.s.z, x.s.w};
+  float acc = 0.f;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const uint32_t* src = (qd & 1) ? qb : qa;
+    const int shift = qd < 2 ? 0 : 4;
+    float s = 0.f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t w = ((src[half] >> shift) & 0x0f0f0f0fu) | (((qh[half] >> (2 * qd)) & 0x03030303u) << 4);
+      s += dot4u(x.x[2 * qd + half], w);
+    }
+    s -= 32.0f * sr[qd];
+    const int si = (b >> 1) + 2 * qd;
+    const uint32_t sw = si < 4 ? f.sc.x : f.sc.y;
+    acc += (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * s;
+  }
+  return h2f(f.d) * acc;
+}
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q8_0>(const Frag<QT_Q8_0>& f, int u, const XF& x) {
+  const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int v = 0; v < 8; v += 2) {
+    a0 += (x.x[v].x * sb(q[v], 0) + x.x[v].y * sb(q[v], 1)) + (x.x[v].z * sb(q[v], 2) + x.x[v].w * sb(q[v], 3));
+    a1 += (x.x[v + 1].x * sb(q[v + 1], 0) + x.x[v + 1].y * sb(q[v + 1], 1)) +
+          (x.x[v + 1].z * sb(q[v + 1], 2) + x.x[v + 1].w * sb(q[v + 1], 3));
+  }
+  (void)u;
+  return h2f(f.d) * (a0 + a1);
+}
+
+// Q5_0 / Q5_1 codes 0..31 (fifth bit from qh): sum(x * code)
+__device__ __forceinline__ float dot_q5f_codes(const uint4 qs, uint32_t qh, const XF& x) {
+  const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t hl = ((((qh >> (4 * v)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+    const uint32_t hh = ((((qh >> (16 + 4 * v)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+    lo += dot4u(x.x[v], (q[v] & 0x0f0f0f0fu) | hl);
+    hi += dot4u(x.x[4 + v], ((q[v] >> 4) & 0x0f0f0f0fu) | hh);
+  }
+  return lo + hi;
+}
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q5_0>(const Frag<QT_Q5_0>& f, int u, const XF& x) {
+  (void)u;
+  const float s = (x.s.x + x.s.y) + (x.s.z + x.s.w);
+  return h2f(f.d) * (dot_q5f_codes(f.qs, f.qh, x) - 16.0f * s);
+}
+
+template <>
+__device__ __forceinline__ float dot_f<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, const XF& x) {
+  (void)u;
+  const float s = (x.s.x + x.s.y) + (x.s.z + x.s.w);
+  return h2f(f.d) * dot_q5f_codes(f.qs, f.qh, x) + h2f(f.m) * s;
+}
+
 // ---- exact dequantization ------------------------------------------------------
 // out[e] for unit-local element e (placement per unit_col), computed with the
 // reference's fp32 operation order and no contraction.
