@@ -81,7 +81,10 @@ def kernel_symbol(cls: str, info: dict) -> str:
         mv = {"gateup": "k_mvr_gelu_ln", "qkv": "k_mvr_store_ln", "oproj": "k_mvr_add_bias", "down": "k_mvr_add_bias"}
     else:  # one-row-per-lane-group kernels (layers after the first; llama/qwen3 prologues)
         mv = {"gateup": "k_mvr_swiglu_norm", "qkv": "k_mvr_store_norm", "oproj": "k_mvr_add_plain",
-              "down": "k_mvr_add_plain", "inproj": "k_mvr_store_norm", "outproj": "k_mvr_add_conv"}
+              "down": "k_mvr_add_plain", "inproj": "k_mvr_store_norm", "outproj": "k_mvr_add_conv",
+              "ssm": "k_mamba_ssm"}
+        if info.get("architecture") == 6:  # granitehybrid: out_proj's prologue is the gated norm
+            mv["outproj"] = "k_mvr_add_gate"
     if info["ffn"] > 4096 and "down" in mv and os.environ.get("CHONK_MV") != "generic":
         mv["down"] = "k_mvr_add_bias_wide"  # rows above 4096 stage the input through LDS
     return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
@@ -245,7 +248,8 @@ def main() -> int:
               "(see DESIGN.md, 'More than one GPU'); run with --gpus 1", file=sys.stderr)
         return 2
 
-    from chonklm_amd import (WORKLOADS, generate_llama_wgsl, load_gpt_wgsl_model, load_lfm_wgsl_model,
+    from chonklm_amd import (WORKLOADS, generate_llama_wgsl, load_gpt_wgsl_model, load_granite_wgsl_model,
+                             load_lfm_wgsl_model,
                              load_llama_wgsl_model)
 
     if args.calibrate_copy:
@@ -268,7 +272,8 @@ def main() -> int:
     ctx = w.prompt_tokens + 1 + args.warmup + args.steps + 8
     md = w.model_def(path)
     md.max_context = ctx
-    loaded = {"gpt-webgpu": load_gpt_wgsl_model, "lfm2-webgpu": load_lfm_wgsl_model}.get(
+    loaded = {"gpt-webgpu": load_gpt_wgsl_model, "lfm2-webgpu": load_lfm_wgsl_model,
+              "granite-webgpu": load_granite_wgsl_model}.get(
         md.runtime, load_llama_wgsl_model)(md)
     eng = loaded.engine
     info = eng.info

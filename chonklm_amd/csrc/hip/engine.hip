@@ -174,6 +174,7 @@ struct LayerCfg {
   int window = 0;
   int heads = 0, kv_heads = 0, ffn = 0;  // openelm varies them per layer
   bool conv = false;                     // lfm2: a gated short-convolution layer instead of attention
+  bool mamba = false;                    // granitehybrid: a Mamba2 layer instead of attention
 };
 
 struct ModelCfg {
@@ -183,6 +184,9 @@ struct ModelCfg {
   int gmax = 1;          // largest GQA group of any layer
   bool gpt = false;  // GGUF architecture gpt2: the reference's GPT runtime (gpt-wgsl-runtime.ts)
   bool lfm = false;  // GGUF architecture lfm2: the reference's LFM runtime (lfm-wgsl-runtime.ts)
+  bool granite = false;  // GGUF architecture granitehybrid: the reference's Granite runtime (granite-wgsl-runtime.ts)
+  int ssm_inner = 0, ssm_conv = 0, ssm_heads = 0;  // granitehybrid Mamba2: inner size, xBC channels, heads
+  float res_scale = 0, logit_scale = 0;            // granitehybrid: residual x0.246, logits x1/3 (0: none)
   int pos_rows = 0;  // gpt2: rows of the learned position table (gpt2.context_length)
   int hidden = 0, ffn = 0, vocab = 0, layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float eps = 1e-5f, qk_eps = 1e-5f, scale = 0, embed_scale = 1;
@@ -302,6 +306,98 @@ ModelCfg build_config(const GgufFile& g, const chonk_model_def& def) {
       throw Error(CHONK_EINVAL, "LFM argmax supports at most 65536 vocab entries, got " + std::to_string(c.vocab));
     return c;
   }
+  if (c.arch == "granitehybrid") {
+    // The Granite runtime (granite-wgsl-runtime.ts:309-371, :526-624) fixes the
+    // Granite-4.0-H-350M shape in code; here the dimensions come from the
+    // tensor shapes with the same fixed SSM head width (32), state size (128),
+    // 4 conv taps and head_dim 64, and the constants stay the reference's: eps
+    // 1e-5, embedding x12, residual x0.246, attention scores x0.015625 without
+    // rotary embedding, logits x1/3, 4096 positions. A layer holding
+    // blk.N.ssm_in.weight is a Mamba2 layer (the registry's layerTypes,
+    // registry.ts:48-53, list the same layers).
+    c.granite = true;
+    const std::string id = def.id ? def.id : "";
+    const GgufValue* ft = g.value("general.file_type");
+    const int file_type = ft && ft->is_number() ? (int)ft->number : -1;
+    if (file_type != 7 && file_type != 15)  // validateGraniteGguf (:359-371)
+      throw Error(CHONK_EINVAL, "Granite WGSL " + id + ": expected GGUF Q8_0 or Q4_K_M file_type, got " +
+                                    std::to_string(file_type));
+    for (const char* name : {"token_embd.weight", "output_norm.weight", "blk.0.attn_norm.weight"})
+      if (!g.find(name)) throw Error(CHONK_EINVAL, "Granite WGSL " + id + ": GGUF missing tensor " + name);
+    for (const GgufTensorInfo& t : g.tensors)  // dtypeForGgmlType (:373-390)
+      if (t.type != GGML_F32 && t.type != GGML_F16 && t.type != GGML_Q8_0 && t.type != GGML_Q4_K &&
+          t.type != GGML_Q6_K)
+        throw Error(CHONK_EINVAL, "Granite WGSL unsupported GGML tensor type " + type_name(t.type));
+    const GgufTensorInfo* te = g.find("token_embd.weight");
+    if (te->shape.size() != 2) throw Error(CHONK_EINVAL, "Granite WGSL tensor token_embd.weight is not a matrix");
+    c.hidden = (int)te->shape[0];
+    c.vocab = (int)te->shape[1];
+    int nl = 0;
+    while (g.find("blk." + std::to_string(nl) + ".attn_norm.weight")) ++nl;
+    c.layers = nl;
+    c.hd = 64;
+    c.ctx = 4096;
+    c.eps = c.qk_eps = 1e-5f;
+    c.scale = 0.015625f;
+    c.embed_scale = 12.0f;
+    c.res_scale = 0.246f;
+    c.logit_scale = (float)0.3333333333333333;
+    c.heads = c.kv_heads = c.ffn = 0;
+    auto rows = [&](const std::string& name) -> int {
+      const GgufTensorInfo* t = g.find(name);
+      if (!t || t->shape.size() != 2) throw Error(CHONK_EINVAL, "Granite WGSL manifest missing tensor " + name);
+      return (int)t->shape[1];
+    };
+    for (int i = 0; i < nl; ++i) {
+      const std::string p = "blk." + std::to_string(i) + ".";
+      LayerCfg L;
+      L.theta = 0;  // STORE_KV_WGSL stores k as projected: no rotary embedding
+      L.mamba = g.find(p + "ssm_in.weight") != nullptr;
+      L.ffn = rows(p + "ffn_gate.weight");
+      c.ffn = std::max(c.ffn, L.ffn);
+      if (L.mamba) {
+        // the inner size is out_proj's row length
+        const GgufTensorInfo* so = g.find(p + "ssm_out.weight");
+        if (!so || so->shape.size() != 2)
+          throw Error(CHONK_EINVAL, "Granite WGSL manifest missing tensor " + p + "ssm_out.weight");
+        const int inner = (int)so->shape[0];
+        if (c.ssm_inner && inner != c.ssm_inner)
+          throw Error(CHONK_EINVAL, "Granite WGSL: the SSM inner size differs between layers");
+        c.ssm_inner = inner;
+      } else {
+        L.heads = rows(p + "attn_q.weight") / c.hd;
+        L.kv_heads = rows(p + "attn_k.weight") / c.hd;
+        c.heads = std::max(c.heads, L.heads);
+        c.kv_heads = std::max(c.kv_heads, L.kv_heads);
+      }
+      c.layer.push_back(L);
+    }
+    if (c.layers <= 0 || c.hidden <= 0 || c.ffn <= 0 || c.vocab <= 0)
+      throw Error(CHONK_EINVAL, "model has a non-positive dimension or context");
+    if (c.kv_heads <= 0) throw Error(CHONK_EINVAL, "Granite WGSL GGUF has no attention layer");
+    for (LayerCfg& L : c.layer) {
+      if (L.mamba) {  // (kept valid for the attention geometry; a Mamba2 layer has no heads)
+        L.heads = c.heads;
+        L.kv_heads = c.kv_heads;
+      }
+      if (L.kv_heads <= 0 || L.heads % L.kv_heads != 0 || L.heads / L.kv_heads > 8)
+        throw Error(CHONK_EINVAL, "GQA group size must divide heads and be at most 8");
+      c.gmax = std::max(c.gmax, L.heads / L.kv_heads);
+    }
+    if (c.ssm_inner) {
+      // the Mamba2 kernel's geometry: 32-wide heads, 128 states, one group
+      if (c.ssm_inner % 32 != 0 || c.ssm_inner > 4096)
+        throw Error(CHONK_EINVAL, "Granite WGSL: the SSM inner size must be a multiple of 32 and at most 4096");
+      c.ssm_heads = c.ssm_inner / 32;
+      c.ssm_conv = c.ssm_inner + 2 * 128;
+    }
+    if (c.hidden > 4096 || c.hidden % 32 != 0)
+      throw Error(CHONK_EINVAL, "Granite WGSL hidden size must be a multiple of 32 and at most 4096");
+    // the class-major lm_head: one workgroup per residue class of at most 512 ids
+    if (c.vocab > 131072)
+      throw Error(CHONK_EINVAL, "Granite WGSL argmax supports at most 131072 vocab entries, got " + std::to_string(c.vocab));
+    return c;
+  }
   if (c.arch != "qwen3" && c.arch != "llama" && c.arch != "gemma3" && c.arch != "openelm")
     throw Error(CHONK_EINVAL, "Llama GGUF WGSL does not support architecture " + c.arch);
   c.gemma = c.arch == "gemma3";
@@ -383,6 +479,11 @@ struct LayerDev {
   float* conv_w = nullptr;   // [hidden][3] taps
   float *conv_s1 = nullptr, *conv_s2 = nullptr;  // B * x two positions and one position back
   DevMat qkv;  // gpt2: fused q|k|v
+  // granitehybrid Mamba2 layer: in_proj (rows z | xBC | dt), out_proj, conv taps
+  // [conv][4] and bias, per-head dt bias / A / D, gated-norm weight; state
+  DevMat ssm_in, ssm_out;
+  float *c1d_w = nullptr, *c1d_b = nullptr, *dt_b = nullptr, *a_neg = nullptr, *d_w = nullptr, *ssm_norm = nullptr;
+  float *ssm_state = nullptr, *mconv_state = nullptr;  // [heads][32][128], [2][conv][3]
   // gpt2: LayerNorm biases (in_norm / post_norm hold the weights) and linear biases
   float *in_norm_b = nullptr, *post_norm_b = nullptr, *qkv_b = nullptr, *o_b = nullptr, *up_b = nullptr,
         *down_b = nullptr;
@@ -392,8 +493,9 @@ struct LayerDev {
 };
 
 struct Launch {
-  enum Kind { MV, ATTN, SEL, STEP } kind = MV;
+  enum Kind { MV, ATTN, SEL, STEP, SSM } kind = MV;
   MvArgs mv{};
+  SsmArgs ssm{};
   AttnArgs at{};
   SelArgs sel{};
   StepArgs step{};
@@ -429,6 +531,7 @@ struct chonk_engine {
   float *resA = nullptr, *resB = nullptr, *delta = nullptr, *qkv = nullptr, *attn = nullptr, *ff = nullptr,
         *logits = nullptr, *part = nullptr;
   float* conv_proj = nullptr;  // lfm2: [3 * hidden] in_proj output of the current convolution layer
+  float *mproj = nullptr, *my = nullptr;  // granitehybrid: Mamba2 in_proj output, scan output
   Candidate* cand = nullptr;
   uint32_t* cnt = nullptr;
   void* uncached = nullptr;       // part + cnt, from the uncached pool
@@ -685,6 +788,34 @@ float* lfm_floats(Arena& arena, const ByteSource& src, const GgufFile& g, const 
   return upload_floats(arena, src, g, name, n);
 }
 
+// The Granite loader's checks (granite-wgsl-runtime.ts:397-491) with its
+// wording: a missing tensor, a linear tensor that is not a quantized matrix of
+// shape [k, n], a float tensor that is not F32 / F16.
+const GgufTensorInfo& granite_tensor(const GgufFile& g, const std::string& name) {
+  const GgufTensorInfo* t = g.find(name);
+  if (!t) throw Error(CHONK_EINVAL, "Granite WGSL manifest missing tensor " + name);
+  return *t;
+}
+const GgufTensorInfo& granite_linear(const GgufFile& g, const std::string& name, int64_t K, int64_t N) {
+  const GgufTensorInfo& t = granite_tensor(g, name);
+  if (t.type != GGML_Q8_0 && t.type != GGML_Q4_K && t.type != GGML_Q6_K)
+    throw Error(CHONK_EINVAL, "Granite WGSL tensor " + name + " is " + type_name(t.type) +
+                                  ", expected a GGUF quantized matrix");
+  if (t.shape.size() != 2 || (int64_t)t.shape[0] != K || (int64_t)t.shape[1] != N) {
+    std::string got;
+    for (size_t i = 0; i < t.shape.size(); ++i) got += (i ? ", " : "") + std::to_string(t.shape[i]);
+    throw Error(CHONK_EINVAL, "Granite WGSL tensor " + name + " shape [" + got + "], expected [" + std::to_string(K) +
+                                  ", " + std::to_string(N) + "]");
+  }
+  return t;
+}
+float* granite_floats(Arena& arena, const ByteSource& src, const GgufFile& g, const std::string& name, int64_t n) {
+  const GgufTensorInfo& t = granite_tensor(g, name);
+  if (t.type != GGML_F32 && t.type != GGML_F16)
+    throw Error(CHONK_EINVAL, "Granite WGSL tensor " + name + " is " + type_name(t.type) + ", expected float32/float16");
+  return upload_floats(arena, src, g, name, n);
+}
+
 // Rows of the class-major lm_head copy: 256 classes (id mod 256) of
 // ceil(V / 256) rows each.
 int64_t class_rows(int64_t V) { return 256 * ((V + 255) / 256); }
@@ -918,10 +1049,80 @@ void build_steps(chonk_engine* e) {
         steps.push_back(L);
       }
     }
+    if (lc.mamba) {
+      // GraniteWgslEngine.runToken's Mamba branch (granite-wgsl-runtime.ts:786-791):
+      // in_proj with the input norm as prologue; the convolution and selective
+      // scan; out_proj whose prologue is MAMBA_GATE_NORM and whose epilogue is
+      // the scaled residual add (the reference's addScaledRmsNorm add)
+      {
+        Launch L;
+        MvArgs a = mv_base();
+        a.k = H;
+        a.nseg = 1;
+        plan_seg(a.seg[0], Ld.ssm_in.q, c.ssm_inner + c.ssm_conv + c.ssm_heads, false, 0);
+        a.seg[0].out = e->mproj;
+        a.epi = EPI_STORE;
+        a.w_norm = Ld.in_norm;
+        if (i == 0) {
+          a.pro = PRO_EMBED_NORM;
+          a.res_out = e->resA;
+        } else {
+          a.pro = PRO_NORM;
+          a.in = e->resA;
+        }
+        finish(L, a, a.seg[0].tile);
+        L.name = li + "inproj";
+        L.weight_bytes = Ld.ssm_in.gguf_bytes + (i == 0 ? e->embed.gguf_bytes / c.vocab : 0);
+        L.layer = i;
+        steps.push_back(L);
+      }
+      {
+        Launch L;
+        L.kind = Launch::SSM;
+        SsmArgs& m = L.ssm;
+        m.proj = e->mproj;
+        m.conv_w = Ld.c1d_w;
+        m.conv_b = Ld.c1d_b;
+        m.conv_state = Ld.mconv_state;
+        m.dt_bias = Ld.dt_b;
+        m.a_neg = Ld.a_neg;
+        m.d = Ld.d_w;
+        m.ssm_state = Ld.ssm_state;
+        m.y = e->my;
+        m.st = e->st;
+        m.inner = c.ssm_inner;
+        m.conv = c.ssm_conv;
+        m.heads = c.ssm_heads;
+        L.grid = c.ssm_heads * 4;
+        L.name = li + "ssm";
+        L.layer = i;
+        steps.push_back(L);
+      }
+      {
+        Launch L;
+        MvArgs a = mv_base();
+        a.k = c.ssm_inner;
+        a.nseg = 1;
+        plan_seg(a.seg[0], Ld.ssm_out.q, H, false, 0);
+        a.pro = PRO_GATE;
+        a.in = e->my;
+        a.gate_z = e->mproj;
+        a.w_norm = Ld.ssm_norm;
+        a.epi = EPI_ADD;
+        a.seg[0].out = e->resB;
+        a.seg[0].add = e->resA;
+        a.add_scale = c.res_scale;
+        finish(L, a, a.seg[0].tile);
+        L.name = li + "outproj";
+        L.weight_bytes = Ld.ssm_out.gguf_bytes;
+        L.layer = i;
+        steps.push_back(L);
+      }
+    }
     // qkv (gpt2: one fused matrix with bias, LayerNorm prologue; embedding +
     // position on layer 0)
-    if (lc.conv) {
-      // (no attention in a convolution layer)
+    if (lc.conv || lc.mamba) {
+      // (no attention in a convolution or Mamba2 layer)
     } else if (c.gpt) {
       Launch L;
       MvArgs a = mv_base();
@@ -989,7 +1190,7 @@ void build_steps(chonk_engine* e) {
       steps.push_back(L);
     }
     // attention
-    if (!lc.conv) {
+    if (!lc.conv && !lc.mamba) {
       Launch L;
       L.kind = Launch::ATTN;
       AttnArgs& t = L.at;
@@ -1037,7 +1238,7 @@ void build_steps(chonk_engine* e) {
       steps.push_back(L);
     }
     // o projection
-    if (!lc.conv) {
+    if (!lc.conv && !lc.mamba) {
       Launch L;
       MvArgs a = mv_base();
       a.k = qdim;
@@ -1045,6 +1246,7 @@ void build_steps(chonk_engine* e) {
       plan_seg(a.seg[0], Ld.o.q, H, false, 0);
       a.pro = PRO_PLAIN;
       a.in = e->attn;
+      a.add_scale = c.res_scale;  // (granitehybrid: residual + out * 0.246)
       if (c.gemma) {
         a.epi = EPI_STORE;
         a.seg[0].out = e->delta;
@@ -1126,6 +1328,7 @@ void build_steps(chonk_engine* e) {
       plan_seg(a.seg[0], Ld.down.q, H, false, 0);
       a.pro = PRO_PLAIN;
       a.in = e->ff;
+      a.add_scale = c.res_scale;  // (granitehybrid: ADD_SCALED_WGSL's residual + out * 0.246)
       if (c.gemma) {
         a.epi = EPI_STORE;
         a.seg[0].out = e->delta;
@@ -1160,12 +1363,13 @@ void build_steps(chonk_engine* e) {
     sg.tile = 256;
     sg.wg_begin = 0;
     sg.out = e->logits;
-    if (c.lfm) {
+    if (c.lfm || c.granite) {
       // class-major rows: workgroup c computes ids c, c + 256, ... (TOPK256's slot c)
       sg.n_out = (int)class_rows(c.vocab);
       sg.tile = sg.n_out / 256;
       a.lfm_classes = 1;
     }
+    a.logit_scale = c.logit_scale;  // (granitehybrid: SCALE_LOGITS_WGSL's x 1/3)
     a.epi = EPI_LOGITS;
     a.w_norm = e->final_norm;
     a.gpt_argmax = c.gpt ? 1 : 0;
@@ -1183,7 +1387,7 @@ void build_steps(chonk_engine* e) {
       a.pro = PRO_NORM;
       a.in = e->resA;
     }
-    finish(L, a, 256);
+    finish(L, a, std::max(256, sg.tile));
     L.name = "lmhead";
     L.weight_bytes = e->lm_head.gguf_bytes;
     steps.push_back(L);
@@ -1194,7 +1398,7 @@ void build_steps(chonk_engine* e) {
     SelArgs& s = L.sel;
     s.cand = e->cand;
     // (ARGMAX_WGSL's stage over the 256 slots is the same strict-greater tree, lfm-wgsl-runtime.ts:1903-1922)
-    s.gpt_argmax = c.gpt || c.lfm ? 1 : 0;
+    s.gpt_argmax = c.gpt || c.lfm || c.granite ? 1 : 0;
     s.groups = e->groups;
     s.vocab = c.vocab;
     s.ctx = c.ctx;
@@ -1220,7 +1424,7 @@ bool build_step(chonk_engine* e) {
   const int G = c.heads / c.kv_heads;
   const bool kv16 = e->kv_elem == 2;
   if (c.gpt) return false;  // the persistent step runs the llama-family layer only
-  if (c.openelm || c.lfm) return false;  // and one head geometry, attention in every layer
+  if (c.openelm || c.lfm || c.granite) return false;  // and one head geometry, attention in every layer
   if (!step_supported(G, kv16)) return false;
   int cus = 0;
   HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
@@ -1562,6 +1766,7 @@ void enqueue(const Launch& L, hipStream_t s) {
   switch (L.kind) {
     case Launch::MV: HIP_OK(launch_matvec(L.mv, L.grid, L.shmem, s)); break;
     case Launch::ATTN: HIP_OK(launch_attention(L.at, L.shmem, s)); break;
+    case Launch::SSM: HIP_OK(launch_ssm(L.ssm, s)); break;
     case Launch::SEL: HIP_OK(launch_select(L.sel, s)); break;
     case Launch::STEP:
       HIP_OK(launch_step(L.d_step, L.step.phases, L.step_group, L.step_kv16, L.grid, L.shmem, s));
@@ -1640,9 +1845,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     wbytes += stripes_bytes(t.type, N, K);
   };
   auto vec_bytes = [&](int64_t n) { wbytes += align256((size_t)n * 4); };
-  if (c.lfm) {
-    // the embedding, its class-major copy as lm_head, token_embd_norm
-    const GgufTensorInfo& te = lfm_linear(g, "token_embd.weight");
+  if (c.lfm || c.granite) {
+    // the embedding, its class-major copy as lm_head, the final norm
+    const GgufTensorInfo& te = c.granite ? granite_linear(g, "token_embd.weight", H, c.vocab)
+                                         : lfm_linear(g, "token_embd.weight");
     check_matrix(te, H, c.vocab);
     wbytes += stripes_bytes(te.type, c.vocab, H) + stripes_bytes(te.type, class_rows(c.vocab), H);
   } else {
@@ -1698,7 +1904,34 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     vec_bytes(H);
     vec_bytes(H);
   }
-  for (int i = 0; i < (c.gpt || c.lfm ? 0 : c.layers); ++i) {
+  const int64_t ssm_proj = (int64_t)c.ssm_inner + c.ssm_conv + c.ssm_heads;  // granitehybrid in_proj rows
+  for (int i = 0; i < (c.granite ? c.layers : 0); ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    const LayerCfg& lc = c.layer[i];
+    auto lin = [&](const std::string& name, int64_t K, int64_t N) {
+      wbytes += stripes_bytes(granite_linear(g, p + name, K, N).type, N, K);
+    };
+    if (lc.mamba) {
+      lin("ssm_in.weight", H, ssm_proj);
+      lin("ssm_out.weight", c.ssm_inner, H);
+      vec_bytes(4 * (int64_t)c.ssm_conv);
+      vec_bytes(c.ssm_conv);
+      for (int v = 0; v < 3; ++v) vec_bytes(c.ssm_heads);
+      vec_bytes(c.ssm_inner);
+    } else {
+      lin("attn_q.weight", H, lc.heads * c.hd);
+      lin("attn_k.weight", H, lc.kv_heads * c.hd);
+      lin("attn_v.weight", H, lc.kv_heads * c.hd);
+      lin("attn_output.weight", lc.heads * c.hd, H);
+      vec_bytes(c.hd / 2);  // (zero) rotary table
+    }
+    lin("ffn_gate.weight", H, lc.ffn);
+    lin("ffn_up.weight", H, lc.ffn);
+    lin("ffn_down.weight", lc.ffn, H);
+    vec_bytes(H);
+    vec_bytes(H);
+  }
+  for (int i = 0; i < (c.gpt || c.lfm || c.granite ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     const LayerCfg& lc = c.layer[i];
     const int lq = lc.heads * c.hd, lkv = lc.kv_heads * c.hd;
@@ -1729,9 +1962,9 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
   // state arena: K/V cache + activations + bookkeeping
   // (lfm2: one argmax slot per residue class, TOPK256_WGSL)
-  e->groups = c.lfm ? 256 : (c.vocab + 255) / 256;
-  int kv_layers = 0, conv_layers = 0;  // layers holding a K/V cache / a convolution state
-  for (const LayerCfg& lc : c.layer) (lc.conv ? conv_layers : kv_layers) += 1;
+  e->groups = c.lfm || c.granite ? 256 : (c.vocab + 255) / 256;
+  int kv_layers = 0, conv_layers = 0, mamba_layers = 0;  // layers holding a K/V cache / a conv state / an SSM state
+  for (const LayerCfg& lc : c.layer) (lc.conv ? conv_layers : lc.mamba ? mamba_layers : kv_layers) += 1;
   // attention chunk: the smallest power of two >= 16 giving at most ~512
   // workgroups and at most 32 chunks over the whole context (the last chunk to
   // finish merges all chunks), capped by the kernel's limit for hd
@@ -1753,7 +1986,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     e->dnchunk = (c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk();
     for (const LayerCfg& lc : c.layer) {
       const int lg = lc.heads / lc.kv_heads;
-      if (lc.conv) continue;
+      if (lc.conv || lc.mamba) continue;
       if (e->dec_attn && (!attn_dec_supported(lg, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) ||
                           attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, e->dnchunk)) <
                               lc.kv_heads * e->dnchunk))
@@ -1764,6 +1997,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
   size_t sbytes = 2 * align256(kv_bytes) * kv_layers;
   sbytes += c.lfm ? align256((size_t)3 * H * 4) + 2 * align256((size_t)H * 4) * conv_layers : 0;
+  const size_t ssm_state_bytes = (size_t)c.ssm_heads * 32 * 128 * 4, mconv_bytes = (size_t)2 * c.ssm_conv * 3 * 4;
+  sbytes += c.granite ? align256((size_t)ssm_proj * 4) + align256((size_t)c.ssm_inner * 4) +
+                            (align256(ssm_state_bytes) + align256(mconv_bytes)) * mamba_layers
+                      : 0;
   sbytes += 3 * align256((size_t)H * 4) + align256((size_t)(qdim + 2 * kvdim) * 4) + align256((size_t)qdim * 4) +
             align256((size_t)c.ffn * 4) + align256((size_t)c.vocab * 4) +
             align256((size_t)e->groups * 8) + align256(sizeof(DevState)) + align256(sizeof(DevSampling)) +
@@ -1779,6 +2016,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     // LfmWgslEngine.create (:501-580): the embedding doubles as the lm_head
     e->lm_head = upload_class_major(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
     e->final_norm = lfm_floats(e->weights, *src, g, "token_embd_norm.weight", H);
+  } else if (c.granite) {
+    // GraniteWgslEngine.create (:544-555): the embedding doubles as the lm_head
+    e->lm_head = upload_class_major(e->weights, *src, g, tensor(g, "token_embd.weight"), H, c.vocab);
+    e->final_norm = granite_floats(e->weights, *src, g, "output_norm.weight", H);
   } else {
     e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
     e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
@@ -1799,6 +2040,44 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     } else {
       L.q_norm = lfm_floats(e->weights, *src, g, p + "attn_q_norm.weight", c.hd);
       L.k_norm = lfm_floats(e->weights, *src, g, p + "attn_k_norm.weight", c.hd);
+      L.q = lin("attn_q.weight", H, lc.heads * c.hd);
+      L.k = lin("attn_k.weight", H, lc.kv_heads * c.hd);
+      L.v = lin("attn_v.weight", H, lc.kv_heads * c.hd);
+      L.o = lin("attn_output.weight", lc.heads * c.hd, H);
+      L.kc = e->state.take(kv_bytes);
+      L.vc = e->state.take(kv_bytes);
+    }
+    L.gate = lin("ffn_gate.weight", H, lc.ffn);
+    L.up = lin("ffn_up.weight", H, lc.ffn);
+    L.down = lin("ffn_down.weight", lc.ffn, H);
+    if (L.gate.q.type != L.up.q.type)
+      throw Error(CHONK_EINVAL, "ffn_gate and ffn_up of layer " + std::to_string(i) + " have different types");
+    e->layers.push_back(L);
+  }
+  for (int i = 0; i < (c.granite ? c.layers : 0); ++i) {
+    // GraniteWgslEngine.create's loadLayer (:571-624)
+    const std::string p = "blk." + std::to_string(i) + ".";
+    const LayerCfg& lc = c.layer[i];
+    LayerDev L;
+    auto lin = [&](const std::string& name, int64_t K, int64_t N) {
+      return upload_matrix(e->weights, *src, g, granite_linear(g, p + name, K, N), K, N);
+    };
+    auto vec = [&](const std::string& name, int64_t n) { return granite_floats(e->weights, *src, g, p + name, n); };
+    L.in_norm = vec("attn_norm.weight", H);
+    L.post_norm = vec("ffn_norm.weight", H);
+    if (lc.mamba) {
+      L.ssm_in = lin("ssm_in.weight", H, ssm_proj);
+      L.ssm_out = lin("ssm_out.weight", c.ssm_inner, H);
+      const GgufTensorInfo& cw = granite_tensor(g, p + "ssm_conv1d.weight");
+      if (cw.shape.size() != 2 || cw.shape[0] != 4 || (int64_t)cw.shape[1] != c.ssm_conv)
+        throw Error(CHONK_EINVAL, "Granite WGSL tensor " + cw.name + " must be [4, " + std::to_string(c.ssm_conv) + "]");
+      L.c1d_w = vec("ssm_conv1d.weight", 4 * (int64_t)c.ssm_conv);
+      L.c1d_b = vec("ssm_conv1d.bias", c.ssm_conv);
+      L.dt_b = vec("ssm_dt.bias", c.ssm_heads);
+      L.a_neg = vec("ssm_a", c.ssm_heads);
+      L.d_w = vec("ssm_d", c.ssm_heads);
+      L.ssm_norm = vec("ssm_norm.weight", c.ssm_inner);
+    } else {
       L.q = lin("attn_q.weight", H, lc.heads * c.hd);
       L.k = lin("attn_k.weight", H, lc.kv_heads * c.hd);
       L.v = lin("attn_v.weight", H, lc.kv_heads * c.hd);
@@ -1837,7 +2116,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       e->layers.push_back(L);
     }
   }
-  for (int i = 0; i < (c.gpt || c.lfm ? 0 : c.layers); ++i) {
+  for (int i = 0; i < (c.gpt || c.lfm || c.granite ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     LayerDev L;
     L.in_norm = upload_floats(e->weights, *src, g, p + "attn_norm.weight", H);
@@ -1874,7 +2153,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     wpt += L.q.gguf_bytes + L.k.gguf_bytes + L.v.gguf_bytes + L.qkv.gguf_bytes + L.o.gguf_bytes + L.gate.gguf_bytes +
            L.up.gguf_bytes + L.down.gguf_bytes + (uint64_t)H * 4 * (c.gemma || c.gpt ? 4 : 2) +
            (c.qk_norm && !L.conv_w ? 2ull * c.hd * 4 : 0) + (c.gpt ? 4ull * (5 * (uint64_t)H + c.ffn) : 0) +
-           L.conv_in.gguf_bytes + L.conv_out.gguf_bytes + (L.conv_w ? 12ull * H : 0);
+           L.conv_in.gguf_bytes + L.conv_out.gguf_bytes + (L.conv_w ? 12ull * H : 0) + L.ssm_in.gguf_bytes +
+           L.ssm_out.gguf_bytes + (L.c1d_w ? 4ull * (5ull * c.ssm_conv + 3ull * c.ssm_heads + c.ssm_inner) : 0);
   if (c.gpt) wpt += 8ull * H;  // final LayerNorm bias, the position row
   e->weight_bytes_per_token = wpt;
 
@@ -1893,6 +2173,15 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
       if (!c.layer[i].conv) continue;
       e->layers[i].conv_s1 = (float*)e->state.take((size_t)H * 4);
       e->layers[i].conv_s2 = (float*)e->state.take((size_t)H * 4);
+    }
+  }
+  if (c.granite) {
+    e->mproj = (float*)e->state.take((size_t)ssm_proj * 4);
+    e->my = (float*)e->state.take((size_t)c.ssm_inner * 4);
+    for (size_t i = 0; i < e->layers.size(); ++i) {
+      if (!c.layer[i].mamba) continue;
+      e->layers[i].ssm_state = (float*)e->state.take(ssm_state_bytes);
+      e->layers[i].mconv_state = (float*)e->state.take(mconv_bytes);
     }
   }
   {
@@ -1936,7 +2225,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
   // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
-  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt && !c.lfm &&
+  e->batched_prefill = !(pv && std::strcmp(pv, "token") == 0) && !c.gpt && !c.lfm && !c.granite &&
                        std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) <= 4096;
   // the no-allocation prompt pass: as many rows (a multiple of 16, at most one
   // full pass) as fit the scratch with this model's row buffers
@@ -2002,7 +2291,7 @@ DevSampling make_sampling(chonk_engine* e, const chonk_sampling* s, bool stage1,
   d.sample_mode = (temperature > 0 || top_p < 1 || top_k > 0) ? 1 : 0;  // needsSamplingReadback
   // the LFM runtime also takes the candidate path for any penalty other than 1
   // (needsCandidateReadback, sampling.ts:18-21; lfm-wgsl-runtime.ts:787-806)
-  if (e->cfg.lfm && rp != 1.0) d.sample_mode = 1;
+  if ((e->cfg.lfm || e->cfg.granite) && rp != 1.0) d.sample_mode = 1;
   // the caller decides: llama applies the list when rp > 1 (:1649-1661), the
   // GPT-2 runtime whenever rp != 1 (gpt-wgsl-runtime.ts:789-798)
   d.stage1_penalty = stage1 ? 1 : 0;
@@ -2044,7 +2333,7 @@ void put_token(chonk_engine* e, int position, int32_t token) {
 // The context error in the wording of the engine's runtime
 // (llama-wgsl-runtime.ts:1032, gpt-wgsl-runtime.ts:751-753, lfm-wgsl-runtime.ts:732-734).
 Error context_exhausted(const chonk_engine* e) {
-  const char* name = e->cfg.gpt ? "GPT" : e->cfg.lfm ? "LFM" : "Llama";
+  const char* name = e->cfg.gpt ? "GPT" : e->cfg.lfm ? "LFM" : e->cfg.granite ? "Granite" : "Llama";
   return Error(CHONK_ECONTEXT, std::string(name) + " WGSL context exhausted at " + std::to_string(e->cfg.ctx) + " tokens");
 }
 
@@ -2064,6 +2353,10 @@ void engine_reset(chonk_engine* e) {
     if (L.conv_s1) {  // LfmWgslEngine.reset clears each convolution state (:711-724)
       HIP_OK(hipMemsetAsync(L.conv_s1, 0, (size_t)e->cfg.hidden * 4, e->stream));
       HIP_OK(hipMemsetAsync(L.conv_s2, 0, (size_t)e->cfg.hidden * 4, e->stream));
+    }
+    if (L.ssm_state) {  // GraniteWgslEngine.reset clears each conv and SSM state (:750-763)
+      HIP_OK(hipMemsetAsync(L.ssm_state, 0, (size_t)e->cfg.ssm_heads * 32 * 128 * 4, e->stream));
+      HIP_OK(hipMemsetAsync(L.mconv_state, 0, (size_t)2 * e->cfg.ssm_conv * 3 * 4, e->stream));
     }
   }
   DevState s{};
@@ -2450,7 +2743,7 @@ int32_t run_token(chonk_engine* e, int32_t token, bool need_logits, const chonk_
     const double rp = s ? s->repetition_penalty : 1.0;
     // (the GPT-2 runtime applies the list whenever the penalty is not 1, :785-796)
     // (the LFM runtime has no penalty list: its penalty acts on the candidates)
-    const bool stage1 = !e->cfg.lfm && (e->cfg.gpt ? rp != 1.0 : rp > 1) && n_pen > 0;
+    const bool stage1 = !e->cfg.lfm && !e->cfg.granite && (e->cfg.gpt ? rp != 1.0 : rp > 1) && n_pen > 0;
     const size_t keep = std::min(n_pen, (size_t)e->cfg.ctx);
     if (stage1) upload_bits(e, e->pen_bits, pen + (n_pen - keep), keep);
     const DevSampling d = make_sampling(e, s, stage1, n_seen > 0);
@@ -2494,7 +2787,9 @@ chonk_sampling effective_sampling(const chonk_engine* e, const chonk_sampling* s
   s.top_p = 1;
   s.top_k = 0;
   s.repetition_penalty =
-      (!e->cfg.gpt && !e->cfg.lfm && e->def.default_repetition_penalty > 0) ? e->def.default_repetition_penalty : 1.0;
+      (!e->cfg.gpt && !e->cfg.lfm && !e->cfg.granite && e->def.default_repetition_penalty > 0)
+          ? e->def.default_repetition_penalty
+          : 1.0;
   if (s_in) {
     s.temperature = s_in->temperature;
     s.top_p = s_in->top_p;
@@ -2526,7 +2821,7 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
   auto is_eos = [&](int32_t id) { return std::find(e->eos.begin(), e->eos.end(), id) != e->eos.end(); };
 
   // penalty list = prompt (+ generated ids, appended on the device)
-  const bool stage1 = !c.lfm && s.repetition_penalty > 1;
+  const bool stage1 = !c.lfm && !c.granite && s.repetition_penalty > 1;
   DevSampling d = make_sampling(e, &s, stage1, true);
   if (stage1 || d.seen_penalty) {
     upload_bits(e, e->pen_bits, prompt, n_prompt);
@@ -2598,8 +2893,9 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
       HIP_OK(hipMemcpy(generated.data(), e->gen, generated.size() * 4, hipMemcpyDeviceToHost));
     e->pos = st.pos;
     next = generated.empty() ? next : generated.back();
-    if (c.lfm && !generated.empty() && !is_eos(generated.back())) {
-      // generateLfmWgsl also runs the last generated id (lfm-wgsl-runtime.ts:288-300):
+    if ((c.lfm || c.granite) && !generated.empty() && !is_eos(generated.back())) {
+      // generateLfmWgsl / generateGraniteWgsl also run the last generated id
+      // (lfm-wgsl-runtime.ts:288-300, granite-wgsl-runtime.ts:270-284):
       // its pick is the cached next id; the device holds that id at hist[pos]
       st.generating = 0;
       st.stopped = 0;
@@ -2651,7 +2947,7 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
   }
   int32_t next = 0;
   const size_t n_suffix = n_prompt - (size_t)prefix;
-  const bool gpt = e->cfg.gpt, lfm = e->cfg.lfm;
+  const bool gpt = e->cfg.gpt, lfm = e->cfg.lfm || e->cfg.granite;  // (granitehybrid: the LFM loop, :223-292)
   if (n_suffix == 0 && gpt && !e->has_cached_next)
     throw Error(CHONK_EINVAL, "GPT WGSL has no cached next token for an empty prompt");
   if (n_suffix == 0 && e->has_cached_next) {
@@ -2788,7 +3084,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->head_dim = c.hd;
   out->context = c.ctx;
   out->architecture = c.arch == "llama" ? 0 : c.arch == "qwen3" ? 1 : c.arch == "gemma3" ? 2 : c.arch == "gpt2" ? 3
-                      : c.arch == "openelm" ? 4 : 5;
+                      : c.arch == "openelm" ? 4 : c.arch == "lfm2" ? 5 : 6;
   out->qk_norm = c.qk_norm;
   out->interleaved_rope = c.interleaved;
   out->kv_dtype = e->kv_elem == 2 ? CHONK_KV_F16 : CHONK_KV_F32;
@@ -2842,7 +3138,8 @@ int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t 
     if (e->noalloc_rows <= 0)
       throw Error(CHONK_EINVAL, std::string("chonk_engine_prefill_noalloc: this model has no row-batch prompt pass ") +
                                     "that fits the " + std::to_string(kNoAllocScratchBytes >> 20) +
-                                    " MiB scratch (gpt2, rows wider than 4096, or CHONK_PREFILL=token)");
+                                    " MiB scratch (gpt2, lfm2, granitehybrid, rows wider than 4096, or "
+                                    "CHONK_PREFILL=token)");
     if (n > (size_t)e->noalloc_rows)
       throw Error(CHONK_EINVAL, "chonk_engine_prefill_noalloc takes at most " + std::to_string(e->noalloc_rows) +
                                     " tokens per call for this model (its " +
@@ -2972,7 +3269,9 @@ int chonk_engine_read_kv(chonk_engine* e, int32_t layer, int32_t is_value, int32
     if (layer < 0 || layer >= c.layers || pos < 0 || pos >= c.ctx || !out) throw Error(CHONK_EINVAL, "bad layer/position");
     HIP_OK(hipStreamSynchronize(e->stream));
     const LayerDev& L = e->layers[layer];
-    if (!L.kc) throw Error(CHONK_EINVAL, "layer " + std::to_string(layer) + " is a convolution layer (no K/V cache)");
+    if (!L.kc)
+      throw Error(CHONK_EINVAL, "layer " + std::to_string(layer) + " is a " +
+                                    (e->cfg.granite ? "Mamba2" : "convolution") + " layer (no K/V cache)");
     const uint8_t* base = (const uint8_t*)(is_value ? L.vc : L.kc);
     std::vector<uint8_t> row((size_t)c.hd * e->kv_elem);
     for (int h = 0; h < c.kv_heads; ++h) {
@@ -3506,7 +3805,8 @@ void batch_create(chonk_engine* e, int max_seqs, int max_tokens, chonk_batch** o
   if (std::max(c.hidden, std::max(c.heads * c.hd, c.ffn)) > 4096)
     throw Error(CHONK_EINVAL, "batched decoding needs hidden, q and ffn widths of at most 4096");
   if (c.gpt) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not gpt2");
-  if (c.lfm) throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not lfm2");
+  if (c.lfm || c.granite)
+    throw Error(CHONK_EINVAL, "batched decoding covers the llama-family runtime, not lfm2 or granitehybrid");
   if (e->kv_elem != 2) throw Error(CHONK_EINVAL, "batched decoding needs the fp16 K/V cache");
   if (c.heads / c.kv_heads > 16) throw Error(CHONK_EINVAL, "batched decoding supports GQA groups up to 16");
   if (c.openelm) throw Error(CHONK_EINVAL, "batched decoding needs one head geometry for every layer (not openelm)");

@@ -23,6 +23,7 @@ enum ProMode : int32_t {
   PRO_NORM = 1,          // xs = rmsnorm(in) * w_norm
   PRO_EMBED_NORM = 2,    // r = embed(hist[pos]) * scale; WG0 writes r; xs = rmsnorm(r) * w_norm
   PRO_RES_NORM = 3,      // r = clamp(in + rmsnorm(delta) * w_delta, +-65000); WG0 writes r; xs = rmsnorm(r) * w_norm
+  PRO_GATE = 4,          // v = in * silu(gate_z); xs = rmsnorm(v) * w_norm (granitehybrid Mamba2 gated norm)
   PRO_LN = 5,            // xs = layernorm(in) * w_norm + norm_b (GPT-2)
   PRO_EMBED_LN = 6,      // r = embed(hist[pos]) + pos_embd[pos]; WG0 writes r; xs = layernorm(r) * w_norm + norm_b
   PRO_CONV = 7,          // xs = C * (s1 * w0 + s2 * w1 + (B * x) * w2), B | C | x = conv_proj (lfm2)
@@ -85,6 +86,28 @@ struct MvArgs {
   int32_t conv_commit;     // WG0 sets s1 = s2, s2 = B * x
   int32_t lfm_classes;     // EPI_LOGITS: rows stored class-major, workgroup c computes ids c, c + 256, ...
   int32_t pad_lfm;
+  const float* gate_z;     // PRO_GATE: the gate z (the first k rows of the Mamba2 in_proj output)
+  float add_scale;         // EPI_ADD: out = add + acc * add_scale when non-zero (granitehybrid's 0.246)
+  float logit_scale;       // EPI_LOGITS: logits = acc * logit_scale when non-zero (granitehybrid's 1/3)
+};
+
+// One Mamba2 step of a granitehybrid layer (granite-wgsl-runtime.ts:1476-1562):
+// the causal 4-tap convolution + silu of the xBC channels and the selective
+// scan of every (head, channel) over its 128 states. Workgroup (n, y) owns head
+// n's channels 8y .. 8y+7; every workgroup evaluates the convolution of the
+// shared B and C channels itself.
+struct SsmArgs {
+  const float* proj;       // [inner + conv + heads] in_proj output: z | xBC | dt
+  const float* conv_w;     // [conv][4] taps
+  const float* conv_b;     // [conv]
+  float* conv_state;       // [2][conv][3]: each channel's last three inputs, the buffer chosen by position parity
+  const float* dt_bias;    // [heads]
+  const float* a_neg;      // [heads] A = -exp(A_log)
+  const float* d;          // [heads]
+  float* ssm_state;        // [heads][32][128]
+  float* y;                // [inner] scan output
+  DevState* st;
+  int32_t inner, conv, heads;
 };
 
 struct AttnArgs {
@@ -348,6 +371,7 @@ size_t lds_limit();
 constexpr int kRowUnits = 4;
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s);
+hipError_t launch_ssm(const SsmArgs& a, hipStream_t s);
 // The register-resident decode attention (attn_decode.hip): fp16 cache,
 // head_dim 64/128/256, GQA group <= 8 (group x head_dim <= 1536), at most 128
 // chunks of attn_dec_chunk() positions over the context.

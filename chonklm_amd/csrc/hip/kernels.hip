@@ -291,29 +291,43 @@ __device__ __forceinline__ void matvec_body(const MvArgs& a) {
       for (int t = tid; t < nt; t += kWg) g.out[t0 + t] = __fmul_rn(gelu_tanh(res[2 * t]), res[2 * t + 1]);
       break;
     case EPI_LOGITS: {
-      // tile == 256: one ARGMAX_STAGE1 group per workgroup
+      // tile == 256 (class-major: up to 512): one ARGMAX_STAGE1 group per workgroup
       float* vals = res + 256;
       uint32_t* idx = (uint32_t*)(vals + 256);
       float v = kNegBig;
       uint32_t id = (a.gpt_argmax || a.lfm_classes) ? 0u : 0xffffffffu;
-      // lfm2: the rows are stored class-major, so workgroup c holds ids c,
-      // c + 256, ... in order and its candidate is TOPK256_WGSL's slot c
-      const int row = a.lfm_classes ? tid * 256 + ((int)blockIdx.x - g.wg_begin) : t0 + tid;
-      if (tid < nt && row < a.vocab) {
-        v = res[tid];
-        g.out[row] = v;
-        if (a.samp->stage1_penalty && bit_test(a.pen_bits, (uint32_t)row)) {
-          const float p = a.samp->stage1_pen;
-          v = v > 0.0f ? __fdiv_rn(v, p) : __fmul_rn(v, p);
-        }
-        id = (uint32_t)row;
-        // (the slot's scan starts from (-3.402823e38, 0) and only a strictly
-        // greater logit replaces it: NaN and values at or below it never do)
-        if (a.lfm_classes && !(v > kNegBig)) {
-          v = kNegBig;
-          id = 0u;
+      // lfm2 / granitehybrid: the rows are stored class-major, so workgroup c
+      // holds ids c, c + 256, ... in order and its candidate is TOPK256_WGSL's
+      // slot c; a class of more than 256 ids (granitehybrid's 100352-entry
+      // vocab) gives a thread two rows, tid and tid + 256, scanned in id order
+      const int cls = (int)blockIdx.x - g.wg_begin;
+      for (int part = 0; part < (a.lfm_classes ? 2 : 1); ++part) {
+        const int j = tid + 256 * part;
+        const int row = a.lfm_classes ? j * 256 + cls : t0 + j;
+        if (j < nt && row < a.vocab) {
+          float rv = res[j];
+          if (a.logit_scale != 0.f) rv = __fmul_rn(rv, a.logit_scale);  // SCALE_LOGITS_WGSL (granite :1740-1751)
+          g.out[row] = rv;
+          if (a.samp->stage1_penalty && bit_test(a.pen_bits, (uint32_t)row)) {
+            const float p = a.samp->stage1_pen;
+            rv = rv > 0.0f ? __fdiv_rn(rv, p) : __fmul_rn(rv, p);
+          }
+          if (part == 0) {
+            v = rv;
+            id = (uint32_t)row;
+            // (the slot's scan starts from (-3.402823e38, 0) and only a strictly
+            // greater logit replaces it: NaN and values at or below it never do)
+            if (a.lfm_classes && !(v > kNegBig)) {
+              v = kNegBig;
+              id = 0u;
+            }
+          } else if (rv > v) {
+            v = rv;
+            id = (uint32_t)row;
+          }
         }
       }
+      // (each thread read only res[tid] and res[tid + 256], the slots written here)
       vals[tid] = v;
       idx[tid] = id;
       __syncthreads();
@@ -406,7 +420,8 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   p.pro = PRO;
   // plain, norm and convolution prologues keep x (and the norm weight) in
   // registers: thread t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
-  constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM || PRO == PRO_CONV) && GB != 2;
+  constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM || PRO == PRO_CONV || PRO == PRO_GATE) && GB != 2;
+  constexpr bool norm_pro = PRO == PRO_NORM || PRO == PRO_GATE;
   const int n4 = a.k >> 2;
   float4 xv[4], wv[4];
 #pragma unroll
@@ -418,6 +433,12 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
       if (i4 < n4) {
         if constexpr (PRO == PRO_CONV) {
           xv[r] = conv_block4(a.conv_proj, a.conv_s1, a.conv_s2, a.conv_w, a.k, i4);
+        } else if constexpr (PRO == PRO_GATE) {
+          // MAMBA_GATE_NORM_WGSL's v = ssm_y * silu(z) (granite-wgsl-runtime.ts:1590-1606)
+          const float4 y4 = ldg4f(p.in + 4 * i4), z4 = ldg4f(a.gate_z + 4 * i4);
+          auto gz = [](float y, float z) { return __fmul_rn(y, __fdiv_rn(z, __fadd_rn(1.0f, expf(-z)))); };
+          xv[r] = make_float4(gz(y4.x, z4.x), gz(y4.y, z4.y), gz(y4.z, z4.z), gz(y4.w, z4.w));
+          wv[r] = ldg4f(p.w_norm + 4 * i4);
         } else {
           xv[r] = ldg4f(p.in + 4 * i4);
           if constexpr (PRO == PRO_NORM) wv[r] = ldg4f(p.w_norm + 4 * i4);
@@ -455,7 +476,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     CHONK_MV_T(tr, 1);
     if (stopped) return;
     if constexpr (reg_pro) {
-      if constexpr (PRO == PRO_NORM) {
+      if constexpr (norm_pro) {
         float ss = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -512,7 +533,8 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     }
     if constexpr (EPI == EPI_STORE) g.out[row] = rg;
     if constexpr (EPI == EPI_ADD) {
-      float y = __fadd_rn(addv, rg);
+      // (granitehybrid: ADD_SCALED_WGSL's residual + add * 0.246, granite-wgsl-runtime.ts:1458-1474)
+      float y = a.add_scale != 0.f ? __fadd_rn(addv, __fmul_rn(rg, a.add_scale)) : __fadd_rn(addv, rg);
       if (GB && a.sanitize) y = y != y ? 0.0f : fminf(fmaxf(y, -10000.0f), 10000.0f);  // SANITIZE (gpt-wgsl-runtime.ts:1726-1746)
       g.out[row] = y;
     }
@@ -533,6 +555,7 @@ CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, 0)
 CHONK_MVR(k_mvr_store_resnorm, EPI_STORE, PRO_RES_NORM, 0)
 CHONK_MVR(k_mvr_add_plain, EPI_ADD, PRO_PLAIN, 0)
 CHONK_MVR(k_mvr_add_conv, EPI_ADD, PRO_CONV, 0)
+CHONK_MVR(k_mvr_add_gate, EPI_ADD, PRO_GATE, 0)
 CHONK_MVR(k_mvr_swiglu_norm, EPI_GLU_SILU, PRO_NORM, 0)
 CHONK_MVR(k_mvr_swiglu_resnorm, EPI_GLU_SILU, PRO_RES_NORM, 0)
 CHONK_MVR(k_mvr_geglu_norm, EPI_GLU_GELU, PRO_NORM, 0)
@@ -657,6 +680,76 @@ __global__ __launch_bounds__(kWg) void k_attention(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Mamba2 step of a granitehybrid layer: MAMBA_CONV_WGSL + MAMBA_SSM_WGSL
+// (granite-wgsl-runtime.ts:1476-1562) in one launch. Workgroup (n, y) owns the
+// 8 channels 8y .. 8y+7 of SSM head n (32 lanes per channel, 4 of the 128
+// states per lane). The convolution window of each xBC channel is read from
+// the position's parity buffer and shifted into the other one (no reader of
+// the old window is ever raced): the workgroup owning an x channel writes its
+// window, workgroup (0, 0) those of the shared B and C channels.
+constexpr int kSsmHd = 32, kSsmState = 128, kSsmCh = 8;
+
+__global__ __launch_bounds__(kWg) void k_mamba_ssm(const SsmArgs a) {
+  __shared__ float sB[kSsmState], sC[kSsmState], sx[kSsmCh], sdt[2];
+  const int n = (int)blockIdx.x, c0 = (int)blockIdx.y * kSsmCh, tid = (int)threadIdx.x;
+  const int h = tid >> 5, l = tid & 31;
+  const int nh = n * kSsmHd + c0 + h;
+  // the state rows first: nothing else in this launch writes or depends on them
+  float* sp = a.ssm_state + (size_t)nh * kSsmState + l;
+  float sv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sv[j] = sp[32 * j];
+  const int stopped = __hip_atomic_load(&a.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (stopped) return;
+  const int par = a.st->pos & 1;
+  const float* cs_old = a.conv_state + (size_t)par * a.conv * 3;
+  float* cs_new = a.conv_state + (size_t)(par ^ 1) * a.conv * 3;
+  // channel c of xBC: ((((p1 w0 + p2 w1) + p3 w2) + x w3) + bias), then silu
+  auto conv_ch = [&](int c, bool write) {
+    const float nv = a.proj[a.inner + c];
+    const float p1 = cs_old[3 * c], p2 = cs_old[3 * c + 1], p3 = cs_old[3 * c + 2];
+    const float4 w = reinterpret_cast<const float4*>(a.conv_w)[c];
+    const float y = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(p1, w.x), __fmul_rn(p2, w.y)), __fmul_rn(p3, w.z)),
+                                        __fmul_rn(nv, w.w)),
+                              a.conv_b[c]);
+    if (write) {
+      cs_new[3 * c] = p2;
+      cs_new[3 * c + 1] = p3;
+      cs_new[3 * c + 2] = nv;
+    }
+    return __fdiv_rn(y, __fadd_rn(1.0f, expf(-y)));
+  };
+  if (tid < 2 * kSsmState) {
+    const float v = conv_ch(a.inner + tid, n == 0 && c0 == 0);
+    if (tid < kSsmState)
+      sB[tid] = v;
+    else
+      sC[tid - kSsmState] = v;
+  }
+  // (kWg == 2 * kSsmState: a second pass covers the x channels and dt)
+  if (tid < kSsmCh) sx[tid] = conv_ch(n * kSsmHd + c0 + tid, true);
+  if (tid == kSsmCh) {
+    // softplus as MAMBA_SSM_WGSL selects it, then the decay
+    const float x = __fadd_rn(a.proj[a.inner + a.conv + n], a.dt_bias[n]);
+    const float dt = x > 20.0f ? __fadd_rn(x, logf(__fadd_rn(1.0f, expf(-x)))) : logf(__fadd_rn(1.0f, expf(x)));
+    sdt[0] = dt;
+    sdt[1] = expf(__fmul_rn(dt, a.a_neg[n]));
+  }
+  __syncthreads();
+  const float dt = sdt[0], decay = sdt[1], hs = sx[h];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s = l + 32 * j;
+    const float next = __fadd_rn(__fmul_rn(sv[j], decay), __fmul_rn(__fmul_rn(dt, sB[s]), hs));
+    sp[32 * j] = next;
+    acc += next * sC[s];
+  }
+  acc = group_sum<32>(acc);
+  if (l == 0) a.y[nh] = __fadd_rn(acc, __fmul_rn(a.d[n], hs));
+}
+
 __global__ __launch_bounds__(kWg) void k_select(const SelArgs a) {
   __shared__ __align__(16) uint8_t ws[kSelectWorkspaceBytes];
   if (a.st->stopped) return;
@@ -749,8 +842,8 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[42] = {
-      (const void*)k_mvr_add_conv,
+  const void* fns[43] = {
+      (const void*)k_mvr_add_conv,           (const void*)k_mvr_add_gate,
       (const void*)k_mvr_add_bias,           (const void*)k_mvr_add_bias_wide,
       (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
       (const void*)k_mv_logits_t<QT_Q4_K>,   (const void*)k_mv_logits_t<QT_Q5_K>,   (const void*)k_mv_logits_t<QT_Q6_K>,
@@ -797,6 +890,10 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
         if (gb || a.k > 4 * 4 * kWg) return hipErrorInvalidValue;
         k = k_mvr_add_conv;
         break;
+      case EPI_ADD * 8 + PRO_GATE:
+        if (gb || a.k > 4 * 4 * kWg) return hipErrorInvalidValue;
+        k = k_mvr_add_gate;
+        break;
       case EPI_GLU_SILU * 8 + PRO_NORM: k = k_mvr_swiglu_norm; break;
       case EPI_GLU_SILU * 8 + PRO_RES_NORM: k = k_mvr_swiglu_resnorm; break;
       case EPI_GLU_GELU * 8 + PRO_NORM: k = k_mvr_geglu_norm; break;
@@ -828,6 +925,15 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
       break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_ssm(const SsmArgs& a, hipStream_t s) {
+  // the kernel's fixed geometry: 32-wide heads of 128 states, one x channel
+  // per lane group of 32, B | C over the 256 threads
+  if (a.inner != a.heads * kSsmHd || a.conv != a.inner + 2 * kSsmState || kWg != 2 * kSsmState)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mamba_ssm, dim3(a.heads, kSsmHd / kSsmCh), dim3(kWg), 0, s, a);
   return hipGetLastError();
 }
 

@@ -19,7 +19,13 @@
 //   lfm2.attention.head_count_kv, one entry per layer, 0 on convolution layers.
 // Type recipe (Q4_K_M): llama.cpp's llama_tensor_get_type as restated in the
 // header of synth.h. Architecture gpt2 follows the GPT runtime's manifest
-// (src/lib/gpt-wgsl-runtime.ts:274-356; gpt2_plan below).
+// (src/lib/gpt-wgsl-runtime.ts:274-356; gpt2_plan below). Architecture
+// granitehybrid follows the Granite runtime's loader
+// (src/lib/granite-wgsl-runtime.ts:536-624; granite_plan below): Mamba2 layers
+// (layer_kv_heads 0) hold blk.N.ssm_{in, out}.weight, ssm_conv1d.{weight, bias},
+// ssm_dt.bias, ssm_a, ssm_d and ssm_norm.weight with the runtime's fixed ratios
+// (inner size 2 * hidden, 32-wide heads, 128 states, 4 taps, one group).
+
 #include "synth.h"
 
 #include <algorithm>
@@ -62,6 +68,10 @@ inline float normal_at(uint64_t stream, uint64_t i) {
 // Standard deviation of the synthetic short-convolution taps: large enough that
 // the convolution branch moves the residual stream.
 constexpr float kLfmConvStd = 0.5f;
+// granitehybrid: the Granite runtime's fixed Mamba2 geometry (granite-wgsl-runtime.ts:526-533,
+// :586-596) and the spread of the synthetic depthwise conv taps
+constexpr uint64_t kGraniteHeadDim = 32, kGraniteState = 128;
+constexpr float kGraniteConvStd = 0.25f;
 
 bool use_more_bits(int i, int n) { return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2; }
 
@@ -140,13 +150,62 @@ std::vector<TensorPlan> gpt2_plan(const SynthConfig& c) {
   return plan;
 }
 
+// The tensor plan of a Granite-4.0-H hybrid decoder (granite-wgsl-runtime.ts:
+// 536-624): per layer attn_norm, ffn_norm, the SwiGLU matrices, and either a
+// Mamba2 block or NoPE attention; token_embd doubles as the output projection.
+// ssm_a holds -exp(A_log) (negative), ssm_dt.bias sits near softplus^-1 of a
+// small step, ssm_d near 1.
+std::vector<TensorPlan> granite_plan(const SynthConfig& c, const std::vector<int>& lkv, int head_dim) {
+  const uint64_t H = (uint64_t)c.hidden, F = (uint64_t)c.ffn;
+  const uint64_t inner = 2 * H, conv = inner + 2 * kGraniteState, nh = inner / kGraniteHeadDim;
+  std::vector<TensorPlan> plan;
+  plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H, recipe_tensor_type(c.recipe, "output", -1, c.layers, H),
+                  0.f, c.weight_std});
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    auto lin = [&](const std::string& role, uint64_t n, uint64_t k) {
+      plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f,
+                      c.weight_std});
+    };
+    auto vec = [&](const std::string& name, uint64_t n, float mean, float std) {
+      plan.push_back({p + name, 1, n, GGML_F32, mean, std});
+    };
+    vec("attn_norm.weight", H, 1.f, c.norm_std);
+    if (lkv[(size_t)i] == 0) {
+      lin("ssm_in", inner + conv + nh, H);
+      plan.push_back({p + "ssm_conv1d.weight", conv, 4, GGML_F32, 0.f, kGraniteConvStd});
+      vec("ssm_conv1d.bias", conv, 0.f, c.weight_std);
+      vec("ssm_dt.bias", nh, -4.f, 0.5f);
+      vec("ssm_a", nh, -4.f, 0.5f);
+      vec("ssm_d", nh, 1.f, 0.1f);
+      vec("ssm_norm.weight", inner, 1.f, c.norm_std);
+      lin("ssm_out", H, inner);
+    } else {
+      const uint64_t qdim = (uint64_t)c.heads * head_dim, kvdim = (uint64_t)lkv[(size_t)i] * head_dim;
+      lin("attn_q", qdim, H);
+      lin("attn_k", kvdim, H);
+      lin("attn_v", kvdim, H);
+      lin("attn_output", H, qdim);
+    }
+    vec("ffn_norm.weight", H, 1.f, c.norm_std);
+    lin("ffn_gate", F, H);
+    lin("ffn_up", F, H);
+    lin("ffn_down", H, F);
+  }
+  plan.push_back({"output_norm.weight", 1, H, GGML_F32, 1.f, c.norm_std});
+  return plan;
+}
+
 void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_threads) {
   const std::string& a = c.arch;
-  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2" && a != "openelm" && a != "lfm2")
+  if (a != "llama" && a != "qwen3" && a != "gemma3" && a != "gpt2" && a != "openelm" && a != "lfm2" &&
+      a != "granitehybrid")
     throw std::runtime_error("synthetic writer: unsupported arch " + a);
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0)
     throw std::runtime_error("synthetic writer: non-positive dimension");
-  const bool openelm = a == "openelm", lfm = a == "lfm2";
+  const bool granite = a == "granitehybrid";
+  // (a 0 kv-head entry marks an lfm2 convolution layer or a granitehybrid Mamba2 layer)
+  const bool openelm = a == "openelm", lfm = a == "lfm2" || granite;
   auto per_layer = [&](const std::vector<int>& v, int fallback, const char* what, bool zero_ok) {
     if (v.empty()) return std::vector<int>((size_t)c.layers, fallback);
     if (!openelm && !(lfm && zero_ok))
@@ -173,10 +232,16 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
 
   std::vector<TensorPlan> plan;
   if (a == "gpt2") plan = gpt2_plan(c);
+  if (granite) {
+    if (c.recipe != "q4_k_m" && c.recipe != "q8_0")
+      throw std::runtime_error("synthetic writer: granitehybrid files are Q4_K_M or Q8_0");
+    if (c.hidden % 16 != 0) throw std::runtime_error("synthetic writer: granitehybrid hidden must be a multiple of 16");
+    plan = granite_plan(c, lkv, head_dim);
+  }
   // tied embeddings: token_embd doubles as the output projection ("output" role)
-  if (a != "gpt2") plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H,
+  if (a != "gpt2" && !granite) plan.push_back({"token_embd.weight", (uint64_t)c.vocab, H,
                   recipe_tensor_type(c.recipe, "output", -1, c.layers, H), 0.f, w_std});
-  for (int i = 0; i < (a == "gpt2" ? 0 : c.layers); ++i) {
+  for (int i = 0; i < (a == "gpt2" || granite ? 0 : c.layers); ++i) {
     const std::string p = "blk." + std::to_string(i) + ".";
     auto lin = [&](const std::string& role, uint64_t n, uint64_t k) {
       plan.push_back({p + role + ".weight", n, k, recipe_tensor_type(c.recipe, role, i, c.layers, k), 0.f, w_std});
@@ -215,7 +280,8 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     lin("ffn_down", H, F);
     if (gemma) norm("post_ffw_norm", H);
   }
-  if (a != "gpt2") plan.push_back({lfm ? "token_embd_norm.weight" : "output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
+  if (a != "gpt2" && !granite)
+    plan.push_back({lfm ? "token_embd_norm.weight" : "output_norm.weight", 1, H, GGML_F32, 1.f, n_std});
 
   GgufWriter w;
   w.set_string("general.architecture", a);
@@ -228,7 +294,22 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     w.set_u32(a + ".feed_forward_length", (uint32_t)c.ffn);
     w.set_u32(a + ".attention.head_count", (uint32_t)c.heads);
     w.set_u32_array(a + ".attention.head_count_kv", std::vector<uint32_t>(lkv.begin(), lkv.end()));
-    w.set_u32(a + ".shortconv.l_cache", 3u);
+    if (granite) {
+      // llama.cpp's granitehybrid keys (the Granite runtime itself reads only
+      // general.architecture and general.file_type, :359-371)
+      w.set_u32(a + ".ssm.conv_kernel", 4u);
+      w.set_u32(a + ".ssm.state_size", (uint32_t)kGraniteState);
+      w.set_u32(a + ".ssm.group_count", 1u);
+      w.set_u32(a + ".ssm.inner_size", (uint32_t)(2 * H));
+      w.set_u32(a + ".ssm.time_step_rank", (uint32_t)(2 * H / kGraniteHeadDim));
+      w.set_f32(a + ".embedding_scale", 12.f);
+      w.set_f32(a + ".residual_scale", 0.246f);
+      w.set_f32(a + ".logit_scale", 3.f);
+      w.set_f32(a + ".attention.scale", 0.015625f);
+      w.set_f32(a + ".attention.layer_norm_rms_epsilon", c.norm_eps);
+    } else {
+      w.set_u32(a + ".shortconv.l_cache", 3u);
+    }
   } else if (openelm) {
     auto u32s = [](const std::vector<int>& v) { return std::vector<uint32_t>(v.begin(), v.end()); };
     w.set_u32_array(a + ".feed_forward_length", u32s(lff));
@@ -244,7 +325,7 @@ void write_synthetic_gguf(const SynthConfig& c, const std::string& path, int n_t
     w.set_u32(a + ".attention.key_length", (uint32_t)head_dim);
     w.set_u32(a + ".attention.value_length", (uint32_t)head_dim);
   }
-  if (a != "gpt2") {
+  if (a != "gpt2" && !granite) {
     w.set_u32(a + ".rope.dimension_count", (uint32_t)head_dim);
     w.set_f32(a + ".rope.freq_base", c.rope_theta);
     w.set_f32(a + ".attention.layer_norm_rms_epsilon", c.norm_eps);

@@ -4,7 +4,8 @@
 
 export interface ModelDef {
   id: string;
-  runtime: string; // "llama-webgpu" (llama / qwen3 / gemma3 / openelm files), "gpt-webgpu" (gpt2), "lfm2-webgpu" (lfm2)
+  runtime: string; // "llama-webgpu" (llama / qwen3 / gemma3 / openelm files), "gpt-webgpu" (gpt2), "lfm2-webgpu" (lfm2),
+  // "granite-webgpu" (granitehybrid)
   eosIds: number[];
   vocab: number;
   layers: number;
@@ -120,6 +121,27 @@ export declare function generateLfmWgsl(
 
 export declare function disposeLfmWgsl(loaded: LoadedLfmWgslModel): void;
 export declare function resetLfmWgslConversation(loaded: LoadedLfmWgslModel): void;
+
+/** LoadedGraniteWgslModel (src/lib/granite-wgsl-runtime.ts:158-166). */
+export interface LoadedGraniteWgslModel extends Omit<LoadedLlamaWgslModel, "runtime"> {
+  runtime: "granite-webgpu";
+}
+
+export declare function loadGraniteWgslModel(
+  model: ModelDef,
+  onProgress?: ProgressCallback,
+  onStep?: LoadStepCallback,
+  options?: { tokenizer?: Tokenizer; device?: number },
+): Promise<LoadedGraniteWgslModel>;
+
+export declare function generateGraniteWgsl(
+  loaded: LoadedGraniteWgslModel,
+  promptIds: number[],
+  opts?: GenerateOptions,
+): Promise<{ text: string; ids: number[]; tokensPerSec: number }>;
+
+export declare function disposeGraniteWgsl(loaded: LoadedGraniteWgslModel): void;
+export declare function resetGraniteWgslConversation(loaded: LoadedGraniteWgslModel): void;
 
 export {
   loadLlamaWgslModel as loadPleiasWgslModel,

@@ -89,8 +89,9 @@ async function loadLlamaWgslModel(model, onProgress, onStep, options) {
   }
   if (!model.gguf) throw new Error(`Llama WGSL ${model.id} is missing gguf path`);
   const engine = await openEngine(model, onProgress, onStep, options);
-  if (engine.info.architecture === ARCH_GPT2 || engine.info.architecture === ARCH_LFM2) {
-    const arch = engine.info.architecture === ARCH_GPT2 ? 'gpt2' : 'lfm2';
+  if (engine.info.architecture === ARCH_GPT2 || engine.info.architecture === ARCH_LFM2 ||
+      engine.info.architecture === ARCH_GRANITE) {
+    const arch = ARCH_NAMES[engine.info.architecture];
     engine.dispose();
     throw new Error(`Llama GGUF WGSL does not support architecture ${arch}`);
   }
@@ -129,10 +130,27 @@ async function loadLfmWgslModel(model, onProgress, onStep, options) {
   return loadedRecord('lfm2-webgpu', model, engine, options);
 }
 
+// loadGraniteWgslModel (src/lib/granite-wgsl-runtime.ts:168-221). The engine runs the
+// granitehybrid architecture of the GGUF file (Mamba2 layers beside NoPE GQA attention
+// layers, the scaled residuals and logits, TOPK256 candidates and the Granite generate loop).
+async function loadGraniteWgslModel(model, onProgress, onStep, options) {
+  if (model.runtime !== 'granite-webgpu') throw new Error(`loadGraniteWgslModel: unsupported model ${model.id}`);
+  if (!model.gguf) throw new Error(`Granite WGSL model ${model.id} missing 'gguf' URL`);
+  const engine = await openEngine(model, onProgress, onStep, options);
+  if (engine.info.architecture !== ARCH_GRANITE) {
+    const arch = ARCH_NAMES[engine.info.architecture];
+    engine.dispose();
+    throw new Error(`Granite WGSL ${model.id}: expected GGUF architecture granitehybrid, got ${arch}`);
+  }
+  if (onStep) onStep({ step: 'ready', detail: 'Granite HIP runtime ready' });
+  return loadedRecord('granite-webgpu', model, engine, options);
+}
+
 // chonk_engine_info.architecture
 const ARCH_GPT2 = 3;
 const ARCH_LFM2 = 5;
-const ARCH_NAMES = ['llama', 'qwen3', 'gemma3', 'gpt2', 'openelm', 'lfm2'];
+const ARCH_GRANITE = 6;
+const ARCH_NAMES = ['llama', 'qwen3', 'gemma3', 'gpt2', 'openelm', 'lfm2', 'granitehybrid'];
 
 function loadedRecord(runtime, model, engine, options) {
   return {
@@ -237,6 +255,12 @@ module.exports = {
   generateLfmWgsl,
   disposeLfmWgsl: disposeLlamaWgsl,
   resetLfmWgslConversation: resetLlamaWgslConversation,
+  // Granite runtime (src/lib/granite-wgsl-runtime.ts:168-302): generateGraniteWgsl takes
+  // opts.repetitionPenalty ?? 1 (:236-241) and runs one more step after the last id, as the LFM loop
+  loadGraniteWgslModel,
+  generateGraniteWgsl: generateLfmWgsl,
+  disposeGraniteWgsl: disposeLlamaWgsl,
+  resetGraniteWgslConversation: resetLlamaWgslConversation,
   // PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
   loadPleiasWgslModel: loadLlamaWgslModel,
   generatePleiasWgsl: generateLlamaWgsl,

@@ -74,7 +74,8 @@ class Workload:
         return np.random.default_rng(seed).integers(0, self.spec.vocab, self.prompt_tokens if n is None else n).tolist()
 
     def model_def(self, path: str, kv_dtype: str = "f16", device: int = 0) -> ModelDef:
-        runtime = {"gpt2": "gpt-webgpu", "lfm2": "lfm2-webgpu"}.get(self.spec.arch, "llama-webgpu")
+        runtime = {"gpt2": "gpt-webgpu", "lfm2": "lfm2-webgpu", "granitehybrid": "granite-webgpu"}.get(
+            self.spec.arch, "llama-webgpu")
         return ModelDef(id=self.name, vocab=self.spec.vocab, layers=self.spec.layers, max_context=self.max_context,
                         eos_ids=list(self.eos_ids), path=path, kv_dtype=kv_dtype, device=device, runtime=runtime)
 
@@ -104,6 +105,17 @@ LFM2_TYPES = ["conv", "conv", "attention", "conv", "conv", "attention", "conv", 
 LFM2_350M = dict(arch="lfm2", hidden=1024, layers=16, heads=16, kv_heads=8, head_dim=64, ffn=4608, vocab=65536,
                  context_length=128000, rope_theta=1000000.0, norm_eps=1e-5,
                  layer_kv_heads=[8 if t == "attention" else 0 for t in LFM2_TYPES])
+
+# Granite-4.0-H-350M-shaped (registry.ts:48-53, :271-319; the runtime's fixed
+# shape, granite-wgsl-runtime.ts:335-345, :526-533): Mamba2 and NoPE attention
+# layers in the registry's order (0 kv heads marks a Mamba2 layer, as
+# granitehybrid.attention.head_count_kv does), 12 q / 4 kv heads of 64, SSM
+# inner size 1536 (48 heads of 32, 128 states)
+GRANITE_TYPES = (["mamba"] * 10 + ["attention"] + ["mamba"] * 2 + ["attention"] + ["mamba"] * 3 + ["attention"] +
+                 ["mamba"] * 9 + ["attention"] + ["mamba"] * 4)
+GRANITE_350M = dict(arch="granitehybrid", hidden=768, layers=32, heads=12, kv_heads=4, head_dim=64, ffn=2048,
+                    vocab=100352, context_length=32768, norm_eps=1e-5,
+                    layer_kv_heads=[4 if t == "attention" else 0 for t in GRANITE_TYPES])
 
 WORKLOADS: dict[str, Workload] = {
     w.name: w
@@ -136,6 +148,14 @@ WORKLOADS: dict[str, Workload] = {
         Workload("lfm2.5-350m-q8_0", SynthSpec(recipe="q8_0", seed=41, **LFM2_350M), max_context=4096,
                  eos_ids=[7, 2], prompt_tokens=32, decode_tokens=128,
                  description="LFM2.5-350M-shaped hybrid decoder (lfm2 runtime), Q8_0, 32-token prompt, greedy 128"),
+        Workload("granite-4.0-h-350m-q4_k_m", SynthSpec(recipe="q4_k_m", seed=53, **GRANITE_350M), max_context=4096,
+                 eos_ids=[100257, 100265], prompt_tokens=32, decode_tokens=128,
+                 description="Granite-4.0-H-350M-shaped hybrid decoder (28 Mamba2 and 4 attention layers, "
+                             "granite runtime), Q4_K_M, 32-token prompt, greedy 128"),
+        Workload("granite-4.0-h-350m-q8_0", SynthSpec(recipe="q8_0", seed=53, **GRANITE_350M), max_context=4096,
+                 eos_ids=[100257, 100265], prompt_tokens=32, decode_tokens=128,
+                 description="Granite-4.0-H-350M-shaped hybrid decoder (granite runtime), Q8_0, 32-token prompt, "
+                             "greedy 128"),
         # small decoders for oracle parity (each exercises a different type mix)
         Workload("tiny-qwen3", SynthSpec(arch="qwen3", recipe="q4_k_m", hidden=256, layers=3, heads=4, kv_heads=2,
                                          head_dim=64, ffn=512, vocab=1200, context_length=4096,
@@ -169,6 +189,14 @@ WORKLOADS: dict[str, Workload] = {
         Workload("tiny-lfm2-q8", SynthSpec(arch="lfm2", recipe="q8_0", hidden=192, layers=3, heads=6, kv_heads=2,
                                            head_dim=32, ffn=384, vocab=700, context_length=4096,
                                            rope_theta=1000000.0, norm_eps=1e-5, seed=47, layer_kv_heads=[0, 0, 2]),
+                 max_context=160, eos_ids=[7, 2], prompt_tokens=16, decode_tokens=24),
+        Workload("tiny-granite", SynthSpec(arch="granitehybrid", recipe="q4_k_m", hidden=256, layers=4, heads=4,
+                                           kv_heads=2, head_dim=64, ffn=512, vocab=1024, context_length=4096,
+                                           norm_eps=1e-5, seed=59, layer_kv_heads=[0, 2, 0, 0]),
+                 max_context=160, eos_ids=[7, 2], prompt_tokens=24, decode_tokens=32),
+        Workload("tiny-granite-q8", SynthSpec(arch="granitehybrid", recipe="q8_0", hidden=192, layers=3, heads=3,
+                                              kv_heads=1, head_dim=64, ffn=384, vocab=700, context_length=4096,
+                                              norm_eps=1e-5, seed=61, layer_kv_heads=[0, 1, 0]),
                  max_context=160, eos_ids=[7, 2], prompt_tokens=16, decode_tokens=24),
         Workload("tiny-gemma3", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=320, layers=7, heads=4,
                                           kv_heads=1, head_dim=128, ffn=512, vocab=1500, context_length=4096,

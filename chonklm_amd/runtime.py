@@ -140,7 +140,8 @@ class LlamaWgslEngine:
 
     def read_buffer(self, which: int) -> np.ndarray:
         i = self.info
-        slots = 256 if i["architecture"] == 5 else (i["vocab"] + 255) // 256  # lfm2: one per residue class
+        # lfm2 / granitehybrid: one slot per residue class
+        slots = 256 if i["architecture"] in (5, 6) else (i["vocab"] + 255) // 256
         sizes = {0: i["hidden"] * 4, 1: i["heads"] * i["head_dim"] * 4, 2: slots * 8,
                  3: (i["heads"] + 2 * i["kv_heads"]) * i["head_dim"] * 4}
         buf = np.empty(sizes[which], dtype=np.uint8)
@@ -218,7 +219,7 @@ def load_llama_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = Non
     if on_step:
         on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
     engine = LlamaWgslEngine(model)
-    arch = {3: "gpt2", 5: "lfm2"}.get(engine.info["architecture"])
+    arch = {3: "gpt2", 5: "lfm2", 6: "granitehybrid"}.get(engine.info["architecture"])
     if arch:
         engine.dispose()
         raise ValueError(f"Llama GGUF WGSL does not support architecture {arch}")
@@ -436,6 +437,48 @@ def dispose_lfm_wgsl(loaded: LoadedLfmWgslModel) -> None:
     dispose_llama_wgsl(loaded)
 
 
+@dataclass
+class LoadedGraniteWgslModel(LoadedLlamaWgslModel):
+    """LoadedGraniteWgslModel (granite-wgsl-runtime.ts:158-166)."""
+
+    runtime: str = "granite-webgpu"
+
+
+def load_granite_wgsl_model(model: ModelDef, on_progress: Optional[Callable] = None,
+                            on_step: Optional[Callable] = None, tokenizer: object = None) -> LoadedGraniteWgslModel:
+    """loadGraniteWgslModel (:168-221): rejects a definition not tagged for the Granite runtime
+    and a GGUF file whose architecture is not granitehybrid (validateGraniteGguf, :359-371)."""
+    if model.runtime != "granite-webgpu":
+        raise ValueError(f"loadGraniteWgslModel: unsupported model {model.id}")
+    if on_step:
+        on_step({"step": "weights", "detail": "uploading GGUF tensors to the GPU"})
+    engine = LlamaWgslEngine(model)
+    if engine.info["architecture"] != 6:
+        arch = {0: "llama", 1: "qwen3", 2: "gemma3", 3: "gpt2", 4: "openelm", 5: "lfm2"}.get(engine.info["architecture"])
+        engine.dispose()
+        raise ValueError(f"Granite WGSL {model.id}: expected GGUF architecture granitehybrid, got {arch}")
+    if on_step:
+        on_step({"step": "ready", "detail": "Granite HIP runtime ready"})
+    return LoadedGraniteWgslModel(def_=model, engine=engine, tokenizer=tokenizer)
+
+
+def generate_granite_wgsl(loaded: LoadedGraniteWgslModel, prompt_ids: Sequence[int],
+                          max_new_tokens: Optional[int] = None, **kw) -> dict:
+    """generateGraniteWgsl (:223-292): the engine follows the Granite loop (one more step runs
+    after the last generated token; repetitionPenalty defaults to 1, not to the definition's)."""
+    return generate_llama_wgsl(loaded, prompt_ids, max_new_tokens, **kw)
+
+
+def reset_granite_wgsl_conversation(loaded: LoadedGraniteWgslModel) -> None:
+    """resetGraniteWgslConversation (:298-302)."""
+    reset_llama_wgsl_conversation(loaded)
+
+
+def dispose_granite_wgsl(loaded: LoadedGraniteWgslModel) -> None:
+    """disposeGraniteWgsl (:294-296)."""
+    dispose_llama_wgsl(loaded)
+
+
 # PleIAs aliases (src/lib/pleias-wgsl-runtime.ts:1-6)
 load_pleias_wgsl_model = load_llama_wgsl_model
 generate_pleias_wgsl = generate_llama_wgsl
@@ -474,5 +517,6 @@ __all__ = [
     "ChonkError", "LlamaWgslEngine", "LoadedLlamaWgslModel", "ModelDef", "load_llama_wgsl_model",
     "generate_llama_wgsl", "dispose_llama_wgsl", "LlamaWgslBatch", "reset_llama_wgsl_conversation", "write_synthetic_gguf",
     "shard_gguf", "LoadedLfmWgslModel", "load_lfm_wgsl_model", "generate_lfm_wgsl", "reset_lfm_wgsl_conversation",
-    "dispose_lfm_wgsl",
+    "dispose_lfm_wgsl", "LoadedGraniteWgslModel", "load_granite_wgsl_model", "generate_granite_wgsl",
+    "reset_granite_wgsl_conversation", "dispose_granite_wgsl",
 ]

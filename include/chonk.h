@@ -83,7 +83,7 @@ typedef struct {
 
 typedef struct {
   int32_t hidden, ffn, vocab, layers, heads, kv_heads, head_dim, context;
-  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3, 3 gpt2, 4 openelm, 5 lfm2 */
+  int32_t architecture;      /* 0 llama, 1 qwen3, 2 gemma3, 3 gpt2, 4 openelm, 5 lfm2, 6 granitehybrid */
   int32_t qk_norm, interleaved_rope, kv_dtype;
   uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
   uint64_t device_bytes;            /* device memory held by the engine */

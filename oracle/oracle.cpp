@@ -512,6 +512,13 @@ struct Layer {
   bool conv = false;
   Matrix conv_in, conv_out;
   std::vector<float> conv_w, conv_state;
+  // Granite-4.0-H Mamba2 layer (granite-wgsl-runtime.ts:64-76): in_proj rows
+  // z | xBC | dt, out_proj, the [conv][4] depthwise taps and bias, per-head dt
+  // bias, A (= -exp(A_log)) and D, the gated norm weight, and the state:
+  // [conv][4] conv window, [heads][head_dim][state] SSM state
+  bool mamba = false;
+  Matrix ssm_in, ssm_out;
+  std::vector<float> c1d_w, c1d_b, dt_b, a_neg, d_w, ssm_norm, mconv_state, ssm_state;
 };
 
 }  // namespace
@@ -524,6 +531,9 @@ struct orc_model {
   bool gpt = false;                         // GGUF architecture gpt2 (gpt-wgsl-runtime.ts)
   bool openelm = false;                     // fused attn_qkv, per-layer heads / kv heads / ffn
   bool lfm = false;                         // GGUF architecture lfm2 (lfm-wgsl-runtime.ts)
+  bool granite = false;                     // GGUF architecture granitehybrid (granite-wgsl-runtime.ts)
+  // granitehybrid: Mamba2 geometry (inner = heads * head_dim, conv = inner + 2 * state)
+  int ssm_inner = 0, ssm_conv = 0, ssm_heads = 0, ssm_hdim = 0, ssm_state = 0;
   std::vector<float> pos_embd, final_norm_b;  // GPT-2: [context][hidden] position table, final LayerNorm bias
   int hidden = 0, ffn = 0, vocab = 0, n_layers = 0, heads = 0, kv_heads = 0, hd = 0, ctx = 0;
   float norm_eps = 1e-5f, qk_eps = 1e-5f, attn_scale = 0, embed_scale = 1;
@@ -533,6 +543,7 @@ struct orc_model {
   int pos = 0;
   // scratch of the last step
   std::vector<float> hA, hB, hC, norm, q, k, v, qn, attn, gate, up, ff, logits, scores, qkv, proj, conv_mid;
+  std::vector<float> mproj, mconv, my, mnormed;  // granitehybrid Mamba2 scratch
   std::vector<uint8_t> candidates;
   std::vector<float> last_residual;
 };
@@ -878,6 +889,149 @@ void build_lfm(orc_model* m, const orc_model_def* def) {
   if (m->kv_heads == 0) throw std::runtime_error("LFM GGUF has no attention layer");
 }
 
+// The Granite runtime's GGUF checks (granite-wgsl-runtime.ts:359-395, :397-491)
+// with its wording: tensor types F32 / F16 / Q8_0 / Q4_K / Q6_K only, linear
+// tensors quantized with shape [k, n], float tensors F32 / F16.
+void granite_check_types(orc_model* m) {
+  for (const auto& kv : m->g.tensors) {
+    const uint32_t t = kv.second.type;
+    if (t != 0 && t != 1 && t != 8 && t != 12 && t != 14)
+      throw std::runtime_error("Granite WGSL unsupported GGML tensor type " + std::to_string(t));
+  }
+}
+
+Matrix granite_linear(orc_model* m, const std::string& name, uint64_t k, uint64_t n) {
+  auto it = m->g.tensors.find(name);
+  if (it == m->g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + name);
+  const Tensor& t = it->second;
+  if (t.type != 8 && t.type != 12 && t.type != 14)
+    throw std::runtime_error("Granite WGSL tensor " + name + " is not a GGUF quantized matrix");
+  if (t.shape.size() != 2 || t.shape[0] != k || t.shape[1] != n) {  // validateMatrixShape (:482-486)
+    std::string got;
+    for (size_t i = 0; i < t.shape.size(); ++i) got += (i ? ", " : "") + std::to_string(t.shape[i]);
+    throw std::runtime_error("Granite WGSL tensor " + name + " shape [" + got + "], expected [" + std::to_string(k) +
+                             ", " + std::to_string(n) + "]");
+  }
+  return matrix(m, name, k, n);
+}
+
+std::vector<float> granite_floats(orc_model* m, const std::string& name, size_t n) {
+  auto it = m->g.tensors.find(name);
+  if (it == m->g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + name);
+  if (it->second.type != 0 && it->second.type != 1)
+    throw std::runtime_error("Granite WGSL tensor " + name + " is not float32/float16");
+  return floats(m, name, n);
+}
+
+// GraniteWgslEngine.create (:536-624). The reference fixes the
+// Granite-4.0-H-350M shape in code (hidden 768, intermediate 2048, 12 heads /
+// 4 kv heads of 64, conv 1792, 48 SSM heads of 32, 128 states); here the
+// dimensions come from the tensor shapes with the same fixed SSM head width
+// (32) and state size (128), and the constants stay the reference's: eps 1e-5,
+// embedding x12, residual x0.246, attention x0.015625, logits x1/3, 4096
+// positions. A layer holding blk.N.ssm_in.weight is a Mamba2 layer (the
+// registry's layerTypes, :48-53).
+void build_granite(orc_model* m, const orc_model_def* def) {
+  const Gguf& g = m->g;
+  m->granite = true;
+  // validateGraniteGguf (:359-371)
+  auto ft = g.kv.find("general.file_type");
+  const double file_type = ft != g.kv.end() && ft->second.type != 8 && ft->second.type != 9 ? ft->second.num : -1;
+  if (file_type != 7 && file_type != 15)
+    throw std::runtime_error("Granite WGSL: expected GGUF Q8_0 or Q4_K_M file_type, got " +
+                             std::to_string((int)file_type));
+  for (const char* name : {"token_embd.weight", "output_norm.weight", "blk.0.attn_norm.weight"})
+    if (!g.tensors.count(name)) throw std::runtime_error(std::string("Granite WGSL: GGUF missing tensor ") + name);
+  granite_check_types(m);
+  const Tensor& te = g.tensors.at("token_embd.weight");
+  if (te.shape.size() != 2) throw std::runtime_error("Granite WGSL token_embd.weight is not a matrix");
+  const int H = (int)te.shape[0];
+  m->hidden = H;
+  m->vocab = (int)te.shape[1];
+  int nl = 0;
+  while (g.tensors.count("blk." + std::to_string(nl) + ".attn_norm.weight")) ++nl;
+  m->n_layers = nl;
+  m->hd = 64;                                // head_dim (:526, the STORE_KV / ATTENTION kernels' 64)
+  m->ctx = 4096;                             // GraniteWgslEngine.maxContext (:530)
+  m->norm_eps = 1e-5f;                       // RMS_NORM_WGSL / ADD_SCALED_RMS_NORM_WGSL / MAMBA_GATE_NORM_WGSL
+  m->attn_scale = 0.015625f;                 // ATTENTION_SCORE_WGSL (:1668)
+  m->embed_scale = 12.0f;                    // EMBEDDING_Q8_WGSL (:1362)
+  m->kv_f16 = def->kv_f16 != 0;
+  m->ssm_hdim = 32;                          // mambaDHead (:533)
+  m->ssm_state = 128;                        // the SSM kernel's 128-lane state (:1543-1547)
+  m->embed = granite_linear(m, "token_embd.weight", (uint64_t)H, (uint64_t)m->vocab);
+  m->lm_head = m->embed;                     // the embedding is the lm_head (:547-555)
+  m->final_norm = granite_floats(m, "output_norm.weight", H);
+  m->kv_heads = 0;
+  m->heads = 0;
+  m->ffn = 0;
+  for (int i = 0; i < nl; ++i) {
+    Layer L;
+    const std::string p = "blk." + std::to_string(i) + ".";
+    L.mamba = g.tensors.count(p + "ssm_in.weight") != 0;
+    L.in_norm = granite_floats(m, p + "attn_norm.weight", H);
+    L.post_norm = granite_floats(m, p + "ffn_norm.weight", H);
+    const auto& tg = g.tensors.find(p + "ffn_gate.weight");
+    if (tg == g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + p + "ffn_gate.weight");
+    L.ffn = (int)tg->second.shape.back();
+    m->ffn = std::max(m->ffn, L.ffn);
+    L.gate = granite_linear(m, p + "ffn_gate.weight", H, L.ffn);
+    L.up = granite_linear(m, p + "ffn_up.weight", H, L.ffn);
+    L.down = granite_linear(m, p + "ffn_down.weight", L.ffn, H);
+    L.window = 0;
+    L.theta_u32 = 0;
+    if (L.mamba) {
+      auto ti = g.tensors.find(p + "ssm_out.weight");
+      if (ti == g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + p + "ssm_out.weight");
+      const int inner = (int)ti->second.shape[0];
+      if (inner % m->ssm_hdim) throw std::runtime_error("Granite WGSL: SSM inner size is not a multiple of 32");
+      if (m->ssm_inner && inner != m->ssm_inner) throw std::runtime_error("Granite WGSL: SSM inner size differs by layer");
+      m->ssm_inner = inner;
+      m->ssm_heads = inner / m->ssm_hdim;
+      m->ssm_conv = inner + 2 * m->ssm_state;
+      const int nproj = inner + m->ssm_conv + m->ssm_heads;
+      L.ssm_in = granite_linear(m, p + "ssm_in.weight", H, nproj);
+      L.ssm_out = granite_linear(m, p + "ssm_out.weight", inner, H);
+      L.c1d_w = granite_floats(m, p + "ssm_conv1d.weight", 4 * (size_t)m->ssm_conv);
+      L.c1d_b = granite_floats(m, p + "ssm_conv1d.bias", m->ssm_conv);
+      L.dt_b = granite_floats(m, p + "ssm_dt.bias", m->ssm_heads);
+      L.a_neg = granite_floats(m, p + "ssm_a", m->ssm_heads);
+      L.d_w = granite_floats(m, p + "ssm_d", m->ssm_heads);
+      L.ssm_norm = granite_floats(m, p + "ssm_norm.weight", inner);
+      L.mconv_state.assign(4 * (size_t)m->ssm_conv, 0.0f);
+      L.ssm_state.assign((size_t)m->ssm_heads * m->ssm_hdim * m->ssm_state, 0.0f);
+      L.heads = 0;
+      L.kv_heads = 0;
+    } else {
+      auto tq = g.tensors.find(p + "attn_q.weight"), tk = g.tensors.find(p + "attn_k.weight");
+      if (tq == g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + p + "attn_q.weight");
+      if (tk == g.tensors.end()) throw std::runtime_error("Granite WGSL manifest missing tensor " + p + "attn_k.weight");
+      L.qdim = (int)tq->second.shape.back();
+      L.kvdim = (int)tk->second.shape.back();
+      L.heads = L.qdim / m->hd;
+      L.kv_heads = L.kvdim / m->hd;
+      if (L.qdim % m->hd || L.kvdim % m->hd || L.kv_heads <= 0 || L.heads % L.kv_heads != 0)
+        throw std::runtime_error("Granite WGSL: attention heads must be whole 64-wide heads in whole groups");
+      m->heads = std::max(m->heads, L.heads);
+      m->kv_heads = std::max(m->kv_heads, L.kv_heads);
+      L.q = granite_linear(m, p + "attn_q.weight", H, L.qdim);
+      L.k = granite_linear(m, p + "attn_k.weight", H, L.kvdim);
+      L.v = granite_linear(m, p + "attn_v.weight", H, L.kvdim);
+      L.o = granite_linear(m, p + "attn_output.weight", L.qdim, H);
+      L.kcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
+      L.vcache.assign((size_t)L.kvdim * m->ctx, 0.0f);
+    }
+    m->layers.push_back(std::move(L));
+  }
+  if (nl == 0) throw std::runtime_error("Granite WGSL: GGUF has no layers");
+  if (m->heads == 0) m->heads = 1;
+  for (Layer& L : m->layers)
+    if (L.mamba) {
+      L.qdim = 0;
+      L.kvdim = 0;
+    }
+}
+
 void build(orc_model* m, const orc_model_def* def) {
   const Gguf& g = m->g;
   auto it = g.kv.find("general.architecture");
@@ -889,6 +1043,10 @@ void build(orc_model* m, const orc_model_def* def) {
   }
   if (arch == "lfm2") {
     build_lfm(m, def);
+    return;
+  }
+  if (arch == "granitehybrid") {
+    build_granite(m, def);
     return;
   }
   if (arch != "qwen3" && arch != "llama" && arch != "gemma3" && arch != "openelm")
@@ -1155,7 +1313,13 @@ orc_model* orc_model_load(const char* path, const orc_model_def* def, char* err,
     m->up.assign(m->ffn, 0);
     m->ff.assign(m->ffn, 0);
     m->logits.assign(m->vocab, 0);
-    m->candidates.assign((size_t)(m->lfm ? 256 : (m->vocab + 255) / 256) * 8, 0);
+    m->candidates.assign((size_t)(m->lfm || m->granite ? 256 : (m->vocab + 255) / 256) * 8, 0);
+    if (m->granite) {
+      m->mproj.assign((size_t)m->ssm_inner + m->ssm_conv + m->ssm_heads, 0);
+      m->mconv.assign(m->ssm_conv, 0);
+      m->my.assign(m->ssm_inner, 0);
+      m->mnormed.assign(m->ssm_inner, 0);
+    }
     if (m->lfm) {
       m->proj.assign(3 * (size_t)H, 0);
       m->conv_mid.assign(H, 0);
@@ -1188,6 +1352,8 @@ void orc_model_reset(orc_model* m) {
     std::fill(L.kcache.begin(), L.kcache.end(), 0.0f);
     std::fill(L.vcache.begin(), L.vcache.end(), 0.0f);
     std::fill(L.conv_state.begin(), L.conv_state.end(), 0.0f);  // LfmWgslEngine.reset (:711-724)
+    std::fill(L.mconv_state.begin(), L.mconv_state.end(), 0.0f);  // GraniteWgslEngine.reset (:750-763)
+    std::fill(L.ssm_state.begin(), L.ssm_state.end(), 0.0f);
   }
 }
 
@@ -1546,11 +1712,149 @@ int32_t run_token_lfm(orc_model* m, int32_t token, int32_t need_logits, const or
   return best;
 }
 
+float silu_g(float x) {  // silu of MAMBA_CONV / MAMBA_GATE_NORM / SILU_MUL (:1484-1486, :1579-1581)
+  return x / (1.0f + std::exp(-x));
+}
+
+float softplus_g(float x) {  // MAMBA_SSM_WGSL's softplus (:1524-1526)
+  return x > 20.0f ? x + std::log(1.0f + std::exp(-x)) : std::log(1.0f + std::exp(x));
+}
+
+// MAMBA_CONV_WGSL (:1476-1511): the channel's window shifts by one (slot 0
+// drops out, the new xBC value enters slot 3), then four taps over the
+// previous three values and the new one, the bias, and silu.
+void granite_conv(orc_model* m, Layer& L, const float* proj, float* out) {
+  const int inner = m->ssm_inner;
+  for (int c = 0; c < m->ssm_conv; ++c) {
+    const float nv = proj[inner + c];
+    float* st = L.mconv_state.data() + 4 * (size_t)c;
+    const float p1 = st[1], p2 = st[2], p3 = st[3];
+    st[0] = p1;
+    st[1] = p2;
+    st[2] = p3;
+    st[3] = nv;
+    const float* w = L.c1d_w.data() + 4 * (size_t)c;
+    const float y = (((p1 * w[0] + p2 * w[1]) + p3 * w[2]) + nv * w[3]) + L.c1d_b[c];
+    out[c] = silu_g(y);
+  }
+}
+
+// MAMBA_SSM_WGSL (:1513-1562): per (head n, channel h) a 128-state selective
+// scan step with dt = softplus(dt_raw + dt_bias), decay = exp(dt * A), the
+// shared B and C of the single group, the state sum through the stride 64..1
+// tree, plus D * x.
+void granite_ssm(orc_model* m, Layer& L, const float* proj, const float* conv, float* y) {
+  const int inner = m->ssm_inner, S = m->ssm_state, hdim = m->ssm_hdim;
+  m->pool->run(m->ssm_heads, [&](int64_t nb, int64_t ne) {
+    float partial[128];
+    for (int64_t n = nb; n < ne; ++n) {
+      const float dt = softplus_g(proj[inner + m->ssm_conv + n] + L.dt_b[n]);
+      const float decay = std::exp(dt * L.a_neg[n]);
+      for (int h = 0; h < hdim; ++h) {
+        const int nh = (int)n * hdim + h;
+        const float hs = conv[nh];
+        for (int st = 0; st < S; ++st) {
+          const float b = conv[inner + st], c = conv[inner + S + st];
+          float& sv = L.ssm_state[(size_t)nh * S + st];
+          const float next = sv * decay + (dt * b) * hs;
+          sv = next;
+          partial[st] = next * c;
+        }
+        for (int stride = 64; stride >= 1; stride >>= 1)
+          for (int t = 0; t < stride; ++t) partial[t] = partial[t] + partial[t + stride];
+        y[nh] = partial[0] + L.d_w[n] * hs;
+      }
+    }
+  });
+}
+
+// MAMBA_GATE_NORM_WGSL (:1564-1608): v = y * silu(z) over the inner size,
+// RMSNorm over the 256-lane strided sums, ((y * silu(z)) * inv) * w.
+void granite_gate_norm(orc_model* m, const Layer& L, const float* z, const float* y, float* out) {
+  const int n = m->ssm_inner;
+  float partial[256];
+  for (int t = 0; t < 256; ++t) {
+    float sum = 0.0f;
+    for (int i = t; i < n; i += 256) {
+      const float v = y[i] * silu_g(z[i]);
+      sum = sum + v * v;
+    }
+    partial[t] = sum;
+  }
+  for (int s = 128; s >= 1; s >>= 1)
+    for (int t = 0; t < s; ++t) partial[t] = partial[t] + partial[t + s];
+  const float inv = 1.0f / std::sqrt(partial[0] / (float)n + m->norm_eps);
+  for (int i = 0; i < n; ++i) out[i] = ((y[i] * silu_g(z[i])) * inv) * L.ssm_norm[i];
+}
+
+// ADD_SCALED_RMS_NORM_WGSL (:1415-1456): residual += add * 0.246, then RMSNorm.
+void granite_add_norm(float* residual, const float* add, const float* w, float* out, int n, float eps) {
+  for (int i = 0; i < n; ++i) residual[i] = residual[i] + add[i] * 0.246f;
+  rms_norm(residual, w, out, n, eps);
+}
+
+// GraniteWgslEngine.runToken (:769-858)
+int32_t run_token_granite(orc_model* m, int32_t token, int32_t need_logits, const orc_sampling* s,
+                          const int32_t* seen, int64_t n_seen, double uniform) {
+  if (m->pos >= m->ctx)
+    throw std::runtime_error("Granite WGSL context exhausted at " + std::to_string(m->ctx) + " tokens");
+  const int H = m->hidden, pos = m->pos;
+  Pool& pool = *m->pool;
+  float* hA = m->hA.data();
+  float* hB = m->hB.data();
+  embedding(m, token, hA);  // EMBEDDING_{Q8,Q4_K,Q6_K}_WGSL (:1348-1372): dequant * 12
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    Layer& L = m->layers[li];
+    rms_norm(hA, L.in_norm.data(), m->norm.data(), H, m->norm_eps);
+    if (L.mamba) {
+      matvec(pool, L.ssm_in.type, L.ssm_in.data, L.ssm_in.n, L.ssm_in.k, m->norm.data(), m->mproj.data());
+      granite_conv(m, L, m->mproj.data(), m->mconv.data());
+      granite_ssm(m, L, m->mproj.data(), m->mconv.data(), m->my.data());
+      granite_gate_norm(m, L, m->mproj.data(), m->my.data(), m->mnormed.data());
+      matvec(pool, L.ssm_out.type, L.ssm_out.data, L.ssm_out.n, L.ssm_out.k, m->mnormed.data(), hB);
+    } else {
+      matvec(pool, L.q.type, L.q.data, L.q.n, L.q.k, m->norm.data(), m->q.data());
+      matvec(pool, L.k.type, L.k.data, L.k.n, L.k.k, m->norm.data(), m->k.data());
+      matvec(pool, L.v.type, L.v.data, L.v.n, L.v.k, m->norm.data(), m->v.data());
+      // STORE_KV_WGSL (:1610-1631): no rotary embedding
+      for (int i = 0; i < L.kvdim; ++i) {
+        const int kh = i / m->hd, d = i % m->hd;
+        const size_t at = ((size_t)kh * m->ctx + pos) * m->hd + d;
+        L.kcache[at] = kv_round(m, m->k[i]);
+        L.vcache[at] = kv_round(m, m->v[i]);
+      }
+      attention(m, L, pos, m->q.data(), m->attn.data());  // ATTENTION_SCORE / _VALUE_WGSL (:1633-1718)
+      matvec(pool, L.o.type, L.o.data, L.o.n, L.o.k, m->attn.data(), hB);
+    }
+    granite_add_norm(hA, hB, L.post_norm.data(), m->norm.data(), H, m->norm_eps);
+    matvec(pool, L.gate.type, L.gate.data, L.gate.n, L.gate.k, m->norm.data(), m->gate.data());
+    matvec(pool, L.up.type, L.up.data, L.up.n, L.up.k, m->norm.data(), m->up.data());
+    for (int i = 0; i < L.ffn; ++i) m->ff[i] = silu_mul(m->gate[i], m->up[i]);
+    matvec(pool, L.down.type, L.down.data, L.down.n, L.down.k, m->ff.data(), hB);
+    for (int i = 0; i < H; ++i) hA[i] = hA[i] + hB[i] * 0.246f;  // ADD_SCALED_WGSL (:1458-1474)
+  }
+  m->last_residual.assign(hA, hA + H);
+  int32_t best = 0;
+  if (need_logits) {
+    rms_norm(hA, m->final_norm.data(), m->norm.data(), H, m->norm_eps);
+    matvec(pool, m->lm_head.type, m->lm_head.data, (uint64_t)m->vocab, m->lm_head.k, m->norm.data(),
+           m->logits.data());
+    for (int i = 0; i < m->vocab; ++i) m->logits[i] = m->logits[i] * 0.333333333333333333f;  // SCALE_LOGITS_WGSL
+    lfm_top256(m->logits.data(), m->vocab, m->candidates.data());  // TOPK256_WGSL / ARGMAX_WGSL (:1753-1820)
+    const bool cand = s && (s->temperature > 0 || s->top_p < 1 || s->top_k > 0 || s->repetition_penalty != 1);
+    best = cand ? orc_sample_candidates(m->candidates.data(), 256, s, seen, n_seen, uniform)
+                : lfm_argmax(m->candidates.data());
+  }
+  m->pos += 1;
+  return best;
+}
+
 }  // namespace
 
 extern "C" {
 
 int orc_model_is_lfm(const orc_model* m) { return m->lfm ? 1 : 0; }
+int orc_model_is_granite(const orc_model* m) { return m->granite ? 1 : 0; }
 
 int orc_lfm_select(const float* logits, int64_t vocab, uint8_t* candidate_pairs, int32_t* token) {
   uint8_t pairs[256 * 8];
@@ -1566,6 +1870,10 @@ int orc_model_run_token(orc_model* m, int32_t token, int32_t need_logits, const 
   try {
     if (m->lfm) {
       *out_token = run_token_lfm(m, token, need_logits, s, seen, n_seen, uniform);
+      return 0;
+    }
+    if (m->granite) {
+      *out_token = run_token_granite(m, token, need_logits, s, seen, n_seen, uniform);
       return 0;
     }
     if (m->gpt) {

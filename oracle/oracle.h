@@ -67,6 +67,8 @@ int orc_model_context(const orc_model* m);
 int orc_model_is_gpt(const orc_model* m);
 /* 1 for a GGUF of architecture lfm2 (lfm-wgsl-runtime.ts), else 0. */
 int orc_model_is_lfm(const orc_model* m);
+/* 1 when the model is a granitehybrid (Granite-4.0-H) decoder. */
+int orc_model_is_granite(const orc_model* m);
 /* Vocabulary of the loaded model (ModelDef.vocab, or token_embd's rows for gpt2). */
 int orc_model_vocab(const orc_model* m);
 int orc_model_position(const orc_model* m);

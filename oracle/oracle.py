@@ -51,6 +51,7 @@ def lib():
         L.orc_model_context.argtypes = [P]
         L.orc_model_is_gpt.argtypes = [P]
         L.orc_model_is_lfm.argtypes = [P]
+        L.orc_model_is_granite.argtypes = [P]
         L.orc_lfm_select.argtypes = [P, C.c_int64, P, I32P]
         L.orc_model_vocab.argtypes = [P]
         L.orc_model_position.argtypes = [P]
@@ -146,7 +147,9 @@ def sample_candidates(pairs: np.ndarray, temperature: float, top_p: float, top_k
 class OracleModel:
     """CPU restatement of LlamaWgslEngine + generateLlamaWgsl, for a gpt2 GGUF
     of GptWgslEngine + generateGptWgsl (gpt-wgsl-runtime.ts), for an lfm2 GGUF
-    of LfmWgslEngine + generateLfmWgsl (lfm-wgsl-runtime.ts)."""
+    of LfmWgslEngine + generateLfmWgsl (lfm-wgsl-runtime.ts), for a
+    granitehybrid GGUF of GraniteWgslEngine + generateGraniteWgsl
+    (granite-wgsl-runtime.ts)."""
 
     def __init__(self, path: str, vocab: int, layers: int, max_context: int, kv_f16: bool = True,
                  threads: int = 8, eos_ids: Sequence[int] = (), default_repetition_penalty: Optional[float] = None):
@@ -157,6 +160,7 @@ class OracleModel:
             raise RuntimeError(err.value.decode())
         self.gpt = bool(lib().orc_model_is_gpt(self._h))
         self.lfm = bool(lib().orc_model_is_lfm(self._h))
+        self.granite = bool(lib().orc_model_is_granite(self._h))
         self.vocab = int(lib().orc_model_vocab(self._h))
         self.max_context = max_context
         self.eos_ids = set(eos_ids)
@@ -223,16 +227,18 @@ class OracleModel:
         """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314); generateGptWgsl
         (gpt-wgsl-runtime.ts:182-249) for gpt2, which also runs the token after
         the last generated one and refuses an empty prompt with no cached token;
-        generateLfmWgsl (lfm-wgsl-runtime.ts:219-306) for lfm2, which runs the
-        token after the last generated one, starts an empty prompt with no
-        cached token from id 0 and ignores the definition's default penalty."""
+        generateLfmWgsl (lfm-wgsl-runtime.ts:219-306) for lfm2 and
+        generateGraniteWgsl (granite-wgsl-runtime.ts:223-292) for granitehybrid,
+        which run the token after the last generated one, start an empty prompt
+        with no cached token from id 0 and ignore the definition's default
+        penalty."""
         prompt = list(prompt_ids)
         mx = min(128 if max_new_tokens is None else max_new_tokens, self.max_context - len(prompt))
         t = 0.0 if temperature is None else temperature
         tp = 1.0 if top_p is None else top_p
         tk = 0 if top_k is None else top_k
         rp = repetition_penalty if repetition_penalty is not None else (
-            1.0 if self.lfm else (self.default_repetition_penalty or 1.0))
+            1.0 if self.lfm or self.granite else (self.default_repetition_penalty or 1.0))
         n = 0
         while n < min(len(self.cached_token_ids), len(prompt)) and self.cached_token_ids[n] == prompt[n]:
             n += 1
@@ -260,7 +266,7 @@ class OracleModel:
             generated.append(next_id)
             if next_id in self.eos_ids:
                 break
-            if step + 1 >= mx and not self.gpt and not self.lfm:
+            if step + 1 >= mx and not self.gpt and not self.lfm and not self.granite:
                 break
             ids = prompt + generated
             next_id = self.run_token(next_id, True, t, tp, tk, rp, ids, ids, seed)

@@ -328,3 +328,113 @@ class NumpyLfm2:
         self.pos += 1
         self.last_hidden = x
         return self.emb[: self.vocab] @ self._rms(x, self.final_norm)
+
+
+class NumpyGranite:
+    """Float64 Granite-4.0-H decoder (the reference's Granite runtime,
+    src/lib/granite-wgsl-runtime.ts:769-858).
+
+    Embedding x12; per layer RMSNorm (eps 1e-5) -> either a Mamba2 block or NoPE
+    GQA attention (scores x 1/64); residual += 0.246 * out; RMSNorm -> SwiGLU ->
+    residual += 0.246 * out. Final RMSNorm, the tied embedding as lm_head, logits
+    x 1/3. The Mamba2 block is evaluated in its dual (attention-like) form from
+    the history of every position's (dt, B, x), not from a running state:
+        y_t[n, h] = sum_{tau <= t} (C_t . B_tau) prod_{tau < u <= t} exp(dt_u[n] A[n])
+                    * dt_tau[n] x_tau[n, h]  +  D[n] x_t[n, h],
+    with the causal 4-tap convolution (+ bias, silu) over the history of xBC,
+    then y * silu(z) through an RMSNorm over the inner size."""
+
+    HDIM, STATE = 32, 128
+
+    def __init__(self, path: str, max_context: int = 4096, kv_f16: bool = False):
+        g: Gguf = read_gguf(path)
+        f = lambda n: matrix(g, n).astype(np.float64)
+        self.emb = f("token_embd.weight")
+        self.H = self.emb.shape[1]
+        self.final_norm = f("output_norm.weight")
+        self.kv_f16 = kv_f16
+        self.layers = []
+        i = 0
+        while f"blk.{i}.attn_norm.weight" in g.tensors:
+            b = f"blk.{i}."
+            lay = dict(in_norm=f(b + "attn_norm.weight"), post=f(b + "ffn_norm.weight"), gate=f(b + "ffn_gate.weight"),
+                       up=f(b + "ffn_up.weight"), down=f(b + "ffn_down.weight"))
+            lay["mamba"] = (b + "ssm_in.weight") in g.tensors
+            if lay["mamba"]:
+                lay.update(inp=f(b + "ssm_in.weight"), out=f(b + "ssm_out.weight"),
+                           cw=f(b + "ssm_conv1d.weight").reshape(-1, 4), cb=f(b + "ssm_conv1d.bias"),
+                           dtb=f(b + "ssm_dt.bias"), A=f(b + "ssm_a"), D=f(b + "ssm_d"), nw=f(b + "ssm_norm.weight"))
+            else:
+                lay.update(q=f(b + "attn_q.weight"), k=f(b + "attn_k.weight"), v=f(b + "attn_v.weight"),
+                           o=f(b + "attn_output.weight"))
+            self.layers.append(lay)
+            i += 1
+        self.reset()
+
+    def reset(self):
+        self.pos = 0
+        self.K = [[] for _ in self.layers]
+        self.V = [[] for _ in self.layers]
+        self.xbc = [[] for _ in self.layers]   # every position's pre-convolution xBC
+        self.hist = [[] for _ in self.layers]  # every position's (dt, B, x)
+
+    @staticmethod
+    def _rms(x, w):
+        return x / np.sqrt(np.mean(x * x) + 1e-5) * w
+
+    @staticmethod
+    def _silu(x):
+        return x / (1 + np.exp(-x))
+
+    def _mamba(self, i, lay, n):
+        inner = lay["out"].shape[1]
+        nh, S = inner // self.HDIM, self.STATE
+        pr = lay["inp"] @ n
+        z, xbc, dtr = pr[:inner], pr[inner:inner + inner + 2 * S], pr[inner + inner + 2 * S:]
+        self.xbc[i].append(xbc)
+        win = ([np.zeros_like(xbc)] * 3 + self.xbc[i])[-4:]  # positions t-3 .. t (zeros before 0)
+        conv = self._silu(sum(lay["cw"][:, j] * win[j] for j in range(4)) + lay["cb"])
+        x, B, C = conv[:inner].reshape(nh, self.HDIM), conv[inner:inner + S], conv[inner + S:]
+        sp = dtr + lay["dtb"]
+        dt = np.where(sp > 20, sp + np.log1p(np.exp(-np.minimum(sp, 20.0))), np.log1p(np.exp(np.minimum(sp, 20.0))))
+        self.hist[i].append((dt, B, x))
+        y = lay["D"][:, None] * x
+        logdecay = 0.0  # sum over u in (tau, t] of dt_u * A
+        for dtt, Bt, xt in reversed(self.hist[i]):
+            y = y + (C @ Bt) * (np.exp(logdecay) * dtt)[:, None] * xt
+            logdecay = logdecay + dtt * lay["A"]
+        g = y.reshape(-1) * self._silu(z)
+        return lay["out"] @ self._rms(g, lay["nw"])
+
+    def step(self, token: int) -> np.ndarray:
+        hd = 64
+        x = self.emb[token] * 12.0
+        for i, lay in enumerate(self.layers):
+            n = self._rms(x, lay["in_norm"])
+            if lay["mamba"]:
+                o = self._mamba(i, lay, n)
+            else:
+                nq, nkv = lay["q"].shape[0] // hd, lay["k"].shape[0] // hd
+                q = (lay["q"] @ n).reshape(nq, hd)
+                k = (lay["k"] @ n).reshape(nkv, hd)
+                v = (lay["v"] @ n).reshape(nkv, hd)
+                if self.kv_f16:
+                    k = k.astype(np.float16).astype(np.float64)
+                    v = v.astype(np.float16).astype(np.float64)
+                self.K[i].append(k)
+                self.V[i].append(v)
+                KK, VV = np.stack(self.K[i]), np.stack(self.V[i])
+                grp = nq // nkv
+                att = np.empty((nq, hd))
+                for h in range(nq):
+                    s = KK[:, h // grp] @ q[h] * 0.015625
+                    pw = np.exp(s - s.max())
+                    att[h] = (pw / pw.sum()) @ VV[:, h // grp]
+                o = lay["o"] @ att.reshape(-1)
+            x = x + 0.246 * o
+            n = self._rms(x, lay["post"])
+            gte, up = lay["gate"] @ n, lay["up"] @ n
+            x = x + 0.246 * (lay["down"] @ (self._silu(gte) * up))
+        self.pos += 1
+        self.last_hidden = x
+        return (self.emb @ self._rms(x, self.final_norm)) / 3.0

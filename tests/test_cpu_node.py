@@ -56,7 +56,8 @@ def test_exports_and_load_errors(tmp_path):
                                      "generatePleiasWgsl", "disposePleiasWgsl", "loadGptWgslModel",
                                      "generateGptWgsl", "disposeGptWgsl", "resetGptWgslConversation",
                                      "loadLfmWgslModel", "generateLfmWgsl", "disposeLfmWgsl",
-                                     "resetLfmWgslConversation"])
+                                     "resetLfmWgslConversation", "loadGraniteWgslModel", "generateGraniteWgsl",
+                                     "disposeGraniteWgsl", "resetGraniteWgslConversation"])
     e = out["errors"]
     assert not e[0]["ok"] and "is not configured for the Llama WGSL runtime" in e[0]["message"]
     assert e[1]["code"] == "EIO" and "missing.gguf" in e[1]["message"]
