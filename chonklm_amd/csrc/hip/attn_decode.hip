@@ -2,32 +2,33 @@
 // qkNormRopeStore + attention score/value passes, src/lib/llama-wgsl-runtime.ts
 // :1467-1509, :1548-1570, WGSL :2868-3490), laid out for latency on gfx950.
 //
-// One workgroup per (kv head, chunk of 64 positions); each wave owns 16
-// positions of the chunk and keeps them in registers:
-//   A  the position by a scalar load, then every load of the workgroup: the
-//      wave's K rows (four lanes per position, HD/4 dims each) and V rows
-//      (HD/64 dims of each of the 16 positions per lane) into registers, q
-//      heads of the group, new k/v and norm weights into LDS, and the rotary
-//      (cos, sin) of the position from the engine's table.
-//   B  every wave does the q RMSNorm + rotary of the group into its own LDS
-//      copy (no workgroup barrier).
-//   C  scores by quads of lanes, softmax statistics over the wave's 16
-//      positions, weights through LDS (broadcast reads), V walked from
-//      registers — over the cached positions [start, pos); the new position
-//      is not in the cache yet.
-//   D  the four wave partials rescale to the chunk maximum and go to the
-//      chunk's row as tagged words {f32, u32 tag} (no wait); then every active
-//      chunk merges a slice of the output dims: it polls the rows' (max, sum)
-//      words and its dims' acc words until all carry this launch's tag, forms
-//      the weights exp(m_c - M) once per (head, chunk) with the lanes of one
-//      wave, and writes one weighted sum per output element. The new position
-//      joins every merge as one more term: while the rows travel, each chunk
-//      normalises, rotates and rounds k (and rounds v) itself, and the
-//      newest chunk stores both to the cache — so no chunk does more work
-//      than another before its row is out. The chunks of a
-//      launch wait for each other, so the engine uses this kernel only when
-//      its whole grid fits on the device at once; every wait is also bounded
-//      in time (DevState.error = 4 past the bound).
+// One workgroup per (kv head, chunk of 64 positions). A wave64 VALU
+// instruction occupies its 16-lane SIMD for four cycles and the grid leaves
+// about one workgroup per CU, so the kernel is laid out to keep each wave's
+// instruction count after the loads small:
+//   A  the position by a scalar load, then every load of the workgroup: K rows
+//      (four lanes per position, HD/4 dims each) and V rows (wave w holds
+//      dims [w*HD/4, (w+1)*HD/4) of all 64 positions, a lane 2 or 4 dims of
+//      every PG-th position) into registers, q heads, new k/v and norm weights
+//      into LDS, the rotary (cos, sin) of the position from the engine's table.
+//   B  the G q heads, the new k and the new v are G + 2 items over the four
+//      waves: RMSNorm and rotary into one shared q copy; k (normalised,
+//      rotated) and v rounded to fp16 like the cache, stored by the newest
+//      chunk.
+//   C  scores by quads of lanes; the chunk maximum per head through LDS; the
+//      weights exp(s - max) into LDS; weighted V from registers, each wave
+//      summing its dims over the position groups in registers (no cross-wave
+//      rescale).
+//   D  the chunk's row [max, sum, acc] per head goes out as tagged words
+//      {f32, u32 tag} (no wait), the new position's score is formed, then
+//      every active chunk merges a slice of the output dims: it polls the
+//      rows' (max, sum) words and its dims' acc words until all carry this
+//      launch's tag (addresses formed once), forms exp(m_c - M) / L once per
+//      (head, chunk), and writes one weighted sum per output element, the new
+//      position joining as one more term. The chunks of a launch wait for
+//      each other, so the engine uses this kernel only when its whole grid
+//      fits on the device at once; every wait is also bounded in time
+//      (DevState.error = 4 past the bound).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -42,36 +43,6 @@ namespace {
 constexpr int kDecChunk = 64;  // positions per workgroup
 constexpr int kDecWave = 16;   // positions per wave
 
-// DPL consecutive halves of one V row held by a lane.
-template <int DPL>
-struct VRow;
-template <>
-struct VRow<1> {
-  uint32_t w;
-  __device__ void load(const __half* p) { w = (uint32_t)*gbl((const uint16_t*)p); }
-  __device__ void get(float* f) const { f[0] = __half2float(__ushort_as_half((unsigned short)w)); }
-};
-template <>
-struct VRow<2> {
-  uint32_t w;
-  __device__ void load(const __half* p) { w = ldg1(p); }
-  __device__ void get(float* f) const {
-    f[0] = __half2float(__ushort_as_half((unsigned short)(w & 0xffffu)));
-    f[1] = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
-  }
-};
-template <>
-struct VRow<4> {
-  uint2 w;
-  __device__ void load(const __half* p) { w = ldg2(p); }
-  __device__ void get(float* f) const {
-    f[0] = __half2float(__ushort_as_half((unsigned short)(w.x & 0xffffu)));
-    f[1] = __half2float(__ushort_as_half((unsigned short)(w.x >> 16)));
-    f[2] = __half2float(__ushort_as_half((unsigned short)(w.y & 0xffffu)));
-    f[3] = __half2float(__ushort_as_half((unsigned short)(w.y >> 16)));
-  }
-};
-
 __device__ __forceinline__ float2 ldg2f(const float2* p) {
   const uint2 v = ldg2(p);
   return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
@@ -83,23 +54,6 @@ __device__ __forceinline__ float2 ldg2f(const float2* p) {
 template <class T>
 __device__ __forceinline__ T ld_scalar(const T* p) {
   return *(const __attribute__((address_space(4))) T*)p;
-}
-
-__device__ __forceinline__ void halves8(const uint4& v, float* f) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xffffu)));
-    f[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
-  }
-}
-
-// Two floats that are exact fp16 values, packed (truncating conversion).
-__device__ __forceinline__ uint32_t pkrtz(float a, float b) {
-  const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
-  uint32_t u;
-  __builtin_memcpy(&u, &h, 4);
-  return u;
 }
 
 // A wait for chunk rows is bounded (wall clock, 100 MHz): past the bound the
@@ -116,21 +70,46 @@ __device__ __forceinline__ uint64_t tag_get(const tagged_t* p) {
 __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
+// Sum over the position groups of a wave whose lanes are (group, dim pair):
+// lanes that differ only in the bits at and above log2(DW) (DW = 8 or 16
+// lanes per group). Every lane ends with its dim pair's total.
+template <int DW>
+__device__ __forceinline__ float pg_sum(float v) {
+  if constexpr (DW <= 8) v += dpp<0x128>(v);  // row_ror:8 = lane ^ 8 inside a 16-lane row
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
+}
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 // LDS (floats): q_s[G][HD] (raw) | kx[HD] | vx[HD] | nq[HD] | nk[HD] |
-// qw[4][G][HD] (each wave's normalised, rotated q) | ew[4][G][16] |
-// wml[4][G][2] | area: wave partials [4][G][HD], later the merge weights [G][ncp].
+// qn[G][HD] (normalised, rotated q, shared by the waves) | wmx[4][G] (each
+// wave's score maximum) | ew[G][64] (the chunk's weights; position p at
+// (p % PG) * NP + p / PG, so a lane reads its V positions contiguously) |
+// hv[G][4] (the new position's score per head).
 //
 // Chunk rows (a.tpart, [kv][nchunk][rowf] tagged words): per head [max, sum,
 // acc[HD]], each word {f32, u32 tag}; the tag of a launch is the kv head's
-// epoch a.cnt[kv], which the merging workgroup advances when it is done.
+// epoch a.cnt[kv], which the newest chunk advances when it is done.
 template <int G, int HD>
 __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   extern __shared__ __align__(16) float sm[];
   constexpr int HALF = HD / 2;
-  constexpr int DPT = HD / 4;       // K dims per lane (four lanes per position)
-  constexpr int NKV = DPT / 8;      // 16-byte K vectors per lane
-  constexpr int DPL = HD / 64;      // V dims per lane
+  constexpr int DPT = HD / 4;            // K dims per lane (four lanes per position)
+  constexpr int NKV = DPT / 8;           // 16-byte K vectors per lane
   constexpr int NPR = (HALF + 63) / 64;  // rotary pairs per lane
+  // V: wave w owns dims [w * HD / 4, (w + 1) * HD / 4) of all 64 positions;
+  // a lane holds VD consecutive dims (VW dwords) of NP positions
+  constexpr int VD = HD >= 256 ? 4 : 2;
+  constexpr int VW = VD / 2;
+  constexpr int DW = HD / 4 / VD;        // lanes per position row: 8 or 16
+  constexpr int LDW = DW == 8 ? 3 : 4;
+  constexpr int PG = 64 / DW;            // position groups
+  constexpr int NP = kDecChunk / PG;     // positions per lane
+  static_assert(DW == 8 || DW == 16, "head size");
   const int kv = blockIdx.x, c = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,16 +118,16 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   float* vx = kx + HD;
   float* nq = vx + HD;
   float* nk = nq + HD;
-  float* qw = nk + HD + wave * G * HD;
-  float* ew = nk + HD + 4 * G * HD;
-  float* wml = ew + 4 * G * kDecWave;
-  float* area = wml + 8 * G;
+  float* qn = nk + HD;
+  float* wmx = qn + G * HD;
+  float* ew = wmx + 4 * G;
+  float* hv = ew + kDecChunk * G;
   uint64_t tr[8];
   CHONK_MV_T(tr, 0);
 
   // A: the position, stop flag and epoch by scalar loads (their own counter,
   // so nothing below waits on them early), then the vector loads: the rotary
-  // frequencies, the wave's K/V rows, the LDS copies — with the rotary cos/sin
+  // frequencies, the K/V rows, the LDS copies — with the rotary cos/sin
   // computed while they are in flight
   DevState* st = a.st;
   const int pos = ld_scalar(&st->pos);
@@ -157,18 +136,26 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   const int t_lo = c * kDecChunk;
   const int kp = kDecWave * wave + (lane >> 2);  // this lane's K position in the chunk
   const int kd0 = (lane & 3) * DPT;
+  const int pg = lane >> LDW;                    // this lane's V positions: pg + PG * j
+  const int vd = wave * (HD / 4) + VD * (lane & (DW - 1));
   const __half* kc = (const __half*)a.kc + (size_t)kv * a.ctx * HD;
   const __half* vc = (const __half*)a.vc + (size_t)kv * a.ctx * HD;
   uint4 kr[NKV];
-  VRow<DPL> vr[kDecWave];
+  uint32_t vr[NP][VW];
   auto load_kv = [&]() {
     const int tk = min(t_lo + kp, a.ctx - 1);
 #pragma unroll
     for (int v = 0; v < NKV; ++v) kr[v] = ldg4(kc + (size_t)tk * HD + kd0 + 8 * v);
 #pragma unroll
-    for (int p = 0; p < kDecWave; ++p) {
-      const int tv = min(t_lo + kDecWave * wave + p, a.ctx - 1);
-      vr[p].load(vc + (size_t)tv * HD + lane * DPL);
+    for (int j = 0; j < NP; ++j) {
+      const __half* p = vc + (size_t)min(t_lo + pg + PG * j, a.ctx - 1) * HD + vd;
+      if constexpr (VW == 1) {
+        vr[j][0] = ldg1(p);
+      } else {
+        const uint2 w = ldg2(p);
+        vr[j][0] = w.x;
+        vr[j][VW - 1] = w.y;
+      }
     }
   };
   if (a.spec_kv) load_kv();
@@ -204,8 +191,10 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   }
   if (!active) return;
 
-  // B: every wave normalises and rotates the group's q heads into its own copy
-  // (all heads in one pass, so the reductions overlap)
+  // B: the group's q heads, the new k and the new v are G + 2 items spread
+  // over the waves: RMSNorm (if any) and rotary of q into qn; of k, rounded to
+  // fp16 like the cache, into kx; v rounded into vx. The newest chunk also
+  // stores k and v to the cache.
   int ia[NPR], ib[NPR];
 #pragma unroll
   for (int j = 0; j < NPR; ++j) {
@@ -213,311 +202,246 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     ia[j] = a.interleaved ? 2 * d : d;
     ib[j] = a.interleaved ? 2 * d + 1 : d + HALF;
   }
-  {
-    float x0[G][NPR], x1[G][NPR];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
+  const size_t kv_row = ((size_t)kv * a.ctx + pos) * HD;
+  for (int it = wave; it < G + 2; it += 4) {
+    if (it <= G) {
+      const float* src = it < G ? q_s + it * HD : kx;
+      const float* nw = it < G ? nq : nk;
+      float x0[NPR], x1[NPR];
 #pragma unroll
       for (int j = 0; j < NPR; ++j) {
-        x0[h][j] = q_s[h * HD + ia[j]];
-        x1[h][j] = q_s[h * HD + ib[j]];
+        x0[j] = src[ia[j]];
+        x1[j] = src[ib[j]];
       }
-    if (a.qn_w) {
-      float ss[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        ss[h] = 0.f;
+      if (a.qn_w) {
+        float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < NPR; ++j)
-          if (lane + 64 * j < HALF) ss[h] += x0[h][j] * x0[h][j] + x1[h][j] * x1[h][j];
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) ss[h] = wave_sum(ss[h]);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float r = 1.0f / sqrtf(ss[h] / (float)HD + a.eps);
+          if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss / (float)HD + a.eps);
 #pragma unroll
         for (int j = 0; j < NPR; ++j) {
-          x0[h][j] = __fmul_rn(__fmul_rn(x0[h][j], r), nq[ia[j]]);
-          x1[h][j] = __fmul_rn(__fmul_rn(x1[h][j], r), nq[ib[j]]);
+          x0[j] = __fmul_rn(__fmul_rn(x0[j], r), nw[ia[j]]);
+          x1[j] = __fmul_rn(__fmul_rn(x1[j], r), nw[ib[j]]);
         }
       }
+      float y0[NPR], y1[NPR];
+#pragma unroll
+      for (int j = 0; j < NPR; ++j) {
+        y0[j] = __fsub_rn(__fmul_rn(x0[j], co[j]), __fmul_rn(x1[j], si[j]));
+        y1[j] = __fadd_rn(__fmul_rn(x0[j], si[j]), __fmul_rn(x1[j], co[j]));
+      }
+      if (it < G) {
+#pragma unroll
+        for (int j = 0; j < NPR; ++j)
+          if (lane + 64 * j < HALF) {
+            qn[it * HD + ia[j]] = y0[j];
+            qn[it * HD + ib[j]] = y1[j];
+          }
+      } else {
+        // (every lane read its kx elements above; a lane writes only its own)
+#pragma unroll
+        for (int j = 0; j < NPR; ++j)
+          if (lane + 64 * j < HALF) {
+            const __half h0 = __float2half_rn(y0[j]), h1 = __float2half_rn(y1[j]);
+            if (c == c_hi) {
+              *gblw((unsigned short*)a.kc + kv_row + ia[j]) = __half_as_ushort(h0);
+              *gblw((unsigned short*)a.kc + kv_row + ib[j]) = __half_as_ushort(h1);
+            }
+            kx[ia[j]] = __half2float(h0);
+            kx[ib[j]] = __half2float(h1);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int d = lane; d < HD; d += 64) {
+        const __half vh = __float2half_rn(vx[d]);
+        if (c == c_hi) *gblw((unsigned short*)a.vc + kv_row + d) = __half_as_ushort(vh);
+        vx[d] = __half2float(vh);
+      }
     }
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int j = 0; j < NPR; ++j)
-        if (lane + 64 * j < HALF) {
-          qw[h * HD + ia[j]] = __fsub_rn(__fmul_rn(x0[h][j], co[j]), __fmul_rn(x1[h][j], si[j]));
-          qw[h * HD + ib[j]] = __fadd_rn(__fmul_rn(x0[h][j], si[j]), __fmul_rn(x1[h][j], co[j]));
-        }
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's q copy is in LDS
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
 
-  // C: scores, the wave's softmax statistics, weighted V
+  // C: scores over the cached positions [start, pos) (the new position is
+  // not in the registers: the merge adds it), the chunk maximum per head,
+  // then the weights exp(s - max) into ew
   const int tk = t_lo + kp;
-  // the new position is not in the registers (its row is written by this
-  // launch): the merge adds it
   const bool kvalid = tk >= start && tk < pos;
   float s[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) s[g] = 0.f;
 #pragma unroll
   for (int v = 0; v < NKV; ++v) {
-    float kf[8];
-    halves8(kr[v], kf);
+    const uint32_t w[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float4 q0 = *(const float4*)(qw + g * HD + kd0 + 8 * v);
-      const float4 q1 = *(const float4*)(qw + g * HD + kd0 + 8 * v + 4);
-      s[g] += ((q0.x * kf[0] + q0.y * kf[1]) + (q0.z * kf[2] + q0.w * kf[3])) +
-              ((q1.x * kf[4] + q1.y * kf[5]) + (q1.z * kf[6] + q1.w * kf[7]));
+      const float4 q0 = *(const float4*)(qn + g * HD + kd0 + 8 * v);
+      const float4 q1 = *(const float4*)(qn + g * HD + kd0 + 8 * v + 4);
+      s[g] = fmaf(q0.x, h2f(w[0]), s[g]);
+      s[g] = fmaf(q0.y, h2f(w[0] >> 16), s[g]);
+      s[g] = fmaf(q0.z, h2f(w[1]), s[g]);
+      s[g] = fmaf(q0.w, h2f(w[1] >> 16), s[g]);
+      s[g] = fmaf(q1.x, h2f(w[2]), s[g]);
+      s[g] = fmaf(q1.y, h2f(w[2] >> 16), s[g]);
+      s[g] = fmaf(q1.z, h2f(w[3]), s[g]);
+      s[g] = fmaf(q1.w, h2f(w[3] >> 16), s[g]);
     }
   }
-  float m[G], l[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float sc = group_sum<4>(s[g]);
-    const float sv = kvalid ? sc * a.scale : -INFINITY;
-    m[g] = wave_max(sv);
-    const float e = kvalid ? expf(sv - m[g]) : 0.f;
-    l[g] = wave_sum((lane & 3) == 0 ? e : 0.f);
-    if ((lane & 3) == 0) ew[(wave * G + g) * kDecWave + (lane >> 2)] = e;
+    const float sc = group_sum<4>(s[g]);  // (all lanes take part in the DPP steps)
+    s[g] = kvalid ? sc * a.scale : -INFINITY;
+    const float mw = wave_max(s[g]);
+    if (lane == 0) wmx[wave * G + g] = mw;
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's weights are in LDS
-  __builtin_amdgcn_wave_barrier();
-  float o[G][DPL];
+  __syncthreads();
+  float mx[G];
+  const int ei = (kp % PG) * NP + kp / PG;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mx[g] = fmaxf(fmaxf(wmx[g], wmx[G + g]), fmaxf(wmx[2 * G + g], wmx[3 * G + g]));
+    const float e = kvalid ? exp_fast(s[g] - mx[g]) : 0.f;
+    if ((lane & 3) == 0) ew[g * kDecChunk + ei] = e;
+  }
+  __syncthreads();
+
+  // weighted V over the chunk's 64 positions: rows outside [start, pos) carry
+  // weight 0, and their registers are cleared so that no unwritten value
+  // reaches the sum
+  if (t_lo < start || t_lo + kDecChunk > pos) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int p = t_lo + pg + PG * j;
+      if (p < start || p >= pos)
+#pragma unroll
+        for (int t = 0; t < VW; ++t) vr[j][t] = 0u;
+    }
+  }
+  float o[G][VD];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) o[g][k] = 0.f;
-  const int p0 = t_lo + kDecWave * wave;
+    for (int k = 0; k < VD; ++k) o[g][k] = 0.f;
 #pragma unroll
-  for (int p4 = 0; p4 < kDecWave / 4; ++p4) {
+  for (int j4 = 0; j4 < NP / 4; ++j4) {
     float4 w4[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) w4[g] = *(const float4*)(ew + (wave * G + g) * kDecWave + 4 * p4);
+    for (int g = 0; g < G; ++g) w4[g] = *(const float4*)(ew + g * kDecChunk + pg * NP + 4 * j4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int p = 4 * p4 + i;
-      float vf[DPL];
-      vr[p].get(vf);
-      // positions outside [start, pos) carry weight 0; their (possibly
-      // unwritten) rows must not reach the sum
-      const bool ok = p0 + p >= start && p0 + p < pos;
+      const int j = 4 * j4 + i;
+      float vf[VD];
+#pragma unroll
+      for (int t = 0; t < VW; ++t) {
+        vf[2 * t] = h2f(vr[j][t]);
+        vf[2 * t + 1] = h2f(vr[j][t] >> 16);
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float wt = i == 0 ? w4[g].x : i == 1 ? w4[g].y : i == 2 ? w4[g].z : w4[g].w;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) o[g][k] += ok ? wt * vf[k] : 0.f;
+        for (int k = 0; k < VD; ++k) o[g][k] = fmaf(wt, vf[k], o[g][k]);
       }
     }
   }
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) area[(wave * G + g) * HD + lane * DPL + k] = o[g][k];
-    if (lane == 0) {
-      wml[(wave * G + g) * 2] = m[g];
-      wml[(wave * G + g) * 2 + 1] = l[g];
-    }
-  }
-  __syncthreads();
+    for (int k = 0; k < VD; ++k) o[g][k] = pg_sum<DW>(o[g][k]);
   CHONK_MV_T(tr, 2);
 
-  // D: chunk partial [max, sum, acc[HD]] per head, to the chunk's row
+  // D: the chunk's row [max, sum, acc[HD]] per head, as tagged words (no
+  // wait): the position groups of a wave share the stores of its dims
   const int rowf = attn_rowf(G, HD);
   tagged_t* row = a.tpart + (size_t)(kv * a.nchunk + c) * rowf;
-  for (int i = tid; i < G * HD; i += kWg) {
-    const int g = i / HD, d = i - g * HD;
-    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * G + g) * 2]);
-    float acc = 0.f;
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = wml[(w * G + g) * 2];
-      if (mw != -INFINITY) acc += area[(w * G + g) * HD + d] * expf(mw - M);
+    for (int k = 0; k < VD; ++k)
+      if ((g * VD + k) % PG == pg) tag_put(row + g * (HD + 2) + 2 + vd + k, o[g][k], tag);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    if (g % 4 == wave) {
+      const float l = wave_sum(ew[g * kDecChunk + lane]);
+      if (lane == 0) {
+        tag_put(row + g * (HD + 2), mx[g], tag);
+        tag_put(row + g * (HD + 2) + 1, l, tag);
+      }
     }
-    tag_put(row + g * (HD + 2) + 2 + d, acc, tag);
-  }
-  if (tid < G) {
-    float M = -INFINITY, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * G + tid) * 2]);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = wml[(w * G + tid) * 2];
-      if (mw != -INFINITY) L += wml[(w * G + tid) * 2 + 1] * expf(mw - M);
-    }
-    tag_put(row + tid * (HD + 2), M, tag);
-    tag_put(row + tid * (HD + 2) + 1, L, tag);
-  }
-
   CHONK_MV_T(tr, 3);
-  // merge, shared by the active chunks: chunk ci merges dims [ci*SD, ci*SD+SD)
-  // of every head of the group. It polls the (max, sum) words of every row and
-  // its dims' acc words until all carry this launch's tag (one pass costs one
-  // memory round trip), then weights exp(m_c - M) per (head, chunk) by the
-  // lanes of one wave, then one weighted sum per output element.
-  const int nact = c_hi - c_lo + 1, ci = c - c_lo;
-  const int SD = (HD + nact - 1) / nact;
-  const int d_lo = min(ci * SD, HD), nd = min(SD, HD - d_lo);
-  const tagged_t* rows0 = a.tpart + (size_t)(kv * a.nchunk + c_lo) * rowf;
-  __syncthreads();  // area (the wave partials) is reused
-  float* ml = area;                  // [G][nact][2]
-  float* colv = ml + 2 * G * nact;   // [G][nd][nact]
-  float* wts = colv + G * SD * nact; // [G][nact], then 1/L per head in wml
-  const int n_ml = 2 * G * nact, n_col = G * nd * nact, total = n_ml + n_col;
-  // the new position, while the rows are on their way: wave 0 normalises,
-  // rotates and rounds k, wave 1 rounds v (the newest chunk also stores both
-  // to the cache); every chunk adds the position to its merge
-  const size_t kv_row = ((size_t)kv * a.ctx + pos) * HD;
-  if (wave == 0) {
-    float x0[NPR], x1[NPR];
+  // the new position's score per head, while the rows travel
 #pragma unroll
-    for (int j = 0; j < NPR; ++j) {
-      x0[j] = kx[ia[j]];
-      x1[j] = kx[ib[j]];
+  for (int g = 0; g < G; ++g)
+    if (g % 4 == wave) {
+      float sn = 0.f;
+#pragma unroll
+      for (int d = lane; d < HD; d += 64) sn += qn[g * HD + d] * kx[d];
+      sn = wave_sum(sn) * a.scale;
+      if (lane == 0) hv[4 * g] = sn;
     }
-    if (a.qn_w) {
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < NPR; ++j)
-        if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
-      ss = wave_sum(ss);
-      const float r = 1.0f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-      for (int j = 0; j < NPR; ++j) {
-        x0[j] = __fmul_rn(__fmul_rn(x0[j], r), nk[ia[j]]);
-        x1[j] = __fmul_rn(__fmul_rn(x1[j], r), nk[ib[j]]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NPR; ++j)
-      if (lane + 64 * j < HALF) {
-        const __half h0 = __float2half_rn(__fsub_rn(__fmul_rn(x0[j], co[j]), __fmul_rn(x1[j], si[j])));
-        const __half h1 = __float2half_rn(__fadd_rn(__fmul_rn(x0[j], si[j]), __fmul_rn(x1[j], co[j])));
-        if (c == c_hi) {
-          *gblw((unsigned short*)a.kc + kv_row + ia[j]) = __half_as_ushort(h0);
-          *gblw((unsigned short*)a.kc + kv_row + ib[j]) = __half_as_ushort(h1);
-        }
-        kx[ia[j]] = __half2float(h0);
-        kx[ib[j]] = __half2float(h1);
-      }
-  } else if (wave == 1) {
-#pragma unroll
-    for (int d = lane; d < HD; d += 64) {
-      const __half vh = __float2half_rn(vx[d]);
-      if (c == c_hi) *gblw((unsigned short*)a.vc + kv_row + d) = __half_as_ushort(vh);
-      vx[d] = __half2float(vh);
-    }
-  }
   CHONK_MV_T(tr, 4);
-  constexpr int NW = 4;  // words per thread per pass
+
+  // merge, shared by the active chunks: chunk c merges dims [s*SD, s*SD+SD)
+  // of every head of the group, s = c_hi - c. The newest chunk's slice is
+  // never empty, so it has seen every chunk's row carry this launch's tag —
+  // every chunk has read the epoch — before it advances the epoch. Each
+  // output element (g, d) of the slice has a group of tpi lanes (tpi >=
+  // nact / 2, so a lane covers at most two chunks) in one wave; each lane polls its chunks' (max, sum, acc[d]) words until
+  // all carry this launch's tag (one pass costs one memory round trip; the
+  // wave repeats while any lane still sees an old tag), then the group forms
+  // M, the weights exp(m_c - M), the sum L and the weighted acc in registers,
+  // the new position joining as one more term.
+  const int nact = c_hi - c_lo + 1;
+  const int SD = (HD + nact - 1) / nact;
+  const int d_lo = min((c_hi - c) * SD, HD), nd = min(SD, HD - d_lo);
+  const tagged_t* rows0 = a.tpart + (size_t)(kv * a.nchunk + c_lo) * rowf;
+  int ltpi = 0;
+  while (ltpi < 6 && (2 << ltpi) < nact) ++ltpi;
+  const int tpi = 1 << ltpi;
+  const int n_el = G * nd;
+  __syncthreads();  // the new-position scores and the rounded v
   const uint64_t t0 = wall_clock64();
   bool late = false;
-  for (int base = 0; base < total && !late; base += NW * kWg) {
-    for (uint32_t it = 0;; ++it) {
-      uint64_t w[NW];
-#pragma unroll
-      for (int k = 0; k < NW; ++k) {
-        const int e = min(base + tid + k * kWg, total - 1);
-        const tagged_t* src;
-        if (e < n_ml) {
-          const int g = e / (2 * nact), r = e - g * 2 * nact;
-          src = rows0 + (size_t)(r >> 1) * rowf + g * (HD + 2) + (r & 1);
-        } else {
-          const int f = e - n_ml;
-          const int g = f / (nd * nact), r = f - g * nd * nact;
-          const int dd = r / nact, cc = r - dd * nact;
-          src = rows0 + (size_t)cc * rowf + g * (HD + 2) + 2 + d_lo + dd;
-        }
-        w[k] = tag_get(src);
-      }
-      int stale = 0;
-#pragma unroll
-      for (int k = 0; k < NW; ++k) {
-        const int e = base + tid + k * kWg;
-        if (e < total) {
-          stale |= !tag_is(w[k], tag);
-          if (e < n_ml)
-            ml[e] = tag_val(w[k]);
-          else
-            colv[e - n_ml] = tag_val(w[k]);
-        }
-      }
-      if (!__syncthreads_or(stale)) break;
-      if ((it & 3) == 3) {
-        const int t_out = tid == 0 && wall_clock64() - t0 > kDecPollTicks;
-        if (__syncthreads_or(t_out)) {
-          late = true;
-          break;
-        }
-      }
-    }
-  }
-  CHONK_MV_T(tr, 5);
-  // (the poll's barriers also publish the rounded k and v)
-  for (int g = wave; g < G; g += 4) {
-    // the new position's score with the wave's own copy of q head g
-    float sn = 0.f;
-#pragma unroll
-    for (int d = lane; d < HD; d += 64) sn += qw[g * HD + d] * kx[d];
-    sn = wave_sum(sn) * a.scale;
-    float mv[2], lv[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cc = lane + 64 * j;
-      mv[j] = cc < nact ? ml[(g * nact + cc) * 2] : -INFINITY;
-      lv[j] = cc < nact ? ml[(g * nact + cc) * 2 + 1] : 0.f;
-    }
-    const float M = fmaxf(wave_max(fmaxf(mv[0], mv[1])), sn);
-    float L = 0.f;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cc = lane + 64 * j;
-      const float f = mv[j] == -INFINITY ? 0.f : expf(mv[j] - M);
-      if (cc < nact) wts[g * nact + cc] = f;
-      L += lv[j] * f;
-    }
-    const float fn = expf(sn - M);
-    L = wave_sum(L) + fn;
-    if (lane == 0) {
-      wml[2 * g] = 1.0f / L;
-      wml[2 * g + 1] = fn;
-    }
-  }
-  __syncthreads();
-  // the weighted sum over the chunks of each output element of the slice, by
-  // tpi lanes per element (every tpi-th chunk each, then a DPP sum): the
-  // workgroup's lanes spread over the G * nd elements
-  const int n_el = G * nd;
-  int tpi = 1;
-  while (tpi < 64 && 2 * tpi * n_el <= kWg && tpi < nact) tpi *= 2;
-  for (int base = 0; base < n_el * tpi; base += kWg) {
+  for (int base = 0; base < n_el * tpi && !late; base += kWg) {
     const int q = base + tid;
-    const int i = q / tpi, sub = q & (tpi - 1);
-    if (i < n_el) {
-      const int g = i / nd, dd = i - g * nd;
-      const float* src = colv + (size_t)(g * nd + dd) * nact;
-      const float* wv = wts + g * nact;
-      float a0 = 0.f, a1 = 0.f;
-      int cc = sub;
-      for (; cc + tpi < nact; cc += 2 * tpi) {
-        a0 += src[cc] * wv[cc];
-        a1 += src[cc + tpi] * wv[cc + tpi];
-      }
-      if (cc < nact) a0 += src[cc] * wv[cc];
-      const float sum = group_sum_n(a0 + a1, tpi);
-      if (sub == 0) {
-        const float acc = sum + wml[2 * g + 1] * vx[d_lo + dd];
-        a.out[(size_t)kv * G * HD + g * HD + d_lo + dd] = acc * wml[2 * g];
+    const int i = q >> ltpi, sub = q & (tpi - 1);
+    const bool el = i < n_el;
+    const int g = el ? i / nd : 0, d = d_lo + (el ? i - g * nd : 0);
+    const bool h0 = el && sub < nact, h1 = el && sub + tpi < nact;
+    const tagged_t* r0 = rows0 + (size_t)min(sub, nact - 1) * rowf + g * (HD + 2);
+    const tagged_t* r1 = rows0 + (size_t)min(sub + tpi, nact - 1) * rowf + g * (HD + 2);
+    uint64_t w[6];
+    for (uint32_t it = 0;; ++it) {
+      w[0] = tag_get(r0);
+      w[1] = tag_get(r0 + 1);
+      w[2] = tag_get(r0 + 2 + d);
+      w[3] = tag_get(r1);
+      w[4] = tag_get(r1 + 1);
+      w[5] = tag_get(r1 + 2 + d);
+      bool stale = h0 && !(tag_is(w[0], tag) && tag_is(w[1], tag) && tag_is(w[2], tag));
+      stale |= h1 && !(tag_is(w[3], tag) && tag_is(w[4], tag) && tag_is(w[5], tag));
+      if (__builtin_amdgcn_ballot_w64(stale) == 0) break;
+      if ((it & 3) == 3 && __builtin_amdgcn_readfirstlane(wall_clock64() - t0 > kDecPollTicks ? 1 : 0)) {
+        late = true;
+        break;
       }
     }
+    if (late) break;
+    const float m0 = h0 ? tag_val(w[0]) : -INFINITY, m1 = h1 ? tag_val(w[3]) : -INFINITY;
+    const float sn = hv[4 * g];
+    const float M = fmaxf(group_max_n(fmaxf(m0, m1), tpi), sn);
+    const float f0 = m0 == -INFINITY ? 0.f : exp_fast(m0 - M);
+    const float f1 = m1 == -INFINITY ? 0.f : exp_fast(m1 - M);
+    const float l = (h0 ? tag_val(w[1]) * f0 : 0.f) + (h1 ? tag_val(w[4]) * f1 : 0.f);
+    const float s = (h0 ? tag_val(w[2]) * f0 : 0.f) + (h1 ? tag_val(w[5]) * f1 : 0.f);
+    const float L = group_sum_n(l, tpi), S = group_sum_n(s, tpi);
+    const float fn = exp_fast(sn - M);
+    if (el && sub == 0) a.out[(size_t)kv * G * HD + g * HD + d] = __fdiv_rn(S + fn * vx[d], L + fn);
   }
   if (late && tid == 0) st->error = 4;
+  CHONK_MV_T(tr, 5);
   CHONK_MV_T(tr, 6);
   CHONK_MV_TRACE_END(tr, 7 * 65536);
   // every producer of this launch has read the tag once all rows carry it:
@@ -537,11 +461,10 @@ bool attn_dec_supported(int group, int hd, int ctx, int kv_f16) {
 int attn_dec_chunk() { return kDecChunk; }
 
 size_t attn_dec_shared_bytes(int group, int hd, int nchunk) {
-  // merge buffers: (max, sum) and weights per (head, chunk), the acc words of
-  // ceil(hd / nact) dims per head and chunk (at most hd + nact per head)
-  const size_t merge = (size_t)group * (3 * (size_t)nchunk + hd + nchunk);
-  const size_t area = std::max((size_t)4 * group * hd, merge);
-  return sizeof(float) * ((size_t)(group + 4) * hd + (size_t)4 * group * hd + 4 * group * kDecWave + 8 * group + area);
+  // q_s, qn [G][hd]; kx, vx, nq, nk [hd]; wmx [4][G], ew [G][64], hv [G][4]
+  (void)nchunk;
+  const size_t g = (size_t)group;
+  return sizeof(float) * (2 * g * hd + 4 * (size_t)hd + g * (4 + kDecChunk + 4));
 }
 
 namespace {

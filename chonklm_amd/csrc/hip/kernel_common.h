@@ -103,6 +103,17 @@ __device__ __forceinline__ float group_sum_n(float v, int n) {
     default: return v;
   }
 }
+__device__ __forceinline__ float group_max_n(float v, int n) {
+  switch (n) {
+    case 2: return group_max<2>(v);
+    case 4: return group_max<4>(v);
+    case 8: return group_max<8>(v);
+    case 16: return group_max<16>(v);
+    case 32: return group_max<32>(v);
+    case 64: return group_max<64>(v);
+    default: return v;
+  }
+}
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 

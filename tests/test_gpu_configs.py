@@ -218,3 +218,35 @@ def test_batched_rows_match_oracle_at_config_shape(synth):
         cur = nxt
     b.close()
     loaded.engine.dispose()
+
+
+def test_decode_attention_across_chunk_counts(synth):
+    """The Qwen3-0.6B shape with the benchmark's 2304-position cache (36 chunks of 64) stepped
+    at positions that give every kind of merge: one chunk, a full last chunk, a newest chunk
+    holding only the new position, and 30-36 active chunks, where the output dims divide
+    unevenly over the chunks and some chunks merge no dims. The newest chunk advances the kv
+    head's epoch only after it has seen every chunk's row; a launch that waited on a stale
+    epoch would report error 4 here. Logits within 1e-3 of the oracle, identical ids."""
+    name = "qwen3-0.6b-q4_k_m"
+    w = WORKLOADS[name]
+    path = synth(name)
+    ctx = 2304
+    md = w.model_def(path)
+    md.max_context = ctx
+    loaded = load_llama_wgsl_model(md)
+    eng = loaded.engine
+    assert eng.info["persistent_step"] == 0
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
+    tok = 17
+    for pos in (1, 63, 64, 127, 700, 1900, 1919, 1920, 2047, 2048, 2111, 2112, 2240, 2302):
+        eng.fake_context(pos, seed=pos)
+        ref.fake_context(pos, seed=pos)
+        for i in range(2):
+            a = eng.run_token(tok, True)
+            b = ref.run_token(tok, True)
+            e = rel_err(eng.read_logits(), ref.logits())
+            assert e <= 1e-3, f"position {pos + i}: logits rel err {e:.3e}"
+            assert a == b, f"position {pos + i}: token {a} != {b}"
+            tok = a
+    eng.dispose()
+    ref.close()
