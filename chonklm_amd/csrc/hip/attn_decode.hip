@@ -353,14 +353,22 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   CHONK_MV_T(tr, 2);
 
   // D: the chunk's row [max, sum, acc[HD]] per head, as tagged words (no
-  // wait): the position groups of a wave share the stores of its dims
+  // wait): in each store instruction lane (pg, dw) writes item pg + PG * it
+  // (head item / VD, dim vd + item % VD), so the lanes of one head cover
+  // consecutive words and every cache line is written whole
   const int rowf = attn_rowf(G, HD);
   tagged_t* row = a.tpart + (size_t)(kv * a.nchunk + c) * rowf;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int it = 0; it < (G * VD + PG - 1) / PG; ++it) {
+    const int item = it * PG + pg;
+    float val = 0.f;
 #pragma unroll
-    for (int k = 0; k < VD; ++k)
-      if ((g * VD + k) % PG == pg) tag_put(row + g * (HD + 2) + 2 + vd + k, o[g][k], tag);
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < VD; ++k)
+        if (g * VD + k == item) val = o[g][k];
+    if (item < G * VD) tag_put(row + (item / VD) * (HD + 2) + 2 + vd + item % VD, val, tag);
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g)
     if (g % 4 == wave) {
