@@ -70,21 +70,6 @@ __device__ __forceinline__ uint64_t tag_get(const tagged_t* p) {
 __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
-// Sum over the position groups of a wave whose lanes are (group, dim pair):
-// lanes that differ only in the bits at and above log2(DW) (DW = 8 or 16
-// lanes per group). Every lane ends with its dim pair's total.
-template <int DW>
-__device__ __forceinline__ float pg_sum(float v) {
-  if constexpr (DW <= 8) v += dpp<0x128>(v);  // row_ror:8 = lane ^ 8 inside a 16-lane row
-  float a, b;
-  swap16(v, a, b);
-  v = a + b;
-  swap32(v, a, b);
-  return a + b;
-}
-
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-
 // LDS (floats): q_s[G][HD] (raw) | kx[HD] | vx[HD] | nq[HD] | nk[HD] |
 // qn[G][HD] (normalised, rotated q, shared by the waves) | wmx[4][G] (each
 // wave's score maximum) | ew[G][64] (the chunk's weights; position p at

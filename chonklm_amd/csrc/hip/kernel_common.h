@@ -117,6 +117,21 @@ __device__ __forceinline__ float group_max_n(float v, int n) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+// Sum over the position groups of a wave whose lanes are (group, dim pair):
+// lanes that differ only in the bits at and above log2(DW) (DW = 8 or 16
+// lanes per group). Every lane ends with its dim pair's total.
+template <int DW>
+__device__ __forceinline__ float pg_sum(float v) {
+  if constexpr (DW <= 8) v += dpp<0x128>(v);  // row_ror:8 = lane ^ 8 inside a 16-lane row
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
+}
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 // Sum over the 256 threads; red must hold 4 floats. Callable repeatedly.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);

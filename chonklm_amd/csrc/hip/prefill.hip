@@ -762,124 +762,234 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   }
 }
 
-// Decode attention of batch rows over paged K/V: one workgroup per (page,
-// kv head, row) holds the row's G query heads against the page's (up to) 64
-// positions and leaves a partial [max, sum, acc[hd]] per head; k_bd_merge
-// combines a row's pages. Same arithmetic as the decode attention's chunks
-// and merge, with pages for chunks.
+// Decode attention of batch rows over paged K/V. One workgroup per (kv head,
+// row, segment) walks a segment of the row's pages [start, pos] with the
+// decode attention's layout: a page's K rows in registers (four lanes per
+// position), its V rows in registers (wave w holds dims [w*HD/4, (w+1)*HD/4)
+// of every position, a lane 2 or 4 dims of every PG-th position); the next
+// page's rows are requested before the current page is reduced. The softmax
+// runs online over the pages (running maximum and sum per head, the
+// accumulators rescaled when the maximum grows). With one segment per row the
+// workgroup writes the attention output; otherwise a partial [max, sum,
+// acc[hd]] per head for k_bd_merge.
 template <int HD>
-__global__ __launch_bounds__(kWg) void k_bd_attn(PfAttnArgs a, float* part, int max_pages) {
-  __shared__ float q_s[8 * HD];
-  __shared__ float sc[8][kKvPage];
-  __shared__ float red[8][4];
-  __shared__ __align__(16) __half v_s[kKvPage * HD];
-  const int page = blockIdx.x, kv = blockIdx.y, r = blockIdx.z, tid = threadIdx.x;
+__global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg) {
+  constexpr int DPT = HD / 4;  // K dims per lane
+  constexpr int NKV = DPT / 8;
+  constexpr int VD = HD >= 256 ? 4 : 2, VW = VD / 2;
+  constexpr int DW = HD / 4 / VD;  // lanes per V position row: 8 or 16
+  constexpr int LDW = DW == 8 ? 3 : 4;
+  constexpr int PG = 64 / DW, NP = kKvPage / PG;
+  static_assert(kKvPage == 64 && (DW == 8 || DW == 16), "page geometry");
+  __shared__ __align__(16) float q_s[8 * HD];
+  __shared__ float wmx[4][8];
+  __shared__ __align__(16) float ew[8][kKvPage];
+  __shared__ float lsum[8];
+  const int kv = blockIdx.x, r = blockIdx.y, sg = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.heads / a.kv_heads;
   const int pos = row_pos(a.kv, r);
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-  const int k0 = page * kKvPage;
-  if (k0 > pos || k0 + kKvPage <= start) return;  // page outside [start, pos]
+  const int j_lo = start / kKvPage, np = pos / kKvPage - j_lo + 1;
+  // this segment's pages [p_lo, p_hi) of the row's range
+  const int p_lo = j_lo + (int)((int64_t)np * sg / nseg), p_hi = j_lo + (int)((int64_t)np * (sg + 1) / nseg);
   const int seq = row_seq(a.kv, r);
-  const int phys = a.kv.pages[(size_t)seq * a.kv.max_pages + page];
-  const __half* kb = (const __half*)a.kv.kc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
-  const __half* vb = (const __half*)a.kv.vc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
   const float* q = a.qkv + (size_t)r * a.ld + kv * G * HD;
-  lds_dma((const float*)vb, (float*)v_s, kKvPage * HD / 2);  // the page's V rows, in flight
-  for (int i = tid; i < G * HD; i += kWg) q_s[i] = q[i];
-  __syncthreads();
-  // scores: four threads per position, HD / 4 dims each
-  const int key = tid >> 2, part4 = tid & 3;
-  const bool valid = k0 + key >= start && k0 + key <= pos;
-  float s[8];
+  const int kp = 16 * wave + (lane >> 2), kd0 = (lane & 3) * DPT;
+  const int pg = lane >> LDW, vd = wave * (HD / 4) + VD * (lane & (DW - 1));
+  const int ei = (kp % PG) * NP + kp / PG;
+  auto load = [&](int j, uint4 (&kr)[NKV], uint32_t (&vr)[NP][VW]) {
+    const int phys = a.kv.pages[(size_t)seq * a.kv.max_pages + j];
+    const __half* kb = (const __half*)a.kv.kc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
+    const __half* vb = (const __half*)a.kv.vc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) s[g] = 0.f;
-  {
-    const __half* kr = kb + key * HD + part4 * (HD / 4);
+    for (int v = 0; v < NKV; ++v) kr[v] = ldg4(kb + (size_t)kp * HD + kd0 + 8 * v);
 #pragma unroll
-    for (int d = 0; d < HD / 4; d += 8) {
-      const uint4 w4 = *(const uint4*)(kr + d);
-      const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-      float kf[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kf[2 * i] = h2f(w[i]);
-        kf[2 * i + 1] = h2f(w[i] >> 16);
+    for (int t = 0; t < NP; ++t) {
+      const __half* p = vb + (size_t)(pg + PG * t) * HD + vd;
+      if constexpr (VW == 1) {
+        vr[t][0] = ldg1(p);
+      } else {
+        const uint2 w = ldg2(p);
+        vr[t][0] = w.x;
+        vr[t][VW - 1] = w.y;
       }
+    }
+  };
+  float mrun[8], o[8][VD];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    mrun[g] = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < VD; ++k) o[g][k] = 0.f;
+  }
+  float lrun[8];  // wave g % 4's running sum of head g
+#pragma unroll
+  for (int g = 0; g < 8; ++g) lrun[g] = 0.f;
+  auto page = [&](int j, uint4 (&kr)[NKV], uint32_t (&vr)[NP][VW]) {
+    const int k0 = j * kKvPage;
+    const bool valid = k0 + kp >= start && k0 + kp <= pos;
+    float s[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) s[g] = 0.f;
+#pragma unroll
+    for (int v = 0; v < NKV; ++v) {
+      const uint32_t w[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
         if (g < G) {
-          const float* qq = q_s + g * HD + part4 * (HD / 4) + d;
-          float acc = 0.f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc += qq[i] * kf[i];
-          s[g] += acc;
+          const float4 q0 = *(const float4*)(q_s + g * HD + kd0 + 8 * v);
+          const float4 q1 = *(const float4*)(q_s + g * HD + kd0 + 8 * v + 4);
+          s[g] = fmaf(q0.x, h2f(w[0]), s[g]);
+          s[g] = fmaf(q0.y, h2f(w[0] >> 16), s[g]);
+          s[g] = fmaf(q0.z, h2f(w[1]), s[g]);
+          s[g] = fmaf(q0.w, h2f(w[1] >> 16), s[g]);
+          s[g] = fmaf(q1.x, h2f(w[2]), s[g]);
+          s[g] = fmaf(q1.y, h2f(w[2] >> 16), s[g]);
+          s[g] = fmaf(q1.z, h2f(w[3]), s[g]);
+          s[g] = fmaf(q1.w, h2f(w[3] >> 16), s[g]);
         }
       }
     }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g < G) {
+        const float sc = group_sum<4>(s[g]);
+        s[g] = valid ? sc * a.scale : -INFINITY;
+        const float mw = wave_max(s[g]);
+        if (lane == 0) wmx[wave][g] = mw;
+      }
+    }
+    __syncthreads();  // the page maxima (and the previous page's weights are consumed)
+    float alpha[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g < G) {
+        const float mp = fmaxf(fmaxf(wmx[0][g], wmx[1][g]), fmaxf(wmx[2][g], wmx[3][g]));
+        const float mn = fmaxf(mrun[g], mp);  // finite: every page of the range holds a position
+        alpha[g] = exp_fast(mrun[g] - mn);     // 0 on the first page
+        mrun[g] = mn;
+        const float e = valid ? exp_fast(s[g] - mn) : 0.f;
+        if ((lane & 3) == 0) ew[g][ei] = e;
+      }
+    }
+    __syncthreads();  // the page's weights
+    if (k0 < start || k0 + kKvPage - 1 > pos) {
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
+        const int p = k0 + pg + PG * t;
+        if (p < start || p > pos)
+#pragma unroll
+          for (int u = 0; u < VW; ++u) vr[t][u] = 0u;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g < G) {
+        if (g % 4 == wave) lrun[g] = lrun[g] * alpha[g] + wave_sum(ew[g][lane]);
+#pragma unroll
+        for (int k = 0; k < VD; ++k) o[g][k] *= alpha[g];
+#pragma unroll
+        for (int t4 = 0; t4 < NP / 4; ++t4) {
+          const float4 w4 = *(const float4*)(&ew[g][pg * NP + 4 * t4]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 4 * t4 + i;
+            const float wt = i == 0 ? w4.x : i == 1 ? w4.y : i == 2 ? w4.z : w4.w;
+#pragma unroll
+            for (int u = 0; u < VW; ++u) {
+              o[g][2 * u] = fmaf(wt, h2f(vr[t][u]), o[g][2 * u]);
+              o[g][2 * u + 1] = fmaf(wt, h2f(vr[t][u] >> 16), o[g][2 * u + 1]);
+            }
+          }
+        }
+      }
+    }
+  };
+  uint4 ka[NKV], kb2[NKV];
+  uint32_t va[NP][VW], vb2[NP][VW];
+  // q first: its loads complete before the page's, which stay in flight
+  float qv[6];
+#pragma unroll
+  for (int c = 0; c < 6; ++c) qv[c] = tid + kWg * c < G * HD ? q[tid + kWg * c] : 0.f;
+  if (p_lo < p_hi) load(p_lo, ka, va);
+#pragma unroll
+  for (int c = 0; c < 6; ++c)
+    if (tid + kWg * c < G * HD) q_s[tid + kWg * c] = qv[c];
+  __syncthreads();
+  for (int j = p_lo; j < p_hi; j += 2) {
+    if (j + 1 < p_hi) load(j + 1, kb2, vb2);
+    page(j, ka, va);
+    if (j + 1 >= p_hi) break;
+    if (j + 2 < p_hi) load(j + 2, ka, va);
+    page(j + 1, kb2, vb2);
   }
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    if (g < G) {
-      const float v = group_sum<4>(s[g]);
-      if (part4 == 0) sc[g][key] = valid ? v * a.scale : -INFINITY;
+  for (int g = 0; g < 8; ++g)
+    if (g < G)
+#pragma unroll
+      for (int k = 0; k < VD; ++k) o[g][k] = pg_sum<DW>(o[g][k]);
+  // lanes (pg, dw) write item pg + PG * it (head item / VD, dim vd + item % VD)
+  if (nseg == 1) {
+    if (lane == 0)
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+        if (g < G && g % 4 == wave) lsum[g] = lrun[g];
+    __syncthreads();
+    float* out = a.out + (size_t)r * a.ldo + kv * G * HD;
+    for (int it = 0; it * PG < G * VD; ++it) {
+      const int item = it * PG + pg;
+      float val = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+#pragma unroll
+        for (int k = 0; k < VD; ++k)
+          if (g * VD + k == item) val = o[g][k];
+      if (item < G * VD) out[(item / VD) * HD + vd + item % VD] = val / lsum[item / VD];
     }
-  }
-  __syncthreads();
-  // per head: max and exp over the page (one wave per head, lanes = positions)
-  const int lane = tid & 63, wave = tid >> 6;
-  for (int g = wave; g < G; g += 4) {
-    const float v = sc[g][lane];
-    const float m = wave_max(v);
-    const float e = v == -INFINITY ? 0.f : expf(v - m);
-    sc[g][lane] = e;
-    const float l = wave_sum(e);
-    if (lane == 0) {
-      red[g][0] = m;
-      red[g][1] = l;
+  } else {
+    const int rowf = attn_rowf(G, HD);
+    float* out = part + (((size_t)r * a.kv_heads + kv) * max_pages + sg) * rowf;
+    for (int it = 0; it * PG < G * VD; ++it) {
+      const int item = it * PG + pg;
+      float val = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+#pragma unroll
+        for (int k = 0; k < VD; ++k)
+          if (g * VD + k == item) val = o[g][k];
+      if (item < G * VD) out[(item / VD) * (HD + 2) + 2 + vd + item % VD] = val;
     }
-  }
-  __syncthreads();
-  // weighted V: thread per (head, dim)
-  const int rowf = attn_rowf(G, HD);
-  float* out = part + (((size_t)r * a.kv_heads + kv) * max_pages + page) * rowf;
-  // only the page's valid positions (other slots may hold anything)
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  const int kl = max(0, start - k0), kh = min(kKvPage - 1, pos - k0);
-  for (int i = tid; i < G * HD; i += kWg) {
-    const int g = i / HD, d = i - g * HD;
-    float acc = 0.f;
-    for (int k = kl; k <= kh; ++k) acc += sc[g][k] * __half2float(v_s[k * HD + d]);
-    out[g * (HD + 2) + 2 + d] = acc;
-  }
-  if (tid < G) {
-    out[tid * (HD + 2)] = red[tid][0];
-    out[tid * (HD + 2) + 1] = red[tid][1];
+    if (lane == 0)
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+        if (g < G && g % 4 == wave) {
+          out[g * (HD + 2)] = mrun[g];  // -inf for a segment without pages
+          out[g * (HD + 2) + 1] = lrun[g];
+        }
   }
 }
 
-// out row r, heads of kv head blockIdx.x: the pages' partials merged (chunk
-// weights exp(m_j - M), normalised by the merged sum).
+// out row r, heads of kv head blockIdx.x: the segments' partials merged
+// (weights exp(m_j - M), normalised by the merged sum).
 template <int HD>
-__global__ __launch_bounds__(kWg) void k_bd_merge(PfAttnArgs a, const float* part, int max_pages) {
+__global__ __launch_bounds__(kWg) void k_bd_merge(PfAttnArgs a, const float* part, int max_pages, int nseg) {
   __shared__ float w[8][64];
   __shared__ float inv[8];
   const int kv = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = a.heads / a.kv_heads;
-  const int pos = row_pos(a.kv, r);
-  const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-  const int j_lo = start / kKvPage, j_hi = pos / kKvPage;
-  const int n = j_hi - j_lo + 1;
+  const int n = nseg;
   const int rowf = attn_rowf(G, HD);
-  const float* base = part + (((size_t)r * a.kv_heads + kv) * max_pages + j_lo) * rowf;
+  const float* base = part + ((size_t)r * a.kv_heads + kv) * max_pages * rowf;
   for (int g = wave; g < G; g += 4) {
     float M = -INFINITY;
     for (int j = lane; j < n; j += 64) M = fmaxf(M, base[(size_t)j * rowf + g * (HD + 2)]);
     M = wave_max(M);
     float L = 0.f;
     for (int j = lane; j < n; j += 64) {
-      const float f = expf(base[(size_t)j * rowf + g * (HD + 2)] - M);
-      if (j < 64) w[g][j] = f;
+      const float mj = base[(size_t)j * rowf + g * (HD + 2)];
+      const float f = mj == -INFINITY ? 0.f : expf(mj - M);
+      w[g][j] = f;
       L += base[(size_t)j * rowf + g * (HD + 2) + 1] * f;
     }
     L = wave_sum(L);
@@ -889,10 +999,7 @@ __global__ __launch_bounds__(kWg) void k_bd_merge(PfAttnArgs a, const float* par
   for (int i = tid; i < G * HD; i += kWg) {
     const int g = i / HD, d = i - g * HD;
     float acc = 0.f;
-    for (int j = 0; j < n; ++j) {
-      const float f = j < 64 ? w[g][j] : 0.f;
-      acc += base[(size_t)j * rowf + g * (HD + 2) + 2 + d] * f;
-    }
+    for (int j = 0; j < n; ++j) acc += base[(size_t)j * rowf + g * (HD + 2) + 2 + d] * w[g][j];
     a.out[(size_t)r * a.ldo + (kv * G + g) * HD + d] = acc * inv[g];
   }
 }
@@ -1127,25 +1234,27 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
   a.rows = rows;
   const int G = a.heads / a.kv_heads;
   const int mp = a.kv.max_pages;
-  if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || mp > 64 ||
-      (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap)
+  // segments per row: enough (kv head, row, segment) workgroups to cover the
+  // device; with one segment the walk writes the output itself
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return hipErrorInvalidValue;
-  const dim3 g1(mp, a.kv_heads, rows), g2(a.kv_heads, rows);
+  const int nseg = std::max(1, std::min(mp, (2 * cus + rows * a.kv_heads - 1) / std::max(1, rows * a.kv_heads)));
+  if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || G * a.hd > 1536 || mp > 64 ||
+      (nseg > 1 && (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap))
+    return hipErrorInvalidValue;
+  const dim3 g1(a.kv_heads, rows, nseg), g2(a.kv_heads, rows);
+#define CHONK_BD_CASE(HH)                                                                     \
+  case HH:                                                                                    \
+    hipLaunchKernelGGL(k_bd_walk<HH>, g1, dim3(kWg), 0, s, a, part, mp, nseg);                \
+    if (nseg > 1) hipLaunchKernelGGL(k_bd_merge<HH>, g2, dim3(kWg), 0, s, a, part, mp, nseg); \
+    return hipGetLastError();
   switch (a.hd) {
-    case 64:
-      hipLaunchKernelGGL(k_bd_attn<64>, g1, dim3(kWg), 0, s, a, part, mp);
-      hipLaunchKernelGGL(k_bd_merge<64>, g2, dim3(kWg), 0, s, a, part, mp);
-      break;
-    case 128:
-      hipLaunchKernelGGL(k_bd_attn<128>, g1, dim3(kWg), 0, s, a, part, mp);
-      hipLaunchKernelGGL(k_bd_merge<128>, g2, dim3(kWg), 0, s, a, part, mp);
-      break;
-    case 256:
-      hipLaunchKernelGGL(k_bd_attn<256>, g1, dim3(kWg), 0, s, a, part, mp);
-      hipLaunchKernelGGL(k_bd_merge<256>, g2, dim3(kWg), 0, s, a, part, mp);
-      break;
+    CHONK_BD_CASE(64)
+    CHONK_BD_CASE(128)
+    CHONK_BD_CASE(256)
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+#undef CHONK_BD_CASE
 }
 }  // namespace chonk
