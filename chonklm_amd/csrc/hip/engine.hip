@@ -2601,11 +2601,17 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     at.kv16 = r.kv16;
     at.scale = c.scale;
     at.kv = r.kv;
-    if (pl.row_seq && c.hd >= 64 && lc.heads / lc.kv_heads <= 8 && kvs.max_pages <= 64)
-      HIP_OK(launch_bd_attn(at, T, b.part, P, s));
-    else
+    bool planes = false;  // the attention wrote the o-projection's operand planes
+    if (pl.row_seq && c.hd >= 64 && lc.heads / lc.kv_heads <= 8 && kvs.max_pages <= 64) {
+      at.oh = b.h;
+      at.ol = b.l;
+      at.oscale = b.xscale;
+      at.okpad = gemm_kpad(qdim);
+      HIP_OK(launch_bd_attn(at, T, b.part, P, s, &planes));
+    } else {
       HIP_OK(launch_pf_attn(at, T, s));
-    split(b.att, qdim, qdim, nullptr, T, PartSum{}, nullptr);
+    }
+    if (!planes) split(b.att, qdim, qdim, nullptr, T, PartSum{}, nullptr);
     const PartSum po = gemm(L.o, T, 0, P);
     // x += o (Gemma-3: x = clamp(x + RMSNorm(o) * post_norm)), then the ffn norm
     split(b.x, H, H, c.gemma ? L.pre_ffn_norm : L.post_norm, T, po, c.gemma ? L.post_norm : nullptr);

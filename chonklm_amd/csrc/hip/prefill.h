@@ -93,6 +93,13 @@ struct PfAttnArgs {
   int32_t rows;           // rows of the pass (set by the launcher)
   float scale;
   KvAddr kv;
+  // batched decode: the next GEMM's operand planes [rows][okpad] (hi, lo) and
+  // row scales, written instead of `out` when set and the rows are not split
+  // into segments (the output of attention needs no scaling: |x| <= max |V|)
+  _Float16* oh;
+  _Float16* ol;
+  float* oscale;
+  int32_t okpad;
 };
 
 // K padded for the GEMM's activation planes.
@@ -116,7 +123,8 @@ hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s);
 // Decode attention of rows with their own sequences (kv.row_seq) over paged
 // K/V: per-page partials in `part`, then a merge per (row, kv head).
-hipError_t launch_bd_attn(const PfAttnArgs& a, int rows, float* part, int64_t part_cap, hipStream_t s);
+// *planes: whether the launch wrote a.oh / a.ol / a.oscale (else a.out)
+hipError_t launch_bd_attn(const PfAttnArgs& a, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes);
 // Greedy id per row of logits [rows][vocab] (the reference's argmax ordering);
 // scratch holds 64 floats per row.
 hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* scratch, int32_t* out, hipStream_t s);

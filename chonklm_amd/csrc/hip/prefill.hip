@@ -936,7 +936,7 @@ __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int 
       for (int g = 0; g < 8; ++g)
         if (g < G && g % 4 == wave) lsum[g] = lrun[g];
     __syncthreads();
-    float* out = a.out + (size_t)r * a.ldo + kv * G * HD;
+    const size_t col = (size_t)kv * G * HD;
     for (int it = 0; it * PG < G * VD; ++it) {
       const int item = it * PG + pg;
       float val = 0.f;
@@ -945,7 +945,26 @@ __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int 
 #pragma unroll
         for (int k = 0; k < VD; ++k)
           if (g * VD + k == item) val = o[g][k];
-      if (item < G * VD) out[(item / VD) * HD + vd + item % VD] = val / lsum[item / VD];
+      if (item < G * VD) {
+        const size_t i = col + (item / VD) * HD + vd + item % VD;
+        const float y = val / lsum[item / VD];
+        if (a.oh) {
+          // the next GEMM's operand planes at scale 1 (x = hi + lo to ~2^-22)
+          const _Float16 h = (_Float16)y;
+          a.oh[(size_t)r * a.okpad + i] = h;
+          a.ol[(size_t)r * a.okpad + i] = (_Float16)(y - (float)h);
+        } else {
+          a.out[(size_t)r * a.ldo + i] = y;
+        }
+      }
+    }
+    if (a.oh && kv == 0) {
+      // the planes past the row's last column are zero; its scale is 1
+      for (int i = a.heads * HD + tid; i < a.okpad; i += kWg) {
+        a.oh[(size_t)r * a.okpad + i] = (_Float16)0.f;
+        a.ol[(size_t)r * a.okpad + i] = (_Float16)0.f;
+      }
+      if (tid == 0) a.oscale[r] = 1.0f;
     }
   } else {
     const int rowf = attn_rowf(G, HD);
@@ -1229,7 +1248,7 @@ hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* sc
 }  // namespace chonk
 
 namespace chonk {
-hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t part_cap, hipStream_t s) {
+hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes) {
   PfAttnArgs a = a0;
   a.rows = rows;
   const int G = a.heads / a.kv_heads;
@@ -1243,6 +1262,9 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
   if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || G * a.hd > 1536 || mp > 64 ||
       (nseg > 1 && (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap))
     return hipErrorInvalidValue;
+  if (nseg > 1) a.oh = nullptr;  // the merge writes a.out
+  if (a.oh && (!a.ol || !a.oscale || a.okpad < a.heads * a.hd)) return hipErrorInvalidValue;
+  *planes = a.oh != nullptr;
   const dim3 g1(a.kv_heads, rows, nseg), g2(a.kv_heads, rows);
 #define CHONK_BD_CASE(HH)                                                                     \
   case HH:                                                                                    \
