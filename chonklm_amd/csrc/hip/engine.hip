@@ -2587,8 +2587,13 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     r.eps = c.qk_eps;
     r.rope_inv = rope_table(e, c.layer[i].theta, c.hd);
     r.kv = kv_addr(i);
-    HIP_OK(launch_pf_rope_kv(r, T, s));
-    if (i == c.layers - 1 && !logits) break;  // only the last layer's K/V are needed from it
+    const bool last_kv = i == c.layers - 1 && !logits;  // only the last layer's K/V are needed from it
+    // decode batches: the page-walking attention (one workgroup per (kv head,
+    // row) walking all of its pages also does the rotary/K-V write)
+    const bool walk = pl.row_seq && c.hd >= 64 && lc.heads / lc.kv_heads <= 8 && kvs.max_pages <= 64;
+    const bool fuse_rope = walk && !last_kv && bd_attn_segments(T, lc.kv_heads, kvs.max_pages) == 1;
+    if (!fuse_rope) HIP_OK(launch_pf_rope_kv(r, T, s));
+    if (last_kv) break;
     PfAttnArgs at{};
     at.qkv = b.qkv;
     at.ld = ldqkv;
@@ -2602,12 +2607,12 @@ void run_rows(chonk_engine* e, const RowBufs& b, const RowKv& kvs, const RowPlac
     at.scale = c.scale;
     at.kv = r.kv;
     bool planes = false;  // the attention wrote the o-projection's operand planes
-    if (pl.row_seq && c.hd >= 64 && lc.heads / lc.kv_heads <= 8 && kvs.max_pages <= 64) {
+    if (walk) {
       at.oh = b.h;
       at.ol = b.l;
       at.oscale = b.xscale;
       at.okpad = gemm_kpad(qdim);
-      HIP_OK(launch_bd_attn(at, T, b.part, P, s, &planes));
+      HIP_OK(launch_bd_attn(at, T, b.part, P, s, &planes, fuse_rope ? &r : nullptr));
     } else {
       HIP_OK(launch_pf_attn(at, T, s));
     }

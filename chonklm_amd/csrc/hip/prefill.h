@@ -123,8 +123,14 @@ hipError_t launch_pf_rope_kv(const PfRopeArgs& a, int rows, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s);
 // Decode attention of rows with their own sequences (kv.row_seq) over paged
 // K/V: per-page partials in `part`, then a merge per (row, kv head).
-// *planes: whether the launch wrote a.oh / a.ol / a.oscale (else a.out)
-hipError_t launch_bd_attn(const PfAttnArgs& a, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes);
+// Segments per row of the batched decode attention (1: one workgroup walks all
+// of a (row, kv head)'s pages; 0: no device).
+int bd_attn_segments(int rows, int kv_heads, int max_pages);
+// *planes: whether the launch wrote a.oh / a.ol / a.oscale (else a.out). With
+// `rope` (only when bd_attn_segments is 1) the attention also does that
+// launch's rotary/K-V write, reading q, k and v from the projections.
+hipError_t launch_bd_attn(const PfAttnArgs& a, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes,
+                          const PfRopeArgs* rope);
 // Greedy id per row of logits [rows][vocab] (the reference's argmax ordering);
 // scratch holds 64 floats per row.
 hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* scratch, int32_t* out, hipStream_t s);

@@ -773,7 +773,8 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
 // workgroup writes the attention output; otherwise a partial [max, sum,
 // acc[hd]] per head for k_bd_merge.
 template <int HD>
-__global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg) {
+__global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg, PfRopeArgs ra,
+                                               int rope) {
   constexpr int DPT = HD / 4;  // K dims per lane
   constexpr int NKV = DPT / 8;
   constexpr int VD = HD >= 256 ? 4 : 2, VW = VD / 2;
@@ -908,15 +909,89 @@ __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int 
   };
   uint4 ka[NKV], kb2[NKV];
   uint32_t va[NP][VW], vb2[NP][VW];
-  // q first: its loads complete before the page's, which stay in flight
-  float qv[6];
+  if (rope) {
+    // this (row, kv head)'s share of the rotary/K-V write (k_pf_rope_kv's
+    // arithmetic): the G q heads, k and v gathered from the projections'
+    // partial sums are G + 2 items over the waves; q goes to LDS, k and v to
+    // the cache. The first page is requested first unless it is the newest,
+    // which is read only after the barrier below publishes the new row.
+    if (p_lo < p_hi && p_lo < pos / kKvPage) load(p_lo, ka, va);
+    constexpr int NPR = 2;  // pairs per lane: head_dim <= 256
+    constexpr int HALF = HD / 2;
+    int ia[NPR], ib[NPR];
 #pragma unroll
-  for (int c = 0; c < 6; ++c) qv[c] = tid + kWg * c < G * HD ? q[tid + kWg * c] : 0.f;
-  if (p_lo < p_hi) load(p_lo, ka, va);
+    for (int j = 0; j < NPR; ++j) {
+      const int d = min(lane + 64 * j, HALF - 1);
+      ia[j] = ra.interleaved ? 2 * d : d;
+      ib[j] = ra.interleaved ? 2 * d + 1 : d + HALF;
+    }
+    const size_t base = kv_row(ra.kv, ra.kv_heads, HD, seq, kv, pos);
+    for (int it = wave; it < G + 2; it += 4) {
+      if (it <= G) {
+        const bool is_k = it == G;
+        const PartSum& P = is_k ? ra.pk : ra.pq;
+        const int pcol = is_k ? kv * HD : (kv * G + it) * HD;
+        const int col = is_k ? ra.heads * HD + kv * HD : (kv * G + it) * HD;
+        const float* row = ra.qkv + (size_t)r * ra.ld;
+        float x0[NPR], x1[NPR];
 #pragma unroll
-  for (int c = 0; c < 6; ++c)
-    if (tid + kWg * c < G * HD) q_s[tid + kWg * c] = qv[c];
-  __syncthreads();
+        for (int j = 0; j < NPR; ++j) {
+          x0[j] = P.p ? part_at(P, r, pcol + ia[j]) : row[col + ia[j]];
+          x1[j] = P.p ? part_at(P, r, pcol + ib[j]) : row[col + ib[j]];
+        }
+        float rn = 1.0f;
+        if (ra.qn_w) {
+          float ss = 0.f;
+#pragma unroll
+          for (int j = 0; j < NPR; ++j)
+            if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
+          ss = wave_sum(ss);
+          rn = 1.0f / sqrtf(ss / (float)HD + ra.eps);
+        }
+        const float* w = is_k ? ra.kn_w : ra.qn_w;
+#pragma unroll
+        for (int j = 0; j < NPR; ++j) {
+          const int d = lane + 64 * j;
+          if (d >= HALF) continue;
+          float v0 = x0[j], v1 = x1[j];
+          if (ra.qn_w) {
+            v0 = __fmul_rn(__fmul_rn(v0, rn), w[ia[j]]);
+            v1 = __fmul_rn(__fmul_rn(v1, rn), w[ib[j]]);
+          }
+          const float ang = __fmul_rn((float)pos, ra.rope_inv[d]);
+          const float co = cosf(ang), si = sinf(ang);
+          const float y0 = __fsub_rn(__fmul_rn(v0, co), __fmul_rn(v1, si));
+          const float y1 = __fadd_rn(__fmul_rn(v0, si), __fmul_rn(v1, co));
+          if (is_k) {
+            ((__half*)ra.kv.kc)[base + ia[j]] = __float2half_rn(y0);
+            ((__half*)ra.kv.kc)[base + ib[j]] = __float2half_rn(y1);
+          } else {
+            q_s[it * HD + ia[j]] = y0;
+            q_s[it * HD + ib[j]] = y1;
+          }
+        }
+      } else {
+        const float* row = ra.qkv + (size_t)r * ra.ld;
+        const int vcol = (ra.heads + ra.kv_heads) * HD + kv * HD;
+        for (int d = lane; d < HD; d += 64) {
+          const float v = ra.pv.p ? part_at(ra.pv, r, kv * HD + d) : row[vcol + d];
+          ((__half*)ra.kv.vc)[base + d] = __float2half_rn(v);
+        }
+      }
+    }
+    __syncthreads();  // q in LDS; the new K/V row visible to this workgroup's loads
+    if (p_lo < p_hi && p_lo >= pos / kKvPage) load(p_lo, ka, va);
+  } else {
+    // q first: its loads complete before the page's, which stay in flight
+    float qv[6];
+#pragma unroll
+    for (int c = 0; c < 6; ++c) qv[c] = tid + kWg * c < G * HD ? q[tid + kWg * c] : 0.f;
+    if (p_lo < p_hi) load(p_lo, ka, va);
+#pragma unroll
+    for (int c = 0; c < 6; ++c)
+      if (tid + kWg * c < G * HD) q_s[tid + kWg * c] = qv[c];
+    __syncthreads();
+  }
   for (int j = p_lo; j < p_hi; j += 2) {
     if (j + 1 < p_hi) load(j + 1, kb2, vb2);
     page(j, ka, va);
@@ -1248,17 +1323,25 @@ hipError_t launch_row_argmax(const float* logits, int vocab, int rows, float* sc
 }  // namespace chonk
 
 namespace chonk {
-hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes) {
+int bd_attn_segments(int rows, int kv_heads, int max_pages) {
+  // enough (kv head, row, segment) workgroups to cover the device; with one
+  // segment the walk writes the output (and may do the rotary/K-V write)
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return std::max(1, std::min(max_pages, (2 * cus + rows * kv_heads - 1) / std::max(1, rows * kv_heads)));
+}
+
+hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t part_cap, hipStream_t s, bool* planes,
+                          const PfRopeArgs* rope) {
   PfAttnArgs a = a0;
   a.rows = rows;
   const int G = a.heads / a.kv_heads;
   const int mp = a.kv.max_pages;
-  // segments per row: enough (kv head, row, segment) workgroups to cover the
-  // device; with one segment the walk writes the output itself
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return hipErrorInvalidValue;
-  const int nseg = std::max(1, std::min(mp, (2 * cus + rows * a.kv_heads - 1) / std::max(1, rows * a.kv_heads)));
+  const int nseg = bd_attn_segments(rows, a.kv_heads, mp);
+  if (nseg <= 0 || (rope && nseg != 1)) return hipErrorInvalidValue;
+  PfRopeArgs ra{};
+  if (rope) ra = *rope;
   if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || G * a.hd > 1536 || mp > 64 ||
       (nseg > 1 && (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap))
     return hipErrorInvalidValue;
@@ -1268,7 +1351,7 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
   const dim3 g1(a.kv_heads, rows, nseg), g2(a.kv_heads, rows);
 #define CHONK_BD_CASE(HH)                                                                     \
   case HH:                                                                                    \
-    hipLaunchKernelGGL(k_bd_walk<HH>, g1, dim3(kWg), 0, s, a, part, mp, nseg);                \
+    hipLaunchKernelGGL(k_bd_walk<HH>, g1, dim3(kWg), 0, s, a, part, mp, nseg, ra, rope ? 1 : 0); \
     if (nseg > 1) hipLaunchKernelGGL(k_bd_merge<HH>, g2, dim3(kWg), 0, s, a, part, mp, nseg); \
     return hipGetLastError();
   switch (a.hd) {
