@@ -23,6 +23,7 @@ Also reported:
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -238,6 +239,9 @@ def main() -> int:
                     help="only the batched-decode measurement (profiling runs: per-step kernel time is the "
                          "difference of two runs with different --batched-steps)")
     ap.add_argument("--batched-steps", type=int, default=32)
+    ap.add_argument("--prompt-tokens", type=int, default=0,
+                    help="override the workload's prompt length (with --fake-prefill the K/V rows are filled "
+                         "synthetically): contexts past 8192 positions run the chunked decode attention")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first run 4 device-to-device copies of MIB MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -265,6 +269,8 @@ def main() -> int:
         del src, dst
 
     w = WORKLOADS[args.workload]
+    if args.prompt_tokens > 0:
+        w = dataclasses.replace(w, prompt_tokens=args.prompt_tokens)
     t_build = time.perf_counter()
     path = build_model(args.workload, Path(args.model_cache))
     build_s = time.perf_counter() - t_build
