@@ -74,7 +74,7 @@ def kernel_symbol(cls: str, info: dict) -> str:
     kv16 = "true" if info.get("kv_dtype", 0) == 0 else "false"  # CHONK_KV_F16 == 0
     # the engine's rule for the register-resident decode attention (attn_dec_supported)
     dec = (kv16 == "true" and hd in (64, 128, 256) and 1 <= g <= 8 and g * hd <= 1536
-           and (info["context"] + 63) // 64 <= 128 and os.environ.get("CHONK_ATTN") != "chunked")
+           and (info["context"] + 63) // 64 <= 128 * 16 and os.environ.get("CHONK_ATTN") != "chunked")
     attn = f"k_attn_dec<{g}, {hd}>" if dec else f"k_attention<{g}, {kv16}>"
     if os.environ.get("CHONK_MV") == "generic":
         mv = {"gateup": "k_mv_swiglu", "qkv": "k_mv_store", "oproj": "k_mv_add", "down": "k_mv_add"}

@@ -42,6 +42,7 @@ namespace {
 
 constexpr int kDecChunk = 64;  // positions per workgroup
 constexpr int kDecWave = 16;   // positions per wave
+constexpr int kDecSubMax = 16; // sub-chunks per workgroup (128 workgroups per kv head merge)
 
 __device__ __forceinline__ float2 ldg2f(const float2* p) {
   const uint2 v = ldg2(p);
@@ -79,7 +80,9 @@ __device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((u
 // Chunk rows (a.tpart, [kv][nchunk][rowf] tagged words): per head [max, sum,
 // acc[HD]], each word {f32, u32 tag}; the tag of a launch is the kv head's
 // epoch a.cnt[kv], which the newest chunk advances when it is done.
-template <int G, int HD>
+// WALK: the workgroup walks a.sub sub-chunks (long contexts); otherwise its
+// chunk is one sub-chunk and the code is that of a single chunk.
+template <int G, int HD, bool WALK>
 __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   extern __shared__ __align__(16) float sm[];
   constexpr int HALF = HD / 2;
@@ -118,7 +121,8 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   const int pos = ld_scalar(&st->pos);
   const int stopped = ld_scalar(&st->stopped);
   const uint32_t tag = ld_scalar(&a.cnt[kv]);
-  const int t_lo = c * kDecChunk;
+  const int span = WALK ? kDecChunk * a.sub : kDecChunk;  // positions of this workgroup's chunk
+  const int t_lo = c * span;
   const int kp = kDecWave * wave + (lane >> 2);  // this lane's K position in the chunk
   const int kd0 = (lane & 3) * DPT;
   const int pg = lane >> LDW;                    // this lane's V positions: pg + PG * j
@@ -127,13 +131,16 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   const __half* vc = (const __half*)a.vc + (size_t)kv * a.ctx * HD;
   uint4 kr[NKV];
   uint32_t vr[NP][VW];
-  auto load_kv = [&]() {
-    const int tk = min(t_lo + kp, a.ctx - 1);
+  // K / V rows of the 64 positions from t0
+  auto load_k = [&](int t0) {
+    const int tk = min(t0 + kp, a.ctx - 1);
 #pragma unroll
     for (int v = 0; v < NKV; ++v) kr[v] = ldg4(kc + (size_t)tk * HD + kd0 + 8 * v);
+  };
+  auto load_v = [&](int t0) {
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-      const __half* p = vc + (size_t)min(t_lo + pg + PG * j, a.ctx - 1) * HD + vd;
+      const __half* p = vc + (size_t)min(t0 + pg + PG * j, a.ctx - 1) * HD + vd;
       if constexpr (VW == 1) {
         vr[j][0] = ldg1(p);
       } else {
@@ -143,7 +150,11 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       }
     }
   };
-  if (a.spec_kv) load_kv();
+  auto load_kv = [&](int t0) {
+    load_k(t0);
+    load_v(t0);
+  };
+  if (a.spec_kv) load_kv(t_lo);
   lds_dma(a.qkv + (size_t)kv * G * HD, q_s, G * HD);
   lds_dma(a.qkv + (size_t)a.heads * HD + (size_t)kv * HD, kx, HD);
   lds_dma(a.qkv + (size_t)(a.heads + a.kv_heads) * HD + (size_t)kv * HD, vx, HD);
@@ -163,9 +174,9 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     }
   }
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-  const int c_lo = start / kDecChunk, c_hi = pos / kDecChunk;
+  const int c_lo = start / span, c_hi = pos / span;
   const bool active = !stopped && pos < a.ctx && c >= c_lo && c <= c_hi;
-  if (active && !a.spec_kv) load_kv();
+  if (active && !a.spec_kv) load_kv(t_lo);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   CHONK_MV_T(tr, 1);
@@ -249,87 +260,115 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   }
   __syncthreads();
 
-  // C: scores over the cached positions [start, pos) (the new position is
-  // not in the registers: the merge adds it), the chunk maximum per head,
-  // then the weights exp(s - max) into ew
-  const int tk = t_lo + kp;
-  const bool kvalid = tk >= start && tk < pos;
-  float s[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) s[g] = 0.f;
-#pragma unroll
-  for (int v = 0; v < NKV; ++v) {
-    const uint32_t w[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float4 q0 = *(const float4*)(qn + g * HD + kd0 + 8 * v);
-      const float4 q1 = *(const float4*)(qn + g * HD + kd0 + 8 * v + 4);
-      s[g] = fmaf(q0.x, h2f(w[0]), s[g]);
-      s[g] = fmaf(q0.y, h2f(w[0] >> 16), s[g]);
-      s[g] = fmaf(q0.z, h2f(w[1]), s[g]);
-      s[g] = fmaf(q0.w, h2f(w[1] >> 16), s[g]);
-      s[g] = fmaf(q1.x, h2f(w[2]), s[g]);
-      s[g] = fmaf(q1.y, h2f(w[2] >> 16), s[g]);
-      s[g] = fmaf(q1.z, h2f(w[3]), s[g]);
-      s[g] = fmaf(q1.w, h2f(w[3] >> 16), s[g]);
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float sc = group_sum<4>(s[g]);  // (all lanes take part in the DPP steps)
-    s[g] = kvalid ? sc * a.scale : -INFINITY;
-    const float mw = wave_max(s[g]);
-    if (lane == 0) wmx[wave * G + g] = mw;
-  }
-  __syncthreads();
-  float mx[G];
+  // C: over the workgroup's sub-chunks of 64 positions that hold cached
+  // positions of [start, pos) (the new position is not in the registers: the
+  // merge adds it): scores, the sub-chunk maximum per head, the weights
+  // exp(s - max) into ew, weighted V; the softmax runs online over the
+  // sub-chunks (running maximum and sum, accumulators rescaled when the
+  // maximum grows). The next sub-chunk's K rows are requested once the scores
+  // are formed, its V rows once the weighted sum is done.
+  const int s_first = max(0, (start - t_lo) / kDecChunk);
+  // (-1 when no cached position of [start, pos) lies in this chunk)
+  const int s_last = pos > t_lo && start < pos ? min(WALK ? a.sub - 1 : 0, (pos - 1 - t_lo) / kDecChunk) : -1;
   const int ei = (kp % PG) * NP + kp / PG;
+  float mx[G], lsum[G], o[G][VD];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    mx[g] = fmaxf(fmaxf(wmx[g], wmx[G + g]), fmaxf(wmx[2 * G + g], wmx[3 * G + g]));
-    const float e = kvalid ? exp_fast(s[g] - mx[g]) : 0.f;
-    if ((lane & 3) == 0) ew[g * kDecChunk + ei] = e;
-  }
-  __syncthreads();
-
-  // weighted V over the chunk's 64 positions: rows outside [start, pos) carry
-  // weight 0, and their registers are cleared so that no unwritten value
-  // reaches the sum
-  if (t_lo < start || t_lo + kDecChunk > pos) {
-#pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      const int p = t_lo + pg + PG * j;
-      if (p < start || p >= pos)
-#pragma unroll
-        for (int t = 0; t < VW; ++t) vr[j][t] = 0u;
-    }
-  }
-  float o[G][VD];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
+    mx[g] = -INFINITY;
+    lsum[g] = 0.f;  // wave g % 4's running sum of head g
 #pragma unroll
     for (int k = 0; k < VD; ++k) o[g][k] = 0.f;
+  }
+  if (WALK && s_first > 0 && s_first <= s_last) load_kv(t_lo + kDecChunk * s_first);  // (a window start)
+  for (int sc = s_first; sc <= s_last; ++sc) {
+    const int t0 = t_lo + kDecChunk * sc;
+    const int tk = t0 + kp;
+    const bool kvalid = tk >= start && tk < pos;
+    float s[G];
 #pragma unroll
-  for (int j4 = 0; j4 < NP / 4; ++j4) {
-    float4 w4[G];
+    for (int g = 0; g < G; ++g) s[g] = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) w4[g] = *(const float4*)(ew + g * kDecChunk + pg * NP + 4 * j4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * j4 + i;
-      float vf[VD];
-#pragma unroll
-      for (int t = 0; t < VW; ++t) {
-        vf[2 * t] = h2f(vr[j][t]);
-        vf[2 * t + 1] = h2f(vr[j][t] >> 16);
-      }
+    for (int v = 0; v < NKV; ++v) {
+      const uint32_t w[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float wt = i == 0 ? w4[g].x : i == 1 ? w4[g].y : i == 2 ? w4[g].z : w4[g].w;
-#pragma unroll
-        for (int k = 0; k < VD; ++k) o[g][k] = fmaf(wt, vf[k], o[g][k]);
+        const float4 q0 = *(const float4*)(qn + g * HD + kd0 + 8 * v);
+        const float4 q1 = *(const float4*)(qn + g * HD + kd0 + 8 * v + 4);
+        s[g] = fmaf(q0.x, h2f(w[0]), s[g]);
+        s[g] = fmaf(q0.y, h2f(w[0] >> 16), s[g]);
+        s[g] = fmaf(q0.z, h2f(w[1]), s[g]);
+        s[g] = fmaf(q0.w, h2f(w[1] >> 16), s[g]);
+        s[g] = fmaf(q1.x, h2f(w[2]), s[g]);
+        s[g] = fmaf(q1.y, h2f(w[2] >> 16), s[g]);
+        s[g] = fmaf(q1.z, h2f(w[3]), s[g]);
+        s[g] = fmaf(q1.w, h2f(w[3] >> 16), s[g]);
       }
     }
+    if (WALK && sc < s_last) load_k(t0 + kDecChunk);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sc4 = group_sum<4>(s[g]);  // (all lanes take part in the DPP steps)
+      s[g] = kvalid ? sc4 * a.scale : -INFINITY;
+      const float mw = wave_max(s[g]);
+      if (lane == 0) wmx[wave * G + g] = mw;
+    }
+    __syncthreads();  // the maxima (and the previous sub-chunk's weights are consumed)
+    float alpha[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      // finite: the sub-chunk holds a cached position
+      const float mp = fmaxf(fmaxf(wmx[g], wmx[G + g]), fmaxf(wmx[2 * G + g], wmx[3 * G + g]));
+      const float mn = WALK ? fmaxf(mx[g], mp) : mp;
+      if constexpr (WALK) alpha[g] = exp_fast(mx[g] - mn);  // 0 on the first sub-chunk
+      mx[g] = mn;
+      const float e = kvalid ? exp_fast(s[g] - mn) : 0.f;
+      if ((lane & 3) == 0) ew[g * kDecChunk + ei] = e;
+    }
+    __syncthreads();
+    // rows outside [start, pos) carry weight 0, and their registers are
+    // cleared so that no unwritten value reaches the sum
+    if (t0 < start || t0 + kDecChunk > pos) {
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const int p = t0 + pg + PG * j;
+        if (p < start || p >= pos)
+#pragma unroll
+          for (int t = 0; t < VW; ++t) vr[j][t] = 0u;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if constexpr (WALK) {
+        if (g % 4 == wave) lsum[g] = lsum[g] * alpha[g] + wave_sum(ew[g * kDecChunk + lane]);
+#pragma unroll
+        for (int k = 0; k < VD; ++k) o[g][k] *= alpha[g];
+      } else {
+        if (g % 4 == wave) lsum[g] = wave_sum(ew[g * kDecChunk + lane]);
+      }
+    }
+#pragma unroll
+    for (int j4 = 0; j4 < NP / 4; ++j4) {
+      float4 w4[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) w4[g] = *(const float4*)(ew + g * kDecChunk + pg * NP + 4 * j4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * j4 + i;
+        float vf[VD];
+#pragma unroll
+        for (int t = 0; t < VW; ++t) {
+          vf[2 * t] = h2f(vr[j][t]);
+          vf[2 * t + 1] = h2f(vr[j][t] >> 16);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float wt = i == 0 ? w4[g].x : i == 1 ? w4[g].y : i == 2 ? w4[g].z : w4[g].w;
+#pragma unroll
+          for (int k = 0; k < VD; ++k) o[g][k] = fmaf(wt, vf[k], o[g][k]);
+        }
+      }
+    }
+    if (WALK && sc < s_last) load_v(t0 + kDecChunk);
   }
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -357,10 +396,9 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g)
     if (g % 4 == wave) {
-      const float l = wave_sum(ew[g * kDecChunk + lane]);
       if (lane == 0) {
-        tag_put(row + g * (HD + 2), mx[g], tag);
-        tag_put(row + g * (HD + 2) + 1, l, tag);
+        tag_put(row + g * (HD + 2), mx[g], tag);  // -inf when no cached position
+        tag_put(row + g * (HD + 2) + 1, lsum[g], tag);
       }
     }
   CHONK_MV_T(tr, 3);
@@ -448,7 +486,12 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
 bool attn_dec_supported(int group, int hd, int ctx, int kv_f16) {
   // (group 8 at head_dim 256 would spill its score operands)
   return kv_f16 && (hd == 64 || hd == 128 || hd == 256) && group >= 1 && group <= 8 && group * hd <= 1536 &&
-         (ctx + kDecChunk - 1) / kDecChunk <= 128;
+         (ctx + kDecChunk - 1) / kDecChunk <= 128 * kDecSubMax;
+}
+
+int attn_dec_sub(int ctx, int per_head) {
+  const int cap = std::max(1, std::min(128, per_head));
+  return ((ctx + kDecChunk - 1) / kDecChunk + cap - 1) / cap;
 }
 
 int attn_dec_chunk() { return kDecChunk; }
@@ -472,15 +515,15 @@ __global__ __launch_bounds__(kWg) void k_rope_cs(const float* inv, int half, int
 }
 
 template <int G, int HD>
-const void* dec_fn() {
-  return (const void*)k_attn_dec<G, HD>;
+const void* dec_fn(bool walk) {
+  return walk ? (const void*)k_attn_dec<G, HD, true> : (const void*)k_attn_dec<G, HD, false>;
 }
-const void* dec_kernel(int group, int hd) {
+const void* dec_kernel(int group, int hd, bool walk) {
 #define CHONK_DEC_FN(GG)                              \
   if (group == GG) {                                  \
-    if (hd == 64) return dec_fn<GG, 64>();            \
-    if (hd == 128) return dec_fn<GG, 128>();          \
-    if (hd == 256) return dec_fn<GG, 256>();          \
+    if (hd == 64) return dec_fn<GG, 64>(walk);        \
+    if (hd == 128) return dec_fn<GG, 128>(walk);      \
+    if (hd == 256) return dec_fn<GG, 256>(walk);      \
   }
   CHONK_DEC_FN(1)
   CHONK_DEC_FN(2)
@@ -495,8 +538,8 @@ const void* dec_kernel(int group, int hd) {
 }
 }  // namespace
 
-int attn_dec_resident(int device, int group, int hd, size_t shmem) {
-  const void* f = dec_kernel(group, hd);
+int attn_dec_resident(int device, int group, int hd, size_t shmem, bool walk) {
+  const void* f = dec_kernel(group, hd, walk);
   if (!f) return 0;
   int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, kWg, shmem) != hipSuccess) return 0;
@@ -514,7 +557,13 @@ hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s) {
   const int group = a.heads / a.kv_heads;
   const dim3 grid(a.kv_heads, a.nchunk);
 #define CHONK_DEC_CASE(GG, HH) \
-  if (group == GG && a.hd == HH) { hipLaunchKernelGGL((k_attn_dec<GG, HH>), grid, dim3(kWg), shmem, s, a); return hipGetLastError(); }
+  if (group == GG && a.hd == HH) {                                                                 \
+    if (a.sub > 1)                                                                                 \
+      hipLaunchKernelGGL((k_attn_dec<GG, HH, true>), grid, dim3(kWg), shmem, s, a);                 \
+    else                                                                                           \
+      hipLaunchKernelGGL((k_attn_dec<GG, HH, false>), grid, dim3(kWg), shmem, s, a);                \
+    return hipGetLastError();                                                                      \
+  }
 #define CHONK_DEC_G(GG) CHONK_DEC_CASE(GG, 64) CHONK_DEC_CASE(GG, 128) CHONK_DEC_CASE(GG, 256)
   CHONK_DEC_G(1)
   CHONK_DEC_G(2)

@@ -542,7 +542,8 @@ struct chonk_engine {
   uint32_t *pen_bits = nullptr, *seen_bits = nullptr;
   int groups = 0, chunk = 0, nchunk = 0;
   bool dec_attn = false;          // per-phase attention: k_attn_dec over dnchunk chunks
-  int dnchunk = 0;
+  int dnchunk = 0;                // workgroup chunks of dsub x 64 positions
+  int dsub = 1;
   tagged_t* dpart = nullptr;      // k_attn_dec chunk rows
   std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
   std::vector<std::pair<uint32_t, float2*>> rope_cs;     // theta -> [ctx][hd/2] (cos, sin)
@@ -1229,6 +1230,7 @@ void build_steps(chonk_engine* e) {
         t.rope_cs = rope_cs_table(e, c.layer[i].theta, c.hd);
         t.chunk = attn_dec_chunk();
         t.nchunk = e->dnchunk;
+        t.sub = e->dsub;
         t.merge_floats = attn_merge_floats(G, c.hd, e->dnchunk);
         L.shmem = attn_dec_shared_bytes(G, c.hd, e->dnchunk);
         L.grid = lc.kv_heads * e->dnchunk;
@@ -1425,6 +1427,7 @@ bool build_step(chonk_engine* e) {
   const bool kv16 = e->kv_elem == 2;
   if (c.gpt) return false;  // the persistent step runs the llama-family layer only
   if (c.openelm || c.lfm || c.granite) return false;  // and one head geometry, attention in every layer
+  if (e->dsub > 1) return false;  // contexts whose decode attention walks sub-chunks
   if (!step_supported(G, kv16)) return false;
   int cus = 0;
   HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
@@ -1983,12 +1986,25 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   {
     const char* av = std::getenv("CHONK_ATTN");
     e->dec_attn = !(av && std::strcmp(av, "chunked") == 0);
-    e->dnchunk = (c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk();
+    e->dsub = attn_dec_sub(c.ctx, 128);
+    if (e->dsub > 1) {
+      // long contexts: each workgroup walks several 64-position chunks, as many
+      // workgroups per kv head as stay resident together with the walking kernel
+      int per_head = 128;
+      for (const LayerCfg& lc : c.layer) {
+        if (lc.conv || lc.mamba) continue;
+        const int lg = lc.heads / lc.kv_heads;
+        per_head = std::min(per_head, attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, 128), true) /
+                                          std::max(1, lc.kv_heads));
+      }
+      e->dsub = attn_dec_sub(c.ctx, per_head);
+    }
+    e->dnchunk = ((c.ctx + attn_dec_chunk() - 1) / attn_dec_chunk() + e->dsub - 1) / e->dsub;
     for (const LayerCfg& lc : c.layer) {
       const int lg = lc.heads / lc.kv_heads;
       if (lc.conv || lc.mamba) continue;
       if (e->dec_attn && (!attn_dec_supported(lg, c.hd, c.ctx, e->kv_elem == 2 ? 1 : 0) ||
-                          attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, e->dnchunk)) <
+                          attn_dec_resident(e->device, lg, c.hd, attn_dec_shared_bytes(lg, c.hd, e->dnchunk), e->dsub > 1) <
                               lc.kv_heads * e->dnchunk))
         e->dec_attn = false;
     }

@@ -129,6 +129,7 @@ struct AttnArgs {
   int32_t interleaved, kv_f16;
   int32_t merge_floats;   // LDS floats available for staging chunk partials
   int32_t spec_kv;        // request the chunk's K/V before the position is known
+  int32_t sub;            // k_attn_dec: 64-position sub-chunks walked by one workgroup
   int32_t tpp;            // threads per position in the score phase (power of two)
   int32_t variant;        // 0: k_attention; 1: k_attn_dec (fp16 cache, 64-position chunks)
   float eps, scale;
@@ -377,10 +378,13 @@ hipError_t launch_ssm(const SsmArgs& a, hipStream_t s);
 // chunks of attn_dec_chunk() positions over the context.
 bool attn_dec_supported(int group, int hd, int ctx, int kv_f16);
 int attn_dec_chunk();
+// 64-position sub-chunks per k_attn_dec workgroup at a context, with at most
+// min(128, per_head) workgroups per kv head.
+int attn_dec_sub(int ctx, int per_head);
 size_t attn_dec_shared_bytes(int group, int hd, int nchunk);
 // Workgroups of k_attn_dec that fit on the device at once (its active chunks
 // wait for each other, so the whole grid must be resident).
-int attn_dec_resident(int device, int group, int hd, size_t shmem);
+int attn_dec_resident(int device, int group, int hd, size_t shmem, bool walk);
 hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s);
 // cs[p][d] = (cos, sin)(p * inv[d]) for p < ctx, d < half.
 hipError_t launch_rope_cs(const float* inv, int half, int ctx, float2* cs, hipStream_t s);

@@ -289,3 +289,33 @@ def test_batched_walk_with_interleaved_rope_matches_oracle(synth):
         cur = nxt
     b.close()
     loaded.engine.dispose()
+
+
+def test_decode_attention_walks_sub_chunks_at_long_context(synth):
+    """The Qwen3-0.6B shape with a 9000-position cache: 141 chunks of 64 positions are more
+    than one workgroup per chunk can merge, so each workgroup walks two 64-position sub-chunks
+    with an online softmax (running maximum and sum, accumulators rescaled). Positions where a
+    workgroup's second sub-chunk is empty, partial and full, and where the newest workgroup
+    holds only the new position; logits within 1e-3 of the oracle and identical ids."""
+    name = "qwen3-0.6b-q4_k_m"
+    w = WORKLOADS[name]
+    path = synth(name)
+    ctx = 9000
+    md = w.model_def(path)
+    md.max_context = ctx
+    loaded = load_llama_wgsl_model(md)
+    eng = loaded.engine
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
+    tok = 23
+    for pos in (100, 8000, 8063, 8064, 8191, 8960, 8998):
+        eng.fake_context(pos, seed=pos)
+        ref.fake_context(pos, seed=pos)
+        for i in range(2 if pos + 2 <= ctx else 1):
+            a = eng.run_token(tok, True)
+            b = ref.run_token(tok, True)
+            e = rel_err(eng.read_logits(), ref.logits())
+            assert e <= 1e-3, f"position {pos + i}: logits rel err {e:.3e}"
+            assert a == b, f"position {pos + i}: token {a} != {b}"
+            tok = a
+    eng.dispose()
+    ref.close()
