@@ -75,7 +75,8 @@ def kernel_symbol(cls: str, info: dict) -> str:
     # the engine's rule for the register-resident decode attention (attn_dec_supported)
     dec = (kv16 == "true" and hd in (64, 128, 256) and 1 <= g <= 8 and g * hd <= 1536
            and (info["context"] + 63) // 64 <= 128 * 16 and os.environ.get("CHONK_ATTN") != "chunked")
-    attn = f"k_attn_dec<{g}, {hd}>" if dec else f"k_attention<{g}, {kv16}>"
+    walk = "true" if (info["context"] + 63) // 64 > 128 else "false"  # sub-chunks per workgroup (long contexts)
+    attn = f"k_attn_dec<{g}, {hd}, {walk}>" if dec else f"k_attention<{g}, {kv16}>"
     if os.environ.get("CHONK_MV") == "generic":
         mv = {"gateup": "k_mv_swiglu", "qkv": "k_mv_store", "oproj": "k_mv_add", "down": "k_mv_add"}
     elif info.get("architecture") == 3:  # gpt2 row kernels (LayerNorm prologues, biases)
