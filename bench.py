@@ -89,7 +89,7 @@ def kernel_symbol(cls: str, info: dict) -> str:
             mv["outproj"] = "k_mvr_add_gate"
     if info["ffn"] > 4096 and "down" in mv and os.environ.get("CHONK_MV") != "generic":
         mv["down"] = "k_mvr_add_bias_wide"  # rows above 4096 stage the input through LDS
-    return {"step": f"k_step<{g}, {kv16}>", "attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
+    return {"attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
 
 
 def host_cpus() -> int:
@@ -225,7 +225,7 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3-0.6b-q4_k_m")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-rounds", type=int, default=1,
+    ap.add_argument("--kernel-rounds", type=int, default=10,
                     help="back-to-back passes over each kernel class (one launch per layer) timed with HIP events")
     ap.add_argument("--cold-reps", type=int, default=100,
                     help="launches per kernel for the cold / warm per-launch timing (0 skips it)")
@@ -316,7 +316,7 @@ def main() -> int:
     # launch meets its weights / K/V rows as cold as in the step; bytes at this position
     n_kernels = info["kernels_per_step"]
     classes: dict[str, dict] = {}
-    if not args.no_kernel_times and not info.get("persistent_step"):
+    if not args.no_kernel_times:
         ids_of: dict[str, list[int]] = {}
         for kid in range(n_kernels - 1):  # the select kernel moves no bulk data
             name, _, nbytes = eng.bench_kernel(kid, 0)
@@ -340,15 +340,9 @@ def main() -> int:
     step_bytes = info["weight_bytes_per_token"] + kv_bytes
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    if info.get("persistent_step"):
-        # one kernel per token: the dominant kernel is the persistent step itself
-        dom_name = "step"
-        dom_us = ms_per_step * 1000.0
-        dom_bytes = step_bytes
-    else:
-        dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["us"])
-        dom_us = dom["us"] / dom["launches"]
-        dom_bytes = dom["bytes"] / dom["launches"]
+    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["us"])
+    dom_us = dom["us"] / dom["launches"]
+    dom_bytes = dom["bytes"] / dom["launches"]
     dom_gbs = dom_bytes / dom_us / 1e3
 
     result = {
@@ -372,7 +366,6 @@ def main() -> int:
             "context_at_timed_start": pos0 + args.warmup,
             "context_at_end": pos_end,
             "kv_cache": "f16" if info.get("kv_dtype", 0) == 0 else "f32",
-            "persistent_step": bool(info.get("persistent_step")),
             "weights": f"{w.spec.recipe.upper()} GGUF (llama.cpp type recipe), random N(0,0.02)",
         },
         "roofline": {

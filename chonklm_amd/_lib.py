@@ -144,8 +144,6 @@ SIGNATURES = [
     ("chonk_engine_read_buffer", C.c_int, [P, C.c_int32, P, C.c_size_t]),
     ("chonk_engine_read_kv", C.c_int, [P, C.c_int32, C.c_int32, C.c_int32, F32P]),
     ("chonk_engine_bench_decode", C.c_int, [P, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
-    ("chonk_engine_profile_step", C.c_int, [P, C.POINTER(C.c_double), C.c_int32, I32P]),
-    ("chonk_engine_profile_step_raw", C.c_int, [P, C.POINTER(C.c_uint64), C.c_size_t, I32P, I32P]),
     ("chonk_batch_create", C.c_int, [P, C.c_int32, C.c_int32, C.POINTER(P)]),
     ("chonk_batch_destroy", C.c_int, [P]),
     ("chonk_batch_prefill", C.c_int, [P, C.c_int32, I32P, C.c_size_t, I32P]),

@@ -20,7 +20,7 @@ LIB_DIR = PKG / "_lib"
 LIB_PATH = LIB_DIR / "libchonk.so"
 OBJ_DIR = LIB_DIR / "obj"
 
-HIP_SOURCES = [PKG / "csrc/hip/engine.hip", PKG / "csrc/hip/kernels.hip", PKG / "csrc/hip/step_kernel.hip",
+HIP_SOURCES = [PKG / "csrc/hip/engine.hip", PKG / "csrc/hip/kernels.hip",
                PKG / "csrc/hip/prefill.hip", PKG / "csrc/hip/attn_decode.hip"]
 HOST_SOURCES = [PKG / "csrc/host/gguf.cpp", PKG / "csrc/host/quantize.cpp", PKG / "csrc/host/synth.cpp"]
 HEADERS = sorted((PKG / "csrc").rglob("*.h")) + [ROOT / "include/chonk.h"]

@@ -493,15 +493,11 @@ struct LayerDev {
 };
 
 struct Launch {
-  enum Kind { MV, ATTN, SEL, STEP, SSM } kind = MV;
+  enum Kind { MV, ATTN, SEL, SSM } kind = MV;
   MvArgs mv{};
   SsmArgs ssm{};
   AttnArgs at{};
   SelArgs sel{};
-  StepArgs step{};
-  const StepArgs* d_step = nullptr;  // STEP: device copy of `step`
-  int step_group = 0;         // STEP: GQA group and K/V type of the instantiation
-  bool step_kv16 = true;
   int grid = 0;
   size_t shmem = 0;
   std::string name;
@@ -549,16 +545,8 @@ struct chonk_engine {
   std::vector<std::pair<uint32_t, float2*>> rope_cs;     // theta -> [ctx][hd/2] (cos, sin)
   // per-phase kernels of one step (qkv, attn, oproj, gateup, down per layer; lm_head, select)
   std::vector<Launch> kernels_logits, kernels_plain;
-  // what a step replays: the per-phase kernels, or the single persistent step kernel
+  // what a step replays (captured as one graph each)
   std::vector<Launch> step_logits, step_plain;
-  // persistent step (one launch per token)
-  bool use_step = false;
-  int step_group = 0;
-  void* tagged = nullptr;          // tagged activations, epoch and done counter (device memory)
-  StepPhase* d_phases = nullptr;   // phase table (device memory)
-  tagged_t *t_resid = nullptr, *t_attn = nullptr, *t_qkv = nullptr;  // last layer's buffers (readback)
-  std::vector<std::string> phase_names;  // persistent step phases (profiling)
-  StepDebug* step_dbg = nullptr;   // abort record of the persistent step
   hipGraph_t graph_logits = nullptr, graph_plain = nullptr;
   hipGraphExec_t exec_logits = nullptr, exec_plain = nullptr;
   // pinned host staging
@@ -1417,363 +1405,12 @@ void build_steps(chonk_engine* e) {
   e->kernels_logits = steps;
 }
 
-// The persistent step: one launch per token, phases in the order of the
-// per-phase kernels above, activations exchanged through tagged buffers.
-// Returns false (and leaves the per-phase kernels in use) when this model's
-// GQA group / K/V type is not compiled into it or it cannot be resident.
-bool build_step(chonk_engine* e) {
-  const ModelCfg& c = e->cfg;
-  const int G = c.heads / c.kv_heads;
-  const bool kv16 = e->kv_elem == 2;
-  if (c.gpt) return false;  // the persistent step runs the llama-family layer only
-  if (c.openelm || c.lfm || c.granite) return false;  // and one head geometry, attention in every layer
-  if (e->dsub > 1) return false;  // contexts whose decode attention walks sub-chunks
-  if (!step_supported(G, kv16)) return false;
-  int cus = 0;
-  HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
-  if (cus <= 0) return false;
-  const int grid = cus;
-  const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd, F = c.ffn, NL = c.layers;
-  // attention chunk of the step: the largest that keeps a task's K/V rows,
-  // rotary table and norm weights within one prefetch slot
-  int schunk = 0;
-  for (int ch = attn_max_chunk(c.hd); ch >= 16 && !schunk; ch >>= 1) {
-    AttnSlot L;
-    if (attn_slot_layout(c.hd, ch, (int)e->kv_elem, &L) <= kStepSlotBytes) schunk = ch;
-  }
-  if (!schunk) return false;
-  const int snchunk = (c.ctx + schunk - 1) / schunk;
-  const size_t shmem = step_shared_bytes(std::max(H, std::max(qdim, F)), 0, G, c.hd, schunk, snchunk, (int)e->kv_elem);
-  if (shmem > lds_limit() || step_occupancy(G, kv16, shmem) < 1) return false;
-
-  // tagged buffers: R0 | RFIN | per layer QKV, ATT, RMID, FF, REND, DO, DD, attention partials | epoch, done
-  // (a partial row is written and read once per step, so a workgroup that
-  // merges several layers never meets a row it has read before)
-  const size_t rowf = (size_t)attn_rowf(G, c.hd);
-  const size_t part_layer = (size_t)c.kv_heads * snchunk * rowf;  // words
-  const size_t per_layer = (size_t)(qdim + 2 * kvdim) + qdim + H + F + H + (c.gemma ? 2 * H : 0) + part_layer;
-  const size_t dbg_words = (sizeof(StepDebug) + 7) / 8;
-  const size_t words = 2 * (size_t)H + per_layer * NL + 2 + dbg_words;
-  HIP_OK(hipMalloc(&e->tagged, words * sizeof(tagged_t)));
-  HIP_OK(hipMemset(e->tagged, 0, words * sizeof(tagged_t)));
-  tagged_t* cur = (tagged_t*)e->tagged;
-  auto take = [&](size_t n) {
-    tagged_t* p = cur;
-    cur += n;
-    return p;
-  };
-  tagged_t* r0 = take(H);
-  tagged_t* rfin = take(H);
-  struct TL {
-    tagged_t *qkv, *att, *rmid, *ff, *rend, *d_o, *d_down, *part;
-  };
-  std::vector<TL> tl((size_t)NL);
-  for (int i = 0; i < NL; ++i) {
-    tl[i].qkv = take((size_t)qdim + 2 * kvdim);
-    tl[i].att = take(qdim);
-    tl[i].rmid = take(H);
-    tl[i].ff = take(F);
-    tl[i].rend = take(H);
-    tl[i].d_o = c.gemma ? take(H) : nullptr;
-    tl[i].d_down = c.gemma ? take(H) : nullptr;
-    tl[i].part = take(part_layer);
-  }
-  uint32_t* epoch = (uint32_t*)take(1);
-  uint32_t* done = (uint32_t*)take(1);
-  e->step_dbg = (StepDebug*)take(dbg_words);
-  const uint32_t one = 1;
-  HIP_OK(hipMemcpy(epoch, &one, 4, hipMemcpyHostToDevice));
-  std::vector<StepPhase> ph;
-  auto seg = [&](MvSeg& sg, const QMat& w, int n_out, int tile, int first) {
-    sg.w = w;
-    sg.n_out = n_out;
-    sg.lpr = pick_lpr(w.k / 32);
-    sg.tile = tile;
-    sg.wg_begin = first;
-    return (n_out + tile - 1) / tile;
-  };
-  auto mv = [&](int k) {
-    StepPhase p{};
-    p.kind = PH_MV;
-    p.k = k;
-    p.nseg = 1;
-    return p;
-  };
-  for (int i = 0; i < NL; ++i) {
-    const LayerDev& Ld = e->layers[i];
-    tagged_t* rprev = i == 0 ? r0 : tl[i - 1].rend;
-    {  // q | k | v
-      StepPhase p = mv(H);
-      p.nseg = 3;
-      const int tile = (qdim + 2 * kvdim + grid - 1) / grid;
-      int n = seg(p.seg[0], Ld.q.q, qdim, tile, 0);
-      n += seg(p.seg[1], Ld.k.q, kvdim, tile, n);
-      n += seg(p.seg[2], Ld.v.q, kvdim, tile, n);
-      p.n_tasks = n;
-      p.tout[0] = tl[i].qkv;
-      p.tout[1] = tl[i].qkv + qdim;
-      p.tout[2] = tl[i].qkv + qdim + kvdim;
-      p.epi = EPI_STORE;
-      p.w_norm = Ld.in_norm;
-      if (i == 0) {
-        p.pro = PRO_EMBED_NORM;
-        p.res_out = r0;
-      } else if (c.gemma) {
-        p.pro = PRO_RES_NORM;
-        p.in = tl[i - 1].rmid;
-        p.delta = tl[i - 1].d_down;
-        p.w_delta = e->layers[i - 1].post_ffn_norm;
-        p.res_out = tl[i - 1].rend;
-      } else {
-        p.pro = PRO_NORM;
-        p.in = rprev;
-      }
-      ph.push_back(p);
-    }
-    {  // attention: the per-phase kernel's arguments with per-layer tagged partials
-      StepPhase p{};
-      p.kind = PH_ATTN;
-      for (const Launch& L : e->kernels_logits)
-        if (L.kind == Launch::ATTN && L.layer == i) p.at = L.at;
-      p.at.cnt = nullptr;
-      p.at.part = nullptr;
-      // the step's own attention geometry (the per-phase kernel may use k_attn_dec's)
-      p.at.variant = 0;
-      p.at.chunk = schunk;
-      p.at.nchunk = snchunk;
-      p.at.merge_floats = attn_merge_floats(c.heads / c.kv_heads, c.hd, snchunk);
-      p.at.tpp = attn_threads_per_position(c.hd, schunk, (int)e->kv_elem);
-      p.n_tasks = c.kv_heads * snchunk;
-      p.qkv_in = tl[i].qkv;
-      p.attn_out = tl[i].att;
-      p.tpart = tl[i].part;
-      ph.push_back(p);
-    }
-    {  // o projection
-      StepPhase p = mv(qdim);
-      p.n_tasks = seg(p.seg[0], Ld.o.q, H, (H + grid - 1) / grid, 0);
-      p.pro = PRO_PLAIN;
-      p.in = tl[i].att;
-      if (c.gemma) {
-        p.epi = EPI_STORE;
-        p.tout[0] = tl[i].d_o;
-      } else {
-        p.epi = EPI_ADD;
-        p.add = rprev;
-        p.tout[0] = tl[i].rmid;
-      }
-      ph.push_back(p);
-    }
-    {  // gate | up
-      StepPhase p = mv(H);
-      p.n_tasks = seg(p.seg[0], Ld.gate.q, F, (F + grid - 1) / grid, 0);
-      p.seg[0].w2 = Ld.up.q;
-      p.tout[0] = tl[i].ff;
-      p.epi = c.gemma ? EPI_GLU_GELU : EPI_GLU_SILU;
-      if (c.gemma) {
-        p.pro = PRO_RES_NORM;
-        p.in = rprev;
-        p.delta = tl[i].d_o;
-        p.w_delta = Ld.post_norm;
-        p.res_out = tl[i].rmid;
-        p.w_norm = Ld.pre_ffn_norm;
-      } else {
-        p.pro = PRO_NORM;
-        p.in = tl[i].rmid;
-        p.w_norm = Ld.post_norm;
-      }
-      ph.push_back(p);
-    }
-    {  // down
-      StepPhase p = mv(F);
-      p.n_tasks = seg(p.seg[0], Ld.down.q, H, (H + grid - 1) / grid, 0);
-      p.pro = PRO_PLAIN;
-      p.in = tl[i].ff;
-      if (c.gemma) {
-        p.epi = EPI_STORE;
-        p.tout[0] = tl[i].d_down;
-      } else {
-        p.epi = EPI_ADD;
-        p.add = tl[i].rmid;
-        p.tout[0] = tl[i].rend;
-      }
-      ph.push_back(p);
-    }
-  }
-  {  // lm_head + group argmax: one 256-row group per task
-    StepPhase p = mv(H);
-    p.n_tasks = seg(p.seg[0], e->lm_head.q, c.vocab, 256, 0);
-    p.epi = EPI_LOGITS;
-    p.logits = e->logits;
-    p.w_norm = e->final_norm;
-    if (c.gemma) {
-      p.pro = PRO_RES_NORM;
-      p.in = tl[NL - 1].rmid;
-      p.delta = tl[NL - 1].d_down;
-      p.w_delta = e->layers[NL - 1].post_ffn_norm;
-      p.res_out = rfin;
-    } else {
-      p.pro = PRO_NORM;
-      p.in = tl[NL - 1].rend;
-    }
-    ph.push_back(p);
-  }
-  for (const StepPhase& p : ph)
-    for (int si = 0; si < p.nseg && p.kind == PH_MV; ++si)
-      if (2 * p.seg[si].tile > 1024) throw Error(CHONK_EINVAL, "persistent step: matvec tile too large");
-  // every task before the lm_head must find its rows and norm weights in one slot
-  for (const StepPhase& p : ph) {
-    if (p.kind != PH_MV || p.epi == EPI_LOGITS) continue;
-    const bool glu = p.epi == EPI_GLU_SILU || p.epi == EPI_GLU_GELU;
-    const int norms = p.pro == PRO_PLAIN ? 0 : (p.pro == PRO_RES_NORM ? 2 : 1);
-    for (int si = 0; si < p.nseg; ++si) {
-      const MvSeg& sg = p.seg[si];
-      for (int t0 = 0; t0 < sg.n_out; t0 += sg.tile) {
-        MvSlot sl;
-        if (mv_slot_layout(sg.w.type, p.k, t0, std::min(sg.tile, sg.n_out - t0), glu ? 2 : 1, norms, &sl) >
-            kStepSlotBytes) {
-          (void)hipFree(e->tagged);
-          e->tagged = nullptr;
-          return false;
-        }
-      }
-    }
-  }
-  // each workgroup's task list: task t of a phase runs on workgroup t mod grid
-  int max_tasks = 0;
-  for (int b = 0; b < grid; ++b) {
-    int n = 0;
-    for (const StepPhase& p : ph) n += p.n_tasks > b ? (p.n_tasks - b + grid - 1) / grid : 0;
-    max_tasks = std::max(max_tasks, n);
-  }
-  const int stride = max_tasks + kStepDescRing;  // end records cover the descriptor prefetch
-  std::vector<StepTask> tasks((size_t)grid * stride);
-  for (StepTask& d : tasks) d.phase = INT32_MAX;
-  for (int b = 0; b < grid; ++b) {
-    StepTask* out = tasks.data() + (size_t)b * stride;
-    for (int pi = 0; pi < (int)ph.size(); ++pi) {
-      const StepPhase& p = ph[(size_t)pi];
-      for (int t = b; t < p.n_tasks; t += grid) {
-        StepTask d{};
-        d.phase = pi;
-        d.t = t;
-        if (p.kind == PH_ATTN) {
-          d.kind = STASK_ATTN;
-        } else if (p.epi == EPI_LOGITS) {
-          d.kind = STASK_LM;
-        } else {
-          d.kind = STASK_MV;
-          const int si = (p.nseg > 2 && t >= p.seg[2].wg_begin) ? 2 : (p.nseg > 1 && t >= p.seg[1].wg_begin) ? 1 : 0;
-          const MvSeg& sg = p.seg[si];
-          const int task = t - sg.wg_begin;
-          d.type = sg.w.type;
-          d.k = p.k;
-          d.lpr = sg.lpr;
-          d.uc = (p.k >> 5) <= sg.lpr ? 1 : 2;
-          d.t0 = task * sg.tile;
-          d.nt = std::min(sg.tile, sg.n_out - d.t0);
-          d.glu = p.epi == EPI_GLU_SILU || p.epi == EPI_GLU_GELU;
-          d.pro = p.pro;
-          d.epi = p.epi;
-          if (p.pro == PRO_EMBED_NORM || p.pro == PRO_RES_NORM) {
-            const int S = (p.k + p.n_tasks - 1) / p.n_tasks;
-            d.res_lo = std::min(p.k, t * S);
-            d.res_hi = std::min(p.k, d.res_lo + S);
-          }
-          d.in = p.in;
-          d.delta = p.delta;
-          d.add = p.epi == EPI_ADD ? p.add + d.t0 : nullptr;
-          d.out = p.tout[si] + d.t0;
-          d.res_out = p.res_out;
-          MvSlot sl;
-          mv_slot_layout(d.type, p.k, d.t0, d.nt, d.glu ? 2 : 1,
-                         p.pro == PRO_PLAIN ? 0 : (p.pro == PRO_RES_NORM ? 2 : 1), &sl);
-          d.wn = sl.wn;
-          d.wd = sl.wd;
-          auto dma = [&](const void* src, int dst, int n16) {
-            if (d.n_dma >= kStepMaxDma) throw Error(CHONK_EINVAL, "persistent step: too many slot copies");
-            d.dma[d.n_dma++] = StepDma{(const uint8_t*)src, dst, n16};
-          };
-          if (sl.wn >= 0) dma(p.w_norm, sl.wn, p.k / 4);
-          if (sl.wd >= 0) dma(p.w_delta, sl.wd, p.k / 4);
-          const uint8_t* const src[2][4] = {{sg.w.s0, sg.w.s1, sg.w.s2, sg.w.s3}, {sg.w2.s0, sg.w2.s1, sg.w2.s2, sg.w2.s3}};
-          for (int j = 0; j < 2; ++j)
-            for (int q = 0; q < 4; ++q) {
-              d.data[j][q] = sl.data[j][q];
-              if (sl.n16[j][q] > 0) dma(src[j][q] + sl.src0[j][q], sl.dst[j][q], sl.n16[j][q]);
-            }
-        }
-        *out++ = d;
-      }
-    }
-  }
-  // device copies: the phase table, the task lists, then the argument blocks (with / without logits, traced)
-  const size_t ph_bytes = align256(ph.size() * sizeof(StepPhase));
-  const size_t task_bytes = align256(tasks.size() * sizeof(StepTask));
-  HIP_OK(hipMalloc((void**)&e->d_phases, ph_bytes + task_bytes + 3 * align256(sizeof(StepArgs))));
-  HIP_OK(hipMemcpy(e->d_phases, ph.data(), ph.size() * sizeof(StepPhase), hipMemcpyHostToDevice));
-  StepTask* d_tasks = (StepTask*)((uint8_t*)e->d_phases + ph_bytes);
-  HIP_OK(hipMemcpy(d_tasks, tasks.data(), tasks.size() * sizeof(StepTask), hipMemcpyHostToDevice));
-  StepArgs* d_args = (StepArgs*)((uint8_t*)d_tasks + task_bytes);
-
-  StepArgs a{};
-  a.phases = e->d_phases;
-  a.tasks = d_tasks;
-  a.task_stride = stride;
-  a.st = e->st;
-  a.epoch = epoch;
-  a.done = done;
-  a.embed = e->embed.q;
-  a.embed_scale = c.embed_scale;
-  a.eps = c.eps;
-  a.vocab = c.vocab;
-  a.hist = e->hist;
-  a.samp = e->samp;
-  a.pen_bits = e->pen_bits;
-  a.cand = e->cand;
-  a.sel = e->kernels_logits.back().sel;
-  a.dbg = e->step_dbg;
-  Launch L;
-  L.kind = Launch::STEP;
-  L.grid = grid;
-  L.shmem = shmem;
-  L.step_group = G;
-  L.step_kv16 = kv16;
-  L.name = "step";
-  L.weight_bytes = e->weight_bytes_per_token;
-  Launch Lp = L;
-  L.step = a;
-  L.step.n_phases = (int32_t)ph.size();
-  L.step.logits = 1;
-  Lp.step = a;
-  Lp.step.n_phases = (int32_t)ph.size() - 1;
-  Lp.step.logits = 0;
-  Lp.weight_bytes = e->weight_bytes_per_token - e->lm_head.gguf_bytes;
-  HIP_OK(hipMemcpy(d_args, &L.step, sizeof(StepArgs), hipMemcpyHostToDevice));
-  HIP_OK(hipMemcpy((uint8_t*)d_args + align256(sizeof(StepArgs)), &Lp.step, sizeof(StepArgs), hipMemcpyHostToDevice));
-  L.d_step = d_args;
-  Lp.d_step = (const StepArgs*)((uint8_t*)d_args + align256(sizeof(StepArgs)));
-  e->step_logits = {L};
-  e->step_plain = {Lp};
-  for (int i = 0; i < NL; ++i)
-    for (const char* n : {"qkv", "attn", "oproj", "gateup", "down"}) e->phase_names.push_back("L" + std::to_string(i) + "." + n);
-  e->phase_names.push_back("lmhead");
-  e->t_resid = c.gemma ? rfin : tl[NL - 1].rend;
-  e->t_attn = tl[NL - 1].att;
-  e->t_qkv = tl[NL - 1].qkv;
-  e->use_step = true;
-  return true;
-}
-
 void enqueue(const Launch& L, hipStream_t s) {
   switch (L.kind) {
     case Launch::MV: HIP_OK(launch_matvec(L.mv, L.grid, L.shmem, s)); break;
     case Launch::ATTN: HIP_OK(launch_attention(L.at, L.shmem, s)); break;
     case Launch::SSM: HIP_OK(launch_ssm(L.ssm, s)); break;
     case Launch::SEL: HIP_OK(launch_select(L.sel, s)); break;
-    case Launch::STEP:
-      HIP_OK(launch_step(L.d_step, L.step.phases, L.step_group, L.step_kv16, L.grid, L.shmem, s));
-      break;
   }
 }
 
@@ -1801,8 +1438,6 @@ void engine_free(chonk_engine* e) {
   e->weights.release();
   e->state.release();
   uncached_pool().give_back(e->device, e->uncached);
-  if (e->tagged) (void)hipFree(e->tagged);
-  if (e->d_phases) (void)hipFree(e->d_phases);
   if (e->pf_mem) (void)hipFree(e->pf_mem);
   if (e->flush) (void)hipFree(e->flush);
   for (auto& t : e->rope_cs) (void)hipFree(t.second);
@@ -2234,10 +1869,6 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   build_steps(e.get());
   e->step_logits = e->kernels_logits;
   e->step_plain = e->kernels_plain;
-  // the per-phase kernels (one graph per step) are the default; CHONK_STEP=1
-  // selects the persistent step kernel
-  const char* sv = std::getenv("CHONK_STEP");
-  if (sv && sv[0] == '1') build_step(e.get());
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
   const char* pv = std::getenv("CHONK_PREFILL");
   // (the row-batch glue kernels hold a row of at most 4096 elements in registers)
@@ -2382,29 +2013,10 @@ void engine_reset(chonk_engine* e) {
   e->logits_valid = false;
 }
 
-// The error a step reported, with the persistent step's abort record.
+// The error a step reported.
 Error device_error(chonk_engine* e, const DevState& st) {
-  std::string msg = "device reported error code " + std::to_string(st.error);
-  if (st.error == 3 && e->step_dbg) {
-    StepDebug d;
-    if (hipMemcpy(&d, e->step_dbg, sizeof(d), hipMemcpyDeviceToHost) == hipSuccess && d.claimed) {
-      const int n = std::min(1024, e->step_logits.empty() ? 0 : e->step_logits[0].grid);
-      uint64_t lo = ~0ull, hi = 0;
-      for (int i = 0; i < n; ++i) {
-        lo = std::min(lo, d.start[i]);
-        hi = std::max(hi, d.start[i]);
-      }
-      char buf[512];
-      std::snprintf(buf, sizeof buf,
-                    " (persistent step aborted: workgroup %d waited over 20 ms in phase %d task %d for input word %d,"
-                    " tag %u, expected %u, at position %d; workgroup starts spread over %.1f us, abort %.1f us after"
-                    " the first start)",
-                    d.wg, d.phase, d.task, d.index, d.seen, d.want, d.pos, (double)(hi - lo) / 100.0,
-                    (double)(d.abort_time - lo) / 100.0);
-      msg += buf;
-    }
-  }
-  return Error(CHONK_EHIP, msg);
+  (void)e;
+  return Error(CHONK_EHIP, "device reported error code " + std::to_string(st.error));
 }
 
 // ---- row batches: prompt pass and batched decode ---------------------------------------
@@ -3021,44 +2633,6 @@ void generate_stepped(chonk_engine* e, const int32_t* prompt, size_t n_prompt, i
 
 // ---- C ABI ------------------------------------------------------------------------
 
-namespace chonk {
-namespace {
-// One persistent step with wall-clock stamps; returns the raw trace.
-std::vector<uint64_t> trace_step(chonk_engine* e, int* np_out, int* grid_out) {
-  if (!e->use_step) throw Error(CHONK_EINVAL, "the engine does not run the persistent step");
-  const ModelCfg& c = e->cfg;
-  if (e->pos >= c.ctx) throw context_exhausted(e);
-  const Launch& L = e->step_logits[0];
-  const int np = L.step.n_phases, grid = L.grid;
-  const size_t words = (size_t)(np + 1) * grid + (size_t)np * grid * kStepStamps;
-  uint64_t* tr = nullptr;
-  HIP_OK(hipMalloc(&tr, words * 8));
-  Launch run = L;
-  run.step.trace = tr;
-  StepArgs* slot = (StepArgs*)((uint8_t*)L.d_step + 2 * align256(sizeof(StepArgs)));
-  HIP_OK(hipMemcpy(slot, &run.step, sizeof(StepArgs), hipMemcpyHostToDevice));
-  run.d_step = slot;
-  const DevState saved = read_state(e);
-  DevState st = saved;
-  st.stopped = 0;
-  st.generating = 0;
-  upload_state_fields(e, st);
-  enqueue(run, e->stream);  // warm
-  HIP_OK(hipMemsetAsync(tr, 0, words * 8, e->stream));
-  upload_state_fields(e, st);
-  enqueue(run, e->stream);
-  HIP_OK(hipStreamSynchronize(e->stream));
-  std::vector<uint64_t> h(words);
-  HIP_OK(hipMemcpy(h.data(), tr, words * 8, hipMemcpyDeviceToHost));
-  (void)hipFree(tr);
-  upload_state_fields(e, saved);
-  *np_out = np;
-  *grid_out = grid;
-  return h;
-}
-}  // namespace
-}  // namespace chonk
-
 extern "C" {
 
 const char* chonk_last_error(void) { return g_last_error.c_str(); }
@@ -3118,7 +2692,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->weight_bytes_per_token = e->weight_bytes_per_token;
   out->device_bytes = e->weights.capacity() + e->state.capacity();
   out->kernels_per_step = (int32_t)e->kernels_logits.size();
-  out->persistent_step = e->use_step ? 1 : 0;
+  out->persistent_step = 0;  // (the one-launch-per-token step was retired: the graph ran twice as fast)
   out->noalloc_prefill_rows = e->noalloc_rows;
   return CHONK_OK;
 }
@@ -3266,27 +2840,16 @@ int chonk_engine_read_buffer(chonk_engine* e, int32_t which, void* out, size_t n
     const ModelCfg& c = e->cfg;
     const void* src = nullptr;
     size_t bytes = 0;
-    const tagged_t* tsrc = nullptr;
     switch (which) {
-      case 0: src = e->resA; tsrc = e->t_resid; bytes = (size_t)c.hidden * 4; break;
-      case 1: src = e->attn; tsrc = e->t_attn; bytes = (size_t)c.heads * c.hd * 4; break;
+      case 0: src = e->resA; bytes = (size_t)c.hidden * 4; break;
+      case 1: src = e->attn; bytes = (size_t)c.heads * c.hd * 4; break;
       case 2: src = e->cand; bytes = (size_t)e->groups * 8; break;
-      case 3: src = e->qkv; tsrc = e->t_qkv; bytes = (size_t)(c.heads + 2 * c.kv_heads) * c.hd * 4; break;
+      case 3: src = e->qkv; bytes = (size_t)(c.heads + 2 * c.kv_heads) * c.hd * 4; break;
       default: throw Error(CHONK_EINVAL, "unknown buffer id");
     }
     if (!out || n_bytes < bytes) throw Error(CHONK_EINVAL, "output buffer too small");
     HIP_OK(hipStreamSynchronize(e->stream));
-    if (e->use_step && tsrc) {
-      // tagged words {value, epoch}: keep the values
-      std::vector<uint64_t> w(bytes / 4);
-      HIP_OK(hipMemcpy(w.data(), tsrc, w.size() * 8, hipMemcpyDeviceToHost));
-      for (size_t i = 0; i < w.size(); ++i) {
-        const uint32_t v = (uint32_t)w[i];
-        std::memcpy((uint8_t*)out + 4 * i, &v, 4);
-      }
-    } else {
-      HIP_OK(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
-    }
+    HIP_OK(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost));
   });
 }
 
@@ -3407,34 +2970,6 @@ int chonk_engine_time_kernels(chonk_engine* e, const int32_t* ids, int32_t n_ids
     (void)hipEventDestroy(b);
     upload_state_fields(e, saved);
     *us_per_launch = total_ms * 1000.0 / ((double)rounds * n_ids);
-  });
-}
-
-int chonk_engine_profile_step_raw(chonk_engine* e, uint64_t* out, size_t cap, int32_t* n_phases, int32_t* n_wg) {
-  return api(e, [&] {
-    int np = 0, grid = 0;
-    const std::vector<uint64_t> h = trace_step(e, &np, &grid);
-    if (out) std::memcpy(out, h.data(), std::min(cap, h.size()) * 8);
-    if (n_phases) *n_phases = np;
-    if (n_wg) *n_wg = grid;
-  });
-}
-
-
-int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases) {
-  return api(e, [&] {
-    int np = 0, grid = 0;
-    const std::vector<uint64_t> h = trace_step(e, &np, &grid);
-    const size_t words = (size_t)(np + 1) * grid;
-    (void)words;
-    uint64_t t0 = ~0ull;
-    for (int w = 0; w < grid; ++w) t0 = std::min(t0, h[(size_t)np * grid + w]);
-    for (int p = 0; p < np && p < cap; ++p) {
-      uint64_t end = 0;
-      for (int w = 0; w < grid; ++w) end = std::max(end, h[(size_t)p * grid + w]);
-      phase_end_us[p] = (double)(end - t0) / 100.0;  // 100 MHz wall clock
-    }
-    if (n_phases) *n_phases = np;
   });
 }
 

@@ -1,4 +1,4 @@
-// Device helpers shared by the decode kernels (kernels.hip, step_kernel.hip).
+// Device helpers shared by the decode kernels (kernels.hip, attn_decode.hip, prefill.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -200,7 +200,7 @@ struct SegView {
   int n_out, tile, lpr, wg_begin;
 };
 
-// ---- matvec core (k_mv_* and the persistent step) --------------------------------
+// ---- matvec core (k_mv_*) -----------------------------------------------
 
 // LDS of the integer-digit form of x at `base`: three digit planes of K bytes,
 // then bsc[K/32] and xs8[K/8] (3.625 K bytes in all); xs16[K/16] lies apart.
@@ -551,7 +551,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, float* sm, int kv,
   float* wts = wml + 8 * kMaxG;
   float* cpart = wts + G * ncp;
   // the rotary table, norm weights and V rows come from sm, or from the
-  // caller's copies (the persistent step's prefetch slot)
+  // caller's copies when it passes them
   float* tile = vtile ? (float*)vtile : cpart + attn_rowf(G, hd);
   if (inv_in) inv = (float*)inv_in;
   if (qn_in) qn = (float*)qn_in;

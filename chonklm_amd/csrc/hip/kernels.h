@@ -153,207 +153,10 @@ struct SelArgs {
   DevState* st;
 };
 
-// Persistent decode step --------------------------------------------------------
-//
-// The whole token (every layer, lm_head, selection) as one launch of one
-// workgroup per CU. Phases follow each other in the order of the step; a
-// workgroup walks its tasks of every phase (task t of a phase runs on
-// workgroup (t + rot) mod grid). Activations crossing workgroups are "tagged":
-// 8-byte words {f32 value, u32 step epoch} written and read with agent-scope
-// atomics, so a consumer waits for its inputs by polling the words themselves
-// (no counters, no cache maintenance), with a bounded wait that aborts the step
-// (DevState.error = 3) instead of hanging.
+// Words {f32 value, u32 epoch} written and read with agent-scope atomics: a
+// consumer in another workgroup waits for a value by polling the word itself
+// until it carries the launch's epoch (no counters, no cache maintenance).
 typedef uint64_t tagged_t;
-
-enum PhaseKind : int32_t { PH_MV = 0, PH_ATTN = 1 };
-
-struct StepPhase {
-  int32_t kind;
-  int32_t n_tasks;
-  int32_t rot;
-  int32_t nseg;
-  // PH_MV: up to three matrices sharing the input (q | k | v); seg[i].wg_begin
-  // is the segment's first task, seg[i].tile its rows per task.
-  MvSeg seg[3];
-  int32_t pro, epi, k, pad0;
-  const tagged_t* in;      // input [k] (PRO_PLAIN, PRO_NORM, PRO_RES_NORM)
-  const tagged_t* delta;   // PRO_RES_NORM: branch output to normalise and add
-  const float* w_norm;
-  const float* w_delta;
-  tagged_t* res_out;       // PRO_EMBED_NORM / PRO_RES_NORM: residual [k], written in task slices
-  const tagged_t* add;     // EPI_ADD: residual input [n_out]
-  tagged_t* tout[3];       // per-segment tagged outputs (EPI_STORE / EPI_ADD / EPI_GLU_*)
-  float* logits;           // EPI_LOGITS: plain logits [vocab]
-  // PH_ATTN: one task per (kv head, chunk); q|k|v come from qkv_in. Every
-  // chunk but the newest stores its partial in tpart ([kv][nchunk] rows of
-  // attn_rowf words); the newest chunk's task merges them into attn_out.
-  AttnArgs at;
-  const tagged_t* qkv_in;
-  tagged_t* attn_out;
-  tagged_t* tpart;
-};
-
-// Record of the first wait that exceeded its time bound (diagnostics).
-struct StepDebug {
-  uint32_t claimed;        // set by the first workgroup that aborts
-  int32_t wg, phase, task, index;
-  uint32_t seen, want;     // tag found at `index` / tag expected
-  int32_t pos;
-  uint64_t abort_time;     // wall clock (100 MHz ticks)
-  uint64_t start[1024];    // per-workgroup start time of the last step
-};
-
-// Wall-clock stamps per persistent-step task when tracing: matvec: start,
-// input arrived, prologue done, input quantized, dot products done, next slot
-// requested, epilogue stored, end; attention: start, input arrived, K rows
-// loaded, chunk done, next slot requested, partial stored or heads merged,
-// next slot requested (merging chunk), end.
-constexpr int kStepStamps = 8;
-
-// One task of a workgroup's list in the persistent step, resolved on the host
-// from the phase table: a matvec task carries its rows, the slot layout of
-// its weight rows and norm weights, the direct-to-LDS copies that fill that
-// slot and the addresses of its tagged inputs and outputs, so the device
-// reads one record per task instead of walking the phase's segments.
-enum StepTaskKind : int32_t {
-  STASK_MV = 0,    // matvec task whose rows and norm weights are in the slot
-  STASK_ATTN = 1,  // attention task (kv head, chunk) = (t / nchunk, t % nchunk)
-  STASK_LM = 2,    // lm_head task: rows streamed from memory, group argmax
-};
-struct StepDma {
-  const uint8_t* src;
-  int32_t dst, n16;  // slot offset, 16-byte units
-};
-constexpr int kStepMaxDma = 10;  // two norm weights + two matrices of up to four streams
-struct alignas(16) StepTask {
-  int32_t phase;         // index in the phase table; >= n_phases ends the list
-  int32_t t;             // task index within the phase
-  int32_t kind;          // StepTaskKind
-  int32_t type, uc, k, lpr;
-  int32_t t0, nt, glu;   // rows [t0, t0 + nt) of the segment
-  int32_t pro, epi;
-  int32_t res_lo, res_hi;  // residual slice stored by this task (PRO_EMBED_NORM / PRO_RES_NORM)
-  int32_t n_dma;
-  int32_t wn, wd;        // slot offsets of the norm weights (-1: none)
-  int32_t data[2][4];    // slot offset of row t0 of each (matrix, stream) (-1: none)
-  int32_t pad[3];
-  const tagged_t* in;    // [k] unless PRO_EMBED_NORM
-  const tagged_t* delta; // [k] for PRO_RES_NORM
-  const tagged_t* add;   // EPI_ADD: residual words of rows [t0, t0 + nt)
-  tagged_t* out;         // output words of rows [t0, t0 + nt)
-  tagged_t* res_out;     // residual words [k] (the task stores [res_lo, res_hi))
-  StepDma dma[kStepMaxDma];
-  int32_t pad2[2];
-};
-static_assert(sizeof(StepTask) == 320, "StepTask is copied in 16-byte units");
-constexpr int kStepDescRing = 8;  // task records a workgroup keeps in LDS (prefetched ahead)
-
-struct StepArgs {
-  const StepPhase* phases;
-  const StepTask* tasks;   // [grid][task_stride]: each workgroup's tasks in order, then end records
-  int32_t task_stride;
-  int32_t n_phases;
-  int32_t logits;          // 1: the step ends with token selection
-  DevState* st;
-  uint32_t* epoch;         // step epoch (tags); advanced by the last workgroup
-  uint32_t* done;          // workgroups finished; reset by the last one
-  QMat embed;
-  float embed_scale;
-  float eps;
-  int32_t vocab;
-  int32_t pad0;
-  const int32_t* hist;
-  const DevSampling* samp;
-  const uint32_t* pen_bits;
-  Candidate* cand;
-  SelArgs sel;
-  StepDebug* dbg;
-  uint64_t* trace;         // optional wall-clock stamps: [n_phases + 1][grid] phase ends, then start;
-                           // then [n_phases][grid][kStepStamps] per task (see k_step)
-};
-
-// Each task of the persistent step finds the inputs that do not depend on the
-// previous phases (norm weights, its weight rows, its K/V chunk) in an LDS
-// slot filled by direct-to-LDS loads issued during the workgroup's previous
-// task; two slots of kStepSlotBytes alternate.
-constexpr int kStepSlotBytes = 36 * 1024;
-
-// Bytes per row of stream s of a [N][K] matrix of `type` in the striped layout
-// (device_common.h); 0 for a stream the type does not use.
-__host__ __device__ constexpr int stripe_row_bytes(int type, int k, int s) {
-  switch (type) {
-    case QT_Q4_K: return s == 0 ? k / 2 : s == 1 ? k / 16 : 0;
-    case QT_Q5_K: return s == 0 ? k / 2 : s == 1 ? k / 16 : s == 2 ? k / 8 : 0;
-    case QT_Q6_K: return s == 0 ? k / 2 : s == 1 ? k / 4 : s == 2 ? k / 16 : k / 128;
-    case QT_Q8_0: return s == 0 ? k : s == 1 ? k / 16 : 0;
-    case QT_Q5_0: return s == 0 ? k / 2 : s == 1 ? k / 8 : s == 2 ? k / 16 : 0;
-    case QT_Q5_1: return s == 0 ? k / 2 : s == 1 ? k / 8 : k / 16;
-  }
-  return 0;
-}
-
-// Slot layout of a matvec task over rows [t0, t0 + nt) of a K-column matrix
-// (two matrices for GLU): the norm weights (K floats each) first, then each
-// stream's row range as a 16-byte-aligned copy. data[m][s] is the slot offset
-// of row t0's first byte of stream s of matrix m; returns the slot bytes used.
-struct MvSlot {
-  int wn, wd;        // norm weight / residual-norm weight offsets (-1: none)
-  int data[2][4];    // per matrix and stream: offset of row t0 (-1: none)
-  int dst[2][4];     // slot offset of the copy (16-aligned)
-  int src0[2][4];    // first byte (16-aligned) of the copied range within the stream
-  int n16[2][4];     // 16-byte units copied
-};
-__host__ __device__ inline int mv_slot_layout(int type, int k, int t0, int nt, int nmat, int n_norms, MvSlot* m) {
-  int off = 0;
-  m->wn = n_norms > 0 ? off : -1;
-  off += n_norms > 0 ? 4 * k : 0;
-  m->wd = n_norms > 1 ? off : -1;
-  off += n_norms > 1 ? 4 * k : 0;
-  for (int j = 0; j < 2; ++j)
-    for (int s = 0; s < 4; ++s) {
-      const int rb = stripe_row_bytes(type, k, s);
-      if (j >= nmat || rb == 0 || nt <= 0) {
-        m->data[j][s] = -1;
-        m->dst[j][s] = 0;
-        m->src0[j][s] = 0;
-        m->n16[j][s] = 0;
-        continue;
-      }
-      const int b0 = t0 * rb, b1 = (t0 + nt) * rb;
-      const int a0 = b0 & ~15, a1 = (b1 + 15) & ~15;
-      m->src0[j][s] = a0;
-      m->n16[j][s] = (a1 - a0) / 16;
-      m->dst[j][s] = off;
-      m->data[j][s] = off + (b0 - a0);
-      off += a1 - a0;
-    }
-  return off;
-}
-
-// Slot layout of an attention task: rotary inverse frequencies [hd/2], q / k
-// norm weights [hd] each, then K and V rows of the chunk indexed by chunk
-// position (only the positions the task reads are copied).
-struct AttnSlot {
-  int inv, qn, kn, k, v;
-};
-__host__ __device__ inline int attn_slot_layout(int hd, int chunk, int kv_elem, AttnSlot* s) {
-  s->inv = 0;
-  s->qn = (hd / 2 * 4 + 15) & ~15;
-  s->kn = s->qn + hd * 4;
-  s->k = s->kn + hd * 4;
-  s->v = s->k + chunk * hd * kv_elem;
-  return s->v + chunk * hd * kv_elem;
-}
-
-// Dynamic LDS bytes of the persistent step for this model.
-size_t step_shared_bytes(int max_k, int max_tile_rows, int group, int hd, int chunk, int nchunk, int kv_elem);
-// Whether the persistent step is compiled for this GQA group / K/V type.
-bool step_supported(int group, bool kv_f16);
-// Workgroups of the persistent step resident per CU with `shmem` bytes of LDS (0: cannot run).
-int step_occupancy(int group, bool kv_f16, size_t shmem);
-// `a` and `phases` point to device memory holding the step's arguments and phase table.
-hipError_t launch_step(const StepArgs* a, const StepPhase* phases, int group, bool kv_f16, int grid, size_t shmem,
-                       hipStream_t s);
 
 // Launch parameter helpers -------------------------------------------------------
 size_t mv_shared_bytes(int k, int max_tile_rows);

@@ -110,34 +110,6 @@ class LlamaWgslEngine:
         check(lib().chonk_engine_read_logits(self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size), self._h)
         return out
 
-    def profile_step(self) -> list[tuple[str, float]]:
-        """Persistent step only: (phase, microseconds from the step's start to the
-        phase's last workgroup finishing) for one decode step."""
-        n_layers = self.info["layers"]
-        names = [f"L{i}.{p}" for i in range(n_layers) for p in ("qkv", "attn", "oproj", "gateup", "down")]
-        names.append("lmhead")
-        out = (C.c_double * len(names))()
-        n = C.c_int32()
-        check(lib().chonk_engine_profile_step(self._h, out, len(names), C.byref(n)), self._h)
-        return list(zip(names, list(out)[: n.value]))
-
-    def profile_step_raw(self) -> tuple[np.ndarray, np.ndarray]:
-        """Persistent step only: (phase ends [n_phases][n_wg], task stamps [n_phases][n_wg][8], in
-        the order chonk_engine_profile_step_raw documents) in microseconds from the first
-        workgroup's start (0 where a workgroup had no task in a phase or a stamp was not taken)."""
-        np_, ng = C.c_int32(), C.c_int32()
-        check(lib().chonk_engine_profile_step_raw(self._h, None, 0, C.byref(np_), C.byref(ng)), self._h)
-        P_, G_ = np_.value, ng.value
-        n = (P_ + 1) * G_ + P_ * G_ * 8
-        buf = np.zeros(n, dtype=np.uint64)
-        check(lib().chonk_engine_profile_step_raw(self._h, buf.ctypes.data_as(C.POINTER(C.c_uint64)), n,
-                                                  C.byref(np_), C.byref(ng)), self._h)
-        t0 = int(buf[P_ * G_:(P_ + 1) * G_].min())
-        ends = (buf[:P_ * G_].astype(np.float64) - t0).reshape(P_, G_) / 100.0
-        st = buf[(P_ + 1) * G_:].astype(np.float64).reshape(P_, G_, 8)
-        st = np.where(st > 0, (st - t0) / 100.0, 0.0)
-        return ends, st
-
     def read_buffer(self, which: int) -> np.ndarray:
         i = self.info
         # lfm2 / granitehybrid: one slot per residue class

@@ -88,7 +88,7 @@ typedef struct {
   uint64_t weight_bytes_per_token;  /* GGUF bytes of every matrix read per token (incl. lm_head + embedding row) */
   uint64_t device_bytes;            /* device memory held by the engine */
   int32_t kernels_per_step;         /* per-phase kernels of one decode step (chonk_engine_bench_kernel ids) */
-  int32_t persistent_step;          /* 1: a step runs as one persistent kernel launch */
+  int32_t persistent_step;          /* always 0 (kept for layout: the one-launch step was retired) */
   int32_t noalloc_prefill_rows;     /* most tokens one chonk_engine_prefill_noalloc call takes (0: none) */
 } chonk_engine_info;
 
@@ -217,18 +217,6 @@ int chonk_engine_bench_kernel_cold(chonk_engine* e, int32_t kernel_id, int32_t r
  * and K/V rows as cold as the step does, unlike repeats of one launch. */
 int chonk_engine_time_kernels(chonk_engine* e, const int32_t* ids, int32_t n_ids, int32_t rounds,
                               double* us_per_launch);
-/* Persistent step only: runs one decode step with per-phase time stamps and
- * returns, per phase (q|k|v, attention, o_proj, gate|up, down per layer, then
- * lm_head), the time from the first workgroup's start to the last workgroup's
- * end of that phase, in microseconds (the step's state is restored). */
-int chonk_engine_profile_step(chonk_engine* e, double* phase_end_us, int32_t cap, int32_t* n_phases);
-/* Persistent step only: the raw wall-clock trace (100 MHz ticks) of one step:
- * [n_phases + 1][n_wg] phase ends then workgroup starts, followed by
- * [n_phases][n_wg][8] per task: start, input arrived, prologue done, input
- * quantized, dot products done, next slot requested, epilogue stored, end
- * (attention: start, input arrived, K rows loaded, chunk done, next slot
- * requested, partial stored or heads merged, next slot requested, end). */
-int chonk_engine_profile_step_raw(chonk_engine* e, uint64_t* out, size_t cap, int32_t* n_phases, int32_t* n_wg);
 /* Writes `pos` synthetic positions into the K/V cache and sets the position,
  * so that long-context decode can be measured without a full prefill. */
 int chonk_engine_fake_context(chonk_engine* e, int32_t pos, uint64_t seed);

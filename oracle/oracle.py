@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as C
 import subprocess
 from pathlib import Path
-from typing import Optional, Sequence
+from typing import Callable, Optional, Sequence
 
 import numpy as np
 
@@ -223,7 +223,8 @@ class OracleModel:
 
     def generate(self, prompt_ids: Sequence[int], max_new_tokens: Optional[int] = None, temperature=None,
                  top_p=None, top_k=None, repetition_penalty=None, seed: int = 0,
-                 margins: Optional[list] = None) -> list[int]:
+                 margins: Optional[list] = None,
+                 on_logits: Optional[Callable[[int, np.ndarray], None]] = None) -> list[int]:
         """generateLlamaWgsl (llama-wgsl-runtime.ts:242-314); generateGptWgsl
         (gpt-wgsl-runtime.ts:182-249) for gpt2, which also runs the token after
         the last generated one and refuses an empty prompt with no cached token;
@@ -231,7 +232,8 @@ class OracleModel:
         generateGraniteWgsl (granite-wgsl-runtime.ts:223-292) for granitehybrid,
         which run the token after the last generated one, start an empty prompt
         with no cached token from id 0 and ignore the definition's default
-        penalty."""
+        penalty. ``on_logits(i, logits)`` sees the logits that pick generated
+        id i (i = 0: those of the last prompt token)."""
         prompt = list(prompt_ids)
         mx = min(128 if max_new_tokens is None else max_new_tokens, self.max_context - len(prompt))
         t = 0.0 if temperature is None else temperature
@@ -261,6 +263,8 @@ class OracleModel:
                 next_id = self.run_token(tok, need, t, tp, tk, rp, ids, ids, seed)
                 if need and margins is not None:
                     margins.append(self._margin())
+                if need and on_logits is not None:
+                    on_logits(0, self.logits())
         generated: list[int] = []
         for step in range(mx):
             generated.append(next_id)
@@ -272,6 +276,8 @@ class OracleModel:
             next_id = self.run_token(next_id, True, t, tp, tk, rp, ids, ids, seed)
             if margins is not None:
                 margins.append(self._margin())
+            if on_logits is not None:
+                on_logits(step + 1, self.logits())
         self.cached_token_ids = prompt + generated
         self.cached_next_id = None if (generated and generated[-1] in self.eos_ids) else next_id
         return generated

@@ -7,8 +7,7 @@
   tests/golden/make_config_golden.py (the oracle runs the reference's
   token-by-token loop, llama-wgsl-runtime.ts:242-314, in the build
   container; the fixture is keyed by the GGUF file's SHA-256).
-* Decode steps at the configurations' contexts against the oracle run live,
-  through the per-phase graph and through the persistent step kernel:
+* Decode steps at the configurations' contexts against the oracle run live:
   logits within 1e-3 (max |d| / max |ref|) and identical ids. The K/V cache
   holds the same synthetic positions on both sides (SmolLM2: the real prompt),
   so these steps run the kernels at their configuration geometry: decode
@@ -82,16 +81,8 @@ def test_config_generate_matches_golden(synth, name):
     loaded.engine.dispose()
 
 
-@pytest.fixture(params=["graph", "persistent"])
-def step_mode(request, monkeypatch):
-    """Both decode-step executions: the per-phase kernels replayed as one graph
-    (default) and the persistent step kernel (CHONK_STEP=1)."""
-    monkeypatch.setenv("CHONK_STEP", "1" if request.param == "persistent" else "0")
-    return request.param
-
-
 @pytest.mark.parametrize("name", CONFIGS)
-def test_config_steps_match_oracle(synth, name, step_mode):
+def test_config_steps_match_oracle(synth, name):
     w = WORKLOADS[name]
     path = synth(name)
     ctx = w.prompt_tokens + 16
@@ -99,7 +90,6 @@ def test_config_steps_match_oracle(synth, name, step_mode):
     md.max_context = ctx
     loaded = load_llama_wgsl_model(md)
     eng = loaded.engine
-    assert eng.info["persistent_step"] == (1 if step_mode == "persistent" else 0)
     ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
     prompt = w.prompt(1234)
     samp = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, seed=9)
@@ -235,7 +225,6 @@ def test_decode_attention_across_chunk_counts(synth):
     md.max_context = ctx
     loaded = load_llama_wgsl_model(md)
     eng = loaded.engine
-    assert eng.info["persistent_step"] == 0
     ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
     tok = 17
     for pos in (1, 63, 64, 127, 700, 1900, 1919, 1920, 2047, 2048, 2111, 2112, 2240, 2302):

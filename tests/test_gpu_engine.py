@@ -46,20 +46,9 @@ def _prompt(w, seed=0, n=None):
     return rng.integers(0, w.spec.vocab, n or w.prompt_tokens).tolist()
 
 
-@pytest.fixture(params=["graph", "persistent"])
-def step_mode(request, monkeypatch):
-    """Both decode-step executions: the per-phase kernels replayed as one graph
-    (default) and the persistent step kernel (CHONK_STEP=1)."""
-    monkeypatch.setenv("CHONK_STEP", "1" if request.param == "persistent" else "0")
-    return request.param
-
-
 @pytest.mark.parametrize("name", TINY)
-def test_step_logits_and_tokens(name, synth, step_mode):
+def test_step_logits_and_tokens(name, synth):
     w, loaded, ref = _pair(synth, name)
-    # the persistent step runs one head geometry for every layer (not openelm)
-    persistent = step_mode == "persistent" and w.spec.arch != "openelm"
-    assert loaded.engine.info["persistent_step"] == (1 if persistent else 0)
     eng = loaded.engine
     prompt = _prompt(w)
     toks_g, toks_r = [], []
@@ -82,7 +71,7 @@ def test_step_logits_and_tokens(name, synth, step_mode):
 
 
 @pytest.mark.parametrize("name", TINY)
-def test_generate_matches_oracle(name, synth, step_mode):
+def test_generate_matches_oracle(name, synth):
     w, loaded, ref = _pair(synth, name)
     prompt = _prompt(w, seed=1)
     out = generate_llama_wgsl(loaded, prompt, w.decode_tokens, temperature=w.temperature, top_k=w.top_k, seed=9)

@@ -44,12 +44,10 @@ def _prompt(w, seed=0, n=None):
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
 @pytest.mark.parametrize("name", TINY_LFM)
-def test_lfm_step_logits_and_tokens(name, kv, synth, monkeypatch):
-    # the persistent step declines lfm2 (attention is not in every layer)
-    monkeypatch.setenv("CHONK_STEP", "1")
+def test_lfm_step_logits_and_tokens(name, kv, synth):
     w, loaded, ref = _pair(synth, name, kv=kv)
     eng = loaded.engine
-    assert eng.info["architecture"] == 5 and eng.info["persistent_step"] == 0
+    assert eng.info["architecture"] == 5
     prompt = _prompt(w)
     tok = prompt[0]
     for i in range(len(prompt) + 12):
