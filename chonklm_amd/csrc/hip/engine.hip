@@ -520,6 +520,7 @@ struct chonk_engine {
   Arena weights, state;
   std::vector<LayerDev> layers;
   DevMat embed, lm_head;
+  DevMat lm_lanes;  // the lm_head's lane-interleaved copy (k_lm_lanes); s0 null when absent
   float* final_norm = nullptr;
   float *final_norm_b = nullptr, *pos_embd = nullptr;  // gpt2: final LayerNorm bias, position table
   size_t kv_elem = 2;
@@ -840,6 +841,78 @@ DevMat upload_class_major(Arena& arena, const ByteSource& src, const GgufFile& g
     *dst[i] = (const uint8_t*)p;
   }
   m.gguf_bytes = (uint64_t)V * row_bytes;
+  return m;
+}
+
+// The lm_head's lane-interleaved copy (qdot.h, load_lane_unit): rows in blocks of
+// 64, the fragments of one unit of the block's 64 rows side by side in each
+// stream, so that k_lm_lanes (one row per lane) reads every unit of a wave as
+// one contiguous run. Rows past N (up to a multiple of 256, the rows of a
+// k_lm_lanes workgroup) are zero blocks (they decode to 0). The bytes
+// per stream are those of the striped layout of the padded matrix.
+bool lane_layout_type(uint32_t type) { return type == GGML_Q4_K || type == GGML_Q6_K || type == GGML_Q8_0; }
+int64_t lane_rows(int64_t N) { return 256 * ((N + 255) / 256); }  // whole k_lm_lanes workgroups
+
+DevMat upload_lanes(Arena& arena, const ByteSource& src, const GgufFile& g, const GgufTensorInfo& t, int64_t K,
+                    int64_t N) {
+  check_matrix(t, K, N);
+  if (!lane_layout_type(t.type)) throw Error(CHONK_EINVAL, "no lane-interleaved layout for " + type_name(t.type));
+  std::vector<uint8_t> raw = read_tensor(src, g, t);
+  TypeTraits tt;
+  type_traits(t.type, &tt);
+  const size_t row_bytes = (size_t)(K / tt.block_elems) * tt.block_bytes;
+  const int64_t NP = lane_rows(N), U = K / 32, SB = K / 256;
+  const size_t nb = (size_t)(NP * (K / tt.block_elems));
+  Stripes st;
+  switch (t.type) {
+    case GGML_Q6_K: st.s[0].assign(nb * 128, 0); st.s[1].assign(nb * 64, 0); st.s[2].assign(nb * 16, 0); st.s[3].assign(nb * 2, 0); break;
+    case GGML_Q8_0: st.s[0].assign(nb * 32, 0); st.s[1].assign(nb * 2, 0); break;
+    default: st.s[0].assign(nb * 128, 0); st.s[1].assign(nb * 16, 0); break;  // Q4_K
+  }
+  for (int64_t r = 0; r < N; ++r) {
+    const uint8_t* row = raw.data() + (size_t)r * row_bytes;
+    const int64_t blk = r >> 6, lane = r & 63;
+    auto ui = [&](int64_t u) { return (size_t)((blk * U + u) * 64 + lane); };
+    auto sj = [&](int64_t sb) { return (size_t)((blk * SB + sb) * 64 + lane); };
+    if (t.type == GGML_Q8_0) {
+      for (int64_t u = 0; u < U; ++u) {
+        const uint8_t* p = row + 34 * u;
+        std::memcpy(st.s[0].data() + 32 * ui(u), p + 2, 32);
+        std::memcpy(st.s[1].data() + 2 * ui(u), p, 2);
+      }
+      continue;
+    }
+    for (int64_t sb = 0; sb < SB; ++sb) {
+      const uint8_t* p = row + (size_t)sb * tt.block_bytes;
+      if (t.type == GGML_Q6_K) {
+        // unit c of the super-block: half h = c / 4, run b = c % 4 (load_unit<Q6_K>)
+        for (int c = 0; c < 8; ++c) {
+          const int h = c >> 2, b = c & 3;
+          const size_t i = ui(8 * sb + c);
+          std::memcpy(st.s[0].data() + 16 * i, p + 64 * h + 8 * b, 8);
+          std::memcpy(st.s[0].data() + 16 * i + 8, p + 64 * h + 32 + 8 * b, 8);
+          std::memcpy(st.s[1].data() + 8 * i, p + 128 + 32 * h + 8 * b, 8);
+        }
+        std::memcpy(st.s[2].data() + 16 * sj(sb), p + 192, 16);
+        std::memcpy(st.s[3].data() + 2 * sj(sb), p + 208, 2);
+      } else {  // Q4_K: header (d, dmin, scales) then 128 bytes of nibbles, 16 per unit
+        for (int c = 0; c < 8; ++c) std::memcpy(st.s[0].data() + 16 * ui(8 * sb + c), p + 16 + 16 * c, 16);
+        std::memcpy(st.s[1].data() + 16 * sj(sb), p, 16);
+      }
+    }
+  }
+  DevMat m;
+  m.q.type = (int32_t)t.type;
+  m.q.n = (int32_t)NP;
+  m.q.k = (int32_t)K;
+  const uint8_t** dst[4] = {&m.q.s0, &m.q.s1, &m.q.s2, &m.q.s3};
+  for (int i = 0; i < 4; ++i) {
+    if (st.s[i].empty()) continue;
+    void* ptr = arena.take(st.s[i].size());
+    HIP_OK(hipMemcpy(ptr, st.s[i].data(), st.s[i].size(), hipMemcpyHostToDevice));
+    *dst[i] = (const uint8_t*)ptr;
+  }
+  m.gguf_bytes = (uint64_t)N * row_bytes;
   return m;
 }
 
@@ -1360,6 +1433,10 @@ void build_steps(chonk_engine* e) {
       a.lfm_classes = 1;
     }
     a.logit_scale = c.logit_scale;  // (granitehybrid: SCALE_LOGITS_WGSL's x 1/3)
+    if (e->lm_lanes.q.s0) {
+      sg.w = e->lm_lanes.q;
+      a.lm_lanes = 1;
+    }
     a.epi = EPI_LOGITS;
     a.w_norm = e->final_norm;
     a.gpt_argmax = c.gpt ? 1 : 0;
@@ -1475,6 +1552,11 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd;
   const std::string lm_name = g.find("output.weight") ? "output.weight" : "token_embd.weight";
   const bool tied = lm_name == "token_embd.weight";
+  // the lm_head's lane-interleaved copy for k_lm_lanes (CHONK_LM=rows keeps k_mv_logits_t)
+  const char* lmv = std::getenv("CHONK_LM");
+  // (k_lm_lanes keeps 2 or 4 units in flight per lane: an even number of 32-element units per row)
+  const bool lm_lanes = !c.lfm && !c.granite && lane_layout_type(tensor(g, lm_name).type) && (H / 32) % 2 == 0 &&
+                        !(lmv && std::strcmp(lmv, "rows") == 0);
   // size the weight arena
   size_t wbytes = 0;
   auto mat_bytes = [&](const std::string& name, int64_t K, int64_t N) {
@@ -1492,6 +1574,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   } else {
     mat_bytes("token_embd.weight", H, c.vocab);
     if (!tied) mat_bytes(lm_name, H, c.vocab);
+    if (lm_lanes) wbytes += stripes_bytes(tensor(g, lm_name).type, lane_rows(c.vocab), H);
   }
   vec_bytes(H);
   if (c.gpt) {
@@ -1673,6 +1756,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     e->final_norm = granite_floats(e->weights, *src, g, "output_norm.weight", H);
   } else {
     e->lm_head = tied ? e->embed : upload_matrix(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
+    if (lm_lanes) e->lm_lanes = upload_lanes(e->weights, *src, g, tensor(g, lm_name), H, c.vocab);
     e->final_norm = upload_floats(e->weights, *src, g, "output_norm.weight", H);
   }
   for (int i = 0; i < (c.lfm ? c.layers : 0); ++i) {

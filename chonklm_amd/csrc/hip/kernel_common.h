@@ -283,6 +283,21 @@ __device__ __forceinline__ void xf_build(const float* xs, int K, float4* X, floa
   for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg) xf_put<T>(reinterpret_cast<const float4*>(xs)[i4], i4, K >> 5, X, S);
 }
 
+// The same into the unit-major layout of the row-per-lane lm_head (qdot.h,
+// acc_lane): XU[u * 9 + v] = float4 v of unit u, XU[u * 9 + 8] = its run sums.
+template <int T>
+__device__ __forceinline__ void xu_build(const float* xs, int K, float4* XU) {
+  for (int i4 = threadIdx.x; i4 < (K >> 2); i4 += kWg) {
+    const float4 v = reinterpret_cast<const float4*>(xs)[i4];
+    int u, e;
+    unit_of_col<T>(4 * i4, u, e);
+    XU[9 * u + (e >> 2)] = v;
+    const float s4 = (v.x + v.y) + (v.z + v.w);
+    const float s8 = s4 + dpp<0xb1>(s4);
+    if ((i4 & 1) == 0) reinterpret_cast<float*>(XU + 9 * u + 8)[e >> 3] = s8;
+  }
+}
+
 // A lane's share of a matvec task: lane group lg (of ng groups of lpr lanes)
 // owns virtual rows lg, lg + ng, ... (GLU: even rows gate, odd rows up); lane
 // li owns units li, li + lpr, ... of each row.

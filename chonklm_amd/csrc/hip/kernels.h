@@ -85,7 +85,7 @@ struct MvArgs {
   int32_t conv_n;          // channels (the hidden size)
   int32_t conv_commit;     // WG0 sets s1 = s2, s2 = B * x
   int32_t lfm_classes;     // EPI_LOGITS: rows stored class-major, workgroup c computes ids c, c + 256, ...
-  int32_t pad_lfm;
+  int32_t lm_lanes;        // EPI_LOGITS: seg[0].w is the lane-interleaved copy (k_lm_lanes, 256 ids per workgroup)
   const float* gate_z;     // PRO_GATE: the gate z (the first k rows of the Mamba2 in_proj output)
   float add_scale;         // EPI_ADD: out = add + acc * add_scale when non-zero (granitehybrid's 0.246)
   float logit_scale;       // EPI_LOGITS: logits = acc * logit_scale when non-zero (granitehybrid's 1/3)

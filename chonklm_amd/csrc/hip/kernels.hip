@@ -583,6 +583,115 @@ __global__ __launch_bounds__(kWg, 3) void k_mv_logits_t(const MvArgs a) {
   matvec_body<EPI_LOGITS, T, T == QT_Q6_K ? 1 : 2>(a);
 }
 
+// lm_head over the lane-interleaved copy (qdot.h): every lane owns one vocab
+// row and walks all of its units, so no cross-lane reduction is needed; the
+// wave's 64 rows of one unit are one contiguous run, and every lane reads the
+// same x unit from LDS (a broadcast). D units of every lane (and, for the
+// K-quants, the next super-block's scales) are in flight while one unit is
+// reduced. Workgroup b covers ids [256 b, 256 b + 256) (thread t owns id
+// 256 b + t) and ends with ARGMAX_STAGE1 over them, as k_mv_logits.
+template <int T, int D>
+__device__ __forceinline__ void lm_lanes_body(const MvArgs& a) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr bool kq = T != QT_Q8_0;  // K-quants: 8 units per super-block of scales
+  const MvLds l = mv_lds(smem, a.k);
+  const int tid = (int)threadIdx.x, lane = tid & 63;
+  const int blk = (int)blockIdx.x * 4 + (tid >> 6);
+  const int U = a.k >> 5;
+  const QMat w = a.seg[0].w;
+  const int SB = U >> 3;  // (K-quants)
+  LaneFrag<T> f[D];
+  LaneHead<T> ha{}, hb{};
+#pragma unroll
+  for (int j = 0; j < D; ++j) f[j] = load_lane_frag<T>(w, blk, j, lane);
+  if constexpr (kq) {
+    ha = load_lane_head<T>(w, blk, 0, lane);
+    hb = load_lane_head<T>(w, blk, min(1, SB - 1), lane);
+  }
+  const MvPro p = mv_pro(a);
+  mv_stage(p, l);
+  const int stopped = __hip_atomic_load(&p.st->stopped, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (stopped) return;
+  mv_norm(p, l);
+  float4* XU = reinterpret_cast<float4*>(l.dl);  // 1.125 K floats: dl and the start of wd
+  xu_build<T>(l.xs, a.k, XU);
+  __syncthreads();
+  float acc = 0.f;
+  // (each unit register is reloaded right after its unit is reduced, so the
+  // D - 1 other units stay in flight; past the last unit the loads repeat
+  // unit U - 1 and are dropped, so that every load is unconditional and the
+  // loop bodies are straight-line code)
+  auto run = [&](int u0, int n, const LaneHead<T>& h) {
+    const float4* xg = XU + 9 * u0;
+#pragma unroll
+    for (int c = 0; c < n; ++c) {
+      acc = acc_lane<T>(f[c % D], h, c, xg + 9 * c, acc);
+      f[c % D] = load_lane_frag<T>(w, blk, min(u0 + c + D, U - 1), lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if constexpr (kq) {
+    // super-blocks in pairs, their scales in two alternating register sets
+    // (ha: even super-blocks, hb: odd), each reloaded two super-blocks ahead
+    int sb = 0;
+    for (; sb + 1 < SB; sb += 2) {
+      run(8 * sb, 8, ha);
+      ha = load_lane_head<T>(w, blk, min(sb + 2, SB - 1), lane);
+      run(8 * sb + 8, 8, hb);
+      hb = load_lane_head<T>(w, blk, min(sb + 3, SB - 1), lane);
+    }
+    if (sb < SB) run(8 * sb, 8, ha);
+  } else {
+    for (int u0 = 0; u0 < U; u0 += D) run(u0, D, ha);  // (U is a multiple of D)
+  }
+  // epilogue: logits, stage-1 penalty and the group argmax (as matvec_body's EPI_LOGITS)
+  float* vals = l.res + 256;
+  uint32_t* idx = (uint32_t*)(vals + 256);
+  const int row = (int)blockIdx.x * 256 + tid;
+  float v = kNegBig;
+  uint32_t id = a.gpt_argmax ? 0u : 0xffffffffu;
+  if (row < a.vocab) {
+    float rv = acc;
+    if (a.logit_scale != 0.f) rv = __fmul_rn(rv, a.logit_scale);
+    a.seg[0].out[row] = rv;
+    if (a.samp->stage1_penalty && bit_test(a.pen_bits, (uint32_t)row)) {
+      const float pen = a.samp->stage1_pen;
+      rv = rv > 0.0f ? __fdiv_rn(rv, pen) : __fmul_rn(rv, pen);
+    }
+    v = rv;
+    id = (uint32_t)row;
+  }
+  vals[tid] = v;
+  idx[tid] = id;
+  __syncthreads();
+  for (int stride = 128; stride >= 1; stride >>= 1) {
+    if (tid < stride) {
+      const float ov = vals[tid + stride];
+      const uint32_t oi = idx[tid + stride];
+      if (a.gpt_argmax ? ov > vals[tid] : better(ov, oi, vals[tid], idx[tid])) {
+        vals[tid] = ov;
+        idx[tid] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    Candidate c;
+    c.value = vals[0];
+    c.index = idx[0];
+    a.cand[blockIdx.x] = c;
+  }
+  if (a.advance_pos && blockIdx.x == 0 && tid == 0) a.st->pos = a.st->pos + 1;
+}
+
+// D units in flight per lane; the row length in units must be a multiple of D
+template <int T, int D>
+__global__ __launch_bounds__(kWg, 3) void k_lm_lanes(const MvArgs a) {
+  lm_lanes_body<T, D>(a);
+}
+
 // ---------------------------------------------------------------------------
 // GQA decode attention, one workgroup per (kv head, chunk of positions).
 //
@@ -845,7 +954,9 @@ hipError_t init_kernel_attributes() {
   (void)hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   (void)hipDeviceGetAttribute(&max_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
   const int want = max_optin > max_block ? max_optin : max_block;
-  const void* fns[43] = {
+  const void* fns[47] = {
+      (const void*)k_lm_lanes<QT_Q4_K, 8>,   (const void*)k_lm_lanes<QT_Q6_K, 8>,   (const void*)k_lm_lanes<QT_Q8_0, 4>,
+      (const void*)k_lm_lanes<QT_Q8_0, 2>,
       (const void*)k_mvr_add_conv,           (const void*)k_mvr_add_gate,
       (const void*)k_mvr_add_bias,           (const void*)k_mvr_add_bias_wide,
       (const void*)k_mvr_store_ln,           (const void*)k_mvr_store_embed_ln,     (const void*)k_mvr_gelu_ln,
@@ -915,6 +1026,21 @@ hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s)
     case EPI_GLU_SILU: hipLaunchKernelGGL(k_mv_swiglu, dim3(grid), dim3(kWg), shmem, s, a); break;
     case EPI_GLU_GELU: hipLaunchKernelGGL(k_mv_geglu, dim3(grid), dim3(kWg), shmem, s, a); break;
     case EPI_LOGITS:
+      if (a.lm_lanes) {
+        // the lane-interleaved copy: 256 ids per workgroup
+        if (a.nseg != 1 || a.lfm_classes || grid * 256 < a.vocab || a.seg[0].w.n < grid * 256 ||
+            (a.seg[0].w.k & (a.seg[0].w.type == QT_Q8_0 ? 31 : 255)) != 0)
+          return hipErrorInvalidValue;
+        const int U = a.seg[0].w.k >> 5;
+        switch (a.seg[0].w.type * 8 + (U % 4 == 0 ? 4 : U % 2 == 0 ? 2 : 0)) {
+          case QT_Q4_K * 8 + 4: hipLaunchKernelGGL((k_lm_lanes<QT_Q4_K, 8>), dim3(grid), dim3(kWg), shmem, s, a); break;
+          case QT_Q6_K * 8 + 4: hipLaunchKernelGGL((k_lm_lanes<QT_Q6_K, 8>), dim3(grid), dim3(kWg), shmem, s, a); break;
+          case QT_Q8_0 * 8 + 4: hipLaunchKernelGGL((k_lm_lanes<QT_Q8_0, 4>), dim3(grid), dim3(kWg), shmem, s, a); break;
+          case QT_Q8_0 * 8 + 2: hipLaunchKernelGGL((k_lm_lanes<QT_Q8_0, 2>), dim3(grid), dim3(kWg), shmem, s, a); break;
+          default: return hipErrorInvalidValue;
+        }
+        break;
+      }
       // one segment, a type known here: the per-type lm_head kernel
       switch (a.nseg == 1 ? a.seg[0].w.type : -1) {
         case QT_Q4_K: hipLaunchKernelGGL(k_mv_logits_t<QT_Q4_K>, dim3(grid), dim3(kWg), shmem, s, a); break;

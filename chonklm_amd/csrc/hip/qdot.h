@@ -142,6 +142,79 @@ __device__ __forceinline__ Frag<QT_Q5_1> load_unit<QT_Q5_1>(const QMat& w, int r
   return f;
 }
 
+// ---- lane-interleaved copy (the lm_head's row-per-lane layout) ----------------
+// Rows in blocks of 64 (one per lane of a wave); per (block, unit) the 64 rows'
+// unit bytes lie side by side, and per (block, super-block) the 64 rows'
+// super-block scales, so that a wave's load of one unit is one contiguous run
+// (1 KiB of Q6_K ql) instead of 64 rows' strided pieces, and a K-quant lane
+// loads its super-block scales once per 8 units. Streams (R = 64 rows, U = K/32
+// units, SB = K/256 super-blocks, i = (blk*U + u)*R + lane, j = (blk*SB + sb)*R + lane):
+//   Q6_K  s0 [i][16] ql (the unit's two 8-byte runs)  s1 [i][8] qh  s2 [j][16] scales  s3 [j][2] d
+//   Q8_0  s0 [i][32] qs                                s1 [i][2] d
+//   Q4_K  s0 [i][16] qs                                s1 [j][16] header (d, dmin, scales)
+// The bytes are those of the GGUF blocks (rows padded with zero blocks to a
+// multiple of 256).
+template <int T>
+struct LaneFrag;  // one unit of one row
+template <int T>
+struct LaneHead;  // one super-block's scales of one row (K-quants)
+template <>
+struct LaneFrag<QT_Q6_K> {
+  uint4 ql;
+  uint2 qh;
+};
+template <>
+struct LaneHead<QT_Q6_K> {
+  uint4 sc;
+  uint32_t d;
+};
+template <>
+struct LaneFrag<QT_Q4_K> {
+  uint4 qs;
+};
+template <>
+struct LaneHead<QT_Q4_K> {
+  uint4 hdr;
+};
+template <>
+struct LaneFrag<QT_Q8_0> {
+  uint4 q0, q1;
+  uint32_t d;
+};
+template <>
+struct LaneHead<QT_Q8_0> {};
+
+template <int T>
+__device__ __forceinline__ LaneFrag<T> load_lane_frag(const QMat& w, int blk, int u, int lane) {
+  const size_t i = ((size_t)blk * (size_t)(w.k >> 5) + u) * 64 + lane;
+  LaneFrag<T> f;
+  if constexpr (T == QT_Q6_K) {
+    f.ql = ldg4(w.s0 + 16 * i);
+    f.qh = ldg2(w.s1 + 8 * i);
+  } else if constexpr (T == QT_Q4_K) {
+    f.qs = ldg4(w.s0 + 16 * i);
+  } else {
+    f.q0 = ldg4(w.s0 + 32 * i);
+    f.q1 = ldg4(w.s0 + 32 * i + 16);
+    f.d = ld_u16(w.s1 + 2 * i);
+  }
+  return f;
+}
+
+template <int T>
+__device__ __forceinline__ LaneHead<T> load_lane_head(const QMat& w, int blk, int sb, int lane) {
+  const size_t j = ((size_t)blk * (size_t)(w.k >> 8) + sb) * 64 + lane;
+  LaneHead<T> h;
+  if constexpr (T == QT_Q6_K) {
+    h.sc = ldg4(w.s2 + 16 * j);
+    h.d = ld_u16(w.s3 + 2 * j);
+  } else if constexpr (T == QT_Q4_K) {
+    h.hdr = ldg4(w.s1 + 16 * j);
+  }
+  (void)j;
+  return h;
+}
+
 // ---- element index of unit-local element e (0..31) within the row ----------
 // Q4_K/Q5_K: e<16 -> low nibble of qs byte e; e>=16 -> high nibble of byte e-16.
 // Q6_K: e = 8*qd + i (quarter qd, i<8).  Q8_0/Q5_x: e is the block element.
@@ -521,6 +594,89 @@ __device__ __forceinline__ float dot_f<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, c
   (void)u;
   const float s = (x.s.x + x.s.y) + (x.s.z + x.s.w);
   return h2f(f.d) * dot_q5f_codes(f.qs, f.qh, x) + h2f(f.m) * s;
+}
+
+// acc + sum over unit c of a super-block (any unit for Q8_0) of x * w for the
+// row-per-lane lm_head. x is in the unit-major layout XU[u * 9 + v] (float4 v
+// = elements 4v .. 4v+3 of unit u in the unit's own element order, then the
+// four 8-element run sums), so that every lane of a wave reads the same
+// 144-byte unit (broadcast reads). The dot_f arithmetic as one fma chain per
+// run (4 cvt + 4 fma per 4 weights).
+template <int T>
+__device__ __forceinline__ float acc_lane(const LaneFrag<T>& f, const LaneHead<T>& h, int c, const float4* xu,
+                                          float acc);
+
+__device__ __forceinline__ float fma4u(float4 a, uint32_t w, float s) {
+  s = fmaf(a.x, ub(w, 0), s);
+  s = fmaf(a.y, ub(w, 1), s);
+  s = fmaf(a.z, ub(w, 2), s);
+  return fmaf(a.w, ub(w, 3), s);
+}
+
+__device__ __forceinline__ uint32_t word4(const uint4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+template <>
+__device__ __forceinline__ float acc_lane<QT_Q6_K>(const LaneFrag<QT_Q6_K>& f, const LaneHead<QT_Q6_K>& h, int c,
+                                                   const float4* xu, float acc) {
+  // unit c: half hh = c / 4, run b = c % 4; scale byte 8 hh + (b >> 1) + 2 qd
+  const int hh = c >> 2, b = c & 3;
+  const float4 s4 = xu[8];
+  const float sr[4] = {s4.x, s4.y, s4.z, s4.w};
+  const uint32_t qa[2] = {f.ql.x, f.ql.y}, qb[2] = {f.ql.z, f.ql.w}, qh[2] = {f.qh.x, f.qh.y};
+  float su = 0.f;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const uint32_t* src = (qd & 1) ? qb : qa;
+    const int shift = qd < 2 ? 0 : 4;
+    float s = -32.0f * sr[qd];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t w = ((src[half] >> shift) & 0x0f0f0f0fu) | (((qh[half] >> (2 * qd)) & 0x03030303u) << 4);
+      s = fma4u(xu[2 * qd + half], w, s);
+    }
+    const int si = 8 * hh + (b >> 1) + 2 * qd;
+    su = fmaf((float)(int8_t)((word4(h.sc, si >> 2) >> (8 * (si & 3))) & 0xffu), s, su);
+  }
+  return fmaf(h2f(h.d), su, acc);
+}
+
+template <>
+__device__ __forceinline__ float acc_lane<QT_Q8_0>(const LaneFrag<QT_Q8_0>& f, const LaneHead<QT_Q8_0>& h, int c,
+                                                   const float4* xu, float acc) {
+  (void)h;
+  (void)c;
+  const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const float4 a = xu[v];
+    s = fmaf(a.x, sb(q[v], 0), s);
+    s = fmaf(a.y, sb(q[v], 1), s);
+    s = fmaf(a.z, sb(q[v], 2), s);
+    s = fmaf(a.w, sb(q[v], 3), s);
+  }
+  return fmaf(h2f(f.d), s, acc);
+}
+
+template <>
+__device__ __forceinline__ float acc_lane<QT_Q4_K>(const LaneFrag<QT_Q4_K>& f, const LaneHead<QT_Q4_K>& h, int c,
+                                                   const float4* xu, float acc) {
+  const int g = c >> 1;
+  const float4 s4 = xu[8];
+  const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    lo = fma4u(xu[v], q[v] & 0x0f0f0f0fu, lo);
+    hi = fma4u(xu[4 + v], (q[v] >> 4) & 0x0f0f0f0fu, hi);
+  }
+  uint32_t sc0, m0, sc1, m1;
+  scale_min(2 * g, h.hdr.y, h.hdr.z, h.hdr.w, &sc0, &m0);
+  scale_min(2 * g + 1, h.hdr.y, h.hdr.z, h.hdr.w, &sc1, &m1);
+  const float d = h2f(h.hdr.x), dmin = h2f(h.hdr.x >> 16);
+  const float pos = fmaf((float)sc1, hi, (float)sc0 * lo);
+  const float neg = fmaf((float)m1, s4.z + s4.w, (float)m0 * (s4.x + s4.y));
+  return fmaf(d, pos, fmaf(-dmin, neg, acc));
 }
 
 // ---- exact dequantization ------------------------------------------------------
