@@ -7,8 +7,9 @@
   tests/golden/make_config_golden.py (the oracle runs the reference's
   token-by-token loop, llama-wgsl-runtime.ts:242-314, in the build
   container; the fixture is keyed by the GGUF file's SHA-256).
-* Decode steps at the configurations' contexts against the oracle run live:
-  logits within 1e-3 (max |d| / max |ref|) and identical ids. The K/V cache
+* Sixteen decode steps at the configurations' contexts against the oracle run
+  live, with this build's fp16 K/V cache and with the reference's fp32 cache
+  (llama-wgsl-runtime.ts:830-831) on both sides: logits within 1e-3 (max |d| / max |ref|) and identical ids. The K/V cache
   holds the same synthetic positions on both sides (SmolLM2: the real prompt),
   so these steps run the kernels at their configuration geometry: decode
   attention with interleaved rotary over a 3-group GQA (SmolLM2), 33 chunks
@@ -18,8 +19,9 @@
   over 192, 594 and 1024 groups.
 * Batched decoding at 64 sequences x 512-token prompts, 128 greedy steps:
   every row follows the batch-1 engine on the same prompt (ids up to the
-  first near-tie of the batch-1 logits, logits at the end); two rows at a
-  short prompt against the oracle.
+  first near-tie of the batch-1 logits, logits at the end); four of the 64
+  rows against the oracle at three positions; two rows at a short prompt
+  against the oracle.
 """
 from __future__ import annotations
 
@@ -81,16 +83,17 @@ def test_config_generate_matches_golden(synth, name):
     loaded.engine.dispose()
 
 
+@pytest.mark.parametrize("kv", ["f16", "f32"])
 @pytest.mark.parametrize("name", CONFIGS)
-def test_config_steps_match_oracle(synth, name):
+def test_config_steps_match_oracle(synth, name, kv):
     w = WORKLOADS[name]
     path = synth(name)
-    ctx = w.prompt_tokens + 16
-    md = w.model_def(path)
+    ctx = w.prompt_tokens + 24
+    md = w.model_def(path, kv_dtype=kv)
     md.max_context = ctx
     loaded = load_llama_wgsl_model(md)
     eng = loaded.engine
-    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=kv == "f16", threads=16)
     prompt = w.prompt(1234)
     samp = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, seed=9)
     if w.prompt_tokens <= 64:
@@ -104,12 +107,12 @@ def test_config_steps_match_oracle(synth, name):
         ref.fake_context(w.prompt_tokens, seed=3)
         tok = prompt[-1]
     hist = list(prompt)
-    for i in range(6):
+    for i in range(16):
         a = eng.run_token(tok, True, penalized_token_ids=hist, seen_ids=hist, **samp)
         b = ref.run_token(tok, True, penalized=hist, seen=hist, **samp)
         e = rel_err(eng.read_logits(), ref.logits())
-        assert e <= 1e-3, f"{name} step {i} at position {eng.position - 1}: logits rel err {e:.3e}"
-        assert a == b, f"{name} step {i}: token {a} != {b}"
+        assert e <= 1e-3, f"{name} ({kv} K/V) step {i} at position {eng.position - 1}: logits rel err {e:.3e}"
+        assert a == b, f"{name} ({kv} K/V) step {i}: token {a} != {b}"
         tok = a
         hist.append(a)
     assert eng.position == ref.position
@@ -175,6 +178,51 @@ def test_batched_64x512_follows_batch1(synth):
                 assert e <= 1e-3, f"row {s}: last-step logits rel err {e:.3e}"
     assert full >= seqs // 2, f"only {full} of {seqs} rows compared over all {STEPS} steps"
     eng.dispose()
+
+
+def test_batched_64x512_rows_match_oracle(synth):
+    """Config 5 at its full size against the oracle: 64 sequences x 512-token prompts,
+    the batched prompt pass and three greedy steps over all 64 rows at once; rows 0,
+    21, 42 and 63 (each with its own page set) are run token by token by four oracle
+    models over the same prompts, and at the prompt's end and the next two positions
+    the row's logits are within 1e-3 of the oracle's and its ids are the oracle's."""
+    name = "qwen3-0.6b-q4_k_m"
+    w = WORKLOADS[name]
+    path = synth(name)
+    seqs, plen, steps = 64, 512, 3
+    md = w.model_def(path)
+    md.max_context = plen + 16
+    loaded = load_llama_wgsl_model(md)
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, w.spec.vocab, plen).tolist() for _ in range(seqs)]
+    b = LlamaWgslBatch(loaded.engine, seqs, plen + 16)
+    check = (0, 21, 42, 63)
+    cur, got_logits = [], {}
+    for s in range(seqs):
+        cur.append(b.prefill(s, prompts[s]))
+        if s in check:
+            got_logits[s] = [b.read_logits(0)]  # (a prefill's logits are its batch's row 0)
+    got_ids = {s: [cur[s]] for s in check}
+    rows = list(range(seqs))
+    for _ in range(steps - 1):
+        cur = b.step(rows, cur)
+        for s in check:
+            got_logits[s].append(b.read_logits(s))
+            got_ids[s].append(cur[s])
+    b.close()
+    loaded.engine.dispose()
+    for s in check:
+        ref = OracleModel(path, w.spec.vocab, w.spec.layers, plen + 16, kv_f16=True, threads=16)
+        for t in prompts[s][:-1]:
+            ref.run_token(t, False)
+        tok = prompts[s][-1]
+        for i in range(steps):
+            want = ref.run_token(tok, True)
+            e = rel_err(got_logits[s][i], ref.logits())
+            assert e <= 1e-3, f"row {s} position {plen - 1 + i}: logits rel err {e:.3e}"
+            assert got_ids[s][i] == want, f"row {s} position {plen - 1 + i}: id {got_ids[s][i]} != {want}"
+            tok = want
+        ref.close()
 
 
 def test_batched_rows_match_oracle_at_config_shape(synth):
