@@ -75,6 +75,7 @@ class EngineInfoC(C.Structure):
         ("kernels_per_step", C.c_int32),
         ("persistent_step", C.c_int32),
         ("noalloc_prefill_rows", C.c_int32),
+        ("spin_attention", C.c_int32),
     ]
 
 

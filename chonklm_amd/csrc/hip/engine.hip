@@ -931,6 +931,17 @@ uint8_t* scratch_address(int device) {
   return (uint8_t*)p;
 }
 
+// Serializes the no-allocation prompt passes on one GPU: every engine on the
+// device shares that device's scratch array.
+std::mutex& scratch_lock(int device) {
+  static std::mutex* mu = new std::mutex();
+  static std::map<int, std::unique_ptr<std::mutex>>* locks = new std::map<int, std::unique_ptr<std::mutex>>();
+  std::lock_guard<std::mutex> l(*mu);
+  std::unique_ptr<std::mutex>& m = (*locks)[device];
+  if (!m) m.reset(new std::mutex());
+  return *m;
+}
+
 // Rows of one no-allocation prompt pass for this model (defined with the row buffers).
 int noalloc_rows_for(const ModelCfg& c);
 
@@ -1504,8 +1515,39 @@ void capture(chonk_engine* e, const std::vector<Launch>& steps, hipGraph_t* g, h
   HIP_OK(hipGraphInstantiate(x, *g, nullptr, nullptr, 0));
 }
 
+// At most one engine per GPU runs the spin-merging decode attention
+// (k_attn_dec): its chunks wait for each other's rows, so its whole grid must
+// be resident at once, and the grids of two engines decoding on different
+// threads could together exceed the device and wait until the time bound.
+// The first engine on a device that qualifies claims the device; engines
+// created while the claim is held use the arrival-counter k_attention (no
+// waiting). The claim ends with the engine.
+struct SpinClaims {
+  std::mutex mu;
+  std::map<int, const chonk_engine*> owner;
+};
+SpinClaims& spin_claims() {
+  static SpinClaims* c = new SpinClaims();
+  return *c;
+}
+bool claim_spin(int device, const chonk_engine* e) {
+  SpinClaims& c = spin_claims();
+  std::lock_guard<std::mutex> l(c.mu);
+  auto it = c.owner.find(device);
+  if (it != c.owner.end() && it->second != e) return false;
+  c.owner[device] = e;
+  return true;
+}
+void release_spin(int device, const chonk_engine* e) {
+  SpinClaims& c = spin_claims();
+  std::lock_guard<std::mutex> l(c.mu);
+  auto it = c.owner.find(device);
+  if (it != c.owner.end() && it->second == e) c.owner.erase(it);
+}
+
 void engine_free(chonk_engine* e) {
   if (!e) return;
+  release_spin(e->device, e);
   (void)hipSetDevice(e->device);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   if (e->exec_logits) (void)hipGraphExecDestroy(e->exec_logits);
@@ -1726,6 +1768,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
                               lc.kv_heads * e->dnchunk))
         e->dec_attn = false;
     }
+    // (another engine on this GPU holds the spin-merging attention: k_attention)
+    if (e->dec_attn && !claim_spin(e->device, e.get())) e->dec_attn = false;
   }
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
@@ -2778,6 +2822,7 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->kernels_per_step = (int32_t)e->kernels_logits.size();
   out->persistent_step = 0;  // (the one-launch-per-token step was retired: the graph ran twice as fast)
   out->noalloc_prefill_rows = e->noalloc_rows;
+  out->spin_attention = e->dec_attn ? 1 : 0;
   return CHONK_OK;
 }
 
@@ -2834,7 +2879,10 @@ int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t 
     if ((int64_t)e->pos + (int64_t)n > e->cfg.ctx)
       throw context_exhausted(e);
     // every row buffer is written before it is read (the operand split writes
-    // its own zero padding), so the previous call's contents need no clearing
+    // its own zero padding), so the previous call's contents need no clearing;
+    // calls of engines on the same GPU take turns (the call returns once its
+    // pass has finished on the device)
+    std::lock_guard<std::mutex> scratch_turn(scratch_lock(e->device));
     RowBufs b;
     row_bufs_layout(e->cfg, e->noalloc_rows, e->scratch, &b);
     HIP_OK(hipMemcpy(e->hist + e->pos, tokens, n * 4, hipMemcpyHostToDevice));

@@ -26,7 +26,11 @@
  * X", "Llama GGUF WGSL does not support architecture X", ...).
  * An engine is not re-entrant: a call made while another call on the same
  * engine is in progress returns CHONK_EBUSY (the reference's `active` guard,
- * :1221-1224). Engines on different threads are independent.
+ * :1221-1224). Engines on different threads are independent: of the engines
+ * on one GPU only the first that qualifies decodes with the spin-merging
+ * attention (chunks of one launch wait for each other, so its grid must be
+ * resident at once); engines created while it exists use the arrival-counter
+ * attention, which never waits, so concurrent decoding cannot stall.
  * A HIP error marks the engine lost; later calls that touch the device
  * (position, info and destroy still answer) fail fast with CHONK_ELOST
  * (the LFM runtime's deviceLost behaviour, lfm-wgsl-runtime.ts:704-707,
@@ -90,6 +94,7 @@ typedef struct {
   int32_t kernels_per_step;         /* per-phase kernels of one decode step (chonk_engine_bench_kernel ids) */
   int32_t persistent_step;          /* always 0 (kept for layout: the one-launch step was retired) */
   int32_t noalloc_prefill_rows;     /* most tokens one chonk_engine_prefill_noalloc call takes (0: none) */
+  int32_t spin_attention;           /* 1: decodes with the spin-merging attention (one engine per GPU) */
 } chonk_engine_info;
 
 typedef struct {
@@ -132,17 +137,20 @@ int chonk_engine_run_token(chonk_engine* e, int32_t token, int32_t need_logits, 
 int chonk_engine_prefill(chonk_engine* e, const int32_t* tokens, size_t n);
 
 /* chonk_engine_prefill without any device allocation. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). It is not for code under
+ * HIP graph capture: the call copies the token ids to the device and waits
+ * for its pass to finish before it returns.
  * The row buffers of the pass come from one 48 MiB device array per GPU,
  * reserved when the library is loaded on that GPU and held until the process
  * ends, instead of the ~50-60 MB that chonk_engine_prefill allocates on its
  * first call. One call takes at most chonk_engine_info.noalloc_prefill_rows
  * tokens (one pass; CHONK_EINVAL beyond that, or when the model's row buffers
- * do not fit). Every call on one GPU shares that GPU's array: calls that
- * overlap in time on one GPU (two engines on two threads) race and must be
- * serialized by the caller. Results equal chonk_engine_prefill's to fp32
- * rounding (passes of a different row count change the GEMMs' K split). */
+ * do not fit). Every call on one GPU shares that GPU's array: calls of
+ * engines on one GPU take turns on a per-GPU lock (a second thread's call
+ * waits until the first has finished). Results equal chonk_engine_prefill's
+ * to fp32 rounding (passes of a different row count change the GEMMs' K
+ * split). */
 int chonk_engine_prefill_noalloc(chonk_engine* e, const int32_t* tokens, size_t n);
 
 /* generateLlamaWgsl: prefix reuse against the previous conversation, prompt
