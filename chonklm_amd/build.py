@@ -8,6 +8,7 @@ they travel with the repository snapshot to the GPU host.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -35,12 +36,38 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libchonk.so")
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     # hipcc's host pass warns about the gfx-only target feature; keep other output
     lines = [ln for ln in proc.stdout.splitlines() if "packed-fp32-ops' is not a recognized" not in ln]
     if proc.returncode != 0:
         raise RuntimeError("build step failed: " + " ".join(cmd) + "\n" + "\n".join(lines))
+    return proc.stdout
+
+
+def _attn_dec_admitted(group: int, hd: int, walk: bool) -> bool:
+    """The engine's rule for the register-resident decode attention (attn_dec_supported)."""
+    return group * hd <= 1536 and not (hd == 256 and group >= 6 and walk)
+
+
+def check_attn_dec_scratch(remarks: str) -> None:
+    """Every k_attn_dec instance the engine may pick keeps its registers (no scratch):
+    the kernel-resource-usage remarks of attn_decode.hip are read back here."""
+    name = None
+    bad = []
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        g = re.search(r"k_attn_decILi(\d+)ELi(\d+)ELb(\d)", name or "")
+        if m and g and int(m.group(1)) > 0:
+            group, hd, walk = int(g.group(1)), int(g.group(2)), g.group(3) == "1"
+            if _attn_dec_admitted(group, hd, walk):
+                bad.append(f"k_attn_dec<{group}, {hd}, {str(walk).lower()}> ({m.group(1)} bytes per lane)")
+    if bad:
+        raise RuntimeError("decode attention instances the engine may pick spill to scratch: " + ", ".join(bad))
 
 
 def build_library(jobs: int = 8) -> Path:
@@ -52,12 +79,16 @@ def build_library(jobs: int = 8) -> Path:
     jobs_list = []
     for src in HIP_SOURCES:
         obj = OBJ_DIR / (src.stem + ".o")
-        jobs_list.append((obj, [hipcc, *gpu, *common, "-c", str(src), "-o", str(obj)]))
+        extra = ["-Rpass-analysis=kernel-resource-usage"] if src.name == "attn_decode.hip" else []
+        jobs_list.append((obj, [hipcc, *gpu, *common, *extra, "-c", str(src), "-o", str(obj)]))
     for src in HOST_SOURCES:
         obj = OBJ_DIR / (src.stem + ".host.o")
         jobs_list.append((obj, ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", str(src), "-o", str(obj)]))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        list(ex.map(lambda j: _run(j[1]), jobs_list))
+        outs = list(ex.map(lambda j: _run(j[1]), jobs_list))
+    for (obj, _), out in zip(jobs_list, outs):
+        if obj.stem == "attn_decode":
+            check_attn_dec_scratch(out)
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, *gpu, "-shared", "-fPIC", "-o", str(tmp), *[str(o) for o, _ in jobs_list], "-lpthread"])
     os.replace(tmp, LIB_PATH)

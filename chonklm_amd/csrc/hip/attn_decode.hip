@@ -484,9 +484,12 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
 }  // namespace
 
 bool attn_dec_supported(int group, int hd, int ctx, int kv_f16) {
-  // (group 8 at head_dim 256 would spill its score operands)
+  // (registers: at head_dim 256 groups 7 and 8 spill to scratch in both variants,
+  // group 6 in the one that walks sub-chunks, used past 128 chunks)
+  const int chunks = (ctx + kDecChunk - 1) / kDecChunk;
+  if (hd == 256 && group >= 6 && chunks > 128) return false;
   return kv_f16 && (hd == 64 || hd == 128 || hd == 256) && group >= 1 && group <= 8 && group * hd <= 1536 &&
-         (ctx + kDecChunk - 1) / kDecChunk <= 128 * kDecSubMax;
+         chunks <= 128 * kDecSubMax;
 }
 
 int attn_dec_sub(int ctx, int per_head) {
@@ -541,6 +544,9 @@ const void* dec_kernel(int group, int hd, bool walk) {
 int attn_dec_resident(int device, int group, int hd, size_t shmem, bool walk) {
   const void* f = dec_kernel(group, hd, walk);
   if (!f) return 0;
+  // an instance that spills to scratch is not used (0: cannot run)
+  hipFuncAttributes at{};
+  if (hipFuncGetAttributes(&at, f) != hipSuccess || at.localSizeBytes != 0) return 0;
   int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, kWg, shmem) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;

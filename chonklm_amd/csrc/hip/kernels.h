@@ -186,7 +186,8 @@ int attn_dec_chunk();
 int attn_dec_sub(int ctx, int per_head);
 size_t attn_dec_shared_bytes(int group, int hd, int nchunk);
 // Workgroups of k_attn_dec that fit on the device at once (its active chunks
-// wait for each other, so the whole grid must be resident).
+// wait for each other, so the whole grid must be resident); 0 for an instance
+// that spills registers to scratch, which the engine then does not use.
 int attn_dec_resident(int device, int group, int hd, size_t shmem, bool walk);
 hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s);
 // cs[p][d] = (cos, sin)(p * inv[d]) for p < ctx, d < half.

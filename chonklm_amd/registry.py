@@ -202,5 +202,16 @@ WORKLOADS: dict[str, Workload] = {
                                           kv_heads=1, head_dim=128, ffn=512, vocab=1500, context_length=4096,
                                           rope_theta=1000000.0, norm_eps=1e-6, sliding_window=16, seed=17),
                  max_context=96, eos_ids=[1, 106], prompt_tokens=40, decode_tokens=24, temperature=0.8, top_k=40),
+        # long-context decode attention with 512-position windows (5 of 6 layers) past 8192
+        # positions, where each attention workgroup walks several 64-position sub-chunks:
+        # head_dim 256 with a 4-head group (Gemma-3's geometry) and head_dim 64
+        Workload("tiny-gemma3-hd256", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=512, layers=6, heads=4,
+                                                kv_heads=1, head_dim=256, ffn=512, vocab=1000, context_length=16384,
+                                                rope_theta=1000000.0, norm_eps=1e-6, sliding_window=512, seed=71),
+                 max_context=9000, eos_ids=[1, 106], prompt_tokens=16, decode_tokens=16),
+        Workload("tiny-gemma3-hd64", SynthSpec(arch="gemma3", recipe="q4_k_m", hidden=256, layers=6, heads=8,
+                                               kv_heads=2, head_dim=64, ffn=512, vocab=1000, context_length=16384,
+                                               rope_theta=1000000.0, norm_eps=1e-6, sliding_window=512, seed=73),
+                 max_context=9000, eos_ids=[1, 106], prompt_tokens=16, decode_tokens=16),
     ]
 }

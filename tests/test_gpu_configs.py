@@ -356,3 +356,35 @@ def test_decode_attention_walks_sub_chunks_at_long_context(synth):
             tok = a
     eng.dispose()
     ref.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-gemma3-hd256", "tiny-gemma3-hd64"])
+def test_decode_attention_windows_past_8192_positions(synth, name):
+    """Sliding windows of 512 positions (5 of 6 layers) on a 9000-position cache, where each
+    attention workgroup walks two 64-position sub-chunks: head_dim 256 with a 4-head group
+    (Gemma-3's geometry) and head_dim 64. Positions whose window starts in the middle of a
+    workgroup's first sub-chunk (8211: start 7700), of its second (8300: start 7789), on a
+    workgroup boundary (8959: start 8448), near the cache's end, and a short position;
+    logits within 1e-3 of the oracle and identical ids."""
+    w = WORKLOADS[name]
+    path = synth(name)
+    ctx = 9000
+    md = w.model_def(path)
+    md.max_context = ctx
+    loaded = load_llama_wgsl_model(md)
+    eng = loaded.engine
+    assert eng.info["spin_attention"] == 1 or eng.info["kv_dtype"] != 0
+    ref = OracleModel(path, w.spec.vocab, w.spec.layers, ctx, kv_f16=True, threads=16)
+    tok = 29
+    for pos in (100, 8211, 8300, 8959, 8997):
+        eng.fake_context(pos, seed=pos)
+        ref.fake_context(pos, seed=pos)
+        for i in range(2):
+            a = eng.run_token(tok, True)
+            b = ref.run_token(tok, True)
+            e = rel_err(eng.read_logits(), ref.logits())
+            assert e <= 1e-3, f"{name} position {pos + i}: logits rel err {e:.3e}"
+            assert a == b, f"{name} position {pos + i}: token {a} != {b}"
+            tok = a
+    eng.dispose()
+    ref.close()
