@@ -11,6 +11,7 @@
 // the products accumulated in fp32 by gfx950's v_mfma_f32_16x16x32_f16.
 #include <hip/hip_runtime.h>
 #include <cstdlib>
+#include <cstring>
 
 #include <algorithm>
 
@@ -336,6 +337,490 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       }
     }
   }
+}
+
+// ---- decode-batch GEMM (at most 64 token rows) ------------------------------------
+//
+// With 64 or fewer token rows the GEMM streams weights: every weight is used
+// by at most 64 products, so staging dequantized tiles through LDS (k_gemm)
+// costs more than the products. Here each wave owns 64 weight rows x all 64
+// token rows over a quarter of the workgroup's K range, with no LDS for the
+// operands: the x planes are loaded straight into MFMA A operands (lane l:
+// token l % 16 of each 16-token tile, k 8 (l / 16) .. + 8 of the 32-k step)
+// and the weights are dequantized in registers into B operands (lane l: row
+// l % 16 of each 16-row tile, the same 8 k), as fp16 hi + lo of W 2^ws; three
+// MFMAs per step (Ah Bh + Al Bh + Ah Bl). The lane's weight bytes for its 8 k
+// are consecutive in the striped rows: Q4_K sub-blocks 2c and 2c+1 share the
+// bytes qs[32c + 8g .. + 8] (low / high nibbles), Q6_K's four 32-k quarters of
+// a 128-k half share ql and qh bytes the same way, so the loads of a block
+// (64 k of Q4_K, 128 k of Q6_K) are used whole. The four waves' sums meet in
+// LDS at the end (in wave order) and the workgroup writes its K split's partial.
+
+constexpr int kSkRows = 64;  // weight rows per wave (and per workgroup)
+
+__device__ __forceinline__ half8_t pack8(const float (&w)[8]) {
+  half8_t h;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = (_Float16)w[i];
+  return h;
+}
+// hi = fp16(w), lo = fp16(w - hi)
+__device__ __forceinline__ void split8(const float (&w)[8], half8_t& h, half8_t& l) {
+  h = pack8(w);
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = w[i] - (float)h[i];
+  l = pack8(r);
+}
+__device__ __forceinline__ float nib(uint32_t w, int i) { return (float)((w >> (4 * i)) & 15u); }
+
+// A block is 64 k: two 32-k steps whose weights the lane reads from one run of
+// bytes (Q4_K: sub-blocks 2c and 2c + 1 of qs[32c + 8g .. + 8], low and high
+// nibbles; Q6_K: quarters p and p + 2 of a 128-k half, low and high nibbles of
+// ql run p, the half's qh bits 2p and 2p + 4).
+template <int T>
+struct SkBlock;  // the lane's weight bytes of one block for one row
+template <>
+struct SkBlock<QT_Q4_K> {
+  uint2 qs;      // qs[32c + 8g .. + 8]
+  uint4 hdr;     // the super-block header (d, dmin, scales)
+};
+template <>
+struct SkBlock<QT_Q6_K> {
+  uint2 ql;      // ql[64h + 32p + 8g .. + 8]
+  uint2 qh;      // qh[32h + 8g .. + 8]
+  uint2 sc;      // the half's 8 scales sc[8h .. + 8]
+  uint32_t d;
+};
+constexpr int kSkBlockK = 64;
+
+// First column of step s2 (0 or 1) of block blk.
+template <int T>
+__device__ __forceinline__ int sk_col(int blk, int s2) {
+  if constexpr (T == QT_Q4_K) return 64 * blk + 32 * s2;
+  // Q6_K block blk: super-block blk / 4, half (blk / 2) % 2, run p = blk % 2; quarter p + 2 s2
+  return 256 * (blk >> 2) + 128 * ((blk >> 1) & 1) + 32 * ((blk & 1) + 2 * s2);
+}
+
+template <int T>
+__device__ __forceinline__ SkBlock<T> sk_load(const QMat& w, int row, int blk, int g) {
+  const size_t K = (size_t)w.k;
+  SkBlock<T> b;
+  if constexpr (T == QT_Q4_K) {
+    b.qs = ldg2(w.s0 + row * (K / 2) + 32 * blk + 8 * g);
+    b.hdr = ldg4(w.s1 + row * (K / 16) + 16 * (blk >> 2));
+  } else {
+    const int sb = blk >> 2, h = (blk >> 1) & 1, p = blk & 1;
+    b.ql = ldg2(w.s0 + row * (K / 2) + 128 * sb + 64 * h + 32 * p + 8 * g);
+    b.qh = ldg2(w.s1 + row * (K / 4) + 64 * sb + 32 * h + 8 * g);
+    b.sc = ldg2(w.s2 + row * (K / 16) + 16 * sb + 8 * h);
+    b.d = ld_u16(w.s3 + 2 * (row * (K / 256) + sb));
+  }
+  return b;
+}
+
+// The lane's 8 weights (times 2^ws) of step s2 of the block.
+template <int T>
+__device__ __forceinline__ void sk_weights(const SkBlock<T>& b, int blk, int s2, int g, float wsc, float (&w)[8]) {
+  if constexpr (T == QT_Q4_K) {
+    // sub-block j = 2c + s2 of the super-block: nibble s2 of the lane's bytes
+    const int j = ((blk & 3) << 1) + s2;
+    uint32_t sc, m;
+    scale_min(j, b.hdr.y, b.hdr.z, b.hdr.w, &sc, &m);
+    const float dsc = h2f(b.hdr.x) * (float)sc * wsc, dm = h2f(b.hdr.x >> 16) * (float)m * wsc;
+    // four codes per word at once: byte i = nibble s2 of the lane's byte i
+    const uint32_t c0 = (b.qs.x >> (4 * s2)) & 0x0f0f0f0fu, c1 = (b.qs.y >> (4 * s2)) & 0x0f0f0f0fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = fmaf(dsc, ub(c0, i), -dm);
+      w[4 + i] = fmaf(dsc, ub(c1, i), -dm);
+    }
+  } else {
+    // quarter q = p + 2 s2 of the half: nibble s2 of the ql run, qh bits 2q;
+    // the lane's 8 k lie in sub-block 2q + (g >> 1) of the half
+    const int q = (blk & 1) + 2 * s2;
+    const int si = 2 * q + (g >> 1);
+    const uint32_t sw = si < 4 ? b.sc.x : b.sc.y;
+    const float dsc = h2f(b.d) * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu) * wsc, off = -32.0f * dsc;
+    // four 6-bit codes per word at once (byte i: low 4 bits from ql, bits 4-5 from qh)
+    const uint32_t c0 = ((b.ql.x >> (4 * s2)) & 0x0f0f0f0fu) | (((b.qh.x >> (2 * q)) & 0x03030303u) << 4);
+    const uint32_t c1 = ((b.ql.y >> (4 * s2)) & 0x0f0f0f0fu) | (((b.qh.y >> (2 * q)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = fmaf(dsc, ub(c0, i), off);
+      w[4 + i] = fmaf(dsc, ub(c1, i), off);
+    }
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(kWg, 2) void k_gemm_sk(GemmArgs a) {
+  extern __shared__ __align__(16) float ssm[];
+  constexpr int BK = kSkBlockK;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kSkRows;
+  const int N = a.n_all ? a.n_all : a.w.n;
+  const int seg = a.n_all ? (n0 >= a.n2 ? 2 : (n0 >= a.n1 ? 1 : 0)) : 0;
+  const int sb0 = seg == 2 ? a.n2 : (seg == 1 ? a.n1 : 0);
+  QMat wm = a.w;
+#define CHONK_PICK_W(f) wm.f = seg == 2 ? a.w3.f : (seg == 1 ? a.w2.f : a.w.f)
+  CHONK_PICK_W(s0);
+  CHONK_PICK_W(s1);
+  CHONK_PICK_W(s2);
+  CHONK_PICK_W(s3);
+  CHONK_PICK_W(n);
+#undef CHONK_PICK_W
+  // this workgroup's blocks (split blockIdx.z of ksplit), then this wave's quarter
+  const int nblk = a.w.k / BK;
+  const int z_lo = (int)((int64_t)nblk * blockIdx.z / a.ksplit), z_hi = (int)((int64_t)nblk * (blockIdx.z + 1) / a.ksplit);
+  const int b_lo = z_lo + (z_hi - z_lo) * wave / 4, b_hi = z_lo + (z_hi - z_lo) * (wave + 1) / 4;
+  const float wsc = ldexpf(1.0f, a.ws);
+  // rows of the lane in the matrix (clamped: a ragged tile loads a valid row, its sums are dropped)
+  int rows[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) rows[rt] = min(n0 + 16 * rt + r16, N - 1) - sb0;
+  // token rows of the lane's A operands, clamped: rows past a.t load a valid row
+  // and their sums are never written
+  int xrow[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) xrow[tt] = min(16 * tt + r16, a.t - 1);
+  // the epilogue's operand scales, requested up front (read from LDS at the end)
+  if (tid < a.t) ssm[4 * 64 * kSkRows + tid] = a.xscale[tid];
+
+  float4_t acc[4][4];  // [token tile][row tile]: lane holds tokens 16 tt + 4 g + i, row 16 rt + r16
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  SkBlock<T> cur[4];
+  if (b_lo < b_hi) {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) cur[rt] = sk_load<T>(wm, rows[rt], b_lo, g);
+  }
+  for (int blk = b_lo; blk < b_hi; ++blk) {
+    // the next block's bytes are requested before this one is reduced (the
+    // last block reloads itself, so that the loads stay unconditional)
+    SkBlock<T> nxt[4];
+    const int bn = min(blk + 1, b_hi - 1);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) nxt[rt] = sk_load<T>(wm, rows[rt], bn, g);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int k0 = sk_col<T>(blk, s2) + 8 * g;  // this lane's 8 k of the step
+      half8_t ah[4], al[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const size_t off = (size_t)xrow[tt] * a.kpad + k0;
+        ah[tt] = *gbl((const half8_t*)(a.xh + off));
+        al[tt] = *gbl((const half8_t*)(a.xl + off));
+      }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        float w[8];
+        sk_weights<T>(cur[rt], blk, s2, g, wsc, w);
+        half8_t bh, bl;
+        split8(w, bh, bl);
+        // (the four token tiles' chains interleaved: no MFMA waits on the one before it)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bh, acc[tt][rt]);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(al[tt], bh, acc[tt][rt]);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bl, acc[tt][rt]);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) cur[rt] = nxt[rt];
+  }
+  // the four waves' sums, added in wave order: [wave][token][row] floats
+  float* red = ssm;
+  float* xs = ssm + 4 * 64 * kSkRows;  // the token rows' operand scales
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(wave * 64 + 16 * tt + 4 * g + i) * kSkRows + 16 * rt + r16] = acc[tt][rt][i];
+  __syncthreads();
+  // thread (tg, r) writes row n0 + r of tokens tg, tg + 4, ...: one coalesced
+  // 256-byte run per token and store instruction
+  const int r = tid & 63, tg = tid >> 6, n = n0 + r;
+  if (n < N) {
+    const float wun = ldexpf(1.0f, -a.ws);
+    for (int t = tg; t < a.t; t += 4) {
+      const int e = t * kSkRows + r;
+      const float v = (((red[e] + red[64 * kSkRows + e]) + red[2 * 64 * kSkRows + e]) + red[3 * 64 * kSkRows + e]) *
+                      (wun * xs[t]);
+      if (a.ksplit > 1 || a.defer) {
+        a.part[((size_t)blockIdx.z * a.t + t) * N + n] = v;
+      } else if (a.epi == GEMM_ADD) {
+        float* y = a.y + (size_t)t * a.ldy + n;
+        *y = __fadd_rn(*y, v);
+      } else {
+        a.y[(size_t)t * a.ldy + n] = v;
+      }
+    }
+  }
+}
+
+// The same with exactly one 64-k block per wave (the K split of the decode
+// step's layer GEMMs): every load of the wave — its x operands, copied
+// straight into its own 16 KiB of LDS, and its weight bytes — is issued at
+// entry and awaited once, so the wave pays one memory round trip before its
+// two steps of products. LDS per wave: [plane][step][token][32 halves].
+template <int T>
+__global__ __launch_bounds__(kWg, 2) void k_gemm_sk1(GemmArgs a) {
+  extern __shared__ __align__(16) float ssm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kSkRows;
+  const int N = a.n_all ? a.n_all : a.w.n;
+  const int seg = a.n_all ? (n0 >= a.n2 ? 2 : (n0 >= a.n1 ? 1 : 0)) : 0;
+  const int sb0 = seg == 2 ? a.n2 : (seg == 1 ? a.n1 : 0);
+  QMat wm = a.w;
+#define CHONK_PICK_W(f) wm.f = seg == 2 ? a.w3.f : (seg == 1 ? a.w2.f : a.w.f)
+  CHONK_PICK_W(s0);
+  CHONK_PICK_W(s1);
+  CHONK_PICK_W(s2);
+  CHONK_PICK_W(s3);
+  CHONK_PICK_W(n);
+#undef CHONK_PICK_W
+  // this wave's block: one per wave, the workgroup's four in a row
+  const int blk = (int)blockIdx.z * 4 + wave;
+  _Float16* xw = (_Float16*)ssm + (size_t)wave * (2 * 2 * 64 * 32);  // this wave's x operands
+  float* xs = ssm + 4 * 64 * kSkRows;                                // the token rows' operand scales
+  // x: 16 copies of 1 KiB (16 tokens x 64 bytes each); lane l moves token
+  // 16 i + l / 4, piece l % 4 (token rows past a.t repeat the last row: their
+  // sums are never written)
+  {
+    const int tok = lane >> 2, pc = lane & 3;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = min(16 * i + tok, a.t - 1);
+          const _Float16* src = (p ? a.xl : a.xh) + (size_t)t * a.kpad + sk_col<T>(blk, s2) + 8 * pc;
+          __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)(xw + ((p * 2 + s2) * 64 + 16 * i) * 32), 16,
+                                           0, 0);
+        }
+  }
+  const float wsc = ldexpf(1.0f, a.ws);
+  SkBlock<T> bk[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) bk[rt] = sk_load<T>(wm, min(n0 + 16 * rt + r16, N - 1) - sb0, blk, g);
+  if (tid < a.t) xs[tid] = a.xscale[tid];
+  __builtin_amdgcn_s_waitcnt(0);  // (the copies into LDS land before they are read)
+  __syncthreads();
+  float4_t acc[4][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    half8_t ah[4], al[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      ah[tt] = *(const half8_t*)(xw + ((0 * 2 + s2) * 64 + 16 * tt + r16) * 32 + 8 * g);
+      al[tt] = *(const half8_t*)(xw + ((1 * 2 + s2) * 64 + 16 * tt + r16) * 32 + 8 * g);
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      float w[8];
+      sk_weights<T>(bk[rt], blk, s2, g, wsc, w);
+      half8_t bh, bl;
+      split8(w, bh, bl);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bh, acc[tt][rt]);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(al[tt], bh, acc[tt][rt]);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bl, acc[tt][rt]);
+    }
+  }
+  __syncthreads();  // every wave has read its x operands (the area is reused below)
+  float* red = ssm;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(wave * 64 + 16 * tt + 4 * g + i) * kSkRows + 16 * rt + r16] = acc[tt][rt][i];
+  __syncthreads();
+  const int r = tid & 63, tg = tid >> 6, n = n0 + r;
+  if (n < N) {
+    const float wun = ldexpf(1.0f, -a.ws);
+    for (int t = tg; t < a.t; t += 4) {
+      const int e = t * kSkRows + r;
+      const float v = (((red[e] + red[64 * kSkRows + e]) + red[2 * 64 * kSkRows + e]) + red[3 * 64 * kSkRows + e]) *
+                      (wun * xs[t]);
+      a.part[((size_t)blockIdx.z * a.t + t) * N + n] = v;
+    }
+  }
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// A workgroup barrier that orders LDS accesses only: no wait for the global
+// loads in flight (__syncthreads waits for every outstanding memory access).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same for a matrix with many row groups (the lm_head): a workgroup owns
+// 4 x 64 weight rows over the whole K, the four waves sharing each 64-k block
+// of x operands, copied into LDS one block ahead (two buffers; each wave
+// copies a quarter); every wave writes its own rows' results. Per block:
+// weights of the next block and its x copies are issued, then this block's
+// copies are awaited (s_waitcnt counts the loads issued since) and the waves
+// meet at a barrier before the products.
+template <int T>
+__global__ __launch_bounds__(kWg, 2) void k_gemm_lm(GemmArgs a) {
+  extern __shared__ __align__(16) float ssm[];
+  constexpr int W = T == QT_Q4_K ? 8 : 16;  // weight loads per block and wave (4 row tiles)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * (4 * kSkRows) + wave * kSkRows;  // this wave's rows
+  const int N = a.w.n, nblk = a.w.k / kSkBlockK;
+  _Float16* xb = (_Float16*)ssm;  // [buffer][plane][step][token][32 halves]
+  float* xs = (float*)(xb + 2 * (2 * 2 * 64 * 32));
+  const float wsc = ldexpf(1.0f, a.ws);
+  int rows[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) rows[rt] = min(n0 + 16 * rt + r16, N - 1);
+  // x of block b into buffer b & 1: this wave's four of its sixteen 1-KiB copies
+  const int tok = lane >> 2, pc = lane & 3;
+  auto copy_x = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = wave * 4 + j, p = c >> 3, s2 = (c >> 2) & 1, i = c & 3;
+      const int t = min(16 * i + tok, a.t - 1);
+      const _Float16* src = (p ? a.xl : a.xh) + (size_t)t * a.kpad + sk_col<T>(b, s2) + 8 * pc;
+      __builtin_amdgcn_global_load_lds((gmem_void*)src,
+                                       (lds_void*)(xb + (((b & 1) * 4 + p * 2 + s2) * 64 + 16 * i) * 32), 16, 0, 0);
+    }
+  };
+  if (tid < a.t) xs[tid] = a.xscale[tid];
+  SkBlock<T> cur[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) cur[rt] = sk_load<T>(a.w, rows[rt], 0, g);
+  __builtin_amdgcn_sched_barrier(0);
+  copy_x(0);
+  __builtin_amdgcn_sched_barrier(0);
+  float4_t acc[4][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < nblk; ++b) {
+    // the next block's weights, then its x copies (the last block copies
+    // itself into the other buffer, which is not read again: the loop body
+    // stays branch-free, so every wait counts exactly)
+    const int bn = min(b + 1, nblk - 1);
+    SkBlock<T> nxt[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) nxt[rt] = sk_load<T>(a.w, rows[rt], bn, g);
+    __builtin_amdgcn_sched_barrier(0);
+    copy_x(bn);
+    __builtin_amdgcn_sched_barrier(0);
+    // this block's copies have landed once at most the loads issued after
+    // them are outstanding: the next block's W weight loads and 4 copies
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(W + 4));
+    // (a bare barrier: __syncthreads would also wait for the loads in flight)
+    lds_barrier();
+    const _Float16* xc = xb + (size_t)(b & 1) * 4 * 64 * 32;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      half8_t ah[4], al[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        ah[tt] = *(const half8_t*)(xc + ((0 * 2 + s2) * 64 + 16 * tt + r16) * 32 + 8 * g);
+        al[tt] = *(const half8_t*)(xc + ((1 * 2 + s2) * 64 + 16 * tt + r16) * 32 + 8 * g);
+      }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        float w[8];
+        sk_weights<T>(cur[rt], b, s2, g, wsc, w);
+        half8_t bh, bl;
+        split8(w, bh, bl);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bh, acc[tt][rt]);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(al[tt], bh, acc[tt][rt]);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt][rt] = mfma32(ah[tt], bl, acc[tt][rt]);
+      }
+    }
+    lds_barrier();  // every wave has read buffer b & 1 before block b + 2's copies overwrite it
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) cur[rt] = nxt[rt];
+  }
+  const float wun = ldexpf(1.0f, -a.ws);
+  const bool add = a.epi == GEMM_ADD;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * tt + 4 * g + i;
+      if (t >= a.t) continue;
+      const float sc = wun * xs[t];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const int n = n0 + 16 * rt + r16;
+        if (n >= N) continue;
+        float* y = a.y + (size_t)t * a.ldy + n;
+        const float v = acc[tt][rt][i] * sc;
+        if (add)
+          *y = __fadd_rn(*y, v);
+        else
+          *y = v;
+      }
+    }
+}
+
+size_t gemm_lm_shared_bytes() { return sizeof(_Float16) * 2 * (2 * 2 * 64 * 32) + sizeof(float) * 64; }
+
+size_t gemm_sk_shared_bytes() { return sizeof(float) * (4 * 64 * kSkRows + 64); }
+
+// The decode-batch GEMM applies: at most 64 token rows and a K-quant type it covers.
+bool gemm_sk_applies(const GemmArgs& a) {
+  static const bool off = [] {
+    const char* v = std::getenv("CHONK_GEMM");
+    return v && std::strcmp(v, "tiles") == 0;
+  }();
+  return !off && a.t >= 1 && a.t <= 64 && (a.w.type == QT_Q4_K || a.w.type == QT_Q6_K) && a.w.k % 256 == 0 &&
+         a.kpad >= a.w.k;
+}
+
+// K split of a decode-batch GEMM: about 256 workgroups (one per CU), at least
+// one block per wave.
+int gemm_sk_split(const GemmArgs& a, int row_groups) {
+  const int nblk = a.w.k / kSkBlockK;
+  int ks = std::max(1, std::min(kMaxDeferSplit, (256 + row_groups - 1) / row_groups));
+  while (ks > 1 && nblk / ks < 4) --ks;
+  return ks;
+}
+
+hipError_t launch_gemm_sk(const GemmArgs& a, int n_rows, hipStream_t s) {
+  const dim3 grid((n_rows + kSkRows - 1) / kSkRows, 1, a.ksplit);
+  const size_t sh = gemm_sk_shared_bytes();
+  if (a.w.type == QT_Q4_K)
+    hipLaunchKernelGGL(k_gemm_sk<QT_Q4_K>, grid, dim3(kWg), sh, s, a);
+  else
+    hipLaunchKernelGGL(k_gemm_sk<QT_Q6_K>, grid, dim3(kWg), sh, s, a);
+  return hipGetLastError();
 }
 
 // y[t][n] (=|+=) the K-split partial sums, added in split order.
@@ -1169,6 +1654,28 @@ size_t fattn_shared_bytes(int hd) {
 
 hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
   GemmArgs a = a0;
+  if (!a.n_all && gemm_sk_applies(a) && a.w.n >= 128 * 4 * kSkRows) {
+    // many row groups (the lm_head): four per workgroup over the whole K, x shared in LDS
+    const dim3 grid((a.w.n + 4 * kSkRows - 1) / (4 * kSkRows));
+    if (a.w.type == QT_Q4_K)
+      hipLaunchKernelGGL(k_gemm_lm<QT_Q4_K>, grid, dim3(kWg), gemm_lm_shared_bytes(), s, a);
+    else
+      hipLaunchKernelGGL(k_gemm_lm<QT_Q6_K>, grid, dim3(kWg), gemm_lm_shared_bytes(), s, a);
+    return hipGetLastError();
+  }
+  if (!a.n_all && gemm_sk_applies(a)) {
+    const int groups = (a.w.n + kSkRows - 1) / kSkRows;
+    int ks = a.part ? gemm_sk_split(a, groups) : 1;
+    while (ks > 1 && (int64_t)ks * a.t * a.w.n > a.part_cap) --ks;
+    a.ksplit = ks;
+    a.defer = 0;
+    hipError_t e = launch_gemm_sk(a, a.w.n, s);
+    if (e != hipSuccess || ks == 1) return e;
+    const int64_t total = (int64_t)a.t * a.w.n;
+    const int blocks = (int)std::min<int64_t>((total + kWg - 1) / kWg, 4096);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(kWg), 0, s, a);
+    return hipGetLastError();
+  }
   const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
   a.ksplit = 1;
@@ -1207,6 +1714,33 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
       return hipErrorInvalidValue;
   }
   if ((int64_t)a.t * N > region_cap) return hipErrorInvalidValue;
+  if (gemm_sk_applies(a)) {
+    // one 64-k block per wave when the partial sums of that split fit
+    const int ks1 = a.w.k / kSkBlockK / 4;
+    const bool one = ks1 <= kMaxDeferSplit && (int64_t)ks1 * a.t * N <= region_cap;
+    int ks = one ? ks1 : gemm_sk_split(a, (N + kSkRows - 1) / kSkRows);
+    while (ks > 1 && (int64_t)ks * a.t * N > region_cap) --ks;
+    a.ksplit = ks;
+    a.part = region;
+    a.defer = 1;
+    hipError_t e;
+    if (one) {
+      const dim3 grid((N + kSkRows - 1) / kSkRows, 1, ks);
+      if (a.w.type == QT_Q4_K)
+        hipLaunchKernelGGL(k_gemm_sk1<QT_Q4_K>, grid, dim3(kWg), gemm_sk_shared_bytes(), s, a);
+      else
+        hipLaunchKernelGGL(k_gemm_sk1<QT_Q6_K>, grid, dim3(kWg), gemm_sk_shared_bytes(), s, a);
+      e = hipGetLastError();
+    } else {
+      e = launch_gemm_sk(a, N, s);
+    }
+    out->p = region;
+    out->n = N;
+    out->ld = N;
+    out->ks = ks;
+    out->zs = (int64_t)a.t * N;
+    return e;
+  }
   const int tiles = ((N + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
   // split K until about two workgroups per CU are busy; a decode batch (one
@@ -1244,6 +1778,11 @@ hipError_t init_gemm_attributes() {
                         (const void*)k_gemm<QT_Q8_0>, (const void*)k_gemm<QT_Q5_0>, (const void*)k_gemm<QT_Q5_1>};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh);
+    if (e != hipSuccess) return e;
+  }
+  for (const void* f : {(const void*)k_gemm_sk<QT_Q4_K>, (const void*)k_gemm_sk<QT_Q6_K>,
+                        (const void*)k_gemm_sk1<QT_Q4_K>, (const void*)k_gemm_sk1<QT_Q6_K>}) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_sk_shared_bytes());
     if (e != hipSuccess) return e;
   }
   const void* fa[8] = {(const void*)k_pf_fattn<32, false>,  (const void*)k_pf_fattn<64, false>,
@@ -1366,3 +1905,4 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
 #undef CHONK_BD_CASE
 }
 }  // namespace chonk
+
