@@ -83,6 +83,14 @@ template <class T>
 __device__ __forceinline__ __attribute__((address_space(1))) T* gblw(T* p) {
   return (__attribute__((address_space(1))) T*)p;
 }
+// Load of a workgroup-uniform address through the scalar data cache, for data
+// that nothing writes while the kernel runs (row tables, page tables). Scalar
+// loads have their own counter, so waiting for one never waits for the vector
+// loads in flight. (A non-uniform address falls back to a vector load.)
+template <class T>
+__device__ __forceinline__ T ld_scalar(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // 16 / 8 / 4-byte global loads (HIP's uint4 / uint2 cannot be assigned from

@@ -39,46 +39,76 @@ __device__ __forceinline__ float4_t mfma32(half8_t a, half8_t b, float4_t c) {
 
 constexpr int kMaxDeferSplit = 16;  // K split of a deferred GEMM (loads of a sum issued together)
 
-// Row t of a deferred result, elements j0 + S * e for e < 4 (zero past n):
-// every load of the four sums is issued before any is added, so a call costs
-// one memory round trip; the sums add the partials in split order.
-template <int S = kWg>
-__device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float (&v)[4]) {
+// Elements j[e] (valid columns) of row t of a deferred result: the partials
+// are read four splits at a time, every load of a round issued before any is
+// added (split indices past ks are clamped to the last split and their sums
+// not taken, so no load sits behind a branch: a conditional load makes the
+// compiler wait for every outstanding load where the paths join); the sums
+// add the partials in split order. With ks <= 4 a call costs one memory round
+// trip for all N elements.
+// part_gather in two halves, so that the first round's loads can be issued
+// early and summed where the values are needed: part_issue loads splits 0..3
+// (clamped to the last split) of elements j[e]; part_finish adds them in split
+// order and reads any further splits four at a time.
+template <int N>
+__device__ __forceinline__ void part_issue(const PartSum& P, int t, const int (&j)[N], float (&w)[N][4]) {
   const float* q = P.p + (int64_t)t * P.ld;
-  if (P.ks == 1) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = j0 + S * e < P.n ? q[j0 + S * e] : 0.f;
-    return;
+  for (int e = 0; e < N; ++e)
+#pragma unroll
+    for (int z = 0; z < 4; ++z) w[e][z] = q[(int64_t)min(z, P.ks - 1) * P.zs + j[e]];
+}
+template <int N>
+__device__ __forceinline__ void part_finish(const PartSum& P, int t, const int (&j)[N], float (&w)[N][4],
+                                            float (&v)[N]) {
+  const float* q = P.p + (int64_t)t * P.ld;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    v[e] = w[e][0];
+#pragma unroll
+    for (int z = 1; z < 4; ++z) v[e] = z < P.ks ? v[e] + w[e][z] : v[e];
   }
-  float w[4][kMaxDeferSplit];
+  for (int z0 = 4; z0 < P.ks; z0 += 4) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int j = min(j0 + S * e, P.n - 1);
+    for (int e = 0; e < N; ++e)
 #pragma unroll
-    for (int z = 0; z < kMaxDeferSplit; ++z) w[e][z] = z < P.ks ? q[(int64_t)z * P.zs + j] : 0.f;
-  }
+      for (int z = 0; z < 4; ++z) w[e][z] = q[(int64_t)min(z0 + z, P.ks - 1) * P.zs + j[e]];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float a = w[e][0];
+    for (int e = 0; e < N; ++e)
 #pragma unroll
-    for (int z = 1; z < kMaxDeferSplit; ++z)
-      if (z < P.ks) a += w[e][z];
-    v[e] = j0 + S * e < P.n ? a : 0.f;
+      for (int z = 0; z < 4; ++z) v[e] = z0 + z < P.ks ? v[e] + w[e][z] : v[e];
   }
 }
 
-// Element j of row t of a deferred result (the partials added in split order).
-__device__ __forceinline__ float part_at(const PartSum& P, int t, int j) {
-  const float* q = P.p + (int64_t)t * P.ld + j;
-  if (P.ks == 1) return q[0];
-  float w[kMaxDeferSplit];
+// Elements j[e] (valid columns) of row t of a deferred result: the partials
+// are read four splits at a time, every load of a round issued before any is
+// added (split indices past ks are clamped to the last split and their sums
+// not taken, so no load sits behind a branch: a conditional load makes the
+// compiler wait for every outstanding load where the paths join); the sums
+// add the partials in split order. With ks <= 4 a call costs one memory round
+// trip for all N elements.
+template <int N>
+__device__ __forceinline__ void part_gather(const PartSum& P, int t, const int (&j)[N], float (&v)[N]) {
+  if (P.ks == 1) {
+    const float* q = P.p + (int64_t)t * P.ld;
 #pragma unroll
-  for (int z = 0; z < kMaxDeferSplit; ++z) w[z] = z < P.ks ? q[(int64_t)z * P.zs] : 0.f;
-  float a = w[0];
+    for (int e = 0; e < N; ++e) v[e] = q[j[e]];
+    return;
+  }
+  float w[N][4];
+  part_issue<N>(P, t, j, w);
+  part_finish<N>(P, t, j, w, v);
+}
+
+// Row t of a deferred result, elements j0 + S * e for e < 4 (zero past n).
+template <int S = kWg>
+__device__ __forceinline__ void part_row4(const PartSum& P, int t, int j0, float (&v)[4]) {
+  int j[4];
 #pragma unroll
-  for (int z = 1; z < kMaxDeferSplit; ++z)
-    if (z < P.ks) a += w[z];
-  return a;
+  for (int e = 0; e < 4; ++e) j[e] = min(j0 + S * e, P.n - 1);
+  part_gather<4>(P, t, j, v);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = j0 + S * e < P.n ? v[e] : 0.f;
 }
 
 // The per-row glue kernels run one workgroup of kRowT threads per token row
@@ -122,10 +152,9 @@ __global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
   float* xw = const_cast<float*>(a.x + (size_t)t * a.ldx);
   float v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int i = tid + kRowT * e;
-    v[e] = i < a.k ? xw[i] : 0.f;
-  }
+  for (int e = 0; e < 4; ++e) v[e] = xw[min(tid + kRowT * e, a.k - 1)];  // unconditional (no branch)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = tid + kRowT * e < a.k ? v[e] : 0.f;
   if (a.add.p) {
     float d[4];
     part_row4<kRowT>(a.add, t, tid, d);
@@ -946,10 +975,25 @@ __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
     const int d = min(lane + 64 * j, half - 1);
     ia[j] = a.interleaved ? 2 * d : d;
     ib[j] = a.interleaved ? 2 * d + 1 : d + half;
-    if (P.p) {
-      x0[j] = part_at(P, t, pcol + ia[j]);
-      x1[j] = part_at(P, t, pcol + ib[j]);
-    } else {
+  }
+  if (P.p) {
+    // both elements of every pair in one round of loads
+    int jj[2 * NP];
+    float xx[2 * NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      jj[2 * j] = pcol + ia[j];
+      jj[2 * j + 1] = pcol + ib[j];
+    }
+    part_gather<2 * NP>(P, t, jj, xx);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      x0[j] = xx[2 * j];
+      x1[j] = xx[2 * j + 1];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
       x0[j] = row[col + ia[j]];
       x1[j] = row[col + ib[j]];
     }
@@ -994,12 +1038,27 @@ __global__ __launch_bounds__(kWg) void k_pf_rope_kv(PfRopeArgs a) {
   }
   if (is_k) {
     const int vcol = (a.heads + a.kv_heads) * hd + kv * hd;
-    for (int d = lane; d < hd; d += 64) {
-      const float v = a.pv.p ? part_at(a.pv, t, kv * hd + d) : row[vcol + d];
+    // lane's dims lane + 64 i (head_dim <= 256), every load issued at once
+    int jv[4];
+    float vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) jv[i] = min(lane + 64 * i, hd - 1);
+    if (a.pv.p) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) jv[i] += kv * hd;
+      part_gather<4>(a.pv, t, jv, vv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vv[i] = row[vcol + jv[i]];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = lane + 64 * i;
+      if (d >= hd) continue;
       if (a.kv16)
-        ((__half*)a.kv.vc)[base + d] = __float2half_rn(v);
+        ((__half*)a.kv.vc)[base + d] = __float2half_rn(vv[i]);
       else
-        ((float*)a.kv.vc)[base + d] = v;
+        ((float*)a.kv.vc)[base + d] = vv[i];
     }
   }
 }
@@ -1257,9 +1316,8 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
 // accumulators rescaled when the maximum grows). With one segment per row the
 // workgroup writes the attention output; otherwise a partial [max, sum,
 // acc[hd]] per head for k_bd_merge.
-template <int HD>
-__global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg, PfRopeArgs ra,
-                                               int rope) {
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg, PfRopeArgs ra) {
   constexpr int DPT = HD / 4;  // K dims per lane
   constexpr int NKV = DPT / 8;
   constexpr int VD = HD >= 256 ? 4 : 2, VW = VD / 2;
@@ -1271,28 +1329,76 @@ __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int 
   __shared__ float wmx[4][8];
   __shared__ __align__(16) float ew[8][kKvPage];
   __shared__ float lsum[8];
+  __shared__ int pt_s[64];  // the segment's page table entries (max_pages <= 64)
   const int kv = blockIdx.x, r = blockIdx.y, sg = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.heads / a.kv_heads;
-  const int pos = row_pos(a.kv, r);
+  // With ROPE, the rotary/K-V write of this (row, kv head) comes first (the
+  // arithmetic of k_pf_rope_kv): the G q heads, k and v, gathered from the
+  // projections' partial sums, are G + 2 items over the waves; q goes to LDS,
+  // k and v to the cache. Item `it`: four elements per lane (q/k: the two
+  // elements of the lane's rotary pairs lane and lane + 64; v: dims lane + 64 e),
+  // clamped so that every item issues the same loads. The first item's loads
+  // go out before anything else.
+  constexpr int NPR = 2;  // pairs per lane: head_dim <= 256
+  constexpr int HALF = HD / 2;
+  int ia[NPR], ib[NPR];
+#pragma unroll
+  for (int j = 0; j < NPR; ++j) {
+    const int d = min(lane + 64 * j, HALF - 1);
+    ia[j] = ra.interleaved ? 2 * d : d;
+    ib[j] = ra.interleaved ? 2 * d + 1 : d + HALF;
+  }
+  // item it's partial sums and columns
+  auto item_cols = [&](int it, int (&jj)[4]) -> const PartSum& {
+    if (it == G + 1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) jj[e] = kv * HD + min(lane + 64 * e, HD - 1);
+      return ra.pv;
+    }
+    const int pcol = it == G ? kv * HD : (kv * G + it) * HD;
+#pragma unroll
+    for (int j = 0; j < NPR; ++j) {
+      jj[2 * j] = pcol + ia[j];
+      jj[2 * j + 1] = pcol + ib[j];
+    }
+    return it == G ? ra.pk : ra.pq;
+  };
+  const int it0 = min(wave, G + 1);
+  int jj0[4];
+  float w0[4][4];
+  if constexpr (ROPE) part_issue<4>(item_cols(it0, jj0), r, jj0, w0);
+  // The row's position and sequence and its page table entries are read
+  // through the scalar cache (the scalar load counter is separate: waiting for
+  // them never waits for the vector loads in flight), and the segment's
+  // entries are staged in LDS for the page loop.
+  const int pos = ld_scalar(a.kv.row_pos + r);
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
   const int j_lo = start / kKvPage, np = pos / kKvPage - j_lo + 1;
   // this segment's pages [p_lo, p_hi) of the row's range
-  const int p_lo = j_lo + (int)((int64_t)np * sg / nseg), p_hi = j_lo + (int)((int64_t)np * (sg + 1) / nseg);
-  const int seq = row_seq(a.kv, r);
+  const int p_lo = j_lo + np * sg / nseg, p_hi = j_lo + np * (sg + 1) / nseg;  // np, nseg <= 64
+  const int seq = ld_scalar(a.kv.row_seq + r);
+  const int* ptab = a.kv.pages + (size_t)seq * a.kv.max_pages;
+  const int jnew = pos / kKvPage;  // the newest page (entries past it may be unassigned)
+  const int pt_mine = ptab[min(p_lo + tid, jnew)];
+  const int phys0 = ld_scalar(ptab + min(p_lo, jnew));
   const float* q = a.qkv + (size_t)r * a.ld + kv * G * HD;
   const int kp = 16 * wave + (lane >> 2), kd0 = (lane & 3) * DPT;
   const int pg = lane >> LDW, vd = wave * (HD / 4) + VD * (lane & (DW - 1));
   const int ei = (kp % PG) * NP + kp / PG;
-  auto load = [&](int j, uint4 (&kr)[NKV], uint32_t (&vr)[NP][VW]) {
-    const int phys = a.kv.pages[(size_t)seq * a.kv.max_pages + j];
-    const __half* kb = (const __half*)a.kv.kc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
-    const __half* vb = (const __half*)a.kv.vc + ((size_t)phys * a.kv_heads + kv) * kKvPage * HD;
+  // a page's rows are addressed from a workgroup-uniform base with 32-bit
+  // per-lane byte offsets (scalar base + vector offset loads: no 64-bit
+  // address arithmetic per load)
+  const uint32_t koff = 2u * (uint32_t)(kp * HD + kd0), voff = 2u * (uint32_t)(pg * HD + vd);
+  auto load = [&](int phys, uint4 (&kr)[NKV], uint32_t (&vr)[NP][VW]) {
+    const size_t pb = ((size_t)__builtin_amdgcn_readfirstlane(phys) * a.kv_heads + kv) * (kKvPage * HD * 2);
+    const char* kb = (const char*)a.kv.kc + pb;
+    const char* vb = (const char*)a.kv.vc + pb;
 #pragma unroll
-    for (int v = 0; v < NKV; ++v) kr[v] = ldg4(kb + (size_t)kp * HD + kd0 + 8 * v);
+    for (int v = 0; v < NKV; ++v) kr[v] = ldg4(kb + koff + 16 * v);
 #pragma unroll
     for (int t = 0; t < NP; ++t) {
-      const __half* p = vb + (size_t)(pg + PG * t) * HD + vd;
+      const char* p = vb + (2 * PG * HD) * t + voff;
       if constexpr (VW == 1) {
         vr[t][0] = ldg1(p);
       } else {
@@ -1394,96 +1500,92 @@ __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int 
   };
   uint4 ka[NKV], kb2[NKV];
   uint32_t va[NP][VW], vb2[NP][VW];
-  if (rope) {
-    // this (row, kv head)'s share of the rotary/K-V write (k_pf_rope_kv's
-    // arithmetic): the G q heads, k and v gathered from the projections'
-    // partial sums are G + 2 items over the waves; q goes to LDS, k and v to
-    // the cache. The first page is requested first unless it is the newest,
-    // which is read only after the barrier below publishes the new row.
-    if (p_lo < p_hi && p_lo < pos / kKvPage) load(p_lo, ka, va);
-    constexpr int NPR = 2;  // pairs per lane: head_dim <= 256
-    constexpr int HALF = HD / 2;
-    int ia[NPR], ib[NPR];
+  if constexpr (ROPE) {
+    // (one segment) the first page is requested before the rotary work; when
+    // it is the newest, it is requested again after the barrier below that
+    // publishes the new row
+    load(phys0, ka, va);
+    const size_t base = (((size_t)ld_scalar(ptab + jnew) * ra.kv_heads + kv) * kKvPage + (pos & (kKvPage - 1))) * HD;
+    auto item_do = [&](int it, const float (&xx)[4]) {
+      if (it == G + 1) {
 #pragma unroll
-    for (int j = 0; j < NPR; ++j) {
-      const int d = min(lane + 64 * j, HALF - 1);
-      ia[j] = ra.interleaved ? 2 * d : d;
-      ib[j] = ra.interleaved ? 2 * d + 1 : d + HALF;
-    }
-    const size_t base = kv_row(ra.kv, ra.kv_heads, HD, seq, kv, pos);
-    for (int it = wave; it < G + 2; it += 4) {
-      if (it <= G) {
-        const bool is_k = it == G;
-        const PartSum& P = is_k ? ra.pk : ra.pq;
-        const int pcol = is_k ? kv * HD : (kv * G + it) * HD;
-        const int col = is_k ? ra.heads * HD + kv * HD : (kv * G + it) * HD;
-        const float* row = ra.qkv + (size_t)r * ra.ld;
-        float x0[NPR], x1[NPR];
+        for (int e = 0; e < HD / 64; ++e) ((__half*)ra.kv.vc)[base + lane + 64 * e] = __float2half_rn(xx[e]);
+        return;
+      }
+      const bool is_k = it == G;
+      const float x0[NPR] = {xx[0], xx[2]}, x1[NPR] = {xx[1], xx[3]};
+      float rn = 1.0f;
+      if (ra.qn_w) {
+        float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < NPR; ++j) {
-          x0[j] = P.p ? part_at(P, r, pcol + ia[j]) : row[col + ia[j]];
-          x1[j] = P.p ? part_at(P, r, pcol + ib[j]) : row[col + ib[j]];
-        }
-        float rn = 1.0f;
+        for (int j = 0; j < NPR; ++j)
+          if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
+        ss = wave_sum(ss);
+        rn = 1.0f / sqrtf(ss / (float)HD + ra.eps);
+      }
+      const float* w = is_k ? ra.kn_w : ra.qn_w;
+#pragma unroll
+      for (int j = 0; j < NPR; ++j) {
+        const int d = lane + 64 * j;
+        if (d >= HALF) continue;
+        float v0 = x0[j], v1 = x1[j];
         if (ra.qn_w) {
-          float ss = 0.f;
-#pragma unroll
-          for (int j = 0; j < NPR; ++j)
-            if (lane + 64 * j < HALF) ss += x0[j] * x0[j] + x1[j] * x1[j];
-          ss = wave_sum(ss);
-          rn = 1.0f / sqrtf(ss / (float)HD + ra.eps);
+          v0 = __fmul_rn(__fmul_rn(v0, rn), w[ia[j]]);
+          v1 = __fmul_rn(__fmul_rn(v1, rn), w[ib[j]]);
         }
-        const float* w = is_k ? ra.kn_w : ra.qn_w;
-#pragma unroll
-        for (int j = 0; j < NPR; ++j) {
-          const int d = lane + 64 * j;
-          if (d >= HALF) continue;
-          float v0 = x0[j], v1 = x1[j];
-          if (ra.qn_w) {
-            v0 = __fmul_rn(__fmul_rn(v0, rn), w[ia[j]]);
-            v1 = __fmul_rn(__fmul_rn(v1, rn), w[ib[j]]);
-          }
-          const float ang = __fmul_rn((float)pos, ra.rope_inv[d]);
-          const float co = cosf(ang), si = sinf(ang);
-          const float y0 = __fsub_rn(__fmul_rn(v0, co), __fmul_rn(v1, si));
-          const float y1 = __fadd_rn(__fmul_rn(v0, si), __fmul_rn(v1, co));
-          if (is_k) {
-            ((__half*)ra.kv.kc)[base + ia[j]] = __float2half_rn(y0);
-            ((__half*)ra.kv.kc)[base + ib[j]] = __float2half_rn(y1);
-          } else {
-            q_s[it * HD + ia[j]] = y0;
-            q_s[it * HD + ib[j]] = y1;
-          }
-        }
-      } else {
-        const float* row = ra.qkv + (size_t)r * ra.ld;
-        const int vcol = (ra.heads + ra.kv_heads) * HD + kv * HD;
-        for (int d = lane; d < HD; d += 64) {
-          const float v = ra.pv.p ? part_at(ra.pv, r, kv * HD + d) : row[vcol + d];
-          ((__half*)ra.kv.vc)[base + d] = __float2half_rn(v);
+        const float ang = __fmul_rn((float)pos, ra.rope_inv[d]);
+        const float co = cosf(ang), si = sinf(ang);
+        const float y0 = __fsub_rn(__fmul_rn(v0, co), __fmul_rn(v1, si));
+        const float y1 = __fadd_rn(__fmul_rn(v0, si), __fmul_rn(v1, co));
+        if (is_k) {
+          ((__half*)ra.kv.kc)[base + ia[j]] = __float2half_rn(y0);
+          ((__half*)ra.kv.kc)[base + ib[j]] = __float2half_rn(y1);
+        } else {
+          q_s[it * HD + ia[j]] = y0;
+          q_s[it * HD + ib[j]] = y1;
         }
       }
+    };
+    if (wave < G + 2) {
+      float xx[4];
+      part_finish<4>(item_cols(it0, jj0), r, jj0, w0, xx);
+      item_do(wave, xx);
     }
-    __syncthreads();  // q in LDS; the new K/V row visible to this workgroup's loads
-    if (p_lo < p_hi && p_lo >= pos / kKvPage) load(p_lo, ka, va);
+    for (int it = wave + 4; it < G + 2; it += 4) {  // groups above 2
+      int jj[4];
+      float xx[4];
+      part_gather<4>(item_cols(it, jj), r, jj, xx);
+      item_do(it, xx);
+    }
+    if (tid < 64) pt_s[tid] = pt_mine;
+    __syncthreads();  // q and the page table in LDS; the new K/V row visible to this workgroup's loads
+    if (p_lo == jnew) load(phys0, ka, va);
   } else {
     // q first: its loads complete before the page's, which stay in flight
     float qv[6];
 #pragma unroll
     for (int c = 0; c < 6; ++c) qv[c] = tid + kWg * c < G * HD ? q[tid + kWg * c] : 0.f;
-    if (p_lo < p_hi) load(p_lo, ka, va);
+    if (p_lo < p_hi) load(phys0, ka, va);
 #pragma unroll
     for (int c = 0; c < 6; ++c)
       if (tid + kWg * c < G * HD) q_s[tid + kWg * c] = qv[c];
+    if (tid < 64) pt_s[tid] = pt_mine;
     __syncthreads();
   }
+  // The next page's loads are issued unconditionally (the last page requests
+  // itself again, a cache hit) so that the loop body has no branch around
+  // them: the compiler's load-counter waits then count exactly and page j's
+  // reduction waits for page j's rows only.
   for (int j = p_lo; j < p_hi; j += 2) {
-    if (j + 1 < p_hi) load(j + 1, kb2, vb2);
+    load(pt_s[min(j + 1, p_hi - 1) - p_lo], kb2, vb2);
+    __builtin_amdgcn_sched_barrier(0);  // issued before page j's reduction starts
     page(j, ka, va);
     if (j + 1 >= p_hi) break;
-    if (j + 2 < p_hi) load(j + 2, ka, va);
+    load(pt_s[min(j + 2, p_hi - 1) - p_lo], ka, va);
+    __builtin_amdgcn_sched_barrier(0);
     page(j + 1, kb2, vb2);
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the last redundant request has returned
 #pragma unroll
   for (int g = 0; g < 8; ++g)
     if (g < G)
@@ -1884,7 +1986,8 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
   if (nseg <= 0 || (rope && nseg != 1)) return hipErrorInvalidValue;
   PfRopeArgs ra{};
   if (rope) ra = *rope;
-  if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || G > 8 || G * a.hd > 1536 || mp > 64 ||
+  if (rope && (!ra.pq.p || !ra.pk.p || !ra.pv.p)) return hipErrorInvalidValue;  // the partial sums are read
+  if (!a.kv16 || !a.kv.pages || !a.kv.row_seq || !a.kv.row_pos || G > 8 || G * a.hd > 1536 || mp > 64 ||
       (nseg > 1 && (int64_t)rows * a.kv_heads * mp * attn_rowf(G, a.hd) > part_cap))
     return hipErrorInvalidValue;
   if (nseg > 1) a.oh = nullptr;  // the merge writes a.out
@@ -1893,7 +1996,10 @@ hipError_t launch_bd_attn(const PfAttnArgs& a0, int rows, float* part, int64_t p
   const dim3 g1(a.kv_heads, rows, nseg), g2(a.kv_heads, rows);
 #define CHONK_BD_CASE(HH)                                                                     \
   case HH:                                                                                    \
-    hipLaunchKernelGGL(k_bd_walk<HH>, g1, dim3(kWg), 0, s, a, part, mp, nseg, ra, rope ? 1 : 0); \
+    if (rope)                                                                                 \
+      hipLaunchKernelGGL((k_bd_walk<HH, true>), g1, dim3(kWg), 0, s, a, part, mp, nseg, ra);  \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_bd_walk<HH, false>), g1, dim3(kWg), 0, s, a, part, mp, nseg, ra); \
     if (nseg > 1) hipLaunchKernelGGL(k_bd_merge<HH>, g2, dim3(kWg), 0, s, a, part, mp, nseg); \
     return hipGetLastError();
   switch (a.hd) {
