@@ -2149,7 +2149,7 @@ Error device_error(chonk_engine* e, const DevState& st) {
 
 // ---- row batches: prompt pass and batched decode ---------------------------------------
 
-constexpr int kPrefillRows = 512;  // prompt rows per pass (longer prompts take several)
+constexpr int kPrefillRows = 2048;  // prompt rows per pass (longer prompts take several)
 constexpr int64_t kPartFloats = (int64_t)4 << 20;  // K-split partial sums
 
 // Device buffers of a row batch (rows <= cap).
