@@ -1144,165 +1144,236 @@ __global__ __launch_bounds__(kWg) void k_pf_attn(PfAttnArgs a) {
 
 // Causal attention of the prompt rows on the matrix cores (fp16 K/V cache):
 // one workgroup per (block of 64 / G tokens, kv head); its 64 query rows
-// (token, q head of the group) are four waves of 16. Per block of 64 keys:
-// S = Q K^T (q split into fp16 hi + lo, K exact), a running softmax per row
-// inside each wave, then O += P V (P split into hi + lo, V exact).
+// (token, q head of the group) are four waves of 16. The products run
+// transposed so that no operand needs a shuffle: per block of 64 keys,
+//   S^T = K Q^T  (v_mfma 16x16x32: K rows from LDS, q split into fp16 hi + lo),
+// whose accumulator layout (lane: query lane % 16, keys 4 (lane / 16) + i of
+// each 16-key tile) is the B operand layout of the 16x16x16 product, so
+//   O^T += V^T P^T  (P split into hi + lo; V^T staged in LDS, V exact)
+// takes P straight from the registers, and every lane keeps the running
+// maximum, sum and output of its own query. Scores are kept in log2 units
+// (scale * log2 e folded into one multiply) and the exponent base is only
+// raised when a block's maximum exceeds it by more than 8 (P <= 2^8 stays
+// exact enough in fp16 hi + lo and the sums in fp32), so the output rescale
+// is skipped by the whole wave on most blocks; blocks that no query of the
+// wave sees partly masked skip the masking. The next block's K and V are
+// loaded into registers while the current one is multiplied; workgroups
+// with the most keys (the last tokens) are dispatched first, and workgroup
+// ids step through the kv heads fastest: consecutive ids go to different XCDs
+// (id mod 8), so with 8 kv heads each XCD's L2 holds one head's K/V.
 constexpr int kFaKeys = 64;
+
+__device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// max / sum over the four lanes of one query (lanes l, l ^ 16, l ^ 32, l ^ 48)
+__device__ __forceinline__ float xquad_max(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xquad_sum(float v) {
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
+}
 
 template <int HD, bool PAGED>
 __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   extern __shared__ __align__(16) _Float16 fsm[];
-  constexpr int KS = HD + 8, VS = kFaKeys + 8, PS = kFaKeys + 8;
-  _Float16* ks = fsm;                         // [64 keys][KS]
-  _Float16* vt = ks + kFaKeys * KS;           // [HD dims][VS]   (V transposed)
-  _Float16* pw = vt + HD * VS;                // [4 waves][2][16 rows][PS]
+  constexpr int KS = HD + 8, VS = kFaKeys + 8;
+  constexpr int NKP = HD / 32;                   // K pieces (8 halves) per thread and block
+  constexpr int NVI = HD >= 64 ? HD / 64 : 1;    // V items (2 keys x 8 dims) per thread and block
+  constexpr int VITEMS = (kFaKeys / 2) * (HD / 8);
+  _Float16* ks = fsm;                  // [64 keys][KS]
+  _Float16* vt = ks + kFaKeys * KS;    // [HD dims][VS]   (V transposed)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // rows of one workgroup share a sequence: one token per workgroup when
   // every row has its own
   const int G = a.heads / a.kv_heads, TW = a.kv.row_seq ? 1 : 64 / G;
-  const int t0 = blockIdx.x * TW, kv = blockIdx.y;
+  const int ntiles = gridDim.x / a.kv_heads;
+  const int kv = blockIdx.x % a.kv_heads, t0 = (ntiles - 1 - (int)blockIdx.x / a.kv_heads) * TW;
   const int col = lane & 15, quad = lane >> 4;
   const int seq = row_seq(a.kv, t0);
   const __half* kc = (const __half*)a.kv.kc;
   const __half* vc = (const __half*)a.kv.vc;
 
-  // this lane's A-operand row of Q (row 16 * wave + col), hi and lo halves
+  // this lane's query: row 16 * wave + col of the workgroup (token, head);
+  // its B operand of S^T (dims 32 k + 8 quad .. + 8), hi and lo halves
+  const int qr = 16 * wave + col, qt = t0 + qr / G;
+  const bool qok = qr < TW * G && qt < a.rows;
   half8_t qh[HD / 32], ql[HD / 32];
   {
-    const int r = 16 * wave + col, t = t0 + r / G;
-    const bool ok = r < TW * G && t < a.rows;
-    const float* q = a.qkv + (size_t)(ok ? t : 0) * a.ld + (kv * G + r % G) * HD;
+    const float* q = a.qkv + (size_t)(qok ? qt : t0) * a.ld + (kv * G + qr % G) * HD;
 #pragma unroll
     for (int k = 0; k < HD / 32; ++k) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = q[32 * k + 8 * quad + i];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float v = ok ? q[32 * k + 8 * quad + i] : 0.f;
-        qh[k][i] = (_Float16)v;
-        ql[k][i] = (_Float16)(v - (float)qh[k][i]);
+        const float x = qok ? v[i] : 0.f;
+        qh[k][i] = (_Float16)x;
+        ql[k][i] = (_Float16)(x - (float)qh[k][i]);
       }
     }
   }
-  // rows of this lane's C values: 16 * wave + 4 * quad + i
-  int rpos[4], rstart[4];
-  bool rok[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * wave + 4 * quad + i, t = t0 + r / G;
-    rok[i] = r < TW * G && t < a.rows;
-    rpos[i] = rok[i] ? row_pos(a.kv, t) : 0;
-    rstart[i] = (a.window != 0 && rpos[i] + 1 > a.window) ? rpos[i] + 1 - a.window : 0;
-  }
+  const int qpos = qok ? row_pos(a.kv, qt) : -1;
+  const int qstart = (a.window != 0 && qpos + 1 > a.window) ? qpos + 1 - a.window : 0;
+  // the wave's key range seen by every one of its queries (unused rows excluded)
+  const int wpos_min = (int)-wave_max(-(float)(qok ? qpos : 1 << 24));
+  const int wstart_max = (int)wave_max((float)(qok ? qstart : 0));
+  const float sl2 = a.scale * 1.44269504088896341f;
   const int t_last = min(t0 + TW, a.rows) - 1;
   const int pos_hi = row_pos(a.kv, t_last), pos_lo = row_pos(a.kv, t0);
   const int st_lo = (a.window != 0 && pos_lo + 1 > a.window) ? pos_lo + 1 - a.window : 0;
+  const int kb_lo = st_lo / kFaKeys, kb_hi = pos_hi / kFaKeys;
 
-  float m_run[4], l_run[4];
-  float4_t o[HD / 16];
+  // staging: K piece (key, 8 dims) and V item (key pair, 8 dims) of the thread
+  uint4 kreg[NKP], vreg[NVI][2];
+  // block kb's first K/V row (workgroup-uniform) and the last row of the block
+  // that may be addressed (the cache ends inside the block)
+  auto block_base = [&](int kb) -> size_t {
+    if constexpr (PAGED) {
+      const int page = ld_scalar(a.kv.pages + (size_t)seq * a.kv.max_pages + kb);
+      return ((size_t)page * a.kv_heads + kv) * kKvPage * HD;
+    } else {
+      return ((size_t)kv * a.kv.ctx + kb * kFaKeys) * HD;
+    }
+  };
+  auto key_cap = [&](int kb) -> int { return PAGED ? kFaKeys - 1 : min(kFaKeys - 1, a.kv.ctx - 1 - kb * kFaKeys); };
+  // Keys past the block's last position were never written (fresh pages can
+  // hold NaN bit patterns, and P = 0 times NaN is NaN): staged as zeros.
+  auto fetch = [&](int kb) {
+    const int k0 = kb * kFaKeys, cap = key_cap(kb);
+    const size_t base = block_base(kb);
+    const __half* kb0 = kc + base;
+    const __half* vb0 = vc + base;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.f;
-  }
+    for (int j = 0; j < NKP; ++j) {
+      const int piece = tid + kWg * j, key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
+      const uint4 v = ldg4(kb0 + (uint32_t)(min(key, cap) * HD + d8));
+      kreg[j] = k0 + key <= pos_hi ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < NVI; ++j) {
+      const int item = min(tid + kWg * j, VITEMS - 1), kp = item % (kFaKeys / 2), d8 = (item / (kFaKeys / 2)) * 8;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int key = 2 * kp + h;
+        const uint4 v = ldg4(vb0 + (uint32_t)(min(key, cap) * HD + d8));
+        vreg[j][h] = k0 + key <= pos_hi ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < NKP; ++j) {
+      const int piece = tid + kWg * j, key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
+      *(uint4*)(ks + key * KS + d8) = kreg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NVI; ++j) {
+      const int item = tid + kWg * j, kp = item % (kFaKeys / 2), d8 = (item / (kFaKeys / 2)) * 8;
+      if (item < VITEMS) {
+        // dims d8 .. d8 + 7 of keys 2 kp and 2 kp + 1 as eight (key, key + 1) pairs
+        const uint32_t* w0 = (const uint32_t*)&vreg[j][0];
+        const uint32_t* w1 = (const uint32_t*)&vreg[j][1];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          *(uint32_t*)(vt + (d8 + 2 * d) * VS + 2 * kp) = (w0[d] & 0xffffu) | (w1[d] << 16);
+          *(uint32_t*)(vt + (d8 + 2 * d + 1) * VS + 2 * kp) = (w0[d] >> 16) | (w1[d] & 0xffff0000u);
+        }
+      }
+    }
+  };
+
+  float m_use = -INFINITY, l_run = 0.f;  // exponent base (log2 units) and running sum of the lane's query
+  float4_t o[HD / 16];  // O^T tiles: dims 16 dt + 4 quad + i of the lane's query
 #pragma unroll
   for (int d = 0; d < HD / 16; ++d) o[d] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = st_lo / kFaKeys; kb <= pos_hi / kFaKeys; ++kb) {
+  fetch(kb_lo);
+  for (int kb = kb_lo; kb <= kb_hi; ++kb) {
     const int k0 = kb * kFaKeys;
     __syncthreads();  // the previous block's K / V^T are consumed
-    // K rows and V^T: 16-byte pieces (8 halves), keys past the cache clamped.
-    // Keys past the block's last position were never written (fresh pages can
-    // hold NaN bit patterns, and P = 0 times NaN is NaN): staged as zeros.
-    for (int piece = tid; piece < kFaKeys * HD / 8; piece += kWg) {
-      const int key = piece / (HD / 8), d8 = (piece % (HD / 8)) * 8;
-      size_t row;
-      if constexpr (PAGED) {
-        const int page = a.kv.pages[(size_t)seq * a.kv.max_pages + kb];
-        row = (((size_t)page * a.kv_heads + kv) * kKvPage + key) * HD;
-      } else {
-        row = ((size_t)kv * a.kv.ctx + min(k0 + key, a.kv.ctx - 1)) * HD;
-      }
-      const bool live = k0 + key <= pos_hi;
-      const uint4 kv8 = live ? *(const uint4*)(kc + row + d8) : make_uint4(0u, 0u, 0u, 0u);
-      *(uint4*)(ks + key * KS + d8) = kv8;
-      const uint4 vv8 = live ? *(const uint4*)(vc + row + d8) : make_uint4(0u, 0u, 0u, 0u);
-      const _Float16* vh = (const _Float16*)&vv8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vt[(d8 + i) * VS + key] = vh[i];
-    }
+    stage();
     __syncthreads();
-    // S for the wave's 16 rows x 64 keys (four 16 x 16 tiles)
-    float4_t s[4];
+    fetch(min(kb + 1, kb_hi));  // the next block (the last one again at the end: cache hits)
+    // S^T for the block's 64 keys x the wave's 16 queries (four 16 x 16 tiles)
+    float s[4][4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      s[kt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < HD / 32; ++k) {
-        const half8_t b = *(const half8_t*)(ks + (16 * kt + col) * KS + 32 * k + 8 * quad);
-        s[kt] = mfma32(qh[k], b, s[kt]);
-        s[kt] = mfma32(ql[k], b, s[kt]);
+        const half8_t kk = *(const half8_t*)(ks + (16 * kt + col) * KS + 32 * k + 8 * quad);
+        acc = mfma32(kk, qh[k], acc);
+        acc = mfma32(kk, ql[k], acc);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kt][i] = acc[i] * sl2;
     }
-    // masked, scaled scores; block maximum per row (over the 16 lanes of a row group)
-    float mb[4];
+    if (!(k0 >= wstart_max && k0 + kFaKeys - 1 <= wpos_min)) {
+      // some query of the wave sees only part of the block
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float m = -INFINITY;
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = k0 + 16 * kt + col;
-        const bool in = rok[i] && key >= rstart[i] && key <= rpos[i];
-        const float v = in ? s[kt][i] * a.scale : -INFINITY;
-        s[kt][i] = v;
-        m = fmaxf(m, v);
-      }
-      mb[i] = group_max<16>(m);
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kt + 4 * quad + i;
+          s[kt][i] = key >= qstart && key <= qpos ? s[kt][i] : -INFINITY;
+        }
     }
-    _Float16* ph = pw + (size_t)wave * 2 * 16 * PS;
-    _Float16* pl = ph + 16 * PS;
+    float mb = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float mn = fmaxf(m_run[i], mb[i]);
-      const float ro = (m_run[i] == -INFINITY) ? 0.f : expf(m_run[i] - mn);
-      float lb = 0.f;
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const float p = (mn == -INFINITY || s[kt][i] == -INFINITY) ? 0.f : expf(s[kt][i] - mn);
+      for (int i = 0; i < 4; ++i) mb = fmaxf(mb, s[kt][i]);
+    mb = xquad_max(mb);
+    const bool upd = mb > m_use + 8.0f;
+    const float alpha = !upd ? 1.0f : (m_use == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_use - mb));
+    m_use = upd ? mb : m_use;
+    const float base = m_use == -INFINITY ? 0.f : m_use;  // masked scores give exp2(-inf) = 0
+    float lb = 0.f;
+    half4_t ph[4], pl[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[kt][i] - base);
         lb += p;
-        const _Float16 h = (_Float16)p;
-        ph[(4 * quad + i) * PS + 16 * kt + col] = h;
-        pl[(4 * quad + i) * PS + 16 * kt + col] = (_Float16)(p - (float)h);
+        ph[kt][i] = (_Float16)p;
+        pl[kt][i] = (_Float16)(p - (float)ph[kt][i]);
       }
-      lb = group_sum<16>(lb);
-      l_run[i] = l_run[i] * ro + lb;
-      m_run[i] = mn;
+    l_run = l_run * alpha + xquad_sum(lb);
+    if (__builtin_amdgcn_ballot_w64(upd) != 0) {
 #pragma unroll
-      for (int d = 0; d < HD / 16; ++d) o[d][i] *= ro;
+      for (int d = 0; d < HD / 16; ++d) o[d] *= alpha;
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's P rows are in LDS
-    __builtin_amdgcn_wave_barrier();
-    // O += P V over the block's 64 keys
+    // O^T += V^T P^T over the block's keys (four 16-key steps)
 #pragma unroll
-    for (int kq = 0; kq < kFaKeys / 32; ++kq) {
-      const half8_t ah = *(const half8_t*)(ph + col * PS + 32 * kq + 8 * quad);
-      const half8_t al = *(const half8_t*)(pl + col * PS + 32 * kq + 8 * quad);
+    for (int d = 0; d < HD / 16; ++d) {
 #pragma unroll
-      for (int d = 0; d < HD / 16; ++d) {
-        const half8_t b = *(const half8_t*)(vt + (16 * d + col) * VS + 32 * kq + 8 * quad);
-        o[d] = mfma32(ah, b, o[d]);
-        o[d] = mfma32(al, b, o[d]);
+      for (int kt = 0; kt < 4; ++kt) {
+        const half4_t vv = *(const half4_t*)(vt + (16 * d + col) * VS + 16 * kt + 4 * quad);
+        o[d] = mfma16(vv, ph[kt], o[d]);
+        o[d] = mfma16(vv, pl[kt], o[d]);
       }
     }
   }
-  // out[token][head * HD + dim] for the lane's rows
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the last redundant fetch has returned
+  // out[token][head * HD + dim]: the lane's query, dims 16 d + 4 quad .. + 4
+  if (qok) {
+    float* out = a.out + (size_t)qt * a.ldo + (kv * G + qr % G) * HD;
+    const float inv = 1.0f / l_run;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (!rok[i]) continue;
-    const int r = 16 * wave + 4 * quad + i, t = t0 + r / G;
-    float* out = a.out + (size_t)t * a.ldo + (kv * G + r % G) * HD;
-    const float inv = 1.0f / l_run[i];
-#pragma unroll
-    for (int d = 0; d < HD / 16; ++d) out[16 * d + col] = o[d][i] * inv;
+    for (int d = 0; d < HD / 16; ++d)
+      *(float4*)(out + 16 * d + 4 * quad) = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
   }
 }
 
@@ -1750,7 +1821,7 @@ __global__ __launch_bounds__(64) void k_row_argmax2(const float* pv, const uint3
 size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM + 2 * kGT) * kGS; }
 
 size_t fattn_shared_bytes(int hd) {
-  return sizeof(_Float16) * ((size_t)kFaKeys * (hd + 8) + (size_t)hd * (kFaKeys + 8) + 4 * 2 * 16 * (kFaKeys + 8));
+  return sizeof(_Float16) * ((size_t)kFaKeys * (hd + 8) + (size_t)hd * (kFaKeys + 8));
 }
 
 
@@ -1935,7 +2006,7 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, int rows, hipStream_t s) {
   PfAttnArgs b = a;
   b.rows = rows;
   const int tw = a.kv.row_seq ? 1 : 64 / G;
-  const dim3 grid((rows + tw - 1) / tw, a.kv_heads);
+  const dim3 grid((rows + tw - 1) / tw * a.kv_heads);
   const size_t sh = fattn_shared_bytes(a.hd);
   const bool paged = a.kv.pages != nullptr;
 #define CHONK_FA(H)                                                              \
