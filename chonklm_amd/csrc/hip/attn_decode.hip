@@ -75,7 +75,8 @@ __device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((u
 // qn[G][HD] (normalised, rotated q, shared by the waves) | wmx[4][G] (each
 // wave's score maximum) | ew[G][64] (the chunk's weights; position p at
 // (p % PG) * NP + p / PG, so a lane reads its V positions contiguously) |
-// hv[G][4] (the new position's score per head).
+// hv[G][4] (the new position's score per head) | cs[HD] (the rotary (cos, sin)
+// pairs of the position).
 //
 // Chunk rows (a.tpart, [kv][nchunk][rowf] tagged words): per head [max, sum,
 // acc[HD]], each word {f32, u32 tag}; the tag of a launch is the kv head's
@@ -110,6 +111,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   float* wmx = qn + G * HD;
   float* ew = wmx + 4 * G;
   float* hv = ew + kDecChunk * G;
+  float* cs_s = hv + 4 * G;  // (cos, sin) of the rotary pairs at the position
   uint64_t tr[8];
   CHONK_MV_T(tr, 0);
 
@@ -154,7 +156,9 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     load_k(t0);
     load_v(t0);
   };
-  if (a.spec_kv) load_kv(t_lo);
+  // (the q/k/v copies and the rotary table first: the K/V loads are the last
+  // NKV + NP of the wave, so phase B only waits for what was issued before
+  // them and runs while they are in flight)
   lds_dma(a.qkv + (size_t)kv * G * HD, q_s, G * HD);
   lds_dma(a.qkv + (size_t)a.heads * HD + (size_t)kv * HD, kx, HD);
   lds_dma(a.qkv + (size_t)(a.heads + a.kv_heads) * HD + (size_t)kv * HD, vx, HD);
@@ -162,23 +166,19 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
     lds_dma(a.qn_w, nq, HD);
     lds_dma(a.kn_w, nk, HD);
   }
-  // rotary (cos, sin) of the lane's pairs at the position
-  float co[NPR], si[NPR];
-  {
-    const int pc = min(pos, a.ctx - 1);
-#pragma unroll
-    for (int j = 0; j < NPR; ++j) {
-      const float2 v = ldg2f(a.rope_cs + (size_t)pc * HALF + min(lane + 64 * j, HALF - 1));
-      co[j] = v.x;
-      si[j] = v.y;
-    }
-  }
+  // the rotary (cos, sin) row of the position, through LDS as well (a value
+  // loaded into registers before the K/V loads would be awaited with them)
+  lds_dma((const float*)(a.rope_cs + (size_t)min(pos, a.ctx - 1) * HALF), cs_s, HD);
+  __builtin_amdgcn_sched_barrier(0);  // (kept in this order)
+  if (a.spec_kv) load_kv(t_lo);
   const int start = (a.window != 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
   const int c_lo = start / span, c_hi = pos / span;
   const bool active = !stopped && pos < a.ctx && c >= c_lo && c <= c_hi;
   if (active && !a.spec_kv) load_kv(t_lo);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  // everything but the K/V loads has landed (an inactive workgroup, which may
+  // not have issued them, leaves below without reading LDS)
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(NKV + NP));
+  lds_barrier();
   CHONK_MV_T(tr, 1);
   if (stopped) return;
   if (pos >= a.ctx) {
@@ -192,11 +192,14 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
   // fp16 like the cache, into kx; v rounded into vx. The newest chunk also
   // stores k and v to the cache.
   int ia[NPR], ib[NPR];
+  float co[NPR], si[NPR];
 #pragma unroll
   for (int j = 0; j < NPR; ++j) {
     const int d = min(lane + 64 * j, HALF - 1);
     ia[j] = a.interleaved ? 2 * d : d;
     ib[j] = a.interleaved ? 2 * d + 1 : d + HALF;
+    co[j] = cs_s[2 * d];
+    si[j] = cs_s[2 * d + 1];
   }
   const size_t kv_row = ((size_t)kv * a.ctx + pos) * HD;
   for (int it = wave; it < G + 2; it += 4) {
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(kWg) void k_attn_dec(const AttnArgs a) {
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the chunk's K/V rows
   __syncthreads();
 
   // C: over the workgroup's sub-chunks of 64 positions that hold cached
@@ -500,10 +504,10 @@ int attn_dec_sub(int ctx, int per_head) {
 int attn_dec_chunk() { return kDecChunk; }
 
 size_t attn_dec_shared_bytes(int group, int hd, int nchunk) {
-  // q_s, qn [G][hd]; kx, vx, nq, nk [hd]; wmx [4][G], ew [G][64], hv [G][4]
+  // q_s, qn [G][hd]; kx, vx, nq, nk [hd]; wmx [4][G], ew [G][64], hv [G][4]; cs [hd]
   (void)nchunk;
   const size_t g = (size_t)group;
-  return sizeof(float) * (2 * g * hd + 4 * (size_t)hd + g * (4 + kDecChunk + 4));
+  return sizeof(float) * (2 * g * hd + 5 * (size_t)hd + g * (4 + kDecChunk + 4));
 }
 
 namespace {

@@ -178,6 +178,20 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
+// s_waitcnt immediate that waits until at most n vector memory operations of
+// the wave are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt
+// and lgkmcnt left at their maxima, i.e. not waited for).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// A workgroup barrier that orders LDS accesses only: no wait for the global
+// loads in flight (__syncthreads waits for every outstanding memory access).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Copies n floats from global memory into LDS with the CDNA3/4 direct-to-LDS
 // loads (16 bytes per lane, no registers); completion is awaited with
 // s_waitcnt vmcnt(0) + a barrier by the caller.

@@ -696,17 +696,6 @@ __global__ __launch_bounds__(kWg, 2) void k_gemm_sk1(GemmArgs a) {
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// A workgroup barrier that orders LDS accesses only: no wait for the global
-// loads in flight (__syncthreads waits for every outstanding memory access).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 // The same for a matrix with many row groups (the lm_head): a workgroup owns
 // 4 x 64 weight rows over the whole K, the four waves sharing each 64-k block
 // of x operands, copied into LDS one block ahead (two buffers; each wave
