@@ -191,7 +191,19 @@ def q4k_matvec_bandwidth(rows: int = 262144, k: int = 2048, reps: int = 20) -> d
             "note": "generic Q4_K matvec kernel, 256-row tiles; matrix larger than the Infinity Cache"}
 
 
-def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: int) -> dict:
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16
+
+
+def gemm_params(spec) -> int:
+    """Weights of every linear layer of a step (q, k, v, o, gate, up, down per
+    layer and the lm_head): a decode batch multiplies each by every row."""
+    hd = spec.head_dim or spec.hidden // spec.heads
+    per_layer = spec.hidden * (spec.heads + 2 * spec.kv_heads) * hd + spec.heads * hd * spec.hidden \
+        + 3 * spec.hidden * spec.ffn
+    return spec.layers * per_layer + spec.hidden * spec.vocab
+
+
+def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: int, spec=None) -> dict:
     """The batched-decode configuration: `seqs` independent sequences with a
     `prompt`-token random prompt each, then greedy steps over all of them at
     once (one MFMA GEMM per linear layer over the batch rows, paged fp16 K/V)."""
@@ -210,11 +222,21 @@ def batched_decode(eng, vocab: int, seqs: int, prompt: int, steps: int, warmup: 
         cur = b.step(rows, cur)
     el = time.perf_counter() - t1
     b.close()
-    return {"sequences": seqs, "prompt_tokens": prompt, "steps": steps, "warmup": warmup,
-            "ms_per_step": round(1000.0 * el / steps, 4) if steps else None,
-            "tokens_per_sec": round(seqs * steps / el, 1) if steps else None,
-            "prefill_tokens_per_sec": round(seqs * prompt / prefill_s, 1),
-            "note": "host-timed, step = one greedy token for every sequence"}
+    out = {"sequences": seqs, "prompt_tokens": prompt, "steps": steps, "warmup": warmup,
+           "ms_per_step": round(1000.0 * el / steps, 4) if steps else None,
+           "tokens_per_sec": round(seqs * steps / el, 1) if steps else None,
+           "prefill_tokens_per_sec": round(seqs * prompt / prefill_s, 1),
+           "note": "host-timed, step = one greedy token for every sequence"}
+    if spec is not None and steps:
+        # matrix-core use of the whole step: the GEMMs' algorithmic flops (2 x rows x
+        # weights) and the products the hi/lo fp16 split issues (3 per weight-row pair)
+        alg = 2.0 * seqs * gemm_params(spec) / (el / steps) / 1e12
+        out["mfma_util"] = {"alg_tflops": round(alg, 2), "issued_tflops": round(3 * alg, 2),
+                            "peak_tflops": MFMA_PEAK_TFLOPS, "frac_alg": round(alg / MFMA_PEAK_TFLOPS, 4),
+                            "frac_issued": round(3 * alg / MFMA_PEAK_TFLOPS, 4),
+                            "note": "step-level: GEMM flops over the whole step time (attention and glue "
+                                    "included); the per-kernel counters are in profiles/"}
+    return out
 
 
 def main() -> int:
@@ -223,6 +245,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--workload", default="qwen3-0.6b-q4_k_m")
+    ap.add_argument("--kv-dtype", default="f16", choices=["f16", "f32"],
+                    help="K/V cache element type (the reference keeps fp32 K/V)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-rounds", type=int, default=10,
@@ -277,7 +301,7 @@ def main() -> int:
     build_s = time.perf_counter() - t_build
 
     ctx = w.prompt_tokens + 1 + args.warmup + args.steps + 8
-    md = w.model_def(path)
+    md = w.model_def(path, kv_dtype=args.kv_dtype)
     md.max_context = ctx
     loaded = {"gpt-webgpu": load_gpt_wgsl_model, "lfm2-webgpu": load_lfm_wgsl_model,
               "granite-webgpu": load_granite_wgsl_model}.get(
@@ -287,7 +311,7 @@ def main() -> int:
     prompt = w.prompt(1234)
 
     if args.batched_only:
-        bd = batched_decode(eng, w.spec.vocab, 64, 512, args.batched_steps, 4)
+        bd = batched_decode(eng, w.spec.vocab, 64, 512, args.batched_steps, 4, w.spec)
         print(json.dumps({"metric": "batched decode tokens/s (64 sequences), 1xMI355X", "batched_decode": bd,
                           "config": {"workload": w.name}}))
         eng.dispose()
@@ -418,7 +442,7 @@ def main() -> int:
         result["kernel_cold_warm"] = kernel_cold_warm(eng, info, args.cold_reps)
         result["q4k_matvec_hbm"] = q4k_matvec_bandwidth()
     if not args.no_batched and info.get("kv_dtype", 0) == 0 and info.get("architecture") not in (3, 5):
-        result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4)
+        result["batched_decode"] = batched_decode(eng, w.spec.vocab, 64, 512, 32, 4, w.spec)
     if not args.no_cpu_baseline:
         threads = min(16, host_cpus())  # the GPU box's CPU share is 16 threads
         result["cpu_baseline"] = cpu_baseline(path, w, pos0, args.cpu_seconds, threads)

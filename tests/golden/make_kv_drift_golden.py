@@ -2,15 +2,16 @@
 
 The reference keeps K and V in fp32 (llama-wgsl-runtime.ts:830-831); this
 build's default cache is fp16. For the Qwen3-0.6B Q4_K_M configuration
-(2048-token prompt, greedy) and the Gemma-3-270M Q4_K_M configuration
-(1024-token prompt, top-k 40 / T 0.8, seed 9) the oracle runs the reference
+(2048-token prompt, greedy), the Gemma-3-270M Q4_K_M configuration
+(1024-token prompt, top-k 40 / T 0.8, seed 9) and the SmolLM2-135M Q4_K_M
+configuration (32-token prompt, greedy) the oracle runs the reference
 loop twice in lockstep over the same token stream, once with an fp32 cache
 (the reference's semantics, whose choices drive the stream) and once with
 fp16 rounding on store. Every step records the fp32 run's token, its top-1 /
 top-2 logit margin, the drift max|l16 - l32| / max|l32| of the logits, and
 whether the fp16 run picks the same token.
 
-Run: python tests/golden/make_kv_drift_golden.py   (~25 min on 8 cores)
+Run: python tests/golden/make_kv_drift_golden.py [name ...]   (~25 min on 8 cores)
 """
 from __future__ import annotations
 
@@ -30,7 +31,7 @@ sys.path.insert(0, str(ROOT))
 from chonklm_amd import WORKLOADS, write_synthetic_gguf  # noqa: E402
 from oracle.oracle import OracleModel  # noqa: E402
 
-CONFIGS = ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m"]
+CONFIGS = ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m", "smollm2-135m-q4_k_m"]
 STEPS = 128
 OUT = Path(__file__).with_name("kv_drift_golden.json")
 

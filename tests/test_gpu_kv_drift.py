@@ -3,8 +3,9 @@
 The reference stores K and V in fp32 (llama-wgsl-runtime.ts:830-831); this
 build's cache is fp16 by default, fp32 on request. tests/golden/kv_drift_golden.json
 (written by tests/golden/make_kv_drift_golden.py) holds, for the Qwen3-0.6B
-Q4_K_M configuration (2048-token prompt, greedy) and the Gemma-3-270M Q4_K_M
-configuration (1024-token prompt, top-k 40 / T 0.8, seed 9), the token stream of
+Q4_K_M configuration (2048-token prompt, greedy), the Gemma-3-270M Q4_K_M
+configuration (1024-token prompt, top-k 40 / T 0.8, seed 9) and the SmolLM2-135M
+Q4_K_M configuration (32-token prompt, greedy), the token stream of
 the oracle run with an fp32 cache (the reference's semantics), the top-1/top-2
 logit margin at every step, the logit drift of an fp16-cache run fed the same
 stream and whether its pick agrees.
@@ -12,10 +13,10 @@ stream and whether its pick agrees.
 On the GPU both caches are fed that stream (teacher forcing, so one divergent
 pick does not change the later contexts):
 
-* fp32 cache: every pick equals the fp32 oracle's (both configurations);
-* fp16 cache, greedy Qwen3: every pick of the 128 steps equals the fp32
-  oracle's, so the default cache reproduces the reference's greedy output at
-  2K context;
+* fp32 cache: every pick equals the fp32 oracle's (every configuration);
+* fp16 cache, greedy Qwen3 and SmolLM2: every pick of the 128 steps equals the
+  fp32 oracle's, so the default cache reproduces the reference's greedy output
+  (Qwen3 at 2K context);
 * fp16 cache, sampled Gemma-3: the fp16 oracle itself picks differently from
   the fp32 oracle at 3 of 128 steps. A sampled pick moves when a candidate
   group's winner changes or when the draw sits near a cumulative-probability
@@ -69,7 +70,7 @@ def _stream_picks(synth, name: str, kv: str) -> tuple[list[int], dict]:
     return picks, g
 
 
-@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m"])
+@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m", "smollm2-135m-q4_k_m"])
 def test_fp32_cache_follows_fp32_oracle(synth, name):
     picks, g = _stream_picks(synth, name, "f32")
     bad = [i for i, (a, b) in enumerate(zip(picks, g["ids_fp32_kv"])) if a != b]
@@ -77,7 +78,7 @@ def test_fp32_cache_follows_fp32_oracle(synth, name):
                      f"(oracle margins there {[round(g['margins_fp32_kv'][i], 6) for i in bad[:8]]})")
 
 
-@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m"])
+@pytest.mark.parametrize("name", ["qwen3-0.6b-q4_k_m", "gemma3-270m-q4_k_m", "smollm2-135m-q4_k_m"])
 def test_fp16_cache_drift_against_fp32_oracle(synth, name):
     picks, g = _stream_picks(synth, name, "f16")
     assert max(g["drift_fp16_vs_fp32"]) < 1e-3
