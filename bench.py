@@ -89,7 +89,9 @@ def kernel_symbol(cls: str, info: dict) -> str:
             mv["outproj"] = "k_mvr_add_gate"
     if info["ffn"] > 4096 and "down" in mv and os.environ.get("CHONK_MV") != "generic":
         mv["down"] = "k_mvr_add_bias_wide"  # rows above 4096 stage the input through LDS
-    return {"attn": attn, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
+    # the q|k|v matvec and the decode attention in one launch (layers after the first)
+    fused = f"k_qkv_attn<{g}, {hd}>"
+    return {"attn": attn, "qkv_attn": fused, "lmhead": "k_mv_logits", **mv}.get(cls, cls)
 
 
 def host_cpus() -> int:

@@ -76,6 +76,7 @@ class EngineInfoC(C.Structure):
         ("persistent_step", C.c_int32),
         ("noalloc_prefill_rows", C.c_int32),
         ("spin_attention", C.c_int32),
+        ("fused_attention", C.c_int32),
     ]
 
 

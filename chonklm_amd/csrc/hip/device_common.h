@@ -49,7 +49,8 @@ struct DevState {
   int32_t generating;     // 1: select appends to gen[] and checks EOS / budget
   int32_t n_generated;
   int32_t max_generated;
-  int32_t error;          // 1: a kernel saw pos >= context
+  int32_t error;          // 1: a kernel saw pos >= context; 2: token id out of range; 4: the decode attention's
+                          // chunk rows, 5: the fused launch's q|k|v rows did not arrive within the wait bound
   int32_t last_token;     // token selected by the last logits step
   int32_t pad;
 };

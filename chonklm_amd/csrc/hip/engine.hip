@@ -493,12 +493,15 @@ struct LayerDev {
 };
 
 struct Launch {
-  enum Kind { MV, ATTN, SEL, SSM } kind = MV;
+  // QKVATTN: the q|k|v matvec (mv, nq workgroups) and the decode attention (at)
+  // in one launch (k_qkv_attn)
+  enum Kind { MV, ATTN, SEL, SSM, QKVATTN } kind = MV;
   MvArgs mv{};
   SsmArgs ssm{};
   AttnArgs at{};
   SelArgs sel{};
   int grid = 0;
+  int nq = 0;  // QKVATTN: the matvec's workgroups, ahead of the attention's
   size_t shmem = 0;
   std::string name;
   uint64_t weight_bytes = 0;  // GGUF weight bytes read (matvec)
@@ -542,6 +545,10 @@ struct chonk_engine {
   int dnchunk = 0;                // workgroup chunks of dsub x 64 positions
   int dsub = 1;
   tagged_t* dpart = nullptr;      // k_attn_dec chunk rows
+  // the q|k|v matvec inside the attention launch (k_qkv_attn): its rows as
+  // tagged words, [heads * hd | kv_heads * hd | kv_heads * hd]
+  bool fuse_qkv = false;
+  tagged_t* qkv_tag = nullptr;
   std::vector<std::pair<uint32_t, float*>> rope_tables;  // theta -> [hd/2] inverse frequencies
   std::vector<std::pair<uint32_t, float2*>> rope_cs;     // theta -> [ctx][hd/2] (cos, sin)
   // per-phase kernels of one step (qkv, attn, oproj, gateup, down per layer; lm_head, select)
@@ -550,6 +557,12 @@ struct chonk_engine {
   std::vector<Launch> step_logits, step_plain;
   hipGraph_t graph_logits = nullptr, graph_plain = nullptr;
   hipGraphExec_t exec_logits = nullptr, exec_plain = nullptr;
+  // the same steps with the q|k|v matvec and the attention as separate launches:
+  // what the engine replays while another engine lives on its device (fuse_qkv)
+  std::vector<Launch> step_logits_sep, step_plain_sep;
+  hipGraph_t graph_logits_sep = nullptr, graph_plain_sep = nullptr;
+  hipGraphExec_t exec_logits_sep = nullptr, exec_plain_sep = nullptr;
+  bool registered = false;  // counted in device_engines()
   // pinned host staging
   DevState* h_state = nullptr;
   int32_t* h_tok = nullptr;
@@ -1042,7 +1055,8 @@ const float2* rope_cs_table(chonk_engine* e, uint32_t theta, int hd) {
   return p;
 }
 
-void build_steps(chonk_engine* e) {
+// fuse: join each qualifying layer's q|k|v matvec and attention (fuse_qkv engines)
+void build_steps(chonk_engine* e, bool fuse) {
   const ModelCfg& c = e->cfg;
   const int H = c.hidden;
   auto mv_base = [&]() {
@@ -1309,7 +1323,44 @@ void build_steps(chonk_engine* e) {
       }
       L.name = li + "attn";
       L.layer = i;
-      steps.push_back(L);
+      // the layer's q|k|v matvec (the launch before) joins this one when it is
+      // the three-matrix row kernel with the RMSNorm prologue, an instance
+      // exists and the joint grid fits on the device at once
+      Launch* Q = steps.empty() ? nullptr : &steps.back();
+      if (fuse && e->fuse_qkv && Q && Q->kind == Launch::MV && Q->layer == i && Q->name == li + "qkv" &&
+          Q->mv.pro == PRO_NORM && Q->mv.nseg == 3 && Q->mv.row_kernel && L.at.variant == 1 && L.at.sub == 1) {
+        Launch F;
+        F.kind = Launch::QKVATTN;
+        F.mv = Q->mv;
+        F.mv.epi = EPI_TAG;
+        F.mv.tag_epoch = e->cnt;
+        F.mv.seg[0].out = (float*)e->qkv_tag;  // (EPI_TAG stores 8-byte tagged words)
+        F.mv.seg[1].out = (float*)(e->qkv_tag + qdim);
+        F.mv.seg[2].out = (float*)(e->qkv_tag + qdim + kvdim);
+        F.mv.seg[0].tag_div = G * c.hd;
+        F.mv.seg[1].tag_div = c.hd;
+        F.mv.seg[2].tag_div = c.hd;
+        F.at = L.at;
+        F.at.qkv_tag = e->qkv_tag;
+        // the attention's K/V requests wait 0.9 us, behind the matvec's loads (measured at the
+        // Qwen3-0.6B shape at 2K context: 1223 -> 1240 tokens/s; 0.6 and 1.2 us gained less);
+        // CHONK_KV_DELAY overrides (ticks of 10 ns)
+        F.at.kv_delay = 90;
+        if (const char* kd = std::getenv("CHONK_KV_DELAY")) F.at.kv_delay = std::max(0, std::min(1000, std::atoi(kd)));
+        F.nq = Q->grid;
+        F.grid = Q->grid + L.grid;
+        F.shmem = std::max(Q->shmem, L.shmem);
+        F.name = li + "qkv_attn";
+        F.weight_bytes = Q->weight_bytes;
+        F.layer = i;
+        if (qkv_attn_resident(e->device, G, c.hd, F.shmem) >= F.grid) {
+          steps.back() = F;
+        } else {
+          steps.push_back(L);
+        }
+      } else {
+        steps.push_back(L);
+      }
     }
     // o projection
     if (!lc.conv && !lc.mamba) {
@@ -1499,6 +1550,7 @@ void enqueue(const Launch& L, hipStream_t s) {
     case Launch::ATTN: HIP_OK(launch_attention(L.at, L.shmem, s)); break;
     case Launch::SSM: HIP_OK(launch_ssm(L.ssm, s)); break;
     case Launch::SEL: HIP_OK(launch_select(L.sel, s)); break;
+    case Launch::QKVATTN: HIP_OK(launch_qkv_attn(L.mv, L.nq, L.at, L.shmem, s)); break;
   }
 }
 
@@ -1545,8 +1597,41 @@ void release_spin(int device, const chonk_engine* e) {
   if (it != c.owner.end() && it->second == e) c.owner.erase(it);
 }
 
+// The engines alive on each device. The fused q|k|v + attention launch needs
+// its whole grid resident at once (the attention's chunks wait for each
+// other's rows). A launch of another engine's stream that the dispatcher
+// interleaves with a partly dispatched fused grid can wait for the resources
+// its resident workgroups hold while the rest of the grid waits behind it, so
+// an engine replays its fused steps only while it is the only engine on its
+// device (under this lock, which also orders a new engine's registration after
+// the fused steps already queued: registration waits for them to finish).
+struct DeviceEngines {
+  std::mutex mu;
+  std::map<int, std::vector<chonk_engine*>> live;
+};
+DeviceEngines& device_engines() {
+  static DeviceEngines* d = new DeviceEngines();
+  return *d;
+}
+void register_engine(chonk_engine* e) {
+  DeviceEngines& d = device_engines();
+  std::lock_guard<std::mutex> l(d.mu);
+  for (chonk_engine* o : d.live[e->device]) HIP_OK(hipStreamSynchronize(o->stream));
+  d.live[e->device].push_back(e);
+  e->registered = true;
+}
+void unregister_engine(chonk_engine* e) {
+  if (!e->registered) return;
+  DeviceEngines& d = device_engines();
+  std::lock_guard<std::mutex> l(d.mu);
+  auto& v = d.live[e->device];
+  v.erase(std::remove(v.begin(), v.end(), e), v.end());
+  e->registered = false;
+}
+
 void engine_free(chonk_engine* e) {
   if (!e) return;
+  unregister_engine(e);
   release_spin(e->device, e);
   (void)hipSetDevice(e->device);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
@@ -1554,6 +1639,10 @@ void engine_free(chonk_engine* e) {
   if (e->exec_plain) (void)hipGraphExecDestroy(e->exec_plain);
   if (e->graph_logits) (void)hipGraphDestroy(e->graph_logits);
   if (e->graph_plain) (void)hipGraphDestroy(e->graph_plain);
+  if (e->exec_logits_sep) (void)hipGraphExecDestroy(e->exec_logits_sep);
+  if (e->exec_plain_sep) (void)hipGraphExecDestroy(e->exec_plain_sep);
+  if (e->graph_logits_sep) (void)hipGraphDestroy(e->graph_logits_sep);
+  if (e->graph_plain_sep) (void)hipGraphDestroy(e->graph_plain_sep);
   e->weights.release();
   e->state.release();
   uncached_pool().give_back(e->device, e->uncached);
@@ -1589,6 +1678,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   const ModelCfg& c = e->cfg;
   HIP_OK(hipSetDevice(e->device));
   HIP_OK(hipStreamCreate(&e->stream));
+  register_engine(e.get());
   e->kv_elem = def->kv_dtype == CHONK_KV_F32 ? 4 : 2;
 
   const int H = c.hidden, qdim = c.heads * c.hd, kvdim = c.kv_heads * c.hd;
@@ -1770,6 +1860,11 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     }
     // (another engine on this GPU holds the spin-merging attention: k_attention)
     if (e->dec_attn && !claim_spin(e->device, e.get())) e->dec_attn = false;
+    // the q|k|v matvec joins the attention launch where the layer allows it
+    // (build_steps checks the instance and the grid's residency per layer);
+    // CHONK_FUSE=0 keeps them apart
+    const char* fv = std::getenv("CHONK_FUSE");
+    e->fuse_qkv = e->dec_attn && e->dsub == 1 && !(fv && std::strcmp(fv, "0") == 0);
   }
   const size_t kv_bytes = (size_t)kvdim * c.ctx * e->kv_elem;
   const size_t bits_words = (size_t)(c.vocab + 31) / 32;
@@ -1786,6 +1881,8 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   const size_t dpart_bytes =
       e->dec_attn ? (size_t)c.kv_heads * e->dnchunk * attn_rowf(G, c.hd) * sizeof(tagged_t) : 0;
   sbytes += align256(dpart_bytes);
+  const size_t qkv_tag_bytes = e->fuse_qkv ? (size_t)(qdim + 2 * kvdim) * sizeof(tagged_t) : 0;
+  sbytes += align256(qkv_tag_bytes);
   e->state.reserve(sbytes);
 
   // weights
@@ -1972,6 +2069,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
     HIP_OK(hipMemset(e->cnt, 0, (size_t)c.kv_heads * 4));
   }
   if (e->dec_attn) e->dpart = (tagged_t*)e->state.take(dpart_bytes);
+  if (e->fuse_qkv) e->qkv_tag = (tagged_t*)e->state.take(qkv_tag_bytes);
   e->st = (DevState*)e->state.take(sizeof(DevState));
   e->samp = (DevSampling*)e->state.take(sizeof(DevSampling));
   e->hist = (int32_t*)e->state.take((size_t)(c.ctx + 1) * 4);
@@ -1981,6 +2079,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
   HIP_OK(hipMemset((void*)e->resA, 0, e->state.capacity() - 2 * align256(kv_bytes) * kv_layers));
   // chunk rows start with tag 0xffffffff, which no launch uses (epochs start at 0)
   if (e->dpart) HIP_OK(hipMemset(e->dpart, 0xff, dpart_bytes));
+  if (e->qkv_tag) HIP_OK(hipMemset(e->qkv_tag, 0xff, qkv_tag_bytes));
   for (const LayerDev& L : e->layers) {
     if (!L.kc) continue;
     HIP_OK(hipMemset(L.kc, 0, kv_bytes));
@@ -1994,7 +2093,15 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
 
   HIP_OK(init_kernel_attributes());
   HIP_OK(init_gemm_attributes());
-  build_steps(e.get());
+  build_steps(e.get(), false);
+  if (e->fuse_qkv) {
+    e->step_logits_sep = e->kernels_logits;
+    e->step_plain_sep = e->kernels_plain;
+    build_steps(e.get(), true);
+    bool any = false;
+    for (const Launch& L : e->kernels_logits) any = any || L.kind == Launch::QKVATTN;
+    e->fuse_qkv = any;  // (no layer qualified: one set of steps)
+  }
   e->step_logits = e->kernels_logits;
   e->step_plain = e->kernels_plain;
   // CHONK_PREFILL=token keeps the reference's token-by-token prompt pass
@@ -2014,6 +2121,10 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
                                     std::to_string(lds_limit()) + "-byte limit of this device");
   capture(e.get(), e->step_plain, &e->graph_plain, &e->exec_plain);
   capture(e.get(), e->step_logits, &e->graph_logits, &e->exec_logits);
+  if (e->fuse_qkv) {
+    capture(e.get(), e->step_plain_sep, &e->graph_plain_sep, &e->exec_plain_sep);
+    capture(e.get(), e->step_logits_sep, &e->graph_logits_sep, &e->exec_logits_sep);
+  }
   *out = e.release();
 }
 
@@ -2028,12 +2139,22 @@ void check_injected_failure(chonk_engine* e, const char* where) {
 
 // One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
 // cannot trace graph launches) the same launches issued one by one.
+// (an engine with fused steps replays them only while it is alone on its device)
 void replay(chonk_engine* e, bool logits) {
   check_injected_failure(e, "hipGraphLaunch");
+  std::unique_lock<std::mutex> l;
+  bool sep = false;
+  if (e->fuse_qkv) {
+    DeviceEngines& d = device_engines();
+    l = std::unique_lock<std::mutex>(d.mu);
+    sep = d.live[e->device].size() > 1;
+  }
   if (e->use_graph) {
-    HIP_OK(hipGraphLaunch(logits ? e->exec_logits : e->exec_plain, e->stream));
+    hipGraphExec_t x = logits ? (sep ? e->exec_logits_sep : e->exec_logits) : (sep ? e->exec_plain_sep : e->exec_plain);
+    HIP_OK(hipGraphLaunch(x, e->stream));
   } else {
-    for (const Launch& L : logits ? e->step_logits : e->step_plain) enqueue(L, e->stream);
+    for (const Launch& L : logits ? (sep ? e->step_logits_sep : e->step_logits) : (sep ? e->step_plain_sep : e->step_plain))
+      enqueue(L, e->stream);
   }
 }
 
@@ -2823,6 +2944,8 @@ int chonk_engine_info_get(const chonk_engine* e, chonk_engine_info* out) {
   out->persistent_step = 0;  // (the one-launch-per-token step was retired: the graph ran twice as fast)
   out->noalloc_prefill_rows = e->noalloc_rows;
   out->spin_attention = e->dec_attn ? 1 : 0;
+  out->fused_attention = 0;
+  for (const Launch& L : e->kernels_logits) out->fused_attention += L.kind == Launch::QKVATTN ? 1 : 0;
   return CHONK_OK;
 }
 
@@ -3142,10 +3265,11 @@ int chonk_engine_bench_kernel(chonk_engine* e, int32_t kernel_id, int32_t reps, 
     if (name && name_len) std::snprintf(name, name_len, "%s", L.name.c_str());
     if (bytes) {
       uint64_t by = L.weight_bytes;
-      if (L.kind == Launch::MV) {
+      if (L.kind == Launch::MV || L.kind == Launch::QKVATTN) {
         by += (uint64_t)L.mv.k * 4;
-        for (int i = 0; i < L.mv.nseg; ++i) by += (uint64_t)L.mv.seg[i].n_out * 4;
-      } else if (L.kind == Launch::ATTN) {
+        for (int i = 0; i < L.mv.nseg; ++i) by += (uint64_t)L.mv.seg[i].n_out * (L.kind == Launch::MV ? 4 : 8);
+      }
+      if (L.kind == Launch::ATTN || L.kind == Launch::QKVATTN) {
         const int pos = e->pos;
         const int w = L.at.window;
         const int start = (w != 0 && pos + 1 > w) ? pos + 1 - w : 0;

@@ -211,7 +211,7 @@ struct SegView {
   float* out;
   const float* add;
   const float* bias;
-  int n_out, tile, lpr, wg_begin;
+  int n_out, tile, lpr, wg_begin, tag_div;
 };
 
 // ---- matvec core (k_mv_*) -----------------------------------------------

@@ -36,6 +36,7 @@ enum EpiMode : int32_t {
   EPI_GLU_GELU = 3, // out[n] = gelu_tanh(gate_n) * up_n
   EPI_LOGITS = 4,   // logits[n] = acc; group candidate per 256 rows (lfm2: per residue class mod 256)
   EPI_GELU = 5,     // out[n] = gelu_tanh(acc + bias[n]) (GPT-2 MLP up projection)
+  EPI_TAG = 6,      // ((uint64_t*)out)[n] = {acc, tag_epoch[n / tag_div]}: q|k|v rows of the fused attention launch
 };
 
 struct MvSeg {
@@ -48,6 +49,7 @@ struct MvSeg {
   int32_t tile;      // output rows per workgroup
   int32_t lpr;       // lanes per row (power of two, <= 64)
   int32_t wg_begin;  // first workgroup of this segment
+  int32_t tag_div;   // EPI_TAG: rows per kv head (the row's tag is tag_epoch[row / tag_div])
 };
 
 struct MvArgs {
@@ -89,6 +91,7 @@ struct MvArgs {
   const float* gate_z;     // PRO_GATE: the gate z (the first k rows of the Mamba2 in_proj output)
   float add_scale;         // EPI_ADD: out = add + acc * add_scale when non-zero (granitehybrid's 0.246)
   float logit_scale;       // EPI_LOGITS: logits = acc * logit_scale when non-zero (granitehybrid's 1/3)
+  const uint32_t* tag_epoch;  // EPI_TAG: the attention's per-kv-head epochs
 };
 
 // One Mamba2 step of a granitehybrid layer (granite-wgsl-runtime.ts:1476-1562):
@@ -121,6 +124,7 @@ struct AttnArgs {
   uint32_t* cnt;          // [kv_heads], uncached memory: k_attention's arrival counters (zero
                           // between launches), k_attn_dec's per-head epochs
   uint64_t* tpart;        // k_attn_dec: [kv_heads][nchunk] rows of tagged words
+  const uint64_t* qkv_tag;  // fused q|k|v + attention launch: q | k | v as tagged words (qkv unused)
   const float2* rope_cs;  // k_attn_dec: [ctx][hd/2] (cos, sin) of the rotary angles
   float* out;             // [heads*hd]
   DevState* st;
@@ -132,6 +136,7 @@ struct AttnArgs {
   int32_t sub;            // k_attn_dec: 64-position sub-chunks walked by one workgroup
   int32_t tpp;            // threads per position in the score phase (power of two)
   int32_t variant;        // 0: k_attention; 1: k_attn_dec (fp16 cache, 64-position chunks)
+  int32_t kv_delay;       // fused q|k|v + attention launch: 10 ns ticks before the K/V requests
   float eps, scale;
 };
 
@@ -190,6 +195,12 @@ size_t attn_dec_shared_bytes(int group, int hd, int nchunk);
 // that spills registers to scratch, which the engine then does not use.
 int attn_dec_resident(int device, int group, int hd, size_t shmem, bool walk);
 hipError_t launch_attn_dec(const AttnArgs& a, size_t shmem, hipStream_t s);
+// The fused q|k|v matvec + decode attention launch (k_qkv_attn): the matvec's
+// nq workgroups (m planned for the row kernel, EPI_TAG, PRO_NORM) ahead of the
+// attention's kv_heads * nchunk. Resident workgroups of the instance for
+// (group, hd) at `shmem` bytes of LDS on the device (0: no such instance).
+int qkv_attn_resident(int device, int group, int hd, size_t shmem);
+hipError_t launch_qkv_attn(const MvArgs& m, int nq, const AttnArgs& a, size_t shmem, hipStream_t s);
 // cs[p][d] = (cos, sin)(p * inv[d]) for p < ctx, d < half.
 hipError_t launch_rope_cs(const float* inv, int half, int ctx, float2* cs, hipStream_t s);
 hipError_t launch_select(const SelArgs& a, hipStream_t s);

@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "attn_dec_body.h"
 #include "kernel_common.h"
 #include "kernels.h"
 #include "qdot.h"
@@ -30,8 +31,7 @@ namespace {
 // This workgroup's segment, picked field by field (forming a reference into
 // the argument block would make the compiler copy the whole block to scratch).
 
-__device__ __forceinline__ SegView seg_view(const MvArgs& a) {
-  const int b = (int)blockIdx.x;
+__device__ __forceinline__ SegView seg_view(const MvArgs& a, int b) {
   const bool s1 = a.nseg > 1 && b >= a.seg[1].wg_begin;
   const bool s2 = a.nseg > 2 && b >= a.seg[2].wg_begin;
 #define CHONK_PICK(f) (s2 ? a.seg[2].f : (s1 ? a.seg[1].f : a.seg[0].f))
@@ -55,6 +55,7 @@ __device__ __forceinline__ SegView seg_view(const MvArgs& a) {
   v.tile = CHONK_PICK(tile);
   v.lpr = CHONK_PICK(lpr);
   v.wg_begin = CHONK_PICK(wg_begin);
+  v.tag_div = CHONK_PICK(tag_div);
 #undef CHONK_PICK
   return v;
 }
@@ -248,7 +249,7 @@ template <int EPI, int TT = -1, int AH = 0>
 __device__ __forceinline__ void matvec_body(const MvArgs& a) {
   extern __shared__ __align__(16) float smem[];
   const MvLds l = mv_lds(smem, a.k);
-  const SegView g = seg_view(a);
+  const SegView g = seg_view(a, (int)blockIdx.x);
   const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
@@ -398,13 +399,15 @@ __device__ __forceinline__ void conv_commit(const float* proj, float* s1, float*
 // GB: 0 llama family; 1 GPT-2 epilogue terms (a per-row bias and the residual sanitize)
 // compiled in; 2 as 1 with the input staged through LDS (rows wider than the 4096 that the
 // register-resident prologue holds)
+// wg: the workgroup's index in the launch's matvec grid (blockIdx.x, or its
+// index among the q|k|v workgroups of the fused attention launch).
 template <int EPI, int PRO, int GB>
-__device__ __forceinline__ void mv_row_body(const MvArgs& a) {
+__device__ __forceinline__ void mv_row_body(const MvArgs& a, int wg) {
   extern __shared__ __align__(16) float smem[];
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
   const MvLds l = mv_lds(smem, a.k);
-  const SegView g = seg_view(a);
-  const int t0 = ((int)blockIdx.x - g.wg_begin) * g.tile;
+  const SegView g = seg_view(a, wg);
+  const int t0 = (wg - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
   const int lpr = g.lpr;
   const int lg = (int)threadIdx.x >> __builtin_ctz((unsigned)lpr);
@@ -450,6 +453,8 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
   }
   float addv = 0.f, biasv = 0.f;
   if constexpr (EPI == EPI_ADD) addv = g.add[row];
+  uint32_t tagv = 0;
+  if constexpr (EPI == EPI_TAG) tagv = a.tag_epoch[row / g.tag_div];
   if constexpr (GB) {
     if (g.bias) biasv = g.bias[row];
   }
@@ -526,7 +531,7 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     live = true;
   });
   if (!live) return;
-  if (a.conv_commit && blockIdx.x == 0) conv_commit(a.conv_proj, a.conv_s1, a.conv_s2, a.conv_n);
+  if (a.conv_commit && wg == 0) conv_commit(a.conv_proj, a.conv_s1, a.conv_s2, a.conv_n);
   if (owner) {
     if constexpr (GB) {
       if (g.bias) rg = __fadd_rn(rg, biasv);
@@ -541,14 +546,15 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a) {
     if constexpr (EPI == EPI_GLU_SILU) g.out[row] = silu_mul(rg, ru);
     if constexpr (EPI == EPI_GLU_GELU) g.out[row] = __fmul_rn(gelu_tanh(rg), ru);
     if constexpr (EPI == EPI_GELU) g.out[row] = gelu_tanh(rg);
+    if constexpr (EPI == EPI_TAG) tag_put((tagged_t*)g.out + row, rg, tagv);
   }
-  if (a.advance_pos && blockIdx.x == 0 && threadIdx.x == 0) a.st->pos = a.st->pos + 1;
+  if (a.advance_pos && wg == 0 && threadIdx.x == 0) a.st->pos = a.st->pos + 1;
   CHONK_MV_T(tr, 4);
   CHONK_MV_TRACE_END(tr, EPI * 65536 + a.k);
 }
 
 #define CHONK_MVR(NAME, EPI, PRO, GB) \
-  __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO, GB>(a); }
+  __global__ __launch_bounds__(kWg) void NAME(const MvArgs a) { mv_row_body<EPI, PRO, GB>(a, (int)blockIdx.x); }
 CHONK_MVR(k_mvr_store_plain, EPI_STORE, PRO_PLAIN, 0)
 CHONK_MVR(k_mvr_store_norm, EPI_STORE, PRO_NORM, 0)
 CHONK_MVR(k_mvr_store_embed, EPI_STORE, PRO_EMBED_NORM, 0)
@@ -567,6 +573,41 @@ CHONK_MVR(k_mvr_gelu_ln, EPI_GELU, PRO_LN, 1)
 CHONK_MVR(k_mvr_add_bias, EPI_ADD, PRO_PLAIN, 1)
 CHONK_MVR(k_mvr_add_bias_wide, EPI_ADD, PRO_PLAIN, 2)
 #undef CHONK_MVR
+
+// One attention layer's q|k|v matvec and decode attention in one launch.
+// Workgroups [0, nq) are the matvec (RMSNorm prologue; each row stored as a
+// word tagged with its kv head's epoch, the tag the attention of that head
+// polls for); workgroup nq + w is the attention of kv head w % kv_heads, chunk
+// w / kv_heads, which requests its K/V rows at entry and polls its group's q,
+// k and v words while they are in flight. The matvec workgroups wait for
+// nothing, and the engine uses this kernel only when the whole grid fits on
+// the device at once (the attention's chunks wait for each other's rows).
+template <int G, int HD>
+__global__ __launch_bounds__(kWg, 4) void k_qkv_attn(const MvArgs m, const AttnArgs a, int nq) {
+  const int b = (int)blockIdx.x;
+  if (b < nq) {
+    mv_row_body<EPI_TAG, PRO_NORM, 0>(m, b);
+    return;
+  }
+  const int w = b - nq;
+  attn_dec_body<G, HD, false, true>(a, w % a.kv_heads, w / a.kv_heads);
+}
+
+template <int G, int HD>
+const void* qkv_attn_fn() {
+  return (const void*)k_qkv_attn<G, HD>;
+}
+// the instances built: groups 1-4 at head sizes 64 and 128
+const void* qkv_attn_kernel(int group, int hd) {
+  if (hd != 64 && hd != 128) return nullptr;
+  switch (group) {
+    case 1: return hd == 64 ? qkv_attn_fn<1, 64>() : qkv_attn_fn<1, 128>();
+    case 2: return hd == 64 ? qkv_attn_fn<2, 64>() : qkv_attn_fn<2, 128>();
+    case 3: return hd == 64 ? qkv_attn_fn<3, 64>() : qkv_attn_fn<3, 128>();
+    case 4: return hd == 64 ? qkv_attn_fn<4, 64>() : qkv_attn_fn<4, 128>();
+    default: return nullptr;
+  }
+}
 
 __global__ __launch_bounds__(kWg) void k_mv_store(const MvArgs a) { matvec_body<EPI_STORE>(a); }
 __global__ __launch_bounds__(kWg) void k_mv_add(const MvArgs a) { matvec_body<EPI_ADD>(a); }
@@ -1090,6 +1131,28 @@ hipError_t launch_attention(const AttnArgs& a, size_t shmem, hipStream_t s) {
   }
 #undef CHONK_ATTN_CASE
   return hipGetLastError();
+}
+
+int qkv_attn_resident(int device, int group, int hd, size_t shmem) {
+  const void* f = qkv_attn_kernel(group, hd);
+  if (!f) return 0;
+  // an instance that spills to scratch is not used (0: cannot run)
+  hipFuncAttributes at{};
+  if (hipFuncGetAttributes(&at, f) != hipSuccess || at.localSizeBytes != 0) return 0;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, kWg, shmem) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+  return per_cu * cus;
+}
+
+hipError_t launch_qkv_attn(const MvArgs& m, int nq, const AttnArgs& a, size_t shmem, hipStream_t s) {
+  const int group = a.heads / a.kv_heads;
+  const void* f = qkv_attn_kernel(group, a.hd);
+  if (!f || a.variant != 1 || a.sub != 1 || !a.qkv_tag || m.epi != EPI_TAG || m.pro != PRO_NORM || !m.row_kernel ||
+      nq <= 0)
+    return hipErrorInvalidValue;
+  void* args[] = {(void*)&m, (void*)&a, (void*)&nq};
+  return hipLaunchKernel(f, dim3((unsigned)(nq + a.kv_heads * a.nchunk)), dim3(kWg), args, shmem, s);
 }
 
 hipError_t launch_select(const SelArgs& a, hipStream_t s) {

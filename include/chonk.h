@@ -95,6 +95,7 @@ typedef struct {
   int32_t persistent_step;          /* always 0 (kept for layout: the one-launch step was retired) */
   int32_t noalloc_prefill_rows;     /* most tokens one chonk_engine_prefill_noalloc call takes (0: none) */
   int32_t spin_attention;           /* 1: decodes with the spin-merging attention (one engine per GPU) */
+  int32_t fused_attention;          /* layers whose q|k|v matvec runs inside the attention launch */
 } chonk_engine_info;
 
 typedef struct {

@@ -26,7 +26,7 @@ def test_prefill_noalloc_matches_prefill(synth, name, lengths):
     a = LlamaWgslEngine(md)
     b = LlamaWgslEngine(md)
     rows = b.info["noalloc_prefill_rows"]
-    assert 16 <= rows <= 512 and rows % 16 == 0
+    assert 16 <= rows <= 2048 and rows % 16 == 0  # (at most one full pass of 2048 rows)
     first, second = lengths
     first = first or min(rows, md.max_context - 8)
     assert second < first <= rows
