@@ -30,7 +30,9 @@
  * on one GPU only the first that qualifies decodes with the spin-merging
  * attention (chunks of one launch wait for each other, so its grid must be
  * resident at once); engines created while it exists use the arrival-counter
- * attention, which never waits, so concurrent decoding cannot stall.
+ * attention, which never waits, so concurrent decoding cannot stall. The
+ * spin-merging engine runs its q|k|v matvec inside the attention launch only
+ * while it is the only engine on its GPU (separate launches otherwise).
  * A HIP error marks the engine lost; later calls that touch the device
  * (position, info and destroy still answer) fail fast with CHONK_ELOST
  * (the LFM runtime's deviceLost behaviour, lfm-wgsl-runtime.ts:704-707,
