@@ -31,9 +31,13 @@ namespace {
 // This workgroup's segment, picked field by field (forming a reference into
 // the argument block would make the compiler copy the whole block to scratch).
 
+// ONE: a single-segment launch (the host checks nseg == 1): the fields come
+// straight from seg[0], so the kernel's argument loads are one round of scalar
+// loads instead of two (the segment index, then that segment's fields).
+template <bool ONE = false>
 __device__ __forceinline__ SegView seg_view(const MvArgs& a, int b) {
-  const bool s1 = a.nseg > 1 && b >= a.seg[1].wg_begin;
-  const bool s2 = a.nseg > 2 && b >= a.seg[2].wg_begin;
+  const bool s1 = !ONE && a.nseg > 1 && b >= a.seg[1].wg_begin;
+  const bool s2 = !ONE && a.nseg > 2 && b >= a.seg[2].wg_begin;
 #define CHONK_PICK(f) (s2 ? a.seg[2].f : (s1 ? a.seg[1].f : a.seg[0].f))
   SegView v;
   v.w.s0 = CHONK_PICK(w.s0);
@@ -406,7 +410,9 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a, int wg) {
   extern __shared__ __align__(16) float smem[];
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
   const MvLds l = mv_lds(smem, a.k);
-  const SegView g = seg_view(a, wg);
+  // (the add and GLU epilogues run single-segment launches)
+  constexpr bool one = EPI == EPI_ADD || EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU || EPI == EPI_GELU;
+  const SegView g = seg_view<one>(a, wg);
   const int t0 = (wg - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
   const int lpr = g.lpr;
@@ -421,6 +427,16 @@ __device__ __forceinline__ void mv_row_body(const MvArgs& a, int wg) {
   CHONK_MV_T(tr, 0);
   MvPro p = mv_pro(a);
   p.pro = PRO;
+  if constexpr (one && (PRO == PRO_PLAIN || PRO == PRO_NORM)) {
+    // every kernel argument the loads below need, in one round of scalar loads
+    // (left to the scheduler they come in two, the second after the first is
+    // awaited): the asm takes them as operands, the barrier keeps the vector
+    // loads after it
+    asm volatile("" ::"s"(g.w.s0), "s"(g.w.s1), "s"(g.w.s2), "s"(g.w.s3), "s"(g.w.type), "s"(g.w.k), "s"(g.u0),
+                 "s"(g.u1), "s"(g.out), "s"(g.add), "s"(t0), "s"(nt), "s"(lpr), "s"(p.in), "s"(p.w_norm), "s"(p.st),
+                 "s"(p.k));
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // plain, norm and convolution prologues keep x (and the norm weight) in
   // registers: thread t holds elements 4 * (t + 256 r) .. + 3 for r < 4 (K <= 4096)
   constexpr bool reg_pro = (PRO == PRO_PLAIN || PRO == PRO_NORM || PRO == PRO_CONV || PRO == PRO_GATE) && GB != 2;
@@ -1027,6 +1043,8 @@ hipError_t init_kernel_attributes() {
 hipError_t launch_matvec(const MvArgs& a, int grid, size_t shmem, hipStream_t s) {
   if (a.row_kernel) {
     void (*k)(const MvArgs) = nullptr;
+    // (the add, GLU and GELU row kernels read segment 0 only)
+    if (a.epi != EPI_STORE && a.nseg != 1) return hipErrorInvalidValue;
     bool gb = a.sanitize != 0;
     for (int i = 0; i < a.nseg; ++i) gb = gb || a.seg[i].bias != nullptr;
     const bool ln = a.pro == PRO_LN || a.pro == PRO_EMBED_LN;
