@@ -26,6 +26,23 @@ namespace {
 
 constexpr float kNegBig = -3.402823e38f;  // the WGSL literal -3.402823e38
 
+// Touches every 64-byte line of the kernel arguments' first BYTES bytes with
+// one round of scalar loads (awaited once), so that the argument loads that
+// depend on each other (a segment's fields after the segment index) find their
+// lines in the scalar cache instead of each round going to memory.
+template <int BYTES>
+__device__ __forceinline__ void warm_kernarg() {
+  static_assert(BYTES <= 16 * 64, "at most 16 lines");
+  const uint32_t* ka = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = i * 64 < BYTES ? ld_scalar(ka + i * 16) : 0u;
+  asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]), "s"(v[8]),
+               "s"(v[9]), "s"(v[10]), "s"(v[11]), "s"(v[12]), "s"(v[13]), "s"(v[14]), "s"(v[15]));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+
 // Cross-lane steps without the LDS crossbar: DPP quad/row permutations inside
 // 16-lane rows, then gfx950's permlane swaps across the rows of a 32-lane half
 // (v_permlane16_swap) and across the halves (v_permlane32_swap) — VALU ops,

@@ -407,11 +407,17 @@ __device__ __forceinline__ void conv_commit(const float* proj, float* s1, float*
 // index among the q|k|v workgroups of the fused attention launch).
 template <int EPI, int PRO, int GB>
 __device__ __forceinline__ void mv_row_body(const MvArgs& a, int wg) {
+  // (the q|k|v launches pick one of three segments: their argument lines are
+  // warmed first; the fused attention launch, EPI_TAG, warms all of its
+  // arguments at entry)
+  if constexpr (EPI == EPI_STORE && GB == 0 && (PRO == PRO_NORM || PRO == PRO_EMBED_NORM))
+    warm_kernarg<(int)sizeof(MvArgs)>();
   extern __shared__ __align__(16) float smem[];
   constexpr bool glu = EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU;
   const MvLds l = mv_lds(smem, a.k);
   // (the add and GLU epilogues run single-segment launches)
   constexpr bool one = EPI == EPI_ADD || EPI == EPI_GLU_SILU || EPI == EPI_GLU_GELU || EPI == EPI_GELU;
+  // (the q|k|v launches pick one of three segments: their argument lines are warmed first)
   const SegView g = seg_view<one>(a, wg);
   const int t0 = (wg - g.wg_begin) * g.tile;
   const int nt = min(g.tile, g.n_out - t0);
@@ -600,6 +606,7 @@ CHONK_MVR(k_mvr_add_bias_wide, EPI_ADD, PRO_PLAIN, 2)
 // the device at once (the attention's chunks wait for each other's rows).
 template <int G, int HD>
 __global__ __launch_bounds__(kWg, 4) void k_qkv_attn(const MvArgs m, const AttnArgs a, int nq) {
+  warm_kernarg<(int)(sizeof(MvArgs) + sizeof(AttnArgs) + sizeof(int))>();
   const int b = (int)blockIdx.x;
   if (b < nq) {
     mv_row_body<EPI_TAG, PRO_NORM, 0>(m, b);
