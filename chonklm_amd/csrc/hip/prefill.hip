@@ -145,6 +145,7 @@ __device__ __forceinline__ float rowt_max(float v, float* red) {
 // that |x| < 2^14 and split into fp16 hi + lo planes (zero-padded to kpad).
 // mode 0: plain; 1: RMSNorm with w.
 __global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
+  warm_kernarg<(int)(sizeof(PfSplitArgs))>();  // (dependent argument rounds hit the scalar cache)
   // the row lives in registers: element tid + kRowT * e of this thread is v[e]
   // (rows of at most 4 * kRowT elements; the launcher checks)
   __shared__ float red[kRowW];
@@ -386,6 +387,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
 // LDS at the end (in wave order) and the workgroup writes its K split's partial.
 
 constexpr int kSkRows = 64;  // weight rows per wave (and per workgroup)
+constexpr int kSkRed = kSkRows + 4;  // k_gemm_sk1's LDS row stride of the per-wave tiles (bank spread)
 
 __device__ __forceinline__ half8_t pack8(const float (&w)[8]) {
   half8_t h;
@@ -621,7 +623,7 @@ __global__ __launch_bounds__(kWg, 2) void k_gemm_sk1(GemmArgs a) {
   // this wave's block: one per wave, the workgroup's four in a row
   const int blk = (int)blockIdx.z * 4 + wave;
   _Float16* xw = (_Float16*)ssm + (size_t)wave * (2 * 2 * 64 * 32);  // this wave's x operands
-  float* xs = ssm + 4 * 64 * kSkRows;                                // the token rows' operand scales
+  float* xs = ssm + 4 * 64 * kSkRed;                                 // the token rows' operand scales
   // x: 16 copies of 1 KiB (16 tokens x 64 bytes each); lane l moves token
   // 16 i + l / 4, piece l % 4 (token rows past a.t repeat the last row: their
   // sums are never written)
@@ -674,22 +676,44 @@ __global__ __launch_bounds__(kWg, 2) void k_gemm_sk1(GemmArgs a) {
     }
   }
   __syncthreads();  // every wave has read its x operands (the area is reused below)
+  // the four waves' tiles [wave][token][row] (rows padded to kSkRed floats, so
+  // that neither the writes below nor the 16-byte reads after them collide on
+  // LDS banks); then thread (token tid / 4, rows 16 (tid % 4) .. + 15) sums its
+  // 16 outputs over the waves with 16-byte reads and stores them with 16-byte
+  // stores — one pass instead of 16 dependent rounds of single floats
   float* red = ssm;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[(wave * 64 + 16 * tt + 4 * g + i) * kSkRows + 16 * rt + r16] = acc[tt][rt][i];
+      for (int i = 0; i < 4; ++i) red[(wave * 64 + 16 * tt + 4 * g + i) * kSkRed + 16 * rt + r16] = acc[tt][rt][i];
   __syncthreads();
-  const int r = tid & 63, tg = tid >> 6, n = n0 + r;
-  if (n < N) {
-    const float wun = ldexpf(1.0f, -a.ws);
-    for (int t = tg; t < a.t; t += 4) {
-      const int e = t * kSkRows + r;
-      const float v = (((red[e] + red[64 * kSkRows + e]) + red[2 * 64 * kSkRows + e]) + red[3 * 64 * kSkRows + e]) *
-                      (wun * xs[t]);
-      a.part[((size_t)blockIdx.z * a.t + t) * N + n] = v;
+  const int t = tid >> 2, q = tid & 3;
+  if (t < a.t) {
+    const float sc = ldexpf(1.0f, -a.ws) * xs[t];
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float* e = red + t * kSkRed + 16 * q + 4 * j;
+      const float4 w0 = *(const float4*)e, w1 = *(const float4*)(e + 64 * kSkRed);
+      const float4 w2 = *(const float4*)(e + 2 * 64 * kSkRed), w3 = *(const float4*)(e + 3 * 64 * kSkRed);
+      v[j] = make_float4((((w0.x + w1.x) + w2.x) + w3.x) * sc, (((w0.y + w1.y) + w2.y) + w3.y) * sc,
+                         (((w0.z + w1.z) + w2.z) + w3.z) * sc, (((w0.w + w1.w) + w2.w) + w3.w) * sc);
+    }
+    const int nq = n0 + 16 * q;
+    float* dst = a.part + ((size_t)blockIdx.z * a.t + t) * N + nq;
+    if (nq + 16 <= N && (N & 3) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *(float4*)(dst + 4 * j) = v[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float o[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2)
+          if (nq + 4 * j + e2 < N) dst[4 * j + e2] = o[e2];
+      }
     }
   }
 }
@@ -810,7 +834,7 @@ __global__ __launch_bounds__(kWg, 2) void k_gemm_lm(GemmArgs a) {
 
 size_t gemm_lm_shared_bytes() { return sizeof(_Float16) * 2 * (2 * 2 * 64 * 32) + sizeof(float) * 64; }
 
-size_t gemm_sk_shared_bytes() { return sizeof(float) * (4 * 64 * kSkRows + 64); }
+size_t gemm_sk_shared_bytes() { return sizeof(float) * (4 * 64 * kSkRed + 64); }
 
 // The decode-batch GEMM applies: at most 64 token rows and a K-quant type it covers.
 bool gemm_sk_applies(const GemmArgs& a) {
@@ -890,6 +914,7 @@ __global__ __launch_bounds__(kWg) void k_pf_norm_add(const float* d, const float
 // act = silu(g) * u or gelu_tanh(g) * u per element, then the split of the row
 // into fp16 planes (one workgroup per token row).
 __global__ __launch_bounds__(kRowT) void k_pf_glu_split(PfGluArgs a) {
+  warm_kernarg<(int)(sizeof(PfGluArgs))>();  // (dependent argument rounds hit the scalar cache)
   // element tid + kRowT * e of the row is v[e] (at most 4 * kRowT elements)
   __shared__ float red[kRowW];
   const int t = blockIdx.x, tid = threadIdx.x;
@@ -1378,6 +1403,7 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
 // acc[hd]] per head for k_bd_merge.
 template <int HD, bool ROPE>
 __global__ __launch_bounds__(kWg) void k_bd_walk(PfAttnArgs a, float* part, int max_pages, int nseg, PfRopeArgs ra) {
+  warm_kernarg<(int)(sizeof(PfAttnArgs) + 2 * sizeof(void*) + sizeof(PfRopeArgs))>();  // (dependent argument rounds hit the scalar cache)
   constexpr int DPT = HD / 4;  // K dims per lane
   constexpr int NKV = DPT / 8;
   constexpr int VD = HD >= 256 ? 4 : 2, VW = VD / 2;
