@@ -45,6 +45,15 @@
 // code never uses this name as an address: the device address comes from
 // hipGetSymbolAddress, once per device (scratch_address).
 constexpr size_t kNoAllocScratchBytes = (size_t)48 << 20;
+constexpr int kMultiSteps = 8;  // decode steps per multi-step graph
+// CHONK_MULTI=0 replays every step as its own graph
+bool multi_off() {
+  static const bool off = [] {
+    const char* v = std::getenv("CHONK_MULTI");
+    return v && v[0] == '0';
+  }();
+  return off;
+}
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace chonk {
@@ -562,6 +571,10 @@ struct chonk_engine {
   std::vector<Launch> step_logits_sep, step_plain_sep;
   hipGraph_t graph_logits_sep = nullptr, graph_plain_sep = nullptr;
   hipGraphExec_t exec_logits_sep = nullptr, exec_plain_sep = nullptr;
+  // kMultiSteps logits steps in one graph: what runs of consecutive steps with
+  // no host work between them replay (one launch gap per kMultiSteps tokens)
+  hipGraph_t graph_multi = nullptr;
+  hipGraphExec_t exec_multi = nullptr;
   bool registered = false;  // counted in device_engines()
   // pinned host staging
   DevState* h_state = nullptr;
@@ -1554,10 +1567,11 @@ void enqueue(const Launch& L, hipStream_t s) {
   }
 }
 
-void capture(chonk_engine* e, const std::vector<Launch>& steps, hipGraph_t* g, hipGraphExec_t* x) {
+void capture(chonk_engine* e, const std::vector<Launch>& steps, hipGraph_t* g, hipGraphExec_t* x, int repeat = 1) {
   HIP_OK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   try {
-    for (const Launch& L : steps) enqueue(L, e->stream);
+    for (int r = 0; r < repeat; ++r)
+      for (const Launch& L : steps) enqueue(L, e->stream);
   } catch (...) {
     hipGraph_t tmp;
     (void)hipStreamEndCapture(e->stream, &tmp);
@@ -1643,6 +1657,8 @@ void engine_free(chonk_engine* e) {
   if (e->exec_plain_sep) (void)hipGraphExecDestroy(e->exec_plain_sep);
   if (e->graph_logits_sep) (void)hipGraphDestroy(e->graph_logits_sep);
   if (e->graph_plain_sep) (void)hipGraphDestroy(e->graph_plain_sep);
+  if (e->exec_multi) (void)hipGraphExecDestroy(e->exec_multi);
+  if (e->graph_multi) (void)hipGraphDestroy(e->graph_multi);
   e->weights.release();
   e->state.release();
   uncached_pool().give_back(e->device, e->uncached);
@@ -2121,6 +2137,7 @@ void create_engine(const chonk_model_def* def, std::unique_ptr<ByteSource> src, 
                                     std::to_string(lds_limit()) + "-byte limit of this device");
   capture(e.get(), e->step_plain, &e->graph_plain, &e->exec_plain);
   capture(e.get(), e->step_logits, &e->graph_logits, &e->exec_logits);
+  if (e->use_graph) capture(e.get(), e->step_logits, &e->graph_multi, &e->exec_multi, kMultiSteps);
   if (e->fuse_qkv) {
     capture(e.get(), e->step_plain_sep, &e->graph_plain_sep, &e->exec_plain_sep);
     capture(e.get(), e->step_logits_sep, &e->graph_logits_sep, &e->exec_logits_sep);
@@ -2137,24 +2154,34 @@ void check_injected_failure(chonk_engine* e, const char* where) {
                                       "chonk_engine_debug_fail_next_launch) at ") + where);
 }
 
-// One decode step: graph replay, or (CHONK_NO_GRAPH=1, for profilers that
-// cannot trace graph launches) the same launches issued one by one.
-// (an engine with fused steps replays them only while it is alone on its device)
-void replay(chonk_engine* e, bool logits) {
-  check_injected_failure(e, "hipGraphLaunch");
-  std::unique_lock<std::mutex> l;
-  bool sep = false;
-  if (e->fuse_qkv) {
-    DeviceEngines& d = device_engines();
-    l = std::unique_lock<std::mutex>(d.mu);
-    sep = d.live[e->device].size() > 1;
-  }
-  if (e->use_graph) {
-    hipGraphExec_t x = logits ? (sep ? e->exec_logits_sep : e->exec_logits) : (sep ? e->exec_plain_sep : e->exec_plain);
-    HIP_OK(hipGraphLaunch(x, e->stream));
-  } else {
-    for (const Launch& L : logits ? (sep ? e->step_logits_sep : e->step_logits) : (sep ? e->step_plain_sep : e->step_plain))
-      enqueue(L, e->stream);
+// n consecutive decode steps with no host work between them: graph replays,
+// or (CHONK_NO_GRAPH=1, for profilers that cannot trace graph launches) the
+// same launches issued one by one. Runs of kMultiSteps logits steps replay the
+// multi-step graph. An engine with fused steps replays them (and the
+// multi-step graph) only while it is alone on its device.
+void replay(chonk_engine* e, bool logits, int64_t n = 1) {
+  while (n > 0) {
+    check_injected_failure(e, "hipGraphLaunch");
+    std::unique_lock<std::mutex> l;
+    bool sep = false;
+    if (e->fuse_qkv) {
+      DeviceEngines& d = device_engines();
+      l = std::unique_lock<std::mutex>(d.mu);
+      sep = d.live[e->device].size() > 1;
+    }
+    if (e->use_graph) {
+      if (logits && !sep && e->exec_multi && n >= kMultiSteps && !multi_off()) {
+        HIP_OK(hipGraphLaunch(e->exec_multi, e->stream));
+        n -= kMultiSteps;
+        continue;
+      }
+      hipGraphExec_t x = logits ? (sep ? e->exec_logits_sep : e->exec_logits) : (sep ? e->exec_plain_sep : e->exec_plain);
+      HIP_OK(hipGraphLaunch(x, e->stream));
+    } else {
+      for (const Launch& L : logits ? (sep ? e->step_logits_sep : e->step_logits) : (sep ? e->step_plain_sep : e->step_plain))
+        enqueue(L, e->stream);
+    }
+    --n;
   }
 }
 
@@ -2770,7 +2797,7 @@ void generate(chonk_engine* e, const int32_t* prompt, size_t n_prompt, int32_t m
     int64_t remaining = max - 1;
     while (remaining > 0 && !st.stopped) {
       const int64_t batch = std::min<int64_t>(remaining, 32);
-      for (int64_t i = 0; i < batch; ++i) replay(e, true);
+      replay(e, true, batch);
       remaining -= batch;
       st = read_state(e);
       if (st.error) throw device_error(e, st);
@@ -3166,12 +3193,12 @@ int chonk_engine_bench_decode(chonk_engine* e, int32_t n_warmup, int32_t n_steps
     int32_t tok = 0;
     HIP_OK(hipMemcpy(&tok, e->hist + e->pos, 4, hipMemcpyDeviceToHost));
     check_token(e, tok);
-    for (int i = 0; i < n_warmup; ++i) replay(e, true);
+    replay(e, true, n_warmup);
     hipEvent_t a, b;
     HIP_OK(hipEventCreate(&a));
     HIP_OK(hipEventCreate(&b));
     HIP_OK(hipEventRecord(a, e->stream));
-    for (int i = 0; i < n_steps; ++i) replay(e, true);
+    replay(e, true, n_steps);
     HIP_OK(hipEventRecord(b, e->stream));
     HIP_OK(hipEventSynchronize(b));
     float ms = 0;
