@@ -26,7 +26,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGM = 64;          // weight rows per workgroup tile
-constexpr int kGT = 64;          // token rows per workgroup tile
+constexpr int kGT = 128;         // token rows per workgroup tile
 constexpr int kGK = 128;         // K per stage (whole units for every type)
 constexpr int kGS = kGK + 8;     // LDS row stride in halves (bank spread)
 
@@ -218,15 +218,19 @@ __global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
 
 // ---- dequant-fused GEMM ----------------------------------------------------------
 
-// y[t][n] (=|+=) sum_k x[t][k] W[n][k] for a kGM x kGT tile. Four waves, each
-// a 32 x 32 quarter (2 x 2 MFMA tiles of 16 x 16, three products each).
+// y[t][n] (=|+=) sum_k x[t][k] W[n][k] for a kGM x kGT tile. The tile's
+// weights are dequantized once per stage into LDS (fp16 hi + lo of W * 2^ws)
+// and serve 128 token rows; wave w owns token rows 32 w .. 32 w + 31 against
+// all 64 weight rows (4 x 2 MFMA tiles of 16 x 16, three products each) and
+// reads its activation operands straight from the planes (each element is
+// read by one lane of one wave, so staging them through LDS would only add a
+// copy). With only the weights in LDS (35 KB) the registers bound the
+// workgroups per CU: three for the Q4_K instance, two for Q6_K.
 template <int T>
 __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   extern __shared__ __align__(16) _Float16 gsm[];
   _Float16* wh = gsm;
   _Float16* wl = wh + kGM * kGS;
-  _Float16* xh = wl + kGM * kGS;
-  _Float16* xl = xh + kGT * kGS;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * kGT;
@@ -248,114 +252,102 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   // this workgroup's stages: part blockIdx.z of ksplit
   const int s_lo = (int)((int64_t)nst * blockIdx.z / a.ksplit);
   const int s_hi = (int)((int64_t)nst * (blockIdx.z + 1) / a.ksplit);
-  // staging roles: weight unit (row wr, unit j of the stage); x quarter row
+  // staging role: weight unit (row wr, unit j of the stage)
   const int wr = tid >> 2, wj = tid & 3;
-  const int xt = tid >> 2, xq = tid & 3;
   const bool w_ok = n0 + wr < N;
-  const bool x_ok = t0 + xt < a.t;
   const float wsc = ldexpf(1.0f, a.ws);
+  // operand role: lane l holds row (or token) l % 16 and k 8 (l / 16) .. + 8 of a 32-k step
+  constexpr int TJ = kGT / 64;  // token tiles of 16 per wave
+  const int col = lane & 15, kq = (lane >> 4) * 8;
+  // the lane's plane rows as 32-bit byte offsets from the planes' (uniform)
+  // bases; a token row past t reads row t - 1: its products are computed and
+  // dropped (the launcher checks that a plane fits 32-bit offsets)
+  uint32_t xo[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+    xo[j] = 2u * ((uint32_t)min(t0 + 16 * (TJ * wave + j) + col, a.t - 1) * (uint32_t)a.kpad + (uint32_t)kq);
+  const char* xhb = (const char*)a.xh;
+  const char* xlb = (const char*)a.xl;
 
-  float4_t acc[2][2];
+  float4_t acc[4][TJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  const int rb = (wave & 1) * 32, tb = (wave >> 1) * 32;
+    for (int j = 0; j < TJ; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   Frag<T> f{};
-  uint4 xv[8];
-  // the per-row operand scales of the epilogue, requested up front
-  float xsc[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = t0 + tb + 16 * j + (lane & 15);
-    xsc[j] = t < a.t ? a.xscale[t] : 0.f;
-  }
-  auto fetch = [&](int s) {
-    const int u = s * 4 + wj;
+  auto fetch_w = [&](int st) {
+    const int u = st * 4 + wj;
     if (w_ok && u < U) f = load_unit<T>(wm, n0 - sb + wr, u);
-    if (x_ok) {
-      const uint4* ph = (const uint4*)(a.xh + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
-      const uint4* pl = (const uint4*)(a.xl + (size_t)(t0 + xt) * a.kpad + s * kGK + xq * 32);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        xv[v] = ph[v];
-        xv[4 + v] = pl[v];
-      }
-    }
   };
-  fetch(s_lo);
+  fetch_w(s_lo);
   for (int s = s_lo; s < s_hi; ++s) {
-    __syncthreads();  // the previous stage's tiles are consumed
-    {
-      // weights: the unit's 32 values at their K offsets, hi and lo
-      const int u = s * 4 + wj;
-      float v[32];
-      if (w_ok && u < U) {
-        dequant_unit<T>(f, u, v);
-      } else {
+    // this stage's activation operands (awaited after the weight staging)
+    half8_t bh[kGK / 32][TJ], bl[kGK / 32][TJ];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = 0.f;
+    for (int ks = 0; ks < kGK / 32; ++ks)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const uint32_t o = xo[j] + 2u * (uint32_t)(s * kGK + ks * 32);
+        bh[ks][j] = *(const half8_t*)(xhb + o);
+        bl[ks][j] = *(const half8_t*)(xlb + o);
       }
-      _Float16* rh = wh + wr * kGS;
-      _Float16* rl = wl + wr * kGS;
+    // weights: the unit's 32 values at their K offsets, hi and lo
+    const int u = s * 4 + wj;
+    float v[32];
+    if (w_ok && u < U) {
+      dequant_unit<T>(f, u, v);
+    } else {
 #pragma unroll
-      for (int e = 0; e < 32; e += 4) {
-        const int kk = (u < U ? unit_col<T>(u, e) : 32 * u + e) - s * kGK;
-        half4_t h, l;
+      for (int e = 0; e < 32; ++e) v[e] = 0.f;
+    }
+    // the next stage's unit goes out as soon as this one is decoded (the last
+    // stage requests itself again: no branch around the load)
+    fetch_w(min(s + 1, s_hi - 1));
+    __syncthreads();  // the previous stage's tile is consumed
+    _Float16* rh = wh + wr * kGS;
+    _Float16* rl = wl + wr * kGS;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sv = v[e + i] * wsc;
-          h[i] = (_Float16)sv;
-          l[i] = (_Float16)(sv - (float)h[i]);
-        }
-        *(half4_t*)(rh + kk) = h;
-        *(half4_t*)(rl + kk) = l;
+    for (int e = 0; e < 32; e += 4) {
+      const int kk = (u < U ? unit_col<T>(u, e) : 32 * u + e) - s * kGK;
+      half4_t h, l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sv = v[e + i] * wsc;
+        h[i] = (_Float16)sv;
+        l[i] = (_Float16)(sv - (float)h[i]);
       }
-      // activations: 32 halves of each plane
-      uint4* dh = (uint4*)(xh + xt * kGS + xq * 32);
-      uint4* dl = (uint4*)(xl + xt * kGS + xq * 32);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        dh[q] = x_ok ? xv[q] : make_uint4(0u, 0u, 0u, 0u);
-        dl[q] = x_ok ? xv[4 + q] : make_uint4(0u, 0u, 0u, 0u);
-      }
+      *(half4_t*)(rh + kk) = h;
+      *(half4_t*)(rl + kk) = l;
     }
     __syncthreads();
-    if (s + 1 < s_hi) fetch(s + 1);
-    const int col = lane & 15, kq = (lane >> 4) * 8;
 #pragma unroll
     for (int ks = 0; ks < kGK / 32; ++ks) {
-      half8_t ah[2], al[2], bh[2], bl[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ah[i] = *(const half8_t*)(wh + (rb + 16 * i + col) * kGS + ks * 32 + kq);
-        al[i] = *(const half8_t*)(wl + (rb + 16 * i + col) * kGS + ks * 32 + kq);
-        bh[i] = *(const half8_t*)(xh + (tb + 16 * i + col) * kGS + ks * 32 + kq);
-        bl[i] = *(const half8_t*)(xl + (tb + 16 * i + col) * kGS + ks * 32 + kq);
-      }
+      for (int i = 0; i < 4; ++i) {
+        const half8_t ah = *(const half8_t*)(wh + (16 * i + col) * kGS + ks * 32 + kq);
+        const half8_t al = *(const half8_t*)(wl + (16 * i + col) * kGS + ks * 32 + kq);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = mfma32(ah[i], bh[j], acc[i][j]);
-          acc[i][j] = mfma32(ah[i], bl[j], acc[i][j]);
-          acc[i][j] = mfma32(al[i], bh[j], acc[i][j]);
+        for (int j = 0; j < TJ; ++j) {
+          acc[i][j] = mfma32(ah, bh[ks][j], acc[i][j]);
+          acc[i][j] = mfma32(ah, bl[ks][j], acc[i][j]);
+          acc[i][j] = mfma32(al, bh[ks][j], acc[i][j]);
         }
+      }
     }
   }
   // lane holds rows 4 * (lane / 16) + 0..3 of each row tile, token lane % 16
   const float wun = ldexpf(1.0f, -a.ws);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = t0 + tb + 16 * j + (lane & 15);
-    if (t >= a.t) continue;
-    const float sc = wun * xsc[j];
+  for (int j = 0; j < TJ; ++j) {
+    const int tt = t0 + 16 * (TJ * wave + j) + col;
+    if (tt >= a.t) continue;
+    const float sc = wun * a.xscale[tt];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int n = n0 + rb + 16 * i + 4 * (lane >> 4);
-      float* y = a.y + (size_t)t * a.ldy + n;
-      float* pp = a.part + ((size_t)blockIdx.z * a.t + t) * N + n;
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + 16 * i + 4 * (lane >> 4);
+      float* y = a.y + (size_t)tt * a.ldy + n;
+      float* pp = a.part + ((size_t)blockIdx.z * a.t + tt) * N + n;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if (n + q >= N) break;
@@ -1833,7 +1825,10 @@ __global__ __launch_bounds__(64) void k_row_argmax2(const float* pv, const uint3
 
 // ---- host launchers ----------------------------------------------------------------
 
-size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM + 2 * kGT) * kGS; }
+size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM) * kGS; }
+
+// k_gemm addresses the activation planes with 32-bit byte offsets
+bool gemm_planes_fit(const GemmArgs& a) { return a.t >= 1 && (int64_t)a.t * a.kpad * 2 <= (int64_t)UINT32_MAX; }
 
 size_t fattn_shared_bytes(int hd) {
   return sizeof(_Float16) * ((size_t)kFaKeys * (hd + 8) + (size_t)hd * (kFaKeys + 8));
@@ -1864,6 +1859,7 @@ hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
     hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(kWg), 0, s, a);
     return hipGetLastError();
   }
+  if (!gemm_planes_fit(a)) return hipErrorInvalidValue;
   const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
   a.ksplit = 1;
@@ -1929,13 +1925,14 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
     out->zs = (int64_t)a.t * N;
     return e;
   }
+  if (!gemm_planes_fit(a)) return hipErrorInvalidValue;
   const int tiles = ((N + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
   const int nst = (a.w.k + kGK - 1) / kGK;
-  // split K until about two workgroups per CU are busy; a decode batch (one
-  // row tile) runs faster with half the CUs busy, as fewer, longer-running
+  // split K until about four workgroups per CU are queued (prompt rows); a
+  // decode batch (one row tile) runs faster with half the CUs busy, as fewer, longer-running
   // workgroups amortise the stage pipeline's start (64 rows of the Qwen3-0.6B
   // shapes: 3.86 ms per step at 128, 3.99 at 512, 4.39 at 64)
-  const int target = a.t <= kGT ? 128 : 512;
+  const int target = a.t <= 64 ? 128 : 1024;
   int ks = tiles < target ? std::min(std::min(nst, kMaxDeferSplit), (target + tiles - 1) / tiles) : 1;
   while (ks > 1 && (int64_t)ks * a.t * N > region_cap) --ks;
   a.ksplit = ks;
