@@ -1203,7 +1203,12 @@ __global__ __launch_bounds__(kWg) void k_pf_fattn(PfAttnArgs a) {
   // every row has its own
   const int G = a.heads / a.kv_heads, TW = a.kv.row_seq ? 1 : 64 / G;
   const int ntiles = gridDim.x / a.kv_heads;
-  const int kv = blockIdx.x % a.kv_heads, t0 = (ntiles - 1 - (int)blockIdx.x / a.kv_heads) * TW;
+  // query tiles in complementary pairs: workgroups q and q + hi (dispatched
+  // one dispatch round apart, so that one CU holds both while the grid is two
+  // rounds) take tiles ntiles - 1 - q and q, whose causal key ranges sum to a
+  // constant
+  const int q = (int)blockIdx.x / a.kv_heads, hi = ntiles - ntiles / 2;
+  const int kv = blockIdx.x % a.kv_heads, t0 = (q < hi ? ntiles - 1 - q : q - hi) * TW;
   const int col = lane & 15, quad = lane >> 4;
   const int seq = row_seq(a.kv, t0);
   const __half* kc = (const __half*)a.kv.kc;
