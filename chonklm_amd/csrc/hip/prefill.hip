@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
     const int u = s * 4 + wj;
     float v[32];
     if (w_ok && u < U) {
-      dequant_unit<T>(f, u, v);
+      dequant_unit<T>(f, u, v, wsc);  // W * 2^ws (the unit's factors scaled: exact)
     } else {
 #pragma unroll
       for (int e = 0; e < 32; ++e) v[e] = 0.f;
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       half4_t h, l;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float sv = v[e + i] * wsc;
+        const float sv = v[e + i];
         h[i] = (_Float16)sv;
         l[i] = (_Float16)(sv - (float)h[i]);
       }

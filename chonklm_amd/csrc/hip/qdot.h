@@ -681,17 +681,19 @@ __device__ __forceinline__ float acc_lane<QT_Q4_K>(const LaneFrag<QT_Q4_K>& f, c
 
 // ---- exact dequantization ------------------------------------------------------
 // out[e] for unit-local element e (placement per unit_col), computed with the
-// reference's fp32 operation order and no contraction.
+// reference's fp32 operation order and no contraction. `pow2` (a power of two)
+// scales the unit's factors, which scales every result exactly: out[e] is the
+// unscaled value times pow2 bit for bit (normal-range values).
 template <int T>
-__device__ __forceinline__ void dequant_unit(const Frag<T>& f, int u, float out[32]);
+__device__ __forceinline__ void dequant_unit(const Frag<T>& f, int u, float out[32], float pow2 = 1.0f);
 
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q4_K>(const Frag<QT_Q4_K>& f, int u, float out[32]) {
+__device__ __forceinline__ void dequant_unit<QT_Q4_K>(const Frag<QT_Q4_K>& f, int u, float out[32], float pow2) {
   const int g = (u & 7) >> 1;
   uint32_t sc0, m0, sc1, m1;
   scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
   scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
-  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
+  const float d = h2f(f.hdr.x) * pow2, dmin = h2f(f.hdr.x >> 16) * pow2;
   const float a0 = __fmul_rn(d, (float)sc0), b0 = __fmul_rn(dmin, (float)m0);
   const float a1 = __fmul_rn(d, (float)sc1), b1 = __fmul_rn(dmin, (float)m1);
   const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
@@ -703,12 +705,12 @@ __device__ __forceinline__ void dequant_unit<QT_Q4_K>(const Frag<QT_Q4_K>& f, in
 }
 
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q5_K>(const Frag<QT_Q5_K>& f, int u, float out[32]) {
+__device__ __forceinline__ void dequant_unit<QT_Q5_K>(const Frag<QT_Q5_K>& f, int u, float out[32], float pow2) {
   const int g = (u & 7) >> 1;
   uint32_t sc0, m0, sc1, m1;
   scale_min(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, &sc0, &m0);
   scale_min(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, &sc1, &m1);
-  const float d = h2f(f.hdr.x), dmin = h2f(f.hdr.x >> 16);
+  const float d = h2f(f.hdr.x) * pow2, dmin = h2f(f.hdr.x >> 16) * pow2;
   const float a0 = __fmul_rn(d, (float)sc0), b0 = __fmul_rn(dmin, (float)m0);
   const float a1 = __fmul_rn(d, (float)sc1), b1 = __fmul_rn(dmin, (float)m1);
   const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
@@ -725,9 +727,9 @@ __device__ __forceinline__ void dequant_unit<QT_Q5_K>(const Frag<QT_Q5_K>& f, in
 }
 
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q6_K>(const Frag<QT_Q6_K>& f, int u, float out[32]) {
+__device__ __forceinline__ void dequant_unit<QT_Q6_K>(const Frag<QT_Q6_K>& f, int u, float out[32], float pow2) {
   const int b = (u & 7) & 3;
-  const float d = h2f(f.d);
+  const float d = h2f(f.d) * pow2;
   const uint32_t qa[2] = {f.qa.x, f.qa.y}, qb[2] = {f.qb.x, f.qb.y}, qh[2] = {f.qh.x, f.qh.y};
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
@@ -746,16 +748,16 @@ __device__ __forceinline__ void dequant_unit<QT_Q6_K>(const Frag<QT_Q6_K>& f, in
 }
 
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q8_0>(const Frag<QT_Q8_0>& f, int u, float out[32]) {
-  const float d = h2f(f.d);
+__device__ __forceinline__ void dequant_unit<QT_Q8_0>(const Frag<QT_Q8_0>& f, int u, float out[32], float pow2) {
+  const float d = h2f(f.d) * pow2;
   const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
 #pragma unroll
   for (int e = 0; e < 32; ++e) out[e] = __fmul_rn((float)(int8_t)((q[e >> 2] >> (8 * (e & 3))) & 0xffu), d);
 }
 
 template <int T, typename F>
-__device__ __forceinline__ void dequant_q5x(const F& f, float out[32]) {
-  const float d = h2f(f.d);
+__device__ __forceinline__ void dequant_q5x(const F& f, float out[32], float pow2) {
+  const float d = h2f(f.d) * pow2;
   const uint32_t q[4] = {f.qs.x, f.qs.y, f.qs.z, f.qs.w};
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
@@ -766,18 +768,18 @@ __device__ __forceinline__ void dequant_q5x(const F& f, float out[32]) {
     if constexpr (T == QT_Q5_0) {
       out[e] = __fmul_rn(d, (float)((int)qv - 16));
     } else {
-      out[e] = __fadd_rn(__fmul_rn(d, (float)qv), h2f(f.m));
+      out[e] = __fadd_rn(__fmul_rn(d, (float)qv), h2f(f.m) * pow2);
     }
   }
 }
 
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q5_0>(const Frag<QT_Q5_0>& f, int u, float out[32]) {
-  dequant_q5x<QT_Q5_0>(f, out);
+__device__ __forceinline__ void dequant_unit<QT_Q5_0>(const Frag<QT_Q5_0>& f, int u, float out[32], float pow2) {
+  dequant_q5x<QT_Q5_0>(f, out, pow2);
 }
 template <>
-__device__ __forceinline__ void dequant_unit<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, float out[32]) {
-  dequant_q5x<QT_Q5_1>(f, out);
+__device__ __forceinline__ void dequant_unit<QT_Q5_1>(const Frag<QT_Q5_1>& f, int u, float out[32], float pow2) {
+  dequant_q5x<QT_Q5_1>(f, out, pow2);
 }
 
 // Dispatch helper: calls fn.template operator()<T>() for the runtime type.
