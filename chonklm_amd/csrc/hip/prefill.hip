@@ -26,7 +26,11 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGM = 64;          // weight rows per workgroup tile
-constexpr int kGT = 128;         // token rows per workgroup tile
+// token rows per workgroup tile: 128 for passes over 512 rows (each
+// dequantized weight stage serves more products), 64 up to 512 rows (twice the
+// tiles, so that short passes need no K split)
+__host__ __device__ constexpr int gemm_tokens(int tj) { return 64 * tj; }
+inline int gemm_tj(int rows) { return rows > 512 ? 2 : 1; }
 constexpr int kGK = 128;         // K per stage (whole units for every type)
 constexpr int kGS = kGK + 8;     // LDS row stride in halves (bank spread)
 
@@ -218,22 +222,22 @@ __global__ __launch_bounds__(kRowT) void k_pf_split(PfSplitArgs a) {
 
 // ---- dequant-fused GEMM ----------------------------------------------------------
 
-// y[t][n] (=|+=) sum_k x[t][k] W[n][k] for a kGM x kGT tile. The tile's
+// y[t][n] (=|+=) sum_k x[t][k] W[n][k] for a kGM x 64 TJ tile. The tile's
 // weights are dequantized once per stage into LDS (fp16 hi + lo of W * 2^ws)
-// and serve 128 token rows; wave w owns token rows 32 w .. 32 w + 31 against
-// all 64 weight rows (4 x 2 MFMA tiles of 16 x 16, three products each) and
+// and serve 64 TJ token rows; wave w owns token rows 16 TJ w .. 16 TJ (w + 1) - 1
+// against all 64 weight rows (4 x TJ MFMA tiles of 16 x 16, three products each) and
 // reads its activation operands straight from the planes (each element is
 // read by one lane of one wave, so staging them through LDS would only add a
 // copy). With only the weights in LDS (35 KB) the registers bound the
-// workgroups per CU: three for the Q4_K instance, two for Q6_K.
-template <int T>
+// workgroups per CU: at TJ = 2 three for the Q4_K instance, two for Q6_K.
+template <int T, int TJ>
 __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   extern __shared__ __align__(16) _Float16 gsm[];
   _Float16* wh = gsm;
   _Float16* wl = wh + kGM * kGS;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * kGT;
+  const int n0 = blockIdx.x * kGM, t0 = blockIdx.y * gemm_tokens(TJ);
   const int N = a.n_all ? a.n_all : a.w.n;
   // the tile's matrix of a fused launch (segments start on tile boundaries)
   const int seg = a.n_all ? (n0 >= a.n2 ? 2 : (n0 >= a.n1 ? 1 : 0)) : 0;
@@ -257,7 +261,6 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
   const bool w_ok = n0 + wr < N;
   const float wsc = ldexpf(1.0f, a.ws);
   // operand role: lane l holds row (or token) l % 16 and k 8 (l / 16) .. + 8 of a 32-k step
-  constexpr int TJ = kGT / 64;  // token tiles of 16 per wave
   const int col = lane & 15, kq = (lane >> 4) * 8;
   // the lane's plane rows as 32-bit byte offsets from the planes' (uniform)
   // bases; a token row past t reads row t - 1: its products are computed and
@@ -1835,6 +1838,28 @@ size_t gemm_shared_bytes() { return sizeof(_Float16) * (size_t)(2 * kGM) * kGS; 
 // k_gemm addresses the activation planes with 32-bit byte offsets
 bool gemm_planes_fit(const GemmArgs& a) { return a.t >= 1 && (int64_t)a.t * a.kpad * 2 <= (int64_t)UINT32_MAX; }
 
+// k_gemm<type, tj> on the stream; false for a type without an instance
+bool launch_gemm_tiles(const GemmArgs& a, int tj, dim3 grid, hipStream_t s) {
+  const size_t sh = gemm_shared_bytes();
+#define CHONK_GEMM_CASE(QT)                                                 \
+  case QT:                                                                  \
+    if (tj == 2)                                                            \
+      hipLaunchKernelGGL((k_gemm<QT, 2>), grid, dim3(kWg), sh, s, a);       \
+    else                                                                    \
+      hipLaunchKernelGGL((k_gemm<QT, 1>), grid, dim3(kWg), sh, s, a);       \
+    return true;
+  switch (a.w.type) {
+    CHONK_GEMM_CASE(QT_Q4_K)
+    CHONK_GEMM_CASE(QT_Q5_K)
+    CHONK_GEMM_CASE(QT_Q6_K)
+    CHONK_GEMM_CASE(QT_Q8_0)
+    CHONK_GEMM_CASE(QT_Q5_0)
+    CHONK_GEMM_CASE(QT_Q5_1)
+    default: return false;
+  }
+#undef CHONK_GEMM_CASE
+}
+
 size_t fattn_shared_bytes(int hd) {
   return sizeof(_Float16) * ((size_t)kFaKeys * (hd + 8) + (size_t)hd * (kFaKeys + 8));
 }
@@ -1865,7 +1890,8 @@ hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
     return hipGetLastError();
   }
   if (!gemm_planes_fit(a)) return hipErrorInvalidValue;
-  const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
+  const int tj = gemm_tj(a.t), gt = gemm_tokens(tj);
+  const int tiles = ((a.w.n + kGM - 1) / kGM) * ((a.t + gt - 1) / gt);
   const int nst = (a.w.k + kGK - 1) / kGK;
   a.ksplit = 1;
   if (a.part && tiles < 256) {
@@ -1873,17 +1899,8 @@ hipError_t launch_gemm(const GemmArgs& a0, hipStream_t s) {
     while (ks > 1 && (int64_t)ks * a.t * a.w.n > a.part_cap) --ks;
     a.ksplit = ks;
   }
-  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, a.ksplit);
-  const size_t sh = gemm_shared_bytes();
-  switch (a.w.type) {
-    case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_K: hipLaunchKernelGGL(k_gemm<QT_Q5_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q6_K: hipLaunchKernelGGL(k_gemm<QT_Q6_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q8_0: hipLaunchKernelGGL(k_gemm<QT_Q8_0>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_0: hipLaunchKernelGGL(k_gemm<QT_Q5_0>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_1: hipLaunchKernelGGL(k_gemm<QT_Q5_1>, grid, dim3(kWg), sh, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  const dim3 grid((a.w.n + kGM - 1) / kGM, (a.t + gt - 1) / gt, a.ksplit);
+  if (!launch_gemm_tiles(a, tj, grid, s)) return hipErrorInvalidValue;
   if (a.ksplit > 1) {
     const int64_t total = (int64_t)a.t * a.w.n;
     const int blocks = (int)std::min<int64_t>((total + kWg - 1) / kWg, 4096);
@@ -1931,29 +1948,22 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
     return e;
   }
   if (!gemm_planes_fit(a)) return hipErrorInvalidValue;
-  const int tiles = ((N + kGM - 1) / kGM) * ((a.t + kGT - 1) / kGT);
+  const int tj = gemm_tj(a.t), gt = gemm_tokens(tj);
+  const int tiles = ((N + kGM - 1) / kGM) * ((a.t + gt - 1) / gt);
   const int nst = (a.w.k + kGK - 1) / kGK;
-  // split K until about four workgroups per CU are queued (prompt rows); a
-  // decode batch (one row tile) runs faster with half the CUs busy, as fewer, longer-running
+  // split K until about four workgroups per CU are queued (passes of 128-row
+  // tiles; two with 64-row tiles); a decode batch (one row tile) runs faster
+  // with half the CUs busy, as fewer, longer-running
   // workgroups amortise the stage pipeline's start (64 rows of the Qwen3-0.6B
   // shapes: 3.86 ms per step at 128, 3.99 at 512, 4.39 at 64)
-  const int target = a.t <= 64 ? 128 : 1024;
+  const int target = a.t <= 64 ? 128 : (tj == 2 ? 1024 : 512);
   int ks = tiles < target ? std::min(std::min(nst, kMaxDeferSplit), (target + tiles - 1) / tiles) : 1;
   while (ks > 1 && (int64_t)ks * a.t * N > region_cap) --ks;
   a.ksplit = ks;
   a.part = region;
   a.defer = 1;
-  const dim3 grid((N + kGM - 1) / kGM, (a.t + kGT - 1) / kGT, ks);
-  const size_t sh = gemm_shared_bytes();
-  switch (a.w.type) {
-    case QT_Q4_K: hipLaunchKernelGGL(k_gemm<QT_Q4_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_K: hipLaunchKernelGGL(k_gemm<QT_Q5_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q6_K: hipLaunchKernelGGL(k_gemm<QT_Q6_K>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q8_0: hipLaunchKernelGGL(k_gemm<QT_Q8_0>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_0: hipLaunchKernelGGL(k_gemm<QT_Q5_0>, grid, dim3(kWg), sh, s, a); break;
-    case QT_Q5_1: hipLaunchKernelGGL(k_gemm<QT_Q5_1>, grid, dim3(kWg), sh, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  const dim3 grid((N + kGM - 1) / kGM, (a.t + gt - 1) / gt, ks);
+  if (!launch_gemm_tiles(a, tj, grid, s)) return hipErrorInvalidValue;
   out->p = region;
   out->n = N;
   out->ld = N;
@@ -1964,8 +1974,10 @@ hipError_t launch_gemm_deferred(const GemmArgs& a0, float* region, int64_t regio
 
 hipError_t init_gemm_attributes() {
   const size_t sh = gemm_shared_bytes();
-  const void* fns[6] = {(const void*)k_gemm<QT_Q4_K>, (const void*)k_gemm<QT_Q5_K>, (const void*)k_gemm<QT_Q6_K>,
-                        (const void*)k_gemm<QT_Q8_0>, (const void*)k_gemm<QT_Q5_0>, (const void*)k_gemm<QT_Q5_1>};
+  const void* fns[12] = {(const void*)k_gemm<QT_Q4_K, 1>, (const void*)k_gemm<QT_Q5_K, 1>, (const void*)k_gemm<QT_Q6_K, 1>,
+                         (const void*)k_gemm<QT_Q8_0, 1>, (const void*)k_gemm<QT_Q5_0, 1>, (const void*)k_gemm<QT_Q5_1, 1>,
+                         (const void*)k_gemm<QT_Q4_K, 2>, (const void*)k_gemm<QT_Q5_K, 2>, (const void*)k_gemm<QT_Q6_K, 2>,
+                         (const void*)k_gemm<QT_Q8_0, 2>, (const void*)k_gemm<QT_Q5_0, 2>, (const void*)k_gemm<QT_Q5_1, 2>};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh);
     if (e != hipSuccess) return e;
