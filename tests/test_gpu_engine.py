@@ -84,6 +84,8 @@ def test_generate_matches_oracle(name, synth):
 
 @pytest.mark.parametrize("name", ["tiny-qwen3", "tiny-gemma3"])
 def test_stepped_equals_device_loop(name, synth):
+    """The device-driven loop (19 steps: two replays of the eight-step graph, then three
+    single steps) gives the ids of the loop stepped from the host (one graph per step)."""
     w, loaded, _ = _pair(synth, name)
     prompt = _prompt(w, seed=2)
     a = generate_llama_wgsl(loaded, prompt, 20, temperature=w.temperature, top_k=w.top_k, seed=3)["ids"]
