@@ -38,6 +38,9 @@ GEMM_SHAPES = [
     ("Q8_0", 576, 576, 65), ("Q8_0", 192, 608, 3),
     ("Q5_0", 1536, 576, 70), ("Q5_0", 333, 96, 17),
     ("Q5_1", 640, 640, 33), ("Q5_K", 512, 1024, 80),
+    # passes over 512 rows take the 128-row tiles: ragged token and weight-row counts
+    ("Q4_K", 1000, 2048, 700), ("Q6_K", 999, 768, 601), ("Q8_0", 576, 576, 530),
+    ("Q5_0", 333, 96, 515), ("Q5_1", 640, 640, 513), ("Q5_K", 512, 1024, 520),
 ]
 
 
