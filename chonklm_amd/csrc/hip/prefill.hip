@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kWg) void k_gemm(GemmArgs a) {
       for (int e = 0; e < 32; ++e) v[e] = 0.f;
     }
     // the next stage's unit goes out as soon as this one is decoded (the last
-    // stage requests itself again: no branch around the load)
+    // stage requests itself again rather than branching on the stage index)
     fetch_w(min(s + 1, s_hi - 1));
     __syncthreads();  // the previous stage's tile is consumed
     _Float16* rh = wh + wr * kGS;
